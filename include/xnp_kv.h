@@ -1,0 +1,209 @@
+/*
+ * xnp_kv.h -- C ABI of the MI355X (gfx950) flow-LM KV cache: a block-paged K/V store shared by
+ * many concurrent utterance streams, with per-frame append + RoPE, ring slots and eviction,
+ * single-query decode attention and causal prompt prefill, all as hand-written HIP kernels.
+ *
+ * It replaces, batched across streams, the op surface that the reference's
+ * StreamingMultiheadAttention::forward (ptts/src/transformer.rs:183-251) drives through the
+ * `xn` tensor crate, plus the state API above it:
+ *   StreamingMHAState / init_state            transformer.rs:14-25, 169-180   xnp_stream_open
+ *   complete_kv (slice_set / scatter_set)     transformer.rs:61-92, 216-218   xnp_append
+ *   RotaryEmbedding::forward (rope_i)         rope.rs:37-95                   inside append/decode
+ *   sdpa_decode                               transformer.rs:223, 230         xnp_decode
+ *   matmul_t / softmax / matmul (t > 1)       transformer.rs:231-248          xnp_prefill
+ *   RingSlots::decode_mask                    transformer.rs:42-52            per-stream seen bitmap
+ *   start_ring / set_ring_slot / evict        transformer.rs:842-929          xnp_ring_*
+ *   with_seq_budget                           transformer.rs:350-392          xnp_stream_fork
+ *   advance                                   transformer.rs:337-344          xnp_stream_advance
+ *   Session::step eviction policy             s2s.rs:318-333                  xnp_ring_slide
+ *   plan::frame_budget / seq_budget           plan.rs:43-54                   xnp_frame_budget, ...
+ *
+ * Conventions (after ptts-ffi, ptts-ffi/src/lib.rs:56-77 and ptts-ffi/include/ptts.h:50-51):
+ *   - Every call returns an xnp_status; XNP_OK is 0.  On failure, xnp_last_error() returns a
+ *     thread-local message saying why, valid until the next failing call on that thread.
+ *   - A refused call changes nothing (as evict does, transformer.rs:896-904).
+ *   - The pool owns the device pages, the scales and the block tables.  The caller owns every
+ *     q/k/v/out buffer (device memory) and the hipStream_t, passed as void*.  Calls that touch
+ *     the device are asynchronous on that stream and never synchronize it.  All of one pool's
+ *     device work must go to one stream (or the caller orders the streams).
+ *   - One host thread at a time per pool.  No allocation happens between xnp_batch_begin and
+ *     xnp_batch_end, so the per-layer calls of a batch can be captured in a hipGraph.
+ *
+ * Layouts (row-major, D = head_dim, H = num_heads, KVH = num_kv_heads):
+ *   q, out          [n][t][H][D]     activation dtype (f32 or bf16)
+ *   k, v            [n][t][KVH][D]   activation dtype; KV head j serves query heads
+ *                                    j*H/KVH .. (j+1)*H/KVH-1 (transformer.rs:199-211)
+ *   pages           [L][2][num_blocks][H][16][D]   cache dtype; one (page, head) is a
+ *                                    contiguous 16 x D tile
+ *   int8 scales     [L][2][num_blocks][H]          f32, one per (page, head), K and V apart
+ */
+#ifndef XNP_KV_H
+#define XNP_KV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define XNP_BLOCK 16 /* positions per page */
+
+typedef enum xnp_dtype { XNP_F32 = 0, XNP_BF16 = 1, XNP_I8 = 2 } xnp_dtype;
+
+typedef enum xnp_status {
+    XNP_OK = 0,
+    XNP_E_INVALID = 1,       /* bad argument, shape or dtype */
+    XNP_E_STREAM = 2,        /* no such open stream */
+    XNP_E_NO_ROOM = 3,       /* the stream's capacity is full (step_graph.rs:245-247) */
+    XNP_E_OUT_OF_BLOCKS = 4, /* the pool has no free page left */
+    XNP_E_RING = 5,          /* ring misuse: not a ring, slot range, t != 1, slot still holds a row
+                                (transformer.rs:68-73, 855-867) */
+    XNP_E_EVICT = 6,         /* evict refused (transformer.rs:885-901) */
+    XNP_E_BUDGET = 7,        /* fork into a budget smaller than the filled prefix, or of a ring
+                                (transformer.rs:356-364) */
+    XNP_E_HEADS = 8,         /* heads do not divide (transformer.rs:703-711) */
+    XNP_E_STATE = 9,         /* call out of order: batch open or not open, host-only pool */
+    XNP_E_HIP = 10           /* the HIP runtime failed */
+} xnp_status;
+
+/* Ring eviction modes.  XNP_RING_SHIFT is the reference: evict rotates every kept key past the
+ * prefix back by the number of evicted rows, in place (transformer.rs:905-926).  XNP_RING_ABSOLUTE
+ * keeps each key at the rotation it was written with and rotates the query instead, once for
+ * keys before the prefix and once for those past it; attention depends only on the difference
+ * of the two positions, so outputs equal the shifting ring's up to rounding, and no key is ever
+ * rewritten (int8 caches need it). */
+typedef enum xnp_ring_mode { XNP_RING_SHIFT = 1, XNP_RING_ABSOLUTE = 2 } xnp_ring_mode;
+
+#define XNP_POOL_HOST_ONLY 1 /* metadata only: no device memory; device calls return XNP_E_STATE */
+
+typedef struct xnp_pool xnp_pool;
+
+typedef struct xnp_pool_desc {
+    int32_t num_layers;   /* L */
+    int32_t num_heads;    /* H, heads of q, out and the cache */
+    int32_t num_kv_heads; /* KVH, heads of the k and v handed to append; divides H */
+    int32_t head_dim;     /* D; the kernels take 64 */
+    int32_t num_blocks;   /* pages of XNP_BLOCK positions, shared by all streams and layers */
+    int32_t max_streams;
+    int32_t max_blocks_per_stream;
+    int32_t cache_dtype;  /* xnp_dtype of the cached K/V */
+    int32_t act_dtype;    /* xnp_dtype of q/k/v/out: XNP_F32 or XNP_BF16 */
+    float max_period;     /* RoPE theta (rope.rs:47) */
+    int32_t max_pos;      /* RoPE table rows: every position used must be below it */
+    int32_t flags;        /* XNP_POOL_* */
+    uint64_t page_seed;   /* 0: pages are handed out in order; else a Fisher-Yates shuffle of the
+                             free list seeded with it (shuffled block tables) */
+    int32_t device;       /* HIP device ordinal */
+    int32_t chunk_blocks; /* pages per decode work item (split-K chunk); 0 picks the default */
+} xnp_pool_desc;
+
+typedef struct xnp_stream_info {
+    int32_t current_end; /* position of the next row (StreamingMHAState::current_end) */
+    int32_t capacity;    /* positions the stream may hold (S_cap) */
+    int32_t ring_mode;   /* 0 without a ring, else xnp_ring_mode */
+    int32_t ring_write;  /* RingSlots::write */
+    int32_t ring_filled; /* RingSlots::filled */
+    int32_t ring_prefix; /* absolute ring: the prefix its evictions keep */
+    int32_t ring_shift;  /* absolute ring: rows evicted so far */
+    int32_t in_view;     /* valid ring slots */
+    int32_t blocks;      /* pages the stream holds */
+    int32_t shared;      /* of which shared with another stream */
+} xnp_stream_info;
+
+typedef struct xnp_pool_stats {
+    int32_t free_blocks;
+    int32_t open_streams;
+    int32_t batch_open; /* streams in the open batch, 0 if none */
+    int32_t work_items; /* decode work items of the open batch */
+    int64_t device_bytes;
+} xnp_pool_stats;
+
+/* ---- pool ------------------------------------------------------------------------------ */
+xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out);
+xnp_status xnp_pool_destroy(xnp_pool *pool);
+xnp_status xnp_pool_stats_get(const xnp_pool *pool, xnp_pool_stats *out);
+/* Rows pos0 .. pos0+n-1 of the pool's RoPE table as [n][D/2] (cos, sin) pairs: the values the
+ * kernels rotate with, built on the host as rope.rs:44-58 does (RotaryEmbedding::new). */
+xnp_status xnp_pool_rope_rows(const xnp_pool *pool, int32_t pos0, int32_t n, float *cos_sin);
+
+/* ---- streams ---------------------------------------------------------------------------- */
+/* StreamingMultiheadAttention::init_state(1, capacity), transformer.rs:169-180.  Pages are taken
+ * as rows arrive, not up front. */
+xnp_status xnp_stream_open(xnp_pool *pool, int32_t capacity, int32_t *id);
+xnp_status xnp_stream_close(xnp_pool *pool, int32_t id);
+/* with_seq_budget, transformer.rs:350-392: a new stream of `capacity` positions holding src's
+ * filled prefix.  Full pages are shared (no later write can reach them); the partial last page
+ * is copied on hip_stream.  Refused for a ring and for capacity < current_end. */
+xnp_status xnp_stream_fork(xnp_pool *pool, int32_t src, int32_t capacity, int32_t *id,
+                           void *hip_stream);
+xnp_status xnp_stream_info_get(const xnp_pool *pool, int32_t id, xnp_stream_info *out);
+/* StreamingTransformerState::advance, transformer.rs:337-344: count n more filled positions,
+ * taking pages for them; their contents are what xnp_write_rows puts there. */
+xnp_status xnp_stream_advance(xnp_pool *pool, int32_t id, int32_t n);
+/* The stream's page ids, logical block order, -1 where none is held (at most `cap` entries). */
+xnp_status xnp_stream_blocks(const xnp_pool *pool, int32_t id, int32_t *pages, int32_t cap,
+                             int32_t *count);
+/* The seen map attention uses at the next step: valid[slot] for slot < capacity. */
+xnp_status xnp_ring_valid(const xnp_pool *pool, int32_t id, uint8_t *valid, int32_t cap);
+
+/* Raw rows [slot0, slot0 + n) of one layer, kv 0 = keys, 1 = values: rows [n][H][D] in the
+ * cache dtype (device memory); for int8 also scales [nb][H] for the nb pages the rows touch.
+ * No RoPE, no quantization: a voice cache loaded as is, or a cache read back. */
+xnp_status xnp_write_rows(xnp_pool *pool, int32_t id, int32_t layer, int32_t kv, int32_t slot0,
+                          int32_t n, const void *rows, const float *scales, void *hip_stream);
+xnp_status xnp_read_rows(const xnp_pool *pool, int32_t id, int32_t layer, int32_t kv,
+                         int32_t slot0, int32_t n, void *rows, float *scales, void *hip_stream);
+
+/* ---- ring (transformer.rs:842-929) ------------------------------------------------------ */
+/* start_ring: valid[s] = s < current_end; write = filled = current_end.  `prefix` is used by
+ * XNP_RING_ABSOLUTE only.  Shared pages are copied first (on hip_stream). */
+xnp_status xnp_ring_start(xnp_pool *pool, int32_t id, int32_t mode, int32_t prefix,
+                          void *hip_stream);
+xnp_status xnp_ring_set_slot(xnp_pool *pool, int32_t id, int32_t slot);
+/* evict: all slots checked before any change; count > current_end, a slot below the prefix or
+ * holding no row is refused.  XNP_RING_SHIFT rotates the kept keys on hip_stream. */
+xnp_status xnp_ring_evict(xnp_pool *pool, int32_t id, int32_t prefix, const int32_t *slots,
+                          int32_t count, void *hip_stream);
+/* Session::step's policy, s2s.rs:324-333: when `window` slots past the prefix are in view, evict
+ * the oldest `drop`, then set the write slot to prefix + step % span.  s2s runs it with
+ * span = window = context and drop = context / 3; a sliding window uses drop = 1 and
+ * span = window + XNP_BLOCK, so a page is never shared by the oldest and the newest rows. */
+xnp_status xnp_ring_slide(xnp_pool *pool, int32_t id, int32_t prefix, int32_t span,
+                          int32_t window, int32_t drop, int64_t step, void *hip_stream);
+
+/* ---- a batched step ---------------------------------------------------------------------- */
+/* Open a step over streams ids[0..n), t new rows each (t > 1: prompt prefill, no ring).  Checks
+ * every stream (capacity, ring slot) and takes the pages the new rows need, all or nothing;
+ * uploads the step's plan (positions, block tables, masks, decode work list) on hip_stream. */
+xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_t n, int32_t t,
+                           void *hip_stream);
+/* complete_kv for one layer: rotate k at each row's position, write k and v into the pages
+ * (int8: quantize), at current_end (+ row) or the ring's write slot. */
+xnp_status xnp_append(xnp_pool *pool, int32_t layer, const void *k, const void *v,
+                      void *hip_stream);
+/* sdpa_decode for one layer (t == 1): rotate q, attend over the stream's cache including the
+ * appended row, under the ring's mask; out = softmax(q K^T * scale) V. */
+xnp_status xnp_decode(xnp_pool *pool, int32_t layer, const void *q, void *out, float scale,
+                      void *hip_stream);
+/* causal prompt attention for one layer (t > 1, transformer.rs:231-248): row i of a stream sees
+ * positions 0 .. current_end + i. */
+xnp_status xnp_prefill(xnp_pool *pool, int32_t layer, const void *q, void *out, float scale,
+                       void *hip_stream);
+/* xnp_append then xnp_decode (t == 1, one fused kernel) or xnp_prefill (t > 1). */
+xnp_status xnp_attend(xnp_pool *pool, int32_t layer, const void *q, const void *k,
+                      const void *v, void *out, float scale, void *hip_stream);
+/* Close the step: current_end += t; a ring marks the written slot valid. */
+xnp_status xnp_batch_end(xnp_pool *pool);
+/* Drop the step: give back the pages it took; nothing else changes. */
+xnp_status xnp_batch_abort(xnp_pool *pool);
+
+/* ---- budgets (plan.rs:25, 43-54) --------------------------------------------------------- */
+int32_t xnp_frame_budget(int32_t num_tokens, double frame_rate);
+int32_t xnp_seq_budget(int32_t num_tokens, int32_t frame_budget);
+
+const char *xnp_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,595 @@
+/*
+ * oracle.c -- CPU restatement of the reference's flow-LM KV-cache path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker the HIP library is compared against (see oracle.h).
+ * Built with -ffp-contract=off so that every f32 product and sum is rounded on its own, as the
+ * reference's Rust code does (Rust never contracts a*b+c into an fma).
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static __thread char g_err[512];
+
+static int fail(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return -1;
+}
+
+const char *orc_last_error(void) { return g_err; }
+
+/* ---------------------------------------------------------------------------------------- */
+/* element helpers                                                                          */
+
+float orc_bf16_round(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    if ((u & 0x7f800000u) == 0x7f800000u) {
+        if (u & 0x007fffffu) u |= 0x00400000u; /* keep NaN a (quiet) NaN */
+        u &= 0xffff0000u;
+    } else {
+        u += 0x7fffu + ((u >> 16) & 1u); /* round to nearest, ties to even */
+        u &= 0xffff0000u;
+    }
+    memcpy(&x, &u, 4);
+    return x;
+}
+
+static inline uint16_t bf16_bits(float x) {
+    float r = orc_bf16_round(x);
+    uint32_t u;
+    memcpy(&u, &r, 4);
+    return (uint16_t)(u >> 16);
+}
+
+static inline float bf16_value(uint16_t b) {
+    uint32_t u = (uint32_t)b << 16;
+    float x;
+    memcpy(&x, &u, 4);
+    return x;
+}
+
+static inline float round_act(float x, int act_dtype) {
+    return act_dtype == ORC_BF16 ? orc_bf16_round(x) : x;
+}
+
+int8_t orc_quant(float y, float s) {
+    if (!(s > 0.0f)) return 0;
+    float r = rintf(y / s);
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    return (int8_t)r;
+}
+
+/* ---------------------------------------------------------------------------------------- */
+/* RoPE: rope.rs:37-63 (tables) and the rope_i rotation of rope.rs:74-95                   */
+
+void orc_rope_row(int head_dim, float max_period, float pos, int act_dtype, float *cos_out,
+                  float *sin_out) {
+    int half = head_dim / 2;
+    for (int i = 0; i < half; i++) {
+        /* rope.rs:47: 1.0f32 / max_period.powf(i as f32 / half_dim as f32) */
+        float inv_freq = 1.0f / powf(max_period, (float)i / (float)half);
+        float angle = pos * inv_freq; /* rope.rs:54 */
+        cos_out[i] = round_act(cosf(angle), act_dtype);
+        sin_out[i] = round_act(sinf(angle), act_dtype);
+    }
+}
+
+void orc_rotate(int head_dim, float *x, const float *c, const float *s, int act_dtype) {
+    for (int i = 0; i < head_dim / 2; i++) {
+        float x0 = x[2 * i], x1 = x[2 * i + 1];
+        float a = x0 * c[i], b = x1 * s[i];
+        float e = x0 * s[i], f = x1 * c[i];
+        x[2 * i] = round_act(a - b, act_dtype);
+        x[2 * i + 1] = round_act(e + f, act_dtype);
+    }
+}
+
+/* ---------------------------------------------------------------------------------------- */
+/* stream state                                                                             */
+
+struct orc_stream {
+    int L, H, KVH, D, cap, cdt, adt;
+    float theta;
+    void *kc[2];  /* [L][cap][H][D] keys (0) and values (1), element type by cdt */
+    float *sc[2]; /* int8: [L][nblk][H] scales */
+    int nblk;
+    int current_end;
+    int ring, write, filled, prefix, shift;
+    uint8_t *valid; /* [cap] */
+};
+
+static size_t esize(int dt) { return dt == ORC_F32 ? 4 : dt == ORC_BF16 ? 2 : 1; }
+
+orc_stream *orc_open(int layers, int heads, int kv_heads, int head_dim, int capacity,
+                     int cache_dtype, int act_dtype, float max_period) {
+    if (layers <= 0 || heads <= 0 || head_dim <= 0 || head_dim > 256 || (head_dim & 1) || capacity < 0) {
+        fail("bad shape");
+        return NULL;
+    }
+    if (kv_heads <= 0 || heads % kv_heads) {
+        fail("the config's %d key/value heads do not divide its %d attention heads", kv_heads,
+             heads);
+        return NULL;
+    }
+    if (cache_dtype < 0 || cache_dtype > 2 || act_dtype < 0 || act_dtype > 1) {
+        fail("bad dtype");
+        return NULL;
+    }
+    orc_stream *st = calloc(1, sizeof *st);
+    st->L = layers;
+    st->H = heads;
+    st->KVH = kv_heads;
+    st->D = head_dim;
+    st->cap = capacity;
+    st->cdt = cache_dtype;
+    st->adt = act_dtype;
+    st->theta = max_period;
+    st->nblk = (capacity + ORC_BLOCK - 1) / ORC_BLOCK;
+    size_t n = (size_t)layers * capacity * heads * head_dim;
+    for (int kv = 0; kv < 2; kv++) {
+        st->kc[kv] = calloc(n ? n : 1, esize(cache_dtype));
+        if (cache_dtype == ORC_I8)
+            st->sc[kv] = calloc((size_t)layers * (st->nblk ? st->nblk : 1) * heads, 4);
+    }
+    st->valid = calloc(capacity ? capacity : 1, 1);
+    return st;
+}
+
+void orc_close(orc_stream *st) {
+    if (!st) return;
+    for (int kv = 0; kv < 2; kv++) {
+        free(st->kc[kv]);
+        free(st->sc[kv]);
+    }
+    free(st->valid);
+    free(st);
+}
+
+int orc_current_end(const orc_stream *st) { return st->current_end; }
+int orc_capacity(const orc_stream *st) { return st->cap; }
+
+void orc_ring_info(const orc_stream *st, int *mode, int *write, int *filled, int *prefix,
+                   int *shift, uint8_t *valid) {
+    if (mode) *mode = st->ring;
+    if (write) *write = st->write;
+    if (filled) *filled = st->filled;
+    if (prefix) *prefix = st->prefix;
+    if (shift) *shift = st->shift;
+    if (valid) memcpy(valid, st->valid, st->cap);
+}
+
+static inline size_t idx(const orc_stream *st, int layer, int slot, int h) {
+    return (((size_t)layer * st->cap + slot) * st->H + h) * st->D;
+}
+
+static inline float *scale_at(const orc_stream *st, int kv, int layer, int blk, int h) {
+    return &st->sc[kv][((size_t)layer * st->nblk + blk) * st->H + h];
+}
+
+/* The stored element as f32 (dequantized for int8: q * scale, one f32 product). */
+static inline float get(const orc_stream *st, int kv, int layer, int slot, int h, int d) {
+    size_t i = idx(st, layer, slot, h) + d;
+    switch (st->cdt) {
+    case ORC_F32: return ((float *)st->kc[kv])[i];
+    case ORC_BF16: return bf16_value(((uint16_t *)st->kc[kv])[i]);
+    default: return (float)((int8_t *)st->kc[kv])[i] * *scale_at(st, kv, layer, slot / ORC_BLOCK, h);
+    }
+}
+
+/* Whether a row other than `slot` in slot's block can still be attended to: the int8 rule for
+ * starting a block's scale afresh.  Without a ring the rows before `slot` are the filled ones. */
+static int block_has_other_row(const orc_stream *st, int slot) {
+    int b0 = slot / ORC_BLOCK * ORC_BLOCK;
+    if (st->ring == ORC_RING_NONE) return slot > b0;
+    int b1 = b0 + ORC_BLOCK < st->cap ? b0 + ORC_BLOCK : st->cap;
+    for (int s = b0; s < b1; s++)
+        if (s != slot && st->valid[s]) return 1;
+    return 0;
+}
+
+/* Store one head row x[D] (activation values) at `slot`.  For int8: per-(block, head) scale
+ * amax/127; a block holding another live row keeps its scale unless the row needs a larger
+ * one, and then every other row of the block is requantized to the larger scale. */
+static void store_row(orc_stream *st, int kv, int layer, int slot, int h, const float *x) {
+    size_t base = idx(st, layer, slot, h);
+    int D = st->D;
+    if (st->cdt == ORC_F32) {
+        memcpy((float *)st->kc[kv] + base, x, D * 4);
+        return;
+    }
+    if (st->cdt == ORC_BF16) {
+        uint16_t *p = (uint16_t *)st->kc[kv] + base;
+        for (int d = 0; d < D; d++) p[d] = bf16_bits(x[d]);
+        return;
+    }
+    int8_t *q = (int8_t *)st->kc[kv];
+    float *sp = scale_at(st, kv, layer, slot / ORC_BLOCK, h);
+    float amax = 0.0f;
+    for (int d = 0; d < D; d++) amax = fmaxf(amax, fabsf(x[d]));
+    float s_row = amax / 127.0f;
+    int fresh = !block_has_other_row(st, slot);
+    float s_old = *sp;
+    float s_new = fresh ? s_row : fmaxf(s_old, s_row);
+    if (!fresh && s_new > s_old) {
+        int b0 = slot / ORC_BLOCK * ORC_BLOCK;
+        int b1 = b0 + ORC_BLOCK < st->cap ? b0 + ORC_BLOCK : st->cap;
+        for (int s = b0; s < b1; s++) {
+            if (s == slot) continue;
+            int8_t *r = q + idx(st, layer, s, h);
+            for (int d = 0; d < D; d++) r[d] = orc_quant((float)r[d] * s_old, s_new);
+        }
+    }
+    for (int d = 0; d < D; d++) q[base + d] = orc_quant(x[d], s_new);
+    *sp = s_new;
+}
+
+/* The slot the step's row i goes to, or -1 with the error set. */
+static int check_append(const orc_stream *st, int t) {
+    if (t <= 0) return fail("a step appends at least one row, not %d", t);
+    if (st->ring != ORC_RING_NONE) {
+        if (t != 1) return fail("a ring cache takes one row at a time, not %d", t);
+        if (st->valid[st->write])
+            return fail("ring slot %d still holds a row, evict it first", st->write);
+        return 0;
+    }
+    if (st->current_end + t > st->cap)
+        return fail("no room left: the cache holds %d positions", st->cap);
+    return 0;
+}
+
+/* The RoPE position of a key written now at `slot`, step row i. */
+static float key_pos(const orc_stream *st, int slot, int i) {
+    int p = st->current_end + i;
+    if (st->ring == ORC_RING_ABSOLUTE && slot >= st->prefix) p += st->shift;
+    return (float)p;
+}
+
+int orc_append(orc_stream *st, int layer, int t, const float *k, const float *v) {
+    if (layer < 0 || layer >= st->L) return fail("layer %d of %d", layer, st->L);
+    if (check_append(st, t)) return -1;
+    int H = st->H, D = st->D, group = st->H / st->KVH;
+    float *cs = malloc(sizeof(float) * D), *sn = cs + D / 2;
+    float *x = malloc(sizeof(float) * D);
+    for (int i = 0; i < t; i++) {
+        int slot = st->ring != ORC_RING_NONE ? st->write : st->current_end + i;
+        orc_rope_row(D, st->theta, key_pos(st, slot, i), st->adt, cs, sn);
+        for (int h = 0; h < H; h++) {
+            /* transformer.rs:199-211: kv head j serves query heads j*group .. j*group+group-1 */
+            const float *src = k + ((size_t)i * st->KVH + h / group) * D;
+            memcpy(x, src, D * 4);
+            orc_rotate(D, x, cs, sn, st->adt);
+            store_row(st, 0, layer, slot, h, x);
+            store_row(st, 1, layer, slot, h, v + ((size_t)i * st->KVH + h / group) * D);
+        }
+    }
+    free(cs);
+    free(x);
+    return 0;
+}
+
+/* Row `slot` of head h as f32 (dequantized for int8: q * scale, one f32 product). */
+static void load_row(const orc_stream *st, int kv, int layer, int slot, int h, float *out) {
+    size_t i = idx(st, layer, slot, h);
+    int D = st->D;
+    if (st->cdt == ORC_F32) {
+        memcpy(out, (float *)st->kc[kv] + i, D * 4);
+    } else if (st->cdt == ORC_BF16) {
+        const uint16_t *p = (const uint16_t *)st->kc[kv] + i;
+        for (int d = 0; d < D; d++) out[d] = bf16_value(p[d]);
+    } else {
+        const int8_t *p = (const int8_t *)st->kc[kv] + i;
+        float s = *scale_at(st, kv, layer, slot / ORC_BLOCK, h);
+        for (int d = 0; d < D; d++) out[d] = (float)p[d] * s;
+    }
+}
+
+/* Attention of step row i, head h, with rotated query rows qw (keys past the prefix) and qp
+ * (keys before it; the same as qw except on an absolute ring).  f32 in key order; the f64
+ * companion (when out64 is given) from the same operands. */
+static void attend_one(const orc_stream *st, int layer, int i, int h, const float *qw,
+                       const float *qp, float scale, float *out, double *out64,
+                       float *sbuf, double *dbuf) {
+    int D = st->D;
+    int ring = st->ring != ORC_RING_NONE;
+    int span = ring ? (st->filled > st->write + 1 ? st->filled : st->write + 1)
+                    : st->current_end + i + 1;
+    float kbuf[256];
+    float m = -INFINITY;
+    double md = -INFINITY;
+    for (int j = 0; j < span; j++) {
+        int seen = !ring || j == st->write || st->valid[j];
+        if (!seen) {
+            sbuf[j] = -INFINITY;
+            if (out64) dbuf[j] = -INFINITY;
+            continue;
+        }
+        const float *qq = (st->ring == ORC_RING_ABSOLUTE && j < st->prefix) ? qp : qw;
+        load_row(st, 0, layer, j, h, kbuf);
+        float s = 0.0f;
+        for (int d = 0; d < D; d++) s = s + qq[d] * kbuf[d];
+        s = s * scale;
+        sbuf[j] = s;
+        if (s > m) m = s;
+        if (out64) {
+            double sd = 0.0;
+            for (int d = 0; d < D; d++) sd += (double)qq[d] * (double)kbuf[d];
+            sd *= (double)scale;
+            dbuf[j] = sd;
+            if (sd > md) md = sd;
+        }
+    }
+    float l = 0.0f;
+    double ld = 0.0;
+    for (int j = 0; j < span; j++) {
+        float e = sbuf[j] == -INFINITY ? 0.0f : expf(sbuf[j] - m);
+        sbuf[j] = e;
+        l = l + e;
+        if (out64) {
+            double ed = dbuf[j] == -INFINITY ? 0.0 : exp(dbuf[j] - md);
+            dbuf[j] = ed;
+            ld += ed;
+        }
+    }
+    float o[256];
+    double od[256];
+    for (int d = 0; d < D; d++) {
+        o[d] = 0.0f;
+        od[d] = 0.0;
+    }
+    for (int j = 0; j < span; j++) {
+        int seen = !ring || j == st->write || st->valid[j];
+        if (!seen) continue;
+        load_row(st, 1, layer, j, h, kbuf);
+        for (int d = 0; d < D; d++) o[d] = o[d] + sbuf[j] * kbuf[d];
+        if (out64)
+            for (int d = 0; d < D; d++) od[d] += dbuf[j] * (double)kbuf[d];
+    }
+    for (int d = 0; d < D; d++) {
+        out[d] = round_act(o[d] / l, st->adt);
+        if (out64) out64[d] = od[d] / ld;
+    }
+}
+
+int orc_attention(orc_stream *st, int layer, int t, const float *q, float scale, float *out,
+                  double *out64) {
+    if (layer < 0 || layer >= st->L) return fail("layer %d of %d", layer, st->L);
+    if (check_append(st, t)) return -1;
+    int H = st->H, D = st->D;
+    float *cs = malloc(sizeof(float) * D), *sn = cs + D / 2;
+    float *qw = malloc(sizeof(float) * D * 2), *qp = qw + D;
+    int span_max = (st->ring != ORC_RING_NONE ? st->cap : st->current_end + t) + 1;
+    float *sbuf = malloc(sizeof(float) * span_max);
+    double *dbuf = malloc(sizeof(double) * span_max);
+    for (int i = 0; i < t; i++) {
+        for (int h = 0; h < H; h++) {
+            const float *src = q + ((size_t)i * H + h) * D;
+            int p = st->current_end + i;
+            int pw = p + (st->ring == ORC_RING_ABSOLUTE ? st->shift : 0);
+            memcpy(qw, src, D * 4);
+            orc_rope_row(D, st->theta, (float)pw, st->adt, cs, sn);
+            orc_rotate(D, qw, cs, sn, st->adt);
+            memcpy(qp, src, D * 4);
+            orc_rope_row(D, st->theta, (float)p, st->adt, cs, sn);
+            orc_rotate(D, qp, cs, sn, st->adt);
+            attend_one(st, layer, i, h, qw, qp, scale, out + ((size_t)i * H + h) * D,
+                       out64 ? out64 + ((size_t)i * H + h) * D : NULL, sbuf, dbuf);
+        }
+    }
+    free(cs);
+    free(qw);
+    free(sbuf);
+    free(dbuf);
+    return 0;
+}
+
+/* Appending row i of a ring before attending to it: attention must see the new row, which in
+ * the reference is valid from complete_kv on (transformer.rs:74-79).  The oracle keeps the ring
+ * fields untouched until orc_commit, so attention treats the write slot as seen explicitly. */
+int orc_attend(orc_stream *st, int layer, int t, const float *q, const float *k,
+               const float *v, float scale, float *out, double *out64) {
+    if (orc_append(st, layer, t, k, v)) return -1;
+    return orc_attention(st, layer, t, q, scale, out, out64);
+}
+
+int orc_commit(orc_stream *st, int t) {
+    if (check_append(st, t)) return -1;
+    if (st->ring != ORC_RING_NONE) {
+        st->valid[st->write] = 1;
+        if (st->write + 1 > st->filled) st->filled = st->write + 1;
+    }
+    st->current_end += t;
+    return 0;
+}
+
+int orc_advance(orc_stream *st, int n) {
+    if (st->ring != ORC_RING_NONE) return fail("a ring cache steps one row at a time");
+    if (n < 0 || st->current_end + n > st->cap)
+        return fail("no room left: the cache holds %d positions", st->cap);
+    st->current_end += n;
+    return 0;
+}
+
+/* ---------------------------------------------------------------------------------------- */
+/* ring: transformer.rs:842-929                                                             */
+
+int orc_start_ring(orc_stream *st, int mode, int prefix) {
+    if (mode != ORC_RING_SHIFT && mode != ORC_RING_ABSOLUTE) return fail("bad ring mode %d", mode);
+    if (st->ring != ORC_RING_NONE) return fail("the cache is a ring already");
+    if (prefix < 0 || prefix > st->cap) return fail("prefix %d of a %d-slot cache", prefix, st->cap);
+    int used = st->current_end;
+    for (int s = 0; s < st->cap; s++) st->valid[s] = s < used;
+    st->ring = mode;
+    st->write = used;
+    st->filled = used;
+    st->prefix = mode == ORC_RING_ABSOLUTE ? prefix : 0;
+    st->shift = 0;
+    return 0;
+}
+
+int orc_set_ring_slot(orc_stream *st, int slot) {
+    if (st->ring == ORC_RING_NONE) return fail("not a ring cache, see start_ring");
+    if (slot < 0 || slot >= st->cap) return fail("slot %d of a %d-slot ring", slot, st->cap);
+    st->write = slot;
+    return 0;
+}
+
+int orc_evict(orc_stream *st, int prefix, const int *slots, int count) {
+    if (st->ring == ORC_RING_NONE) return fail("not a ring cache, see start_ring");
+    if (count > st->current_end)
+        return fail("cannot evict %d of %d positions", count, st->current_end);
+    if (st->ring == ORC_RING_ABSOLUTE && prefix != st->prefix)
+        return fail("an absolute ring evicts past its prefix %d, not %d", st->prefix, prefix);
+    if (st->ring == ORC_RING_SHIFT && st->cdt == ORC_I8)
+        return fail("an int8 cache evicts on an absolute ring");
+    /* Every slot is checked before any changes (transformer.rs:896-901). */
+    for (int j = 0; j < count; j++) {
+        int s = slots[j];
+        if (s < prefix || s < 0 || s >= st->cap || !st->valid[s])
+            return fail("slot %d holds no row past the prefix", s);
+    }
+    for (int j = 0; j < count; j++) st->valid[slots[j]] = 0;
+    if (st->ring == ORC_RING_SHIFT && count > 0) {
+        /* transformer.rs:905-925: every kept row past the prefix is rotated by -count where
+         * it lies, with the shift_back table of rope.rs:26-35 (rows of position -count). */
+        int D = st->D;
+        float *cs = malloc(sizeof(float) * D), *sn = cs + D / 2, *x = malloc(sizeof(float) * D);
+        orc_rope_row(D, st->theta, -(float)count, st->adt, cs, sn);
+        for (int s = prefix; s < st->filled; s++) {
+            if (!st->valid[s]) continue;
+            for (int layer = 0; layer < st->L; layer++)
+                for (int h = 0; h < st->H; h++) {
+                    for (int d = 0; d < D; d++) x[d] = get(st, 0, layer, s, h, d);
+                    orc_rotate(D, x, cs, sn, st->adt);
+                    store_row(st, 0, layer, s, h, x);
+                }
+        }
+        free(cs);
+        free(x);
+    }
+    if (st->ring == ORC_RING_ABSOLUTE) st->shift += count;
+    st->current_end -= count;
+    return 0;
+}
+
+/* ---------------------------------------------------------------------------------------- */
+/* with_seq_budget: transformer.rs:350-392                                                  */
+
+orc_stream *orc_with_seq_budget(const orc_stream *st, int budget) {
+    if (st->ring != ORC_RING_NONE) {
+        fail("a ring cache cannot be resized");
+        return NULL;
+    }
+    int used = st->current_end;
+    if (used > budget) {
+        fail("cannot fit %d filled KV positions into a budget of %d", used, budget);
+        return NULL;
+    }
+    orc_stream *dst = orc_open(st->L, st->H, st->KVH, st->D, budget, st->cdt, st->adt, st->theta);
+    size_t row = (size_t)st->H * st->D * esize(st->cdt);
+    for (int kv = 0; kv < 2; kv++)
+        for (int layer = 0; layer < st->L; layer++) {
+            memcpy((char *)dst->kc[kv] + idx(dst, layer, 0, 0) * esize(st->cdt),
+                   (char *)st->kc[kv] + idx(st, layer, 0, 0) * esize(st->cdt), row * used);
+            if (st->cdt == ORC_I8) {
+                int nb = (used + ORC_BLOCK - 1) / ORC_BLOCK;
+                memcpy(scale_at(dst, kv, layer, 0, 0), scale_at(st, kv, layer, 0, 0),
+                       sizeof(float) * nb * st->H);
+            }
+        }
+    dst->current_end = used;
+    return dst;
+}
+
+/* ---------------------------------------------------------------------------------------- */
+/* raw rows                                                                                 */
+
+static int check_rows(const orc_stream *st, int layer, int kv, int slot0, int n) {
+    if (layer < 0 || layer >= st->L || kv < 0 || kv > 1) return fail("bad layer or kv");
+    if (slot0 < 0 || n < 0 || slot0 + n > st->cap)
+        return fail("rows %d..%d of a %d-slot cache", slot0, slot0 + n, st->cap);
+    return 0;
+}
+
+int orc_read_rows(const orc_stream *st, int layer, int kv, int slot0, int n, float *vals,
+                  int8_t *q8, float *scales) {
+    if (check_rows(st, layer, kv, slot0, n)) return -1;
+    int H = st->H, D = st->D;
+    for (int s = 0; s < n; s++)
+        for (int h = 0; h < H; h++)
+            for (int d = 0; d < D; d++) {
+                size_t o = ((size_t)s * H + h) * D + d;
+                if (vals) vals[o] = get(st, kv, layer, slot0 + s, h, d);
+                if (q8 && st->cdt == ORC_I8)
+                    q8[o] = ((int8_t *)st->kc[kv])[idx(st, layer, slot0 + s, h) + d];
+            }
+    if (scales && st->cdt == ORC_I8 && n > 0) {
+        int b0 = slot0 / ORC_BLOCK, b1 = (slot0 + n - 1) / ORC_BLOCK;
+        for (int b = b0; b <= b1; b++)
+            memcpy(scales + (size_t)(b - b0) * H, scale_at(st, kv, layer, b, 0), sizeof(float) * H);
+    }
+    return 0;
+}
+
+int orc_write_rows(orc_stream *st, int layer, int kv, int slot0, int n, const float *vals,
+                   const int8_t *q8, const float *scales) {
+    if (check_rows(st, layer, kv, slot0, n)) return -1;
+    int H = st->H, D = st->D;
+    for (int s = 0; s < n; s++)
+        for (int h = 0; h < H; h++) {
+            size_t o = ((size_t)s * H + h) * D;
+            size_t i = idx(st, layer, slot0 + s, h);
+            if (st->cdt == ORC_F32)
+                memcpy((float *)st->kc[kv] + i, vals + o, D * 4);
+            else if (st->cdt == ORC_BF16)
+                for (int d = 0; d < D; d++) ((uint16_t *)st->kc[kv])[i + d] = bf16_bits(vals[o + d]);
+            else
+                memcpy((int8_t *)st->kc[kv] + i, q8 + o, D);
+        }
+    if (st->cdt == ORC_I8 && n > 0) {
+        int b0 = slot0 / ORC_BLOCK, b1 = (slot0 + n - 1) / ORC_BLOCK;
+        for (int b = b0; b <= b1; b++)
+            memcpy(scale_at(st, kv, layer, b, 0), scales + (size_t)(b - b0) * H, sizeof(float) * H);
+    }
+    return 0;
+}
+
+/* ---------------------------------------------------------------------------------------- */
+/* batched CPU step (the CPU baseline): one thread per stream, OpenMP across streams        */
+
+int orc_batch_attend(orc_stream **streams, int n, int layer, const float *q, const float *k,
+                     const float *v, float scale, float *out) {
+    if (n <= 0) return 0;
+    int H = streams[0]->H, KVH = streams[0]->KVH, D = streams[0]->D;
+    int bad = 0;
+#pragma omp parallel for schedule(dynamic, 1) reduction(| : bad)
+    for (int i = 0; i < n; i++) {
+        bad |= orc_attend(streams[i], layer, 1, q + (size_t)i * H * D, k + (size_t)i * KVH * D,
+                          v + (size_t)i * KVH * D, scale, out + (size_t)i * H * D, NULL) != 0;
+    }
+    return bad ? fail("a stream refused the step") : 0;
+}
+
+int orc_batch_commit(orc_stream **streams, int n) {
+    for (int i = 0; i < n; i++)
+        if (orc_commit(streams[i], 1)) return -1;
+    return 0;
+}
+
+int orc_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}

@@ -1,0 +1,106 @@
+/*
+ * oracle.h -- CPU restatement of the reference's flow-LM KV-cache path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This is the checker that the HIP library is compared against:
+ * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load it.  Nothing in
+ * the product (xn-ptts_amd/) links, imports or calls it.
+ *
+ * It restates, per stream and batch 1, what the reference computes below the projections of
+ * StreamingMultiheadAttention::forward (ptts/src/transformer.rs:183-251):
+ *   - the contiguous cache [S_cap][H][D] per layer for K and V (StreamingMHAState,
+ *     transformer.rs:14-25; init_state 169-180), zero-filled;
+ *   - RoPE tables (rope.rs:37-63) and the interleaved-pair rotation (rope.rs:74-95);
+ *   - complete_kv (transformer.rs:61-92): append at current_end or at the ring's write slot;
+ *   - single-query decode attention (sdpa_decode, transformer.rs:223,230) and causal prefill
+ *     (transformer.rs:231-248), both over the cache after the append;
+ *   - the ring: start_ring / set_ring_slot / evict (transformer.rs:842-929) and its decode mask
+ *     (transformer.rs:42-52);
+ *   - with_seq_budget (transformer.rs:350-392) and advance (transformer.rs:337-344).
+ * Two things the reference does not have are restated the way the HIP library defines them:
+ * the int8 cache with per-(block, head) scales, and the "absolute" ring whose eviction keeps
+ * keys at their write-time rotation (see orc_start_ring).
+ *
+ * Arithmetic: f32, no contraction (built with -ffp-contract=off), left-to-right sums.  Every
+ * output also has an f64 companion computed from the same rounded operands.
+ */
+#ifndef XNP_ORACLE_H
+#define XNP_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ORC_F32 = 0, ORC_BF16 = 1, ORC_I8 = 2 };
+enum { ORC_RING_NONE = 0, ORC_RING_SHIFT = 1, ORC_RING_ABSOLUTE = 2 };
+#define ORC_BLOCK 16
+
+typedef struct orc_stream orc_stream;
+
+/* --- element helpers ---------------------------------------------------------------------- */
+float orc_bf16_round(float x);
+/* Quantize y against scale s: 0 when s == 0, else rint(y / s) clamped to [-127, 127]. */
+int8_t orc_quant(float y, float s);
+
+/* --- RoPE (rope.rs:37-63, 74-95) ------------------------------------------------------------ */
+/* cos/sin of one position: inv_freq[i] = 1 / theta^(i / (D/2)), angle = pos * inv_freq[i],
+ * each value rounded to the activation dtype (T::from_f32 in rope.rs:55-56). */
+void orc_rope_row(int head_dim, float max_period, float pos, int act_dtype, float *cos_out,
+                  float *sin_out);
+/* Rotate pairs (2i, 2i+1) of x[head_dim] in place, then round to act_dtype. */
+void orc_rotate(int head_dim, float *x, const float *cos_row, const float *sin_row,
+                int act_dtype);
+
+/* --- one stream's state ---------------------------------------------------------------------- */
+orc_stream *orc_open(int layers, int heads, int kv_heads, int head_dim, int capacity,
+                     int cache_dtype, int act_dtype, float max_period);
+void orc_close(orc_stream *st);
+int orc_current_end(const orc_stream *st);
+int orc_capacity(const orc_stream *st);
+/* ring fields: mode, write, filled, prefix, shift; valid[capacity] copied when non-null */
+void orc_ring_info(const orc_stream *st, int *mode, int *write, int *filled, int *prefix,
+                   int *shift, uint8_t *valid);
+
+/* One layer of one step: rotate q and k at the step's position, append k and v (complete_kv),
+ * attend.  q [t][H][D], k and v [t][KVH][D] hold activation values (bf16-representable when
+ * act_dtype is bf16), out [t][H][D] receives the attention output rounded to act_dtype and
+ * out64 (nullable) the same in f64 without the final rounding.  Every layer of a step appends
+ * at the same position; orc_commit(t) then advances the stream, as complete_kv does per layer.
+ * Returns 0, or -1 with orc_last_error() set and nothing changed. */
+int orc_attend(orc_stream *st, int layer, int t, const float *q, const float *k,
+               const float *v, float scale, float *out, double *out64);
+/* The two halves of orc_attend, as the HIP library also exposes them. */
+int orc_append(orc_stream *st, int layer, int t, const float *k, const float *v);
+int orc_attention(orc_stream *st, int layer, int t, const float *q, float scale, float *out,
+                  double *out64);
+int orc_commit(orc_stream *st, int t);
+/* Count n more filled positions written by orc_write_rows (transformer.rs:337-344). */
+int orc_advance(orc_stream *st, int n);
+
+int orc_start_ring(orc_stream *st, int mode, int prefix);
+int orc_set_ring_slot(orc_stream *st, int slot);
+int orc_evict(orc_stream *st, int prefix, const int *slots, int count);
+/* with_seq_budget: a fresh stream of `budget` positions holding a copy of the filled prefix. */
+orc_stream *orc_with_seq_budget(const orc_stream *st, int budget);
+
+/* Raw cache rows [slot0, slot0+n) of one layer, kv = 0 (keys) or 1 (values).
+ * vals [n][H][D]: the stored values as f32 (dequantized for int8).
+ * q8 [n][H][D] and scales [nblk][H] (blocks slot0/16 .. (slot0+n-1)/16): int8 caches only. */
+int orc_read_rows(const orc_stream *st, int layer, int kv, int slot0, int n, float *vals,
+                  int8_t *q8, float *scales);
+int orc_write_rows(orc_stream *st, int layer, int kv, int slot0, int n, const float *vals,
+                   const int8_t *q8, const float *scales);
+
+/* Many streams, one layer: the CPU baseline's batched step (OpenMP over streams). */
+int orc_batch_attend(orc_stream **streams, int n, int layer, const float *q, const float *k,
+                     const float *v, float scale, float *out);
+int orc_batch_commit(orc_stream **streams, int n);
+int orc_threads(void);
+
+const char *orc_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,229 @@
+"""ctypes wrapper of liboracle.so, the CPU restatement of the reference's KV-cache path.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's CPU
+baseline leg, as the checker.  The product (xn-ptts_amd/) never imports it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liboracle.so")
+F32, BF16, I8 = 0, 1, 2
+RING_NONE, RING_SHIFT, RING_ABSOLUTE = 0, 1, 2
+DT = {"f32": F32, "bf16": BF16, "i8": I8}
+MODES = {"shift": RING_SHIFT, "absolute": RING_ABSOLUTE}
+
+_lib = None
+_fp = ctypes.POINTER(ctypes.c_float)
+_dp = ctypes.POINTER(ctypes.c_double)
+_ip = ctypes.POINTER(ctypes.c_int)
+_i8p = ctypes.POINTER(ctypes.c_int8)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built: make -C oracle")
+        L = ctypes.CDLL(LIB_PATH)
+        sig = {
+            "orc_bf16_round": (ctypes.c_float, [ctypes.c_float]),
+            "orc_quant": (ctypes.c_int8, [ctypes.c_float, ctypes.c_float]),
+            "orc_rope_row": (None, [ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_int, _fp, _fp]),
+            "orc_rotate": (None, [ctypes.c_int, _fp, _fp, _fp, ctypes.c_int]),
+            "orc_open": (ctypes.c_void_p, [ctypes.c_int] * 7 + [ctypes.c_float]),
+            "orc_close": (None, [ctypes.c_void_p]),
+            "orc_current_end": (ctypes.c_int, [ctypes.c_void_p]),
+            "orc_capacity": (ctypes.c_int, [ctypes.c_void_p]),
+            "orc_ring_info": (None, [ctypes.c_void_p, _ip, _ip, _ip, _ip, _ip, _u8p]),
+            "orc_attend": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, _fp, _fp, _fp,
+                                          ctypes.c_float, _fp, _dp]),
+            "orc_append": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, _fp, _fp]),
+            "orc_attention": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, _fp,
+                                             ctypes.c_float, _fp, _dp]),
+            "orc_commit": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+            "orc_advance": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+            "orc_start_ring": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int]),
+            "orc_set_ring_slot": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+            "orc_evict": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _ip, ctypes.c_int]),
+            "orc_with_seq_budget": (ctypes.c_void_p, [ctypes.c_void_p, ctypes.c_int]),
+            "orc_read_rows": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                             ctypes.c_int, _fp, _i8p, _fp]),
+            "orc_write_rows": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                              ctypes.c_int, _fp, _i8p, _fp]),
+            "orc_batch_attend": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int, ctypes.c_int,
+                                                _fp, _fp, _fp, ctypes.c_float, _fp]),
+            "orc_batch_commit": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int]),
+            "orc_threads": (ctypes.c_int, []),
+            "orc_last_error": (ctypes.c_char_p, []),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+class OracleError(RuntimeError):
+    pass
+
+
+def _ok(rc):
+    if rc != 0:
+        raise OracleError(lib().orc_last_error().decode())
+
+
+def _f32(a):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    return a, a.ctypes.data_as(_fp)
+
+
+def bf16_round(x: float) -> float:
+    return lib().orc_bf16_round(x)
+
+
+def quant(y: float, s: float) -> int:
+    return lib().orc_quant(y, s)
+
+
+def rope_row(head_dim: int, max_period: float, pos: float, act: str = "f32"):
+    c = np.zeros(head_dim // 2, np.float32)
+    s = np.zeros(head_dim // 2, np.float32)
+    lib().orc_rope_row(head_dim, max_period, pos, DT[act], c.ctypes.data_as(_fp), s.ctypes.data_as(_fp))
+    return c, s
+
+
+def rotate(x, cos_row, sin_row, act: str = "f32"):
+    x, xp = _f32(np.array(x, np.float32, copy=True))
+    c, cp = _f32(cos_row)
+    s, sp = _f32(sin_row)
+    lib().orc_rotate(x.shape[-1], xp, cp, sp, DT[act])
+    return x
+
+
+class Stream:
+    """One stream's StreamingMHAState over all layers, contiguous [S_cap][H][D] per layer."""
+
+    def __init__(self, layers, heads, head_dim, capacity, cache="f32", act="f32", kv_heads=None,
+                 max_period=10000.0, _handle=None):
+        self.L, self.H, self.D = layers, heads, head_dim
+        self.KVH = kv_heads or heads
+        self.cache, self.act = cache, act
+        self.max_period = max_period
+        if _handle is None:
+            _handle = lib().orc_open(layers, heads, self.KVH, head_dim, capacity, DT[cache], DT[act], max_period)
+            if not _handle:
+                raise OracleError(lib().orc_last_error().decode())
+        self.h = _handle
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().orc_close(self.h)
+            self.h = None
+
+    @property
+    def current_end(self):
+        return lib().orc_current_end(self.h)
+
+    @property
+    def capacity(self):
+        return lib().orc_capacity(self.h)
+
+    def ring_info(self):
+        vals = [ctypes.c_int() for _ in range(5)]
+        valid = np.zeros(max(self.capacity, 1), np.uint8)
+        lib().orc_ring_info(self.h, *[ctypes.byref(v) for v in vals], valid.ctypes.data_as(_u8p))
+        mode, write, filled, prefix, shift = [v.value for v in vals]
+        return dict(mode=mode, write=write, filled=filled, prefix=prefix, shift=shift,
+                    valid=valid[:self.capacity].astype(bool))
+
+    def attend(self, layer, q, k, v, scale=0.125):
+        q, qp = _f32(q)
+        k, kp = _f32(k)
+        v, vp = _f32(v)
+        t = q.shape[0]
+        out = np.zeros((t, self.H, self.D), np.float32)
+        out64 = np.zeros((t, self.H, self.D), np.float64)
+        _ok(lib().orc_attend(self.h, layer, t, qp, kp, vp, scale, out.ctypes.data_as(_fp),
+                             out64.ctypes.data_as(_dp)))
+        return out, out64
+
+    def append(self, layer, k, v):
+        k, kp = _f32(k)
+        v, vp = _f32(v)
+        _ok(lib().orc_append(self.h, layer, k.shape[0], kp, vp))
+
+    def attention(self, layer, q, scale=0.125):
+        q, qp = _f32(q)
+        t = q.shape[0]
+        out = np.zeros((t, self.H, self.D), np.float32)
+        out64 = np.zeros((t, self.H, self.D), np.float64)
+        _ok(lib().orc_attention(self.h, layer, t, qp, scale, out.ctypes.data_as(_fp),
+                                out64.ctypes.data_as(_dp)))
+        return out, out64
+
+    def commit(self, t=1):
+        _ok(lib().orc_commit(self.h, t))
+
+    def advance(self, n):
+        _ok(lib().orc_advance(self.h, n))
+
+    def start_ring(self, mode="shift", prefix=0):
+        _ok(lib().orc_start_ring(self.h, MODES[mode], prefix))
+
+    def set_ring_slot(self, slot):
+        _ok(lib().orc_set_ring_slot(self.h, slot))
+
+    def evict(self, prefix, slots):
+        arr = (ctypes.c_int * max(len(slots), 1))(*slots)
+        _ok(lib().orc_evict(self.h, prefix, arr, len(slots)))
+
+    def with_seq_budget(self, budget):
+        h = lib().orc_with_seq_budget(self.h, budget)
+        if not h:
+            raise OracleError(lib().orc_last_error().decode())
+        return Stream(self.L, self.H, self.D, budget, self.cache, self.act, self.KVH, self.max_period, _handle=h)
+
+    def read_rows(self, layer, kv, slot0, n):
+        vals = np.zeros((n, self.H, self.D), np.float32)
+        q8 = np.zeros((n, self.H, self.D), np.int8)
+        nb = ((slot0 + n - 1) // 16 - slot0 // 16 + 1) if n > 0 else 0
+        scales = np.zeros((max(nb, 1), self.H), np.float32)
+        _ok(lib().orc_read_rows(self.h, layer, kv, slot0, n, vals.ctypes.data_as(_fp),
+                                q8.ctypes.data_as(_i8p), scales.ctypes.data_as(_fp)))
+        return vals, q8, scales[:nb]
+
+    def write_rows(self, layer, kv, slot0, vals=None, q8=None, scales=None):
+        n = (vals if vals is not None else q8).shape[0]
+        v, vp = _f32(vals if vals is not None else np.zeros((n, self.H, self.D), np.float32))
+        q = np.ascontiguousarray(q8 if q8 is not None else np.zeros((n, self.H, self.D), np.int8), np.int8)
+        s, sp = _f32(scales if scales is not None else np.zeros((max(n // 16 + 2, 1), self.H), np.float32))
+        _ok(lib().orc_write_rows(self.h, layer, kv, slot0, n, vp, q.ctypes.data_as(_i8p), sp))
+
+
+def batch_attend(streams, layer, q, k, v, scale=0.125):
+    """One layer of a batched decode step over `streams`, OpenMP across streams."""
+    n = len(streams)
+    arr = (ctypes.c_void_p * n)(*[s.h for s in streams])
+    q, qp = _f32(q)
+    k, kp = _f32(k)
+    v, vp = _f32(v)
+    out = np.zeros_like(q)
+    _ok(lib().orc_batch_attend(arr, n, layer, qp, kp, vp, scale, out.ctypes.data_as(_fp)))
+    return out
+
+
+def batch_commit(streams):
+    n = len(streams)
+    arr = (ctypes.c_void_p * n)(*[s.h for s in streams])
+    _ok(lib().orc_batch_commit(arr, n))
+
+
+def threads() -> int:
+    return lib().orc_threads()

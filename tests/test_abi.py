@@ -1,0 +1,271 @@
+"""CPU tests of the C ABI (libxnp_kv.so) that run no kernel: exported symbols, and the host
+logic -- page allocator, stream state, ring state machine, batch bookkeeping, refusals -- through
+a host-only pool (XNP_POOL_HOST_ONLY), checked against the oracle and the reference's rules."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from conftest import ROOT, oracle, xnp
+
+HEADER = os.path.join(ROOT, "include", "xnp_kv.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const char \*|xnp_status|int32_t)\s*(xnp_\w+)\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(xnp.LIB_PATH)
+    names = declared_symbols()
+    assert len(names) == len(xnp.kv.SIGNATURES)
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    # and the Python binding covers each one
+    assert set(names) <= set(xnp.kv.SIGNATURES)
+
+
+def pool(**kw):
+    args = dict(num_layers=2, num_heads=4, num_blocks=64, max_streams=8, max_blocks_per_stream=8,
+                cache_dtype="f32", act_dtype="f32", host_only=True, max_pos=512)
+    args.update(kw)
+    return xnp.KvPool(**args)
+
+
+def test_budgets_follow_plan_rs():
+    # plan.rs:43-54: frame_budget(64 tokens) = ceil((64/3 + 2) * 12.5) = 292; seq = 64 + 512 + 292
+    assert xnp.frame_budget(64, 12.5) == 292
+    assert xnp.seq_budget(64, 292) == 868
+    assert xnp.frame_budget(0, 12.5) == 25
+
+
+def test_bad_configs_are_refused():
+    for heads, kvh in [(3, 2), (4, 3), (4, 0)]:
+        with pytest.raises(xnp.XnpError) as e:
+            pool(num_heads=heads, num_kv_heads=kvh)
+        assert e.value.name == "XNP_E_HEADS" and "heads" in e.value.message
+    with pytest.raises(xnp.XnpError, match="head_dim"):
+        pool(head_dim=32)
+    with pytest.raises(xnp.XnpError, match="not supported"):
+        pool(cache_dtype="bf16", act_dtype="f32")
+
+
+@pytest.mark.parametrize("act", ["f32", "bf16"])
+def test_rope_table_is_the_oracles_bit_for_bit(act):
+    p = pool(cache_dtype=act, act_dtype=act, max_pos=4096)
+    table = p.rope_rows(0, 4096)
+    for pos in [0, 1, 2, 17, 255, 1000, 2047, 4095]:
+        c, s = oracle.rope_row(64, 10000.0, float(pos), act)
+        assert np.array_equal(table[pos, :, 0].view(np.uint32), c.view(np.uint32))
+        assert np.array_equal(table[pos, :, 1].view(np.uint32), s.view(np.uint32))
+
+
+def test_pages_are_taken_as_rows_arrive_and_returned_on_close():
+    p = pool()
+    a = p.init_state(100)
+    assert p.stats()["free_blocks"] == 64 and p.blocks(a) == [-1] * 7
+    p.begin([a], t=20)
+    assert p.stats()["free_blocks"] == 62
+    p.end()
+    assert p.current_end(a) == 20
+    p.begin([a], t=1)
+    p.end()
+    assert p.stats()["free_blocks"] == 62  # row 20 lands in page 1
+    p.advance(a, 12)  # rows 21..32: page 2 for row 32
+    assert p.current_end(a) == 33 and p.stats()["free_blocks"] == 61
+    p.close(a)
+    assert p.stats()["free_blocks"] == 64 and p.stats()["open_streams"] == 0
+
+
+def test_shuffled_pages_are_a_permutation():
+    p = pool(num_blocks=32, page_seed=20261201, max_blocks_per_stream=32)
+    a = p.init_state(32 * 16)
+    p.advance(a, 32 * 16)
+    pages = p.blocks(a)
+    assert sorted(pages) == list(range(32)) and pages != list(range(32))
+
+
+def test_capacity_and_out_of_blocks_are_refused_and_change_nothing():
+    p = pool(num_blocks=4)
+    a, b = p.init_state(40), p.init_state(40)
+    with pytest.raises(xnp.XnpError) as e:
+        p.begin([a], t=41)
+    assert e.value.name == "XNP_E_NO_ROOM" and "no room left" in e.value.message
+    p.begin([a], t=40)  # 3 pages
+    p.end()
+    with pytest.raises(xnp.XnpError) as e:
+        p.begin([b], t=17)  # 2 pages, 1 free
+    assert e.value.name == "XNP_E_OUT_OF_BLOCKS"
+    assert p.stats()["free_blocks"] == 1 and p.current_end(b) == 0 and p.stats()["batch_open"] == 0
+    with pytest.raises(xnp.XnpError) as e:
+        p.begin([b, 99], t=1)
+    assert e.value.name == "XNP_E_STREAM"
+    with pytest.raises(xnp.XnpError, match="twice"):
+        p.begin([b, b], t=1)
+    with pytest.raises(xnp.XnpError) as e:
+        p.init_state(8 * 16 + 1)
+    assert e.value.name == "XNP_E_INVALID"
+
+
+def test_abort_gives_back_the_pages_and_keeps_the_state():
+    p = pool()
+    a, b = p.init_state(64), p.init_state(64)
+    p.begin([a, b], t=1)
+    assert p.stats()["free_blocks"] == 62
+    p.abort()
+    assert p.stats()["free_blocks"] == 64 and p.current_end(a) == 0
+    with pytest.raises(xnp.XnpError) as e:
+        p.end()
+    assert e.value.name == "XNP_E_STATE"
+
+
+def test_kernel_calls_on_a_host_only_pool_are_refused():
+    p = pool()
+    a = p.init_state(16)
+    p.begin([a])
+    for call in (lambda: p.append(0, None, None), lambda: p.decode(0, None, None, 0.125)):
+        with pytest.raises(xnp.XnpError) as e:
+            call()
+        assert e.value.name == "XNP_E_STATE"
+    with pytest.raises(xnp.XnpError) as e:
+        p.close(a)  # a batch is open
+    assert e.value.name == "XNP_E_STATE"
+    p.abort()
+
+
+def test_decode_work_is_split_in_even_chunks_per_stream():
+    p = pool(max_blocks_per_stream=64, chunk_blocks=4, num_blocks=256, max_pos=2048)
+    ids = [p.init_state(1024) for _ in range(3)]
+    for sid, n in zip(ids, [0, 64, 1000]):
+        p.advance(sid, n)
+    p.begin(ids)
+    # spans 1, 65 and 1001 slots: 1, 5 and 63 pages; chunks of at most 4 pages
+    assert p.stats()["work_items"] == 1 + 2 + 16
+    p.abort()
+
+
+# ---- with_seq_budget (transformer.rs:350-392) ------------------------------------------------
+def test_fork_shares_full_pages_and_copies_the_partial_one():
+    p = pool()
+    a = p.init_state(128)
+    p.advance(a, 40)  # pages 0, 1 full; 2 partial
+    free = p.stats()["free_blocks"]
+    b = p.with_seq_budget(a, 100)
+    ia, ib = p.info(a), p.info(b)
+    assert ib["current_end"] == 40 and ib["capacity"] == 100
+    assert p.blocks(b)[:2] == p.blocks(a)[:2] and p.blocks(b)[2] != p.blocks(a)[2]
+    assert ia["shared"] == 2 and ib["shared"] == 2 and p.stats()["free_blocks"] == free - 1
+    p.close(a)
+    assert p.info(b)["shared"] == 0 and p.stats()["free_blocks"] == free - 1 + 1
+    with pytest.raises(xnp.XnpError) as e:
+        p.with_seq_budget(b, 39)
+    assert e.value.name == "XNP_E_BUDGET" and "40" in e.value.message and "39" in e.value.message
+    p.with_seq_budget(b, 40)
+
+
+def test_a_ring_cannot_be_forked_and_starting_one_unshares():
+    p = pool()
+    a = p.init_state(64)
+    p.advance(a, 32)
+    b = p.with_seq_budget(a, 64)
+    assert p.info(b)["shared"] == 2
+    p.start_ring(b)
+    assert p.info(b)["shared"] == 0 and p.info(a)["shared"] == 0
+    with pytest.raises(xnp.XnpError) as e:
+        p.with_seq_budget(b, 64)
+    assert e.value.name == "XNP_E_BUDGET" and "ring" in e.value.message
+
+
+# ---- ring state machine vs the oracle (transformer.rs:842-929, 1397-1416) ----------------------
+def test_misuse_of_a_ring_is_refused_like_the_oracle():
+    p = pool(num_heads=4)
+    st = oracle.Stream(2, 4, 64, 8)
+    a = p.init_state(8)
+    p.begin([a], t=4)
+    p.end()
+    st.advance(4)
+    both = [(lambda f: f(p, a), lambda g: g(st))]
+
+    def same(fp, fo):
+        errs = []
+        for f in (lambda: fp(), lambda: fo()):
+            try:
+                f()
+                errs.append(None)
+            except (xnp.XnpError, oracle.OracleError) as e:
+                errs.append(str(e).split(": ", 1)[-1])
+        assert errs[0] == errs[1], errs
+        return errs[0]
+
+    assert "not a ring" in same(lambda: p.set_ring_slot(a, 4), lambda: st.set_ring_slot(4))
+    same(lambda: p.start_ring(a), lambda: st.start_ring("shift"))
+    same(lambda: p.set_ring_slot(a, 4), lambda: st.set_ring_slot(4))
+    assert "slot 8 of a 8-slot ring" in same(lambda: p.set_ring_slot(a, 8), lambda: st.set_ring_slot(8))
+
+    def step():
+        p.begin([a])
+        p.end()
+
+    def ostep():
+        st.append(0, np.zeros((1, 4, 64)), np.zeros((1, 4, 64)))
+        st.commit(1)
+
+    same(step, ostep)
+    for slots in ([2], [5], [4, 5]):
+        assert "holds no row past the prefix" in same(lambda: p.evict(a, 4, slots), lambda: st.evict(4, slots))
+    assert p.valid(a)[4]
+    same(lambda: p.set_ring_slot(a, 4), lambda: st.set_ring_slot(4))
+    assert "still holds a row" in same(step, ostep)
+    assert "cannot evict 6 of 5" in same(lambda: p.evict(a, 0, [0, 1, 2, 3, 4, 4]), lambda: st.evict(0, [0, 1, 2, 3, 4, 4]))
+    same(lambda: p.evict(a, 4, [4]), lambda: st.evict(4, [4]))
+    same(step, ostep)
+    info, oinfo = p.info(a), st.ring_info()
+    assert (info["ring_write"], info["ring_filled"], info["current_end"]) == (oinfo["write"], oinfo["filled"], st.current_end)
+    assert p.valid(a) == list(oinfo["valid"])
+    with pytest.raises(xnp.XnpError, match="one row at a time"):
+        p.begin([a], t=2)
+
+
+@pytest.mark.parametrize("mode", ["shift", "absolute"])
+def test_slide_is_the_s2s_session_policy(mode):
+    # s2s.rs:318-333 with a voice prefix of v = 5 and a context of 6: evict the oldest third when
+    # the context is full, then write at v + steps % context.  Restated in Python here.
+    p = pool(num_heads=4)
+    a = p.init_state(11)
+    p.begin([a], t=5)
+    p.end()
+    p.start_ring(a, mode, prefix=5)
+    v, context, in_view = 5, 6, 0
+    valid = [True] * 5 + [False] * 6
+    for steps in range(40):
+        if in_view == context:
+            oldest = steps - in_view
+            for j in range(context // 3):
+                valid[v + (oldest + j) % context] = False
+            in_view -= context // 3
+        write = v + steps % context
+        p.slide(a, v, context, context, context // 3, steps)
+        assert p.info(a)["ring_write"] == write and p.valid(a) == valid
+        p.begin([a])
+        p.end()
+        valid[write] = True
+        in_view += 1
+        assert p.info(a)["current_end"] == 5 + in_view
+
+
+def test_sliding_window_keeps_the_last_window_rows():
+    p = pool(num_heads=4, max_blocks_per_stream=40, num_blocks=128, max_pos=4096)
+    a = p.init_state(528)
+    p.start_ring(a, "absolute", prefix=0)
+    h0 = 1234
+    for n in range(700):
+        p.slide(a, 0, 528, 512, 1, h0 + n)
+        p.begin([a])
+        p.end()
+        info = p.info(a)
+        assert info["in_view"] == min(n + 1, 512)
+        assert info["ring_write"] == (h0 + n) % 528
+    assert info["ring_shift"] == 700 - 512 and info["current_end"] == 512

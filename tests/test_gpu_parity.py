@@ -1,0 +1,277 @@
+"""GPU parity: the HIP path (through the C ABI) against the oracle on the same seeded inputs.
+
+Bars (stated per test): cache contents -- every stored row, and int8 codes and scales -- equal the
+oracle's bit for bit; attention outputs are within 1e-5 relative (f32) or 2e-2 relative (bf16,
+int8 KV) of the oracle's f32 outputs, where relative error is max|got - want| / max|want| over
+each (row, head) vector.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import oracle, xnp
+from helpers import bf16_round, rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"f32": 1e-5, "bf16": 2e-2, "i8": 2e-2}
+TORCH_DT = {"f32": torch.float32, "bf16": torch.bfloat16}
+CACHE_TORCH = {"f32": torch.float32, "bf16": torch.bfloat16, "i8": torch.int8}
+DEV = "cuda:0"
+
+
+def dev(a, act):
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(DEV).to(TORCH_DT[act])
+
+
+def host(t):
+    return t.float().cpu().numpy()
+
+
+class Pair:
+    """A GPU pool and one oracle stream per GPU stream, driven in lockstep."""
+
+    def __init__(self, *, L=2, H=8, KVH=None, cache="bf16", act="bf16", streams=8, cap=256,
+                 chunk=0, seed=0, page_seed=0):
+        self.L, self.H, self.KVH = L, H, KVH or H
+        self.cache, self.act = cache, act
+        self.rng = np.random.default_rng(seed)
+        mbps = (cap + 15) // 16
+        self.pool = xnp.KvPool(num_layers=L, num_heads=H, num_kv_heads=self.KVH, num_blocks=streams * mbps * 2 + 8,
+                               max_streams=streams * 2 + 2, max_blocks_per_stream=mbps, cache_dtype=cache,
+                               act_dtype=act, max_pos=8192, page_seed=page_seed, chunk_blocks=chunk)
+        self.ids, self.orc = [], []
+        for _ in range(streams):
+            self.add(cap)
+
+    def add(self, cap):
+        self.ids.append(self.pool.init_state(cap))
+        self.orc.append(oracle.Stream(self.L, self.H, 64, cap, cache=self.cache, act=self.act, kv_heads=self.KVH))
+
+    def x(self, *shape):
+        a = self.rng.standard_normal(shape).astype(np.float32)
+        return bf16_round(a) if self.act == "bf16" else a
+
+    def fill(self, i, n):
+        """Append n rows to stream i through the multi-row append kernel (no attention)."""
+        if n == 0:
+            return
+        self.pool.begin([self.ids[i]], t=n)
+        for layer in range(self.L):
+            k, v = self.x(n, self.KVH, 64), self.x(n, self.KVH, 64)
+            self.pool.append(layer, dev(k, self.act), dev(v, self.act))
+            self.orc[i].append(layer, k, v)
+        self.pool.end()
+        self.orc[i].commit(n)
+
+    def step(self, which=None, fused=True, check=True):
+        which = list(range(len(self.ids))) if which is None else which
+        n = len(which)
+        self.pool.begin([self.ids[i] for i in which])
+        errs = []
+        for layer in range(self.L):
+            q, k, v = self.x(n, self.H, 64), self.x(n, self.KVH, 64), self.x(n, self.KVH, 64)
+            out = torch.empty((n, self.H, 64), dtype=TORCH_DT[self.act], device=DEV)
+            if fused:
+                self.pool.attend(layer, dev(q, self.act), dev(k, self.act), dev(v, self.act), out, 0.125)
+            else:
+                self.pool.append(layer, dev(k, self.act), dev(v, self.act))
+                self.pool.decode(layer, dev(q, self.act), out, 0.125)
+            torch.cuda.synchronize()
+            got = host(out)
+            for j, i in enumerate(which):
+                want, want64 = self.orc[i].attend(layer, q[j:j + 1], k[j:j + 1], v[j:j + 1])
+                errs.append(rel_err(got[j:j + 1], want))
+                if check:
+                    assert rel_err(got[j:j + 1], want) <= TOL[self.cache], (layer, i)
+        self.pool.end()
+        for i in which:
+            self.orc[i].commit(1)
+        return max(errs) if errs else 0.0
+
+    def assert_cache_equal(self, i, upto=None):
+        sid, st = self.ids[i], self.orc[i]
+        n = st.current_end if upto is None else upto
+        if st.ring_info()["mode"]:
+            n = st.ring_info()["filled"]
+        if n == 0:
+            return
+        valid = st.ring_info()["valid"] if st.ring_info()["mode"] else np.ones(st.capacity, bool)
+        for layer in range(self.L):
+            for kv in (0, 1):
+                rows = torch.empty((n, self.H, 64), dtype=CACHE_TORCH[self.cache], device=DEV)
+                nb = (n - 1) // 16 + 1
+                scales = torch.zeros((nb, self.H), dtype=torch.float32, device=DEV)
+                self.pool.read_rows(sid, layer, kv, 0, rows, scales if self.cache == "i8" else None)
+                torch.cuda.synchronize()
+                vals, q8, osc = st.read_rows(layer, kv, 0, n)
+                m = valid[:n]
+                if self.cache == "i8":
+                    g = rows.cpu().numpy()
+                    assert np.array_equal(g[m], q8[m]), (i, layer, kv)
+                    gs = scales.cpu().numpy()
+                    live = np.array([m[16 * b:16 * b + 16].any() for b in range(nb)])
+                    assert np.array_equal(gs[live].view(np.uint32), osc[live].view(np.uint32)), (i, layer, kv)
+                else:
+                    g = rows.float().cpu().numpy()
+                    assert np.array_equal(g[m].view(np.uint32), vals[m].view(np.uint32)), (i, layer, kv)
+
+
+# ---- linear caches -----------------------------------------------------------------------------
+@pytest.mark.parametrize("cache,act", [("bf16", "bf16"), ("f32", "f32"), ("i8", "bf16"), ("i8", "f32")])
+def test_append_and_decode_match_the_oracle(cache, act):
+    p = Pair(cache=cache, act=act, streams=8, cap=300, seed=1, page_seed=7)
+    lens = [0, 1, 15, 16, 17, 100, 200, 255]
+    for i, n in enumerate(lens):
+        p.fill(i, n)
+    for i in range(8):
+        p.assert_cache_equal(i)
+    for _ in range(3):
+        p.step()
+    for i in range(8):
+        p.assert_cache_equal(i)
+
+
+def test_one_row_returns_its_value_exactly():
+    p = Pair(cache="bf16", act="bf16", streams=2, cap=32, seed=2)
+    p.pool.begin(p.ids)
+    q, k, v = p.x(2, 8, 64), p.x(2, 8, 64), p.x(2, 8, 64)
+    out = torch.empty((2, 8, 64), dtype=torch.bfloat16, device=DEV)
+    p.pool.attend(0, dev(q, "bf16"), dev(k, "bf16"), dev(v, "bf16"), out, 0.125)
+    torch.cuda.synchronize()
+    p.pool.abort()
+    assert np.array_equal(host(out), v)
+
+
+def test_split_chunks_and_separate_calls_agree():
+    outs = []
+    for chunk, fused in [(1, True), (3, True), (64, True), (3, False)]:
+        p = Pair(cache="bf16", act="bf16", streams=4, cap=600, seed=3, chunk=chunk)
+        for i, n in enumerate([1, 37, 300, 590]):
+            p.fill(i, n)
+        p.pool.begin(p.ids)
+        q, k, v = p.x(4, 8, 64), p.x(4, 8, 64), p.x(4, 8, 64)
+        out = torch.empty((4, 8, 64), dtype=torch.bfloat16, device=DEV)
+        if fused:
+            p.pool.attend(0, dev(q, "bf16"), dev(k, "bf16"), dev(v, "bf16"), out, 0.125)
+        else:
+            p.pool.append(0, dev(k, "bf16"), dev(v, "bf16"))
+            p.pool.decode(0, dev(q, "bf16"), out, 0.125)
+        torch.cuda.synchronize()
+        p.pool.end()
+        outs.append(host(out))
+        want = np.concatenate([p.orc[i].attend(0, q[i:i + 1], k[i:i + 1], v[i:i + 1])[0] for i in range(4)])
+        assert rel_err(outs[-1], want) <= 2e-2
+    assert np.array_equal(outs[1], outs[3])  # the fused append changes nothing but the launch
+
+
+def test_grouped_kv_heads():
+    p = Pair(cache="bf16", act="bf16", H=8, KVH=2, streams=4, cap=128, seed=4)
+    for i, n in enumerate([3, 40, 64, 100]):
+        p.fill(i, n)
+    p.step()
+    p.step()
+    for i in range(4):
+        p.assert_cache_equal(i)
+
+
+def test_empty_batch_is_a_no_op():
+    p = Pair(streams=1, cap=16)
+    p.pool.begin([])
+    out = torch.empty((0, 8, 64), dtype=torch.bfloat16, device=DEV)
+    p.pool.attend(0, out, out, out, out, 0.125)
+    p.pool.end()
+    assert p.pool.current_end(p.ids[0]) == 0
+
+
+# ---- with_seq_budget: shared pages ----------------------------------------------------------------
+def test_fork_shares_the_prefix_and_diverges():
+    p = Pair(cache="bf16", act="bf16", streams=1, cap=128, seed=5)
+    p.fill(0, 40)
+    fid = p.pool.with_seq_budget(p.ids[0], 128)
+    p.ids.append(fid)
+    p.orc.append(p.orc[0].with_seq_budget(128))
+    for _ in range(3):
+        p.step()  # both append; the source's partial page must be left alone by the fork
+    p.assert_cache_equal(0)
+    p.assert_cache_equal(1)
+
+
+# ---- rings (transformer.rs:842-929) ----------------------------------------------------------------
+@pytest.mark.parametrize("cache,act,mode", [("f32", "f32", "shift"), ("bf16", "bf16", "shift"),
+                                            ("bf16", "bf16", "absolute"), ("i8", "bf16", "absolute")])
+def test_ring_sessions_match_the_oracle(cache, act, mode):
+    # The s2s policy on several streams at once: a voice prefix, then frames in a context of 24
+    # slots whose oldest third goes whenever it is full (s2s.rs:318-333).
+    p = Pair(cache=cache, act=act, streams=3, cap=64, seed=6)
+    v, context = [5, 16, 0], 24
+    for i in range(3):
+        p.fill(i, v[i])
+        p.pool.start_ring(p.ids[i], mode, prefix=v[i])
+        p.orc[i].start_ring(mode, prefix=v[i])
+    in_view = [0, 0, 0]
+    for steps in range(70):
+        for i in range(3):
+            if in_view[i] == context:
+                oldest = steps - in_view[i]
+                slots = [v[i] + (oldest + j) % context for j in range(context // 3)]
+                p.orc[i].evict(v[i], slots)
+                in_view[i] -= context // 3
+            p.orc[i].set_ring_slot(v[i] + steps % context)
+            p.pool.slide(p.ids[i], v[i], context, context, context // 3, steps)
+            assert p.pool.info(p.ids[i])["ring_write"] == p.orc[i].ring_info()["write"]
+        p.step()
+        for i in range(3):
+            in_view[i] += 1
+        if steps % 23 == 0 or steps == 69:
+            for i in range(3):
+                p.assert_cache_equal(i)
+
+
+def test_int8_sliding_window_with_random_write_heads():
+    # A window of 64 rows on a ring of 80 slots (window + one page), write heads at random
+    # offsets, one eviction per step once the window is full.
+    p = Pair(cache="i8", act="bf16", streams=4, cap=80, seed=7, L=1)
+    heads = [0, 5, 33, 79]
+    for i in range(4):
+        p.pool.start_ring(p.ids[i], "absolute", prefix=0)
+        p.orc[i].start_ring("absolute", prefix=0)
+    in_view = [0] * 4
+    for n in range(150):
+        for i in range(4):
+            step = heads[i] + n
+            if in_view[i] == 64:
+                p.orc[i].evict(0, [(step - 64) % 80])
+                in_view[i] -= 1
+            p.orc[i].set_ring_slot(step % 80)
+            p.pool.slide(p.ids[i], 0, 80, 64, 1, step)
+        p.step()
+        for i in range(4):
+            in_view[i] += 1
+    for i in range(4):
+        p.assert_cache_equal(i)
+
+
+# ---- raw rows ------------------------------------------------------------------------------------
+@pytest.mark.parametrize("cache", ["bf16", "i8"])
+def test_rows_written_raw_read_back_the_same(cache):
+    act = "bf16"
+    pool = xnp.KvPool(num_layers=2, num_heads=8, num_blocks=16, max_streams=2, max_blocks_per_stream=8,
+                      cache_dtype=cache, act_dtype=act, page_seed=3)
+    sid = pool.init_state(100)
+    pool.advance(sid, 70)
+    g = torch.Generator(device="cpu").manual_seed(0)
+    if cache == "i8":
+        rows = torch.randint(-127, 128, (50, 8, 64), generator=g, dtype=torch.int8).to(DEV)
+        scales = torch.rand((4, 8), generator=g).to(DEV)  # rows 13..62 touch pages 0..3
+    else:
+        rows = torch.randn((50, 8, 64), generator=g).to(torch.bfloat16).to(DEV)
+        scales = None
+    pool.write_rows(sid, 1, 1, 13, rows, scales)
+    back = torch.empty_like(rows)
+    sback = torch.zeros((4, 8), device=DEV) if cache == "i8" else None
+    pool.read_rows(sid, 1, 1, 13, back, sback)
+    torch.cuda.synchronize()
+    assert torch.equal(back, rows)
+    if cache == "i8":
+        assert torch.equal(sback, scales)

@@ -1,0 +1,377 @@
+"""Pins of the oracle (the CPU restatement) that do not go through the oracle's own formulas:
+closed forms, textbook definitions computed independently (numpy f64, torch's bf16 cast), and
+restatements of the reference's relational tests (transformer.rs:1022-1417).
+
+The reference holds no golden vectors for this path (its hot-path tests are relational), and its
+Rust code cannot run here, so these are what fix the oracle's numbers.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import oracle
+from helpers import bf16_round, lcg, rel_err
+
+THETA = 10000.0
+
+
+# ---- bf16 rounding ------------------------------------------------------------------------
+def test_bf16_round_matches_torch_cast():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(4000).astype(np.float32) * 10.0 ** rng.integers(-20, 20, 4000),
+                        np.float32([1.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -1.0 - 2 ** -8, 0.0, -0.0,
+                                    3.4e38, 1e-40])])
+    want = torch.from_numpy(x).to(torch.bfloat16).to(torch.float32).numpy()
+    got = np.array([oracle.bf16_round(float(v)) for v in x], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(bf16_round(x).view(np.uint32), want.view(np.uint32))
+
+
+# ---- RoPE (rope.rs:37-95) -------------------------------------------------------------------
+@pytest.mark.parametrize("pos", [1, 7, 100, 4095])
+def test_rope_rotates_each_interleaved_pair_by_pos_times_freq(pos):
+    # x = e_{2i}: rotate gives (cos a, sin a) in pair i with a = pos * theta^(-i/32); e_{2i+1}
+    # gives (-sin a, cos a).  This fixes the pairing (2i, 2i+1), the sign and the frequencies.
+    D = 64
+    c, s = oracle.rope_row(D, THETA, float(pos), "f32")
+    for i in range(D // 2):
+        a = pos * THETA ** (-i / 32)
+        e0 = np.zeros(D, np.float32)
+        e0[2 * i] = 1.0
+        r0 = oracle.rotate(e0, c, s)
+        e1 = np.zeros(D, np.float32)
+        e1[2 * i + 1] = 1.0
+        r1 = oracle.rotate(e1, c, s)
+        tol = 2e-6 * max(1.0, a)  # f32 angle pos * inv_freq carries ~1 ulp of a
+        assert abs(r0[2 * i] - math.cos(a)) < tol and abs(r0[2 * i + 1] - math.sin(a)) < tol
+        assert abs(r1[2 * i] + math.sin(a)) < tol and abs(r1[2 * i + 1] - math.cos(a)) < tol
+        others = np.delete(r0, [2 * i, 2 * i + 1])
+        assert not others.any()
+
+
+def test_rope_position_zero_is_the_identity_exactly():
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal(64).astype(np.float32)
+    c, s = oracle.rope_row(64, THETA, 0.0, "f32")
+    assert np.array_equal(oracle.rotate(x, c, s), x)
+
+
+def test_rope_preserves_pair_norms_and_composes():
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal(64).astype(np.float32)
+    ca, sa = oracle.rope_row(64, THETA, 37.0, "f32")
+    cb, sb = oracle.rope_row(64, THETA, 18.0, "f32")
+    cab, sab = oracle.rope_row(64, THETA, 55.0, "f32")
+    y = oracle.rotate(x, ca, sa)
+    pn = lambda v: np.hypot(v[0::2].astype(np.float64), v[1::2].astype(np.float64))
+    np.testing.assert_allclose(pn(y), pn(x), rtol=1e-6)
+    np.testing.assert_allclose(oracle.rotate(y, cb, sb), oracle.rotate(x, cab, sab), atol=2e-5)
+    # shift_back (rope.rs:26-35) is the rotation by -count: it undoes a rotation by count
+    cm, sm = oracle.rope_row(64, THETA, -18.0, "f32")
+    np.testing.assert_allclose(oracle.rotate(oracle.rotate(x, cab, sab), cm, sm), y, atol=2e-5)
+
+
+def test_rope_bf16_tables_are_the_f32_values_rounded():
+    c32, s32 = oracle.rope_row(64, THETA, 1234.0, "f32")
+    c16, s16 = oracle.rope_row(64, THETA, 1234.0, "bf16")
+    assert np.array_equal(c16, bf16_round(c32)) and np.array_equal(s16, bf16_round(s32))
+
+
+# ---- decode attention (sdpa_decode, transformer.rs:223,230) -----------------------------------
+def sdpa_f64(q, K, V, scale):
+    """Textbook softmax(q K^T * scale) V in f64 (numpy), q [D], K/V [n][D]."""
+    s = (K.astype(np.float64) @ q.astype(np.float64)) * scale
+    p = np.exp(s - s.max())
+    return (p / p.sum()) @ V.astype(np.float64)
+
+
+def rotated(x, pos, act="f32"):
+    c, s = oracle.rope_row(x.shape[-1], THETA, float(pos), act)
+    return oracle.rotate(x, c, s, act)
+
+
+def fill(st, rows_k, rows_v, layer=0):
+    for i in range(rows_k.shape[0]):
+        st.append(layer, rows_k[i:i + 1], rows_v[i:i + 1])
+        st.commit(1)
+
+
+def test_one_key_returns_its_value():
+    rng = np.random.default_rng(3)
+    st = oracle.Stream(1, 2, 64, 8)
+    q, k, v = (rng.standard_normal((1, 2, 64)).astype(np.float32) for _ in range(3))
+    out, out64 = st.attend(0, q, k, v)
+    assert np.array_equal(out, v)  # softmax of a single score is exactly 1
+    np.testing.assert_array_equal(out64, v.astype(np.float64))
+
+
+def test_zero_query_or_identical_keys_give_the_mean_of_values():
+    rng = np.random.default_rng(4)
+    vals = rng.standard_normal((20, 1, 64)).astype(np.float32)
+    # q = 0: every score is exactly 0
+    st = oracle.Stream(1, 1, 64, 32)
+    ks = rng.standard_normal((20, 1, 64)).astype(np.float32)
+    fill(st, ks[:19], vals[:19])
+    out, out64 = st.attend(0, np.zeros((1, 1, 64), np.float32), ks[19:], vals[19:])
+    assert rel_err(out64[0, 0], vals[:, 0].astype(np.float64).mean(axis=0)) < 1e-12
+    assert rel_err(out[0, 0], vals[:, 0].astype(np.float64).mean(axis=0)) < 1e-5
+    # the same stored key in every slot (the new one rotated into place, to rounding)
+    st = oracle.Stream(1, 1, 64, 32)
+    key = rng.standard_normal((1, 1, 64)).astype(np.float32)
+    st.write_rows(0, 0, 0, vals=np.repeat(key, 19, axis=0))
+    st.write_rows(0, 1, 0, vals=vals[:19])
+    st.advance(19)
+    c, s = oracle.rope_row(64, THETA, -19.0, "f32")
+    k_in = oracle.rotate(key[0, 0], c, s)[None, None]
+    out, out64 = st.attend(0, rng.standard_normal((1, 1, 64)).astype(np.float32), k_in, vals[19:])
+    assert rel_err(out64[0, 0], vals[:, 0].astype(np.float64).mean(axis=0)) < 1e-5
+
+
+def test_a_dominant_score_returns_that_value():
+    rng = np.random.default_rng(5)
+    st = oracle.Stream(1, 1, 64, 32)
+    ks = rng.standard_normal((10, 1, 64)).astype(np.float32) * 0.01
+    vs = rng.standard_normal((10, 1, 64)).astype(np.float32)
+    q = np.zeros((1, 1, 64), np.float32)
+    q[0, 0, 0] = 1.0
+    # key 3 is a large multiple of the query's direction once both are rotated into place:
+    # stored key 3 = rotate(k_in, 3) and rotated q = rotate(q, 10), so k_in = rotate(4000 q, 7)
+    c, s = oracle.rope_row(64, THETA, 7.0, "f32")
+    ks[3] = oracle.rotate(q[0, 0] * 4000.0, c, s)[None]
+    fill(st, ks, vs)
+    out, _ = st.attend(0, q, np.zeros((1, 1, 64), np.float32), np.zeros((1, 1, 64), np.float32))
+    np.testing.assert_allclose(out[0, 0], vs[3, 0], atol=1e-5)
+
+
+@pytest.mark.parametrize("n", [1, 2, 17, 300])
+def test_decode_matches_textbook_attention(n):
+    rng = np.random.default_rng(10 + n)
+    H, D = 2, 64
+    st = oracle.Stream(2, H, D, n + 4)
+    K = rng.standard_normal((n, H, D)).astype(np.float32)
+    V = rng.standard_normal((n, H, D)).astype(np.float32)
+    fill(st, K[:-1], V[:-1], layer=1)
+    q = rng.standard_normal((1, H, D)).astype(np.float32)
+    out, out64 = st.attend(1, q, K[-1:], V[-1:])
+    for h in range(H):
+        Kr = np.stack([rotated(K[i, h], i) for i in range(n)])
+        want = sdpa_f64(rotated(q[0, h], n - 1), Kr, V[:, h], 0.125)
+        assert rel_err(out64[0, h], want) < 1e-9
+        assert rel_err(out[0, h], want) < 1e-5
+
+
+def test_prefill_is_causal_textbook_attention():
+    rng = np.random.default_rng(6)
+    H, D, t, cur = 2, 64, 24, 5
+    st = oracle.Stream(1, H, D, 64)
+    K = rng.standard_normal((cur + t, H, D)).astype(np.float32)
+    V = rng.standard_normal((cur + t, H, D)).astype(np.float32)
+    Q = rng.standard_normal((t, H, D)).astype(np.float32)
+    fill(st, K[:cur], V[:cur])
+    out, out64 = st.attend(0, Q, K[cur:], V[cur:])
+    for i in range(t):
+        for h in range(H):
+            Kr = np.stack([rotated(K[j, h], j) for j in range(cur + i + 1)])
+            want = sdpa_f64(rotated(Q[i, h], cur + i), Kr, V[:cur + i + 1, h], 0.125)
+            assert rel_err(out64[i, h], want) < 1e-9
+
+
+def test_bf16_outputs_are_rounded_and_close_to_f64():
+    rng = np.random.default_rng(7)
+    st = oracle.Stream(1, 2, 64, 64, cache="bf16", act="bf16")
+    for i in range(40):
+        k, v = (bf16_round(rng.standard_normal((1, 2, 64))) for _ in range(2))
+        st.append(0, k, v)
+        st.commit(1)
+    q = bf16_round(rng.standard_normal((1, 2, 64)))
+    k, v = (bf16_round(rng.standard_normal((1, 2, 64))) for _ in range(2))
+    out, out64 = st.attend(0, q, k, v)
+    assert np.array_equal(out, bf16_round(out))
+    assert rel_err(out, out64) < 2e-2
+    vals, _, _ = st.read_rows(0, 0, 0, 41)
+    assert np.array_equal(vals, bf16_round(vals))
+
+
+# ---- grouped-query heads (transformer.rs:1112-1164) -----------------------------------------
+def test_grouped_kv_heads_equal_repeated_heads():
+    rand = lcg(1)
+    H, KVH, D = 4, 2, 64
+    a = oracle.Stream(1, H, D, 16, kv_heads=KVH)
+    b = oracle.Stream(1, H, D, 16)
+    for (start, t) in [(0, 3), (3, 1), (4, 1)]:
+        q = rand(t * H * D).reshape(t, H, D)
+        k = rand(t * KVH * D).reshape(t, KVH, D)
+        v = rand(t * KVH * D).reshape(t, KVH, D)
+        oa, _ = a.attend(0, q, k, v)
+        ob, _ = b.attend(0, q, np.repeat(k, H // KVH, axis=1), np.repeat(v, H // KVH, axis=1))
+        a.commit(t)
+        b.commit(t)
+        assert np.array_equal(oa, ob)
+
+
+# ---- with_seq_budget (transformer.rs:1022-1099) ----------------------------------------------
+def filled(seq, used):
+    # k[s, h, d] = s + 100 h, v = -k, as the reference's test pattern
+    st = oracle.Stream(1, 2, 64, seq)
+    k = np.fromfunction(lambda s, h, d: s + 100 * h, (seq, 2, 64), dtype=np.float32).astype(np.float32)
+    st.write_rows(0, 0, 0, vals=k)
+    st.write_rows(0, 1, 0, vals=-k)
+    st.advance(used)
+    return st, k
+
+
+def test_with_seq_budget_copies_the_used_prefix_and_zero_fills_the_rest():
+    small, k = filled(4, 3)
+    big = small.with_seq_budget(10)
+    assert big.current_end == 3 and big.capacity == 10
+    kb, _, _ = big.read_rows(0, 0, 0, 10)
+    assert np.array_equal(kb[:3], k[:3]) and not kb[3:].any()
+    vb, _, _ = big.read_rows(0, 1, 0, 3)
+    assert np.array_equal(vb, -k[:3])
+
+
+def test_the_copy_does_not_share_storage_with_the_source():
+    small, k = filled(4, 2)
+    big = small.with_seq_budget(8)
+    big.write_rows(0, 0, 0, vals=np.full((1, 2, 64), 9e9, np.float32))
+    ks, _, _ = small.read_rows(0, 0, 0, 1)
+    assert ks[0, 1, 0] == 100.0
+
+
+def test_a_budget_smaller_than_the_prefix_is_refused():
+    st, _ = filled(4, 3)
+    with pytest.raises(oracle.OracleError, match="3.*2"):
+        st.with_seq_budget(2)
+    st.with_seq_budget(3)
+
+
+# ---- ring (transformer.rs:1347-1416) ----------------------------------------------------------
+def rows(n, phase, H=4, D=64):
+    # transformer.rs:1350-1354: sin(i * 0.37 + phase), here already split in heads
+    return np.sin(np.arange(n * H * D, dtype=np.float32) * np.float32(0.37) + np.float32(phase)).reshape(n, H, D)
+
+
+@pytest.mark.parametrize("mode", ["shift", "absolute"])
+def test_evicting_leaves_the_cache_of_a_sequence_without_them(mode):
+    # A 5-row prompt and 6 frame slots whose oldest 3 frames go whenever they are full: three
+    # evictions over 15 frames, the later ones wrapping round the ring.  Every frame must see what
+    # it would have seen had the evicted frames never been there (1e-4, as the reference).
+    H, D = 4, 64
+    qs, ks, vs = rows(15, 1.0), rows(15, 2.0), rows(15, 3.0)
+    pk, pv, pq = rows(5, 0.0), rows(5, 0.5), rows(5, 0.25)
+    ring = oracle.Stream(1, H, D, 11)
+    ring.attend(0, pq, pk, pv)
+    ring.commit(5)
+    ring.start_ring(mode, prefix=5)
+    in_view = 0
+    for i in range(15):
+        if in_view == 6:
+            oldest = i - in_view
+            ring.evict(5, [5 + (oldest + j) % 6 for j in range(3)])
+            in_view -= 3
+            assert ring.current_end == 5 + in_view
+        ring.set_ring_slot(5 + i % 6)
+        got, _ = ring.attend(0, qs[i:i + 1], ks[i:i + 1], vs[i:i + 1])
+        ring.commit(1)
+        in_view += 1
+        plain = oracle.Stream(1, H, D, 11)
+        plain.attend(0, pq, pk, pv)
+        plain.commit(5)
+        for j in range(i + 1 - in_view, i + 1):
+            want, _ = plain.attend(0, qs[j:j + 1], ks[j:j + 1], vs[j:j + 1])
+            plain.commit(1)
+        assert np.abs(got - want).max() < 1e-4, f"frame {i}"
+
+
+def test_absolute_ring_equals_shifting_ring():
+    # Evicting with the keys left where they were written and the query rotated twice gives what
+    # rotating the kept keys back gives (bf16: to the rounding of the rotations).
+    rng = np.random.default_rng(8)
+    H, D, cap, pre = 2, 64, 40, 6
+    st = {m: oracle.Stream(1, H, D, cap, cache="bf16", act="bf16") for m in ("shift", "absolute")}
+    q0, k0, v0 = (bf16_round(rng.standard_normal((pre, H, D))) for _ in range(3))
+    for s in st.values():
+        s.attend(0, q0, k0, v0)
+        s.commit(pre)
+    for m, s in st.items():
+        s.start_ring(m, prefix=pre)
+    outs = {m: [] for m in st}
+    in_view, ctx = 0, 20
+    for i in range(90):
+        q, k, v = (bf16_round(rng.standard_normal((1, H, D))) for _ in range(3))
+        for m, s in st.items():
+            if in_view == ctx:
+                s.evict(pre, [pre + (i - in_view + j) % ctx for j in range(7)])
+            s.set_ring_slot(pre + i % ctx)
+            o, _ = s.attend(0, q, k, v)
+            s.commit(1)
+            outs[m].append(o)
+        in_view = in_view - 7 + 1 if in_view == ctx else in_view + 1
+    a, b = np.concatenate(outs["shift"]), np.concatenate(outs["absolute"])
+    assert rel_err(a, b) < 5e-2
+    assert st["shift"].ring_info()["shift"] == 0 and st["absolute"].ring_info()["shift"] > 0
+    assert st["shift"].current_end == st["absolute"].current_end
+
+
+def test_misuse_of_a_ring_is_refused():
+    st = oracle.Stream(1, 4, 64, 8)
+    st.attend(0, rows(4, 0.0), rows(4, 0.1), rows(4, 0.2))
+    st.commit(4)
+    with pytest.raises(oracle.OracleError, match="not a ring"):
+        st.set_ring_slot(4)
+    st.start_ring("shift")
+    with pytest.raises(oracle.OracleError, match="cannot be resized"):
+        st.with_seq_budget(10)
+    st.set_ring_slot(4)
+    st.attend(0, rows(1, 1.0), rows(1, 1.1), rows(1, 1.2))
+    st.commit(1)
+    with pytest.raises(oracle.OracleError):
+        st.evict(4, [2])
+    with pytest.raises(oracle.OracleError):
+        st.evict(4, [5])
+    with pytest.raises(oracle.OracleError):  # refused as a whole: slot 4 stays
+        st.evict(4, [4, 5])
+    assert st.ring_info()["valid"][4]
+    st.set_ring_slot(4)
+    with pytest.raises(oracle.OracleError, match="still holds a row"):
+        st.attend(0, rows(1, 2.0), rows(1, 2.1), rows(1, 2.2))
+    st.evict(4, [4])
+    st.attend(0, rows(1, 2.0), rows(1, 2.1), rows(1, 2.2))
+    with pytest.raises(oracle.OracleError, match="one row at a time"):
+        st.attend(0, rows(2, 2.0), rows(2, 2.1), rows(2, 2.2))
+
+
+# ---- int8 (per-(page, head) scales) -------------------------------------------------------------
+def test_int8_rows_quantize_within_half_a_step():
+    rng = np.random.default_rng(9)
+    st = oracle.Stream(1, 2, 64, 48, cache="i8", act="bf16")
+    V = bf16_round(rng.standard_normal((40, 2, 64)) * rng.uniform(0.1, 3.0, (40, 1, 1)))
+    for i in range(40):
+        st.append(0, np.zeros((1, 2, 64), np.float32), V[i:i + 1])
+        st.commit(1)
+    vals, q8, scales = st.read_rows(0, 1, 0, 40)
+    for b in range(3):
+        blk = V[16 * b:16 * b + 16]
+        amax = np.abs(blk).max(axis=(0, 2))
+        # the final scale is the block's amax / 127 (every row seen by the running max)
+        np.testing.assert_array_equal(scales[b], (amax / np.float32(127)).astype(np.float32))
+        # A row is rounded once when written and once more each time a later row raises the
+        # page's scale: its error is at most (1 + raises after it) half steps of the final scale.
+        run = np.maximum.accumulate(np.abs(blk).max(axis=2), axis=0)  # [rows, H]
+        raises = (run[1:] > run[:-1]).astype(int)
+        later = np.concatenate([np.cumsum(raises[::-1], axis=0)[::-1], np.zeros((1, 2), int)])
+        bound = (1 + later)[:, :, None] * scales[b][None, :, None] / 2
+        err = np.abs(vals[16 * b:16 * b + 16] - blk)
+        assert (err <= bound * (1 + 1e-5)).all()
+        # rows written at the final scale (no raise after them) are within half a step
+        assert (err[later[:, 0] == 0, 0] <= scales[b][0] / 2 * (1 + 1e-5)).all()
+    assert np.abs(q8).max() <= 127
+    # a fresh page (first row) takes its scale from that row alone
+    st2 = oracle.Stream(1, 1, 64, 16, cache="i8", act="f32")
+    x = np.linspace(-2, 3, 64, dtype=np.float32)[None, None]
+    st2.append(0, np.zeros_like(x), x)
+    vals, q8, scales = st2.read_rows(0, 1, 0, 1)
+    assert scales[0, 0] == np.float32(3.0) / np.float32(127.0)
+    assert q8[0, 0, -1] == 127 and np.abs(vals[0, 0] - x[0, 0]).max() <= scales[0, 0] / 2 + 1e-7

@@ -1,0 +1,574 @@
+// HIP kernels of the paged flow-LM KV cache, written for gfx950 (CDNA4, wave64).
+//
+// Bit-exactness contract with the CPU restatement: the library is built with
+// -ffp-contract=off, RoPE rotates with host-computed cos/sin tables, bf16 rounding is
+// round-to-nearest-even on the f32 bits, int8 quantization is rint(y / s) clamped to +-127 with
+// IEEE division.  The attention arithmetic (dots, softmax, weighted sums) is f32 in an order of
+// its own and is checked to a tolerance, not bit for bit.
+#include "xnp_internal.h"
+
+namespace xnp {
+
+// ---------------------------------------------------------------------------------------------
+// element helpers
+
+__device__ __forceinline__ float bf16_value(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+__device__ __forceinline__ uint32_t bf16_bits(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7f800000u) == 0x7f800000u) {
+        if (u & 0x007fffffu) u |= 0x00400000u;
+        return u >> 16;
+    }
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+template <bool ABF> __device__ __forceinline__ float round_act(float x) {
+    if constexpr (ABF) return bf16_value(bf16_bits(x));
+    return x;
+}
+
+__device__ __forceinline__ int quant(float y, float s) {
+    if (!(s > 0.0f)) return 0;
+    float r = __builtin_rintf(y / s);
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    return (int)r;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+template <int CDT> constexpr int esize() { return CDT == DT_F32 ? 4 : CDT == DT_BF16 ? 2 : 1; }
+
+// Element offset of row 0 of tile (layer, kv, page, head).
+__device__ __forceinline__ size_t tile_index(const PoolView &pv, int layer, int kv, int page, int h) {
+    return (((size_t)layer * 2 + kv) * pv.NB + page) * pv.H + h;
+}
+
+// Two activation values (dims 2i, 2i+1) of a head row.
+template <bool ABF> __device__ __forceinline__ float2 load_pair(const void *row, int i) {
+    if constexpr (ABF) {
+        uint32_t w = ((const uint32_t *)row)[i];
+        return make_float2(bf16_value(w & 0xffffu), bf16_value(w >> 16));
+    } else {
+        return ((const float2 *)row)[i];
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// append: one wave writes one new row of one head, keys (lanes 0-31, RoPE'd) and values
+// (lanes 32-63), each lane one pair of dims.  complete_kv, transformer.rs:61-92, with the k
+// rotation of rope.rs:74-95 fused in.
+
+template <int CDT, bool ABF>
+__device__ void append_row_wave(const PoolView &pv, int layer, int page, int row, int h, int key_pos,
+                                const void *krow, const void *vrow, bool fresh) {
+    const int lane = threadIdx.x & 63;
+    const int kv = lane >> 5;
+    const int pr = lane & 31;
+    float2 x = load_pair<ABF>(kv ? vrow : krow, pr);
+    if (kv == 0) {
+        float2 cs = pv.rope[(size_t)key_pos * (pv.D / 2) + pr];
+        float a = x.x * cs.x, b = x.y * cs.y, e = x.x * cs.y, f = x.y * cs.x;
+        x.x = round_act<ABF>(a - b);
+        x.y = round_act<ABF>(e + f);
+    }
+    const size_t tile = tile_index(pv, layer, kv, page, h);
+    if constexpr (CDT == DT_F32) {
+        ((float2 *)pv.pages)[tile * (kBlock * kHeadDim / 2) + row * (kHeadDim / 2) + pr] = x;
+    } else if constexpr (CDT == DT_BF16) {
+        ((uint32_t *)pv.pages)[tile * (kBlock * kHeadDim / 2) + row * (kHeadDim / 2) + pr] =
+            bf16_bits(x.x) | (bf16_bits(x.y) << 16);
+    } else {
+        // int8: per-(page, head) scale amax / 127.  A page holding another live row keeps its
+        // scale unless this row needs a larger one; then its other rows are requantized.
+        float amax = fmaxf(fabsf(x.x), fabsf(x.y));
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+        const float s_row = amax / 127.0f;
+        float *sp = pv.scales + tile;
+        const float s_old = *sp;
+        const float s_new = fresh ? s_row : fmaxf(s_old, s_row);
+        const int req = (!fresh && s_new > s_old) ? 1 : 0;
+        int8_t *pages8 = (int8_t *)pv.pages;
+#pragma unroll
+        for (int which = 0; which < 2; ++which) {
+            const int rq = __shfl(req, which * 32);
+            if (rq) {
+                const float so = __shfl(s_old, which * 32), sn = __shfl(s_new, which * 32);
+                const size_t wt = tile_index(pv, layer, which, page, h);
+                uint4 *tp = (uint4 *)(pages8 + wt * (kBlock * kHeadDim)) + lane;
+                if ((lane >> 2) != row) { // 4 lanes per 64-byte row
+                    uint4 w = *tp;
+                    uint32_t *wv = (uint32_t *)&w;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        uint32_t o = 0;
+#pragma unroll
+                        for (int bt = 0; bt < 4; ++bt) {
+                            int qv = (int)(int8_t)((wv[j] >> (8 * bt)) & 0xffu);
+                            int nq = quant((float)qv * so, sn);
+                            o |= ((uint32_t)(nq & 0xff)) << (8 * bt);
+                        }
+                        wv[j] = o;
+                    }
+                    *tp = w;
+                }
+            }
+        }
+        const uint32_t q0 = (uint32_t)(quant(x.x, s_new) & 0xff), q1 = (uint32_t)(quant(x.y, s_new) & 0xff);
+        ((uint16_t *)(pages8 + tile * (kBlock * kHeadDim)))[row * (kHeadDim / 2) + pr] =
+            (uint16_t)(q0 | (q1 << 8));
+        if (pr == 0) *sp = s_new;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// block-table patches (pages taken since the previous batch)
+
+__global__ void k_patch_tables(int32_t *tables, const TablePatch *patches, int n, int mbps) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) tables[(size_t)patches[i].sid * mbps + patches[i].blk] = patches[i].page;
+}
+
+hipError_t launch_patch_tables(const PoolView &pv, const TablePatch *patches, int n, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_patch_tables, dim3((n + 255) / 256), dim3(256), 0, stream, pv.tables, patches, n,
+                       pv.mbps);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------
+// standalone append of t rows per stream.  Work item = (stream, page the rows touch); one wave
+// per head walks the page's rows in order, since int8 rows of one page depend on each other.
+
+template <int CDT, bool ABF>
+__global__ __launch_bounds__(1024) void k_append(PoolView pv, BatchView bv, int layer, const void *k,
+                                                 const void *v, int nseg) {
+    const int b = blockIdx.x / nseg, seg = blockIdx.x % nseg;
+    const StreamPlan P = bv.plans[b];
+    const int h = threadIdx.x >> 6;
+    const int t = bv.t;
+    const int ws = P.write_slot;
+    const int blk = (ws >> 4) + seg;
+    const int i0 = max(0, blk * kBlock - ws), i1 = min(t, (blk + 1) * kBlock - ws);
+    if (i0 >= i1) return;
+    const int page = pv.tables[(size_t)P.sid * pv.mbps + blk];
+    const int group = pv.H / pv.KVH;
+    constexpr int AE = ABF ? 2 : 4;
+    for (int i = i0; i < i1; ++i) {
+        const int slot = ws + i;
+        const size_t arow = ((size_t)P.out_row * t + i) * pv.KVH + h / group;
+        const bool fresh = P.ring ? (P.fresh != 0) : ((slot & 15) == 0);
+        append_row_wave<CDT, ABF>(pv, layer, page, slot & 15, h, P.key_pos + i,
+                                  (const char *)k + arow * kHeadDim * AE, (const char *)v + arow * kHeadDim * AE,
+                                  fresh);
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// decode: one work group per work item (stream, run of pages), one wave per head.
+//
+// Lane layout over a 16 x 64 tile of one head: every lane loads 16 contiguous bytes per pass,
+// DPL dims of one row (DPL = 4 f32, 8 bf16, 16 int8), so a pass is one coalesced 1 KB read per
+// wave.  The LPR lanes of a row reduce the row's dot product with xor shuffles; each lane keeps
+// an online softmax over the rows it saw and the lanes of one dim slice merge at the end.
+// Scores are kept in log2 units (the query is prescaled by scale * log2(e)).
+
+template <int CDT> struct Lanes {
+    static constexpr int DPL = 16 / esize<CDT>();
+    static constexpr int LPR = kHeadDim / DPL;
+    static constexpr int RPP = 64 / LPR;
+    static constexpr int NP = kBlock / RPP;
+};
+
+template <int CDT>
+__device__ __forceinline__ void unpack(const uint4 &w, float (&x)[Lanes<CDT>::DPL]) {
+    const uint32_t *u = (const uint32_t *)&w;
+    if constexpr (CDT == DT_F32) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = __uint_as_float(u[i]);
+    } else if constexpr (CDT == DT_BF16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x[2 * i] = bf16_value(u[i] & 0xffffu);
+            x[2 * i + 1] = bf16_value(u[i] >> 16);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int bt = 0; bt < 4; ++bt) x[4 * i + bt] = (float)(int8_t)((u[i] >> (8 * bt)) & 0xffu);
+    }
+}
+
+// Rotated query slice (dims DPL*c .. DPL*c+DPL-1) at `pos`, rounded to the activation dtype and
+// prescaled.
+template <int DPL, bool ABF>
+__device__ __forceinline__ void rotated_q(const PoolView &pv, const void *qrow, int c, int pos, float mul,
+                                          float (&out)[DPL]) {
+#pragma unroll
+    for (int i = 0; i < DPL / 2; ++i) {
+        const int pr = c * (DPL / 2) + i;
+        float2 x = load_pair<ABF>(qrow, pr);
+        float2 cs = pv.rope[(size_t)pos * (pv.D / 2) + pr];
+        float a = x.x * cs.x, b = x.y * cs.y, e = x.x * cs.y, f = x.y * cs.x;
+        out[2 * i] = round_act<ABF>(a - b) * mul;
+        out[2 * i + 1] = round_act<ABF>(e + f) * mul;
+    }
+}
+
+template <int CDT, bool ABF>
+__global__ __launch_bounds__(1024) void k_decode(PoolView pv, BatchView bv, int layer, const void *q,
+                                                 const void *knew, const void *vnew, void *out,
+                                                 float qmul, int fused) {
+    using LN = Lanes<CDT>;
+    constexpr int DPL = LN::DPL, LPR = LN::LPR, RPP = LN::RPP, NP = LN::NP;
+    constexpr int AE = ABF ? 2 : 4;
+    const WorkItem W = bv.work[blockIdx.x];
+    const StreamPlan P = bv.plans[W.b];
+    const int h = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int32_t *tab = pv.tables + (size_t)P.sid * pv.mbps;
+
+    if (fused && W.part == P.app_part) {
+        const int slot = P.write_slot;
+        const size_t arow = (size_t)P.out_row * pv.KVH + h / (pv.H / pv.KVH);
+        const bool fresh = P.ring ? (P.fresh != 0) : ((slot & 15) == 0);
+        append_row_wave<CDT, ABF>(pv, layer, tab[slot >> 4], slot & 15, h, P.key_pos,
+                                  (const char *)knew + arow * kHeadDim * AE,
+                                  (const char *)vnew + arow * kHeadDim * AE, fresh);
+        __syncthreads();
+    }
+
+    const int c = lane % LPR, g = lane / LPR;
+    const char *qrow = (const char *)q + ((size_t)P.out_row * pv.H + h) * kHeadDim * AE;
+    float qw[DPL], qp[DPL];
+    rotated_q<DPL, ABF>(pv, qrow, c, P.pos, qmul, qw);
+    const bool two_q = P.prefix > W.blk0 * kBlock;
+    if (two_q) rotated_q<DPL, ABF>(pv, qrow, c, P.pos_pre, qmul, qp);
+
+    // Per-block metadata, lane j holding block blk0 + j: page, seen rows, int8 scales.
+    const int nb = W.blk1 - W.blk0;
+    int my_page = 0;
+    uint32_t my_seen = 0;
+    float my_sk = 0.f, my_sv = 0.f;
+    if (lane < nb) {
+        const int blk = W.blk0 + lane;
+        const int base = blk * kBlock;
+        uint32_t seen = 0xffffu;
+        if (P.mask_off >= 0) seen = (bv.masks[P.mask_off + (base >> 5)] >> (base & 16)) & 0xffffu;
+        const int nvalid = P.span - base;
+        if (nvalid < kBlock) seen &= (1u << max(nvalid, 0)) - 1u;
+        const int pg = tab[blk];
+        if (pg < 0) seen = 0;
+        my_page = pg < 0 ? 0 : pg;
+        my_seen = seen;
+        if constexpr (CDT == DT_I8) {
+            my_sk = pv.scales[tile_index(pv, layer, 0, my_page, h)];
+            my_sv = pv.scales[tile_index(pv, layer, 1, my_page, h)];
+        }
+    }
+
+    const uint4 *kbase = (const uint4 *)((const char *)pv.pages + tile_index(pv, layer, 0, 0, h) * (kBlock * kHeadDim * esize<CDT>()));
+    const uint4 *vbase = (const uint4 *)((const char *)pv.pages + tile_index(pv, layer, 1, 0, h) * (kBlock * kHeadDim * esize<CDT>()));
+    const size_t page_u4 = (size_t)pv.H * (kBlock * kHeadDim * esize<CDT>() / 16);
+
+    float m = -1e30f, l = 0.f;
+    float acc[DPL];
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
+
+    uint4 kc[NP], vc[NP], kn[NP], vn[NP];
+    {
+        const int pg = __builtin_amdgcn_readfirstlane(my_page);
+        const size_t off = (size_t)pg * page_u4 + lane;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            kc[p] = kbase[off + 64 * p];
+            vc[p] = vbase[off + 64 * p];
+        }
+    }
+    for (int j = 0; j < nb; ++j) {
+        if (j + 1 < nb) {
+            const int pg = __builtin_amdgcn_readlane(my_page, j + 1);
+            const size_t off = (size_t)pg * page_u4 + lane;
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                kn[p] = kbase[off + 64 * p];
+                vn[p] = vbase[off + 64 * p];
+            }
+        }
+        const uint32_t seen = __builtin_amdgcn_readlane(my_seen, j);
+        const int base = (W.blk0 + j) * kBlock;
+        float sk = 1.f, sv = 1.f;
+        if constexpr (CDT == DT_I8) {
+            sk = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(my_sk), j));
+            sv = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(my_sv), j));
+        }
+        float s[NP];
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            float x[DPL];
+            unpack<CDT>(kc[p], x);
+            float dw = 0.f;
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) dw = __builtin_fmaf(qw[i], x[i], dw);
+            const int r = g + RPP * p;
+            if (two_q && base + r < P.prefix) {
+                float dp = 0.f;
+#pragma unroll
+                for (int i = 0; i < DPL; ++i) dp = __builtin_fmaf(qp[i], x[i], dp);
+                dw = dp;
+            }
+#pragma unroll
+            for (int o = 1; o < LPR; o <<= 1) dw += __shfl_xor(dw, o);
+            if constexpr (CDT == DT_I8) dw *= sk;
+            s[p] = ((seen >> r) & 1u) ? dw : -INFINITY;
+        }
+        float smax = s[0];
+#pragma unroll
+        for (int p = 1; p < NP; ++p) smax = fmaxf(smax, s[p]);
+        const float m_new = fmaxf(m, smax);
+        const float alpha = fast_exp2(m - m_new);
+        l *= alpha;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) acc[i] *= alpha;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const float e = fast_exp2(s[p] - m_new);
+            l += e;
+            float x[DPL];
+            unpack<CDT>(vc[p], x);
+            const float ev = (CDT == DT_I8) ? e * sv : e;
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) acc[i] = __builtin_fmaf(ev, x[i], acc[i]);
+        }
+        m = m_new;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            kc[p] = kn[p];
+            vc[p] = vn[p];
+        }
+    }
+
+    // Merge the row groups: lanes c, c + LPR, c + 2 LPR, ... hold the same dims.
+#pragma unroll
+    for (int o = LPR; o < 64; o <<= 1) {
+        const float mo = __shfl_xor(m, o), lo = __shfl_xor(l, o);
+        const float mn = fmaxf(m, mo);
+        const float a = fast_exp2(m - mn), bb = fast_exp2(mo - mn);
+        l = l * a + lo * bb;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) {
+            const float ao = __shfl_xor(acc[i], o);
+            acc[i] = acc[i] * a + ao * bb;
+        }
+        m = mn;
+    }
+    if (g != 0) return;
+    if (P.nparts == 1) {
+        const float inv = 1.0f / l;
+        if constexpr (ABF) {
+            uint32_t w[DPL / 2];
+#pragma unroll
+            for (int i = 0; i < DPL / 2; ++i)
+                w[i] = bf16_bits(acc[2 * i] * inv) | (bf16_bits(acc[2 * i + 1] * inv) << 16);
+            uint4 *dst = (uint4 *)((char *)out + (((size_t)P.out_row * pv.H + h) * kHeadDim + c * DPL) * 2);
+#pragma unroll
+            for (int i = 0; i < DPL / 8; ++i) dst[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+        } else {
+            float4 *dst = (float4 *)((float *)out + ((size_t)P.out_row * pv.H + h) * kHeadDim + c * DPL);
+#pragma unroll
+            for (int i = 0; i < DPL / 4; ++i)
+                dst[i] = make_float4(acc[4 * i] * inv, acc[4 * i + 1] * inv, acc[4 * i + 2] * inv, acc[4 * i + 3] * inv);
+        }
+    } else {
+        float *part = bv.parts + ((size_t)W.part * pv.H + h) * kPartStride;
+        float4 *dst = (float4 *)(part + c * DPL);
+#pragma unroll
+        for (int i = 0; i < DPL / 4; ++i) dst[i] = make_float4(acc[4 * i], acc[4 * i + 1], acc[4 * i + 2], acc[4 * i + 3]);
+        if (lane == 0) {
+            part[64] = m;
+            part[65] = l;
+        }
+    }
+}
+
+// Merge the partials of streams split over several work items: one wave per head, lane = dim.
+template <bool ABF>
+__global__ __launch_bounds__(1024) void k_merge(PoolView pv, BatchView bv, void *out) {
+    const StreamPlan P = bv.plans[blockIdx.x];
+    if (P.nparts <= 1) return;
+    const int h = threadIdx.x >> 6, d = threadIdx.x & 63;
+    const float *base = bv.parts + ((size_t)P.part0 * pv.H + h) * kPartStride;
+    const size_t stride = (size_t)pv.H * kPartStride;
+    float M = -1e30f;
+    for (int j = 0; j < P.nparts; ++j) M = fmaxf(M, base[j * stride + 64]);
+    float L = 0.f, A = 0.f;
+    for (int j = 0; j < P.nparts; ++j) {
+        const float *pj = base + j * stride;
+        const float a = fast_exp2(pj[64] - M);
+        L = __builtin_fmaf(pj[65], a, L);
+        A = __builtin_fmaf(pj[d], a, A);
+    }
+    const float r = A / L;
+    const size_t o = ((size_t)P.out_row * pv.H + h) * kHeadDim + d;
+    if constexpr (ABF)
+        ((uint16_t *)out)[o] = (uint16_t)bf16_bits(r);
+    else
+        ((float *)out)[o] = r;
+}
+
+// ---------------------------------------------------------------------------------------------
+// launchers
+
+template <int CDT, bool ABF>
+static hipError_t append_impl(const PoolView &pv, const BatchView &bv, int layer, const void *k,
+                              const void *v, hipStream_t stream) {
+    const int nseg = (bv.t + kBlock - 1) / kBlock + 1;
+    hipLaunchKernelGGL((k_append<CDT, ABF>), dim3(bv.n * nseg), dim3(64 * pv.H), 0, stream, pv, bv, layer, k,
+                       v, nseg);
+    return hipGetLastError();
+}
+
+hipError_t launch_append(const PoolView &pv, const BatchView &bv, int layer, const void *k, const void *v,
+                         hipStream_t stream) {
+    if (bv.n == 0) return hipSuccess;
+    switch (pv.cache_dt * 2 + pv.act_dt) {
+    case DT_F32 * 2 + DT_F32: return append_impl<DT_F32, false>(pv, bv, layer, k, v, stream);
+    case DT_BF16 * 2 + DT_BF16: return append_impl<DT_BF16, true>(pv, bv, layer, k, v, stream);
+    case DT_I8 * 2 + DT_BF16: return append_impl<DT_I8, true>(pv, bv, layer, k, v, stream);
+    case DT_I8 * 2 + DT_F32: return append_impl<DT_I8, false>(pv, bv, layer, k, v, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+template <int CDT, bool ABF>
+static hipError_t decode_impl(const PoolView &pv, const BatchView &bv, int layer, const void *q, const void *k,
+                              const void *v, void *out, float scale, bool fused, hipStream_t stream) {
+    const float qmul = scale * 1.4426950408889634f;
+    hipLaunchKernelGGL((k_decode<CDT, ABF>), dim3(bv.nwork), dim3(64 * pv.H), 0, stream, pv, bv, layer, q, k,
+                       v, out, qmul, fused ? 1 : 0);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((k_merge<ABF>), dim3(bv.n), dim3(64 * pv.H), 0, stream, pv, bv, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode(const PoolView &pv, const BatchView &bv, int layer, const void *q, const void *k,
+                         const void *v, void *out, float scale, bool fused, hipStream_t stream) {
+    if (bv.n == 0) return hipSuccess;
+    switch (pv.cache_dt * 2 + pv.act_dt) {
+    case DT_F32 * 2 + DT_F32: return decode_impl<DT_F32, false>(pv, bv, layer, q, k, v, out, scale, fused, stream);
+    case DT_BF16 * 2 + DT_BF16: return decode_impl<DT_BF16, true>(pv, bv, layer, q, k, v, out, scale, fused, stream);
+    case DT_I8 * 2 + DT_BF16: return decode_impl<DT_I8, true>(pv, bv, layer, q, k, v, out, scale, fused, stream);
+    case DT_I8 * 2 + DT_F32: return decode_impl<DT_I8, false>(pv, bv, layer, q, k, v, out, scale, fused, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// eviction on a shifting ring: rotate one kept key row by -count in place (transformer.rs:905-926)
+
+template <int CDT, bool ABF>
+__global__ void k_evict_rotate(PoolView pv, const EvictRow *rows, const float2 *cs_row) {
+    const EvictRow R = rows[blockIdx.x / pv.L];
+    const int layer = blockIdx.x % pv.L;
+    const int h = threadIdx.x >> 5, pr = threadIdx.x & 31;
+    const int page = pv.tables[(size_t)R.sid * pv.mbps + (R.slot >> 4)];
+    const size_t e = tile_index(pv, layer, 0, page, h) * (kBlock * kHeadDim) + (R.slot & 15) * kHeadDim + 2 * pr;
+    float2 x;
+    if constexpr (CDT == DT_F32) {
+        x = *(const float2 *)((const float *)pv.pages + e);
+    } else {
+        uint32_t w = *(const uint32_t *)((const uint16_t *)pv.pages + e);
+        x = make_float2(bf16_value(w & 0xffffu), bf16_value(w >> 16));
+    }
+    const float2 cs = cs_row[pr];
+    float a = x.x * cs.x, b = x.y * cs.y, ee = x.x * cs.y, f = x.y * cs.x;
+    x.x = round_act<ABF>(a - b);
+    x.y = round_act<ABF>(ee + f);
+    if constexpr (CDT == DT_F32)
+        *(float2 *)((float *)pv.pages + e) = x;
+    else
+        *(uint32_t *)((uint16_t *)pv.pages + e) = bf16_bits(x.x) | (bf16_bits(x.y) << 16);
+}
+
+hipError_t launch_evict_rotate(const PoolView &pv, const EvictRow *rows, int n, const float *cs,
+                               const float *, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    const dim3 grid(n * pv.L), block(32 * pv.H);
+    const float2 *csr = (const float2 *)cs;
+    switch (pv.cache_dt * 2 + pv.act_dt) {
+    case DT_F32 * 2 + DT_F32: hipLaunchKernelGGL((k_evict_rotate<DT_F32, false>), grid, block, 0, stream, pv, rows, csr); break;
+    case DT_BF16 * 2 + DT_BF16: hipLaunchKernelGGL((k_evict_rotate<DT_BF16, true>), grid, block, 0, stream, pv, rows, csr); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------
+// page copy (fork of a partial last page, unsharing before a ring): every layer, K and V, scales
+
+__global__ void k_copy_page(PoolView pv, int src, int dst, int tile_u4) {
+    const int layer = blockIdx.x >> 1, kv = blockIdx.x & 1;
+    const uint4 *s = (const uint4 *)pv.pages + tile_index(pv, layer, kv, src, 0) * tile_u4;
+    uint4 *d = (uint4 *)pv.pages + tile_index(pv, layer, kv, dst, 0) * tile_u4;
+    const int n = tile_u4 * pv.H;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) d[i] = s[i];
+    if (pv.scales && threadIdx.x < pv.H)
+        pv.scales[tile_index(pv, layer, kv, dst, threadIdx.x)] = pv.scales[tile_index(pv, layer, kv, src, threadIdx.x)];
+}
+
+hipError_t launch_copy_page(const PoolView &pv, int src_page, int dst_page, hipStream_t stream) {
+    const int es = pv.cache_dt == DT_F32 ? 4 : pv.cache_dt == DT_BF16 ? 2 : 1;
+    const int tile_u4 = kBlock * kHeadDim * es / 16;
+    hipLaunchKernelGGL(k_copy_page, dim3(pv.L * 2), dim3(256), 0, stream, pv, src_page, dst_page, tile_u4);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------
+// raw row I/O: rows [n][H][D] in the cache dtype <-> the stream's pages; int8 scales per page
+
+__global__ void k_rows_io(PoolView pv, int sid, int layer, int kv, int slot0, void *rows, float *scales,
+                          int write, int row_u4) {
+    const int s = blockIdx.x;
+    const int slot = slot0 + s;
+    const int page = pv.tables[(size_t)sid * pv.mbps + (slot >> 4)];
+    const int per_head = row_u4 / pv.H;
+    for (int i = threadIdx.x; i < row_u4; i += blockDim.x) {
+        const int h = i / per_head, w = i % per_head;
+        uint4 *pg = (uint4 *)pv.pages + tile_index(pv, layer, kv, page, h) * (kBlock * per_head) + (slot & 15) * per_head + w;
+        uint4 *rw = (uint4 *)rows + (size_t)s * row_u4 + i;
+        if (write)
+            *pg = *rw;
+        else
+            *rw = *pg;
+    }
+    if (scales && ((slot & 15) == 0 || s == 0) && threadIdx.x < pv.H) {
+        const int bi = (slot >> 4) - (slot0 >> 4);
+        float *ps = pv.scales + tile_index(pv, layer, kv, page, threadIdx.x);
+        float *us = scales + (size_t)bi * pv.H + threadIdx.x;
+        if (write)
+            *ps = *us;
+        else
+            *us = *ps;
+    }
+}
+
+hipError_t launch_rows_io(const PoolView &pv, int sid, int layer, int kv, int slot0, int n, void *rows,
+                          float *scales, bool write, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    const int es = pv.cache_dt == DT_F32 ? 4 : pv.cache_dt == DT_BF16 ? 2 : 1;
+    const int row_u4 = pv.H * kHeadDim * es / 16;
+    hipLaunchKernelGGL(k_rows_io, dim3(n), dim3(256), 0, stream, pv, sid, layer, kv, slot0, rows,
+                       pv.cache_dt == DT_I8 ? scales : nullptr, write ? 1 : 0, row_u4);
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill(const PoolView &, const BatchView &, int, const void *, void *, float, hipStream_t) {
+    return hipErrorNotSupported;
+}
+
+} // namespace xnp

@@ -1,0 +1,961 @@
+// Host side of the paged flow-LM KV cache: the page allocator, per-stream state (current_end,
+// ring slots), batch plans and the C ABI of include/xnp_kv.h.  Kernels are in kernels.hip.
+#include "../../include/xnp_kv.h"
+#include "xnp_internal.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <utility>
+#include <vector>
+
+using namespace xnp;
+
+namespace {
+
+thread_local std::string g_err;
+
+xnp_status fail(xnp_status code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+xnp_status hip_fail(hipError_t e, const char *what) {
+    return fail(XNP_E_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, what)                                                                        \
+    do {                                                                                           \
+        hipError_t e_ = (expr);                                                                    \
+        if (e_ != hipSuccess) return hip_fail(e_, what);                                           \
+    } while (0)
+
+uint64_t splitmix64(uint64_t &s) {
+    uint64_t z = (s += 0x9e3779b97f4a7c15ull);
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+float bf16_round_host(float x) {
+    uint32_t u;
+    std::memcpy(&u, &x, 4);
+    if ((u & 0x7f800000u) == 0x7f800000u) {
+        if (u & 0x007fffffu) u |= 0x00400000u;
+        u &= 0xffff0000u;
+    } else {
+        u += 0x7fffu + ((u >> 16) & 1u);
+        u &= 0xffff0000u;
+    }
+    std::memcpy(&x, &u, 4);
+    return x;
+}
+
+// RotaryEmbedding::at_positions (rope.rs:37-63) for one position: cos/sin of pos * inv_freq[i],
+// inv_freq[i] = 1 / theta^(i / half), each rounded to the activation dtype (rope.rs:55-56).
+void rope_row(int D, float theta, float pos, bool act_bf16, float2 *out) {
+    const int half = D / 2;
+    for (int i = 0; i < half; i++) {
+        float inv_freq = 1.0f / powf(theta, (float)i / (float)half);
+        float angle = pos * inv_freq;
+        float c = cosf(angle), s = sinf(angle);
+        if (act_bf16) {
+            c = bf16_round_host(c);
+            s = bf16_round_host(s);
+        }
+        out[i] = make_float2(c, s);
+    }
+}
+
+struct Stream {
+    bool open = false;
+    int32_t capacity = 0;
+    int32_t current_end = 0;
+    std::vector<int32_t> blocks; // logical block -> page, -1 where none
+    int32_t ring = RING_NONE, write = 0, filled = 0, prefix = 0, shift = 0;
+    std::vector<uint8_t> valid;
+};
+
+// A pinned host buffer an upload is composed in; reused once its copy has completed.
+struct Staging {
+    char *host = nullptr;
+    hipEvent_t done = nullptr;
+    bool pending = false;
+};
+
+constexpr int kStaging = 4;
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+} // namespace
+
+struct xnp_pool {
+    xnp_pool_desc d{};
+    bool host_only = false;
+    int chunk = 8;
+    int esz = 2;
+    int mask_words = 0; // per stream
+    int max_work = 0;
+
+    // device
+    void *pages = nullptr;
+    float *scales = nullptr;
+    int32_t *tables = nullptr;
+    float2 *rope = nullptr;
+    char *dbatch = nullptr; // batch plan upload
+    char *daux = nullptr;   // table patches and eviction rows
+    float *parts = nullptr;
+    size_t batch_bytes = 0, aux_bytes = 0;
+    Staging stage[kStaging];
+    int stage_next = 0;
+    int64_t device_bytes = 0;
+
+    // host
+    std::vector<float2> rope_host;
+    std::vector<Stream> streams;
+    std::vector<int32_t> free_ids;
+    std::vector<int32_t> free_pages;
+    std::vector<int32_t> refcnt;
+    std::vector<TablePatch> patches;
+
+    struct Batch {
+        bool open = false;
+        int n = 0, t = 0, nwork = 0;
+        hipStream_t stream = nullptr;
+        std::vector<int32_t> ids;
+        std::vector<std::pair<int32_t, int32_t>> taken; // (stream, block) pages taken by begin
+        BatchView bv{};
+    } batch;
+
+    PoolView view() const {
+        PoolView pv;
+        pv.pages = pages;
+        pv.scales = scales;
+        pv.tables = tables;
+        pv.rope = rope;
+        pv.L = d.num_layers;
+        pv.H = d.num_heads;
+        pv.KVH = d.num_kv_heads;
+        pv.D = d.head_dim;
+        pv.NB = d.num_blocks;
+        pv.mbps = d.max_blocks_per_stream;
+        pv.max_pos = d.max_pos;
+        pv.cache_dt = d.cache_dtype;
+        pv.act_dt = d.act_dtype;
+        return pv;
+    }
+
+    Stream *get(int32_t id) {
+        if (id < 0 || id >= (int32_t)streams.size() || !streams[id].open) return nullptr;
+        return &streams[id];
+    }
+    const Stream *get(int32_t id) const {
+        if (id < 0 || id >= (int32_t)streams.size() || !streams[id].open) return nullptr;
+        return &streams[id];
+    }
+
+    int32_t take_page(int32_t sid, int32_t blk) {
+        int32_t p = free_pages.back();
+        free_pages.pop_back();
+        refcnt[p] = 1;
+        streams[sid].blocks[blk] = p;
+        patches.push_back({sid, blk, p, 0});
+        return p;
+    }
+
+    void drop_page(int32_t sid, int32_t blk) {
+        int32_t p = streams[sid].blocks[blk];
+        if (p < 0) return;
+        if (--refcnt[p] == 0) free_pages.push_back(p);
+        streams[sid].blocks[blk] = -1;
+        patches.push_back({sid, blk, -1, 0});
+    }
+
+    // A staging buffer free for composing an upload.
+    xnp_status stage_acquire(Staging **out) {
+        Staging &s = stage[stage_next];
+        stage_next = (stage_next + 1) % kStaging;
+        if (s.pending) {
+            HIP_TRY(hipEventSynchronize(s.done), "waiting for a staging buffer");
+            s.pending = false;
+        }
+        *out = &s;
+        return XNP_OK;
+    }
+
+    xnp_status upload(Staging *s, char *dst, size_t bytes, hipStream_t stream) {
+        HIP_TRY(hipMemcpyAsync(dst, s->host, bytes, hipMemcpyHostToDevice, stream), "plan upload");
+        HIP_TRY(hipEventRecord(s->done, stream), "recording an upload");
+        s->pending = true;
+        return XNP_OK;
+    }
+
+    // Apply the queued block-table changes on the device before anything reads the tables.
+    xnp_status flush_patches(hipStream_t stream) {
+        if (host_only) {
+            patches.clear();
+            return XNP_OK;
+        }
+        size_t cap = aux_bytes / sizeof(TablePatch);
+        size_t done = 0;
+        while (done < patches.size()) {
+            size_t n = std::min(cap, patches.size() - done);
+            Staging *s;
+            if (xnp_status st = stage_acquire(&s)) return st;
+            std::memcpy(s->host, patches.data() + done, n * sizeof(TablePatch));
+            if (xnp_status st = upload(s, daux, n * sizeof(TablePatch), stream)) return st;
+            HIP_TRY(launch_patch_tables(view(), (const TablePatch *)daux, (int)n, stream), "table patch");
+            done += n;
+        }
+        patches.clear();
+        return XNP_OK;
+    }
+
+    // Give `sid` its own copy of every page it shares (before in-place writes).
+    xnp_status unshare(int32_t sid, hipStream_t stream) {
+        Stream &s = streams[sid];
+        int need = 0;
+        for (int32_t p : s.blocks)
+            if (p >= 0 && refcnt[p] > 1) need++;
+        if (need > (int)free_pages.size())
+            return fail(XNP_E_OUT_OF_BLOCKS, "out of blocks: %d needed to unshare, %d free", need,
+                        (int)free_pages.size());
+        std::vector<std::pair<int32_t, int32_t>> copies;
+        for (size_t b = 0; b < s.blocks.size(); b++) {
+            int32_t p = s.blocks[b];
+            if (p < 0 || refcnt[p] <= 1) continue;
+            refcnt[p]--;
+            int32_t q = take_page(sid, (int32_t)b);
+            copies.push_back({p, q});
+        }
+        if (!host_only)
+            for (auto &c : copies) HIP_TRY(launch_copy_page(view(), c.first, c.second, stream), "page copy");
+        return XNP_OK;
+    }
+};
+
+// ---------------------------------------------------------------------------------------------
+// pool
+
+extern "C" const char *xnp_last_error(void) { return g_err.c_str(); }
+
+extern "C" int32_t xnp_frame_budget(int32_t num_tokens, double frame_rate) {
+    // plan.rs:43-45
+    return (int32_t)std::ceil(((double)num_tokens / 3.0 + 2.0) * frame_rate);
+}
+
+extern "C" int32_t xnp_seq_budget(int32_t num_tokens, int32_t frame_budget) {
+    // plan.rs:25, 52-54
+    return num_tokens + 512 + frame_budget;
+}
+
+static void pool_free(xnp_pool *p) {
+    if (!p->host_only) {
+        for (auto &s : p->stage) {
+            if (s.pending && s.done) (void)hipEventSynchronize(s.done);
+            if (s.done) (void)hipEventDestroy(s.done);
+            if (s.host) (void)hipHostFree(s.host);
+        }
+        void *bufs[] = {p->pages, p->scales, p->tables, p->rope, p->dbatch, p->daux, p->parts};
+        for (void *b : bufs)
+            if (b) (void)hipFree(b);
+    }
+    delete p;
+}
+
+extern "C" xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out) {
+    if (!desc || !out) return fail(XNP_E_INVALID, "null argument");
+    *out = nullptr;
+    const xnp_pool_desc &d = *desc;
+    if (d.num_layers <= 0 || d.num_blocks <= 0 || d.max_streams <= 0 || d.max_blocks_per_stream <= 0)
+        return fail(XNP_E_INVALID, "layers, blocks, streams and blocks per stream must be positive");
+    if (d.num_heads <= 0 || d.num_heads > kMaxHeads)
+        return fail(XNP_E_HEADS, "the config's %d attention heads are not in 1..%d", d.num_heads, kMaxHeads);
+    if (d.num_kv_heads <= 0 || d.num_heads % d.num_kv_heads)
+        return fail(XNP_E_HEADS, "the config's %d key/value heads do not divide its %d attention heads",
+                    d.num_kv_heads, d.num_heads);
+    if (d.head_dim != kHeadDim) return fail(XNP_E_INVALID, "head_dim %d: the kernels take %d", d.head_dim, kHeadDim);
+    const bool combo_ok = (d.cache_dtype == XNP_F32 && d.act_dtype == XNP_F32) ||
+                          (d.cache_dtype == XNP_BF16 && d.act_dtype == XNP_BF16) ||
+                          (d.cache_dtype == XNP_I8 && (d.act_dtype == XNP_BF16 || d.act_dtype == XNP_F32));
+    if (!combo_ok)
+        return fail(XNP_E_INVALID, "cache dtype %d with activation dtype %d is not supported", d.cache_dtype,
+                    d.act_dtype);
+    if (d.max_pos <= 0 || !(d.max_period > 0.0f)) return fail(XNP_E_INVALID, "max_pos and max_period must be positive");
+    if (d.chunk_blocks < 0 || d.chunk_blocks > 64) return fail(XNP_E_INVALID, "chunk_blocks %d not in 0..64", d.chunk_blocks);
+    if ((int64_t)d.max_streams * d.max_blocks_per_stream > (int64_t)1 << 28)
+        return fail(XNP_E_INVALID, "max_streams x max_blocks_per_stream too large");
+
+    xnp_pool *p = new (std::nothrow) xnp_pool();
+    if (!p) return fail(XNP_E_INVALID, "out of host memory");
+    p->d = d;
+    p->host_only = (d.flags & XNP_POOL_HOST_ONLY) != 0;
+    p->chunk = d.chunk_blocks ? d.chunk_blocks : 8;
+    p->esz = d.cache_dtype == XNP_F32 ? 4 : d.cache_dtype == XNP_BF16 ? 2 : 1;
+    p->mask_words = (d.max_blocks_per_stream * kBlock + 31) / 32;
+    p->max_work = d.max_streams * ((d.max_blocks_per_stream + p->chunk - 1) / p->chunk);
+
+    p->streams.resize(d.max_streams);
+    for (int32_t i = d.max_streams - 1; i >= 0; i--) p->free_ids.push_back(i);
+    p->refcnt.assign(d.num_blocks, 0);
+    std::vector<int32_t> order(d.num_blocks);
+    for (int32_t i = 0; i < d.num_blocks; i++) order[i] = i;
+    if (d.page_seed) {
+        uint64_t s = d.page_seed;
+        for (int32_t i = d.num_blocks - 1; i > 0; i--) {
+            // Fisher-Yates with an unbiased draw in [0, i] by rejection
+            uint64_t bound = (uint64_t)i + 1, lim = UINT64_MAX - UINT64_MAX % bound, r;
+            do r = splitmix64(s); while (r >= lim);
+            std::swap(order[i], order[(size_t)(r % bound)]);
+        }
+    }
+    p->free_pages.assign(order.rbegin(), order.rend()); // pop_back hands out order[0] first
+
+    const int half = d.head_dim / 2;
+    p->rope_host.resize((size_t)d.max_pos * half);
+    for (int32_t pos = 0; pos < d.max_pos; pos++)
+        rope_row(d.head_dim, d.max_period, (float)pos, d.act_dtype == XNP_BF16, &p->rope_host[(size_t)pos * half]);
+
+    // plan upload layout: plans, work items, masks (each 256-byte aligned)
+    p->batch_bytes = align_up(sizeof(StreamPlan) * d.max_streams, 256) + align_up(sizeof(WorkItem) * p->max_work, 256) +
+                     align_up(sizeof(uint32_t) * (size_t)p->mask_words * d.max_streams, 256);
+    p->aux_bytes = std::max<size_t>(sizeof(TablePatch) * 65536,
+                                    align_up(sizeof(EvictRow) * d.max_blocks_per_stream * kBlock, 256) + 4096);
+
+    if (p->host_only) {
+        *out = p;
+        return XNP_OK;
+    }
+
+    auto dev_fail = [&](hipError_t e, const char *what) {
+        xnp_status st = hip_fail(e, what);
+        pool_free(p);
+        return st;
+    };
+    hipError_t e = hipSetDevice(d.device);
+    if (e != hipSuccess) return dev_fail(e, "hipSetDevice");
+    const size_t page_elems = (size_t)d.num_heads * kBlock * d.head_dim;
+    const size_t page_bytes = page_elems * p->esz;
+    const size_t pages_bytes = page_bytes * d.num_blocks * 2 * d.num_layers;
+    struct {
+        void **ptr;
+        size_t bytes;
+        const char *what;
+    } allocs[] = {
+        {&p->pages, pages_bytes, "pages"},
+        {(void **)&p->scales, d.cache_dtype == XNP_I8 ? sizeof(float) * d.num_heads * (size_t)d.num_blocks * 2 * d.num_layers : 0, "scales"},
+        {(void **)&p->tables, sizeof(int32_t) * (size_t)d.max_streams * d.max_blocks_per_stream, "block tables"},
+        {(void **)&p->rope, sizeof(float2) * p->rope_host.size(), "rope table"},
+        {(void **)&p->dbatch, p->batch_bytes, "batch plan"},
+        {(void **)&p->daux, p->aux_bytes, "aux upload"},
+        {(void **)&p->parts, sizeof(float) * kPartStride * d.num_heads * (size_t)p->max_work, "partials"},
+    };
+    for (auto &a : allocs) {
+        if (!a.bytes) continue;
+        e = hipMalloc(a.ptr, a.bytes);
+        if (e != hipSuccess) return dev_fail(e, a.what);
+        p->device_bytes += (int64_t)a.bytes;
+    }
+    e = hipMemset(p->tables, 0xff, sizeof(int32_t) * (size_t)d.max_streams * d.max_blocks_per_stream);
+    if (e != hipSuccess) return dev_fail(e, "table init");
+    if (p->scales) {
+        e = hipMemset(p->scales, 0, sizeof(float) * d.num_heads * (size_t)d.num_blocks * 2 * d.num_layers);
+        if (e != hipSuccess) return dev_fail(e, "scale init");
+    }
+    e = hipMemcpy(p->rope, p->rope_host.data(), sizeof(float2) * p->rope_host.size(), hipMemcpyHostToDevice);
+    if (e != hipSuccess) return dev_fail(e, "rope table upload");
+    const size_t stage_bytes = std::max(p->batch_bytes, p->aux_bytes);
+    for (auto &s : p->stage) {
+        e = hipHostMalloc((void **)&s.host, stage_bytes, hipHostMallocDefault);
+        if (e != hipSuccess) return dev_fail(e, "pinned staging");
+        e = hipEventCreateWithFlags(&s.done, hipEventDisableTiming);
+        if (e != hipSuccess) return dev_fail(e, "staging event");
+    }
+    e = hipDeviceSynchronize();
+    if (e != hipSuccess) return dev_fail(e, "pool init");
+    *out = p;
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_pool_destroy(xnp_pool *pool) {
+    if (!pool) return XNP_OK;
+    if (!pool->host_only) (void)hipSetDevice(pool->d.device);
+    pool_free(pool);
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_pool_stats_get(const xnp_pool *pool, xnp_pool_stats *out) {
+    if (!pool || !out) return fail(XNP_E_INVALID, "null argument");
+    out->free_blocks = (int32_t)pool->free_pages.size();
+    out->open_streams = (int32_t)(pool->streams.size() - pool->free_ids.size());
+    out->batch_open = pool->batch.open ? std::max(pool->batch.n, 1) : 0;
+    out->work_items = pool->batch.open ? pool->batch.nwork : 0;
+    out->device_bytes = pool->device_bytes;
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_pool_rope_rows(const xnp_pool *pool, int32_t pos0, int32_t n, float *cos_sin) {
+    if (!pool || !cos_sin) return fail(XNP_E_INVALID, "null argument");
+    if (pos0 < 0 || n < 0 || pos0 + n > pool->d.max_pos)
+        return fail(XNP_E_INVALID, "rows %d..%d of a %d-row table", pos0, pos0 + n, pool->d.max_pos);
+    const size_t half = pool->d.head_dim / 2;
+    std::memcpy(cos_sin, pool->rope_host.data() + (size_t)pos0 * half, sizeof(float2) * half * n);
+    return XNP_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// streams
+
+static xnp_status no_batch(const xnp_pool *p) {
+    if (p->batch.open) return fail(XNP_E_STATE, "a batch is open: end or abort it first");
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_stream_open(xnp_pool *pool, int32_t capacity, int32_t *id) {
+    if (!pool || !id) return fail(XNP_E_INVALID, "null argument");
+    if (xnp_status st = no_batch(pool)) return st;
+    const int32_t maxcap = pool->d.max_blocks_per_stream * kBlock;
+    if (capacity < 0 || capacity > maxcap)
+        return fail(XNP_E_INVALID, "capacity %d: a stream holds at most %d positions", capacity, maxcap);
+    if (pool->free_ids.empty()) return fail(XNP_E_STREAM, "all %d streams are open", pool->d.max_streams);
+    int32_t sid = pool->free_ids.back();
+    pool->free_ids.pop_back();
+    Stream &s = pool->streams[sid];
+    s = Stream();
+    s.open = true;
+    s.capacity = capacity;
+    s.blocks.assign((capacity + kBlock - 1) / kBlock, -1);
+    *id = sid;
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_stream_close(xnp_pool *pool, int32_t id) {
+    if (!pool) return fail(XNP_E_INVALID, "null argument");
+    if (xnp_status st = no_batch(pool)) return st;
+    Stream *s = pool->get(id);
+    if (!s) return fail(XNP_E_STREAM, "no open stream %d", id);
+    for (size_t b = 0; b < s->blocks.size(); b++) pool->drop_page(id, (int32_t)b);
+    *s = Stream();
+    pool->free_ids.push_back(id);
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_stream_fork(xnp_pool *pool, int32_t src, int32_t capacity, int32_t *id,
+                                      void *hip_stream) {
+    if (!pool || !id) return fail(XNP_E_INVALID, "null argument");
+    if (xnp_status st = no_batch(pool)) return st;
+    Stream *s = pool->get(src);
+    if (!s) return fail(XNP_E_STREAM, "no open stream %d", src);
+    if (s->ring != RING_NONE) return fail(XNP_E_BUDGET, "a ring cache cannot be resized");
+    const int32_t used = s->current_end;
+    if (used > capacity)
+        return fail(XNP_E_BUDGET, "cannot fit %d filled KV positions into a budget of %d", used, capacity);
+    const int32_t maxcap = pool->d.max_blocks_per_stream * kBlock;
+    if (capacity > maxcap)
+        return fail(XNP_E_INVALID, "capacity %d: a stream holds at most %d positions", capacity, maxcap);
+    if (pool->free_ids.empty()) return fail(XNP_E_STREAM, "all %d streams are open", pool->d.max_streams);
+    const bool tail = used % kBlock != 0;
+    if (tail && pool->free_pages.empty()) return fail(XNP_E_OUT_OF_BLOCKS, "out of blocks: the pool has no free page");
+    int32_t dst;
+    xnp_status st = xnp_stream_open(pool, capacity, &dst);
+    if (st) return st;
+    s = pool->get(src); // streams may not move, but keep the reference fresh
+    Stream &t = pool->streams[dst];
+    t.current_end = used;
+    const int32_t full = used / kBlock;
+    for (int32_t b = 0; b < full; b++) {
+        int32_t p = s->blocks[b];
+        t.blocks[b] = p;
+        pool->refcnt[p]++;
+        pool->patches.push_back({dst, b, p, 0});
+    }
+    if (tail) {
+        int32_t q = pool->take_page(dst, full);
+        if (!pool->host_only) {
+            hipStream_t hs = (hipStream_t)hip_stream;
+            HIP_TRY(hipSetDevice(pool->d.device), "hipSetDevice");
+            HIP_TRY(launch_copy_page(pool->view(), s->blocks[full], q, hs), "page copy");
+        }
+    }
+    *id = dst;
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_stream_info_get(const xnp_pool *pool, int32_t id, xnp_stream_info *out) {
+    if (!pool || !out) return fail(XNP_E_INVALID, "null argument");
+    const Stream *s = pool->get(id);
+    if (!s) return fail(XNP_E_STREAM, "no open stream %d", id);
+    out->current_end = s->current_end;
+    out->capacity = s->capacity;
+    out->ring_mode = s->ring;
+    out->ring_write = s->write;
+    out->ring_filled = s->filled;
+    out->ring_prefix = s->prefix;
+    out->ring_shift = s->shift;
+    int32_t in_view = 0, blocks = 0, shared = 0;
+    for (uint8_t v : s->valid) in_view += v;
+    for (int32_t p : s->blocks)
+        if (p >= 0) {
+            blocks++;
+            shared += pool->refcnt[p] > 1;
+        }
+    out->in_view = in_view;
+    out->blocks = blocks;
+    out->shared = shared;
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_stream_blocks(const xnp_pool *pool, int32_t id, int32_t *pages, int32_t cap,
+                                        int32_t *count) {
+    if (!pool || !count) return fail(XNP_E_INVALID, "null argument");
+    const Stream *s = pool->get(id);
+    if (!s) return fail(XNP_E_STREAM, "no open stream %d", id);
+    *count = (int32_t)s->blocks.size();
+    if (pages)
+        for (int32_t i = 0; i < std::min(cap, *count); i++) pages[i] = s->blocks[i];
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_ring_valid(const xnp_pool *pool, int32_t id, uint8_t *valid, int32_t cap) {
+    if (!pool || !valid) return fail(XNP_E_INVALID, "null argument");
+    const Stream *s = pool->get(id);
+    if (!s) return fail(XNP_E_STREAM, "no open stream %d", id);
+    for (int32_t i = 0; i < std::min(cap, s->capacity); i++)
+        valid[i] = s->ring == RING_NONE ? (i < s->current_end) : s->valid[i];
+    return XNP_OK;
+}
+
+// Pages for blocks [b0, b1) of stream sid, all or nothing.
+static xnp_status take_range(xnp_pool *pool, int32_t sid, int32_t b0, int32_t b1,
+                             std::vector<std::pair<int32_t, int32_t>> *taken) {
+    Stream &s = pool->streams[sid];
+    int need = 0;
+    for (int32_t b = b0; b < b1; b++) need += s.blocks[b] < 0;
+    if (need > (int)pool->free_pages.size())
+        return fail(XNP_E_OUT_OF_BLOCKS, "out of blocks: %d needed, %d free", need, (int)pool->free_pages.size());
+    for (int32_t b = b0; b < b1; b++)
+        if (s.blocks[b] < 0) {
+            pool->take_page(sid, b);
+            if (taken) taken->push_back({sid, b});
+        }
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_stream_advance(xnp_pool *pool, int32_t id, int32_t n) {
+    if (!pool) return fail(XNP_E_INVALID, "null argument");
+    if (xnp_status st = no_batch(pool)) return st;
+    Stream *s = pool->get(id);
+    if (!s) return fail(XNP_E_STREAM, "no open stream %d", id);
+    if (s->ring != RING_NONE) return fail(XNP_E_RING, "a ring cache steps one row at a time");
+    if (n < 0 || s->current_end + n > s->capacity)
+        return fail(XNP_E_NO_ROOM, "no room left: the stream holds %d positions", s->capacity);
+    if (n == 0) return XNP_OK;
+    if (s->current_end + n > pool->d.max_pos)
+        return fail(XNP_E_INVALID, "position %d is beyond the RoPE table (%d rows)", s->current_end + n - 1,
+                    pool->d.max_pos);
+    const int32_t b0 = s->current_end / kBlock, b1 = (s->current_end + n - 1) / kBlock + 1;
+    if (xnp_status st = take_range(pool, id, b0, b1, nullptr)) return st;
+    s->current_end += n;
+    return XNP_OK;
+}
+
+static xnp_status rows_check(const xnp_pool *pool, int32_t id, int32_t layer, int32_t kv, int32_t slot0,
+                             int32_t n, const void *rows) {
+    if (!pool || (!rows && n > 0)) return fail(XNP_E_INVALID, "null argument");
+    if (pool->host_only) return fail(XNP_E_STATE, "a host-only pool has no device pages");
+    const Stream *s = pool->get(id);
+    if (!s) return fail(XNP_E_STREAM, "no open stream %d", id);
+    if (layer < 0 || layer >= pool->d.num_layers) return fail(XNP_E_INVALID, "layer %d of %d", layer, pool->d.num_layers);
+    if (kv != 0 && kv != 1) return fail(XNP_E_INVALID, "kv %d is neither keys (0) nor values (1)", kv);
+    if (slot0 < 0 || n < 0 || slot0 + n > s->capacity)
+        return fail(XNP_E_INVALID, "rows %d..%d of a %d-slot stream", slot0, slot0 + n, s->capacity);
+    for (int32_t slot = slot0; slot < slot0 + n; slot += kBlock - slot % kBlock)
+        if (s->blocks[slot / kBlock] < 0) return fail(XNP_E_INVALID, "slot %d has no page", slot);
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_write_rows(xnp_pool *pool, int32_t id, int32_t layer, int32_t kv, int32_t slot0,
+                                     int32_t n, const void *rows, const float *scales, void *hip_stream) {
+    if (xnp_status st = rows_check(pool, id, layer, kv, slot0, n, rows)) return st;
+    if (pool->d.cache_dtype == XNP_I8 && !scales && n > 0) return fail(XNP_E_INVALID, "an int8 cache needs scales");
+    if (n == 0) return XNP_OK;
+    hipStream_t hs = (hipStream_t)hip_stream;
+    HIP_TRY(hipSetDevice(pool->d.device), "hipSetDevice");
+    // Copy on write: a page shared with a fork gets a copy of its own first.
+    Stream &s = pool->streams[id];
+    const int32_t b0 = slot0 / kBlock, b1 = (slot0 + n - 1) / kBlock + 1;
+    int need = 0;
+    for (int32_t b = b0; b < b1; b++) need += pool->refcnt[s.blocks[b]] > 1;
+    if (need > (int)pool->free_pages.size())
+        return fail(XNP_E_OUT_OF_BLOCKS, "out of blocks: %d needed to copy shared pages", need);
+    for (int32_t b = b0; b < b1; b++) {
+        int32_t p = s.blocks[b];
+        if (pool->refcnt[p] <= 1) continue;
+        pool->refcnt[p]--;
+        int32_t q = pool->take_page(id, b);
+        HIP_TRY(launch_copy_page(pool->view(), p, q, hs), "page copy");
+    }
+    if (xnp_status st = pool->flush_patches(hs)) return st;
+    HIP_TRY(launch_rows_io(pool->view(), id, layer, kv, slot0, n, const_cast<void *>(rows),
+                           const_cast<float *>(scales), true, hs),
+            "row write");
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_read_rows(const xnp_pool *cpool, int32_t id, int32_t layer, int32_t kv, int32_t slot0,
+                                    int32_t n, void *rows, float *scales, void *hip_stream) {
+    if (xnp_status st = rows_check(cpool, id, layer, kv, slot0, n, rows)) return st;
+    if (n == 0) return XNP_OK;
+    xnp_pool *pool = const_cast<xnp_pool *>(cpool); // pending table patches must reach the device
+    hipStream_t hs = (hipStream_t)hip_stream;
+    HIP_TRY(hipSetDevice(pool->d.device), "hipSetDevice");
+    if (xnp_status st = pool->flush_patches(hs)) return st;
+    HIP_TRY(launch_rows_io(pool->view(), id, layer, kv, slot0, n, rows, scales, false, hs), "row read");
+    return XNP_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// ring: transformer.rs:842-929
+
+extern "C" xnp_status xnp_ring_start(xnp_pool *pool, int32_t id, int32_t mode, int32_t prefix, void *hip_stream) {
+    if (!pool) return fail(XNP_E_INVALID, "null argument");
+    if (xnp_status st = no_batch(pool)) return st;
+    Stream *s = pool->get(id);
+    if (!s) return fail(XNP_E_STREAM, "no open stream %d", id);
+    if (mode != XNP_RING_SHIFT && mode != XNP_RING_ABSOLUTE) return fail(XNP_E_INVALID, "bad ring mode %d", mode);
+    if (s->ring != RING_NONE) return fail(XNP_E_RING, "the cache is a ring already");
+    if (prefix < 0 || prefix > s->capacity)
+        return fail(XNP_E_INVALID, "prefix %d of a %d-slot cache", prefix, s->capacity);
+    if (!pool->host_only) HIP_TRY(hipSetDevice(pool->d.device), "hipSetDevice");
+    if (xnp_status st = pool->unshare(id, (hipStream_t)hip_stream)) return st;
+    const int32_t used = s->current_end;
+    s->valid.assign(s->capacity, 0);
+    for (int32_t i = 0; i < used; i++) s->valid[i] = 1;
+    s->ring = mode;
+    s->write = used;
+    s->filled = used;
+    s->prefix = mode == XNP_RING_ABSOLUTE ? prefix : 0;
+    s->shift = 0;
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_ring_set_slot(xnp_pool *pool, int32_t id, int32_t slot) {
+    if (!pool) return fail(XNP_E_INVALID, "null argument");
+    if (xnp_status st = no_batch(pool)) return st;
+    Stream *s = pool->get(id);
+    if (!s) return fail(XNP_E_STREAM, "no open stream %d", id);
+    if (s->ring == RING_NONE) return fail(XNP_E_RING, "not a ring cache, see start_ring");
+    if (slot < 0 || slot >= s->capacity) return fail(XNP_E_RING, "slot %d of a %d-slot ring", slot, s->capacity);
+    s->write = slot;
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_ring_evict(xnp_pool *pool, int32_t id, int32_t prefix, const int32_t *slots,
+                                     int32_t count, void *hip_stream) {
+    if (!pool || (count > 0 && !slots)) return fail(XNP_E_INVALID, "null argument");
+    if (xnp_status st = no_batch(pool)) return st;
+    Stream *s = pool->get(id);
+    if (!s) return fail(XNP_E_STREAM, "no open stream %d", id);
+    if (s->ring == RING_NONE) return fail(XNP_E_RING, "not a ring cache, see start_ring");
+    if (count < 0 || count > s->current_end)
+        return fail(XNP_E_EVICT, "cannot evict %d of %d positions", count, s->current_end);
+    if (s->ring == RING_ABSOLUTE && prefix != s->prefix)
+        return fail(XNP_E_EVICT, "an absolute ring evicts past its prefix %d, not %d", s->prefix, prefix);
+    if (s->ring == RING_SHIFT && pool->d.cache_dtype == XNP_I8)
+        return fail(XNP_E_EVICT, "an int8 cache evicts on an absolute ring");
+    // Every slot is checked before any change (transformer.rs:896-901).
+    for (int32_t j = 0; j < count; j++) {
+        const int32_t sl = slots[j];
+        if (sl < prefix || sl < 0 || sl >= s->capacity || !s->valid[sl])
+            return fail(XNP_E_EVICT, "slot %d holds no row past the prefix", sl);
+    }
+    std::vector<EvictRow> rows;
+    if (s->ring == RING_SHIFT && count > 0) {
+        for (int32_t sl = prefix; sl < s->filled; sl++) {
+            bool evicted = false;
+            for (int32_t j = 0; j < count && !evicted; j++) evicted = slots[j] == sl;
+            if (s->valid[sl] && !evicted) rows.push_back({id, sl});
+        }
+        // The rows must fit one upload (max_blocks_per_stream * 16 of them always do).
+        if (!pool->host_only && !rows.empty()) {
+            hipStream_t hs = (hipStream_t)hip_stream;
+            HIP_TRY(hipSetDevice(pool->d.device), "hipSetDevice");
+            if (xnp_status st = pool->flush_patches(hs)) return st;
+            Staging *sg;
+            if (xnp_status st = pool->stage_acquire(&sg)) return st;
+            const int half = pool->d.head_dim / 2;
+            rope_row(pool->d.head_dim, pool->d.max_period, -(float)count, pool->d.act_dtype == XNP_BF16,
+                     (float2 *)sg->host);
+            const size_t roff = 4096;
+            static_assert(sizeof(float2) * 32 <= 4096, "rope row fits the header");
+            (void)half;
+            std::memcpy(sg->host + roff, rows.data(), sizeof(EvictRow) * rows.size());
+            if (xnp_status st = pool->upload(sg, pool->daux, roff + sizeof(EvictRow) * rows.size(), hs)) return st;
+            HIP_TRY(launch_evict_rotate(pool->view(), (const EvictRow *)(pool->daux + roff), (int)rows.size(),
+                                        (const float *)pool->daux, nullptr, hs),
+                    "evict rotate");
+        }
+    }
+    for (int32_t j = 0; j < count; j++) s->valid[slots[j]] = 0;
+    if (s->ring == RING_ABSOLUTE) s->shift += count;
+    s->current_end -= count;
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_ring_slide(xnp_pool *pool, int32_t id, int32_t prefix, int32_t span, int32_t window,
+                                     int32_t drop, int64_t step, void *hip_stream) {
+    if (!pool) return fail(XNP_E_INVALID, "null argument");
+    if (xnp_status st = no_batch(pool)) return st;
+    Stream *s = pool->get(id);
+    if (!s) return fail(XNP_E_STREAM, "no open stream %d", id);
+    if (s->ring == RING_NONE) return fail(XNP_E_RING, "not a ring cache, see start_ring");
+    if (span <= 0 || window <= 0 || window > span || drop <= 0 || drop > window || prefix < 0 ||
+        prefix + span > s->capacity || step < 0)
+        return fail(XNP_E_INVALID, "slide over %d slots past %d with a window of %d, dropping %d, at step %lld",
+                    span, prefix, window, drop, (long long)step);
+    int32_t in_view = 0;
+    for (int32_t sl = prefix; sl < prefix + span; sl++) in_view += s->valid[sl];
+    if (in_view == window) {
+        // s2s.rs:324-332: frames take the slots after the prefix in turn, so the oldest are the
+        // next ones round.
+        const int64_t oldest = step - in_view;
+        std::vector<int32_t> slots(drop);
+        for (int32_t j = 0; j < drop; j++)
+            slots[j] = prefix + (int32_t)((((oldest + j) % span) + span) % span);
+        if (xnp_status st = xnp_ring_evict(pool, id, prefix, slots.data(), drop, hip_stream)) return st;
+    }
+    return xnp_ring_set_slot(pool, id, prefix + (int32_t)(step % span));
+}
+
+// ---------------------------------------------------------------------------------------------
+// batches
+
+extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_t n, int32_t t, void *hip_stream) {
+    if (!pool || (n > 0 && !ids)) return fail(XNP_E_INVALID, "null argument");
+    if (xnp_status st = no_batch(pool)) return st;
+    if (n < 0 || n > pool->d.max_streams) return fail(XNP_E_INVALID, "%d streams in a batch of at most %d", n, pool->d.max_streams);
+    if (t <= 0) return fail(XNP_E_INVALID, "a step appends at least one row, not %d", t);
+    // check everything first
+    std::vector<uint8_t> seen(pool->streams.size(), 0);
+    int need = 0;
+    for (int32_t i = 0; i < n; i++) {
+        const int32_t id = ids[i];
+        const Stream *s = pool->get(id);
+        if (!s) return fail(XNP_E_STREAM, "no open stream %d", id);
+        if (seen[id]) return fail(XNP_E_INVALID, "stream %d appears twice in the batch", id);
+        seen[id] = 1;
+        int32_t last_pos;
+        if (s->ring != RING_NONE) {
+            if (t != 1) return fail(XNP_E_RING, "a ring cache takes one row at a time, not %d", t);
+            if (s->valid[s->write]) return fail(XNP_E_RING, "ring slot %d still holds a row, evict it first", s->write);
+            need += s->blocks[s->write / kBlock] < 0;
+            last_pos = s->current_end + (s->ring == RING_ABSOLUTE ? s->shift : 0);
+        } else {
+            if (s->current_end + t > s->capacity)
+                return fail(XNP_E_NO_ROOM, "no room left: the stream holds %d positions", s->capacity);
+            for (int32_t b = s->current_end / kBlock; b <= (s->current_end + t - 1) / kBlock; b++) need += s->blocks[b] < 0;
+            last_pos = s->current_end + t - 1;
+        }
+        if (last_pos >= pool->d.max_pos)
+            return fail(XNP_E_INVALID, "position %d is beyond the RoPE table (%d rows)", last_pos, pool->d.max_pos);
+    }
+    if (need > (int)pool->free_pages.size())
+        return fail(XNP_E_OUT_OF_BLOCKS, "out of blocks: %d needed, %d free", need, (int)pool->free_pages.size());
+
+    auto &B = pool->batch;
+    B.ids.assign(ids, ids + n);
+    B.taken.clear();
+    B.n = n;
+    B.t = t;
+    B.stream = (hipStream_t)hip_stream;
+    for (int32_t i = 0; i < n; i++) {
+        Stream &s = pool->streams[ids[i]];
+        if (s.ring != RING_NONE)
+            take_range(pool, ids[i], s.write / kBlock, s.write / kBlock + 1, &B.taken);
+        else
+            take_range(pool, ids[i], s.current_end / kBlock, (s.current_end + t - 1) / kBlock + 1, &B.taken);
+    }
+
+    // the plan, composed in host memory laid out as the device buffer
+    std::vector<StreamPlan> plans(n);
+    std::vector<WorkItem> work;
+    std::vector<uint32_t> masks;
+    int32_t parts = 0;
+    for (int32_t i = 0; i < n; i++) {
+        const Stream &s = pool->streams[ids[i]];
+        StreamPlan &P = plans[i];
+        std::memset(&P, 0, sizeof P);
+        P.sid = ids[i];
+        P.out_row = i;
+        P.mask_off = -1;
+        if (s.ring == RING_NONE) {
+            P.pos = P.pos_pre = s.current_end;
+            P.write_slot = s.current_end;
+            P.key_pos = s.current_end;
+            P.span = s.current_end + 1;
+        } else {
+            P.pos_pre = s.current_end;
+            P.pos = s.current_end + (s.ring == RING_ABSOLUTE ? s.shift : 0);
+            P.prefix = s.ring == RING_ABSOLUTE ? s.prefix : 0;
+            P.write_slot = s.write;
+            P.key_pos = (s.ring == RING_ABSOLUTE && s.write >= s.prefix) ? P.pos : P.pos_pre;
+            P.span = std::max(s.filled, s.write + 1);
+            P.ring = 1;
+            // RingSlots::decode_mask (transformer.rs:42-52): valid slots and the write slot.
+            P.mask_off = (int32_t)masks.size();
+            const int words = (P.span + 31) / 32;
+            masks.resize(masks.size() + words, 0u);
+            for (int32_t sl = 0; sl < P.span; sl++)
+                if (s.valid[sl] || sl == s.write) masks[P.mask_off + sl / 32] |= 1u << (sl % 32);
+            const int32_t b0 = s.write / kBlock * kBlock, b1 = std::min(b0 + kBlock, s.capacity);
+            int other = 0;
+            for (int32_t sl = b0; sl < b1; sl++) other |= (sl != s.write && s.valid[sl]);
+            P.fresh = !other;
+        }
+        if (t == 1) {
+            const int32_t nblk = (P.span + kBlock - 1) / kBlock;
+            const int32_t np = (nblk + pool->chunk - 1) / pool->chunk;
+            P.part0 = parts;
+            P.nparts = np;
+            const int32_t base = nblk / np, rem = nblk % np;
+            int32_t blk = 0;
+            const int32_t wblk = P.write_slot / kBlock;
+            for (int32_t j = 0; j < np; j++) {
+                const int32_t len = base + (j < rem ? 1 : 0);
+                work.push_back({i, blk, blk + len, parts + j});
+                if (wblk >= blk && wblk < blk + len) P.app_part = parts + j;
+                blk += len;
+            }
+            parts += np;
+        }
+    }
+    // longest work items first, so the short ones fill the tail of the launch
+    std::stable_sort(work.begin(), work.end(),
+                     [](const WorkItem &a, const WorkItem &b) { return a.blk1 - a.blk0 > b.blk1 - b.blk0; });
+    B.nwork = (int32_t)work.size();
+
+    if (pool->host_only) {
+        B.open = true;
+        return XNP_OK;
+    }
+    hipStream_t hs = B.stream;
+    auto undo = [&](xnp_status st) {
+        for (auto it = B.taken.rbegin(); it != B.taken.rend(); ++it) pool->drop_page(it->first, it->second);
+        B.taken.clear();
+        return st;
+    };
+    hipError_t he = hipSetDevice(pool->d.device);
+    if (he != hipSuccess) return undo(hip_fail(he, "hipSetDevice"));
+    if (xnp_status st = pool->flush_patches(hs)) return undo(st);
+    Staging *sg;
+    if (xnp_status st = pool->stage_acquire(&sg)) return undo(st);
+    const size_t o_plans = 0;
+    const size_t o_work = align_up(sizeof(StreamPlan) * n, 256);
+    const size_t o_masks = o_work + align_up(sizeof(WorkItem) * work.size(), 256);
+    const size_t total = o_masks + sizeof(uint32_t) * masks.size();
+    std::memcpy(sg->host + o_plans, plans.data(), sizeof(StreamPlan) * n);
+    std::memcpy(sg->host + o_work, work.data(), sizeof(WorkItem) * work.size());
+    std::memcpy(sg->host + o_masks, masks.data(), sizeof(uint32_t) * masks.size());
+    if (xnp_status st = pool->upload(sg, pool->dbatch, total, hs)) return undo(st);
+    B.bv.plans = (const StreamPlan *)(pool->dbatch + o_plans);
+    B.bv.work = (const WorkItem *)(pool->dbatch + o_work);
+    B.bv.masks = (const uint32_t *)(pool->dbatch + o_masks);
+    B.bv.parts = pool->parts;
+    B.bv.n = n;
+    B.bv.t = t;
+    B.bv.nwork = B.nwork;
+    B.open = true;
+    return XNP_OK;
+}
+
+static xnp_status batch_call(xnp_pool *pool, int32_t layer, void *hip_stream, bool decode) {
+    if (!pool) return fail(XNP_E_INVALID, "null argument");
+    if (!pool->batch.open) return fail(XNP_E_STATE, "no batch is open");
+    if (pool->host_only) return fail(XNP_E_STATE, "a host-only pool runs no kernels");
+    if (layer < 0 || layer >= pool->d.num_layers) return fail(XNP_E_INVALID, "layer %d of %d", layer, pool->d.num_layers);
+    if ((hipStream_t)hip_stream != pool->batch.stream)
+        return fail(XNP_E_INVALID, "a batch's calls go to the stream it began on");
+    if (decode && pool->batch.t != 1) return fail(XNP_E_INVALID, "decode takes one row per stream, not %d", pool->batch.t);
+    if (!decode && pool->batch.t == 1) return fail(XNP_E_INVALID, "prefill takes more than one row per stream");
+    HIP_TRY(hipSetDevice(pool->d.device), "hipSetDevice");
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_append(xnp_pool *pool, int32_t layer, const void *k, const void *v, void *hip_stream) {
+    if (!pool) return fail(XNP_E_INVALID, "null argument");
+    if (xnp_status st = batch_call(pool, layer, hip_stream, pool->batch.t == 1)) return st;
+    if (pool->batch.n > 0 && (!k || !v)) return fail(XNP_E_INVALID, "null k or v");
+    HIP_TRY(launch_append(pool->view(), pool->batch.bv, layer, k, v, pool->batch.stream), "append");
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_decode(xnp_pool *pool, int32_t layer, const void *q, void *out, float scale,
+                                 void *hip_stream) {
+    if (xnp_status st = batch_call(pool, layer, hip_stream, true)) return st;
+    if (pool->batch.n > 0 && (!q || !out)) return fail(XNP_E_INVALID, "null q or out");
+    HIP_TRY(launch_decode(pool->view(), pool->batch.bv, layer, q, nullptr, nullptr, out, scale, false,
+                          pool->batch.stream),
+            "decode");
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_prefill(xnp_pool *pool, int32_t layer, const void *q, void *out, float scale,
+                                  void *hip_stream) {
+    if (xnp_status st = batch_call(pool, layer, hip_stream, false)) return st;
+    if (pool->batch.n > 0 && (!q || !out)) return fail(XNP_E_INVALID, "null q or out");
+    HIP_TRY(launch_prefill(pool->view(), pool->batch.bv, layer, q, out, scale, pool->batch.stream), "prefill");
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_attend(xnp_pool *pool, int32_t layer, const void *q, const void *k, const void *v,
+                                 void *out, float scale, void *hip_stream) {
+    if (!pool) return fail(XNP_E_INVALID, "null argument");
+    if (pool->batch.open && pool->batch.t > 1) {
+        if (xnp_status st = xnp_append(pool, layer, k, v, hip_stream)) return st;
+        return xnp_prefill(pool, layer, q, out, scale, hip_stream);
+    }
+    if (xnp_status st = batch_call(pool, layer, hip_stream, true)) return st;
+    if (pool->batch.n > 0 && (!q || !k || !v || !out)) return fail(XNP_E_INVALID, "null q, k, v or out");
+    HIP_TRY(launch_decode(pool->view(), pool->batch.bv, layer, q, k, v, out, scale, true, pool->batch.stream),
+            "attend");
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_batch_end(xnp_pool *pool) {
+    if (!pool) return fail(XNP_E_INVALID, "null argument");
+    auto &B = pool->batch;
+    if (!B.open) return fail(XNP_E_STATE, "no batch is open");
+    for (int32_t id : B.ids) {
+        Stream &s = pool->streams[id];
+        if (s.ring != RING_NONE) {
+            // complete_kv's ring branch, transformer.rs:74-79
+            s.valid[s.write] = 1;
+            s.filled = std::max(s.filled, s.write + 1);
+            s.current_end += 1;
+        } else {
+            s.current_end += B.t;
+        }
+    }
+    B.open = false;
+    B.taken.clear();
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_batch_abort(xnp_pool *pool) {
+    if (!pool) return fail(XNP_E_INVALID, "null argument");
+    auto &B = pool->batch;
+    if (!B.open) return fail(XNP_E_STATE, "no batch is open");
+    for (auto it = B.taken.rbegin(); it != B.taken.rend(); ++it) pool->drop_page(it->first, it->second);
+    B.taken.clear();
+    B.open = false;
+    return XNP_OK;
+}

@@ -1,0 +1,86 @@
+// Structures shared by the host library (pool.cpp) and the HIP kernels (kernels.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace xnp {
+
+constexpr int kBlock = 16;   // positions per page
+constexpr int kHeadDim = 64; // the kernels' head dimension
+constexpr int kMaxHeads = 16;
+constexpr int kPartStride = 68; // floats per (work item, head) partial: acc[64], m, l, pad
+
+enum : int32_t { DT_F32 = 0, DT_BF16 = 1, DT_I8 = 2 };
+enum : int32_t { RING_NONE = 0, RING_SHIFT = 1, RING_ABSOLUTE = 2 };
+
+// Where one pool's device memory lives and how it is strided.
+struct PoolView {
+    void *pages;          // [L][2][NB][H][16][D], cache dtype
+    float *scales;        // [L][2][NB][H] (int8 only)
+    int32_t *tables;      // [max_streams][mbps] page ids, -1 where none
+    const float2 *rope;   // [max_pos][D/2] (cos, sin), rounded to the activation dtype
+    int32_t L, H, KVH, D, NB, mbps, max_pos;
+    int32_t cache_dt, act_dt;
+};
+
+// One stream of an open batch.  64 bytes.
+struct StreamPlan {
+    int32_t sid;        // stream id: row of the block tables
+    int32_t pos;        // RoPE position of query row 0 for keys at or past `prefix`
+    int32_t pos_pre;    // RoPE position of query row 0 for keys before `prefix`
+    int32_t prefix;     // 0 unless an absolute ring keeps a prefix
+    int32_t write_slot; // slot of new row 0 (rows go to write_slot + i)
+    int32_t key_pos;    // RoPE position of new key row 0
+    int32_t span;       // decode attends slots [0, span) (t == 1)
+    int32_t mask_off;   // word offset of the seen bitmap in masks[], -1: every slot is seen
+    int32_t app_part;   // part index of the decode work item that appends the new row
+    int32_t part0;      // first part index of this stream's work items
+    int32_t nparts;     // decode work items of this stream
+    int32_t ring;       // 1 on a ring: int8 freshness comes from `fresh`, not from the slot
+    int32_t fresh;      // ring + int8: the write slot's page holds no other live row
+    int32_t out_row;    // row of q/k/v/out (= index in the batch)
+    int32_t pad0, pad1;
+};
+
+// One decode work item: logical blocks [blk0, blk1) of stream plan b.  16 bytes.
+struct WorkItem {
+    int32_t b, blk0, blk1, part;
+};
+
+// Everything a batch's kernels read, in one device buffer.
+struct BatchView {
+    const StreamPlan *plans;
+    const WorkItem *work;
+    const uint32_t *masks;
+    float *parts; // [parts][H][kPartStride]
+    int32_t n, t, nwork;
+};
+
+// A table entry to set before the batch's kernels run.
+struct TablePatch {
+    int32_t sid, blk, page, pad;
+};
+
+// One row to rotate in place on eviction (XNP_RING_SHIFT).
+struct EvictRow {
+    int32_t sid, slot;
+};
+
+// Launchers (kernels.hip).  All asynchronous on `stream`; return the launch status.
+hipError_t launch_patch_tables(const PoolView &pv, const TablePatch *patches, int n,
+                               hipStream_t stream);
+hipError_t launch_append(const PoolView &pv, const BatchView &bv, int layer, const void *k,
+                         const void *v, hipStream_t stream);
+hipError_t launch_decode(const PoolView &pv, const BatchView &bv, int layer, const void *q,
+                         const void *k, const void *v, void *out, float scale, bool fused,
+                         hipStream_t stream);
+hipError_t launch_prefill(const PoolView &pv, const BatchView &bv, int layer, const void *q,
+                          void *out, float scale, hipStream_t stream);
+hipError_t launch_evict_rotate(const PoolView &pv, const EvictRow *rows, int n,
+                               const float *cos_row, const float *sin_row, hipStream_t stream);
+hipError_t launch_copy_page(const PoolView &pv, int src_page, int dst_page, hipStream_t stream);
+hipError_t launch_rows_io(const PoolView &pv, int sid, int layer, int kv, int slot0, int n,
+                          void *rows, float *scales, bool write, hipStream_t stream);
+
+} // namespace xnp

@@ -1,0 +1,285 @@
+"""Python binding of the C ABI in include/xnp_kv.h (libxnp_kv.so, built next to this file).
+
+The method names follow the reference's Rust API for the flow-LM cache, so a caller ported
+from ptts reads the same:
+
+    StreamingMultiheadAttention::init_state   transformer.rs:169-180   KvPool.init_state
+    StreamingTransformerState::with_seq_budget transformer.rs:350-392  KvPool.with_seq_budget
+    StreamingTransformerState::advance        transformer.rs:337-344   KvPool.advance
+    StreamingTransformer::start_ring          transformer.rs:842-852   KvPool.start_ring
+    StreamingTransformer::set_ring_slot       transformer.rs:855-871   KvPool.set_ring_slot
+    StreamingTransformer::evict               transformer.rs:879-929   KvPool.evict
+    complete_kv + sdpa_decode / prefill       transformer.rs:61-92,183-251  KvPool.attend
+
+Device buffers are torch tensors (plumbing only: every computation runs in the library's HIP
+kernels).  A refused call raises XnpError carrying the library's status and message.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Iterable, Optional, Sequence
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libxnp_kv.so")
+
+F32, BF16, I8 = 0, 1, 2
+DTYPES = {"f32": F32, "bf16": BF16, "i8": I8}
+RING_SHIFT, RING_ABSOLUTE = 1, 2
+RING_MODES = {"shift": RING_SHIFT, "absolute": RING_ABSOLUTE}
+POOL_HOST_ONLY = 1
+BLOCK = 16
+
+STATUS = {
+    0: "XNP_OK", 1: "XNP_E_INVALID", 2: "XNP_E_STREAM", 3: "XNP_E_NO_ROOM",
+    4: "XNP_E_OUT_OF_BLOCKS", 5: "XNP_E_RING", 6: "XNP_E_EVICT", 7: "XNP_E_BUDGET",
+    8: "XNP_E_HEADS", 9: "XNP_E_STATE", 10: "XNP_E_HIP",
+}
+
+# Every entry point include/xnp_kv.h declares, with its ctypes signature.
+_c = ctypes
+_p = _c.c_void_p
+_i32 = _c.c_int32
+_i32p = _c.POINTER(_c.c_int32)
+
+
+class PoolDesc(_c.Structure):
+    _fields_ = [
+        ("num_layers", _i32), ("num_heads", _i32), ("num_kv_heads", _i32), ("head_dim", _i32),
+        ("num_blocks", _i32), ("max_streams", _i32), ("max_blocks_per_stream", _i32),
+        ("cache_dtype", _i32), ("act_dtype", _i32), ("max_period", _c.c_float),
+        ("max_pos", _i32), ("flags", _i32), ("page_seed", _c.c_uint64), ("device", _i32),
+        ("chunk_blocks", _i32),
+    ]
+
+
+class StreamInfo(_c.Structure):
+    _fields_ = [(n, _i32) for n in (
+        "current_end", "capacity", "ring_mode", "ring_write", "ring_filled", "ring_prefix",
+        "ring_shift", "in_view", "blocks", "shared")]
+
+
+class PoolStats(_c.Structure):
+    _fields_ = [("free_blocks", _i32), ("open_streams", _i32), ("batch_open", _i32),
+                ("work_items", _i32), ("device_bytes", _c.c_int64)]
+
+
+SIGNATURES = {
+    "xnp_pool_create": (_i32, [_c.POINTER(PoolDesc), _c.POINTER(_p)]),
+    "xnp_pool_destroy": (_i32, [_p]),
+    "xnp_pool_stats_get": (_i32, [_p, _c.POINTER(PoolStats)]),
+    "xnp_pool_rope_rows": (_i32, [_p, _i32, _i32, _c.POINTER(_c.c_float)]),
+    "xnp_stream_open": (_i32, [_p, _i32, _i32p]),
+    "xnp_stream_close": (_i32, [_p, _i32]),
+    "xnp_stream_fork": (_i32, [_p, _i32, _i32, _i32p, _p]),
+    "xnp_stream_info_get": (_i32, [_p, _i32, _c.POINTER(StreamInfo)]),
+    "xnp_stream_advance": (_i32, [_p, _i32, _i32]),
+    "xnp_stream_blocks": (_i32, [_p, _i32, _i32p, _i32, _i32p]),
+    "xnp_ring_valid": (_i32, [_p, _i32, _c.POINTER(_c.c_uint8), _i32]),
+    "xnp_write_rows": (_i32, [_p, _i32, _i32, _i32, _i32, _i32, _p, _p, _p]),
+    "xnp_read_rows": (_i32, [_p, _i32, _i32, _i32, _i32, _i32, _p, _p, _p]),
+    "xnp_ring_start": (_i32, [_p, _i32, _i32, _i32, _p]),
+    "xnp_ring_set_slot": (_i32, [_p, _i32, _i32]),
+    "xnp_ring_evict": (_i32, [_p, _i32, _i32, _i32p, _i32, _p]),
+    "xnp_ring_slide": (_i32, [_p, _i32, _i32, _i32, _i32, _i32, _c.c_int64, _p]),
+    "xnp_batch_begin": (_i32, [_p, _i32p, _i32, _i32, _p]),
+    "xnp_append": (_i32, [_p, _i32, _p, _p, _p]),
+    "xnp_decode": (_i32, [_p, _i32, _p, _p, _c.c_float, _p]),
+    "xnp_prefill": (_i32, [_p, _i32, _p, _p, _c.c_float, _p]),
+    "xnp_attend": (_i32, [_p, _i32, _p, _p, _p, _p, _c.c_float, _p]),
+    "xnp_batch_end": (_i32, [_p]),
+    "xnp_batch_abort": (_i32, [_p]),
+    "xnp_frame_budget": (_i32, [_i32, _c.c_double]),
+    "xnp_seq_budget": (_i32, [_i32, _i32]),
+    "xnp_last_error": (_c.c_char_p, []),
+}
+
+_lib = None
+
+
+def load_library(path: str = LIB_PATH):
+    """Load libxnp_kv.so; raise if it is missing (there is no fallback path)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built: run __graft_entry__.build() (make -C xn-ptts_amd/csrc)")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+class XnpError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{STATUS.get(status, status)}: {message}")
+        self.status = status
+        self.name = STATUS.get(status, str(status))
+        self.message = message
+
+
+def _check(status: int):
+    if status != 0:
+        raise XnpError(status, _lib.xnp_last_error().decode())
+
+
+def frame_budget(num_tokens: int, frame_rate: float = 12.5) -> int:
+    return load_library().xnp_frame_budget(num_tokens, frame_rate)
+
+
+def seq_budget(num_tokens: int, frame_budget_: int) -> int:
+    return load_library().xnp_seq_budget(num_tokens, frame_budget_)
+
+
+def _ptr(t) -> Optional[int]:
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def _stream(stream) -> Optional[int]:
+    if stream is not None:
+        return stream
+    import torch
+    if torch.cuda.is_available() and torch.cuda.is_initialized():
+        return torch.cuda.current_stream().cuda_stream
+    return None
+
+
+class KvPool:
+    """A paged K/V store for `num_layers` flow-LM layers, shared by many streams on one GPU."""
+
+    def __init__(self, *, num_layers: int, num_heads: int, num_blocks: int, max_streams: int,
+                 max_blocks_per_stream: int, head_dim: int = 64, num_kv_heads: Optional[int] = None,
+                 cache_dtype: str = "bf16", act_dtype: str = "bf16", max_period: float = 10000.0,
+                 max_pos: int = 4096, page_seed: int = 0, host_only: bool = False, device: int = 0,
+                 chunk_blocks: int = 0):
+        lib = load_library()
+        self.desc = PoolDesc(
+            num_layers=num_layers, num_heads=num_heads,
+            num_kv_heads=num_kv_heads if num_kv_heads is not None else num_heads,
+            head_dim=head_dim, num_blocks=num_blocks, max_streams=max_streams,
+            max_blocks_per_stream=max_blocks_per_stream, cache_dtype=DTYPES[cache_dtype],
+            act_dtype=DTYPES[act_dtype], max_period=max_period, max_pos=max_pos,
+            flags=POOL_HOST_ONLY if host_only else 0, page_seed=page_seed, device=device,
+            chunk_blocks=chunk_blocks)
+        self.cache_dtype, self.act_dtype = cache_dtype, act_dtype
+        self.host_only = host_only
+        h = _p()
+        _check(lib.xnp_pool_create(ctypes.byref(self.desc), ctypes.byref(h)))
+        self._h = h
+        self._lib = lib
+
+    # -- pool ---------------------------------------------------------------------------------
+    def close_pool(self):
+        if self._h:
+            self._lib.xnp_pool_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close_pool()
+        except Exception:
+            pass
+
+    def stats(self) -> dict:
+        s = PoolStats()
+        _check(self._lib.xnp_pool_stats_get(self._h, ctypes.byref(s)))
+        return {n: getattr(s, n) for n, _ in PoolStats._fields_}
+
+    def rope_rows(self, pos0: int, n: int):
+        import numpy as np
+        out = np.zeros((n, self.desc.head_dim // 2, 2), np.float32)
+        _check(self._lib.xnp_pool_rope_rows(self._h, pos0, n, out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
+        return out
+
+    # -- streams (transformer.rs:169-180, 337-392) --------------------------------------------
+    def init_state(self, capacity: int) -> int:
+        sid = _i32()
+        _check(self._lib.xnp_stream_open(self._h, capacity, ctypes.byref(sid)))
+        return sid.value
+
+    def close(self, sid: int):
+        _check(self._lib.xnp_stream_close(self._h, sid))
+
+    def with_seq_budget(self, sid: int, budget: int, stream=None) -> int:
+        out = _i32()
+        _check(self._lib.xnp_stream_fork(self._h, sid, budget, ctypes.byref(out), _stream(stream)))
+        return out.value
+
+    def advance(self, sid: int, n: int):
+        _check(self._lib.xnp_stream_advance(self._h, sid, n))
+
+    def info(self, sid: int) -> dict:
+        s = StreamInfo()
+        _check(self._lib.xnp_stream_info_get(self._h, sid, ctypes.byref(s)))
+        return {n: getattr(s, n) for n, _ in StreamInfo._fields_}
+
+    def current_end(self, sid: int) -> int:
+        return self.info(sid)["current_end"]
+
+    def blocks(self, sid: int) -> list:
+        cnt = _i32()
+        _check(self._lib.xnp_stream_blocks(self._h, sid, None, 0, ctypes.byref(cnt)))
+        arr = (_i32 * max(cnt.value, 1))()
+        _check(self._lib.xnp_stream_blocks(self._h, sid, arr, cnt.value, ctypes.byref(cnt)))
+        return list(arr[:cnt.value])
+
+    def valid(self, sid: int) -> list:
+        cap = self.info(sid)["capacity"]
+        arr = (ctypes.c_uint8 * max(cap, 1))()
+        _check(self._lib.xnp_ring_valid(self._h, sid, arr, cap))
+        return [bool(x) for x in arr[:cap]]
+
+    def write_rows(self, sid: int, layer: int, kv: int, slot0: int, rows, scales=None, stream=None):
+        n = rows.shape[0] if rows is not None else 0
+        _check(self._lib.xnp_write_rows(self._h, sid, layer, kv, slot0, n, _ptr(rows), _ptr(scales),
+                                        _stream(stream)))
+
+    def read_rows(self, sid: int, layer: int, kv: int, slot0: int, rows, scales=None, stream=None):
+        n = rows.shape[0]
+        _check(self._lib.xnp_read_rows(self._h, sid, layer, kv, slot0, n, _ptr(rows), _ptr(scales),
+                                       _stream(stream)))
+
+    # -- ring (transformer.rs:842-929, s2s.rs:318-333) ----------------------------------------
+    def start_ring(self, sid: int, mode: str = "shift", prefix: int = 0, stream=None):
+        _check(self._lib.xnp_ring_start(self._h, sid, RING_MODES[mode], prefix, _stream(stream)))
+
+    def set_ring_slot(self, sid: int, slot: int):
+        _check(self._lib.xnp_ring_set_slot(self._h, sid, slot))
+
+    def evict(self, sid: int, prefix: int, slots: Sequence[int], stream=None):
+        arr = (_i32 * max(len(slots), 1))(*slots)
+        _check(self._lib.xnp_ring_evict(self._h, sid, prefix, arr, len(slots), _stream(stream)))
+
+    def slide(self, sid: int, prefix: int, span: int, window: int, drop: int, step: int, stream=None):
+        _check(self._lib.xnp_ring_slide(self._h, sid, prefix, span, window, drop, step, _stream(stream)))
+
+    # -- a batched step -----------------------------------------------------------------------
+    def begin(self, ids: Iterable[int], t: int = 1, stream=None):
+        ids = list(ids)
+        arr = (_i32 * max(len(ids), 1))(*ids)
+        self._stream_h = _stream(stream)
+        _check(self._lib.xnp_batch_begin(self._h, arr, len(ids), t, self._stream_h))
+
+    def append(self, layer: int, k, v):
+        _check(self._lib.xnp_append(self._h, layer, _ptr(k), _ptr(v), self._stream_h))
+
+    def decode(self, layer: int, q, out, scale: float):
+        _check(self._lib.xnp_decode(self._h, layer, _ptr(q), _ptr(out), scale, self._stream_h))
+
+    def prefill(self, layer: int, q, out, scale: float):
+        _check(self._lib.xnp_prefill(self._h, layer, _ptr(q), _ptr(out), scale, self._stream_h))
+
+    def attend(self, layer: int, q, k, v, out, scale: float):
+        _check(self._lib.xnp_attend(self._h, layer, _ptr(q), _ptr(k), _ptr(v), _ptr(out), scale,
+                                    self._stream_h))
+
+    def end(self):
+        _check(self._lib.xnp_batch_end(self._h))
+
+    def abort(self):
+        _check(self._lib.xnp_batch_abort(self._h))
