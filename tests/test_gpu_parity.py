@@ -275,3 +275,27 @@ def test_rows_written_raw_read_back_the_same(cache):
     assert torch.equal(back, rows)
     if cache == "i8":
         assert torch.equal(sback, scales)
+
+
+@pytest.mark.parametrize("chunk", [0, 2])
+def test_many_split_streams_at_the_config2_length_distribution(chunk):
+    # 256 streams with cache lengths U[1, 1024] on shuffled pages: hundreds of split streams whose
+    # last work item merges the others' partials.  Every stream is checked against the oracle.
+    S, L = 256, 1
+    rng = np.random.default_rng(20261202)
+    lens = rng.integers(1, 1025, S)
+    p = Pair(cache="bf16", act="bf16", streams=S, cap=1040, seed=11, L=L, chunk=chunk, page_seed=99)
+    for i, n in enumerate(lens):
+        n = int(n)
+        kk, vv = p.x(n, 8, 64), p.x(n, 8, 64)
+        p.pool.advance(p.ids[i], n)
+        # the oracle stores the pre-rotated rows raw too: load the same rows on both sides
+        p.pool.write_rows(p.ids[i], 0, 0, 0, dev(kk, "bf16"))
+        p.pool.write_rows(p.ids[i], 0, 1, 0, dev(vv, "bf16"))
+        p.orc[i].write_rows(0, 0, 0, vals=kk)
+        p.orc[i].write_rows(0, 1, 0, vals=vv)
+        p.orc[i].advance(n)
+    for _ in range(2):
+        assert p.step() <= 2e-2
+    for i in range(0, S, 37):
+        p.assert_cache_equal(i)

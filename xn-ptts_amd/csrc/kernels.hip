@@ -219,6 +219,48 @@ __device__ __forceinline__ void rotated_q(const PoolView &pv, const void *qrow, 
     }
 }
 
+// Final output of one head: lanes c = 0 .. LPR-1 of the first row group each store DPL dims.
+template <int DPL, bool ABF>
+__device__ __forceinline__ void store_out(const PoolView &pv, void *out, int row, int h, int c, const float (&acc)[DPL],
+                                          float inv) {
+    if constexpr (ABF) {
+        uint32_t w[DPL / 2];
+#pragma unroll
+        for (int i = 0; i < DPL / 2; ++i) w[i] = bf16_bits(acc[2 * i] * inv) | (bf16_bits(acc[2 * i + 1] * inv) << 16);
+        uint4 *dst = (uint4 *)((char *)out + (((size_t)row * pv.H + h) * kHeadDim + c * DPL) * 2);
+#pragma unroll
+        for (int i = 0; i < DPL / 8; ++i) dst[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+    } else {
+        float4 *dst = (float4 *)((float *)out + ((size_t)row * pv.H + h) * kHeadDim + c * DPL);
+#pragma unroll
+        for (int i = 0; i < DPL / 4; ++i)
+            dst[i] = make_float4(acc[4 * i] * inv, acc[4 * i + 1] * inv, acc[4 * i + 2] * inv, acc[4 * i + 3] * inv);
+    }
+}
+
+// Merge the partials (m, l, acc) of a split stream for head h: lane d owns dim d.
+template <bool ABF>
+__device__ __forceinline__ void merge_parts(const PoolView &pv, const BatchView &bv, const StreamPlan &P, int h, int d,
+                                            void *out) {
+    const float *base = bv.parts + ((size_t)P.part0 * pv.H + h) * kPartStride;
+    const size_t stride = (size_t)pv.H * kPartStride;
+    float M = -1e30f;
+    for (int j = 0; j < P.nparts; ++j) M = fmaxf(M, base[j * stride + 64]);
+    float L = 0.f, A = 0.f;
+    for (int j = 0; j < P.nparts; ++j) {
+        const float *pj = base + j * stride;
+        const float a = fast_exp2(pj[64] - M);
+        L = __builtin_fmaf(pj[65], a, L);
+        A = __builtin_fmaf(pj[d], a, A);
+    }
+    const float r = A / L;
+    const size_t o = ((size_t)P.out_row * pv.H + h) * kHeadDim + d;
+    if constexpr (ABF)
+        ((uint16_t *)out)[o] = (uint16_t)bf16_bits(r);
+    else
+        ((float *)out)[o] = r;
+}
+
 template <int CDT, bool ABF>
 __global__ __launch_bounds__(1024) void k_decode(PoolView pv, BatchView bv, int layer, const void *q,
                                                  const void *knew, const void *vnew, void *out,
@@ -279,26 +321,8 @@ __global__ __launch_bounds__(1024) void k_decode(PoolView pv, BatchView bv, int 
 #pragma unroll
     for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
 
-    uint4 kc[NP], vc[NP], kn[NP], vn[NP];
-    {
-        const int pg = __builtin_amdgcn_readfirstlane(my_page);
-        const size_t off = (size_t)pg * page_u4 + lane;
-#pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            kc[p] = kbase[off + 64 * p];
-            vc[p] = vbase[off + 64 * p];
-        }
-    }
-    for (int j = 0; j < nb; ++j) {
-        if (j + 1 < nb) {
-            const int pg = __builtin_amdgcn_readlane(my_page, j + 1);
-            const size_t off = (size_t)pg * page_u4 + lane;
-#pragma unroll
-            for (int p = 0; p < NP; ++p) {
-                kn[p] = kbase[off + 64 * p];
-                vn[p] = vbase[off + 64 * p];
-            }
-        }
+    // One block's scores and softmax/accumulator update from its K and V registers.
+    auto process = [&](const uint4 (&kr)[NP], const uint4 (&vr)[NP], int j) {
         const uint32_t seen = __builtin_amdgcn_readlane(my_seen, j);
         const int base = (W.blk0 + j) * kBlock;
         float sk = 1.f, sv = 1.f;
@@ -310,7 +334,7 @@ __global__ __launch_bounds__(1024) void k_decode(PoolView pv, BatchView bv, int 
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
             float x[DPL];
-            unpack<CDT>(kc[p], x);
+            unpack<CDT>(kr[p], x);
             float dw = 0.f;
 #pragma unroll
             for (int i = 0; i < DPL; ++i) dw = __builtin_fmaf(qw[i], x[i], dw);
@@ -339,18 +363,39 @@ __global__ __launch_bounds__(1024) void k_decode(PoolView pv, BatchView bv, int 
             const float e = fast_exp2(s[p] - m_new);
             l += e;
             float x[DPL];
-            unpack<CDT>(vc[p], x);
+            unpack<CDT>(vr[p], x);
             const float ev = (CDT == DT_I8) ? e * sv : e;
 #pragma unroll
             for (int i = 0; i < DPL; ++i) acc[i] = __builtin_fmaf(ev, x[i], acc[i]);
         }
         m = m_new;
+    };
+    auto load = [&](uint4 (&kr)[NP], uint4 (&vr)[NP], int j) {
+        const int pg = __builtin_amdgcn_readlane(my_page, j);
+        const size_t off = (size_t)pg * page_u4 + lane;
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-            kc[p] = kn[p];
-            vc[p] = vn[p];
+            kr[p] = kbase[off + 64 * p];
+            vr[p] = vbase[off + 64 * p];
         }
+    };
+
+    // Two blocks in flight ahead of the one being reduced.  Every load is unconditional inside
+    // the steady-state loop, so each wait only covers the oldest block's loads.
+    uint4 k0[NP], v0[NP], k1[NP], v1[NP], k2[NP], v2[NP];
+    load(k0, v0, 0);
+    if (nb > 1) load(k1, v1, 1);
+    int j = 0;
+    for (; j + 2 < nb; j += 3) {
+        load(k2, v2, j + 2);
+        process(k0, v0, j);
+        if (j + 3 < nb) load(k0, v0, j + 3);
+        process(k1, v1, j + 1);
+        if (j + 4 < nb) load(k1, v1, j + 4);
+        process(k2, v2, j + 2);
     }
+    if (j < nb) process(k0, v0, j);
+    if (j + 1 < nb) process(k1, v1, j + 1);
 
     // Merge the row groups: lanes c, c + LPR, c + 2 LPR, ... hold the same dims.
 #pragma unroll
@@ -366,25 +411,16 @@ __global__ __launch_bounds__(1024) void k_decode(PoolView pv, BatchView bv, int 
         }
         m = mn;
     }
-    if (g != 0) return;
     if (P.nparts == 1) {
-        const float inv = 1.0f / l;
-        if constexpr (ABF) {
-            uint32_t w[DPL / 2];
-#pragma unroll
-            for (int i = 0; i < DPL / 2; ++i)
-                w[i] = bf16_bits(acc[2 * i] * inv) | (bf16_bits(acc[2 * i + 1] * inv) << 16);
-            uint4 *dst = (uint4 *)((char *)out + (((size_t)P.out_row * pv.H + h) * kHeadDim + c * DPL) * 2);
-#pragma unroll
-            for (int i = 0; i < DPL / 8; ++i) dst[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
-        } else {
-            float4 *dst = (float4 *)((float *)out + ((size_t)P.out_row * pv.H + h) * kHeadDim + c * DPL);
-#pragma unroll
-            for (int i = 0; i < DPL / 4; ++i)
-                dst[i] = make_float4(acc[4 * i] * inv, acc[4 * i + 1] * inv, acc[4 * i + 2] * inv, acc[4 * i + 3] * inv);
-        }
-    } else {
-        float *part = bv.parts + ((size_t)W.part * pv.H + h) * kPartStride;
+        if (g == 0) store_out<DPL, ABF>(pv, out, P.out_row, h, c, acc, 1.0f / l);
+        return;
+    }
+    // Split stream: publish this work item's partial, and let the last of the stream's work items
+    // to finish merge them all.  The fences order the partial stores before the count (release)
+    // and the count before the merging loads (acquire), at device scope: the work items of one
+    // stream run on different XCDs, each with its own L2.
+    float *part = bv.parts + ((size_t)W.part * pv.H + h) * kPartStride;
+    if (g == 0) {
         float4 *dst = (float4 *)(part + c * DPL);
 #pragma unroll
         for (int i = 0; i < DPL / 4; ++i) dst[i] = make_float4(acc[4 * i], acc[4 * i + 1], acc[4 * i + 2], acc[4 * i + 3]);
@@ -393,31 +429,18 @@ __global__ __launch_bounds__(1024) void k_decode(PoolView pv, BatchView bv, int 
             part[65] = l;
         }
     }
-}
-
-// Merge the partials of streams split over several work items: one wave per head, lane = dim.
-template <bool ABF>
-__global__ __launch_bounds__(1024) void k_merge(PoolView pv, BatchView bv, void *out) {
-    const StreamPlan P = bv.plans[blockIdx.x];
-    if (P.nparts <= 1) return;
-    const int h = threadIdx.x >> 6, d = threadIdx.x & 63;
-    const float *base = bv.parts + ((size_t)P.part0 * pv.H + h) * kPartStride;
-    const size_t stride = (size_t)pv.H * kPartStride;
-    float M = -1e30f;
-    for (int j = 0; j < P.nparts; ++j) M = fmaxf(M, base[j * stride + 64]);
-    float L = 0.f, A = 0.f;
-    for (int j = 0; j < P.nparts; ++j) {
-        const float *pj = base + j * stride;
-        const float a = fast_exp2(pj[64] - M);
-        L = __builtin_fmaf(pj[65], a, L);
-        A = __builtin_fmaf(pj[d], a, A);
+    __shared__ int s_last;
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int done = atomicAdd(&bv.counters[W.b], 1);
+        s_last = done == P.nparts - 1;
     }
-    const float r = A / L;
-    const size_t o = ((size_t)P.out_row * pv.H + h) * kHeadDim + d;
-    if constexpr (ABF)
-        ((uint16_t *)out)[o] = (uint16_t)bf16_bits(r);
-    else
-        ((float *)out)[o] = r;
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    merge_parts<ABF>(pv, bv, P, h, lane, out);
+    if (threadIdx.x == 0) bv.counters[W.b] = 0; // ready for the next launch
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -450,9 +473,6 @@ static hipError_t decode_impl(const PoolView &pv, const BatchView &bv, int layer
     const float qmul = scale * 1.4426950408889634f;
     hipLaunchKernelGGL((k_decode<CDT, ABF>), dim3(bv.nwork), dim3(64 * pv.H), 0, stream, pv, bv, layer, q, k,
                        v, out, qmul, fused ? 1 : 0);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((k_merge<ABF>), dim3(bv.n), dim3(64 * pv.H), 0, stream, pv, bv, out);
     return hipGetLastError();
 }
 

@@ -114,6 +114,7 @@ struct xnp_pool {
     char *dbatch = nullptr; // batch plan upload
     char *daux = nullptr;   // table patches and eviction rows
     float *parts = nullptr;
+    int32_t *counters = nullptr;
     size_t batch_bytes = 0, aux_bytes = 0;
     Staging stage[kStaging];
     int stage_next = 0;
@@ -265,7 +266,7 @@ static void pool_free(xnp_pool *p) {
             if (s.done) (void)hipEventDestroy(s.done);
             if (s.host) (void)hipHostFree(s.host);
         }
-        void *bufs[] = {p->pages, p->scales, p->tables, p->rope, p->dbatch, p->daux, p->parts};
+        void *bufs[] = {p->pages, p->scales, p->tables, p->rope, p->dbatch, p->daux, p->parts, p->counters};
         for (void *b : bufs)
             if (b) (void)hipFree(b);
     }
@@ -358,6 +359,7 @@ extern "C" xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out)
         {(void **)&p->dbatch, p->batch_bytes, "batch plan"},
         {(void **)&p->daux, p->aux_bytes, "aux upload"},
         {(void **)&p->parts, sizeof(float) * kPartStride * d.num_heads * (size_t)p->max_work, "partials"},
+        {(void **)&p->counters, sizeof(int32_t) * (size_t)d.max_streams, "split counters"},
     };
     for (auto &a : allocs) {
         if (!a.bytes) continue;
@@ -367,6 +369,8 @@ extern "C" xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out)
     }
     e = hipMemset(p->tables, 0xff, sizeof(int32_t) * (size_t)d.max_streams * d.max_blocks_per_stream);
     if (e != hipSuccess) return dev_fail(e, "table init");
+    e = hipMemset(p->counters, 0, sizeof(int32_t) * (size_t)d.max_streams);
+    if (e != hipSuccess) return dev_fail(e, "counter init");
     if (p->scales) {
         e = hipMemset(p->scales, 0, sizeof(float) * d.num_heads * (size_t)d.num_blocks * 2 * d.num_layers);
         if (e != hipSuccess) return dev_fail(e, "scale init");
@@ -870,6 +874,7 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
     B.bv.work = (const WorkItem *)(pool->dbatch + o_work);
     B.bv.masks = (const uint32_t *)(pool->dbatch + o_masks);
     B.bv.parts = pool->parts;
+    B.bv.counters = pool->counters;
     B.bv.n = n;
     B.bv.t = t;
     B.bv.nwork = B.nwork;

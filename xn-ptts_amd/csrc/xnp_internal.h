@@ -53,7 +53,8 @@ struct BatchView {
     const StreamPlan *plans;
     const WorkItem *work;
     const uint32_t *masks;
-    float *parts; // [parts][H][kPartStride]
+    float *parts;      // [parts][H][kPartStride]
+    int32_t *counters; // [max_streams] finished work items per split stream, 0 between launches
     int32_t n, t, nwork;
 };
 
