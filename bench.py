@@ -3,12 +3,13 @@
 Workload (default): 1024 concurrent streams, 9 layers x 8 heads x 64, bf16 K/V in 16-position
 pages handed out from a shuffled free list, cache length per stream drawn uniform in [1, 1024]
 (seed 20261202), one bf16 query and one new K/V row per stream per layer, N(0, 1).  A step is one
-pass over all 9 layers: plan upload, then per layer the fused append + RoPE + decode kernel and the
-split merge.  frames/s = streams / step time; audio-s/s = frames/s * 0.08 (12.5 Hz frames).
+pass over all 9 layers: plan upload, then per layer one fused append + RoPE + decode kernel.  frames/s = streams / step time; audio-s/s = frames/s * 0.08 (12.5 Hz frames).
 
-Roofline: algorithmic bytes per attend call (per stream: 2 (n+1) H D 2 B of K/V read, 1 KB q,
-2 KB new k/v, 1 KB out, 2 KB append write, 4 ceil((n+1)/16) B of block table) over the call's
-average duration, measured with HIP events on the stream the kernels run on, against 8 TB/s.
+Roofline: algorithmic bytes per decode kernel launch (per stream: 2 (n+1) H D 2 B of K/V read,
+1 KB q, 2 KB new k/v, 1 KB out, 2 KB append write, 4 ceil((n+1)/16) B of block table) over the
+kernel's average duration, against 8 TB/s.  The duration comes from HIP events that the launch
+itself records as the kernel starts and ends (hipExtLaunchKernel, via xnp_pool_time_next), on
+the stream the kernel runs on.
 
 CPU baseline: the oracle (the C restatement, OpenMP over streams) on a bounded sample of the same
 workload -- 128 streams, the same length distribution -- timed on this host's cores.
@@ -39,6 +40,33 @@ def _load(name, path):
     sys.modules[name] = mod
     spec.loader.exec_module(mod)
     return mod
+
+
+class HipEvents:
+    """hipEvent_t handles from the HIP runtime torch loaded (same soname, so the same library)."""
+
+    def __init__(self):
+        import ctypes
+        self.ct = ctypes
+        self.hip = ctypes.CDLL("libamdhip64.so.7")
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def create(self):
+        ev = self.ct.c_void_p()
+        if self.hip.hipEventCreate(self.ct.byref(ev)) != 0:
+            raise RuntimeError("hipEventCreate failed")
+        return ev.value
+
+    def elapsed_ms(self, a, b):
+        ms = self.ct.c_float()
+        if self.hip.hipEventElapsedTime(self.ct.byref(ms), a, b) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+    def destroy(self, ev):
+        self.hip.hipEventDestroy(ev)
 
 
 def algorithmic_bytes(lens, H=8, D=64, elem=2):
@@ -92,10 +120,24 @@ def main():
     ap.add_argument("--streams", type=int, default=1024)
     ap.add_argument("--layers", type=int, default=9)
     ap.add_argument("--max-len", type=int, default=1024)
-    ap.add_argument("--chunk", type=int, default=0, help="pages per decode work item (0: library default)")
+    ap.add_argument("--fixed-len", type=int, default=0,
+                    help="every stream at this cached length instead of U[1, max-len] (a balance check)")
+    ap.add_argument("--split", type=int, default=0, help="waves per (stream, head) in decode: 2, 4, 8 (0: default)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="only copy 1 GiB device to device 5 times: the known-size kernel that scales the "
+                         "FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
+    if args.calibrate:
+        import torch
+        src = torch.ones(1 << 29, dtype=torch.bfloat16, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": src.numel() * src.element_size(), "copies": 5}))
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: streams are independent and would shard "
                                    "by stream across GPUs, but no multi-GPU run is part of it",
@@ -110,13 +152,15 @@ def main():
     S, L, H, D = args.streams, args.layers, 8, 64
     rng = np.random.default_rng(SEED + 1)
     lens = rng.integers(1, args.max_len + 1, S)
+    if args.fixed_len:
+        lens = np.full(S, args.fixed_len)
     total_steps = args.warmup + args.steps
     cap = args.max_len + total_steps + 1
     mbps = (cap + 15) // 16
     nblocks = int(sum((n + total_steps + 16) // 16 + 1 for n in lens)) + 16
     pool = xnp.KvPool(num_layers=L, num_heads=H, num_blocks=nblocks, max_streams=S, max_blocks_per_stream=mbps,
                       cache_dtype="bf16", act_dtype="bf16", max_pos=cap + 16, page_seed=SEED + 2,
-                      chunk_blocks=args.chunk)
+                      decode_split=args.split)
     ids = [pool.init_state(cap) for _ in range(S)]
     gen = torch.Generator(device=dev).manual_seed(SEED + 3)
     maxn = int(lens.max())
@@ -138,18 +182,17 @@ def main():
     def step(events=None):
         pool.begin(ids)
         for layer in range(L):
-            if events is not None:
-                events[layer][0].record()
+            if events is not None:  # recorded by the launch itself, around the kernel alone
+                pool.time_next(events[layer][0], events[layer][1])
             pool.attend(layer, q[layer], k[layer], v[layer], out[layer], 0.125)
-            if events is not None:
-                events[layer][1].record()
         pool.end()
 
     for _ in range(args.warmup):
         step()
         cur += 1
     torch.cuda.synchronize()
-    ev = [[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(L)] for _ in range(args.steps)]
+    hip = HipEvents()
+    ev = [[[hip.create() for _ in range(2)] for _ in range(L)] for _ in range(args.steps)]
     bytes_total = 0
     t0 = time.perf_counter()
     for s in range(args.steps):
@@ -159,12 +202,26 @@ def main():
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms_per_step = (t1 - t0) * 1000.0 / args.steps
-    call_ms = np.array([[ev[s][l][0].elapsed_time(ev[s][l][1]) for l in range(L)] for s in range(args.steps)])
+    call_ms = np.array([[hip.elapsed_ms(ev[s][l][0], ev[s][l][1]) for l in range(L)] for s in range(args.steps)])
+    for e in (e for s_ in ev for l_ in s_ for e in l_):
+        hip.destroy(e)
     avg_call_ms = float(call_ms.mean())
     calls = args.steps * L
     bytes_per_call = bytes_total / calls
     achieved = bytes_per_call / (avg_call_ms * 1e-3) / 1e9
     fps = S / (ms_per_step / 1000.0)
+
+    # HBM traffic per launch from the FETCH_SIZE / WRITE_SIZE counter runs of this same command,
+    # scaled by the factors a copy of known size gives (profiles/decode_traffic.json).
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "decode_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            tr = json.load(f)
+        same = tr.get("workload") == {"streams": S, "layers": L, "max_len": args.max_len, "steps": args.steps,
+                                      "warmup": args.warmup, "fixed_len": args.fixed_len, "split": args.split}
+        if same:
+            traffic = int(tr["traffic_bytes_per_launch"])
 
     cpu = None
     if not args.no_cpu:
@@ -197,10 +254,10 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "k_decode<bf16> + k_merge per layer (one attend call)",
-            "avg_call_us": round(avg_call_ms * 1000.0, 2),
-            "bytes_per_call": int(bytes_per_call),
+            "traffic": traffic,
+            "kernel": "k_decode<bf16> (fused append + RoPE + decode), one launch per layer",
+            "avg_kernel_us": round(avg_call_ms * 1000.0, 2),
+            "bytes_per_launch": int(bytes_per_call),
         },
         "cpu_baseline": cpu,
     }

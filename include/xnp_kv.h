@@ -94,7 +94,8 @@ typedef struct xnp_pool_desc {
     uint64_t page_seed;   /* 0: pages are handed out in order; else a Fisher-Yates shuffle of the
                              free list seeded with it (shuffled block tables) */
     int32_t device;       /* HIP device ordinal */
-    int32_t chunk_blocks; /* pages per decode work item (split-K chunk); 0 picks the default */
+    int32_t decode_split; /* waves sharing one (stream, head) in decode: 1, 2, 4 or 8; a stream
+                             holds at most 60 * decode_split pages; 0: the fewest that fit */
 } xnp_pool_desc;
 
 typedef struct xnp_stream_info {
@@ -114,7 +115,7 @@ typedef struct xnp_pool_stats {
     int32_t free_blocks;
     int32_t open_streams;
     int32_t batch_open; /* streams in the open batch, 0 if none */
-    int32_t work_items; /* decode work items of the open batch */
+    int32_t work_items; /* decode work groups of the open batch: one per (stream, head) */
     int64_t device_bytes;
 } xnp_pool_stats;
 
@@ -196,6 +197,11 @@ xnp_status xnp_attend(xnp_pool *pool, int32_t layer, const void *q, const void *
 xnp_status xnp_batch_end(xnp_pool *pool);
 /* Drop the step: give back the pages it took; nothing else changes. */
 xnp_status xnp_batch_abort(xnp_pool *pool);
+
+/* Measurement hook (no counterpart in the reference): the pool's next decode or prefill launch
+ * records HIP events `start` and `stop` (hipEvent_t, created by the caller) as the kernel starts
+ * and ends (hipExtLaunchKernel), so that the kernel alone is timed.  Applies to one launch. */
+xnp_status xnp_pool_time_next(xnp_pool *pool, void *start_event, void *stop_event);
 
 /* ---- budgets (plan.rs:25, 43-54) --------------------------------------------------------- */
 int32_t xnp_frame_budget(int32_t num_tokens, double frame_rate);

@@ -136,15 +136,21 @@ def test_kernel_calls_on_a_host_only_pool_are_refused():
     p.abort()
 
 
-def test_decode_work_is_split_in_even_chunks_per_stream():
-    p = pool(max_blocks_per_stream=64, chunk_blocks=4, num_blocks=256, max_pos=2048)
+def test_decode_runs_one_work_group_per_stream_and_head():
+    p = pool(max_blocks_per_stream=64, num_blocks=256, max_pos=2048)
     ids = [p.init_state(1024) for _ in range(3)]
     for sid, n in zip(ids, [0, 64, 1000]):
         p.advance(sid, n)
     p.begin(ids)
-    # spans 1, 65 and 1001 slots: 1, 5 and 63 pages; chunks of at most 4 pages
-    assert p.stats()["work_items"] == 1 + 2 + 16
+    assert p.stats()["work_items"] == 3 * 4
     p.abort()
+    p.begin(ids[:1], t=5)  # a prompt step decodes nothing
+    assert p.stats()["work_items"] == 0
+    p.abort()
+    with pytest.raises(xnp.XnpError, match="decode_split"):
+        pool(decode_split=3)
+    with pytest.raises(xnp.XnpError, match="pages per stream"):
+        pool(decode_split=2, max_blocks_per_stream=121)
 
 
 # ---- with_seq_budget (transformer.rs:350-392) ------------------------------------------------

@@ -32,14 +32,14 @@ class Pair:
     """A GPU pool and one oracle stream per GPU stream, driven in lockstep."""
 
     def __init__(self, *, L=2, H=8, KVH=None, cache="bf16", act="bf16", streams=8, cap=256,
-                 chunk=0, seed=0, page_seed=0):
+                 split=0, seed=0, page_seed=0):
         self.L, self.H, self.KVH = L, H, KVH or H
         self.cache, self.act = cache, act
         self.rng = np.random.default_rng(seed)
         mbps = (cap + 15) // 16
         self.pool = xnp.KvPool(num_layers=L, num_heads=H, num_kv_heads=self.KVH, num_blocks=streams * mbps * 2 + 8,
                                max_streams=streams * 2 + 2, max_blocks_per_stream=mbps, cache_dtype=cache,
-                               act_dtype=act, max_pos=8192, page_seed=page_seed, chunk_blocks=chunk)
+                               act_dtype=act, max_pos=8192, page_seed=page_seed, decode_split=split)
         self.ids, self.orc = [], []
         for _ in range(streams):
             self.add(cap)
@@ -145,8 +145,8 @@ def test_one_row_returns_its_value_exactly():
 
 def test_split_chunks_and_separate_calls_agree():
     outs = []
-    for chunk, fused in [(1, True), (3, True), (64, True), (3, False)]:
-        p = Pair(cache="bf16", act="bf16", streams=4, cap=600, seed=3, chunk=chunk)
+    for split, fused in [(2, True), (4, True), (8, True), (4, False)]:
+        p = Pair(cache="bf16", act="bf16", streams=4, cap=600, seed=3, split=split)
         for i, n in enumerate([1, 37, 300, 590]):
             p.fill(i, n)
         p.pool.begin(p.ids)
@@ -277,14 +277,14 @@ def test_rows_written_raw_read_back_the_same(cache):
         assert torch.equal(sback, scales)
 
 
-@pytest.mark.parametrize("chunk", [0, 2])
-def test_many_split_streams_at_the_config2_length_distribution(chunk):
-    # 256 streams with cache lengths U[1, 1024] on shuffled pages: hundreds of split streams whose
-    # last work item merges the others' partials.  Every stream is checked against the oracle.
+@pytest.mark.parametrize("split", [2, 8])
+def test_many_streams_at_the_config2_length_distribution(split):
+    # 256 streams with cache lengths U[1, 1024] on shuffled pages, each head's pages shared out
+    # over `split` waves that merge in LDS.  Every stream is checked against the oracle.
     S, L = 256, 1
     rng = np.random.default_rng(20261202)
     lens = rng.integers(1, 1025, S)
-    p = Pair(cache="bf16", act="bf16", streams=S, cap=1040, seed=11, L=L, chunk=chunk, page_seed=99)
+    p = Pair(cache="bf16", act="bf16", streams=S, cap=1040, seed=11, L=L, split=split, page_seed=99)
     for i, n in enumerate(lens):
         n = int(n)
         kk, vv = p.x(n, 8, 64), p.x(n, 8, 64)

@@ -7,6 +7,11 @@
 // its own and is checked to a tolerance, not bit for bit.
 #include "xnp_internal.h"
 
+#include <hip/hip_ext.h>
+
+#include <algorithm>
+
+
 namespace xnp {
 
 // ---------------------------------------------------------------------------------------------
@@ -168,7 +173,9 @@ __global__ __launch_bounds__(1024) void k_append(PoolView pv, BatchView bv, int 
 }
 
 // ---------------------------------------------------------------------------------------------
-// decode: one work group per work item (stream, run of pages), one wave per head.
+// decode: one work group per (stream, head).  Its SPLIT waves interleave the stream's pages (wave w
+// takes pages w, w + SPLIT, ...), each keeping an online softmax over the rows it reads, and
+// merge through LDS at the end: no partial ever leaves the CU.
 //
 // Lane layout over a 16 x 64 tile of one head: every lane loads 16 contiguous bytes per pass,
 // DPL dims of one row (DPL = 4 f32, 8 bf16, 16 int8), so a pass is one coalesced 1 KB read per
@@ -181,6 +188,10 @@ template <int CDT> struct Lanes {
     static constexpr int LPR = kHeadDim / DPL;
     static constexpr int RPP = 64 / LPR;
     static constexpr int NP = kBlock / RPP;
+    // blocks in flight per wave: 4 KB (f32), 8 KB (bf16), 4 KB (int8) of K and V
+    static constexpr int DEPTH = CDT == DT_F32 ? 1 : 2;
+    // waves per SIMD the register budget is sized for (512 VGPRs / waves)
+    static constexpr int WAVES = CDT == DT_F32 ? 3 : 4;
 };
 
 template <int CDT>
@@ -219,90 +230,38 @@ __device__ __forceinline__ void rotated_q(const PoolView &pv, const void *qrow, 
     }
 }
 
-// Final output of one head: lanes c = 0 .. LPR-1 of the first row group each store DPL dims.
-template <int DPL, bool ABF>
-__device__ __forceinline__ void store_out(const PoolView &pv, void *out, int row, int h, int c, const float (&acc)[DPL],
-                                          float inv) {
-    if constexpr (ABF) {
-        uint32_t w[DPL / 2];
-#pragma unroll
-        for (int i = 0; i < DPL / 2; ++i) w[i] = bf16_bits(acc[2 * i] * inv) | (bf16_bits(acc[2 * i + 1] * inv) << 16);
-        uint4 *dst = (uint4 *)((char *)out + (((size_t)row * pv.H + h) * kHeadDim + c * DPL) * 2);
-#pragma unroll
-        for (int i = 0; i < DPL / 8; ++i) dst[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
-    } else {
-        float4 *dst = (float4 *)((float *)out + ((size_t)row * pv.H + h) * kHeadDim + c * DPL);
-#pragma unroll
-        for (int i = 0; i < DPL / 4; ++i)
-            dst[i] = make_float4(acc[4 * i] * inv, acc[4 * i + 1] * inv, acc[4 * i + 2] * inv, acc[4 * i + 3] * inv);
-    }
-}
-
-// Merge the partials (m, l, acc) of a split stream for head h: lane d owns dim d.
-template <bool ABF>
-__device__ __forceinline__ void merge_parts(const PoolView &pv, const BatchView &bv, const StreamPlan &P, int h, int d,
-                                            void *out) {
-    const float *base = bv.parts + ((size_t)P.part0 * pv.H + h) * kPartStride;
-    const size_t stride = (size_t)pv.H * kPartStride;
-    float M = -1e30f;
-    for (int j = 0; j < P.nparts; ++j) M = fmaxf(M, base[j * stride + 64]);
-    float L = 0.f, A = 0.f;
-    for (int j = 0; j < P.nparts; ++j) {
-        const float *pj = base + j * stride;
-        const float a = fast_exp2(pj[64] - M);
-        L = __builtin_fmaf(pj[65], a, L);
-        A = __builtin_fmaf(pj[d], a, A);
-    }
-    const float r = A / L;
-    const size_t o = ((size_t)P.out_row * pv.H + h) * kHeadDim + d;
-    if constexpr (ABF)
-        ((uint16_t *)out)[o] = (uint16_t)bf16_bits(r);
-    else
-        ((float *)out)[o] = r;
-}
-
-template <int CDT, bool ABF>
-__global__ __launch_bounds__(1024) void k_decode(PoolView pv, BatchView bv, int layer, const void *q,
-                                                 const void *knew, const void *vnew, void *out,
-                                                 float qmul, int fused) {
+template <int CDT, bool ABF, int SPLIT>
+__global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(Lanes<CDT>::WAVES))) void k_decode(
+    PoolView pv, BatchView bv, int layer, const void *q, const void *knew, const void *vnew, void *out, float qmul,
+    int fused) {
     using LN = Lanes<CDT>;
-    constexpr int DPL = LN::DPL, LPR = LN::LPR, RPP = LN::RPP, NP = LN::NP;
+    constexpr int DPL = LN::DPL, LPR = LN::LPR, RPP = LN::RPP, NP = LN::NP, DEPTH = LN::DEPTH;
     constexpr int AE = ABF ? 2 : 4;
-    const WorkItem W = bv.work[blockIdx.x];
-    const StreamPlan P = bv.plans[W.b];
-    const int h = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int32_t *tab = pv.tables + (size_t)P.sid * pv.mbps;
+    __shared__ float part[SPLIT][kPartStride];
 
-    if (fused && W.part == P.app_part) {
-        const int slot = P.write_slot;
-        const size_t arow = (size_t)P.out_row * pv.KVH + h / (pv.H / pv.KVH);
-        const bool fresh = P.ring ? (P.fresh != 0) : ((slot & 15) == 0);
-        append_row_wave<CDT, ABF>(pv, layer, tab[slot >> 4], slot & 15, h, P.key_pos,
-                                  (const char *)knew + arow * kHeadDim * AE,
-                                  (const char *)vnew + arow * kHeadDim * AE, fresh);
-        __syncthreads();
-    }
+    const int h = blockIdx.x % pv.H;
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // The stream record carries everything the group needs, its page ids included.
+    const char *rec = bv.recs + (size_t)(blockIdx.x / pv.H) * bv.rec_stride;
+    const StreamRec R = *(const StreamRec *)rec;
+    const int32_t *rec_pages = (const int32_t *)(rec + sizeof(StreamRec));
+    const int nb = R.nblk > w ? (R.nblk - w + SPLIT - 1) / SPLIT : 0; // this wave's pages
 
-    const int c = lane % LPR, g = lane / LPR;
-    const char *qrow = (const char *)q + ((size_t)P.out_row * pv.H + h) * kHeadDim * AE;
-    float qw[DPL], qp[DPL];
-    rotated_q<DPL, ABF>(pv, qrow, c, P.pos, qmul, qw);
-    const bool two_q = P.prefix > W.blk0 * kBlock;
-    if (two_q) rotated_q<DPL, ABF>(pv, qrow, c, P.pos_pre, qmul, qp);
-
-    // Per-block metadata, lane j holding block blk0 + j: page, seen rows, int8 scales.
-    const int nb = W.blk1 - W.blk0;
+    // Per-page metadata, lane j holding page w + j * SPLIT: page id, seen rows, int8 scales.
+    // Past the wave's last page the lanes hold page 0 with no row seen.
     int my_page = 0;
     uint32_t my_seen = 0;
     float my_sk = 0.f, my_sv = 0.f;
+    // issued with the header load: record slots past nblk hold stale ids and are masked below
+    const int pg_raw = w + lane * SPLIT < pv.mbps ? rec_pages[w + lane * SPLIT] : -1;
     if (lane < nb) {
-        const int blk = W.blk0 + lane;
+        const int blk = w + lane * SPLIT;
         const int base = blk * kBlock;
         uint32_t seen = 0xffffu;
-        if (P.mask_off >= 0) seen = (bv.masks[P.mask_off + (base >> 5)] >> (base & 16)) & 0xffffu;
-        const int nvalid = P.span - base;
+        if (R.mask_off >= 0) seen = (bv.masks[R.mask_off + (base >> 5)] >> (base & 16)) & 0xffffu;
+        const int nvalid = R.span - base;
         if (nvalid < kBlock) seen &= (1u << max(nvalid, 0)) - 1u;
-        const int pg = tab[blk];
+        const int pg = pg_raw;
         if (pg < 0) seen = 0;
         my_page = pg < 0 ? 0 : pg;
         my_seen = seen;
@@ -311,6 +270,34 @@ __global__ __launch_bounds__(1024) void k_decode(PoolView pv, BatchView bv, int 
             my_sv = pv.scales[tile_index(pv, layer, 1, my_page, h)];
         }
     }
+
+    // complete_kv: the wave that owns the write page appends this head's new row, then reads it
+    // back with the rest of its pages (its own lanes' stores; no other wave touches the page).
+    // A workgroup-scope fence orders the stores before the later loads on the same CU; nothing
+    // waits for the stores to reach memory.
+    const int wblk = R.write_slot >> 4;
+    if (fused && w == wblk % SPLIT) {
+        const int slot = R.write_slot, wj = wblk / SPLIT;
+        const size_t arow = (size_t)R.b * pv.KVH + h / (pv.H / pv.KVH);
+        const bool fresh = (R.flags & 1) ? (R.flags & 2) != 0 : ((slot & 15) == 0);
+        append_row_wave<CDT, ABF>(pv, layer, __builtin_amdgcn_readlane(my_page, wj), slot & 15, h, R.key_pos,
+                                  (const char *)knew + arow * kHeadDim * AE, (const char *)vnew + arow * kHeadDim * AE,
+                                  fresh);
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+        if constexpr (CDT == DT_I8) {
+            if (lane == wj) { // the append may have raised this page's scales
+                my_sk = pv.scales[tile_index(pv, layer, 0, my_page, h)];
+                my_sv = pv.scales[tile_index(pv, layer, 1, my_page, h)];
+            }
+        }
+    }
+
+    const int c = lane % LPR, g = lane / LPR;
+    const char *qrow = (const char *)q + ((size_t)R.b * pv.H + h) * kHeadDim * AE;
+    float qw[DPL], qp[DPL];
+    rotated_q<DPL, ABF>(pv, qrow, c, R.pos, qmul, qw);
+    const bool two_q = R.prefix > 0;
+    if (two_q) rotated_q<DPL, ABF>(pv, qrow, c, R.pos_pre, qmul, qp);
 
     const uint4 *kbase = (const uint4 *)((const char *)pv.pages + tile_index(pv, layer, 0, 0, h) * (kBlock * kHeadDim * esize<CDT>()));
     const uint4 *vbase = (const uint4 *)((const char *)pv.pages + tile_index(pv, layer, 1, 0, h) * (kBlock * kHeadDim * esize<CDT>()));
@@ -321,10 +308,10 @@ __global__ __launch_bounds__(1024) void k_decode(PoolView pv, BatchView bv, int 
 #pragma unroll
     for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
 
-    // One block's scores and softmax/accumulator update from its K and V registers.
+    // One page's scores and softmax/accumulator update from its K and V registers.
     auto process = [&](const uint4 (&kr)[NP], const uint4 (&vr)[NP], int j) {
         const uint32_t seen = __builtin_amdgcn_readlane(my_seen, j);
-        const int base = (W.blk0 + j) * kBlock;
+        const int base = (w + j * SPLIT) * kBlock;
         float sk = 1.f, sv = 1.f;
         if constexpr (CDT == DT_I8) {
             sk = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(my_sk), j));
@@ -339,7 +326,7 @@ __global__ __launch_bounds__(1024) void k_decode(PoolView pv, BatchView bv, int 
 #pragma unroll
             for (int i = 0; i < DPL; ++i) dw = __builtin_fmaf(qw[i], x[i], dw);
             const int r = g + RPP * p;
-            if (two_q && base + r < P.prefix) {
+            if (two_q && base + r < R.prefix) {
                 float dp = 0.f;
 #pragma unroll
                 for (int i = 0; i < DPL; ++i) dp = __builtin_fmaf(qp[i], x[i], dp);
@@ -380,22 +367,20 @@ __global__ __launch_bounds__(1024) void k_decode(PoolView pv, BatchView bv, int 
         }
     };
 
-    // Two blocks in flight ahead of the one being reduced.  Every load is unconditional inside
-    // the steady-state loop, so each wait only covers the oldest block's loads.
-    uint4 k0[NP], v0[NP], k1[NP], v1[NP], k2[NP], v2[NP];
-    load(k0, v0, 0);
-    if (nb > 1) load(k1, v1, 1);
-    int j = 0;
-    for (; j + 2 < nb; j += 3) {
-        load(k2, v2, j + 2);
-        process(k0, v0, j);
-        if (j + 3 < nb) load(k0, v0, j + 3);
-        process(k1, v1, j + 1);
-        if (j + 4 < nb) load(k1, v1, j + 4);
-        process(k2, v2, j + 2);
+    // DEPTH pages in flight ahead of the one being reduced.  The loop body has no branch: past
+    // the wave's last page the lanes' page is page 0, whose tile every wave shares and finds in
+    // L2, and its rows are unseen, so reducing it changes nothing.  Each wait then only covers
+    // the oldest page's loads.
+    uint4 kb[DEPTH + 1][NP], vb[DEPTH + 1][NP];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) load(kb[d], vb[d], d);
+    for (int j = 0; j < nb; j += DEPTH + 1) {
+#pragma unroll
+        for (int u = 0; u <= DEPTH; ++u) {
+            load(kb[(u + DEPTH) % (DEPTH + 1)], vb[(u + DEPTH) % (DEPTH + 1)], j + u + DEPTH);
+            process(kb[u], vb[u], j + u);
+        }
     }
-    if (j < nb) process(k0, v0, j);
-    if (j + 1 < nb) process(k1, v1, j + 1);
 
     // Merge the row groups: lanes c, c + LPR, c + 2 LPR, ... hold the same dims.
 #pragma unroll
@@ -411,36 +396,33 @@ __global__ __launch_bounds__(1024) void k_decode(PoolView pv, BatchView bv, int 
         }
         m = mn;
     }
-    if (P.nparts == 1) {
-        if (g == 0) store_out<DPL, ABF>(pv, out, P.out_row, h, c, acc, 1.0f / l);
-        return;
-    }
-    // Split stream: publish this work item's partial, and let the last of the stream's work items
-    // to finish merge them all.  The fences order the partial stores before the count (release)
-    // and the count before the merging loads (acquire), at device scope: the work items of one
-    // stream run on different XCDs, each with its own L2.
-    float *part = bv.parts + ((size_t)W.part * pv.H + h) * kPartStride;
+    // Merge the waves through LDS; wave 0 writes the head's output, lane d owning dim d.
     if (g == 0) {
-        float4 *dst = (float4 *)(part + c * DPL);
 #pragma unroll
-        for (int i = 0; i < DPL / 4; ++i) dst[i] = make_float4(acc[4 * i], acc[4 * i + 1], acc[4 * i + 2], acc[4 * i + 3]);
+        for (int i = 0; i < DPL; ++i) part[w][c * DPL + i] = acc[i];
         if (lane == 0) {
-            part[64] = m;
-            part[65] = l;
+            part[w][64] = m;
+            part[w][65] = l;
         }
     }
-    __shared__ int s_last;
-    __threadfence();
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const int done = atomicAdd(&bv.counters[W.b], 1);
-        s_last = done == P.nparts - 1;
+    if (w != 0) return;
+    float M = -1e30f;
+#pragma unroll
+    for (int k = 0; k < SPLIT; ++k) M = fmaxf(M, part[k][64]);
+    float L = 0.f, A = 0.f;
+#pragma unroll
+    for (int k = 0; k < SPLIT; ++k) {
+        const float a = fast_exp2(part[k][64] - M);
+        L = __builtin_fmaf(part[k][65], a, L);
+        A = __builtin_fmaf(part[k][lane], a, A);
     }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    merge_parts<ABF>(pv, bv, P, h, lane, out);
-    if (threadIdx.x == 0) bv.counters[W.b] = 0; // ready for the next launch
+    const float r = A / L;
+    const size_t o = ((size_t)R.b * pv.H + h) * kHeadDim + lane;
+    if constexpr (ABF)
+        ((uint16_t *)out)[o] = (uint16_t)bf16_bits(r);
+    else
+        ((float *)out)[o] = r;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -469,21 +451,30 @@ hipError_t launch_append(const PoolView &pv, const BatchView &bv, int layer, con
 
 template <int CDT, bool ABF>
 static hipError_t decode_impl(const PoolView &pv, const BatchView &bv, int layer, const void *q, const void *k,
-                              const void *v, void *out, float scale, bool fused, hipStream_t stream) {
+                              const void *v, void *out, float scale, bool fused, hipStream_t stream,
+                              const LaunchTiming &tm) {
     const float qmul = scale * 1.4426950408889634f;
-    hipLaunchKernelGGL((k_decode<CDT, ABF>), dim3(bv.nwork), dim3(64 * pv.H), 0, stream, pv, bv, layer, q, k,
-                       v, out, qmul, fused ? 1 : 0);
+    const dim3 grid(bv.n * pv.H);
+    const int f = fused ? 1 : 0;
+    switch (bv.split) {
+    case 1: hipExtLaunchKernelGGL((k_decode<CDT, ABF, 1>), grid, dim3(64), 0, stream, tm.start, tm.stop, 0, pv, bv, layer, q, k, v, out, qmul, f); break;
+    case 2: hipExtLaunchKernelGGL((k_decode<CDT, ABF, 2>), grid, dim3(128), 0, stream, tm.start, tm.stop, 0, pv, bv, layer, q, k, v, out, qmul, f); break;
+    case 4: hipExtLaunchKernelGGL((k_decode<CDT, ABF, 4>), grid, dim3(256), 0, stream, tm.start, tm.stop, 0, pv, bv, layer, q, k, v, out, qmul, f); break;
+    case 8: hipExtLaunchKernelGGL((k_decode<CDT, ABF, 8>), grid, dim3(512), 0, stream, tm.start, tm.stop, 0, pv, bv, layer, q, k, v, out, qmul, f); break;
+    default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
 hipError_t launch_decode(const PoolView &pv, const BatchView &bv, int layer, const void *q, const void *k,
-                         const void *v, void *out, float scale, bool fused, hipStream_t stream) {
+                         const void *v, void *out, float scale, bool fused, hipStream_t stream,
+                         const LaunchTiming &tm) {
     if (bv.n == 0) return hipSuccess;
     switch (pv.cache_dt * 2 + pv.act_dt) {
-    case DT_F32 * 2 + DT_F32: return decode_impl<DT_F32, false>(pv, bv, layer, q, k, v, out, scale, fused, stream);
-    case DT_BF16 * 2 + DT_BF16: return decode_impl<DT_BF16, true>(pv, bv, layer, q, k, v, out, scale, fused, stream);
-    case DT_I8 * 2 + DT_BF16: return decode_impl<DT_I8, true>(pv, bv, layer, q, k, v, out, scale, fused, stream);
-    case DT_I8 * 2 + DT_F32: return decode_impl<DT_I8, false>(pv, bv, layer, q, k, v, out, scale, fused, stream);
+    case DT_F32 * 2 + DT_F32: return decode_impl<DT_F32, false>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
+    case DT_BF16 * 2 + DT_BF16: return decode_impl<DT_BF16, true>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
+    case DT_I8 * 2 + DT_BF16: return decode_impl<DT_I8, true>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
+    case DT_I8 * 2 + DT_F32: return decode_impl<DT_I8, false>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
     default: return hipErrorInvalidValue;
     }
 }

@@ -101,10 +101,10 @@ size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 struct xnp_pool {
     xnp_pool_desc d{};
     bool host_only = false;
-    int chunk = 8;
+    int split = 4;
     int esz = 2;
     int mask_words = 0; // per stream
-    int max_work = 0;
+    int rec_stride = 0;
 
     // device
     void *pages = nullptr;
@@ -113,11 +113,10 @@ struct xnp_pool {
     float2 *rope = nullptr;
     char *dbatch = nullptr; // batch plan upload
     char *daux = nullptr;   // table patches and eviction rows
-    float *parts = nullptr;
-    int32_t *counters = nullptr;
     size_t batch_bytes = 0, aux_bytes = 0;
     Staging stage[kStaging];
     int stage_next = 0;
+    LaunchTiming timing; // events the next decode or prefill launch records, then cleared
     int64_t device_bytes = 0;
 
     // host
@@ -130,7 +129,7 @@ struct xnp_pool {
 
     struct Batch {
         bool open = false;
-        int n = 0, t = 0, nwork = 0;
+        int n = 0, t = 0;
         hipStream_t stream = nullptr;
         std::vector<int32_t> ids;
         std::vector<std::pair<int32_t, int32_t>> taken; // (stream, block) pages taken by begin
@@ -266,7 +265,7 @@ static void pool_free(xnp_pool *p) {
             if (s.done) (void)hipEventDestroy(s.done);
             if (s.host) (void)hipHostFree(s.host);
         }
-        void *bufs[] = {p->pages, p->scales, p->tables, p->rope, p->dbatch, p->daux, p->parts, p->counters};
+        void *bufs[] = {p->pages, p->scales, p->tables, p->rope, p->dbatch, p->daux};
         for (void *b : bufs)
             if (b) (void)hipFree(b);
     }
@@ -292,7 +291,15 @@ extern "C" xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out)
         return fail(XNP_E_INVALID, "cache dtype %d with activation dtype %d is not supported", d.cache_dtype,
                     d.act_dtype);
     if (d.max_pos <= 0 || !(d.max_period > 0.0f)) return fail(XNP_E_INVALID, "max_pos and max_period must be positive");
-    if (d.chunk_blocks < 0 || d.chunk_blocks > 64) return fail(XNP_E_INVALID, "chunk_blocks %d not in 0..64", d.chunk_blocks);
+    // default: the fewest waves per (stream, head) whose lanes can index a stream's pages
+    const int split = d.decode_split ? d.decode_split
+                      : d.max_blocks_per_stream <= kLaneBlocks * 2 ? 2
+                      : d.max_blocks_per_stream <= kLaneBlocks * 4 ? 4 : 8;
+    if (split != 1 && split != 2 && split != 4 && split != 8)
+        return fail(XNP_E_INVALID, "decode_split %d is not 1, 2, 4 or 8", d.decode_split);
+    if (d.max_blocks_per_stream > kLaneBlocks * split)
+        return fail(XNP_E_INVALID, "%d pages per stream: decode with %d waves per head reads at most %d",
+                    d.max_blocks_per_stream, split, kLaneBlocks * split);
     if ((int64_t)d.max_streams * d.max_blocks_per_stream > (int64_t)1 << 28)
         return fail(XNP_E_INVALID, "max_streams x max_blocks_per_stream too large");
 
@@ -300,10 +307,9 @@ extern "C" xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out)
     if (!p) return fail(XNP_E_INVALID, "out of host memory");
     p->d = d;
     p->host_only = (d.flags & XNP_POOL_HOST_ONLY) != 0;
-    p->chunk = d.chunk_blocks ? d.chunk_blocks : 8;
+    p->split = split;
     p->esz = d.cache_dtype == XNP_F32 ? 4 : d.cache_dtype == XNP_BF16 ? 2 : 1;
     p->mask_words = (d.max_blocks_per_stream * kBlock + 31) / 32;
-    p->max_work = d.max_streams * ((d.max_blocks_per_stream + p->chunk - 1) / p->chunk);
 
     p->streams.resize(d.max_streams);
     for (int32_t i = d.max_streams - 1; i >= 0; i--) p->free_ids.push_back(i);
@@ -327,7 +333,8 @@ extern "C" xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out)
         rope_row(d.head_dim, d.max_period, (float)pos, d.act_dtype == XNP_BF16, &p->rope_host[(size_t)pos * half]);
 
     // plan upload layout: plans, work items, masks (each 256-byte aligned)
-    p->batch_bytes = align_up(sizeof(StreamPlan) * d.max_streams, 256) + align_up(sizeof(WorkItem) * p->max_work, 256) +
+    p->rec_stride = (int)align_up(sizeof(StreamRec) + sizeof(int32_t) * d.max_blocks_per_stream, 64);
+    p->batch_bytes = align_up(sizeof(StreamPlan) * d.max_streams, 256) + align_up((size_t)p->rec_stride * d.max_streams, 256) +
                      align_up(sizeof(uint32_t) * (size_t)p->mask_words * d.max_streams, 256);
     p->aux_bytes = std::max<size_t>(sizeof(TablePatch) * 65536,
                                     align_up(sizeof(EvictRow) * d.max_blocks_per_stream * kBlock, 256) + 4096);
@@ -358,8 +365,6 @@ extern "C" xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out)
         {(void **)&p->rope, sizeof(float2) * p->rope_host.size(), "rope table"},
         {(void **)&p->dbatch, p->batch_bytes, "batch plan"},
         {(void **)&p->daux, p->aux_bytes, "aux upload"},
-        {(void **)&p->parts, sizeof(float) * kPartStride * d.num_heads * (size_t)p->max_work, "partials"},
-        {(void **)&p->counters, sizeof(int32_t) * (size_t)d.max_streams, "split counters"},
     };
     for (auto &a : allocs) {
         if (!a.bytes) continue;
@@ -369,8 +374,6 @@ extern "C" xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out)
     }
     e = hipMemset(p->tables, 0xff, sizeof(int32_t) * (size_t)d.max_streams * d.max_blocks_per_stream);
     if (e != hipSuccess) return dev_fail(e, "table init");
-    e = hipMemset(p->counters, 0, sizeof(int32_t) * (size_t)d.max_streams);
-    if (e != hipSuccess) return dev_fail(e, "counter init");
     if (p->scales) {
         e = hipMemset(p->scales, 0, sizeof(float) * d.num_heads * (size_t)d.num_blocks * 2 * d.num_layers);
         if (e != hipSuccess) return dev_fail(e, "scale init");
@@ -402,8 +405,16 @@ extern "C" xnp_status xnp_pool_stats_get(const xnp_pool *pool, xnp_pool_stats *o
     out->free_blocks = (int32_t)pool->free_pages.size();
     out->open_streams = (int32_t)(pool->streams.size() - pool->free_ids.size());
     out->batch_open = pool->batch.open ? std::max(pool->batch.n, 1) : 0;
-    out->work_items = pool->batch.open ? pool->batch.nwork : 0;
+    out->work_items = pool->batch.open && pool->batch.t == 1 ? pool->batch.n * pool->d.num_heads : 0;
     out->device_bytes = pool->device_bytes;
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_pool_time_next(xnp_pool *pool, void *start_event, void *stop_event) {
+    if (!pool) return fail(XNP_E_INVALID, "null argument");
+    if (!start_event != !stop_event) return fail(XNP_E_INVALID, "give both events or neither");
+    pool->timing.start = (hipEvent_t)start_event;
+    pool->timing.stop = (hipEvent_t)stop_event;
     return XNP_OK;
 }
 
@@ -791,9 +802,7 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
 
     // the plan, composed in host memory laid out as the device buffer
     std::vector<StreamPlan> plans(n);
-    std::vector<WorkItem> work;
     std::vector<uint32_t> masks;
-    int32_t parts = 0;
     for (int32_t i = 0; i < n; i++) {
         const Stream &s = pool->streams[ids[i]];
         StreamPlan &P = plans[i];
@@ -825,28 +834,12 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
             for (int32_t sl = b0; sl < b1; sl++) other |= (sl != s.write && s.valid[sl]);
             P.fresh = !other;
         }
-        if (t == 1) {
-            const int32_t nblk = (P.span + kBlock - 1) / kBlock;
-            const int32_t np = (nblk + pool->chunk - 1) / pool->chunk;
-            P.part0 = parts;
-            P.nparts = np;
-            const int32_t base = nblk / np, rem = nblk % np;
-            int32_t blk = 0;
-            const int32_t wblk = P.write_slot / kBlock;
-            for (int32_t j = 0; j < np; j++) {
-                const int32_t len = base + (j < rem ? 1 : 0);
-                work.push_back({i, blk, blk + len, parts + j});
-                if (wblk >= blk && wblk < blk + len) P.app_part = parts + j;
-                blk += len;
-            }
-            parts += np;
-        }
     }
-    // longest work items first, so the short ones fill the tail of the launch
-    std::stable_sort(work.begin(), work.end(),
-                     [](const WorkItem &a, const WorkItem &b) { return a.blk1 - a.blk0 > b.blk1 - b.blk0; });
-    B.nwork = (int32_t)work.size();
-
+    // decode order: longest streams first, so the short ones fill the tail of the launch
+    std::vector<int32_t> order(n);
+    for (int32_t i = 0; i < n; i++) order[i] = i;
+    if (t == 1)
+        std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) { return plans[a].span > plans[b].span; });
     if (pool->host_only) {
         B.open = true;
         return XNP_OK;
@@ -863,21 +856,38 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
     Staging *sg;
     if (xnp_status st = pool->stage_acquire(&sg)) return undo(st);
     const size_t o_plans = 0;
-    const size_t o_work = align_up(sizeof(StreamPlan) * n, 256);
-    const size_t o_masks = o_work + align_up(sizeof(WorkItem) * work.size(), 256);
+    const size_t o_recs = align_up(sizeof(StreamPlan) * n, 256);
+    const size_t o_masks = o_recs + align_up(t == 1 ? (size_t)pool->rec_stride * n : 0, 256);
     const size_t total = o_masks + sizeof(uint32_t) * masks.size();
     std::memcpy(sg->host + o_plans, plans.data(), sizeof(StreamPlan) * n);
-    std::memcpy(sg->host + o_work, work.data(), sizeof(WorkItem) * work.size());
+    if (t == 1)
+        for (int32_t r = 0; r < n; r++) {
+            const StreamPlan &P = plans[order[r]];
+            StreamRec R;
+            std::memset(&R, 0, sizeof R);
+            R.b = P.out_row;
+            R.nblk = (P.span + kBlock - 1) / kBlock;
+            R.pos = P.pos;
+            R.pos_pre = P.pos_pre;
+            R.prefix = P.prefix;
+            R.write_slot = P.write_slot;
+            R.key_pos = P.key_pos;
+            R.span = P.span;
+            R.mask_off = P.mask_off;
+            R.flags = (P.ring ? 1 : 0) | (P.fresh ? 2 : 0);
+            char *dst = sg->host + o_recs + (size_t)r * pool->rec_stride;
+            std::memcpy(dst, &R, sizeof R);
+            std::memcpy(dst + sizeof R, pool->streams[P.sid].blocks.data(), sizeof(int32_t) * R.nblk);
+        }
     std::memcpy(sg->host + o_masks, masks.data(), sizeof(uint32_t) * masks.size());
     if (xnp_status st = pool->upload(sg, pool->dbatch, total, hs)) return undo(st);
     B.bv.plans = (const StreamPlan *)(pool->dbatch + o_plans);
-    B.bv.work = (const WorkItem *)(pool->dbatch + o_work);
+    B.bv.recs = pool->dbatch + o_recs;
+    B.bv.rec_stride = pool->rec_stride;
+    B.bv.split = pool->split;
     B.bv.masks = (const uint32_t *)(pool->dbatch + o_masks);
-    B.bv.parts = pool->parts;
-    B.bv.counters = pool->counters;
     B.bv.n = n;
     B.bv.t = t;
-    B.bv.nwork = B.nwork;
     B.open = true;
     return XNP_OK;
 }
@@ -907,8 +917,10 @@ extern "C" xnp_status xnp_decode(xnp_pool *pool, int32_t layer, const void *q, v
                                  void *hip_stream) {
     if (xnp_status st = batch_call(pool, layer, hip_stream, true)) return st;
     if (pool->batch.n > 0 && (!q || !out)) return fail(XNP_E_INVALID, "null q or out");
+    const LaunchTiming tm = pool->timing;
+    pool->timing = LaunchTiming();
     HIP_TRY(launch_decode(pool->view(), pool->batch.bv, layer, q, nullptr, nullptr, out, scale, false,
-                          pool->batch.stream),
+                          pool->batch.stream, tm),
             "decode");
     return XNP_OK;
 }
@@ -930,7 +942,9 @@ extern "C" xnp_status xnp_attend(xnp_pool *pool, int32_t layer, const void *q, c
     }
     if (xnp_status st = batch_call(pool, layer, hip_stream, true)) return st;
     if (pool->batch.n > 0 && (!q || !k || !v || !out)) return fail(XNP_E_INVALID, "null q, k, v or out");
-    HIP_TRY(launch_decode(pool->view(), pool->batch.bv, layer, q, k, v, out, scale, true, pool->batch.stream),
+    const LaunchTiming tm = pool->timing;
+    pool->timing = LaunchTiming();
+    HIP_TRY(launch_decode(pool->view(), pool->batch.bv, layer, q, k, v, out, scale, true, pool->batch.stream, tm),
             "attend");
     return XNP_OK;
 }

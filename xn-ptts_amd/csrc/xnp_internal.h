@@ -9,7 +9,8 @@ namespace xnp {
 constexpr int kBlock = 16;   // positions per page
 constexpr int kHeadDim = 64; // the kernels' head dimension
 constexpr int kMaxHeads = 16;
-constexpr int kPartStride = 68; // floats per (work item, head) partial: acc[64], m, l, pad
+constexpr int kPartStride = 68; // floats per wave partial: acc[64], m, l, pad
+constexpr int kLaneBlocks = 60;  // pages one wave's lanes index: 64 minus the prefetch overrun
 
 enum : int32_t { DT_F32 = 0, DT_BF16 = 1, DT_I8 = 2 };
 enum : int32_t { RING_NONE = 0, RING_SHIFT = 1, RING_ABSOLUTE = 2 };
@@ -34,28 +35,30 @@ struct StreamPlan {
     int32_t key_pos;    // RoPE position of new key row 0
     int32_t span;       // decode attends slots [0, span) (t == 1)
     int32_t mask_off;   // word offset of the seen bitmap in masks[], -1: every slot is seen
-    int32_t app_part;   // part index of the decode work item that appends the new row
-    int32_t part0;      // first part index of this stream's work items
-    int32_t nparts;     // decode work items of this stream
     int32_t ring;       // 1 on a ring: int8 freshness comes from `fresh`, not from the slot
     int32_t fresh;      // ring + int8: the write slot's page holds no other live row
     int32_t out_row;    // row of q/k/v/out (= index in the batch)
-    int32_t pad0, pad1;
+    int32_t pad[5];
 };
 
-// One decode work item: logical blocks [blk0, blk1) of stream plan b.  16 bytes.
-struct WorkItem {
-    int32_t b, blk0, blk1, part;
+// One stream of a decode batch, as its work groups read it: 64 bytes, followed in the record by
+// the page ids of its nblk blocks.
+struct StreamRec {
+    int32_t b;          // batch row: row of q/k/v/out
+    int32_t nblk;       // blocks [0, nblk) the decode reads
+    int32_t pos, pos_pre, prefix; // as StreamPlan
+    int32_t write_slot, key_pos, span, mask_off;
+    int32_t flags;      // 1: ring (int8 freshness from bit 2), 2: the write page starts afresh
+    int32_t pad[6];
 };
 
 // Everything a batch's kernels read, in one device buffer.
 struct BatchView {
     const StreamPlan *plans;
-    const WorkItem *work;
+    const char *recs; // stream records in decode order (longest first), rec_stride bytes apart
     const uint32_t *masks;
-    float *parts;      // [parts][H][kPartStride]
-    int32_t *counters; // [max_streams] finished work items per split stream, 0 between launches
-    int32_t n, t, nwork;
+    int32_t n, t, rec_stride;
+    int32_t split; // waves per (stream, head) work group
 };
 
 // A table entry to set before the batch's kernels run.
@@ -73,9 +76,14 @@ hipError_t launch_patch_tables(const PoolView &pv, const TablePatch *patches, in
                                hipStream_t stream);
 hipError_t launch_append(const PoolView &pv, const BatchView &bv, int layer, const void *k,
                          const void *v, hipStream_t stream);
+// Events a launch records around its kernel (both null: none).
+struct LaunchTiming {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+
 hipError_t launch_decode(const PoolView &pv, const BatchView &bv, int layer, const void *q,
                          const void *k, const void *v, void *out, float scale, bool fused,
-                         hipStream_t stream);
+                         hipStream_t stream, const LaunchTiming &timing);
 hipError_t launch_prefill(const PoolView &pv, const BatchView &bv, int layer, const void *q,
                           void *out, float scale, hipStream_t stream);
 hipError_t launch_evict_rotate(const PoolView &pv, const EvictRow *rows, int n,

@@ -49,7 +49,7 @@ class PoolDesc(_c.Structure):
         ("num_blocks", _i32), ("max_streams", _i32), ("max_blocks_per_stream", _i32),
         ("cache_dtype", _i32), ("act_dtype", _i32), ("max_period", _c.c_float),
         ("max_pos", _i32), ("flags", _i32), ("page_seed", _c.c_uint64), ("device", _i32),
-        ("chunk_blocks", _i32),
+        ("decode_split", _i32),
     ]
 
 
@@ -69,6 +69,7 @@ SIGNATURES = {
     "xnp_pool_destroy": (_i32, [_p]),
     "xnp_pool_stats_get": (_i32, [_p, _c.POINTER(PoolStats)]),
     "xnp_pool_rope_rows": (_i32, [_p, _i32, _i32, _c.POINTER(_c.c_float)]),
+    "xnp_pool_time_next": (_i32, [_p, _p, _p]),
     "xnp_stream_open": (_i32, [_p, _i32, _i32p]),
     "xnp_stream_close": (_i32, [_p, _i32]),
     "xnp_stream_fork": (_i32, [_p, _i32, _i32, _i32p, _p]),
@@ -104,6 +105,13 @@ def load_library(path: str = LIB_PATH):
         return _lib
     if not os.path.exists(path):
         raise RuntimeError(f"{path} is not built: run __graft_entry__.build() (make -C xn-ptts_amd/csrc)")
+    # torch ships its own HIP runtime under the same soname (libamdhip64.so.7).  Loading torch
+    # first makes the library bind to that one; loaded the other way round, the process would
+    # hold two HIP runtimes and torch's would find no device.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(path)
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)
@@ -156,7 +164,7 @@ class KvPool:
                  max_blocks_per_stream: int, head_dim: int = 64, num_kv_heads: Optional[int] = None,
                  cache_dtype: str = "bf16", act_dtype: str = "bf16", max_period: float = 10000.0,
                  max_pos: int = 4096, page_seed: int = 0, host_only: bool = False, device: int = 0,
-                 chunk_blocks: int = 0):
+                 decode_split: int = 0):
         lib = load_library()
         self.desc = PoolDesc(
             num_layers=num_layers, num_heads=num_heads,
@@ -165,7 +173,7 @@ class KvPool:
             max_blocks_per_stream=max_blocks_per_stream, cache_dtype=DTYPES[cache_dtype],
             act_dtype=DTYPES[act_dtype], max_period=max_period, max_pos=max_pos,
             flags=POOL_HOST_ONLY if host_only else 0, page_seed=page_seed, device=device,
-            chunk_blocks=chunk_blocks)
+            decode_split=decode_split)
         self.cache_dtype, self.act_dtype = cache_dtype, act_dtype
         self.host_only = host_only
         h = _p()
@@ -189,6 +197,10 @@ class KvPool:
         s = PoolStats()
         _check(self._lib.xnp_pool_stats_get(self._h, ctypes.byref(s)))
         return {n: getattr(s, n) for n, _ in PoolStats._fields_}
+
+    def time_next(self, start_event: int, stop_event: int):
+        """Have the next decode/prefill launch record these hipEvent_t handles around its kernel."""
+        _check(self._lib.xnp_pool_time_next(self._h, start_event, stop_event))
 
     def rope_rows(self, pos0: int, n: int):
         import numpy as np
