@@ -64,6 +64,28 @@ class Pair:
         self.pool.end()
         self.orc[i].commit(n)
 
+    def prefill(self, t, which=None):
+        """A prompt step: t rows on every stream in `which`, through xnp_attend (append + causal)."""
+        which = list(range(len(self.ids))) if which is None else which
+        n = len(which)
+        self.pool.begin([self.ids[i] for i in which], t=t)
+        worst = 0.0
+        for layer in range(self.L):
+            q, k, v = self.x(n, t, self.H, 64), self.x(n, t, self.KVH, 64), self.x(n, t, self.KVH, 64)
+            out = torch.empty((n, t, self.H, 64), dtype=TORCH_DT[self.act], device=DEV)
+            self.pool.attend(layer, dev(q, self.act), dev(k, self.act), dev(v, self.act), out, 0.125)
+            torch.cuda.synchronize()
+            got = host(out)
+            for j, i in enumerate(which):
+                want, _ = self.orc[i].attend(layer, q[j], k[j], v[j])
+                err = rel_err(got[j], want)
+                worst = max(worst, err)
+                assert err <= TOL[self.cache], (layer, i, err)
+        self.pool.end()
+        for i in which:
+            self.orc[i].commit(t)
+        return worst
+
     def step(self, which=None, fused=True, check=True):
         which = list(range(len(self.ids))) if which is None else which
         n = len(which)
@@ -298,4 +320,30 @@ def test_many_streams_at_the_config2_length_distribution(split):
     for _ in range(2):
         assert p.step() <= 2e-2
     for i in range(0, S, 37):
+        p.assert_cache_equal(i)
+
+
+# ---- prompt prefill (transformer.rs:231-248) ------------------------------------------------------
+@pytest.mark.parametrize("cache,act", [("bf16", "bf16"), ("f32", "f32"), ("i8", "bf16")])
+def test_prefill_matches_the_oracle(cache, act):
+    # prior caches of 0..37 rows, then a 20-row prompt on all of them (crossing pages), then
+    # single steps: outputs within tolerance, every cache row bit-exact.
+    p = Pair(cache=cache, act=act, streams=4, cap=128, seed=21, page_seed=5)
+    for i, n in enumerate([0, 5, 16, 37]):
+        p.fill(i, n)
+    p.prefill(20)
+    for i in range(4):
+        p.assert_cache_equal(i)
+    p.step()
+    p.prefill(3, which=[1, 2])
+    p.step()
+    for i in range(4):
+        p.assert_cache_equal(i)
+
+
+def test_prefill_of_a_grouped_head_prompt_at_config3_shape_sample():
+    # 8 streams x 256-position prompts (the prefill configuration's shape, fewer streams)
+    p = Pair(cache="bf16", act="bf16", streams=8, cap=272, seed=22, L=1, page_seed=6)
+    assert p.prefill(256) <= 2e-2
+    for i in range(0, 8, 3):
         p.assert_cache_equal(i)

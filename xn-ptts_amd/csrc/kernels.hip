@@ -230,21 +230,19 @@ __device__ __forceinline__ void rotated_q(const PoolView &pv, const void *qrow, 
     }
 }
 
+// One query row of one head against pages [0, R.nblk) of its stream, by a group of SPLIT waves:
+// the body of the decode kernel and of the prompt-row kernel.  `pages` lists the stream's page
+// ids by logical block (a decode record's copy, or the block table).
 template <int CDT, bool ABF, int SPLIT>
-__global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(Lanes<CDT>::WAVES))) void k_decode(
-    PoolView pv, BatchView bv, int layer, const void *q, const void *knew, const void *vnew, void *out, float qmul,
-    int fused) {
+__device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView &bv, int layer, const StreamRec &R,
+                                            const int32_t *rec_pages, int h, const void *q, const void *knew,
+                                            const void *vnew, void *out, float qmul, int fused) {
     using LN = Lanes<CDT>;
     constexpr int DPL = LN::DPL, LPR = LN::LPR, RPP = LN::RPP, NP = LN::NP, DEPTH = LN::DEPTH;
     constexpr int AE = ABF ? 2 : 4;
     __shared__ float part[SPLIT][kPartStride];
 
-    const int h = blockIdx.x % pv.H;
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    // The stream record carries everything the group needs, its page ids included.
-    const char *rec = bv.recs + (size_t)(blockIdx.x / pv.H) * bv.rec_stride;
-    const StreamRec R = *(const StreamRec *)rec;
-    const int32_t *rec_pages = (const int32_t *)(rec + sizeof(StreamRec));
     const int nb = R.nblk > w ? (R.nblk - w + SPLIT - 1) / SPLIT : 0; // this wave's pages
 
     // Per-page metadata, lane j holding page w + j * SPLIT: page id, seen rows, int8 scales.
@@ -425,6 +423,43 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(Lane
         ((float *)out)[o] = r;
 }
 
+// Decode: one work group per (stream, head), streams longest first.  The stream record carries
+// everything the group needs, its page ids included.
+template <int CDT, bool ABF, int SPLIT>
+__global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(Lanes<CDT>::WAVES))) void k_decode(
+    PoolView pv, BatchView bv, int layer, const void *q, const void *knew, const void *vnew, void *out, float qmul,
+    int fused) {
+    const char *rec = bv.recs + (size_t)(blockIdx.x / pv.H) * bv.rec_stride;
+    const StreamRec R = *(const StreamRec *)rec;
+    attend_core<CDT, ABF, SPLIT>(pv, bv, layer, R, (const int32_t *)(rec + sizeof(StreamRec)), blockIdx.x % pv.H, q,
+                                 knew, vnew, out, qmul, fused);
+}
+
+// Prompt rows (transformer.rs:231-248), after k_append has written all t rows: row i of a stream
+// attends causally to slots [0, current_end + i], its query rotated at position current_end + i.
+// One work group per (stream, row, head), latest rows (the most keys) first.
+template <int CDT, bool ABF, int SPLIT>
+__global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(Lanes<CDT>::WAVES))) void k_prefill_rows(
+    PoolView pv, BatchView bv, int layer, const void *q, void *out, float qmul) {
+    const int t = bv.t;
+    const int h = blockIdx.x % pv.H, rest = blockIdx.x / pv.H;
+    const int i = t - 1 - rest % t, b = rest / t;
+    const StreamPlan P = bv.plans[b];
+    StreamRec R;
+    R.b = P.out_row * t + i;
+    R.span = P.write_slot + i + 1;
+    R.nblk = (R.span + kBlock - 1) / kBlock;
+    R.pos = P.pos + i;
+    R.pos_pre = P.pos_pre + i;
+    R.prefix = P.prefix;
+    R.write_slot = P.write_slot + i;
+    R.key_pos = P.key_pos + i;
+    R.mask_off = -1;
+    R.flags = 0;
+    attend_core<CDT, ABF, SPLIT>(pv, bv, layer, R, pv.tables + (size_t)P.sid * pv.mbps, h, q, nullptr, nullptr, out, qmul,
+                                 0);
+}
+
 // ---------------------------------------------------------------------------------------------
 // launchers
 
@@ -578,8 +613,31 @@ hipError_t launch_rows_io(const PoolView &pv, int sid, int layer, int kv, int sl
     return hipGetLastError();
 }
 
-hipError_t launch_prefill(const PoolView &, const BatchView &, int, const void *, void *, float, hipStream_t) {
-    return hipErrorNotSupported;
+template <int CDT, bool ABF>
+static hipError_t prefill_rows_impl(const PoolView &pv, const BatchView &bv, int layer, const void *q, void *out,
+                                    float scale, hipStream_t stream, const LaunchTiming &tm) {
+    const float qmul = scale * 1.4426950408889634f;
+    const dim3 grid(bv.n * bv.t * pv.H);
+    switch (bv.split) {
+    case 1: hipExtLaunchKernelGGL((k_prefill_rows<CDT, ABF, 1>), grid, dim3(64), 0, stream, tm.start, tm.stop, 0, pv, bv, layer, q, out, qmul); break;
+    case 2: hipExtLaunchKernelGGL((k_prefill_rows<CDT, ABF, 2>), grid, dim3(128), 0, stream, tm.start, tm.stop, 0, pv, bv, layer, q, out, qmul); break;
+    case 4: hipExtLaunchKernelGGL((k_prefill_rows<CDT, ABF, 4>), grid, dim3(256), 0, stream, tm.start, tm.stop, 0, pv, bv, layer, q, out, qmul); break;
+    case 8: hipExtLaunchKernelGGL((k_prefill_rows<CDT, ABF, 8>), grid, dim3(512), 0, stream, tm.start, tm.stop, 0, pv, bv, layer, q, out, qmul); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill(const PoolView &pv, const BatchView &bv, int layer, const void *q, void *out, float scale,
+                          hipStream_t stream, const LaunchTiming &tm) {
+    if (bv.n == 0) return hipSuccess;
+    switch (pv.cache_dt * 2 + pv.act_dt) {
+    case DT_F32 * 2 + DT_F32: return prefill_rows_impl<DT_F32, false>(pv, bv, layer, q, out, scale, stream, tm);
+    case DT_BF16 * 2 + DT_BF16: return prefill_rows_impl<DT_BF16, true>(pv, bv, layer, q, out, scale, stream, tm);
+    case DT_I8 * 2 + DT_BF16: return prefill_rows_impl<DT_I8, true>(pv, bv, layer, q, out, scale, stream, tm);
+    case DT_I8 * 2 + DT_F32: return prefill_rows_impl<DT_I8, false>(pv, bv, layer, q, out, scale, stream, tm);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 } // namespace xnp

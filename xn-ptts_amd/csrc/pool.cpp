@@ -929,7 +929,9 @@ extern "C" xnp_status xnp_prefill(xnp_pool *pool, int32_t layer, const void *q, 
                                   void *hip_stream) {
     if (xnp_status st = batch_call(pool, layer, hip_stream, false)) return st;
     if (pool->batch.n > 0 && (!q || !out)) return fail(XNP_E_INVALID, "null q or out");
-    HIP_TRY(launch_prefill(pool->view(), pool->batch.bv, layer, q, out, scale, pool->batch.stream), "prefill");
+    const LaunchTiming tm = pool->timing;
+    pool->timing = LaunchTiming();
+    HIP_TRY(launch_prefill(pool->view(), pool->batch.bv, layer, q, out, scale, pool->batch.stream, tm), "prefill");
     return XNP_OK;
 }
 

@@ -71,21 +71,21 @@ struct EvictRow {
     int32_t sid, slot;
 };
 
-// Launchers (kernels.hip).  All asynchronous on `stream`; return the launch status.
-hipError_t launch_patch_tables(const PoolView &pv, const TablePatch *patches, int n,
-                               hipStream_t stream);
-hipError_t launch_append(const PoolView &pv, const BatchView &bv, int layer, const void *k,
-                         const void *v, hipStream_t stream);
 // Events a launch records around its kernel (both null: none).
 struct LaunchTiming {
     hipEvent_t start = nullptr, stop = nullptr;
 };
 
+// Launchers (kernels.hip).  All asynchronous on `stream`; return the launch status.
+hipError_t launch_patch_tables(const PoolView &pv, const TablePatch *patches, int n,
+                               hipStream_t stream);
+hipError_t launch_append(const PoolView &pv, const BatchView &bv, int layer, const void *k,
+                         const void *v, hipStream_t stream);
 hipError_t launch_decode(const PoolView &pv, const BatchView &bv, int layer, const void *q,
                          const void *k, const void *v, void *out, float scale, bool fused,
                          hipStream_t stream, const LaunchTiming &timing);
 hipError_t launch_prefill(const PoolView &pv, const BatchView &bv, int layer, const void *q,
-                          void *out, float scale, hipStream_t stream);
+                          void *out, float scale, hipStream_t stream, const LaunchTiming &timing);
 hipError_t launch_evict_rotate(const PoolView &pv, const EvictRow *rows, int n,
                                const float *cos_row, const float *sin_row, hipStream_t stream);
 hipError_t launch_copy_page(const PoolView &pv, int src_page, int dst_page, hipStream_t stream);
