@@ -1,23 +1,32 @@
-"""Batched paged decode attention + KV append for many Phonon-40m-shaped streams on one MI355X.
+"""Benchmarks of the paged flow-LM KV cache on one MI355X.  Each run prints one JSON line.
 
-Workload (default): 1024 concurrent streams, 9 layers x 8 heads x 64, bf16 K/V in 16-position
-pages handed out from a shuffled free list, cache length per stream drawn uniform in [1, 1024]
-(seed 20261202), one bf16 query and one new K/V row per stream per layer, N(0, 1).  A step is one
-pass over all 9 layers: plan upload, then per layer one fused append + RoPE + decode kernel.  frames/s = streams / step time; audio-s/s = frames/s * 0.08 (12.5 Hz frames).
+--workload decode (default; the headline): batched paged decode attention + KV append.
+  1024 concurrent streams, Phonon-40m layers (9 x 8 heads x 64), bf16 K/V in 16-position pages
+  handed out from a shuffled free list, cache length per stream uniform in [1, 1024] (numpy seed
+  20261202), one bf16 query and one new K/V row per stream per layer, N(0, 1).  A step is one pass
+  over all 9 layers: the plan upload, then per layer one fused append + RoPE + decode kernel.
+  frames/s = streams / step time; audio-s/s = frames/s * 0.08 (12.5 Hz frames).
+  Roofline: algorithmic bytes per decode launch (per stream: 2 (n+1) H D 2 B of K/V read, 1 KB q,
+  2 KB new k/v, 1 KB out, 2 KB append write, 4 ceil((n+1)/16) B of page ids) over the kernel's
+  average duration, against 8 TB/s.  The duration comes from HIP events that the launch itself
+  records as the kernel starts and ends (hipExtLaunchKernel, via xnp_pool_time_next), on the
+  stream the kernel runs on.
 
-Roofline: algorithmic bytes per decode kernel launch (per stream: 2 (n+1) H D 2 B of K/V read,
-1 KB q, 2 KB new k/v, 1 KB out, 2 KB append write, 4 ceil((n+1)/16) B of block table) over the
-kernel's average duration, against 8 TB/s.  The duration comes from HIP events that the launch
-itself records as the kernel starts and ends (hipExtLaunchKernel, via xnp_pool_time_next), on
-the stream the kernel runs on.
+--workload prefill: prompt prefill, 64 streams x 256-position prompts, 9 layers, bf16, RoPE
+  theta 10000, causal, K/V written into the pages.  Value: prompt positions/s.  Roofline: causal
+  flops 2 D T (T+1) H S per layer launch against 2.5 PFLOP/s dense bf16 MFMA.
+
+--workload window: int8 K/V with fp32 scales per (page, head), 1024 streams, a sliding window of
+  512 positions on rings of 528 slots whose write heads start at offsets U[0, 4096), each stream
+  holding U[64, 2048] rows written so far; per step every stream evicts its oldest row once the
+  window is full, appends one and attends over min(n+1, 512) rows.  Value: frames/s.
 
 CPU baseline: the oracle (the C restatement, OpenMP over streams) on a bounded sample of the same
-workload -- 128 streams, the same length distribution -- timed on this host's cores.
+workload, timed on this host's cores.
 """
 import argparse
 import importlib.util
 import json
-import math
 import os
 import sys
 import time
@@ -26,7 +35,9 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBS = 8000.0
+BF16_MFMA_PEAK_TFLOPS = 2500.0
 SEED = 20261201
+H, D = 8, 64
 
 
 def _load(name, path):
@@ -69,34 +80,71 @@ class HipEvents:
         self.hip.hipEventDestroy(ev)
 
 
-def algorithmic_bytes(lens, H=8, D=64, elem=2):
+def bf16_np(a):
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32).view(np.float32).reshape(a.shape)
+
+
+def decode_bytes(lens, elem=2):
     """Bytes one layer's append + decode must move for streams with cached lengths `lens`."""
     lens = np.asarray(lens, np.int64)
     kv = 2 * (lens + 1) * H * D * elem
-    fixed = (H * D * elem) * (1 + 2 + 1 + 2)  # q, new k/v, out, append write
+    fixed = (H * D * 2) * (1 + 2 + 1) + 2 * H * D * elem  # q, new k/v, out (bf16); append write
     table = 4 * ((lens + 1 + 15) // 16)
     return int((kv + fixed + table).sum())
 
 
-def cpu_baseline(L, H, lens_all, seconds=10.0, sample=128):
-    """The oracle on `sample` streams of the workload, all layers per step, until `seconds`."""
+def window_bytes(attended):
+    """int8 window: K/V rows attended, one scale per (page, head) for K and V, bf16 q/out/new rows."""
+    a = np.asarray(attended, np.int64)
+    pages = (a + 15) // 16 + 1
+    return int((2 * a * H * D + 2 * H * 4 * pages + H * D * 2 * (1 + 2 + 1) + 2 * H * D + 4 * pages).sum())
+
+
+def timed_steps(step, steps, warmup, L):
+    """Run warmup then `steps` steps, each recording kernel events; wall ms/step and kernel ms."""
+    import torch
+    for _ in range(warmup):
+        step(None)
+    torch.cuda.synchronize()
+    hip = HipEvents()
+    ev = [[[hip.create() for _ in range(2)] for _ in range(L)] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for s in range(steps):
+        step(ev[s])
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    kern = np.array([[hip.elapsed_ms(ev[s][l][0], ev[s][l][1]) for l in range(L)] for s in range(steps)])
+    for e in (e for s_ in ev for l_ in s_ for e in l_):
+        hip.destroy(e)
+    return (t1 - t0) * 1000.0 / steps, kern
+
+
+def line(metric, value, unit, args, ms, dtype, config, roofline, cpu, higher=True, extra=None):
+    out = {"metric": metric, "value": round(value, 1), "unit": unit, "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": higher, "scaling": "weak",
+           "vs_baseline": None, "dtype": dtype, "data": "synthetic", "config": config}
+    if extra:
+        out.update(extra)
+    out["roofline"] = roofline
+    out["cpu_baseline"] = cpu
+    return out
+
+
+# ---- decode (configuration 2; the headline at 1024 streams) -------------------------------------------
+def cpu_decode(L, lens_all, seconds, sample=128):
     oracle = _load("oracle", os.path.join(ROOT, "oracle", "oracle.py"))
     rng = np.random.default_rng(SEED + 100)
     lens = lens_all[:sample]
     cap = int(lens.max()) + 64
-    streams = [oracle.Stream(L, H, 64, cap, cache="bf16", act="bf16") for _ in lens]
-
-    def bf16(a):
-        u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
-        return ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32).view(np.float32).reshape(a.shape)
-
-    pool_rows = bf16(rng.standard_normal((int(lens.max()), H, 64)))
+    streams = [oracle.Stream(L, H, D, cap, cache="bf16", act="bf16") for _ in lens]
+    rows = bf16_np(rng.standard_normal((int(lens.max()), H, D)))
     for st, n in zip(streams, lens):
         for layer in range(L):
-            st.write_rows(layer, 0, 0, vals=pool_rows[:n])
-            st.write_rows(layer, 1, 0, vals=pool_rows[:n][::-1].copy())
+            st.write_rows(layer, 0, 0, vals=rows[:n])
+            st.write_rows(layer, 1, 0, vals=rows[:n][::-1].copy())
         st.advance(int(n))
-    q, k, v = (bf16(rng.standard_normal((len(lens), H, 64))) for _ in range(3))
+    q, k, v = (bf16_np(rng.standard_normal((len(lens), H, D))) for _ in range(3))
     steps, t0 = 0, time.perf_counter()
     while True:
         for layer in range(L):
@@ -106,50 +154,14 @@ def cpu_baseline(L, H, lens_all, seconds=10.0, sample=128):
         el = time.perf_counter() - t0
         if el >= seconds or steps >= 64:
             break
-    fps = len(lens) * steps / el
-    return {"value": round(fps, 1), "unit": "frames/s", "cores": oracle.threads(), "kind": "port",
+    return {"value": round(len(lens) * steps / el, 1), "unit": "frames/s", "cores": oracle.threads(), "kind": "port",
             "sample": f"{len(lens)} streams x {L} layers x {steps} steps of the same workload "
                       f"(bf16, lengths from the same U[1,1024] draw), {el:.1f} s"}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--streams", type=int, default=1024)
-    ap.add_argument("--layers", type=int, default=9)
-    ap.add_argument("--max-len", type=int, default=1024)
-    ap.add_argument("--fixed-len", type=int, default=0,
-                    help="every stream at this cached length instead of U[1, max-len] (a balance check)")
-    ap.add_argument("--split", type=int, default=0, help="waves per (stream, head) in decode: 2, 4, 8 (0: default)")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--calibrate", action="store_true",
-                    help="only copy 1 GiB device to device 5 times: the known-size kernel that scales the "
-                         "FETCH_SIZE / WRITE_SIZE counters")
-    args = ap.parse_args()
-    if args.calibrate:
-        import torch
-        src = torch.ones(1 << 29, dtype=torch.bfloat16, device="cuda:0")
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"calibrate_copy_bytes": src.numel() * src.element_size(), "copies": 5}))
-        return
-    if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU: streams are independent and would shard "
-                                   "by stream across GPUs, but no multi-GPU run is part of it",
-                          "n_gpus": args.gpus}))
-        sys.exit(2)
-
-    import torch
-
-    xnp = _load("xn_ptts_amd", os.path.join(ROOT, "xn-ptts_amd"))
-    xnp.load_library()
+def run_decode(args, xnp, torch):
     dev = torch.device("cuda:0")
-    S, L, H, D = args.streams, args.layers, 8, 64
+    S, L = args.streams, args.layers
     rng = np.random.default_rng(SEED + 1)
     lens = rng.integers(1, args.max_len + 1, S)
     if args.fixed_len:
@@ -176,41 +188,25 @@ def main():
     v = [torch.randn((S, H, D), generator=gen, device=dev).to(torch.bfloat16) for _ in range(L)]
     out = [torch.empty((S, H, D), dtype=torch.bfloat16, device=dev) for _ in range(L)]
     torch.cuda.synchronize()
-
     cur = lens.copy()
+    bytes_timed = [0]
 
-    def step(events=None):
+    def step(events):
+        if events is not None:
+            bytes_timed[0] += L * decode_bytes(cur)
         pool.begin(ids)
         for layer in range(L):
             if events is not None:  # recorded by the launch itself, around the kernel alone
                 pool.time_next(events[layer][0], events[layer][1])
             pool.attend(layer, q[layer], k[layer], v[layer], out[layer], 0.125)
         pool.end()
+        cur[:] += 1
 
-    for _ in range(args.warmup):
-        step()
-        cur += 1
-    torch.cuda.synchronize()
-    hip = HipEvents()
-    ev = [[[hip.create() for _ in range(2)] for _ in range(L)] for _ in range(args.steps)]
-    bytes_total = 0
-    t0 = time.perf_counter()
-    for s in range(args.steps):
-        bytes_total += L * algorithmic_bytes(cur, H, D)
-        step(ev[s])
-        cur += 1
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms_per_step = (t1 - t0) * 1000.0 / args.steps
-    call_ms = np.array([[hip.elapsed_ms(ev[s][l][0], ev[s][l][1]) for l in range(L)] for s in range(args.steps)])
-    for e in (e for s_ in ev for l_ in s_ for e in l_):
-        hip.destroy(e)
-    avg_call_ms = float(call_ms.mean())
-    calls = args.steps * L
-    bytes_per_call = bytes_total / calls
-    achieved = bytes_per_call / (avg_call_ms * 1e-3) / 1e9
-    fps = S / (ms_per_step / 1000.0)
-
+    ms, kern = timed_steps(step, args.steps, args.warmup, L)
+    avg_ms = float(kern.mean())
+    bytes_per_launch = bytes_timed[0] / (args.steps * L)
+    achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
+    fps = S / (ms / 1000.0)
     # HBM traffic per launch from the FETCH_SIZE / WRITE_SIZE counter runs of this same command,
     # scaled by the factors a copy of known size gives (profiles/decode_traffic.json).
     traffic = None
@@ -218,50 +214,238 @@ def main():
     if os.path.exists(tpath):
         with open(tpath) as f:
             tr = json.load(f)
-        same = tr.get("workload") == {"streams": S, "layers": L, "max_len": args.max_len, "steps": args.steps,
-                                      "warmup": args.warmup, "fixed_len": args.fixed_len, "split": args.split}
-        if same:
+        if tr.get("workload") == {"streams": S, "layers": L, "max_len": args.max_len, "steps": args.steps,
+                                  "warmup": args.warmup, "fixed_len": args.fixed_len, "split": args.split}:
             traffic = int(tr["traffic_bytes_per_launch"])
-
-    cpu = None
-    if not args.no_cpu:
-        cpu = cpu_baseline(L, H, lens, seconds=args.cpu_seconds)
-
-    line = {
-        "metric": "frames/sec (audio-sec/sec) at 1024 streams; decode-attn HBM GB/s % peak",
-        "value": round(fps, 1),
-        "unit": "frames/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic",
-        "config": {
-            "workload": f"batched paged decode attention + KV append: {S} streams, Phonon-40m layers "
-                        f"({L} x {H} heads x {D}), bf16 K/V in 16-position pages, shuffled block tables, "
-                        f"cache length U[1,{args.max_len}] growing one row per step",
-            "streams": S, "layers": L, "heads": H, "head_dim": D, "page": 16,
-            "mean_cached_len": round(float(cur.mean()) - (args.steps + 1) / 2.0, 1),
-        },
-        "audio_sec_per_sec": round(fps * 0.08, 1),
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
+    cpu = None if args.no_cpu else cpu_decode(L, lens, args.cpu_seconds)
+    config = {"workload": f"batched paged decode attention + KV append: {S} streams, Phonon-40m layers "
+                          f"({L} x {H} heads x {D}), bf16 K/V in 16-position pages, shuffled block tables, "
+                          f"cache length U[1,{args.max_len}] growing one row per step",
+              "streams": S, "layers": L, "heads": H, "head_dim": D, "page": 16,
+              "mean_cached_len": round(float(cur.mean()) - (args.steps + 1) / 2.0, 1)}
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
             "kernel": "k_decode<bf16> (fused append + RoPE + decode), one launch per layer",
-            "avg_kernel_us": round(avg_call_ms * 1000.0, 2),
-            "bytes_per_launch": int(bytes_per_call),
-        },
-        "cpu_baseline": cpu,
-    }
-    print(json.dumps(line))
+            "avg_kernel_us": round(avg_ms * 1000.0, 2), "bytes_per_launch": int(bytes_per_launch)}
+    return line("frames/sec (audio-sec/sec) at 1024 streams; decode-attn HBM GB/s % peak", fps, "frames/s", args,
+                ms, "bf16", config, roof, cpu, extra={"audio_sec_per_sec": round(fps * 0.08, 1)})
+
+
+# ---- prompt prefill (configuration 3) ---------------------------------------------------------------
+def cpu_prefill(L, T, seconds, sample=4):
+    oracle = _load("oracle", os.path.join(ROOT, "oracle", "oracle.py"))
+    rng = np.random.default_rng(SEED + 200)
+    q, k, v = (bf16_np(rng.standard_normal((sample, T, H, D))) for _ in range(3))
+    done, t0 = 0, time.perf_counter()
+    while True:
+        for i in range(sample):
+            st = oracle.Stream(L, H, D, T, cache="bf16", act="bf16")
+            for layer in range(L):
+                st.append(layer, k[i], v[i])
+                st.attention(layer, q[i])
+            done += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {"value": round(done * T / el, 1), "unit": "positions/s", "cores": 1, "kind": "port",
+            "sample": f"{done} prompts of {T} positions x {L} layers, one thread (the oracle's prefill is "
+                      f"not threaded), {el:.1f} s"}
+
+
+def run_prefill(args, xnp, torch):
+    dev = torch.device("cuda:0")
+    S, L, T = args.prefill_streams, args.layers, args.prompt
+    mbps = (T + 15) // 16
+    pool = xnp.KvPool(num_layers=L, num_heads=H, num_blocks=S * mbps + 16, max_streams=S, max_blocks_per_stream=mbps,
+                      cache_dtype="bf16", act_dtype="bf16", max_pos=T + 16, page_seed=SEED + 3)
+    gen = torch.Generator(device=dev).manual_seed(SEED + 4)
+    q = [torch.randn((S, T, H, D), generator=gen, device=dev).to(torch.bfloat16) for _ in range(L)]
+    k = [torch.randn((S, T, H, D), generator=gen, device=dev).to(torch.bfloat16) for _ in range(L)]
+    v = [torch.randn((S, T, H, D), generator=gen, device=dev).to(torch.bfloat16) for _ in range(L)]
+    out = [torch.empty((S, T, H, D), dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    torch.cuda.synchronize()
+    ids = [pool.init_state(T) for _ in range(S)]
+
+    def step(events):
+        pool.begin(ids, t=T)
+        for layer in range(L):
+            if events is not None:
+                pool.time_next(events[layer][0], events[layer][1])
+            pool.attend(layer, q[layer], k[layer], v[layer], out[layer], 0.125)
+        pool.end()
+        for i, sid in enumerate(ids):  # a new utterance per stream for the next step
+            pool.close(sid)
+            ids[i] = pool.init_state(T)
+
+    ms, kern = timed_steps(step, args.steps, args.warmup, L)
+    avg_ms = float(kern.mean())
+    flops = 2.0 * D * T * (T + 1) * H * S
+    achieved = flops / (avg_ms * 1e-3) / 1e12
+    hbm = 4 * S * T * H * D * 2  # the prefill kernel: q read, out written, K and V read from the pages
+    cpu = None if args.no_cpu else cpu_prefill(L, T, args.cpu_seconds)
+    config = {"workload": f"prompt prefill: {S} streams x {T}-position prompts, {L} layers x {H} heads x {D}, "
+                          f"bf16, RoPE theta 10000, causal, K/V written into 16-position pages",
+              "streams": S, "prompt": T, "layers": L}
+    roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / BF16_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+            "kernel": "k_prefill_mfma (bf16 v_mfma_f32_16x16x32_bf16), one launch per layer after k_append",
+            "avg_kernel_us": round(avg_ms * 1000.0, 2), "flops_per_launch": flops,
+            "hbm_bytes_per_launch": hbm, "hbm_gbs": round(hbm / (avg_ms * 1e-3) / 1e9, 1)}
+    return line("prompt prefill positions/sec (64 streams x 256); MFMA TFLOP/s % peak", S * T / (ms / 1000.0),
+                "positions/s", args, ms, "bf16", config, roof, cpu)
+
+
+# ---- int8 sliding window (configuration 4) ------------------------------------------------------------
+SPAN, WINDOW = 528, 512
+
+
+def cpu_window(L, lens_all, seconds, sample=64):
+    oracle = _load("oracle", os.path.join(ROOT, "oracle", "oracle.py"))
+    rng = np.random.default_rng(SEED + 300)
+    lens = lens_all[:sample]
+    streams, nxt = [], []
+    for n in lens:
+        st = oracle.Stream(L, H, D, SPAN, cache="i8", act="bf16")
+        q8 = rng.integers(-127, 128, (SPAN, H, D)).astype(np.int8)
+        sc = rng.uniform(0.01, 0.03, (SPAN // 16, H)).astype(np.float32)
+        for layer in range(L):
+            for kv in (0, 1):
+                st.write_rows(layer, kv, 0, q8=q8, scales=sc)
+        a = min(int(n), WINDOW)  # rows in view before the next step
+        w0 = int(rng.integers(0, SPAN))  # slot of the next row
+        valid = np.zeros(SPAN, np.uint8)
+        for j in range(a):
+            valid[(w0 - 1 - j) % SPAN] = 1
+        st.ring_restore("absolute", w0, SPAN, 0, int(n) - a, a, valid)
+        streams.append(st)
+        nxt.append(w0)
+    q, k, v = (bf16_np(rng.standard_normal((len(lens), H, D))) for _ in range(3))
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        for i, st in enumerate(streams):  # the sliding-window policy: s2s.rs:324-333 with drop 1
+            if st.current_end == WINDOW:
+                st.evict(0, [(nxt[i] - WINDOW) % SPAN])
+            st.set_ring_slot(nxt[i])
+            nxt[i] = (nxt[i] + 1) % SPAN
+        for layer in range(L):
+            oracle.batch_attend(streams, layer, q, k, v)
+        oracle.batch_commit(streams)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or steps >= 64:
+            break
+    return {"value": round(len(lens) * steps / el, 1), "unit": "frames/s", "cores": oracle.threads(), "kind": "port",
+            "sample": f"{len(lens)} streams x {L} layers x {steps} steps of the same workload (int8 K/V, window "
+                      f"{WINDOW} on {SPAN}-slot rings), {el:.1f} s"}
+
+
+def run_window(args, xnp, torch):
+    dev = torch.device("cuda:0")
+    S, L = args.streams, args.layers
+    rng = np.random.default_rng(SEED + 4)
+    heads = rng.integers(0, 4096, S)
+    lens = rng.integers(64, 2049, S)
+    mbps = SPAN // 16
+    total = int(lens.max()) + args.warmup + args.steps + 2
+    pool = xnp.KvPool(num_layers=L, num_heads=H, num_blocks=S * mbps + 16, max_streams=S, max_blocks_per_stream=mbps,
+                      cache_dtype="i8", act_dtype="bf16", max_pos=total + 16, page_seed=SEED + 5)
+    ids = [pool.init_state(SPAN) for _ in range(S)]
+    for sid in ids:
+        pool.start_ring(sid, "absolute", prefix=0)
+    gen = torch.Generator(device=dev).manual_seed(SEED + 6)
+    kv_new = [torch.randn((S, H, D), generator=gen, device=dev).to(torch.bfloat16) for _ in range(2 * L)]
+    q = [torch.randn((S, H, D), generator=gen, device=dev).to(torch.bfloat16) for _ in range(L)]
+    out = [torch.empty((S, H, D), dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    torch.cuda.synchronize()
+    # write each stream's history: stream i joins at step N - n_i and appends one row per step
+    N = int(lens.max())
+    start = N - lens
+    written = np.zeros(S, np.int64)
+    for s in range(N):
+        act = np.nonzero(start <= s)[0]
+        if len(act) == 0:
+            continue
+        a_ids = [ids[i] for i in act]
+        pool.slide_batch(a_ids, 0, SPAN, WINDOW, 1, heads[act] + written[act])
+        pool.begin(a_ids)
+        na = len(act)
+        for layer in range(L):
+            pool.append(layer, kv_new[2 * layer][:na], kv_new[2 * layer + 1][:na])
+        pool.end()
+        written[act] += 1
+    torch.cuda.synchronize()
+    bytes_timed = [0]
+
+    def step(events):
+        att = np.minimum(written + 1, WINDOW)
+        if events is not None:
+            bytes_timed[0] += L * window_bytes(att)
+        pool.slide_batch(ids, 0, SPAN, WINDOW, 1, heads + written)
+        pool.begin(ids)
+        for layer in range(L):
+            if events is not None:
+                pool.time_next(events[layer][0], events[layer][1])
+            pool.attend(layer, q[layer], kv_new[2 * layer], kv_new[2 * layer + 1], out[layer], 0.125)
+        pool.end()
+        written[:] += 1
+
+    ms, kern = timed_steps(step, args.steps, args.warmup, L)
+    avg_ms = float(kern.mean())
+    bytes_per_launch = bytes_timed[0] / (args.steps * L)
+    achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
+    fps = S / (ms / 1000.0)
+    cpu = None if args.no_cpu else cpu_window(L, lens, args.cpu_seconds)
+    config = {"workload": f"int8 K/V sliding window: {S} streams, {L} layers x {H} heads x {D}, fp32 scales per "
+                          f"(page, head), window {WINDOW} on {SPAN}-slot rings, write heads U[0,4096), "
+                          f"rows written U[64,2048]; evict + append + dequant-on-gather decode per step",
+              "streams": S, "layers": L, "window": WINDOW, "ring_slots": SPAN}
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "k_decode<int8> (fused append + quantize + RoPE + dequant decode), one launch per layer",
+            "avg_kernel_us": round(avg_ms * 1000.0, 2), "bytes_per_launch": int(bytes_per_launch)}
+    return line("frames/sec, int8 KV sliding window (512) at 1024 streams; decode HBM GB/s % peak", fps,
+                "frames/s", args, ms, "int8", config, roof, cpu, extra={"audio_sec_per_sec": round(fps * 0.08, 1)})
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", choices=["decode", "prefill", "window"], default="decode")
+    ap.add_argument("--streams", type=int, default=1024)
+    ap.add_argument("--layers", type=int, default=9)
+    ap.add_argument("--max-len", type=int, default=1024)
+    ap.add_argument("--fixed-len", type=int, default=0,
+                    help="decode: every stream at this cached length instead of U[1, max-len] (a balance check)")
+    ap.add_argument("--split", type=int, default=0, help="decode: waves per (stream, head): 1, 2, 4, 8 (0: default)")
+    ap.add_argument("--prefill-streams", type=int, default=64)
+    ap.add_argument("--prompt", type=int, default=256)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="only copy 1 GiB device to device 5 times: the known-size kernel that scales the "
+                         "FETCH_SIZE / WRITE_SIZE counters")
+    args = ap.parse_args()
+    if args.calibrate:
+        import torch
+        src = torch.ones(1 << 29, dtype=torch.bfloat16, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": src.numel() * src.element_size(), "copies": 5}))
+        return
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU: streams are independent and would shard "
+                                   "by stream across GPUs, but no multi-GPU run is part of it",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+    xnp = _load("xn_ptts_amd", os.path.join(ROOT, "xn-ptts_amd"))
+    xnp.load_library()
+    run = {"decode": run_decode, "prefill": run_prefill, "window": run_window}[args.workload]
+    print(json.dumps(run(args, xnp, torch)))
 
 
 if __name__ == "__main__":

@@ -172,6 +172,12 @@ xnp_status xnp_ring_evict(xnp_pool *pool, int32_t id, int32_t prefix, const int3
 xnp_status xnp_ring_slide(xnp_pool *pool, int32_t id, int32_t prefix, int32_t span,
                           int32_t window, int32_t drop, int64_t step, void *hip_stream);
 
+/* xnp_ring_slide over n streams, stream i at step steps[i]: one call per batched step.  Stops at
+ * the first stream refused (its index in *failed, -1 if none); the streams before it have slid. */
+xnp_status xnp_ring_slide_batch(xnp_pool *pool, const int32_t *ids, int32_t n, int32_t prefix,
+                                int32_t span, int32_t window, int32_t drop, const int64_t *steps,
+                                int32_t *failed, void *hip_stream);
+
 /* ---- a batched step ---------------------------------------------------------------------- */
 /* Open a step over streams ids[0..n), t new rows each (t > 1: prompt prefill, no ring).  Checks
  * every stream (capacity, ring slot) and takes the pages the new rows need, all or nothing;
@@ -197,6 +203,11 @@ xnp_status xnp_attend(xnp_pool *pool, int32_t layer, const void *q, const void *
 xnp_status xnp_batch_end(xnp_pool *pool);
 /* Drop the step: give back the pages it took; nothing else changes. */
 xnp_status xnp_batch_abort(xnp_pool *pool);
+
+/* Consistency check (no counterpart in the reference): apply the pending block-table changes,
+ * read the device tables back (synchronizes hip_stream) and count the entries of open streams
+ * that differ from the host's page map.  0 is the only right answer. */
+xnp_status xnp_pool_check_tables(xnp_pool *pool, int32_t *mismatches, void *hip_stream);
 
 /* Measurement hook (no counterpart in the reference): the pool's next decode or prefill launch
  * records HIP events `start` and `stop` (hipEvent_t, created by the caller) as the kernel starts

@@ -437,6 +437,20 @@ int orc_start_ring(orc_stream *st, int mode, int prefix) {
     return 0;
 }
 
+int orc_ring_restore(orc_stream *st, int mode, int write, int filled, int prefix, int shift,
+                     int current_end, const uint8_t *valid) {
+    if (mode != ORC_RING_SHIFT && mode != ORC_RING_ABSOLUTE) return fail("bad ring mode %d", mode);
+    if (write < 0 || write >= st->cap || filled < 0 || filled > st->cap) return fail("bad ring fields");
+    st->ring = mode;
+    st->write = write;
+    st->filled = filled;
+    st->prefix = prefix;
+    st->shift = shift;
+    st->current_end = current_end;
+    memcpy(st->valid, valid, st->cap);
+    return 0;
+}
+
 int orc_set_ring_slot(orc_stream *st, int slot) {
     if (st->ring == ORC_RING_NONE) return fail("not a ring cache, see start_ring");
     if (slot < 0 || slot >= st->cap) return fail("slot %d of a %d-slot ring", slot, st->cap);

@@ -79,6 +79,10 @@ int orc_commit(orc_stream *st, int t);
 int orc_advance(orc_stream *st, int n);
 
 int orc_start_ring(orc_stream *st, int mode, int prefix);
+/* Set a ring's fields directly (a snapshot restored): the CPU baseline starts windowed streams
+ * this way instead of replaying every row.  valid[capacity]. */
+int orc_ring_restore(orc_stream *st, int mode, int write, int filled, int prefix, int shift,
+                     int current_end, const uint8_t *valid);
 int orc_set_ring_slot(orc_stream *st, int slot);
 int orc_evict(orc_stream *st, int prefix, const int *slots, int count);
 /* with_seq_budget: a fresh stream of `budget` positions holding a copy of the filled prefix. */

@@ -50,6 +50,7 @@ def lib():
             "orc_advance": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
             "orc_start_ring": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int]),
             "orc_set_ring_slot": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+            "orc_ring_restore": (ctypes.c_int, [ctypes.c_void_p] + [ctypes.c_int] * 6 + [_u8p]),
             "orc_evict": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _ip, ctypes.c_int]),
             "orc_with_seq_budget": (ctypes.c_void_p, [ctypes.c_void_p, ctypes.c_int]),
             "orc_read_rows": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
@@ -176,6 +177,11 @@ class Stream:
 
     def start_ring(self, mode="shift", prefix=0):
         _ok(lib().orc_start_ring(self.h, MODES[mode], prefix))
+
+    def ring_restore(self, mode, write, filled, prefix, shift, current_end, valid):
+        v = np.ascontiguousarray(valid, np.uint8)
+        _ok(lib().orc_ring_restore(self.h, MODES[mode], write, filled, prefix, shift, current_end,
+                                   v.ctypes.data_as(_u8p)))
 
     def set_ring_slot(self, slot):
         _ok(lib().orc_set_ring_slot(self.h, slot))

@@ -275,3 +275,27 @@ def test_sliding_window_keeps_the_last_window_rows():
         assert info["in_view"] == min(n + 1, 512)
         assert info["ring_write"] == (h0 + n) % 528
     assert info["ring_shift"] == 700 - 512 and info["current_end"] == 512
+
+
+def test_table_patches_of_reopened_streams_leave_the_live_pages():
+    # Closing a stream queues -1 for its entries; reopening it and taking pages queues the new
+    # ids for the same entries.  The device applies a flush's patches in no particular order
+    # (the host-only shadow applies them in reverse), so each entry must be flushed once, with
+    # its current value.
+    p = pool(num_blocks=64, max_streams=8, max_blocks_per_stream=8)
+    ids = [p.init_state(128) for _ in range(4)]
+    for _ in range(3):
+        p.begin(ids, t=100)
+        p.end()
+        assert p.check_tables() == 0
+        for i, sid in enumerate(ids):
+            p.close(sid)
+            ids[i] = p.init_state(128)
+    p.begin(ids, t=37)
+    p.abort()
+    p.begin(ids, t=50)
+    p.end()
+    a = p.with_seq_budget(ids[0], 128)
+    p.close(ids[1])
+    p.advance(a, 20)
+    assert p.check_tables() == 0

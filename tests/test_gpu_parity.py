@@ -347,3 +347,18 @@ def test_prefill_of_a_grouped_head_prompt_at_config3_shape_sample():
     assert p.prefill(256) <= 2e-2
     for i in range(0, 8, 3):
         p.assert_cache_equal(i)
+
+
+def test_prompts_on_reopened_streams_use_live_pages():
+    # A new utterance per stream each round (close, reopen, prompt): the device tables must hold
+    # the live pages (a stale -1 would send the append and prefill kernels out of the pool).
+    p = Pair(cache="bf16", act="bf16", streams=4, cap=64, seed=23, L=2, page_seed=8)
+    for _ in range(3):
+        p.prefill(40)
+        assert p.pool.check_tables() == 0
+        for i in range(4):
+            p.assert_cache_equal(i)
+            p.pool.close(p.ids[i])
+            p.ids[i] = p.pool.init_state(64)
+            p.orc[i] = oracle.Stream(p.L, p.H, 64, 64, cache="bf16", act="bf16")
+    assert p.pool.check_tables() == 0

@@ -159,6 +159,7 @@ __global__ __launch_bounds__(1024) void k_append(PoolView pv, BatchView bv, int 
     const int i0 = max(0, blk * kBlock - ws), i1 = min(t, (blk + 1) * kBlock - ws);
     if (i0 >= i1) return;
     const int page = pv.tables[(size_t)P.sid * pv.mbps + blk];
+    if (page < 0 || page >= pv.NB) return; // begin took this page; never index the pool without one
     const int group = pv.H / pv.KVH;
     constexpr int AE = ABF ? 2 : 4;
     for (int i = i0; i < i1; ++i) {
@@ -260,8 +261,9 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
         const int nvalid = R.span - base;
         if (nvalid < kBlock) seen &= (1u << max(nvalid, 0)) - 1u;
         const int pg = pg_raw;
-        if (pg < 0) seen = 0;
-        my_page = pg < 0 ? 0 : pg;
+        const bool ok = pg >= 0 && pg < pv.NB;
+        if (!ok) seen = 0;
+        my_page = ok ? pg : 0;
         my_seen = seen;
         if constexpr (CDT == DT_I8) {
             my_sk = pv.scales[tile_index(pv, layer, 0, my_page, h)];
@@ -523,6 +525,7 @@ __global__ void k_evict_rotate(PoolView pv, const EvictRow *rows, const float2 *
     const int layer = blockIdx.x % pv.L;
     const int h = threadIdx.x >> 5, pr = threadIdx.x & 31;
     const int page = pv.tables[(size_t)R.sid * pv.mbps + (R.slot >> 4)];
+    if (page < 0 || page >= pv.NB) return;
     const size_t e = tile_index(pv, layer, 0, page, h) * (kBlock * kHeadDim) + (R.slot & 15) * kHeadDim + 2 * pr;
     float2 x;
     if constexpr (CDT == DT_F32) {
@@ -582,6 +585,7 @@ __global__ void k_rows_io(PoolView pv, int sid, int layer, int kv, int slot0, vo
     const int s = blockIdx.x;
     const int slot = slot0 + s;
     const int page = pv.tables[(size_t)sid * pv.mbps + (slot >> 4)];
+    if (page < 0 || page >= pv.NB) return;
     const int per_head = row_u4 / pv.H;
     for (int i = threadIdx.x; i < row_u4; i += blockDim.x) {
         const int h = i / per_head, w = i % per_head;
@@ -613,6 +617,174 @@ hipError_t launch_rows_io(const PoolView &pv, int sid, int layer, int kv, int sl
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------------------------
+// prompt prefill on MFMA (bf16 cache and activations), transformer.rs:231-248 batched.
+//
+// One work group per (stream, head, 64-row query tile), later tiles (more keys) first; wave w
+// owns query rows 16w .. 16w+15 of the tile.  Per 32 keys (two pages):
+//   S = Q K^T   v_mfma_f32_16x16x32_bf16, A = the wave's rotated query rows (registers), B = K^T
+//               straight from the page tiles (lane: key lane%16, 8 consecutive dims);
+//   softmax     online, in the C layout (lane: key lane%16, query rows 4(lane/16) .. +3);
+//   O += P V    A = P through LDS ([row][key] -> lane: row lane%16, 8 keys), B = V staged
+//               transposed in LDS ([dim][key]) by the whole group, double-buffered.
+// A and B always hold the same key (or dim) in the same (lane / 16, element) slot, so the
+// contraction is right whatever order the instruction walks k in.
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(const uint4 &u) {
+    bf16x8_t r;
+    __builtin_memcpy(&r, &u, 16);
+    return r;
+}
+
+constexpr int kPfTile = 64; // query rows per work group
+constexpr int kPfPad = 40;  // LDS row length in bf16 (32 keys + 8 of padding against bank conflicts)
+
+__global__ __launch_bounds__(256) void k_prefill_mfma(PoolView pv, BatchView bv, int layer, const void *q, void *out,
+                                                      float qmul) {
+    __shared__ uint16_t vt[2][kHeadDim][kPfPad]; // V of the current 32 keys, [dim][key]
+    __shared__ uint16_t pw[4][16][kPfPad];       // each wave's P, [row][key]
+    const int t = bv.t;
+    const int ntiles = (t + kPfTile - 1) / kPfTile;
+    const int h = blockIdx.x % pv.H, rest = blockIdx.x / pv.H;
+    const int tile = ntiles - 1 - rest % ntiles, b = rest / ntiles;
+    const StreamPlan P = bv.plans[b];
+    const int32_t *tab = pv.tables + (size_t)P.sid * pv.mbps;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+    const int c0 = P.write_slot;         // slot (= position) of prompt row 0
+    const int row0 = tile * kPfTile + w * 16; // this wave's first prompt row
+    const int tile_end = min(t, (tile + 1) * kPfTile);
+    const int kend = c0 + tile_end;      // keys [0, kend) are seen by some row of the tile
+
+    // A operand of S: query row row0 + c16, dims 32 kc + 8 g .. +7, rotated at its position and
+    // rounded to bf16 as the reference's bf16 q is.
+    bf16x8_t qa[2];
+    {
+        const int qrow = row0 + c16;
+        const uint16_t *qr = (const uint16_t *)q + (((size_t)P.out_row * t + min(qrow, t - 1)) * pv.H + h) * kHeadDim;
+        const float2 *cs = pv.rope + (size_t)(P.pos + min(qrow, t - 1)) * (kHeadDim / 2);
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) {
+            const int d0 = 32 * kc + 8 * g;
+            const uint4 raw = *(const uint4 *)(qr + d0);
+            const uint32_t *u = (const uint32_t *)&raw;
+            uint32_t o4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float x0 = bf16_value(u[i] & 0xffffu), x1 = bf16_value(u[i] >> 16);
+                const float2 c = cs[d0 / 2 + i];
+                const float a = x0 * c.x, bb = x1 * c.y, e = x0 * c.y, f = x1 * c.x;
+                o4[i] = qrow < t ? (bf16_bits(a - bb) | (bf16_bits(e + f) << 16)) : 0u;
+            }
+            qa[kc] = as_bf16x8(make_uint4(o4[0], o4[1], o4[2], o4[3]));
+        }
+    }
+
+    const size_t ktile0 = tile_index(pv, layer, 0, 0, h) * (kBlock * kHeadDim); // elements
+    const size_t vtile0 = tile_index(pv, layer, 1, 0, h) * (kBlock * kHeadDim);
+    const size_t page_elems = (size_t)pv.H * kBlock * kHeadDim;
+    const uint16_t *pages = (const uint16_t *)pv.pages;
+
+    float m[4], lsum[4];
+    f32x4_t o[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        m[r] = -1e30f;
+        lsum[r] = 0.f;
+    }
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) o[ni] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    const int nchunks = (kend + 31) / 32;
+    for (int ch = 0; ch < nchunks; ++ch) {
+        const int buf = ch & 1;
+        // stage this chunk's V transposed: thread -> page tid / 128, key (tid / 8) % 16, dims 8 (tid % 8)
+        {
+            const int pb = tid >> 7, key = (tid >> 3) & 15, d0 = 8 * (tid & 7);
+            const int blk = ch * 2 + pb;
+            uint4 vv = make_uint4(0, 0, 0, 0);
+            const int pg = blk * kBlock < kend ? tab[blk] : -1;
+            if (pg >= 0 && pg < pv.NB) vv = *(const uint4 *)(pages + vtile0 + (size_t)pg * page_elems + key * kHeadDim + d0);
+            const uint32_t *u = (const uint32_t *)&vv;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                vt[buf][d0 + 2 * i][pb * 16 + key] = (uint16_t)(u[i] & 0xffffu);
+                vt[buf][d0 + 2 * i + 1][pb * 16 + key] = (uint16_t)(u[i] >> 16);
+            }
+        }
+        // B operands of S for the chunk's two pages: key c16, dims 32 kc + 8 g
+        uint4 kb[2][2];
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb) {
+            const int blk = ch * 2 + pb;
+            const int tpg = blk * kBlock < kend ? tab[blk] : -1;
+            const bool live = tpg >= 0 && tpg < pv.NB;
+            const int pg = live ? tpg : 0;
+            const uint16_t *kr = pages + ktile0 + (size_t)pg * page_elems + c16 * kHeadDim + 8 * g;
+#pragma unroll
+            for (int kc = 0; kc < 2; ++kc) kb[pb][kc] = live ? *(const uint4 *)(kr + 32 * kc) : make_uint4(0, 0, 0, 0);
+        }
+        __syncthreads(); // vt[buf] written; everyone is past the chunk that last read it
+
+        float x[2][4];
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb) {
+            f32x4_t s4 = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            s4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[0], as_bf16x8(kb[pb][0]), s4, 0, 0, 0);
+            s4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[1], as_bf16x8(kb[pb][1]), s4, 0, 0, 0);
+            const int ks = ch * 32 + pb * 16 + c16; // key slot
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int qs = c0 + row0 + 4 * g + r; // query slot
+                x[pb][r] = ks <= qs ? s4[r] * qmul : -INFINITY;
+            }
+        }
+        float alpha[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float mx = fmaxf(x[0][r], x[1][r]);
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+            const float mn = fmaxf(m[r], mx);
+            alpha[r] = fast_exp2(m[r] - mn);
+            m[r] = mn;
+            const float p0 = fast_exp2(x[0][r] - mn), p1 = fast_exp2(x[1][r] - mn);
+            lsum[r] = lsum[r] * alpha[r] + p0 + p1;
+            pw[w][4 * g + r][c16] = (uint16_t)bf16_bits(p0);
+            pw[w][4 * g + r][16 + c16] = (uint16_t)bf16_bits(p1);
+        }
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[ni][r] *= alpha[r];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const bf16x8_t pa = as_bf16x8(*(const uint4 *)&pw[w][c16][8 * g]);
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) {
+            const bf16x8_t vb = as_bf16x8(*(const uint4 *)&vt[buf][16 * ni + c16][8 * g]);
+            o[ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vb, o[ni], 0, 0, 0);
+        }
+    }
+    // row sums over the 16 key lanes, then out[row][h][16 ni + c16]
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        float s = lsum[r];
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) s += __shfl_xor(s, off);
+        const int qrow = row0 + 4 * g + r;
+        if (qrow < t) {
+            uint16_t *orow = (uint16_t *)out + (((size_t)P.out_row * t + qrow) * pv.H + h) * kHeadDim;
+            const float inv = 1.0f / s;
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) orow[16 * ni + c16] = (uint16_t)bf16_bits(o[ni][r] * inv);
+        }
+    }
+}
+
 template <int CDT, bool ABF>
 static hipError_t prefill_rows_impl(const PoolView &pv, const BatchView &bv, int layer, const void *q, void *out,
                                     float scale, hipStream_t stream, const LaunchTiming &tm) {
@@ -633,7 +805,12 @@ hipError_t launch_prefill(const PoolView &pv, const BatchView &bv, int layer, co
     if (bv.n == 0) return hipSuccess;
     switch (pv.cache_dt * 2 + pv.act_dt) {
     case DT_F32 * 2 + DT_F32: return prefill_rows_impl<DT_F32, false>(pv, bv, layer, q, out, scale, stream, tm);
-    case DT_BF16 * 2 + DT_BF16: return prefill_rows_impl<DT_BF16, true>(pv, bv, layer, q, out, scale, stream, tm);
+    case DT_BF16 * 2 + DT_BF16: {
+        const int ntiles = (bv.t + kPfTile - 1) / kPfTile;
+        hipExtLaunchKernelGGL(k_prefill_mfma, dim3(bv.n * ntiles * pv.H), dim3(256), 0, stream, tm.start, tm.stop, 0,
+                              pv, bv, layer, q, out, scale * 1.4426950408889634f);
+        return hipGetLastError();
+    }
     case DT_I8 * 2 + DT_BF16: return prefill_rows_impl<DT_I8, true>(pv, bv, layer, q, out, scale, stream, tm);
     case DT_I8 * 2 + DT_F32: return prefill_rows_impl<DT_I8, false>(pv, bv, layer, q, out, scale, stream, tm);
     default: return hipErrorInvalidValue;

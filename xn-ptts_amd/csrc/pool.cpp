@@ -83,6 +83,7 @@ struct Stream {
     std::vector<int32_t> blocks; // logical block -> page, -1 where none
     int32_t ring = RING_NONE, write = 0, filled = 0, prefix = 0, shift = 0;
     std::vector<uint8_t> valid;
+    int32_t nvalid = 0; // valid slots of the ring
 };
 
 // A pinned host buffer an upload is composed in; reused once its copy has completed.
@@ -126,6 +127,9 @@ struct xnp_pool {
     std::vector<int32_t> free_pages;
     std::vector<int32_t> refcnt;
     std::vector<TablePatch> patches;
+    std::vector<uint32_t> patch_mark; // [max_streams * mbps]: generation an entry was last coalesced in
+    uint32_t patch_gen = 0;
+    std::vector<int32_t> shadow_tables; // host-only pools: what the device tables would hold
 
     struct Batch {
         bool open = false;
@@ -199,9 +203,36 @@ struct xnp_pool {
         return XNP_OK;
     }
 
+    // One patch per touched table entry, carrying the entry's value now.  The patch kernel applies
+    // its list in no particular order, so an entry touched twice since the last flush (a stream
+    // closed and reopened, a page dropped and taken again) must appear once, or a stale -1 could
+    // land after the live page id.
+    void coalesce_patches() {
+        if (++patch_gen == 0) {
+            std::fill(patch_mark.begin(), patch_mark.end(), 0u);
+            patch_gen = 1;
+        }
+        std::vector<TablePatch> out;
+        out.reserve(patches.size());
+        for (auto it = patches.rbegin(); it != patches.rend(); ++it) {
+            const size_t key = (size_t)it->sid * d.max_blocks_per_stream + it->blk;
+            if (patch_mark[key] == patch_gen) continue;
+            patch_mark[key] = patch_gen;
+            const Stream &s = streams[it->sid];
+            const int32_t v = s.open && it->blk < (int32_t)s.blocks.size() ? s.blocks[it->blk] : -1;
+            out.push_back({it->sid, it->blk, v, 0});
+        }
+        patches.swap(out);
+    }
+
     // Apply the queued block-table changes on the device before anything reads the tables.
     xnp_status flush_patches(hipStream_t stream) {
+        coalesce_patches();
         if (host_only) {
+            // the host-only pool keeps a shadow of the device tables, patched in reverse order:
+            // any order the kernel could take gives the same tables only if entries are unique
+            for (auto it = patches.rbegin(); it != patches.rend(); ++it)
+                shadow_tables[(size_t)it->sid * d.max_blocks_per_stream + it->blk] = it->page;
             patches.clear();
             return XNP_OK;
         }
@@ -312,6 +343,8 @@ extern "C" xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out)
     p->mask_words = (d.max_blocks_per_stream * kBlock + 31) / 32;
 
     p->streams.resize(d.max_streams);
+    p->patch_mark.assign((size_t)d.max_streams * d.max_blocks_per_stream, 0u);
+    if (p->host_only) p->shadow_tables.assign((size_t)d.max_streams * d.max_blocks_per_stream, -1);
     for (int32_t i = d.max_streams - 1; i >= 0; i--) p->free_ids.push_back(i);
     p->refcnt.assign(d.num_blocks, 0);
     std::vector<int32_t> order(d.num_blocks);
@@ -415,6 +448,34 @@ extern "C" xnp_status xnp_pool_time_next(xnp_pool *pool, void *start_event, void
     if (!start_event != !stop_event) return fail(XNP_E_INVALID, "give both events or neither");
     pool->timing.start = (hipEvent_t)start_event;
     pool->timing.stop = (hipEvent_t)stop_event;
+    return XNP_OK;
+}
+
+static xnp_status no_batch(const xnp_pool *p);
+
+extern "C" xnp_status xnp_pool_check_tables(xnp_pool *pool, int32_t *mismatches, void *hip_stream) {
+    if (!pool || !mismatches) return fail(XNP_E_INVALID, "null argument");
+    if (xnp_status st = no_batch(pool)) return st;
+    hipStream_t hs = (hipStream_t)hip_stream;
+    if (!pool->host_only) HIP_TRY(hipSetDevice(pool->d.device), "hipSetDevice");
+    if (xnp_status st = pool->flush_patches(hs)) return st;
+    const size_t n = (size_t)pool->d.max_streams * pool->d.max_blocks_per_stream;
+    std::vector<int32_t> dev;
+    const int32_t *tab = pool->shadow_tables.data();
+    if (!pool->host_only) {
+        dev.resize(n);
+        HIP_TRY(hipMemcpyAsync(dev.data(), pool->tables, n * sizeof(int32_t), hipMemcpyDeviceToHost, hs), "table read");
+        HIP_TRY(hipStreamSynchronize(hs), "table read");
+        tab = dev.data();
+    }
+    int32_t bad = 0;
+    for (size_t sid = 0; sid < pool->streams.size(); sid++) {
+        const Stream &s = pool->streams[sid];
+        if (!s.open) continue;
+        for (size_t b = 0; b < s.blocks.size(); b++)
+            bad += tab[sid * pool->d.max_blocks_per_stream + b] != s.blocks[b];
+    }
+    *mismatches = bad;
     return XNP_OK;
 }
 
@@ -655,6 +716,7 @@ extern "C" xnp_status xnp_ring_start(xnp_pool *pool, int32_t id, int32_t mode, i
     const int32_t used = s->current_end;
     s->valid.assign(s->capacity, 0);
     for (int32_t i = 0; i < used; i++) s->valid[i] = 1;
+    s->nvalid = used;
     s->ring = mode;
     s->write = used;
     s->filled = used;
@@ -720,7 +782,11 @@ extern "C" xnp_status xnp_ring_evict(xnp_pool *pool, int32_t id, int32_t prefix,
                     "evict rotate");
         }
     }
-    for (int32_t j = 0; j < count; j++) s->valid[slots[j]] = 0;
+    for (int32_t j = 0; j < count; j++)
+        if (s->valid[slots[j]]) {
+            s->valid[slots[j]] = 0;
+            s->nvalid--;
+        }
     if (s->ring == RING_ABSOLUTE) s->shift += count;
     s->current_end -= count;
     return XNP_OK;
@@ -737,8 +803,10 @@ extern "C" xnp_status xnp_ring_slide(xnp_pool *pool, int32_t id, int32_t prefix,
         prefix + span > s->capacity || step < 0)
         return fail(XNP_E_INVALID, "slide over %d slots past %d with a window of %d, dropping %d, at step %lld",
                     span, prefix, window, drop, (long long)step);
-    int32_t in_view = 0;
-    for (int32_t sl = prefix; sl < prefix + span; sl++) in_view += s->valid[sl];
+    // valid slots in [prefix, prefix + span): the ring's count less those outside the window
+    int32_t in_view = s->nvalid;
+    for (int32_t sl = 0; sl < prefix; sl++) in_view -= s->valid[sl];
+    for (int32_t sl = prefix + span; sl < s->capacity; sl++) in_view -= s->valid[sl];
     if (in_view == window) {
         // s2s.rs:324-332: frames take the slots after the prefix in turn, so the oldest are the
         // next ones round.
@@ -749,6 +817,21 @@ extern "C" xnp_status xnp_ring_slide(xnp_pool *pool, int32_t id, int32_t prefix,
         if (xnp_status st = xnp_ring_evict(pool, id, prefix, slots.data(), drop, hip_stream)) return st;
     }
     return xnp_ring_set_slot(pool, id, prefix + (int32_t)(step % span));
+}
+
+extern "C" xnp_status xnp_ring_slide_batch(xnp_pool *pool, const int32_t *ids, int32_t n, int32_t prefix,
+                                           int32_t span, int32_t window, int32_t drop, const int64_t *steps,
+                                           int32_t *failed, void *hip_stream) {
+    if (!pool || (n > 0 && (!ids || !steps))) return fail(XNP_E_INVALID, "null argument");
+    if (failed) *failed = -1;
+    for (int32_t i = 0; i < n; i++) {
+        xnp_status st = xnp_ring_slide(pool, ids[i], prefix, span, window, drop, steps[i], hip_stream);
+        if (st) {
+            if (failed) *failed = i;
+            return st;
+        }
+    }
+    return XNP_OK;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -958,8 +1041,9 @@ extern "C" xnp_status xnp_batch_end(xnp_pool *pool) {
     for (int32_t id : B.ids) {
         Stream &s = pool->streams[id];
         if (s.ring != RING_NONE) {
-            // complete_kv's ring branch, transformer.rs:74-79
+            // complete_kv's ring branch, transformer.rs:74-79 (begin refused a valid write slot)
             s.valid[s.write] = 1;
+            s.nvalid++;
             s.filled = std::max(s.filled, s.write + 1);
             s.current_end += 1;
         } else {

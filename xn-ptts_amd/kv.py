@@ -70,6 +70,7 @@ SIGNATURES = {
     "xnp_pool_stats_get": (_i32, [_p, _c.POINTER(PoolStats)]),
     "xnp_pool_rope_rows": (_i32, [_p, _i32, _i32, _c.POINTER(_c.c_float)]),
     "xnp_pool_time_next": (_i32, [_p, _p, _p]),
+    "xnp_pool_check_tables": (_i32, [_p, _i32p, _p]),
     "xnp_stream_open": (_i32, [_p, _i32, _i32p]),
     "xnp_stream_close": (_i32, [_p, _i32]),
     "xnp_stream_fork": (_i32, [_p, _i32, _i32, _i32p, _p]),
@@ -83,6 +84,7 @@ SIGNATURES = {
     "xnp_ring_set_slot": (_i32, [_p, _i32, _i32]),
     "xnp_ring_evict": (_i32, [_p, _i32, _i32, _i32p, _i32, _p]),
     "xnp_ring_slide": (_i32, [_p, _i32, _i32, _i32, _i32, _i32, _c.c_int64, _p]),
+    "xnp_ring_slide_batch": (_i32, [_p, _i32p, _i32, _i32, _i32, _i32, _i32, _c.POINTER(_c.c_int64), _i32p, _p]),
     "xnp_batch_begin": (_i32, [_p, _i32p, _i32, _i32, _p]),
     "xnp_append": (_i32, [_p, _i32, _p, _p, _p]),
     "xnp_decode": (_i32, [_p, _i32, _p, _p, _c.c_float, _p]),
@@ -198,6 +200,12 @@ class KvPool:
         _check(self._lib.xnp_pool_stats_get(self._h, ctypes.byref(s)))
         return {n: getattr(s, n) for n, _ in PoolStats._fields_}
 
+    def check_tables(self, stream=None) -> int:
+        """Device block-table entries that differ from the host's page map (0 when consistent)."""
+        bad = _i32()
+        _check(self._lib.xnp_pool_check_tables(self._h, ctypes.byref(bad), _stream(stream)))
+        return bad.value
+
     def time_next(self, start_event: int, stop_event: int):
         """Have the next decode/prefill launch record these hipEvent_t handles around its kernel."""
         _check(self._lib.xnp_pool_time_next(self._h, start_event, stop_event))
@@ -269,6 +277,16 @@ class KvPool:
 
     def slide(self, sid: int, prefix: int, span: int, window: int, drop: int, step: int, stream=None):
         _check(self._lib.xnp_ring_slide(self._h, sid, prefix, span, window, drop, step, _stream(stream)))
+
+    def slide_batch(self, ids, prefix: int, span: int, window: int, drop: int, steps, stream=None):
+        """slide() over many streams, stream i at steps[i], in one call."""
+        ids = list(ids)
+        n = len(ids)
+        arr = (_i32 * max(n, 1))(*ids)
+        st = (ctypes.c_int64 * max(n, 1))(*[int(x) for x in steps])
+        failed = _i32(-1)
+        _check(self._lib.xnp_ring_slide_batch(self._h, arr, n, prefix, span, window, drop, st,
+                                              ctypes.byref(failed), _stream(stream)))
 
     # -- a batched step -----------------------------------------------------------------------
     def begin(self, ids: Iterable[int], t: int = 1, stream=None):
