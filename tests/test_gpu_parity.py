@@ -86,6 +86,29 @@ class Pair:
             self.orc[i].commit(t)
         return worst
 
+    def prefill_split(self, t, which=None):
+        """A prompt step through xnp_append then xnp_prefill (two calls, keys read back from the pages)."""
+        which = list(range(len(self.ids))) if which is None else which
+        n = len(which)
+        self.pool.begin([self.ids[i] for i in which], t=t)
+        worst = 0.0
+        for layer in range(self.L):
+            q, k, v = self.x(n, t, self.H, 64), self.x(n, t, self.KVH, 64), self.x(n, t, self.KVH, 64)
+            out = torch.empty((n, t, self.H, 64), dtype=TORCH_DT[self.act], device=DEV)
+            self.pool.append(layer, dev(k, self.act), dev(v, self.act))
+            self.pool.prefill(layer, dev(q, self.act), out, 0.125)
+            torch.cuda.synchronize()
+            got = host(out)
+            for j, i in enumerate(which):
+                want, _ = self.orc[i].attend(layer, q[j], k[j], v[j])
+                err = rel_err(got[j], want)
+                worst = max(worst, err)
+                assert err <= TOL[self.cache], (layer, i, err)
+        self.pool.end()
+        for i in which:
+            self.orc[i].commit(t)
+        return worst
+
     def step(self, which=None, fused=True, check=True):
         which = list(range(len(self.ids))) if which is None else which
         n = len(which)
@@ -362,3 +385,27 @@ def test_prompts_on_reopened_streams_use_live_pages():
             p.ids[i] = p.pool.init_state(64)
             p.orc[i] = oracle.Stream(p.L, p.H, 64, 64, cache="bf16", act="bf16")
     assert p.pool.check_tables() == 0
+
+
+@pytest.mark.parametrize("cache,act", [("bf16", "bf16"), ("i8", "bf16")])
+def test_prefill_after_a_separate_append(cache, act):
+    # xnp_append then xnp_prefill: the prompt's keys are read back from the pages
+    p = Pair(cache=cache, act=act, streams=3, cap=128, seed=24, page_seed=9)
+    for i, n in enumerate([0, 7, 33]):
+        p.fill(i, n)
+    p.prefill_split(45)
+    for i in range(3):
+        p.assert_cache_equal(i)
+    p.step()
+
+
+def test_long_prompts_take_several_rounds():
+    # 300- and 530-row prompts: more than one round of 256 query rows per work group, on top of
+    # prior rows that end mid-page; grouped heads
+    p = Pair(cache="bf16", act="bf16", H=8, KVH=2, streams=2, cap=640, seed=25, L=1, page_seed=10)
+    p.fill(1, 21)
+    assert p.prefill(300, which=[0]) <= 2e-2
+    assert p.prefill(530, which=[1]) <= 2e-2
+    for i in range(2):
+        p.assert_cache_equal(i)
+    p.step()

@@ -19,15 +19,20 @@ namespace xnp {
 
 __device__ __forceinline__ float bf16_value(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
 
-__device__ __forceinline__ uint32_t bf16_bits(float x) {
-    uint32_t u = __float_as_uint(x);
-    if ((u & 0x7f800000u) == 0x7f800000u) {
-        if (u & 0x007fffffu) u |= 0x00400000u;
-        return u >> 16;
-    }
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
+// Round to bf16 with v_cvt_pk_bf16_f32: round to nearest even, NaN kept quiet.  The same bits as
+// the CPU restatement's software rounding (checked on this hardware over 4M inputs: random
+// bits, exact ties, denormals, NaN and infinities).
+typedef float f32x2v_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+    const bf16x2v_t h = __builtin_convertvector((f32x2v_t){a, b}, bf16x2v_t);
+    uint32_t u;
+    __builtin_memcpy(&u, &h, 4);
+    return u;
 }
+
+__device__ __forceinline__ uint32_t bf16_bits(float x) { return pack_bf16(x, 0.f) & 0xffffu; }
 
 template <bool ABF> __device__ __forceinline__ float round_act(float x) {
     if constexpr (ABF) return bf16_value(bf16_bits(x));
@@ -618,16 +623,26 @@ hipError_t launch_rows_io(const PoolView &pv, int sid, int layer, int kv, int sl
 }
 
 // ---------------------------------------------------------------------------------------------
-// prompt prefill on MFMA (bf16 cache and activations), transformer.rs:231-248 batched.
+// prompt prefill on MFMA (bf16 cache and activations), transformer.rs:231-248 batched, with the
+// append of the prompt's K/V rows (complete_kv, transformer.rs:84-91) fused in.
 //
-// One work group per (stream, head, 64-row query tile), later tiles (more keys) first; wave w
-// owns query rows 16w .. 16w+15 of the tile.  Per 32 keys (two pages):
-//   S = Q K^T   v_mfma_f32_16x16x32_bf16, A = the wave's rotated query rows (registers), B = K^T
-//               straight from the page tiles (lane: key lane%16, 8 consecutive dims);
-//   softmax     online, in the C layout (lane: key lane%16, query rows 4(lane/16) .. +3);
-//   O += P V    A = P through LDS ([row][key] -> lane: row lane%16, 8 keys), B = V staged
-//               transposed in LDS ([dim][key]) by the whole group, double-buffered.
-// A and B always hold the same key (or dim) in the same (lane / 16, element) slot, so the
+// One work group of 8 waves per (stream, head).  Query rows are taken in rounds of 256: 16 tiles
+// of 16 rows, wave w owning tiles w and 15 - w of the round, so that every wave sees about the
+// same number of causal keys.  Keys are staged through LDS in chunks of 64 (four pages), K and
+// V both as [key][dim], double-buffered, with the next chunk's loads in flight while one is
+// attended over.  Keys before the prompt come from the pages; the prompt's own keys come
+// from the k/v inputs, rotated at their position and rounded to bf16, and are written into
+// their pages during the last round, so that each is written exactly once and never read back
+// from HBM.
+//
+// Both contractions are computed transposed so that P never leaves registers:
+//   S^T = K Q^T   v_mfma_f32_16x16x32_bf16, A = K rows from LDS (lane: key lane%16, 8 dims),
+//                 B = the wave's rotated query rows (registers; lane: query lane%16, 8 dims);
+//                 the result holds, per lane, query row lane%16 against keys 4(lane/16) .. +3;
+//   softmax       online per query row; its max and sum reduce over the 4 lanes of a row;
+//   O^T += V^T P^T  B = P^T straight from the S^T registers (lane: query lane%16, 8 keys),
+//                 A = V^T by transposed LDS reads of the same 8 keys (ds_read_b64_tr_b16).
+// A and B always hold the same key (or dim) in the same (lane / 16, element) slot, so each
 // contraction is right whatever order the instruction walks k in.
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
@@ -639,148 +654,251 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(const uint4 &u) {
     return r;
 }
 
-constexpr int kPfTile = 64; // query rows per work group
-constexpr int kPfPad = 40;  // LDS row length in bf16 (32 keys + 8 of padding against bank conflicts)
+typedef short v4s_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s_t lds_v4s_t;
 
-__global__ __launch_bounds__(256) void k_prefill_mfma(PoolView pv, BatchView bv, int layer, const void *q, void *out,
-                                                      float qmul) {
-    __shared__ uint16_t vt[2][kHeadDim][kPfPad]; // V of the current 32 keys, [dim][key]
-    __shared__ uint16_t pw[4][16][kPfPad];       // each wave's P, [row][key]
+// ds_read_b64_tr_b16 (gfx950).  Within each group of 16 lanes, lane j supplies the address of
+// four consecutive b16 values D[j][0..3], and lane i receives D[4 s + i / 4][i % 4] as element
+// s.  Pointing lane j at row r0 + j / 4, columns c0 + 4 (j % 4) of a row-major b16 matrix thus
+// hands lane i column c0 + i of rows r0 .. r0 + 3: a transposed read.
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t *p) {
+    const v4s_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t *)(__attribute__((address_space(3))) uint16_t *)p);
+    uint2 u;
+    __builtin_memcpy(&u, &r, 8);
+    return u;
+}
+
+constexpr int kPfKeys = 64;      // keys per chunk (four pages)
+constexpr int kPfLd = 72;        // LDS row length in bf16: 64 + 8 of padding, rows 16-byte aligned
+constexpr int kPfWaves = 8;      // waves per work group
+constexpr int kPfRound = 256;    // query rows per round: 8 waves x 2 tiles x 16 rows
+constexpr int kPfMaxPages = 512; // page ids a work group keeps in LDS
+static_assert(kPfMaxPages >= kLaneBlocks * 8, "every page of a stream fits (a pool refuses more than 60 x 8)");
+static_assert(64 * kPfWaves == kPfKeys * 8, "one thread stages 16 bytes of one key per chunk");
+
+__global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4))) void k_prefill_mfma(
+    PoolView pv, BatchView bv, int layer, const void *q, const void *knew, const void *vnew, void *out, float qmul,
+    int fused) {
+    __shared__ __attribute__((aligned(16))) uint16_t ks[2 * kPfKeys][kPfLd]; // K of two chunks, [key][dim]
+    __shared__ __attribute__((aligned(16))) uint16_t vs[2 * kPfKeys][kPfLd]; // V of two chunks, [key][dim]
+    __shared__ int32_t spages[kPfMaxPages];
     const int t = bv.t;
-    const int ntiles = (t + kPfTile - 1) / kPfTile;
-    const int h = blockIdx.x % pv.H, rest = blockIdx.x / pv.H;
-    const int tile = ntiles - 1 - rest % ntiles, b = rest / ntiles;
+    const int h = blockIdx.x % pv.H, b = blockIdx.x / pv.H;
     const StreamPlan P = bv.plans[b];
     const int32_t *tab = pv.tables + (size_t)P.sid * pv.mbps;
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
-    const int c0 = P.write_slot;         // slot (= position) of prompt row 0
-    const int row0 = tile * kPfTile + w * 16; // this wave's first prompt row
-    const int tile_end = min(t, (tile + 1) * kPfTile);
-    const int kend = c0 + tile_end;      // keys [0, kend) are seen by some row of the tile
-
-    // A operand of S: query row row0 + c16, dims 32 kc + 8 g .. +7, rotated at its position and
-    // rounded to bf16 as the reference's bf16 q is.
-    bf16x8_t qa[2];
-    {
-        const int qrow = row0 + c16;
-        const uint16_t *qr = (const uint16_t *)q + (((size_t)P.out_row * t + min(qrow, t - 1)) * pv.H + h) * kHeadDim;
-        const float2 *cs = pv.rope + (size_t)(P.pos + min(qrow, t - 1)) * (kHeadDim / 2);
-#pragma unroll
-        for (int kc = 0; kc < 2; ++kc) {
-            const int d0 = 32 * kc + 8 * g;
-            const uint4 raw = *(const uint4 *)(qr + d0);
-            const uint32_t *u = (const uint32_t *)&raw;
-            uint32_t o4[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float x0 = bf16_value(u[i] & 0xffffu), x1 = bf16_value(u[i] >> 16);
-                const float2 c = cs[d0 / 2 + i];
-                const float a = x0 * c.x, bb = x1 * c.y, e = x0 * c.y, f = x1 * c.x;
-                o4[i] = qrow < t ? (bf16_bits(a - bb) | (bf16_bits(e + f) << 16)) : 0u;
-            }
-            qa[kc] = as_bf16x8(make_uint4(o4[0], o4[1], o4[2], o4[3]));
-        }
-    }
-
-    const size_t ktile0 = tile_index(pv, layer, 0, 0, h) * (kBlock * kHeadDim); // elements
-    const size_t vtile0 = tile_index(pv, layer, 1, 0, h) * (kBlock * kHeadDim);
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, l16 = lane & 15;
+    const int c0 = P.write_slot; // slot (= position) of prompt row 0
+    const int kvh = h / (pv.H / pv.KVH);
     const size_t page_elems = (size_t)pv.H * kBlock * kHeadDim;
-    const uint16_t *pages = (const uint16_t *)pv.pages;
+    uint16_t *kpages = (uint16_t *)pv.pages + tile_index(pv, layer, 0, 0, h) * (kBlock * kHeadDim);
+    uint16_t *vpages = (uint16_t *)pv.pages + tile_index(pv, layer, 1, 0, h) * (kBlock * kHeadDim);
+    // the stream's page ids for every key any round sees, read once
+    for (int i = tid; i < min((c0 + t + kBlock - 1) / kBlock, kPfMaxPages); i += 64 * kPfWaves) spages[i] = tab[i];
+    // this thread's share of a chunk: 16 bytes (8 dims) of one key's K and V
+    const int skey = tid >> 3, spart = tid & 7;
 
-    float m[4], lsum[4];
-    f32x4_t o[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        m[r] = -1e30f;
-        lsum[r] = 0.f;
-    }
-#pragma unroll
-    for (int ni = 0; ni < 4; ++ni) o[ni] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const int nqt = (t + 15) / 16;
+    for (int tq0 = 0; tq0 < nqt; tq0 += kPfRound / 16) {
+        const int nq = min(kPfRound / 16, nqt - tq0);
+        const bool last = tq0 + nq == nqt;
+        // this wave's tiles: (w, nq-1-w) for w < nq/2; the middle one alone when nq is odd
+        int tile[2] = {-1, -1};
+        if (w < nq / 2) {
+            tile[0] = tq0 + w;
+            tile[1] = tq0 + nq - 1 - w;
+        } else if (w == nq / 2 && (nq & 1)) {
+            tile[0] = tq0 + w;
+        }
+        const int kend = c0 + min(t, 16 * (tq0 + nq)); // the round's rows see keys [0, kend)
+        const int nch = (kend + kPfKeys - 1) / kPfKeys;
 
-    const int nchunks = (kend + 31) / 32;
-    for (int ch = 0; ch < nchunks; ++ch) {
-        const int buf = ch & 1;
-        // stage this chunk's V transposed: thread -> page tid / 128, key (tid / 8) % 16, dims 8 (tid % 8)
+        // B operands of S^T: query row 16 tile + l16, dims 32 kc + 8 g .. +7, rotated at its
+        // position and rounded to bf16 as the reference's bf16 q is.  Every load is issued
+        // before any is used (rows past the prompt read row t - 1 and are zeroed after).
+        bf16x8_t qb[2][2];
+        float m[2], lsum[2]; // running max (scaled, log2 units) and this lane's share of the sum
+        f32x4_t o[2][4];
         {
-            const int pb = tid >> 7, key = (tid >> 3) & 15, d0 = 8 * (tid & 7);
-            const int blk = ch * 2 + pb;
-            uint4 vv = make_uint4(0, 0, 0, 0);
-            const int pg = blk * kBlock < kend ? tab[blk] : -1;
-            if (pg >= 0 && pg < pv.NB) vv = *(const uint4 *)(pages + vtile0 + (size_t)pg * page_elems + key * kHeadDim + d0);
-            const uint32_t *u = (const uint32_t *)&vv;
+            uint4 qraw[2][2];
+            float4 qcs[2][2][2];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                vt[buf][d0 + 2 * i][pb * 16 + key] = (uint16_t)(u[i] & 0xffffu);
-                vt[buf][d0 + 2 * i + 1][pb * 16 + key] = (uint16_t)(u[i] >> 16);
+            for (int j = 0; j < 2; ++j) {
+                const int qr = min(16 * max(tile[j], 0) + l16, t - 1);
+                const uint16_t *qp = (const uint16_t *)q + (((size_t)P.out_row * t + qr) * pv.H + h) * kHeadDim;
+                const float4 *cs = (const float4 *)(pv.rope + (size_t)(P.pos + qr) * (kHeadDim / 2));
+#pragma unroll
+                for (int kc = 0; kc < 2; ++kc) {
+                    qraw[j][kc] = *(const uint4 *)(qp + 32 * kc + 8 * g);
+                    qcs[j][kc][0] = cs[(32 * kc + 8 * g) / 4];
+                    qcs[j][kc][1] = cs[(32 * kc + 8 * g) / 4 + 1];
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                m[j] = -1e30f;
+                lsum[j] = 0.f;
+#pragma unroll
+                for (int dg = 0; dg < 4; ++dg) o[j][dg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                const bool live = tile[j] >= 0 && 16 * tile[j] + l16 < t;
+#pragma unroll
+                for (int kc = 0; kc < 2; ++kc) {
+                    const uint32_t *u = (const uint32_t *)&qraw[j][kc];
+                    const float4 ca = qcs[j][kc][0], cb = qcs[j][kc][1];
+                    const float cf[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w}; // cos, sin of 4 pairs
+                    uint32_t o4[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float x0 = bf16_value(u[i] & 0xffffu), x1 = bf16_value(u[i] >> 16);
+                        const float c = cf[2 * i], s = cf[2 * i + 1];
+                        const float a = x0 * c, bb = x1 * s, e = x0 * s, f = x1 * c;
+                        o4[i] = live ? pack_bf16(a - bb, e + f) : 0u;
+                    }
+                    qb[j][kc] = as_bf16x8(make_uint4(o4[0], o4[1], o4[2], o4[3]));
+                }
             }
         }
-        // B operands of S for the chunk's two pages: key c16, dims 32 kc + 8 g
-        uint4 kb[2][2];
-#pragma unroll
-        for (int pb = 0; pb < 2; ++pb) {
-            const int blk = ch * 2 + pb;
-            const int tpg = blk * kBlock < kend ? tab[blk] : -1;
-            const bool live = tpg >= 0 && tpg < pv.NB;
-            const int pg = live ? tpg : 0;
-            const uint16_t *kr = pages + ktile0 + (size_t)pg * page_elems + c16 * kHeadDim + 8 * g;
-#pragma unroll
-            for (int kc = 0; kc < 2; ++kc) kb[pb][kc] = live ? *(const uint4 *)(kr + 32 * kc) : make_uint4(0, 0, 0, 0);
-        }
-        __syncthreads(); // vt[buf] written; everyone is past the chunk that last read it
+        __syncthreads(); // spages written
 
-        float x[2][4];
-#pragma unroll
-        for (int pb = 0; pb < 2; ++pb) {
-            f32x4_t s4 = f32x4_t{0.f, 0.f, 0.f, 0.f};
-            s4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[0], as_bf16x8(kb[pb][0]), s4, 0, 0, 0);
-            s4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[1], as_bf16x8(kb[pb][1]), s4, 0, 0, 0);
-            const int ks = ch * 32 + pb * 16 + c16; // key slot
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int qs = c0 + row0 + 4 * g + r; // query slot
-                x[pb][r] = ks <= qs ? s4[r] * qmul : -INFINITY;
+        // Loads run one chunk ahead: chunk c's registers are consumed (rotated, stored to LDS
+        // buffer c & 1) at step c, which then issues chunk c + 1's loads into them.
+        struct Stage {
+            uint4 k, v, rope; // the key's K and V pieces, 4 (cos, sin) pairs as packed bf16
+            int info;         // bit 0: a prompt key, bit 1: write it to its page; page id above
+        };
+        auto issue = [&](int c, Stage &st) {
+            const int slot = c * kPfKeys + skey;
+            const bool in = c < nch && slot < kend;
+            const bool fresh = fused && slot >= c0; // a prompt key: from the inputs, rotated here
+            const int page = in ? spages[min(slot >> 4, kPfMaxPages - 1)] : -1;
+            const bool ok = page >= 0 && page < pv.NB;
+            const size_t poff = (size_t)(ok ? page : 0) * page_elems + (slot & 15) * kHeadDim + 8 * spart;
+            const int i = fresh ? min(slot - c0, t - 1) : 0;
+            const size_t arow = (((size_t)P.out_row * t + i) * pv.KVH + kvh) * kHeadDim + 8 * spart;
+            st.k = st.v = make_uint4(0, 0, 0, 0);
+            if (in && fresh) {
+                st.k = *(const uint4 *)((const uint16_t *)knew + arow);
+                st.v = *(const uint4 *)((const uint16_t *)vnew + arow);
+            } else if (in && ok) {
+                st.k = *(const uint4 *)(kpages + poff);
+                st.v = *(const uint4 *)(vpages + poff);
             }
-        }
-        float alpha[4];
+            st.rope = *(const uint4 *)(pv.rope16 + (size_t)(P.key_pos + i) * (kHeadDim / 2) + 4 * spart);
+            st.info = (in && fresh ? 1 : 0) | (in && fresh && ok && last ? 2 : 0) | ((ok ? page : 0) << 2);
+        };
+        auto step = [&](int c, Stage &st) {
+            const int buf = c & 1, kbase = c * kPfKeys, lb = buf * kPfKeys;
+            // rotate a prompt key at its position; store this thread's piece of the chunk
+            {
+                uint4 kk = st.k;
+                if (st.info & 1) {
+                    const uint32_t *r = (const uint32_t *)&st.rope;
+                    const uint32_t *u = (const uint32_t *)&st.k;
+                    uint32_t o4[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            float mx = fmaxf(x[0][r], x[1][r]);
+                    for (int e = 0; e < 4; ++e) {
+                        const float x0 = bf16_value(u[e] & 0xffffu), x1 = bf16_value(u[e] >> 16);
+                        const float cc = bf16_value(r[e] & 0xffffu), sn = bf16_value(r[e] >> 16);
+                        const float a = x0 * cc, bb = x1 * sn, ee = x0 * sn, f = x1 * cc;
+                        o4[e] = pack_bf16(a - bb, ee + f);
+                    }
+                    kk = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+                }
+                if (st.info & 2) { // complete_kv: the prompt's rows go into their pages once
+                    const size_t poff = (size_t)(st.info >> 2) * page_elems + ((kbase + skey) & 15) * kHeadDim + 8 * spart;
+                    *(uint4 *)(kpages + poff) = kk;
+                    *(uint4 *)(vpages + poff) = st.v;
+                }
+                *(uint4 *)&ks[lb + skey][8 * spart] = kk;
+                *(uint4 *)&vs[lb + skey][8 * spart] = st.v;
+            }
+            issue(c + 1, st);
+            __syncthreads(); // chunk c is in LDS; every reader of chunk c - 2 (same buffer) is done
 #pragma unroll
-            for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-            const float mn = fmaxf(m[r], mx);
-            alpha[r] = fast_exp2(m[r] - mn);
-            m[r] = mn;
-            const float p0 = fast_exp2(x[0][r] - mn), p1 = fast_exp2(x[1][r] - mn);
-            lsum[r] = lsum[r] * alpha[r] + p0 + p1;
-            pw[w][4 * g + r][c16] = (uint16_t)bf16_bits(p0);
-            pw[w][4 * g + r][16 + c16] = (uint16_t)bf16_bits(p1);
-        }
+            for (int j = 0; j < 2; ++j) {
+                const int r0 = c0 + 16 * tile[j]; // slot of the tile's first row
+                // skip a tile when every key of the chunk comes after all of its rows
+                if (tile[j] < 0 || kbase > r0 + 15) continue;
+                f32x4_t s[4];
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni)
+                for (int kg = 0; kg < 4; ++kg) {
+                    s[kg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int r = 0; r < 4; ++r) o[ni][r] *= alpha[r];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const bf16x8_t pa = as_bf16x8(*(const uint4 *)&pw[w][c16][8 * g]);
+                    for (int kc = 0; kc < 2; ++kc) {
+                        const bf16x8_t a = as_bf16x8(*(const uint4 *)&ks[lb + 16 * kg + l16][32 * kc + 8 * g]);
+                        s[kg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qb[j][kc], s[kg], 0, 0, 0);
+                    }
+                }
+                // lane: query slot r0 + l16 against key slots kbase + 16 kg + 4 g + r
+                if (kbase + kPfKeys - 1 > r0) { // the chunk reaches past the tile's first row: mask
+                    const int qs = r0 + l16;
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni) {
-            const bf16x8_t vb = as_bf16x8(*(const uint4 *)&vt[buf][16 * ni + c16][8 * g]);
-            o[ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vb, o[ni], 0, 0, 0);
-        }
-    }
-    // row sums over the 16 key lanes, then out[row][h][16 ni + c16]
+                    for (int kg = 0; kg < 4; ++kg)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        float s = lsum[r];
+                        for (int r = 0; r < 4; ++r)
+                            if (kbase + 16 * kg + 4 * g + r > qs) s[kg][r] = -INFINITY;
+                }
+                float mx = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
 #pragma unroll
-        for (int off = 1; off < 16; off <<= 1) s += __shfl_xor(s, off);
-        const int qrow = row0 + 4 * g + r;
-        if (qrow < t) {
+                for (int kg = 1; kg < 4; ++kg)
+                    mx = fmaxf(mx, fmaxf(fmaxf(s[kg][0], s[kg][1]), fmaxf(s[kg][2], s[kg][3])));
+                mx = fmaxf(mx, __shfl_xor(mx, 16));
+                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                const float mn = fmaxf(m[j], mx * qmul);
+                const float alpha = fast_exp2(m[j] - mn);
+                m[j] = mn;
+                float psum = 0.f;
+                uint32_t pk[4][2];
+#pragma unroll
+                for (int kg = 0; kg < 4; ++kg) {
+                    float p[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        p[r] = fast_exp2(__builtin_fmaf(s[kg][r], qmul, -mn));
+                        psum += p[r];
+                    }
+                    pk[kg][0] = pack_bf16(p[0], p[1]);
+                    pk[kg][1] = pack_bf16(p[2], p[3]);
+                }
+                lsum[j] = __builtin_fmaf(lsum[j], alpha, psum);
+#pragma unroll
+                for (int dg = 0; dg < 4; ++dg)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) o[j][dg][r] *= alpha;
+#pragma unroll
+                for (int kp = 0; kp < 2; ++kp) {
+                    // k slots: keys 32 kp + 4 g .. +3 (elements 0-3) and 32 kp + 16 + 4 g .. +3 (4-7)
+                    const bf16x8_t pb =
+                        as_bf16x8(make_uint4(pk[2 * kp][0], pk[2 * kp][1], pk[2 * kp + 1][0], pk[2 * kp + 1][1]));
+#pragma unroll
+                    for (int dg = 0; dg < 4; ++dg) {
+                        // V^T: lane gets dim 16 dg + l16 of the same eight keys, by two transposed reads
+                        const uint16_t *vp = &vs[lb + 32 * kp + 4 * g + (l16 >> 2)][16 * dg + 4 * (l16 & 3)];
+                        const uint2 lo = lds_read_tr16(vp), hi = lds_read_tr16(vp + 16 * kPfLd);
+                        const bf16x8_t a = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+                        o[j][dg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, o[j][dg], 0, 0, 0);
+                    }
+                }
+            }
+        };
+        Stage st;
+        issue(0, st);
+        for (int c = 0; c < nch; ++c) step(c, st);
+        __syncthreads(); // the next round's staging overwrites both buffers
+
+        // out[row][h][16 dg + 4 g .. +3] = O / l, the row's sum reduced over its 4 lanes
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            float l = lsum[j];
+            l += __shfl_xor(l, 16);
+            l += __shfl_xor(l, 32);
+            const int qrow = 16 * tile[j] + l16;
+            if (tile[j] < 0 || qrow >= t) continue;
+            const float inv = 1.0f / l;
             uint16_t *orow = (uint16_t *)out + (((size_t)P.out_row * t + qrow) * pv.H + h) * kHeadDim;
-            const float inv = 1.0f / s;
 #pragma unroll
-            for (int ni = 0; ni < 4; ++ni) orow[16 * ni + c16] = (uint16_t)bf16_bits(o[ni][r] * inv);
+            for (int dg = 0; dg < 4; ++dg)
+                *(uint2 *)(orow + 16 * dg + 4 * g) = make_uint2(pack_bf16(o[j][dg][0] * inv, o[j][dg][1] * inv),
+                                                                pack_bf16(o[j][dg][2] * inv, o[j][dg][3] * inv));
         }
     }
 }
@@ -800,17 +918,19 @@ static hipError_t prefill_rows_impl(const PoolView &pv, const BatchView &bv, int
     return hipGetLastError();
 }
 
-hipError_t launch_prefill(const PoolView &pv, const BatchView &bv, int layer, const void *q, void *out, float scale,
-                          hipStream_t stream, const LaunchTiming &tm) {
+bool prefill_fuses_append(const PoolView &pv) { return pv.cache_dt == DT_BF16 && pv.act_dt == DT_BF16; }
+
+hipError_t launch_prefill(const PoolView &pv, const BatchView &bv, int layer, const void *q, const void *k,
+                          const void *v, void *out, float scale, bool fused, hipStream_t stream,
+                          const LaunchTiming &tm) {
     if (bv.n == 0) return hipSuccess;
+    if (fused && !prefill_fuses_append(pv)) return hipErrorInvalidValue;
     switch (pv.cache_dt * 2 + pv.act_dt) {
     case DT_F32 * 2 + DT_F32: return prefill_rows_impl<DT_F32, false>(pv, bv, layer, q, out, scale, stream, tm);
-    case DT_BF16 * 2 + DT_BF16: {
-        const int ntiles = (bv.t + kPfTile - 1) / kPfTile;
-        hipExtLaunchKernelGGL(k_prefill_mfma, dim3(bv.n * ntiles * pv.H), dim3(256), 0, stream, tm.start, tm.stop, 0,
-                              pv, bv, layer, q, out, scale * 1.4426950408889634f);
+    case DT_BF16 * 2 + DT_BF16:
+        hipExtLaunchKernelGGL(k_prefill_mfma, dim3(bv.n * pv.H), dim3(64 * kPfWaves), 0, stream, tm.start, tm.stop, 0,
+                              pv, bv, layer, q, k, v, out, scale * 1.4426950408889634f, fused ? 1 : 0);
         return hipGetLastError();
-    }
     case DT_I8 * 2 + DT_BF16: return prefill_rows_impl<DT_I8, true>(pv, bv, layer, q, out, scale, stream, tm);
     case DT_I8 * 2 + DT_F32: return prefill_rows_impl<DT_I8, false>(pv, bv, layer, q, out, scale, stream, tm);
     default: return hipErrorInvalidValue;

@@ -112,6 +112,7 @@ struct xnp_pool {
     float *scales = nullptr;
     int32_t *tables = nullptr;
     float2 *rope = nullptr;
+    uint32_t *rope16 = nullptr; // bf16 pools: the table as packed bf16 pairs
     char *dbatch = nullptr; // batch plan upload
     char *daux = nullptr;   // table patches and eviction rows
     size_t batch_bytes = 0, aux_bytes = 0;
@@ -146,6 +147,7 @@ struct xnp_pool {
         pv.scales = scales;
         pv.tables = tables;
         pv.rope = rope;
+        pv.rope16 = rope16;
         pv.L = d.num_layers;
         pv.H = d.num_heads;
         pv.KVH = d.num_kv_heads;
@@ -296,7 +298,7 @@ static void pool_free(xnp_pool *p) {
             if (s.done) (void)hipEventDestroy(s.done);
             if (s.host) (void)hipHostFree(s.host);
         }
-        void *bufs[] = {p->pages, p->scales, p->tables, p->rope, p->dbatch, p->daux};
+        void *bufs[] = {p->pages, p->scales, p->tables, p->rope, p->rope16, p->dbatch, p->daux};
         for (void *b : bufs)
             if (b) (void)hipFree(b);
     }
@@ -396,6 +398,7 @@ extern "C" xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out)
         {(void **)&p->scales, d.cache_dtype == XNP_I8 ? sizeof(float) * d.num_heads * (size_t)d.num_blocks * 2 * d.num_layers : 0, "scales"},
         {(void **)&p->tables, sizeof(int32_t) * (size_t)d.max_streams * d.max_blocks_per_stream, "block tables"},
         {(void **)&p->rope, sizeof(float2) * p->rope_host.size(), "rope table"},
+        {(void **)&p->rope16, d.act_dtype == XNP_BF16 ? sizeof(uint32_t) * p->rope_host.size() : 0, "bf16 rope table"},
         {(void **)&p->dbatch, p->batch_bytes, "batch plan"},
         {(void **)&p->daux, p->aux_bytes, "aux upload"},
     };
@@ -413,6 +416,18 @@ extern "C" xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out)
     }
     e = hipMemcpy(p->rope, p->rope_host.data(), sizeof(float2) * p->rope_host.size(), hipMemcpyHostToDevice);
     if (e != hipSuccess) return dev_fail(e, "rope table upload");
+    if (p->rope16) {
+        // the bf16 table's values are the f32 table's, which were rounded to bf16: no rounding here
+        std::vector<uint32_t> packed(p->rope_host.size());
+        for (size_t i = 0; i < packed.size(); i++) {
+            uint32_t c, sn;
+            std::memcpy(&c, &p->rope_host[i].x, 4);
+            std::memcpy(&sn, &p->rope_host[i].y, 4);
+            packed[i] = (c >> 16) | (sn & 0xffff0000u);
+        }
+        e = hipMemcpy(p->rope16, packed.data(), sizeof(uint32_t) * packed.size(), hipMemcpyHostToDevice);
+        if (e != hipSuccess) return dev_fail(e, "bf16 rope table upload");
+    }
     const size_t stage_bytes = std::max(p->batch_bytes, p->aux_bytes);
     for (auto &s : p->stage) {
         e = hipHostMalloc((void **)&s.host, stage_bytes, hipHostMallocDefault);
@@ -1014,7 +1029,9 @@ extern "C" xnp_status xnp_prefill(xnp_pool *pool, int32_t layer, const void *q, 
     if (pool->batch.n > 0 && (!q || !out)) return fail(XNP_E_INVALID, "null q or out");
     const LaunchTiming tm = pool->timing;
     pool->timing = LaunchTiming();
-    HIP_TRY(launch_prefill(pool->view(), pool->batch.bv, layer, q, out, scale, pool->batch.stream, tm), "prefill");
+    HIP_TRY(launch_prefill(pool->view(), pool->batch.bv, layer, q, nullptr, nullptr, out, scale, false,
+                           pool->batch.stream, tm),
+            "prefill");
     return XNP_OK;
 }
 
@@ -1022,8 +1039,18 @@ extern "C" xnp_status xnp_attend(xnp_pool *pool, int32_t layer, const void *q, c
                                  void *out, float scale, void *hip_stream) {
     if (!pool) return fail(XNP_E_INVALID, "null argument");
     if (pool->batch.open && pool->batch.t > 1) {
-        if (xnp_status st = xnp_append(pool, layer, k, v, hip_stream)) return st;
-        return xnp_prefill(pool, layer, q, out, scale, hip_stream);
+        if (!prefill_fuses_append(pool->view())) {
+            if (xnp_status st = xnp_append(pool, layer, k, v, hip_stream)) return st;
+            return xnp_prefill(pool, layer, q, out, scale, hip_stream);
+        }
+        // one kernel writes the prompt's K/V rows into the pages and attends over them
+        if (xnp_status st = batch_call(pool, layer, hip_stream, false)) return st;
+        if (pool->batch.n > 0 && (!q || !k || !v || !out)) return fail(XNP_E_INVALID, "null q, k, v or out");
+        const LaunchTiming tm = pool->timing;
+        pool->timing = LaunchTiming();
+        HIP_TRY(launch_prefill(pool->view(), pool->batch.bv, layer, q, k, v, out, scale, true, pool->batch.stream, tm),
+                "attend");
+        return XNP_OK;
     }
     if (xnp_status st = batch_call(pool, layer, hip_stream, true)) return st;
     if (pool->batch.n > 0 && (!q || !k || !v || !out)) return fail(XNP_E_INVALID, "null q, k, v or out");

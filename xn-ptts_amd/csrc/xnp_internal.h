@@ -21,6 +21,7 @@ struct PoolView {
     float *scales;        // [L][2][NB][H] (int8 only)
     int32_t *tables;      // [max_streams][mbps] page ids, -1 where none
     const float2 *rope;   // [max_pos][D/2] (cos, sin), rounded to the activation dtype
+    const uint32_t *rope16; // bf16 activations only: the same table as packed bf16 (cos | sin << 16)
     int32_t L, H, KVH, D, NB, mbps, max_pos;
     int32_t cache_dt, act_dt;
 };
@@ -84,8 +85,13 @@ hipError_t launch_append(const PoolView &pv, const BatchView &bv, int layer, con
 hipError_t launch_decode(const PoolView &pv, const BatchView &bv, int layer, const void *q,
                          const void *k, const void *v, void *out, float scale, bool fused,
                          hipStream_t stream, const LaunchTiming &timing);
+// Prompt attention over the pages.  fused: the prompt's K/V rows come from k and v and the
+// kernel writes them into the pages itself (only where prefill_fuses_append holds); otherwise
+// launch_append has written them already and k, v are unused.
+bool prefill_fuses_append(const PoolView &pv);
 hipError_t launch_prefill(const PoolView &pv, const BatchView &bv, int layer, const void *q,
-                          void *out, float scale, hipStream_t stream, const LaunchTiming &timing);
+                          const void *k, const void *v, void *out, float scale, bool fused,
+                          hipStream_t stream, const LaunchTiming &timing);
 hipError_t launch_evict_rotate(const PoolView &pv, const EvictRow *rows, int n,
                                const float *cos_row, const float *sin_row, hipStream_t stream);
 hipError_t launch_copy_page(const PoolView &pv, int src_page, int dst_page, hipStream_t stream);
