@@ -409,3 +409,25 @@ def test_long_prompts_take_several_rounds():
     for i in range(2):
         p.assert_cache_equal(i)
     p.step()
+
+
+@pytest.mark.parametrize("cache,act", [("bf16", "bf16"), ("f32", "f32")])
+def test_unwritten_rows_holding_nan_bytes_do_not_reach_the_output(cache, act):
+    # A page's rows past current_end are never attended, but the kernels read whole tiles: rows
+    # holding NaN bit patterns (left by an earlier user of the memory) must weigh exactly nothing.
+    p = Pair(cache=cache, act=act, streams=2, cap=64, seed=26, L=1, page_seed=11)
+    for i, n in enumerate([20, 37]):
+        sid, st = p.ids[i], p.orc[i]
+        p.pool.advance(sid, n)
+        st.advance(n)
+        full = (n + 15) // 16 * 16  # every row of the pages the stream holds
+        for kv in (0, 1):
+            vals = p.x(n, p.H, 64)
+            st.write_rows(0, kv, 0, vals=vals)
+            rows = np.full((full, p.H, 64), np.nan, np.float32)
+            rows[:n] = vals
+            p.pool.write_rows(sid, 0, kv, 0, dev(rows, act))
+    torch.cuda.synchronize()
+    assert p.step() <= TOL[cache]
+    for i in range(2):
+        p.assert_cache_equal(i)

@@ -213,10 +213,15 @@ __device__ __forceinline__ void unpack(const uint4 &w, float (&x)[Lanes<CDT>::DP
             x[2 * i + 1] = bf16_value(u[i] >> 16);
         }
     } else {
+        // int8 codes q as q + 128: flipping the top bit of each byte makes it unsigned, and an
+        // unsigned byte converts to f32 in one instruction (v_cvt_f32_ubyte0..3).  The callers
+        // take the 128 back out once per dot product / per accumulator.
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t b = u[i] ^ 0x80808080u;
 #pragma unroll
-            for (int bt = 0; bt < 4; ++bt) x[4 * i + bt] = (float)(int8_t)((u[i] >> (8 * bt)) & 0xffu);
+            for (int bt = 0; bt < 4; ++bt) x[4 * i + bt] = (float)((b >> (8 * bt)) & 0xffu);
+        }
     }
 }
 
@@ -239,7 +244,7 @@ __device__ __forceinline__ void rotated_q(const PoolView &pv, const void *qrow, 
 // One query row of one head against pages [0, R.nblk) of its stream, by a group of SPLIT waves:
 // the body of the decode kernel and of the prompt-row kernel.  `pages` lists the stream's page
 // ids by logical block (a decode record's copy, or the block table).
-template <int CDT, bool ABF, int SPLIT>
+template <int CDT, bool ABF, int SPLIT, bool PREFIX>
 __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView &bv, int layer, const StreamRec &R,
                                             const int32_t *rec_pages, int h, const void *q, const void *knew,
                                             const void *vnew, void *out, float qmul, int fused) {
@@ -276,33 +281,23 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
         }
     }
 
-    // complete_kv: the wave that owns the write page appends this head's new row, then reads it
-    // back with the rest of its pages (its own lanes' stores; no other wave touches the page).
-    // A workgroup-scope fence orders the stores before the later loads on the same CU; nothing
-    // waits for the stores to reach memory.
-    const int wblk = R.write_slot >> 4;
-    if (fused && w == wblk % SPLIT) {
-        const int slot = R.write_slot, wj = wblk / SPLIT;
-        const size_t arow = (size_t)R.b * pv.KVH + h / (pv.H / pv.KVH);
-        const bool fresh = (R.flags & 1) ? (R.flags & 2) != 0 : ((slot & 15) == 0);
-        append_row_wave<CDT, ABF>(pv, layer, __builtin_amdgcn_readlane(my_page, wj), slot & 15, h, R.key_pos,
-                                  (const char *)knew + arow * kHeadDim * AE, (const char *)vnew + arow * kHeadDim * AE,
-                                  fresh);
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
-        if constexpr (CDT == DT_I8) {
-            if (lane == wj) { // the append may have raised this page's scales
-                my_sk = pv.scales[tile_index(pv, layer, 0, my_page, h)];
-                my_sv = pv.scales[tile_index(pv, layer, 1, my_page, h)];
-            }
-        }
-    }
-
     const int c = lane % LPR, g = lane / LPR;
     const char *qrow = (const char *)q + ((size_t)R.b * pv.H + h) * kHeadDim * AE;
     float qw[DPL], qp[DPL];
     rotated_q<DPL, ABF>(pv, qrow, c, R.pos, qmul, qw);
-    const bool two_q = R.prefix > 0;
+    const bool two_q = PREFIX && R.prefix > 0; // PREFIX: some stream of the batch keeps a prefix
     if (two_q) rotated_q<DPL, ABF>(pv, qrow, c, R.pos_pre, qmul, qp);
+    // int8: unpack hands out q + 128, so a dot product is sum(qw (q + 128)) - 128 sum(qw) and a
+    // value accumulator carries -128 sum(e sv) on every dim (vbias, taken out after the loop)
+    float qwsum = 0.f, qpsum = 0.f, vbias = 0.f;
+    if constexpr (CDT == DT_I8) {
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) qwsum += qw[i];
+        if (two_q) {
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) qpsum += qp[i];
+        }
+    }
 
     const uint4 *kbase = (const uint4 *)((const char *)pv.pages + tile_index(pv, layer, 0, 0, h) * (kBlock * kHeadDim * esize<CDT>()));
     const uint4 *vbase = (const uint4 *)((const char *)pv.pages + tile_index(pv, layer, 1, 0, h) * (kBlock * kHeadDim * esize<CDT>()));
@@ -330,11 +325,13 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
             float dw = 0.f;
 #pragma unroll
             for (int i = 0; i < DPL; ++i) dw = __builtin_fmaf(qw[i], x[i], dw);
+            if constexpr (CDT == DT_I8) dw = __builtin_fmaf(-128.f, qwsum, dw);
             const int r = g + RPP * p;
             if (two_q && base + r < R.prefix) {
                 float dp = 0.f;
 #pragma unroll
                 for (int i = 0; i < DPL; ++i) dp = __builtin_fmaf(qp[i], x[i], dp);
+                if constexpr (CDT == DT_I8) dp = __builtin_fmaf(-128.f, qpsum, dp);
                 dw = dp;
             }
 #pragma unroll
@@ -350,13 +347,19 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
         l *= alpha;
 #pragma unroll
         for (int i = 0; i < DPL; ++i) acc[i] *= alpha;
+        if constexpr (CDT == DT_I8) vbias *= alpha;
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
             const float e = fast_exp2(s[p] - m_new);
             l += e;
+            // an unseen row weighs 0, but its bytes may be anything (a page's unwritten rows
+            // hold what the memory held before): zero them, since 0 * NaN would still be NaN
+            const bool rs = (seen >> (g + RPP * p)) & 1u;
+            const uint4 vv = rs ? vr[p] : make_uint4(0, 0, 0, 0);
             float x[DPL];
-            unpack<CDT>(vr[p], x);
+            unpack<CDT>(vv, x);
             const float ev = (CDT == DT_I8) ? e * sv : e;
+            if constexpr (CDT == DT_I8) vbias += ev;
 #pragma unroll
             for (int i = 0; i < DPL; ++i) acc[i] = __builtin_fmaf(ev, x[i], acc[i]);
         }
@@ -377,8 +380,38 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
     // L2, and its rows are unseen, so reducing it changes nothing.  Each wait then only covers
     // the oldest page's loads.
     uint4 kb[DEPTH + 1][NP], vb[DEPTH + 1][NP];
+
+    // complete_kv: the wave that owns the write page appends this head's new row, then reads it
+    // back with the rest of its pages (its own lanes' stores; no other wave touches the page).
+    // A workgroup-scope fence orders the stores before the later loads on the same CU; nothing
+    // waits for the stores to reach memory.  When the write page is not among the wave's first
+    // DEPTH pages, those are loaded before the append, so the append's round trips overlap them.
+    const int wblk = R.write_slot >> 4, wj = wblk / SPLIT;
+    const bool owner = fused && w == wblk % SPLIT;
+    const bool early = !owner || wj >= DEPTH;
+    if (early) {
 #pragma unroll
-    for (int d = 0; d < DEPTH; ++d) load(kb[d], vb[d], d);
+        for (int d = 0; d < DEPTH; ++d) load(kb[d], vb[d], d);
+    }
+    if (owner) {
+        const int slot = R.write_slot;
+        const size_t arow = (size_t)R.b * pv.KVH + h / (pv.H / pv.KVH);
+        const bool fresh = (R.flags & 1) ? (R.flags & 2) != 0 : ((slot & 15) == 0);
+        append_row_wave<CDT, ABF>(pv, layer, __builtin_amdgcn_readlane(my_page, wj), slot & 15, h, R.key_pos,
+                                  (const char *)knew + arow * kHeadDim * AE, (const char *)vnew + arow * kHeadDim * AE,
+                                  fresh);
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+        if constexpr (CDT == DT_I8) {
+            if (lane == wj) { // the append may have raised this page's scales
+                my_sk = pv.scales[tile_index(pv, layer, 0, my_page, h)];
+                my_sv = pv.scales[tile_index(pv, layer, 1, my_page, h)];
+            }
+        }
+    }
+    if (!early) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) load(kb[d], vb[d], d);
+    }
     for (int j = 0; j < nb; j += DEPTH + 1) {
 #pragma unroll
         for (int u = 0; u <= DEPTH; ++u) {
@@ -387,6 +420,10 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
         }
     }
 
+    if constexpr (CDT == DT_I8) {
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) acc[i] = __builtin_fmaf(-128.f, vbias, acc[i]);
+    }
     // Merge the row groups: lanes c, c + LPR, c + 2 LPR, ... hold the same dims.
 #pragma unroll
     for (int o = LPR; o < 64; o <<= 1) {
@@ -432,14 +469,14 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
 
 // Decode: one work group per (stream, head), streams longest first.  The stream record carries
 // everything the group needs, its page ids included.
-template <int CDT, bool ABF, int SPLIT>
+template <int CDT, bool ABF, int SPLIT, bool PREFIX>
 __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(Lanes<CDT>::WAVES))) void k_decode(
     PoolView pv, BatchView bv, int layer, const void *q, const void *knew, const void *vnew, void *out, float qmul,
     int fused) {
     const char *rec = bv.recs + (size_t)(blockIdx.x / pv.H) * bv.rec_stride;
     const StreamRec R = *(const StreamRec *)rec;
-    attend_core<CDT, ABF, SPLIT>(pv, bv, layer, R, (const int32_t *)(rec + sizeof(StreamRec)), blockIdx.x % pv.H, q,
-                                 knew, vnew, out, qmul, fused);
+    attend_core<CDT, ABF, SPLIT, PREFIX>(pv, bv, layer, R, (const int32_t *)(rec + sizeof(StreamRec)),
+                                         blockIdx.x % pv.H, q, knew, vnew, out, qmul, fused);
 }
 
 // Prompt rows (transformer.rs:231-248), after k_append has written all t rows: row i of a stream
@@ -463,8 +500,8 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(Lane
     R.key_pos = P.key_pos + i;
     R.mask_off = -1;
     R.flags = 0;
-    attend_core<CDT, ABF, SPLIT>(pv, bv, layer, R, pv.tables + (size_t)P.sid * pv.mbps, h, q, nullptr, nullptr, out, qmul,
-                                 0);
+    attend_core<CDT, ABF, SPLIT, false>(pv, bv, layer, R, pv.tables + (size_t)P.sid * pv.mbps, h, q, nullptr, nullptr,
+                                        out, qmul, 0); // prompts never run on a ring
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -498,13 +535,27 @@ static hipError_t decode_impl(const PoolView &pv, const BatchView &bv, int layer
     const float qmul = scale * 1.4426950408889634f;
     const dim3 grid(bv.n * pv.H);
     const int f = fused ? 1 : 0;
-    switch (bv.split) {
-    case 1: hipExtLaunchKernelGGL((k_decode<CDT, ABF, 1>), grid, dim3(64), 0, stream, tm.start, tm.stop, 0, pv, bv, layer, q, k, v, out, qmul, f); break;
-    case 2: hipExtLaunchKernelGGL((k_decode<CDT, ABF, 2>), grid, dim3(128), 0, stream, tm.start, tm.stop, 0, pv, bv, layer, q, k, v, out, qmul, f); break;
-    case 4: hipExtLaunchKernelGGL((k_decode<CDT, ABF, 4>), grid, dim3(256), 0, stream, tm.start, tm.stop, 0, pv, bv, layer, q, k, v, out, qmul, f); break;
-    case 8: hipExtLaunchKernelGGL((k_decode<CDT, ABF, 8>), grid, dim3(512), 0, stream, tm.start, tm.stop, 0, pv, bv, layer, q, k, v, out, qmul, f); break;
-    default: return hipErrorInvalidValue;
+#define XNP_DECODE(S, PFX)                                                                                          \
+    hipExtLaunchKernelGGL((k_decode<CDT, ABF, S, PFX>), grid, dim3(64 * S), 0, stream, tm.start, tm.stop, 0, pv, bv, \
+                          layer, q, k, v, out, qmul, f)
+    if (bv.prefix) {
+        switch (bv.split) {
+        case 1: XNP_DECODE(1, true); break;
+        case 2: XNP_DECODE(2, true); break;
+        case 4: XNP_DECODE(4, true); break;
+        case 8: XNP_DECODE(8, true); break;
+        default: return hipErrorInvalidValue;
+        }
+    } else {
+        switch (bv.split) {
+        case 1: XNP_DECODE(1, false); break;
+        case 2: XNP_DECODE(2, false); break;
+        case 4: XNP_DECODE(4, false); break;
+        case 8: XNP_DECODE(8, false); break;
+        default: return hipErrorInvalidValue;
+        }
     }
+#undef XNP_DECODE
     return hipGetLastError();
 }
 

@@ -983,6 +983,8 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
     B.bv.recs = pool->dbatch + o_recs;
     B.bv.rec_stride = pool->rec_stride;
     B.bv.split = pool->split;
+    B.bv.prefix = 0;
+    for (int32_t i = 0; i < n; i++) B.bv.prefix |= plans[i].prefix > 0;
     B.bv.masks = (const uint32_t *)(pool->dbatch + o_masks);
     B.bv.n = n;
     B.bv.t = t;

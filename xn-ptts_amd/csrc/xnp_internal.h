@@ -59,7 +59,8 @@ struct BatchView {
     const char *recs; // stream records in decode order (longest first), rec_stride bytes apart
     const uint32_t *masks;
     int32_t n, t, rec_stride;
-    int32_t split; // waves per (stream, head) work group
+    int32_t split;  // waves per (stream, head) work group
+    int32_t prefix; // 1 if some stream of the batch is an absolute ring keeping a prefix
 };
 
 // A table entry to set before the batch's kernels run.
