@@ -16,6 +16,11 @@
   theta 10000, causal, K/V written into the pages.  Value: prompt positions/s.  Roofline: causal
   flops 2 D T (T+1) H S per layer launch against 2.5 PFLOP/s dense bf16 MFMA.
 
+--workload step: the full per-frame flow-LM layer step, 2048 streams x 9 Phonon-40m layers (512 wide,
+  8 heads x 64, FF 2048): LayerNorm, int8 per-channel q8 projections (QKV, out, FF) on MFMA, erf GELU,
+  residuals, RoPE, paged bf16 KV append and decode attention over cache lengths U[1, 1500].  Value:
+  frames/s.  Roofline: the decode attention kernel (the step's dominant kernel) against 8 TB/s.
+
 --workload window: int8 K/V with fp32 scales per (page, head), 1024 streams, a sliding window of
   512 positions on rings of 528 slots whose write heads start at offsets U[0, 4096), each stream
   holding U[64, 2048] rows written so far; per step every stream evicts its oldest row once the
@@ -415,12 +420,136 @@ def run_window(args, xnp, torch):
                 "frames/s", args, ms, "int8", config, roof, cpu, extra={"audio_sec_per_sec": round(fps * 0.08, 1)})
 
 
+# ---- the full per-frame layer step (configuration 5) ---------------------------------------------
+DM, FF = 512, 2048
+
+
+def gemm_flops(rows):
+    """Multiply-adds x 2 of the four q8 projections of one layer over `rows` rows."""
+    return 2.0 * rows * DM * ((H + 2 * H) * D + DM + FF) + 2.0 * rows * FF * DM
+
+
+def step_weights(rng, L):
+    xnp = _load("xn_ptts_amd", os.path.join(ROOT, "xn-ptts_amd"))
+    ws = []
+    for _ in range(L):
+        qr = lambda n, k: xnp.quantize_rows(rng.standard_normal((n, k)).astype(np.float32) * 0.02)
+        parts = dict(zip(["wqkv", "sqkv"], qr(3 * H * D, DM)))
+        parts.update(zip(["wout", "sout"], qr(DM, H * D)))
+        parts.update(zip(["w1", "s1"], qr(FF, DM)))
+        parts.update(zip(["w2", "s2"], qr(DM, FF)))
+        for n in ("ln1", "ln2"):
+            parts[n + "_w"] = np.ones(DM, np.float32)
+            parts[n + "_b"] = np.zeros(DM, np.float32)
+        ws.append(parts)
+    return ws
+
+
+def cpu_step(L, lens_all, weights, seconds, sample=64):
+    oracle = _load("oracle", os.path.join(ROOT, "oracle", "oracle.py"))
+    rng = np.random.default_rng(SEED + 500)
+    lens = lens_all[:sample]
+    cap = int(lens.max()) + 64
+    streams = [oracle.Stream(L, H, D, cap, cache="bf16", act="bf16") for _ in lens]
+    rows = bf16_np(rng.standard_normal((int(lens.max()), H, D)))
+    for st, n in zip(streams, lens):
+        for layer in range(L):
+            st.write_rows(layer, 0, 0, vals=rows[:n])
+            st.write_rows(layer, 1, 0, vals=rows[:n][::-1].copy())
+        st.advance(int(n))
+    W = [oracle.LayerWeights(**w) for w in weights]
+    x0 = bf16_np(rng.standard_normal((len(lens), 1, DM)))
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        x = x0
+        for layer in range(L):
+            x = oracle.layer_step(streams, layer, W[layer], x)
+        oracle.batch_commit(streams)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or steps >= 64:
+            break
+    return {"value": round(len(lens) * steps / el, 1), "unit": "frames/s", "cores": oracle.threads(), "kind": "port",
+            "sample": f"{len(lens)} streams x {L} layers x {steps} steps of the same workload (bf16, lengths from "
+                      f"the same U[1,1500] draw, the same q8 weights), {el:.1f} s"}
+
+
+def run_step(args, xnp, torch):
+    dev = torch.device("cuda:0")
+    S, L = args.step_streams, args.layers
+    rng = np.random.default_rng(SEED + 5)
+    lens = rng.integers(1, args.step_max_len + 1, S)
+    total_steps = args.warmup + args.steps
+    cap = args.step_max_len + total_steps + 1
+    mbps = (cap + 15) // 16
+    nblocks = int(sum((n + total_steps + 16) // 16 + 1 for n in lens)) + 16
+    pool = xnp.KvPool(num_layers=L, num_heads=H, num_blocks=nblocks, max_streams=S, max_blocks_per_stream=mbps,
+                      cache_dtype="bf16", act_dtype="bf16", max_pos=cap + 16, page_seed=SEED + 6)
+    ids = [pool.init_state(cap) for _ in range(S)]
+    gen = torch.Generator(device=dev).manual_seed(SEED + 7)
+    maxn = int(lens.max())
+    for layer in range(L):
+        for kvi in (0, 1):
+            rows = torch.randn((maxn, H, D), generator=gen, device=dev).to(torch.bfloat16)
+            for sid, n in zip(ids, lens):
+                if layer == 0 and kvi == 0:
+                    pool.advance(sid, int(n))
+                pool.write_rows(sid, layer, kvi, 0, rows[:n])
+    wnp = step_weights(np.random.default_rng(SEED + 8), L)
+    W = []
+    for w in wnp:
+        d = {k: torch.from_numpy(v).to(dev) for k, v in w.items()}
+        W.append(xnp.LayerWeights(**d))
+    x0 = torch.randn((S, 1, DM), generator=gen, device=dev).to(torch.bfloat16)
+    x = torch.empty_like(x0)
+    ws = torch.empty(pool.layer_workspace(S, DM, FF), dtype=torch.uint8, device=dev)
+    torch.cuda.synchronize()
+    cur = lens.copy()
+    bytes_timed = [0]
+
+    def step(events):
+        if events is not None:
+            bytes_timed[0] += L * decode_bytes(cur)
+        x.copy_(x0)  # the step's input rows (synthetic; the model's would come from its embeddings)
+        pool.begin(ids)
+        for layer in range(L):
+            if events is not None:
+                pool.time_next(events[layer][0], events[layer][1])
+            pool.layer_step(layer, W[layer], x, ws)
+        pool.end()
+        cur[:] += 1
+
+    ms, kern = timed_steps(step, args.steps, args.warmup, L)
+    avg_ms = float(kern.mean())
+    bytes_per_launch = bytes_timed[0] / (args.steps * L)
+    achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
+    fps = S / (ms / 1000.0)
+    rest_ms = ms / L - avg_ms  # per layer: norms, projections, plan, launch gaps
+    flops = gemm_flops(S)
+    cpu = None if args.no_cpu else cpu_step(L, lens, wnp, args.cpu_seconds)
+    config = {"workload": f"full per-frame flow-LM layer step: {S} streams, Phonon-40m layers ({L} x {DM} wide, "
+                          f"{H} heads x {D}, FF {FF}), int8 per-channel q8 projections (QKV, out, FF) on MFMA, "
+                          f"LayerNorm, erf GELU, residuals, RoPE, paged bf16 KV append and decode attention, cache "
+                          f"length U[1,{args.step_max_len}]",
+              "streams": S, "layers": L, "d_model": DM, "ff": FF}
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "k_decode<bf16> (fused append + RoPE + decode), one launch per layer",
+            "avg_kernel_us": round(avg_ms * 1000.0, 2), "bytes_per_launch": int(bytes_per_launch),
+            "rest_of_layer_us": round(rest_ms * 1000.0, 2), "gemm_gop_per_layer": round(flops / 1e9, 2),
+            "gemm_tops_upper_bound": round(flops / (rest_ms * 1e-3) / 1e12, 2)}
+    return line("frames/sec, full per-frame layer step at 2048 streams; decode-attn HBM GB/s % peak", fps,
+                "frames/s", args, ms, "bf16", config, roof, cpu, extra={"audio_sec_per_sec": round(fps * 0.08, 1)})
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=["decode", "prefill", "window"], default="decode")
+    ap.add_argument("--workload", choices=["decode", "prefill", "window", "step"], default="decode")
+    ap.add_argument("--step-streams", type=int, default=2048)
+    ap.add_argument("--step-max-len", type=int, default=1500)
     ap.add_argument("--streams", type=int, default=1024)
     ap.add_argument("--layers", type=int, default=9)
     ap.add_argument("--max-len", type=int, default=1024)
@@ -452,7 +581,7 @@ def main():
     import torch
     xnp = _load("xn_ptts_amd", os.path.join(ROOT, "xn-ptts_amd"))
     xnp.load_library()
-    run = {"decode": run_decode, "prefill": run_prefill, "window": run_window}[args.workload]
+    run = {"decode": run_decode, "prefill": run_prefill, "window": run_window, "step": run_step}[args.workload]
     print(json.dumps(run(args, xnp, torch)))
 
 

@@ -214,6 +214,57 @@ xnp_status xnp_pool_check_tables(xnp_pool *pool, int32_t *mismatches, void *hip_
  * and ends (hipExtLaunchKernel), so that the kernel alone is timed.  Applies to one launch. */
 xnp_status xnp_pool_time_next(xnp_pool *pool, void *start_event, void *stop_event);
 
+/* ---- the rest of a flow-LM layer (transformer.rs:591-634) --------------------------------- */
+/* The layer around the attention: norm1 -> in_proj -> attention -> out_proj -> residual, norm2 ->
+ * linear1 -> gelu -> linear2 -> residual (StreamingTransformerLayer::forward, transformer.rs:591-634),
+ * for every row of an open batch at once.  Activations are bf16; the projections are linears
+ * without bias (Q::linear_load, transformer.rs:163-164, 549-550) whose weights are int8 with one
+ * f32 scale per output channel, multiplied on MFMA.  All pointers are device memory. */
+typedef enum xnp_gelu { XNP_GELU_ERF = 0, XNP_GELU_TANH = 1 } xnp_gelu; /* Gelu, transformer.rs:615-618 */
+
+typedef struct xnp_layer_weights {
+    int32_t d_model;      /* a multiple of 512, at most 2048 */
+    int32_t ff;           /* dim_feedforward, a multiple of 64 */
+    int32_t gelu;         /* xnp_gelu */
+    const int8_t *wqkv;   /* in_proj  [(H + 2 KVH) D][d_model]: q rows, then k, then v */
+    const float *sqkv;    /*          [(H + 2 KVH) D] */
+    const int8_t *wout;   /* out_proj [d_model][H D] */
+    const float *sout;
+    const int8_t *w1;     /* linear1  [ff][d_model] */
+    const float *s1;
+    const int8_t *w2;     /* linear2  [d_model][ff] */
+    const float *s2;
+    const float *ln1_w, *ln1_b, *ln2_w, *ln2_b; /* norm1, norm2 [d_model], eps 1e-5 */
+    const float *ls1, *ls2;                     /* layer_scale_1/2 [d_model] (layer_scale.rs), or NULL */
+} xnp_layer_weights;
+
+/* Device bytes of scratch xnp_layer_step needs for `rows` rows (n streams x t rows of a batch). */
+xnp_status xnp_layer_workspace(const xnp_pool *pool, int32_t rows, int32_t d_model, int32_t ff,
+                               uint64_t *bytes);
+/* One layer for the open batch: x [n][t][d_model] bf16 (the residual stream, updated in place),
+ * appending each row's k and v into the pages and attending as xnp_attend does (decode for
+ * t == 1, prompt prefill for t > 1).  `workspace` holds at least xnp_layer_workspace bytes; the
+ * call allocates nothing. */
+xnp_status xnp_layer_step(xnp_pool *pool, int32_t layer, const xnp_layer_weights *w, void *x,
+                          void *workspace, uint64_t workspace_bytes, void *hip_stream);
+
+/* The pieces, on caller buffers (the current HIP device):
+ * LayerNorm of rows of `dim` bf16 values (dim a multiple of 512, at most 2048). */
+xnp_status xnp_layer_norm(const void *x, int32_t rows, int32_t dim, const float *w, const float *b,
+                          float eps, void *out, void *hip_stream);
+/* y = epilogue(s[j] * sum_k x[m][k] w[j][k]) for x [rows][k] bf16, w [n][k] int8, s [n] f32; n a
+ * multiple of 64, k of 64.  The product is rounded to bf16, then XNP_EPI_STORE writes it to
+ * y [rows][n], XNP_EPI_GELU_ERF / _TANH write gelu of it, XNP_EPI_RESIDUAL adds it (times ls[j],
+ * rounded, when ls is not NULL) into y and rounds. */
+typedef enum xnp_epilogue {
+    XNP_EPI_STORE = 0, XNP_EPI_GELU_ERF = 1, XNP_EPI_GELU_TANH = 2, XNP_EPI_RESIDUAL = 3
+} xnp_epilogue;
+xnp_status xnp_linear_q8(const void *x, int32_t rows, int32_t k, const int8_t *w, const float *s,
+                         int32_t n, int32_t epilogue, void *y, const float *ls, void *hip_stream);
+/* Per-row int8 weights on the host: s[r] = max |w[r][.]| / 127, q = rint(w / s) clamped to
+ * +-127 (an all-zero row gets s = 0, q = 0). */
+xnp_status xnp_quantize_rows(const float *w, int32_t rows, int32_t cols, int8_t *q, float *scales);
+
 /* ---- budgets (plan.rs:25, 43-54) --------------------------------------------------------- */
 int32_t xnp_frame_budget(int32_t num_tokens, double frame_rate);
 int32_t xnp_seq_budget(int32_t num_tokens, int32_t frame_budget);

@@ -579,6 +579,112 @@ int orc_write_rows(orc_stream *st, int layer, int kv, int slot0, int n, const fl
 }
 
 /* ---------------------------------------------------------------------------------------- */
+/* the rest of the layer: transformer.rs:591-634                                            */
+
+void orc_layer_norm(const float *x, int rows, int dim, const float *w, const float *b, float eps,
+                    int act_dtype, float *out) {
+    for (int r = 0; r < rows; r++) {
+        const float *xr = x + (size_t)r * dim;
+        float sum = 0.f;
+        for (int i = 0; i < dim; i++) sum += xr[i];
+        const float mean = sum / (float)dim;
+        float sq = 0.f;
+        for (int i = 0; i < dim; i++) {
+            float d = xr[i] - mean;
+            sq += d * d;
+        }
+        const float rstd = 1.0f / sqrtf(sq / (float)dim + eps);
+        float *o = out + (size_t)r * dim;
+        for (int i = 0; i < dim; i++) {
+            float y = (xr[i] - mean) * rstd;
+            o[i] = round_act(y * w[i] + b[i], act_dtype);
+        }
+    }
+}
+
+void orc_quantize_rows(const float *w, int rows, int cols, int8_t *q, float *scales) {
+    for (int r = 0; r < rows; r++) {
+        const float *wr = w + (size_t)r * cols;
+        float amax = 0.f;
+        for (int i = 0; i < cols; i++) amax = fmaxf(amax, fabsf(wr[i]));
+        const float s = amax / 127.0f;
+        scales[r] = s;
+        for (int i = 0; i < cols; i++) q[(size_t)r * cols + i] = orc_quant(wr[i], s);
+    }
+}
+
+void orc_linear_q8(const float *x, int rows, int k, const int8_t *q, const float *s, int n,
+                   int act_dtype, float *y) {
+    for (int m = 0; m < rows; m++)
+        for (int j = 0; j < n; j++) {
+            const float *xr = x + (size_t)m * k;
+            const int8_t *qr = q + (size_t)j * k;
+            float acc = 0.f;
+            for (int i = 0; i < k; i++) acc += xr[i] * (float)qr[i];
+            y[(size_t)m * n + j] = round_act(s[j] * acc, act_dtype);
+        }
+}
+
+float orc_gelu(float x, int kind) {
+    if (kind == 1) {
+        const float c = 0.7978845608028654f; /* sqrt(2 / pi) */
+        return 0.5f * x * (1.0f + tanhf(c * (x + 0.044715f * x * x * x)));
+    }
+    return 0.5f * x * (1.0f + erff(x * 0.7071067811865476f));
+}
+
+static int layer_step_one(orc_stream *st, int t, int layer, const orc_layer_weights *w, float scale,
+                          float *x) {
+    const int dm = w->d_model, H = st->H, KVH = st->KVH, D = st->D, adt = st->adt;
+    const int qd = H * D, kd = KVH * D, nqkv = qd + 2 * kd;
+    float *h = malloc(sizeof(float) * (size_t)t * dm);
+    float *qkv = malloc(sizeof(float) * (size_t)t * nqkv);
+    float *q = malloc(sizeof(float) * (size_t)t * qd);
+    float *k = malloc(sizeof(float) * (size_t)t * kd);
+    float *v = malloc(sizeof(float) * (size_t)t * kd);
+    float *att = malloc(sizeof(float) * (size_t)t * qd);
+    float *y = malloc(sizeof(float) * (size_t)t * dm);
+    float *f = malloc(sizeof(float) * (size_t)t * w->ff);
+    /* self-attention block: x + layer_scale_1(attn(norm1(x))) */
+    orc_layer_norm(x, t, dm, w->ln1_w, w->ln1_b, 1e-5f, adt, h);
+    orc_linear_q8(h, t, dm, w->wqkv, w->sqkv, nqkv, adt, qkv);
+    for (int i = 0; i < t; i++) { /* narrow into q, k, v (transformer.rs:195-211) */
+        memcpy(q + (size_t)i * qd, qkv + (size_t)i * nqkv, sizeof(float) * qd);
+        memcpy(k + (size_t)i * kd, qkv + (size_t)i * nqkv + qd, sizeof(float) * kd);
+        memcpy(v + (size_t)i * kd, qkv + (size_t)i * nqkv + qd + kd, sizeof(float) * kd);
+    }
+    int rc = orc_attend(st, layer, t, q, k, v, scale, att, NULL);
+    if (rc == 0) {
+        orc_linear_q8(att, t, qd, w->wout, w->sout, dm, adt, y);
+        for (size_t i = 0; i < (size_t)t * dm; i++) {
+            float a = w->ls1 ? round_act(y[i] * w->ls1[i % dm], adt) : y[i];
+            x[i] = round_act(x[i] + a, adt);
+        }
+        /* feed-forward block: x + layer_scale_2(linear2(gelu(linear1(norm2(x))))) */
+        orc_layer_norm(x, t, dm, w->ln2_w, w->ln2_b, 1e-5f, adt, h);
+        orc_linear_q8(h, t, dm, w->w1, w->s1, w->ff, adt, f);
+        for (size_t i = 0; i < (size_t)t * w->ff; i++) f[i] = round_act(orc_gelu(f[i], w->gelu), adt);
+        orc_linear_q8(f, t, w->ff, w->w2, w->s2, dm, adt, y);
+        for (size_t i = 0; i < (size_t)t * dm; i++) {
+            float a = w->ls2 ? round_act(y[i] * w->ls2[i % dm], adt) : y[i];
+            x[i] = round_act(x[i] + a, adt);
+        }
+    }
+    free(h); free(qkv); free(q); free(k); free(v); free(att); free(y); free(f);
+    return rc;
+}
+
+int orc_layer_step(orc_stream **streams, int n, int t, int layer, const orc_layer_weights *w,
+                   float scale, float *x) {
+    if (n <= 0) return 0;
+    int bad = 0;
+#pragma omp parallel for schedule(dynamic, 1) reduction(| : bad)
+    for (int i = 0; i < n; i++)
+        bad |= layer_step_one(streams[i], t, layer, w, scale, x + (size_t)i * t * w->d_model) != 0;
+    return bad ? fail("a stream refused the step") : 0;
+}
+
+/* ---------------------------------------------------------------------------------------- */
 /* batched CPU step (the CPU baseline): one thread per stream, OpenMP across streams        */
 
 int orc_batch_attend(orc_stream **streams, int n, int layer, const float *q, const float *k,

@@ -96,6 +96,40 @@ int orc_read_rows(const orc_stream *st, int layer, int kv, int slot0, int n, flo
 int orc_write_rows(orc_stream *st, int layer, int kv, int slot0, int n, const float *vals,
                    const int8_t *q8, const float *scales);
 
+/* --- the rest of a flow-LM transformer layer (transformer.rs:591-634) ------------------------ */
+/* LayerNorm over the last dimension, as norm1/norm2 (transformer.rs:547-548, eps 1e-5): per row,
+ * mean and biased variance in f32 (ascending sums), then (x - mean) * (1 / sqrt(var + eps)) * w + b,
+ * rounded to act_dtype.  x and out [rows][dim] may alias. */
+void orc_layer_norm(const float *x, int rows, int dim, const float *w, const float *b, float eps,
+                    int act_dtype, float *out);
+/* Per-row int8 weights, the quantization this build defines for the projections: s = amax / 127
+ * (0 for an all-zero row), q = rint(w / s) clamped to [-127, 127]. */
+void orc_quantize_rows(const float *w, int rows, int cols, int8_t *q, float *scales);
+/* y[m][j] = round_act(s[j] * sum_k x[m][k] * q[j][k]), the sum in f32 with k ascending:
+ * a q8 linear without bias (the flow LM's in_proj, out_proj, linear1, linear2). */
+void orc_linear_q8(const float *x, int rows, int k, const int8_t *q, const float *s, int n,
+                   int act_dtype, float *y);
+/* GELU: kind 0 erf (0.5 x (1 + erf(x / sqrt 2))), kind 1 tanh approximation. */
+float orc_gelu(float x, int kind);
+
+typedef struct orc_layer_weights {
+    int d_model, ff, gelu;                  /* gelu: 0 erf, 1 tanh */
+    const int8_t *wqkv; const float *sqkv; /* [(H + 2 KVH) D][d_model] */
+    const int8_t *wout; const float *sout; /* [d_model][H D] */
+    const int8_t *w1; const float *s1;     /* [ff][d_model] */
+    const int8_t *w2; const float *s2;     /* [d_model][ff] */
+    const float *ln1_w, *ln1_b, *ln2_w, *ln2_b; /* [d_model] */
+    const float *ls1, *ls2;                 /* [d_model] layer scales (layer_scale.rs), or NULL */
+} orc_layer_weights;
+
+/* One layer of StreamingTransformerLayer::forward (transformer.rs:591-634) for t rows of each of
+ * n streams (OpenMP across streams): x [n][t][d_model] holds activation values and is updated in
+ * place.  norm1 -> in_proj -> split q/k/v (transformer.rs:195-211) -> orc_attend -> out_proj ->
+ * layer scale -> residual; norm2 -> linear1 -> gelu -> linear2 -> layer scale -> residual.  Every
+ * tensor is rounded to the activation dtype as it is produced.  The streams are not committed. */
+int orc_layer_step(orc_stream **streams, int n, int t, int layer, const orc_layer_weights *w,
+                   float scale, float *x);
+
 /* Many streams, one layer: the CPU baseline's batched step (OpenMP over streams). */
 int orc_batch_attend(orc_stream **streams, int n, int layer, const float *q, const float *k,
                      const float *v, float scale, float *out);

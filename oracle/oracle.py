@@ -61,6 +61,12 @@ def lib():
                                                 _fp, _fp, _fp, ctypes.c_float, _fp]),
             "orc_batch_commit": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int]),
             "orc_threads": (ctypes.c_int, []),
+            "orc_layer_norm": (None, [_fp, ctypes.c_int, ctypes.c_int, _fp, _fp, ctypes.c_float, ctypes.c_int, _fp]),
+            "orc_quantize_rows": (None, [_fp, ctypes.c_int, ctypes.c_int, _i8p, _fp]),
+            "orc_linear_q8": (None, [_fp, ctypes.c_int, ctypes.c_int, _i8p, _fp, ctypes.c_int, ctypes.c_int, _fp]),
+            "orc_gelu": (ctypes.c_float, [ctypes.c_float, ctypes.c_int]),
+            "orc_layer_step": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int, ctypes.c_int,
+                                              ctypes.c_int, ctypes.c_void_p, ctypes.c_float, _fp]),
             "orc_last_error": (ctypes.c_char_p, []),
         }
         for name, (res, args) in sig.items():
@@ -231,5 +237,89 @@ def batch_commit(streams):
     _ok(lib().orc_batch_commit(arr, n))
 
 
+def batch_commit_t(streams, t):
+    """Commit t rows on every stream (a prompt step)."""
+    for st in streams:
+        st.commit(t)
+
+
 def threads() -> int:
     return lib().orc_threads()
+
+
+# ---- the rest of the layer (transformer.rs:591-634) ------------------------------------------------
+def layer_norm(x, w, b, eps=1e-5, act="f32"):
+    x, xp = _f32(x)
+    out = np.zeros_like(x)
+    w, wp = _f32(w)
+    b, bp = _f32(b)
+    dim = x.shape[-1]
+    lib().orc_layer_norm(xp, x.size // dim, dim, wp, bp, eps, DT[act], out.ctypes.data_as(_fp))
+    return out
+
+
+def quantize_rows(w):
+    """Per-row int8 weights: (q [rows][cols] int8, scales [rows] f32)."""
+    w, wp = _f32(w)
+    q = np.zeros(w.shape, np.int8)
+    s = np.zeros(w.shape[0], np.float32)
+    lib().orc_quantize_rows(wp, w.shape[0], w.shape[1], q.ctypes.data_as(_i8p), s.ctypes.data_as(_fp))
+    return q, s
+
+
+def linear_q8(x, q, s, act="f32"):
+    x, xp = _f32(x)
+    q = np.ascontiguousarray(q, np.int8)
+    s, sp = _f32(s)
+    k = x.shape[-1]
+    rows = x.size // k
+    y = np.zeros(x.shape[:-1] + (q.shape[0],), np.float32)
+    lib().orc_linear_q8(xp, rows, k, q.ctypes.data_as(_i8p), sp, q.shape[0], DT[act], y.ctypes.data_as(_fp))
+    return y
+
+
+def gelu(x: float, kind: str = "erf") -> float:
+    return lib().orc_gelu(x, 0 if kind == "erf" else 1)
+
+
+class _LayerWeightsC(ctypes.Structure):
+    _fields_ = [("d_model", ctypes.c_int), ("ff", ctypes.c_int), ("gelu", ctypes.c_int),
+                ("wqkv", _i8p), ("sqkv", _fp), ("wout", _i8p), ("sout", _fp),
+                ("w1", _i8p), ("s1", _fp), ("w2", _i8p), ("s2", _fp),
+                ("ln1_w", _fp), ("ln1_b", _fp), ("ln2_w", _fp), ("ln2_b", _fp),
+                ("ls1", _fp), ("ls2", _fp)]
+
+
+class LayerWeights:
+    """One layer's q8 projections, norms and optional layer scales, as numpy arrays."""
+
+    def __init__(self, wqkv, sqkv, wout, sout, w1, s1, w2, s2, ln1_w, ln1_b, ln2_w, ln2_b,
+                 ls1=None, ls2=None, gelu="erf"):
+        i8 = lambda a: np.ascontiguousarray(a, np.int8)
+        f = lambda a: None if a is None else np.ascontiguousarray(a, np.float32)
+        self.wqkv, self.wout, self.w1, self.w2 = i8(wqkv), i8(wout), i8(w1), i8(w2)
+        self.sqkv, self.sout, self.s1, self.s2 = f(sqkv), f(sout), f(s1), f(s2)
+        self.ln1_w, self.ln1_b, self.ln2_w, self.ln2_b = f(ln1_w), f(ln1_b), f(ln2_w), f(ln2_b)
+        self.ls1, self.ls2 = f(ls1), f(ls2)
+        self.gelu = gelu
+        self.d_model = self.wout.shape[0]
+        self.ff = self.w1.shape[0]
+
+    def c(self):
+        P = lambda a, t: a.ctypes.data_as(t) if a is not None else ctypes.cast(None, t)
+        return _LayerWeightsC(self.d_model, self.ff, 0 if self.gelu == "erf" else 1,
+                              P(self.wqkv, _i8p), P(self.sqkv, _fp), P(self.wout, _i8p), P(self.sout, _fp),
+                              P(self.w1, _i8p), P(self.s1, _fp), P(self.w2, _i8p), P(self.s2, _fp),
+                              P(self.ln1_w, _fp), P(self.ln1_b, _fp), P(self.ln2_w, _fp), P(self.ln2_b, _fp),
+                              P(self.ls1, _fp), P(self.ls2, _fp))
+
+
+def layer_step(streams, layer, weights: LayerWeights, x, scale=0.125):
+    """One transformer layer on t rows of each stream: x [n][t][d_model] -> the updated x."""
+    x = np.array(x, np.float32, copy=True, order="C")
+    n, t = x.shape[0], x.shape[1]
+    arr = (ctypes.c_void_p * n)(*[s_.h for s_ in streams])
+    cw = weights.c()
+    _ok(lib().orc_layer_step(arr, n, t, layer, ctypes.cast(ctypes.pointer(cw), ctypes.c_void_p), scale,
+                             x.ctypes.data_as(_fp)))
+    return x

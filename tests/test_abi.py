@@ -299,3 +299,27 @@ def test_table_patches_of_reopened_streams_leave_the_live_pages():
     p.close(ids[1])
     p.advance(a, 20)
     assert p.check_tables() == 0
+
+
+def test_quantize_rows_is_the_oracles_bit_for_bit():
+    # a host function of the library: no GPU needed
+    rng = np.random.default_rng(70)
+    w = rng.standard_normal((40, 200)).astype(np.float32) * 0.05
+    w[7] = 0.0
+    q, s = xnp.quantize_rows(w)
+    oq, os_ = oracle.quantize_rows(w)
+    assert np.array_equal(q, oq) and np.array_equal(s.view(np.uint32), os_.view(np.uint32))
+
+
+def test_layer_calls_refuse_bad_shapes_without_running_a_kernel():
+    lib = xnp.load_library()
+    assert lib.xnp_linear_q8(None, 4, 100, None, None, 64, 0, None, None, None) == 1  # k not a multiple of 64
+    assert lib.xnp_linear_q8(None, 4, 64, None, None, 64, 9, None, None, None) == 1   # no such epilogue
+    assert lib.xnp_layer_norm(None, 4, 300, None, None, 1e-5, None, None) == 1        # dim not a multiple of 512
+    pool = xnp.KvPool(num_layers=1, num_heads=8, num_blocks=8, max_streams=2, max_blocks_per_stream=4,
+                      host_only=True)
+    w = xnp.kv.LayerWeightsC()
+    assert lib.xnp_layer_step(pool._h, 0, ctypes.byref(w), None, None, 0, None) == 1  # null x
+    x = ctypes.c_uint16()
+    assert lib.xnp_layer_step(pool._h, 0, ctypes.byref(w), ctypes.byref(x), None, 0, None) == 9  # no batch open
+    assert pool.layer_workspace(2048, 512, 2048) >= 2048 * (512 * 5 + 2048) * 2

@@ -1,0 +1,144 @@
+"""GPU parity of the rest of the flow-LM layer (transformer.rs:591-634): LayerNorm, the q8
+projections and a whole layer step, through the C ABI, against the oracle on the same inputs.
+
+Bars: 2e-2 relative (bf16 activations; relative error per row as in tests/helpers.py:rel_err).
+Cache rows written by a layer step come from projections the GPU sums in its own order, so they
+are compared within the same bar rather than bit for bit (the append's own bit-exactness is pinned
+in test_gpu_parity.py with identical inputs).
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import oracle, xnp
+from helpers import bf16_round, normal, rel_err
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+TOL = 2e-2
+
+
+def dev(a, dtype=torch.bfloat16):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV).to(dtype)
+
+
+def host(t):
+    return t.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("rows,dim", [(1, 512), (37, 512), (130, 1024), (9, 2048)])
+def test_layer_norm_matches_the_oracle(rows, dim):
+    rng = np.random.default_rng(50 + rows)
+    x = normal(rng, (rows, dim), "bf16") * 3 + 0.5
+    x = bf16_round(x)
+    w = (1 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(dim)).astype(np.float32)
+    out = torch.empty((rows, dim), dtype=torch.bfloat16, device=DEV)
+    xnp.layer_norm(dev(x), dev(w, torch.float32), dev(b, torch.float32), out)
+    torch.cuda.synchronize()
+    assert rel_err(host(out), oracle.layer_norm(x, w, b, act="bf16")) <= TOL
+
+
+@pytest.mark.parametrize("rows,k,n", [(1, 512, 64), (37, 512, 1536), (200, 512, 2048), (70, 2048, 512)])
+@pytest.mark.parametrize("epi", ["store", "gelu_erf", "gelu_tanh", "residual"])
+def test_linear_q8_matches_the_oracle(rows, k, n, epi):
+    rng = np.random.default_rng(rows * 7 + n)
+    x = normal(rng, (rows, k), "bf16")
+    q, s = xnp.quantize_rows(rng.standard_normal((n, k)).astype(np.float32) * 0.02)
+    y0 = normal(rng, (rows, n), "bf16")
+    y = dev(y0)
+    ls = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32) if epi == "residual" else None
+    xnp.linear_q8(dev(x), dev(q, torch.int8), dev(s, torch.float32), y, epi,
+                  ls=dev(ls, torch.float32) if ls is not None else None)
+    torch.cuda.synchronize()
+    want = oracle.linear_q8(x, q, s, "bf16")
+    if epi.startswith("gelu"):
+        kind = epi.split("_")[1]
+        want = bf16_round(np.vectorize(lambda v: oracle.gelu(float(v), kind))(want).astype(np.float32))
+    elif epi == "residual":
+        want = bf16_round(y0 + bf16_round(want * ls[None, :]))
+    assert rel_err(host(y), want) <= TOL, epi
+
+
+def test_quantize_rows_matches_the_oracle_bit_for_bit():
+    rng = np.random.default_rng(60)
+    w = rng.standard_normal((70, 300)).astype(np.float32) * 0.02
+    w[3] = 0
+    q, s = xnp.quantize_rows(w)
+    oq, os_ = oracle.quantize_rows(w)
+    assert np.array_equal(q, oq) and np.array_equal(s.view(np.uint32), os_.view(np.uint32))
+
+
+def make_weights(rng, H=8, KVH=8, D=64, dm=512, ff=2048, ls=False):
+    qr = lambda n, k: xnp.quantize_rows(rng.standard_normal((n, k)).astype(np.float32) * 0.02)
+    parts = dict(zip(["wqkv", "sqkv"], qr((H + 2 * KVH) * D, dm)))
+    parts.update(zip(["wout", "sout"], qr(dm, H * D)))
+    parts.update(zip(["w1", "s1"], qr(ff, dm)))
+    parts.update(zip(["w2", "s2"], qr(dm, ff)))
+    for n in ("ln1", "ln2"):
+        parts[n + "_w"] = (1 + 0.1 * rng.standard_normal(dm)).astype(np.float32)
+        parts[n + "_b"] = (0.1 * rng.standard_normal(dm)).astype(np.float32)
+    parts["ls1"] = (0.5 + 0.1 * rng.standard_normal(dm)).astype(np.float32) if ls else None
+    parts["ls2"] = (0.5 + 0.1 * rng.standard_normal(dm)).astype(np.float32) if ls else None
+    orc = oracle.LayerWeights(**parts)
+    d = {k_: (dev(v, torch.int8 if v.dtype == np.int8 else torch.float32) if v is not None else None)
+         for k_, v in parts.items()}
+    return orc, xnp.LayerWeights(**d)
+
+
+@pytest.mark.parametrize("cache,KVH,ls", [("bf16", 8, False), ("bf16", 2, True), ("i8", 8, False)])
+def test_layer_steps_match_the_oracle(cache, KVH, ls):
+    # 5 streams with prior caches of 0..40 rows; a 7-row prompt on all, then 3 single-row steps,
+    # through 2 layers each
+    rng = np.random.default_rng(61 + KVH)
+    L, H, D, dm, ff = 2, 8, 64, 512, 1024
+    W = [make_weights(rng, H=H, KVH=KVH, ff=ff, ls=ls) for _ in range(L)]
+    S, cap = 5, 96
+    pool = xnp.KvPool(num_layers=L, num_heads=H, num_kv_heads=KVH, num_blocks=S * 8 + 8, max_streams=S,
+                      max_blocks_per_stream=cap // 16, cache_dtype=cache, act_dtype="bf16", max_pos=256,
+                      page_seed=12)
+    ids = [pool.init_state(cap) for _ in range(S)]
+    sts = [oracle.Stream(L, H, D, cap, cache=cache, act="bf16", kv_heads=KVH) for _ in range(S)]
+    for i, n in enumerate([0, 5, 16, 40, 3]):
+        if n == 0:
+            continue
+        pool.begin([ids[i]], t=n)
+        for layer in range(L):
+            k, v = normal(rng, (n, KVH, D), "bf16"), normal(rng, (n, KVH, D), "bf16")
+            pool.append(layer, dev(k), dev(v))
+            sts[i].append(layer, k, v)
+        pool.end()
+        sts[i].commit(n)
+    ws = torch.empty(pool.layer_workspace(S * 7, dm, ff), dtype=torch.uint8, device=DEV)
+    for t in (7, 1, 1, 1):
+        x = normal(rng, (S, t, dm), "bf16")
+        xg = dev(x)
+        pool.begin(ids, t=t)
+        want = x
+        for layer in range(L):
+            pool.layer_step(layer, W[layer][1], xg, ws)
+            want = oracle.layer_step(sts, layer, W[layer][0], want)
+        pool.end()
+        torch.cuda.synchronize()
+        for st in sts:
+            st.commit(t)
+        got = host(xg)
+        for i in range(S):
+            assert rel_err(got[i], want[i]) <= TOL, (t, i)
+    # the cache rows the steps wrote, within the same bar
+    for i in range(S):
+        n = sts[i].current_end
+        for layer in range(L):
+            for kv in (0, 1):
+                rows = torch.empty((n, H, D), dtype=torch.bfloat16 if cache == "bf16" else torch.int8, device=DEV)
+                nb = (n + 15) // 16
+                sc = torch.zeros((nb, H), dtype=torch.float32, device=DEV)
+                pool.read_rows(ids[i], layer, kv, 0, rows, sc if cache == "i8" else None)
+                torch.cuda.synchronize()
+                vals, _, _ = sts[i].read_rows(layer, kv, 0, n)
+                if cache == "i8":
+                    got_rows = rows.float().cpu().numpy() * np.repeat(sc.cpu().numpy(), 16, axis=0)[:n, :, None]
+                    bar = 6e-2  # one int8 step of a row whose scale came from slightly different inputs
+                else:
+                    got_rows, bar = host(rows), TOL
+                assert rel_err(got_rows, vals) <= bar, (i, layer, kv)

@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from conftest import oracle
-from helpers import bf16_round, lcg, rel_err
+from helpers import bf16_round, lcg, normal, rel_err
 
 THETA = 10000.0
 
@@ -375,3 +375,121 @@ def test_int8_rows_quantize_within_half_a_step():
     vals, q8, scales = st2.read_rows(0, 1, 0, 1)
     assert scales[0, 0] == np.float32(3.0) / np.float32(127.0)
     assert q8[0, 0, -1] == 127 and np.abs(vals[0, 0] - x[0, 0]).max() <= scales[0, 0] / 2 + 1e-7
+
+
+# ---- the rest of the layer (transformer.rs:591-634) -------------------------------------------
+def test_layer_norm_matches_torch():
+    # torch.nn.functional.layer_norm in f64 is the textbook definition (biased variance, eps inside
+    # the root, affine after); a constant row normalizes to the bias exactly.
+    rng = np.random.default_rng(40)
+    x = rng.standard_normal((7, 512)).astype(np.float32) * 3 + 1
+    w = rng.standard_normal(512).astype(np.float32)
+    b = rng.standard_normal(512).astype(np.float32)
+    got = oracle.layer_norm(x, w, b)
+    want = torch.nn.functional.layer_norm(torch.from_numpy(x).double(), (512,), torch.from_numpy(w).double(),
+                                          torch.from_numpy(b).double(), eps=1e-5).numpy()
+    assert rel_err(got, want) < 2e-6
+    const = oracle.layer_norm(np.full((2, 512), 4.25, np.float32), w, b)
+    assert np.array_equal(const, np.stack([b, b]))
+    got16 = oracle.layer_norm(x, w, b, act="bf16")
+    assert np.array_equal(got16, bf16_round(got))
+
+
+def test_quantize_rows_keeps_every_weight_within_half_a_step():
+    rng = np.random.default_rng(41)
+    w = rng.standard_normal((33, 100)).astype(np.float32) * 0.02
+    w[5] = 0.0
+    q, s = oracle.quantize_rows(w)
+    assert s[5] == 0 and not q[5].any()
+    live = np.arange(33) != 5
+    assert np.allclose(s[live], np.abs(w[live]).max(axis=1) / 127, rtol=1e-7)
+    assert (np.abs(q[live]).max(axis=1) == 127).all()
+    err = np.abs(w[live] - q[live].astype(np.float64) * s[live, None])
+    assert (err <= s[live, None] / 2 * (1 + 1e-6)).all()
+
+
+@pytest.mark.parametrize("act", ["f32", "bf16"])
+def test_linear_q8_is_the_matmul_with_the_dequantized_weights(act):
+    rng = np.random.default_rng(42)
+    x = normal(rng, (9, 512), act)
+    q, s = oracle.quantize_rows(rng.standard_normal((96, 512)).astype(np.float32) * 0.02)
+    got = oracle.linear_q8(x, q, s, act)
+    want = x.astype(np.float64) @ (q.astype(np.float64) * s[:, None].astype(np.float64)).T
+    assert rel_err(got, want) < (1e-5 if act == "f32" else 2 ** -8)
+
+
+@pytest.mark.parametrize("kind", ["erf", "tanh"])
+def test_gelu_matches_torch(kind):
+    x = np.linspace(-6, 6, 241, dtype=np.float32)
+    want = torch.nn.functional.gelu(torch.from_numpy(x).double(), approximate="none" if kind == "erf" else "tanh")
+    got = np.array([oracle.gelu(float(v), kind) for v in x])
+    assert np.abs(got - want.numpy()).max() < 2e-6
+
+
+def _torch_layer(x, hist, layer_w, pos, H, KVH, D, theta=THETA):
+    """The layer (transformer.rs:591-634) in torch f64 from library routines: layer_norm, matmul,
+    gelu, softmax; RoPE with the pinned rope rows; hist holds the rotated K and V rows so far."""
+    t64 = lambda a: torch.from_numpy(np.asarray(a, np.float64))
+    W = layer_w
+    deq = lambda q, s: t64(q) * t64(s)[:, None]
+    X = t64(x)
+    T = X.shape[0]
+    h = torch.nn.functional.layer_norm(X, (X.shape[1],), t64(W.ln1_w), t64(W.ln1_b), eps=1e-5)
+    qkv = h @ deq(W.wqkv, W.sqkv).T
+    q = qkv[:, :H * D].reshape(T, H, D)
+    k = qkv[:, H * D:H * D + KVH * D].reshape(T, KVH, D).repeat_interleave(H // KVH, dim=1)
+    v = qkv[:, H * D + KVH * D:].reshape(T, KVH, D).repeat_interleave(H // KVH, dim=1)
+
+    def rope(a, p):
+        c, s = oracle.rope_row(D, theta, float(p), "f32")
+        c, s = t64(c), t64(s)
+        out = a.clone()
+        out[..., 0::2] = a[..., 0::2] * c - a[..., 1::2] * s
+        out[..., 1::2] = a[..., 0::2] * s + a[..., 1::2] * c
+        return out
+
+    q = torch.stack([rope(q[i], pos + i) for i in range(T)])
+    k = torch.stack([rope(k[i], pos + i) for i in range(T)])
+    hist["k"] = torch.cat([hist["k"], k]) if "k" in hist else k
+    hist["v"] = torch.cat([hist["v"], v]) if "v" in hist else v
+    K, V = hist["k"], hist["v"]
+    n = K.shape[0]
+    att = torch.einsum("thd,nhd->thn", q, K) * (1.0 / math.sqrt(D))
+    causal = torch.arange(n)[None, :] <= (n - T + torch.arange(T))[:, None]
+    att = att.masked_fill(~causal[:, None, :], float("-inf")).softmax(-1)
+    o = torch.einsum("thn,nhd->thd", att, V).reshape(T, H * D)
+    X = X + o @ deq(W.wout, W.sout).T
+    h2 = torch.nn.functional.layer_norm(X, (X.shape[1],), t64(W.ln2_w), t64(W.ln2_b), eps=1e-5)
+    f = torch.nn.functional.gelu(h2 @ deq(W.w1, W.s1).T, approximate="none")
+    X = X + f @ deq(W.w2, W.s2).T
+    return X.numpy()
+
+
+def random_layer_weights(rng, d_model=512, H=8, KVH=8, D=64, ff=2048, std=0.02):
+    qr = lambda n, k: oracle.quantize_rows(rng.standard_normal((n, k)).astype(np.float32) * std)
+    wqkv, sqkv = qr((H + 2 * KVH) * D, d_model)
+    wout, sout = qr(d_model, H * D)
+    w1, s1 = qr(ff, d_model)
+    w2, s2 = qr(d_model, ff)
+    g = lambda: (1 + 0.1 * rng.standard_normal(d_model)).astype(np.float32)
+    b = lambda: (0.1 * rng.standard_normal(d_model)).astype(np.float32)
+    return oracle.LayerWeights(wqkv, sqkv, wout, sout, w1, s1, w2, s2, g(), b(), g(), b())
+
+
+@pytest.mark.parametrize("KVH", [8, 2])
+def test_layer_step_is_the_reference_layer(KVH):
+    # a 6-row prompt, then 3 single-row steps, on two streams; f32 activations and cache
+    rng = np.random.default_rng(43 + KVH)
+    H, D, dm = 8, 64, 512
+    W = random_layer_weights(rng, H=H, KVH=KVH, ff=1024)
+    sts = [oracle.Stream(1, H, D, 64, cache="f32", act="f32", kv_heads=KVH) for _ in range(2)]
+    hists = [{}, {}]
+    pos = 0
+    for t in (6, 1, 1, 1):
+        x = rng.standard_normal((2, t, dm)).astype(np.float32)
+        got = oracle.layer_step(sts, 0, W, x)
+        for i in range(2):
+            want = _torch_layer(x[i], hists[i], W, pos, H, KVH, D)
+            assert rel_err(got[i], want) < 2e-5, (t, i)
+        oracle.batch_commit_t(sts, t)
+        pos += t

@@ -4,8 +4,9 @@ The compute lives in libxnp_kv.so (hand-written HIP kernels for gfx950 behind th
 include/xnp_kv.h); this package is the Python binding over it.  The directory name has a hyphen,
 so load it by path, e.g. importlib.util.spec_from_file_location("xn_ptts_amd", <dir>/__init__.py).
 """
-from .kv import (BF16, BLOCK, DTYPES, F32, I8, LIB_PATH, RING_ABSOLUTE, RING_SHIFT, KvPool,
-                 XnpError, frame_budget, load_library, seq_budget)
+from .kv import (BF16, BLOCK, DTYPES, F32, I8, LIB_PATH, RING_ABSOLUTE, RING_SHIFT, KvPool, LayerWeights,
+                 XnpError, frame_budget, layer_norm, linear_q8, load_library, quantize_rows, seq_budget)
 
-__all__ = ["KvPool", "XnpError", "load_library", "frame_budget", "seq_budget", "LIB_PATH", "F32",
-           "BF16", "I8", "BLOCK", "DTYPES", "RING_SHIFT", "RING_ABSOLUTE"]
+__all__ = ["KvPool", "LayerWeights", "XnpError", "load_library", "frame_budget", "seq_budget", "layer_norm",
+           "linear_q8", "quantize_rows", "LIB_PATH", "F32", "BF16", "I8", "BLOCK", "DTYPES", "RING_SHIFT",
+           "RING_ABSOLUTE"]

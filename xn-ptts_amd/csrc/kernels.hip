@@ -988,4 +988,209 @@ hipError_t launch_prefill(const PoolView &pv, const BatchView &bv, int layer, co
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// the rest of the flow-LM layer (transformer.rs:591-634): LayerNorm, and the q8 projections as
+// MFMA GEMMs with per-channel int8 weights
+
+// LayerNorm over rows of `dim` bf16 values (norm1, norm2: transformer.rs:547-548): one wave per
+// row, each lane holding dim / 64 values; mean and biased variance in f32 (two passes over the
+// registers), y = (x - mean) * (1 / sqrt(var + eps)) * w + b, rounded to bf16.
+template <int CH>
+__global__ __launch_bounds__(256) void k_layer_norm(const uint16_t *x, int rows, int dim, const float *w,
+                                                    const float *b, float eps, uint16_t *out) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const uint16_t *xr = x + (size_t)row * dim;
+    float v[CH][8];
+    float sum = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const uint4 raw = *(const uint4 *)(xr + (c * 64 + lane) * 8);
+        const uint32_t *u = (const uint32_t *)&raw;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[c][2 * i] = bf16_value(u[i] & 0xffffu);
+            v[c][2 * i + 1] = bf16_value(u[i] >> 16);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sum += v[c][i];
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) sum += __shfl_xor(sum, o);
+    const float mean = sum / (float)dim;
+    float sq = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float d = v[c][i] - mean;
+            sq = __builtin_fmaf(d, d, sq);
+        }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) sq += __shfl_xor(sq, o);
+    const float rstd = 1.0f / __builtin_sqrtf(sq / (float)dim + eps);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int e0 = (c * 64 + lane) * 8;
+        const float4 w0 = *(const float4 *)(w + e0), w1 = *(const float4 *)(w + e0 + 4);
+        const float4 b0 = *(const float4 *)(b + e0), b1 = *(const float4 *)(b + e0 + 4);
+        const float ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+        uint32_t o4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float y0 = ((v[c][2 * i] - mean) * rstd) * ww[2 * i] + bb[2 * i];
+            const float y1 = ((v[c][2 * i + 1] - mean) * rstd) * ww[2 * i + 1] + bb[2 * i + 1];
+            o4[i] = pack_bf16(y0, y1);
+        }
+        *(uint4 *)(out + (size_t)row * dim + e0) = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+    }
+}
+
+hipError_t launch_layer_norm(const void *x, int rows, int dim, const float *w, const float *b, float eps, void *out,
+                             hipStream_t stream) {
+    if (rows <= 0) return hipSuccess;
+    const dim3 grid((rows + 3) / 4), block(256);
+    switch (dim / 512) {
+    case 1: hipLaunchKernelGGL(k_layer_norm<1>, grid, block, 0, stream, (const uint16_t *)x, rows, dim, w, b, eps, (uint16_t *)out); break;
+    case 2: hipLaunchKernelGGL(k_layer_norm<2>, grid, block, 0, stream, (const uint16_t *)x, rows, dim, w, b, eps, (uint16_t *)out); break;
+    case 3: hipLaunchKernelGGL(k_layer_norm<3>, grid, block, 0, stream, (const uint16_t *)x, rows, dim, w, b, eps, (uint16_t *)out); break;
+    case 4: hipLaunchKernelGGL(k_layer_norm<4>, grid, block, 0, stream, (const uint16_t *)x, rows, dim, w, b, eps, (uint16_t *)out); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// y = epilogue(s[n] * sum_k A[m][k] W[n][k]): A [M][K] bf16, W [N][K] int8 with one f32 scale per
+// output channel (row of W), the sum on v_mfma_f32_16x16x32_bf16 with W widened to bf16 exactly
+// (|q| <= 127).  One work group of 4 waves per 64 x 64 tile of y, each wave 32 x 32 (2 x 2 MFMA
+// tiles); K in chunks of 64 staged through LDS, double-buffered, the next chunk's loads in flight
+// while one is multiplied.  The product is rounded to bf16 (the projection's output tensor),
+// then: kStore writes it (column ranges may go to separate outputs: q, k and v), kGelu* write
+// gelu(y) rounded, kResidual adds y (times the layer scale, rounded, when given) into X and
+// rounds: X + layer_scale(linear(..)) as transformer.rs:612-633 does.
+constexpr int kGmT = 64;  // tile rows and columns
+constexpr int kGmK = 64;  // K chunk
+constexpr int kGmLd = 72; // LDS row length in bf16
+
+template <int EPI>
+__global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K, const int8_t *W, const float *s,
+                                                 int N, GemmOut go) {
+    __shared__ __attribute__((aligned(16))) uint16_t As[2][kGmT][kGmLd];
+    __shared__ __attribute__((aligned(16))) uint16_t Ws[2][kGmT][kGmLd];
+    const int ntn = N / kGmT;
+    const int m0 = (blockIdx.x / ntn) * kGmT, n0 = (blockIdx.x % ntn) * kGmT;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, l16 = lane & 15;
+    const int wm = w & 1, wn = w >> 1;
+
+    // staging: A rows a_r and a_r + 32, 8 bf16 at k 8 a_k; W row w_r, 16 int8 at k 16 w_k
+    const int a_r = tid >> 3, a_k = tid & 7, w_r = tid >> 2, w_k = tid & 3;
+    const int ar0 = min(m0 + a_r, M - 1), ar1 = min(m0 + a_r + 32, M - 1);
+    uint4 ra0, ra1, rw;
+    auto load = [&](int kc) {
+        const int k0 = kc * kGmK;
+        ra0 = *(const uint4 *)(A + (size_t)ar0 * K + k0 + 8 * a_k);
+        ra1 = *(const uint4 *)(A + (size_t)ar1 * K + k0 + 8 * a_k);
+        rw = *(const uint4 *)(W + (size_t)(n0 + w_r) * K + k0 + 16 * w_k);
+    };
+    auto store = [&](int buf) {
+        *(uint4 *)&As[buf][a_r][8 * a_k] = ra0;
+        *(uint4 *)&As[buf][a_r + 32][8 * a_k] = ra1;
+        const uint32_t *u = (const uint32_t *)&rw;
+        uint32_t p[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float q0 = (float)(int8_t)(u[i] & 0xffu), q1 = (float)(int8_t)((u[i] >> 8) & 0xffu);
+            const float q2 = (float)(int8_t)((u[i] >> 16) & 0xffu), q3 = (float)(int8_t)(u[i] >> 24);
+            p[2 * i] = pack_bf16(q0, q1);
+            p[2 * i + 1] = pack_bf16(q2, q3);
+        }
+        *(uint4 *)&Ws[buf][w_r][16 * w_k] = make_uint4(p[0], p[1], p[2], p[3]);
+        *(uint4 *)&Ws[buf][w_r][16 * w_k + 8] = make_uint4(p[4], p[5], p[6], p[7]);
+    };
+
+    f32x4_t acc[2][2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    const int nk = K / kGmK;
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int kc = 0; kc < nk; ++kc) {
+        const int buf = kc & 1;
+        if (kc + 1 < nk) load(kc + 1);
+#pragma unroll
+        for (int ks = 0; ks < kGmK / 32; ++ks) {
+            bf16x8_t a[2], bw[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                a[i] = as_bf16x8(*(const uint4 *)&As[buf][32 * wm + 16 * i + l16][32 * ks + 8 * g]);
+                bw[i] = as_bf16x8(*(const uint4 *)&Ws[buf][32 * wn + 16 * i + l16][32 * ks + 8 * g]);
+            }
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mi], bw[ni], acc[mi][ni], 0, 0, 0);
+        }
+        if (kc + 1 < nk) store(buf ^ 1); // its last readers finished before the previous barrier
+        __syncthreads();
+    }
+
+    // lane: column n0 + 32 wn + 16 ni + l16, rows m0 + 32 wm + 16 mi + 4 g + r
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+        const int n = n0 + 32 * wn + 16 * ni + l16;
+        const float sc = s[n];
+        int seg = 0;
+        if constexpr (EPI == kStore) {
+            if (go.nseg > 1 && n >= go.col0[1]) seg = (go.nseg > 2 && n >= go.col0[2]) ? 2 : 1;
+        }
+        const float lsn = (EPI == kResidual && go.ls) ? go.ls[n] : 1.f;
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + 32 * wm + 16 * mi + 4 * g + r;
+                if (m >= M) continue;
+                const float y = bf16_value(bf16_bits(acc[mi][ni][r] * sc));
+                if constexpr (EPI == kStore) {
+                    ((uint16_t *)go.out[seg])[(size_t)m * go.ld[seg] + (n - go.col0[seg])] = (uint16_t)bf16_bits(y);
+                } else if constexpr (EPI == kGeluErf || EPI == kGeluTanh) {
+                    float gv;
+                    if constexpr (EPI == kGeluErf) {
+                        gv = 0.5f * y * (1.0f + erff(y * 0.7071067811865476f));
+                    } else {
+                        const float c = 0.7978845608028654f;
+                        gv = 0.5f * y * (1.0f + tanhf(c * (y + 0.044715f * y * y * y)));
+                    }
+                    ((uint16_t *)go.out[0])[(size_t)m * go.ld[0] + n] = (uint16_t)bf16_bits(gv);
+                } else {
+                    const float a = go.ls ? bf16_value(bf16_bits(y * lsn)) : y;
+                    uint16_t *xp = (uint16_t *)go.out[0] + (size_t)m * go.ld[0] + n;
+                    *xp = (uint16_t)bf16_bits(bf16_value(*xp) + a);
+                }
+            }
+    }
+}
+
+hipError_t launch_gemm_q8(const void *A, int M, int K, const int8_t *W, const float *s, int N, int epi,
+                          const GemmOut &go, hipStream_t stream) {
+    if (M <= 0) return hipSuccess;
+    if (N % kGmT || K % kGmK) return hipErrorInvalidValue;
+    const dim3 grid((N / kGmT) * ((M + kGmT - 1) / kGmT)), block(256);
+    const uint16_t *a = (const uint16_t *)A;
+    switch (epi) {
+    case kStore: hipLaunchKernelGGL(k_gemm_q8<kStore>, grid, block, 0, stream, a, M, K, W, s, N, go); break;
+    case kGeluErf: hipLaunchKernelGGL(k_gemm_q8<kGeluErf>, grid, block, 0, stream, a, M, K, W, s, N, go); break;
+    case kGeluTanh: hipLaunchKernelGGL(k_gemm_q8<kGeluTanh>, grid, block, 0, stream, a, M, K, W, s, N, go); break;
+    case kResidual: hipLaunchKernelGGL(k_gemm_q8<kResidual>, grid, block, 0, stream, a, M, K, W, s, N, go); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 } // namespace xnp

@@ -1093,3 +1093,134 @@ extern "C" xnp_status xnp_batch_abort(xnp_pool *pool) {
     B.open = false;
     return XNP_OK;
 }
+
+// ---------------------------------------------------------------------------------------------
+// the rest of the layer: transformer.rs:591-634
+
+extern "C" xnp_status xnp_quantize_rows(const float *w, int32_t rows, int32_t cols, int8_t *q, float *scales) {
+    if ((!w || !q || !scales) && rows > 0 && cols > 0) return fail(XNP_E_INVALID, "null argument");
+    if (rows < 0 || cols < 0) return fail(XNP_E_INVALID, "a %d x %d matrix", rows, cols);
+    for (int32_t r = 0; r < rows; r++) {
+        const float *wr = w + (size_t)r * cols;
+        float amax = 0.f;
+        for (int32_t i = 0; i < cols; i++) amax = std::fmax(amax, std::fabs(wr[i]));
+        const float s = amax / 127.0f;
+        scales[r] = s;
+        for (int32_t i = 0; i < cols; i++) {
+            int v = 0;
+            if (s > 0.0f) v = (int)std::fmin(std::fmax(std::rint(wr[i] / s), -127.0f), 127.0f);
+            q[(size_t)r * cols + i] = (int8_t)v;
+        }
+    }
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_layer_norm(const void *x, int32_t rows, int32_t dim, const float *w, const float *b,
+                                     float eps, void *out, void *hip_stream) {
+    if (rows < 0 || dim <= 0 || dim % 512 || dim > 2048)
+        return fail(XNP_E_INVALID, "layer norm over %d rows of %d: rows of a multiple of 512 up to 2048", rows, dim);
+    if (rows > 0 && (!x || !w || !b || !out)) return fail(XNP_E_INVALID, "null argument");
+    HIP_TRY(launch_layer_norm(x, rows, dim, w, b, eps, out, (hipStream_t)hip_stream), "layer norm");
+    return XNP_OK;
+}
+
+static xnp_status linear_check(int32_t rows, int32_t k, int32_t n) {
+    if (rows < 0 || k <= 0 || n <= 0 || k % 64 || n % 64)
+        return fail(XNP_E_INVALID, "a q8 linear of %d x %d by %d: k and n must be multiples of 64", rows, k, n);
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_linear_q8(const void *x, int32_t rows, int32_t k, const int8_t *w, const float *s,
+                                    int32_t n, int32_t epilogue, void *y, const float *ls, void *hip_stream) {
+    if (xnp_status st = linear_check(rows, k, n)) return st;
+    if (epilogue < XNP_EPI_STORE || epilogue > XNP_EPI_RESIDUAL) return fail(XNP_E_INVALID, "epilogue %d", epilogue);
+    if (rows > 0 && (!x || !w || !s || !y)) return fail(XNP_E_INVALID, "null argument");
+    GemmOut go;
+    go.out[0] = y;
+    go.ld[0] = n;
+    go.ls = epilogue == XNP_EPI_RESIDUAL ? ls : nullptr;
+    HIP_TRY(launch_gemm_q8(x, rows, k, w, s, n, epilogue, go, (hipStream_t)hip_stream), "q8 linear");
+    return XNP_OK;
+}
+
+namespace {
+// The layer step's scratch, carved from the caller's workspace: 256-byte aligned bf16 arrays.
+struct LayerScratch {
+    char *h, *q, *k, *v, *att, *f;
+    uint64_t bytes;
+};
+
+LayerScratch layer_scratch(char *base, int64_t rows, int64_t dm, int64_t qd, int64_t kd, int64_t ff) {
+    LayerScratch L{};
+    uint64_t off = 0;
+    auto take = [&](int64_t elems) {
+        char *p = base ? base + off : nullptr;
+        off += align_up((size_t)(elems * 2), 256);
+        return p;
+    };
+    L.h = take(rows * dm);
+    L.q = take(rows * qd);
+    L.k = take(rows * kd);
+    L.v = take(rows * kd);
+    L.att = take(rows * qd);
+    L.f = take(rows * ff);
+    L.bytes = off;
+    return L;
+}
+} // namespace
+
+extern "C" xnp_status xnp_layer_workspace(const xnp_pool *pool, int32_t rows, int32_t d_model, int32_t ff,
+                                          uint64_t *bytes) {
+    if (!pool || !bytes) return fail(XNP_E_INVALID, "null argument");
+    if (rows < 0 || d_model <= 0 || ff <= 0) return fail(XNP_E_INVALID, "rows %d, d_model %d, ff %d", rows, d_model, ff);
+    const int64_t qd = (int64_t)pool->d.num_heads * pool->d.head_dim, kd = (int64_t)pool->d.num_kv_heads * pool->d.head_dim;
+    *bytes = layer_scratch(nullptr, rows, d_model, qd, kd, ff).bytes;
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_layer_step(xnp_pool *pool, int32_t layer, const xnp_layer_weights *w, void *x,
+                                     void *workspace, uint64_t workspace_bytes, void *hip_stream) {
+    if (!pool || !w || !x) return fail(XNP_E_INVALID, "null argument");
+    if (xnp_status st = batch_call(pool, layer, hip_stream, pool->batch.t == 1)) return st;
+    if (pool->d.act_dtype != XNP_BF16) return fail(XNP_E_INVALID, "the layer step runs on bf16 activations");
+    const int32_t dm = w->d_model, ff = w->ff;
+    const int32_t H = pool->d.num_heads, KVH = pool->d.num_kv_heads, D = pool->d.head_dim;
+    const int32_t qd = H * D, kd = KVH * D, nqkv = qd + 2 * kd;
+    if (dm <= 0 || dm % 512 || dm > 2048) return fail(XNP_E_INVALID, "d_model %d: a multiple of 512 up to 2048", dm);
+    if (ff <= 0 || ff % 64) return fail(XNP_E_INVALID, "dim_feedforward %d: a multiple of 64", ff);
+    if (w->gelu != XNP_GELU_ERF && w->gelu != XNP_GELU_TANH) return fail(XNP_E_INVALID, "gelu %d", w->gelu);
+    if (!w->wqkv || !w->sqkv || !w->wout || !w->sout || !w->w1 || !w->s1 || !w->w2 || !w->s2 || !w->ln1_w ||
+        !w->ln1_b || !w->ln2_w || !w->ln2_b)
+        return fail(XNP_E_INVALID, "a weight of the layer is null");
+    const int64_t rows = (int64_t)pool->batch.n * pool->batch.t;
+    const LayerScratch need = layer_scratch(nullptr, rows, dm, qd, kd, ff);
+    if (!workspace || workspace_bytes < need.bytes)
+        return fail(XNP_E_INVALID, "workspace of %llu bytes; the step needs %llu", (unsigned long long)workspace_bytes,
+                    (unsigned long long)need.bytes);
+    if (rows == 0) return XNP_OK;
+    const LayerScratch S = layer_scratch((char *)workspace, rows, dm, qd, kd, ff);
+    hipStream_t hs = pool->batch.stream;
+    const int M = (int)rows;
+    // self-attention block: x + layer_scale_1(out_proj(attn(in_proj(norm1(x)))))
+    HIP_TRY(launch_layer_norm(x, M, dm, w->ln1_w, w->ln1_b, 1e-5f, S.h, hs), "norm1");
+    GemmOut qkv;
+    qkv.nseg = 3;
+    qkv.out[0] = S.q, qkv.ld[0] = qd, qkv.col0[0] = 0;
+    qkv.out[1] = S.k, qkv.ld[1] = kd, qkv.col0[1] = qd;
+    qkv.out[2] = S.v, qkv.ld[2] = kd, qkv.col0[2] = qd + kd;
+    HIP_TRY(launch_gemm_q8(S.h, M, dm, w->wqkv, w->sqkv, nqkv, kStore, qkv, hs), "in_proj");
+    if (xnp_status st = xnp_attend(pool, layer, S.q, S.k, S.v, S.att, 1.0f / std::sqrt((float)D), hip_stream))
+        return st;
+    GemmOut res;
+    res.out[0] = x, res.ld[0] = dm, res.ls = w->ls1;
+    HIP_TRY(launch_gemm_q8(S.att, M, qd, w->wout, w->sout, dm, kResidual, res, hs), "out_proj");
+    // feed-forward block: x + layer_scale_2(linear2(gelu(linear1(norm2(x)))))
+    HIP_TRY(launch_layer_norm(x, M, dm, w->ln2_w, w->ln2_b, 1e-5f, S.h, hs), "norm2");
+    GemmOut hid;
+    hid.out[0] = S.f, hid.ld[0] = ff;
+    HIP_TRY(launch_gemm_q8(S.h, M, dm, w->w1, w->s1, ff, w->gelu == XNP_GELU_ERF ? kGeluErf : kGeluTanh, hid, hs),
+            "linear1");
+    res.ls = w->ls2;
+    HIP_TRY(launch_gemm_q8(S.f, M, ff, w->w2, w->s2, dm, kResidual, res, hs), "linear2");
+    return XNP_OK;
+}

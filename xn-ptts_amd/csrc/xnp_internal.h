@@ -96,6 +96,24 @@ hipError_t launch_prefill(const PoolView &pv, const BatchView &bv, int layer, co
 hipError_t launch_evict_rotate(const PoolView &pv, const EvictRow *rows, int n,
                                const float *cos_row, const float *sin_row, hipStream_t stream);
 hipError_t launch_copy_page(const PoolView &pv, int src_page, int dst_page, hipStream_t stream);
+// Epilogues of the q8 projection GEMM (launch_gemm_q8).
+enum : int32_t { kStore = 0, kGeluErf = 1, kGeluTanh = 2, kResidual = 3 };
+
+// Where a q8 projection writes.  kStore: columns [col0[j], col0[j+1]) go to out[j] (row stride
+// ld[j], column n - col0[j]), j < nseg; the others: out[0] with stride ld[0] (kResidual reads and
+// writes it, with the layer scale ls when not null).
+struct GemmOut {
+    void *out[3] = {nullptr, nullptr, nullptr};
+    int32_t ld[3] = {0, 0, 0};
+    int32_t col0[3] = {0, 0, 0};
+    int32_t nseg = 1;
+    const float *ls = nullptr;
+};
+
+hipError_t launch_layer_norm(const void *x, int rows, int dim, const float *w, const float *b, float eps, void *out,
+                             hipStream_t stream);
+hipError_t launch_gemm_q8(const void *A, int M, int K, const int8_t *W, const float *s, int N, int epi,
+                          const GemmOut &go, hipStream_t stream);
 hipError_t launch_rows_io(const PoolView &pv, int sid, int layer, int kv, int slot0, int n,
                           void *rows, float *scales, bool write, hipStream_t stream);
 

@@ -53,6 +53,14 @@ class PoolDesc(_c.Structure):
     ]
 
 
+class LayerWeightsC(_c.Structure):
+    """xnp_layer_weights: device pointers of one layer's q8 projections, norms and layer scales."""
+    _fields_ = [("d_model", _i32), ("ff", _i32), ("gelu", _i32),
+                ("wqkv", _p), ("sqkv", _p), ("wout", _p), ("sout", _p), ("w1", _p), ("s1", _p),
+                ("w2", _p), ("s2", _p), ("ln1_w", _p), ("ln1_b", _p), ("ln2_w", _p), ("ln2_b", _p),
+                ("ls1", _p), ("ls2", _p)]
+
+
 class StreamInfo(_c.Structure):
     _fields_ = [(n, _i32) for n in (
         "current_end", "capacity", "ring_mode", "ring_write", "ring_filled", "ring_prefix",
@@ -92,6 +100,11 @@ SIGNATURES = {
     "xnp_attend": (_i32, [_p, _i32, _p, _p, _p, _p, _c.c_float, _p]),
     "xnp_batch_end": (_i32, [_p]),
     "xnp_batch_abort": (_i32, [_p]),
+    "xnp_layer_workspace": (_i32, [_p, _i32, _i32, _i32, _c.POINTER(_c.c_uint64)]),
+    "xnp_layer_step": (_i32, [_p, _i32, _p, _p, _p, _c.c_uint64, _p]),
+    "xnp_layer_norm": (_i32, [_p, _i32, _i32, _p, _p, _c.c_float, _p, _p]),
+    "xnp_linear_q8": (_i32, [_p, _i32, _i32, _p, _p, _i32, _i32, _p, _p, _p]),
+    "xnp_quantize_rows": (_i32, [_p, _i32, _i32, _p, _p]),
     "xnp_frame_budget": (_i32, [_i32, _c.c_double]),
     "xnp_seq_budget": (_i32, [_i32, _i32]),
     "xnp_last_error": (_c.c_char_p, []),
@@ -308,8 +321,60 @@ class KvPool:
         _check(self._lib.xnp_attend(self._h, layer, _ptr(q), _ptr(k), _ptr(v), _ptr(out), scale,
                                     self._stream_h))
 
+    def layer_workspace(self, rows: int, d_model: int, ff: int) -> int:
+        out = _c.c_uint64()
+        _check(self._lib.xnp_layer_workspace(self._h, rows, d_model, ff, _c.byref(out)))
+        return out.value
+
+    def layer_step(self, layer: int, weights: "LayerWeights", x, workspace):
+        """StreamingTransformerLayer::forward (transformer.rs:591-634) on every row of the open
+        batch: x [n][t][d_model] bf16 is the residual stream, updated in place."""
+        _check(self._lib.xnp_layer_step(self._h, layer, _c.byref(weights.c), _ptr(x), _ptr(workspace),
+                                        workspace.numel() * workspace.element_size(), self._stream_h))
+
     def end(self):
         _check(self._lib.xnp_batch_end(self._h))
 
     def abort(self):
         _check(self._lib.xnp_batch_abort(self._h))
+
+
+# ---- the rest of the layer (transformer.rs:591-634) ---------------------------------------------
+GELU = {"erf": 0, "tanh": 1}
+EPILOGUES = {"store": 0, "gelu_erf": 1, "gelu_tanh": 2, "residual": 3}
+
+
+class LayerWeights:
+    """One layer's weights on the device (torch tensors): int8 projections with per-channel f32
+    scales, f32 norm weights and biases, optional layer scales."""
+
+    def __init__(self, wqkv, sqkv, wout, sout, w1, s1, w2, s2, ln1_w, ln1_b, ln2_w, ln2_b,
+                 ls1=None, ls2=None, gelu: str = "erf"):
+        self.tensors = [wqkv, sqkv, wout, sout, w1, s1, w2, s2, ln1_w, ln1_b, ln2_w, ln2_b, ls1, ls2]
+        self.c = LayerWeightsC(d_model=wout.shape[0], ff=w1.shape[0], gelu=GELU[gelu],
+                               wqkv=_ptr(wqkv), sqkv=_ptr(sqkv), wout=_ptr(wout), sout=_ptr(sout),
+                               w1=_ptr(w1), s1=_ptr(s1), w2=_ptr(w2), s2=_ptr(s2), ln1_w=_ptr(ln1_w),
+                               ln1_b=_ptr(ln1_b), ln2_w=_ptr(ln2_w), ln2_b=_ptr(ln2_b), ls1=_ptr(ls1),
+                               ls2=_ptr(ls2))
+
+
+def quantize_rows(w):
+    """Per-row int8 weights of a float32 numpy matrix: (q int8, scales f32), computed by the library."""
+    import numpy as np
+    w = np.ascontiguousarray(w, np.float32)
+    q = np.zeros(w.shape, np.int8)
+    s = np.zeros(w.shape[0], np.float32)
+    _check(load_library().xnp_quantize_rows(w.ctypes.data, w.shape[0], w.shape[1], q.ctypes.data, s.ctypes.data))
+    return q, s
+
+
+def layer_norm(x, w, b, out, eps: float = 1e-5, stream=None):
+    dim = x.shape[-1]
+    _check(load_library().xnp_layer_norm(_ptr(x), x.numel() // dim, dim, _ptr(w), _ptr(b), eps, _ptr(out),
+                                         _stream(stream)))
+
+
+def linear_q8(x, w, s, y, epilogue: str = "store", ls=None, stream=None):
+    k = x.shape[-1]
+    _check(load_library().xnp_linear_q8(_ptr(x), x.numel() // k, k, _ptr(w), _ptr(s), w.shape[0],
+                                        EPILOGUES[epilogue], _ptr(y), _ptr(ls), _stream(stream)))
