@@ -10,7 +10,8 @@
   2 KB new k/v, 1 KB out, 2 KB append write, 4 ceil((n+1)/16) B of page ids) over the kernel's
   average duration, against 8 TB/s.  The duration comes from HIP events that the launch itself
   records as the kernel starts and ends (hipExtLaunchKernel, via xnp_pool_time_next), on the
-  stream the kernel runs on.
+  stream the kernel runs on: one launch per timed step, layer s % 9 at step s (an event pair
+  costs about 17 us of issue time, so timing all nine would slow the steps being measured).
 
 --workload prefill: prompt prefill, 64 streams x 256-position prompts, 9 layers, bf16, RoPE
   theta 10000, causal, K/V written into the pages.  Value: prompt positions/s.  Roofline: causal
@@ -107,21 +108,27 @@ def window_bytes(attended):
 
 
 def timed_steps(step, steps, warmup, L):
-    """Run warmup then `steps` steps, each recording kernel events; wall ms/step and kernel ms."""
+    """Run warmup then `steps` steps; wall ms per step, and the durations (ms) of the timed launches.
+
+    Step s times one launch, layer s % L, with HIP events its launch records around the kernel:
+    a recorded event costs about 17 us of issue time, so timing every launch would slow the very
+    steps the wall clock measures.  Layers are alike, so the rotating sample's mean is the mean
+    launch duration."""
     import torch
     for _ in range(warmup):
         step(None)
     torch.cuda.synchronize()
     hip = HipEvents()
-    ev = [[[hip.create() for _ in range(2)] for _ in range(L)] for _ in range(steps)]
+    ev = [[(hip.create(), hip.create()) if l == s % L else None for l in range(L)] for s in range(steps)]
     t0 = time.perf_counter()
     for s in range(steps):
         step(ev[s])
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    kern = np.array([[hip.elapsed_ms(ev[s][l][0], ev[s][l][1]) for l in range(L)] for s in range(steps)])
-    for e in (e for s_ in ev for l_ in s_ for e in l_):
-        hip.destroy(e)
+    kern = np.array([hip.elapsed_ms(*ev[s][s % L]) for s in range(steps)])
+    for pair in (p_ for s_ in ev for p_ in s_ if p_ is not None):
+        for e in pair:
+            hip.destroy(e)
     return (t1 - t0) * 1000.0 / steps, kern
 
 
@@ -141,7 +148,8 @@ def cpu_decode(L, lens_all, seconds, sample=128):
     oracle = _load("oracle", os.path.join(ROOT, "oracle", "oracle.py"))
     rng = np.random.default_rng(SEED + 100)
     lens = lens_all[:sample]
-    cap = int(lens.max()) + 64
+    room = 512  # steps the sample's caches have room for
+    cap = int(lens.max()) + room
     streams = [oracle.Stream(L, H, D, cap, cache="bf16", act="bf16") for _ in lens]
     rows = bf16_np(rng.standard_normal((int(lens.max()), H, D)))
     for st, n in zip(streams, lens):
@@ -157,7 +165,7 @@ def cpu_decode(L, lens_all, seconds, sample=128):
         oracle.batch_commit(streams)
         steps += 1
         el = time.perf_counter() - t0
-        if el >= seconds:
+        if el >= seconds or steps >= room:
             break
     return {"value": round(len(lens) * steps / el, 1), "unit": "frames/s", "cores": oracle.threads(), "kind": "port",
             "sample": f"{len(lens)} streams x {L} layers x {steps} steps of the same workload "
@@ -201,15 +209,15 @@ def run_decode(args, xnp, torch):
             bytes_timed[0] += L * decode_bytes(cur)
         pool.begin(ids)
         for layer in range(L):
-            if events is not None:  # recorded by the launch itself, around the kernel alone
-                pool.time_next(events[layer][0], events[layer][1])
+            if events is not None and events[layer] is not None:  # recorded by the launch itself
+                pool.time_next(*events[layer])
             pool.attend(layer, q[layer], k[layer], v[layer], out[layer], 0.125)
         pool.end()
         cur[:] += 1
 
     ms, kern = timed_steps(step, args.steps, args.warmup, L)
     avg_ms = float(kern.mean())
-    bytes_per_launch = bytes_timed[0] / (args.steps * L)
+    bytes_per_launch = bytes_timed[0] / (args.steps * L)  # every layer of a step moves the same bytes
     achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
     fps = S / (ms / 1000.0)
     # HBM traffic per launch from the FETCH_SIZE / WRITE_SIZE counter runs of this same command,
@@ -274,8 +282,8 @@ def run_prefill(args, xnp, torch):
     def step(events):
         pool.begin(ids, t=T)
         for layer in range(L):
-            if events is not None:
-                pool.time_next(events[layer][0], events[layer][1])
+            if events is not None and events[layer] is not None:
+                pool.time_next(*events[layer])
             pool.attend(layer, q[layer], k[layer], v[layer], out[layer], 0.125)
         pool.end()
         for i, sid in enumerate(ids):  # a new utterance per stream for the next step
@@ -396,15 +404,15 @@ def run_window(args, xnp, torch):
         pool.slide_batch(ids, 0, SPAN, WINDOW, 1, heads + written)
         pool.begin(ids)
         for layer in range(L):
-            if events is not None:
-                pool.time_next(events[layer][0], events[layer][1])
+            if events is not None and events[layer] is not None:
+                pool.time_next(*events[layer])
             pool.attend(layer, q[layer], kv_new[2 * layer], kv_new[2 * layer + 1], out[layer], 0.125)
         pool.end()
         written[:] += 1
 
     ms, kern = timed_steps(step, args.steps, args.warmup, L)
     avg_ms = float(kern.mean())
-    bytes_per_launch = bytes_timed[0] / (args.steps * L)
+    bytes_per_launch = bytes_timed[0] / (args.steps * L)  # every layer of a step moves the same bytes
     achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
     fps = S / (ms / 1000.0)
     cpu = None if args.no_cpu else cpu_window(L, lens, args.cpu_seconds)
@@ -449,7 +457,8 @@ def cpu_step(L, lens_all, weights, seconds, sample=64):
     oracle = _load("oracle", os.path.join(ROOT, "oracle", "oracle.py"))
     rng = np.random.default_rng(SEED + 500)
     lens = lens_all[:sample]
-    cap = int(lens.max()) + 64
+    room = 512  # steps the sample's caches have room for
+    cap = int(lens.max()) + room
     streams = [oracle.Stream(L, H, D, cap, cache="bf16", act="bf16") for _ in lens]
     rows = bf16_np(rng.standard_normal((int(lens.max()), H, D)))
     for st, n in zip(streams, lens):
@@ -467,7 +476,7 @@ def cpu_step(L, lens_all, weights, seconds, sample=64):
         oracle.batch_commit(streams)
         steps += 1
         el = time.perf_counter() - t0
-        if el >= seconds:
+        if el >= seconds or steps >= room:
             break
     return {"value": round(len(lens) * steps / el, 1), "unit": "frames/s", "cores": oracle.threads(), "kind": "port",
             "sample": f"{len(lens)} streams x {L} layers x {steps} steps of the same workload (bf16, lengths from "
@@ -513,15 +522,15 @@ def run_step(args, xnp, torch):
         x.copy_(x0)  # the step's input rows (synthetic; the model's would come from its embeddings)
         pool.begin(ids)
         for layer in range(L):
-            if events is not None:
-                pool.time_next(events[layer][0], events[layer][1])
+            if events is not None and events[layer] is not None:
+                pool.time_next(*events[layer])
             pool.layer_step(layer, W[layer], x, ws)
         pool.end()
         cur[:] += 1
 
     ms, kern = timed_steps(step, args.steps, args.warmup, L)
     avg_ms = float(kern.mean())
-    bytes_per_launch = bytes_timed[0] / (args.steps * L)
+    bytes_per_launch = bytes_timed[0] / (args.steps * L)  # every layer of a step moves the same bytes
     achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
     fps = S / (ms / 1000.0)
     rest_ms = ms / L - avg_ms  # per layer: norms, projections, plan, launch gaps
