@@ -22,6 +22,11 @@
   residuals, RoPE, paged bf16 KV append and decode attention over cache lengths U[1, 1500].  Value:
   frames/s.  Roofline: the decode attention kernel (the step's dominant kernel) against 8 TB/s.
 
+--workload flowlm: the single-stream flow LM (Phonon-31m shape, fp32): a 64-token text prompt, then
+  greedy frames at temperature 0 through input_linear, the 6 layers, out_norm, the EOS head and the flow
+  net.  Value: frames/s at batch 1; the CPU oracle of the same stream beside it on 1 thread and on all
+  cores.
+
 --workload window: int8 K/V with fp32 scales per (page, head), 1024 streams, a sliding window of
   512 positions on rings of 528 slots whose write heads start at offsets U[0, 4096), each stream
   holding U[64, 2048] rows written so far; per step every stream evicts its oldest row once the
@@ -551,12 +556,101 @@ def run_step(args, xnp, torch):
                 "frames/s", args, ms, "bf16", config, roof, cpu, extra={"audio_sec_per_sec": round(fps * 0.08, 1)})
 
 
+# ---- the single-stream flow LM (configuration 1) ----------------------------------------------------
+def flow_bytes(cfg, n):
+    """Algorithmic bytes of one frame at batch 1: every f32 weight of the transformer, the heads and
+    the flow net read once, plus the K/V rows attended (n cached before the step), in f32."""
+    d, F, ld, ff = cfg.d_model, cfg.flow_dim, cfg.ldim, cfg.dim_feedforward
+    w = d * ld + cfg.num_layers * (4 * d * d + 2 * d * ff + 4 * d) + 2 * d + d + 1
+    w += F * d + F + F * ld + F + cfg.flow_depth * (5 * F * F + 8 * F) + 2 * F * F + 2 * F + ld * F + ld
+    kv = cfg.num_layers * 2 * (n + 1) * d
+    return 4 * (w + kv)
+
+
+def cpu_flowlm(cfg, blob, tokens, seconds, threads):
+    oracle = _load("oracle", os.path.join(ROOT, "oracle", "oracle.py"))
+    oracle.set_threads(threads)
+    m = oracle.FlowLM(cfg, blob)
+    st = m.stream(len(tokens) + 512)
+    m.prompt_text(st, tokens)
+    zero = np.zeros(cfg.ldim, np.float32)
+    lat, frames, t0 = None, 0, time.perf_counter()
+    while True:
+        lat, _ = m.step(st, lat, zero)
+        frames += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or frames >= 512:
+            break
+    return {"value": round(frames / el, 1), "unit": "frames/s", "cores": threads, "kind": "port",
+            "sample": f"the same stream: {len(tokens)}-token prompt, then {frames} frames at temperature 0, "
+                      f"{el:.1f} s on {threads} thread{'s' if threads > 1 else ''}"}
+
+
+def run_flowlm(args, xnp, torch):
+    dev = torch.device("cuda:0")
+    fl = xnp.flow_lm
+    cfg = fl.FlowLMConfig()  # Phonon-31m: 6 x 512, 8 heads, FF 2048, ldim 32, n_bins 4000, flow 512 x 6
+    blob = fl.random_weights(cfg, SEED)
+    rng = np.random.default_rng(SEED)
+    tokens = rng.integers(0, cfg.n_bins + 1, 64).astype(np.int32)
+    frames = args.warmup + args.steps
+    cap = xnp.seq_budget(64, xnp.frame_budget(64))  # plan.rs:52-54: 868
+    if 64 + frames > cap:
+        raise SystemExit(f"{frames} frames do not fit the {cap}-position budget of a 64-token prompt")
+    mbps = (cap + 15) // 16
+    pool = xnp.KvPool(num_layers=cfg.num_layers, num_heads=cfg.num_heads, num_blocks=mbps + 4, max_streams=1,
+                      max_blocks_per_stream=mbps, cache_dtype="f32", act_dtype="f32", max_pos=cap + 16,
+                      page_seed=SEED + 9)
+    sid = pool.init_state(cap)
+    lm = xnp.FlowLM(pool, cfg, blob, max_rows=64)
+    noise = torch.zeros((1, cfg.ldim), dtype=torch.float32, device=dev)  # temperature 0
+    lat = [torch.empty((1, cfg.ldim), dtype=torch.float32, device=dev) for _ in range(2)]
+    eos = torch.empty(1, dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    lm.prompt_text([sid], tokens[None, :])
+    torch.cuda.synchronize()
+    prompt_ms = (time.perf_counter() - t0) * 1000.0
+    cur = [None]
+    for f in range(args.warmup):
+        lm.step([sid], cur[0], noise, lat[f % 2], eos)
+        cur[0] = lat[f % 2]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for f in range(args.warmup, frames):
+        lm.step([sid], cur[0], noise, lat[f % 2], eos)
+        cur[0] = lat[f % 2]
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+    fps = 1000.0 / ms
+    bytes_mean = np.mean([flow_bytes(cfg, 64 + f) for f in range(args.warmup, frames)])
+    gbs = bytes_mean / (ms * 1e-3) / 1e9
+    cpu = None if args.no_cpu else cpu_flowlm(cfg, blob, tokens, args.cpu_seconds, 1)
+    extra = {"audio_sec_per_sec": round(fps * 0.08, 2), "prompt_ms": round(prompt_ms, 3)}
+    if not args.no_cpu:
+        oracle = _load("oracle", os.path.join(ROOT, "oracle", "oracle.py"))
+        extra["cpu_baseline_all_cores"] = cpu_flowlm(cfg, blob, tokens, args.cpu_seconds, os.cpu_count() or 1)
+        oracle.set_threads(os.cpu_count() or 1)
+    config = {"workload": "single-stream flow LM, Phonon-31m shape (6 x 512, 8 heads x 64, FF 2048, ldim 32, "
+                          "n_bins 4000, flow net 512 x 6, 1 LSD step), random-init f32 weights N(0, 0.02), unit "
+                          "norms; 64 seeded tokens, then greedy frames at temperature 0 on an f32 paged cache",
+              "streams": 1, "layers": cfg.num_layers, "prompt_tokens": 64, "frames_timed": args.steps}
+    # batch 1 is launch-bound (about 80 launches a frame): the roofline is the frame's bytes (every
+    # f32 weight once plus the K/V attended) over its wall time, not one kernel's
+    roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "whole frame: f32 linears, LayerNorms, k_decode<f32>, flow net (batch 1, launch-bound)",
+            "bytes_per_frame": int(bytes_mean)}
+    return line("frames/sec, single-stream flow LM (Phonon-31m shape, fp32)", fps, "frames/s", args, ms, "f32",
+                config, roof, cpu, extra=extra)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=["decode", "prefill", "window", "step"], default="decode")
+    ap.add_argument("--workload", choices=["decode", "prefill", "window", "step", "flowlm"], default="decode")
     ap.add_argument("--step-streams", type=int, default=2048)
     ap.add_argument("--step-max-len", type=int, default=1500)
     ap.add_argument("--streams", type=int, default=1024)
@@ -590,7 +684,8 @@ def main():
     import torch
     xnp = _load("xn_ptts_amd", os.path.join(ROOT, "xn-ptts_amd"))
     xnp.load_library()
-    run = {"decode": run_decode, "prefill": run_prefill, "window": run_window, "step": run_step}[args.workload]
+    run = {"decode": run_decode, "prefill": run_prefill, "window": run_window, "step": run_step,
+           "flowlm": run_flowlm}[args.workload]
     print(json.dumps(run(args, xnp, torch)))
 
 

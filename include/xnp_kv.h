@@ -265,6 +265,53 @@ xnp_status xnp_linear_q8(const void *x, int32_t rows, int32_t k, const int8_t *w
  * +-127 (an all-zero row gets s = 0, q = 0). */
 xnp_status xnp_quantize_rows(const float *w, int32_t rows, int32_t cols, int8_t *q, float *scales);
 
+/* ---- the flow LM around the transformer (flow_lm.rs, mlp.rs, conditioners.rs) ----------- */
+/* FlowLM's text prompt and frame steps (TTSModel::prompt_text and generate_step_parts,
+ * tts_model.rs:297-378) on f32 kernels, for batches of an f32 pool's streams: the LUT gather,
+ * input_linear, the transformer (norms, linears, GELU, residuals around the pool's attention),
+ * out_norm, the EOS head and the flow net's LSD decode (SimpleMLPAdaLN, mlp.rs:159-238).  Config
+ * subset: no z_proj, no attn_dim override, no grouped heads, no layer scale, no conditions or
+ * sinks. */
+typedef enum xnp_time_norm { XNP_TIME_RMS = 0, XNP_TIME_RMS_VAR = 1 } xnp_time_norm; /* mlp.rs:17-28 */
+
+typedef struct xnp_flow_lm_desc {
+    int32_t d_model, num_heads, num_layers, ff; /* the transformer; the pool must match it */
+    int32_t ldim, n_bins, flow_dim, flow_depth; /* latent width, LUT rows - 1, flow net width, blocks */
+    int32_t lsd_steps;                          /* lsd_decode_steps */
+    int32_t gelu;                               /* xnp_gelu */
+    int32_t time_norm;                          /* xnp_time_norm */
+    int32_t max_rows;                           /* rows one call may hold: streams x prompt tokens */
+} xnp_flow_lm_desc;
+
+typedef struct xnp_flow_lm xnp_flow_lm;
+
+/* Floats of the weight blob: every tensor f32, row-major [out][in] for linears, in this order --
+ * conditioner.embed [n_bins+1][d]; input_linear [d][ldim]; bos_emb [ldim];
+ * per layer: norm1 w, b [d]; in_proj [3d][d]; out_proj [d][d]; norm2 w, b [d]; linear1 [ff][d];
+ *   linear2 [d][ff];
+ * out_norm w, b [d]; out_eos w [1][d], b [1];
+ * per time embedder (2): freqs [128]; mlp.0 w [F][256], b [F]; mlp.2 w [F][F], b [F]; alpha [F];
+ * cond_embed w [F][d], b [F]; input_proj w [F][ldim], b [F];
+ * per res block: in_ln w, b [F]; mlp.0 w [F][F], b [F]; mlp.2 w [F][F], b [F];
+ *   adaLN_modulation.1 w [3F][F], b [3F];
+ * final_layer: adaLN_modulation.1 w [2F][F], b [2F]; linear w [ldim][F], b [ldim]. */
+xnp_status xnp_flow_lm_weights_size(const xnp_flow_lm_desc *desc, int64_t *nfloats);
+/* Upload the weights (host memory) for a pool with f32 cache and activations whose layers and
+ * heads match; the time embeddings of the solver steps are computed once here, as
+ * lsd_time_embeddings does at load (flow_lm.rs:82-95). */
+xnp_status xnp_flow_lm_create(xnp_pool *pool, const xnp_flow_lm_desc *desc, const float *weights,
+                              int64_t nfloats, xnp_flow_lm **out);
+xnp_status xnp_flow_lm_destroy(xnp_flow_lm *lm);
+/* prompt_text for streams ids[0..n), tokens [n][t] (host int32): their LUT rows through the
+ * transformer, committed.  Token ids past the table are refused (conditioners.rs:248-256). */
+xnp_status xnp_flow_lm_prompt_text(xnp_flow_lm *lm, const int32_t *ids, int32_t n,
+                                   const int32_t *tokens, int32_t t, void *hip_stream);
+/* One frame for streams ids[0..n): latent_in [n][ldim] (NULL: bos_emb for every row), noise
+ * [n][ldim] (the solver's start; zeros at temperature 0), latent_out [n][ldim], eos_logit [n], all
+ * f32 device memory.  The streams advance by one position. */
+xnp_status xnp_flow_lm_step(xnp_flow_lm *lm, const int32_t *ids, int32_t n, const float *latent_in,
+                            const float *noise, float *latent_out, float *eos_logit, void *hip_stream);
+
 /* ---- budgets (plan.rs:25, 43-54) --------------------------------------------------------- */
 int32_t xnp_frame_budget(int32_t num_tokens, double frame_rate);
 int32_t xnp_seq_budget(int32_t num_tokens, int32_t frame_budget);

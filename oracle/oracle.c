@@ -685,6 +685,251 @@ int orc_layer_step(orc_stream **streams, int n, int t, int layer, const orc_laye
 }
 
 /* ---------------------------------------------------------------------------------------- */
+/* the flow LM around the transformer (flow_lm.rs, mlp.rs, conditioners.rs), f32            */
+
+#define ORC_MAXL 64
+
+typedef struct {
+    size_t embed, in_lin, bos;
+    size_t ln1_w[ORC_MAXL], ln1_b[ORC_MAXL], wqkv[ORC_MAXL], wout[ORC_MAXL];
+    size_t ln2_w[ORC_MAXL], ln2_b[ORC_MAXL], w1[ORC_MAXL], w2[ORC_MAXL];
+    size_t on_w, on_b, eos_w, eos_b;
+    size_t te_freqs[2], te_w1[2], te_b1[2], te_w2[2], te_b2[2], te_alpha[2];
+    size_t cond_w, cond_b, inp_w, inp_b;
+    size_t rb_lnw[ORC_MAXL], rb_lnb[ORC_MAXL], rb_w1[ORC_MAXL], rb_b1[ORC_MAXL];
+    size_t rb_w2[ORC_MAXL], rb_b2[ORC_MAXL], rb_aw[ORC_MAXL], rb_ab[ORC_MAXL];
+    size_t fin_aw, fin_ab, fin_w, fin_b;
+    size_t total;
+} flow_layout;
+
+static int flow_layout_of(const orc_flow_lm_desc *d, flow_layout *L) {
+    if (d->num_layers <= 0 || d->num_layers > ORC_MAXL || d->flow_depth < 0 || d->flow_depth > ORC_MAXL ||
+        d->d_model <= 0 || d->num_heads <= 0 || d->d_model % d->num_heads || d->ldim <= 0 || d->flow_dim <= 0 ||
+        d->ff <= 0 || d->n_bins <= 0 || d->lsd_steps <= 0)
+        return fail("bad flow LM shape");
+    const size_t dm = d->d_model, F = d->flow_dim, ld = d->ldim, ff = d->ff, fq = ORC_FREQ_DIM;
+    size_t o = 0;
+#define TAKE(field, n) (L->field = o, o += (size_t)(n))
+    TAKE(embed, (d->n_bins + 1) * dm);
+    TAKE(in_lin, dm * ld);
+    TAKE(bos, ld);
+    for (int l = 0; l < d->num_layers; l++) {
+        TAKE(ln1_w[l], dm); TAKE(ln1_b[l], dm);
+        TAKE(wqkv[l], 3 * dm * dm); TAKE(wout[l], dm * dm);
+        TAKE(ln2_w[l], dm); TAKE(ln2_b[l], dm);
+        TAKE(w1[l], ff * dm); TAKE(w2[l], dm * ff);
+    }
+    TAKE(on_w, dm); TAKE(on_b, dm);
+    TAKE(eos_w, dm); TAKE(eos_b, 1);
+    for (int i = 0; i < 2; i++) {
+        TAKE(te_freqs[i], fq / 2); TAKE(te_w1[i], F * fq); TAKE(te_b1[i], F);
+        TAKE(te_w2[i], F * F); TAKE(te_b2[i], F); TAKE(te_alpha[i], F);
+    }
+    TAKE(cond_w, F * dm); TAKE(cond_b, F);
+    TAKE(inp_w, F * ld); TAKE(inp_b, F);
+    for (int j = 0; j < d->flow_depth; j++) {
+        TAKE(rb_lnw[j], F); TAKE(rb_lnb[j], F);
+        TAKE(rb_w1[j], F * F); TAKE(rb_b1[j], F);
+        TAKE(rb_w2[j], F * F); TAKE(rb_b2[j], F);
+        TAKE(rb_aw[j], 3 * F * F); TAKE(rb_ab[j], 3 * F);
+    }
+    TAKE(fin_aw, 2 * F * F); TAKE(fin_ab, 2 * F);
+    TAKE(fin_w, ld * F); TAKE(fin_b, ld);
+#undef TAKE
+    L->total = o;
+    return 0;
+}
+
+long long orc_flow_lm_size(const orc_flow_lm_desc *d) {
+    flow_layout L;
+    if (flow_layout_of(d, &L)) return -1;
+    return (long long)L.total;
+}
+
+/* y[m][j] = sum_k x[m][k] w[j][k] (+ b[j]), f32, k ascending: xn's Linear (load: no bias; load_b). */
+void orc_linear_f32(const float *x, int rows, int k, const float *w, const float *b, int n, float *y) {
+    /* output channels in parallel: each is summed by one thread in the same order, so the result
+     * does not depend on the thread count */
+#pragma omp parallel for collapse(2) schedule(static) if ((long long)rows * n * k >= (1 << 18))
+    for (int m = 0; m < rows; m++)
+        for (int j = 0; j < n; j++) {
+            const float *xr = x + (size_t)m * k, *wr = w + (size_t)j * k;
+            float acc = 0.f;
+            for (int i = 0; i < k; i++) acc += xr[i] * wr[i];
+            y[(size_t)m * n + j] = b ? acc + b[j] : acc;
+        }
+}
+
+static inline float silu(float x) { return x / (1.0f + expf(-x)); }
+
+/* TimestepEmbedder::forward (mlp.rs:55-67) for one time t, then its norm (mlp.rs:69-86). */
+static void time_embed_one(const orc_flow_lm_desc *d, const float *blob, const flow_layout *L, int i, float t,
+                           float *out) {
+    const int F = d->flow_dim, half = ORC_FREQ_DIM / 2;
+    float emb[ORC_FREQ_DIM];
+    const float *fr = blob + L->te_freqs[i];
+    for (int j = 0; j < half; j++) {
+        float a = t * fr[j];
+        emb[j] = cosf(a);
+        emb[half + j] = sinf(a);
+    }
+    float *h = malloc(sizeof(float) * F);
+    orc_linear_f32(emb, 1, ORC_FREQ_DIM, blob + L->te_w1[i], blob + L->te_b1[i], F, h);
+    for (int j = 0; j < F; j++) h[j] = silu(h[j]);
+    orc_linear_f32(h, 1, F, blob + L->te_w2[i], blob + L->te_b2[i], F, out);
+    const float *alpha = blob + L->te_alpha[i];
+    const float eps = 1e-5f, n = (float)F;
+    if (d->time_norm == 1) { /* RmsVar: centred, unbiased variance */
+        float s = 0.f;
+        for (int j = 0; j < F; j++) s += out[j];
+        const float mean = s * (1.0f / n);
+        float v = 0.f;
+        for (int j = 0; j < F; j++) {
+            float e = out[j] - mean;
+            v += e * e;
+        }
+        const float inv = 1.0f / sqrtf(v * (1.0f / (n - 1.0f)) + eps);
+        for (int j = 0; j < F; j++) out[j] = out[j] * inv * alpha[j];
+    } else { /* Rms: x * alpha / sqrt(mean(x^2) + eps) */
+        float s = 0.f;
+        for (int j = 0; j < F; j++) s += out[j] * out[j];
+        const float inv = 1.0f / sqrtf(s * (1.0f / n) + eps);
+        for (int j = 0; j < F; j++) out[j] = out[j] * inv * alpha[j];
+    }
+    free(h);
+}
+
+int orc_flow_time_embedding(const orc_flow_lm_desc *d, const float *blob, float s, float t, float *out) {
+    flow_layout L;
+    if (flow_layout_of(d, &L)) return -1;
+    const int F = d->flow_dim;
+    float *b = malloc(sizeof(float) * F);
+    time_embed_one(d, blob, &L, 0, s, out);
+    time_embed_one(d, blob, &L, 1, t, b);
+    for (int j = 0; j < F; j++) out[j] = (out[j] + b[j]) * 0.5f; /* mlp.rs:205-212 */
+    free(b);
+    return 0;
+}
+
+/* LayerNorm without rounding, f32, optional affine, then modulate (mlp.rs:4-11) when shift/scale
+ * are given: y * (1 + scale) + shift. */
+static void ln_mod(const float *x, int n, const float *w, const float *b, float eps, const float *shift,
+                   const float *scale, float *out) {
+    float s = 0.f;
+    for (int i = 0; i < n; i++) s += x[i];
+    const float mean = s / (float)n;
+    float q = 0.f;
+    for (int i = 0; i < n; i++) {
+        float e = x[i] - mean;
+        q += e * e;
+    }
+    const float rstd = 1.0f / sqrtf(q / (float)n + eps);
+    for (int i = 0; i < n; i++) {
+        float y = (x[i] - mean) * rstd;
+        if (w) y = y * w[i] + b[i];
+        if (shift) y = y * (scale[i] + 1.0f) + shift[i];
+        out[i] = y;
+    }
+}
+
+int orc_flow_net(const orc_flow_lm_desc *d, const float *blob, const float *c, const float *t_emb,
+                 const float *x0, float *out) {
+    flow_layout L;
+    if (flow_layout_of(d, &L)) return -1;
+    const int F = d->flow_dim, dm = d->d_model, ld = d->ldim;
+    float *x = malloc(sizeof(float) * F), *y = malloc(sizeof(float) * F), *ya = malloc(sizeof(float) * F);
+    float *ada = malloc(sizeof(float) * 3 * F), *h = malloc(sizeof(float) * F), *h2 = malloc(sizeof(float) * F);
+    orc_linear_f32(x0, 1, ld, blob + L.inp_w, blob + L.inp_b, F, x);     /* input_proj */
+    orc_linear_f32(c, 1, dm, blob + L.cond_w, blob + L.cond_b, F, y);   /* cond_embed */
+    for (int j = 0; j < F; j++) ya[j] = silu(t_emb[j] + y[j]);           /* y = t + c; silu */
+    for (int r = 0; r < d->flow_depth; r++) {                            /* ResBlock (mlp.rs:113-131) */
+        orc_linear_f32(ya, 1, F, blob + L.rb_aw[r], blob + L.rb_ab[r], 3 * F, ada);
+        ln_mod(x, F, blob + L.rb_lnw[r], blob + L.rb_lnb[r], 1e-6f, ada, ada + F, h);
+        orc_linear_f32(h, 1, F, blob + L.rb_w1[r], blob + L.rb_b1[r], F, h2);
+        for (int j = 0; j < F; j++) h2[j] = silu(h2[j]);
+        orc_linear_f32(h2, 1, F, blob + L.rb_w2[r], blob + L.rb_b2[r], F, h);
+        for (int j = 0; j < F; j++) x[j] = x[j] + ada[2 * F + j] * h[j];
+    }
+    orc_linear_f32(ya, 1, F, blob + L.fin_aw, blob + L.fin_ab, 2 * F, ada); /* FinalLayer (mlp.rs:155-163) */
+    ln_mod(x, F, NULL, NULL, 1e-6f, ada, ada + F, h);
+    orc_linear_f32(h, 1, F, blob + L.fin_w, blob + L.fin_b, ld, out);
+    free(x); free(y); free(ya); free(ada); free(h); free(h2);
+    return 0;
+}
+
+/* The transformer over t rows of one stream (transformer.rs:591-634, f32 weights), x [t][d]. */
+static int flow_transformer(const orc_flow_lm_desc *d, const float *blob, const flow_layout *L, orc_stream *st,
+                            int t, float *x) {
+    const int dm = d->d_model, ff = d->ff, H = d->num_heads, D = dm / H;
+    float *h = malloc(sizeof(float) * (size_t)t * dm), *qkv = malloc(sizeof(float) * (size_t)t * 3 * dm);
+    float *q = malloc(sizeof(float) * (size_t)t * dm), *k = malloc(sizeof(float) * (size_t)t * dm);
+    float *v = malloc(sizeof(float) * (size_t)t * dm), *att = malloc(sizeof(float) * (size_t)t * dm);
+    float *f = malloc(sizeof(float) * (size_t)t * ff);
+    int rc = 0;
+    for (int l = 0; l < d->num_layers && rc == 0; l++) {
+        orc_layer_norm(x, t, dm, blob + L->ln1_w[l], blob + L->ln1_b[l], 1e-5f, ORC_F32, h);
+        orc_linear_f32(h, t, dm, blob + L->wqkv[l], NULL, 3 * dm, qkv);
+        for (int i = 0; i < t; i++) {
+            memcpy(q + (size_t)i * dm, qkv + (size_t)i * 3 * dm, sizeof(float) * dm);
+            memcpy(k + (size_t)i * dm, qkv + (size_t)i * 3 * dm + dm, sizeof(float) * dm);
+            memcpy(v + (size_t)i * dm, qkv + (size_t)i * 3 * dm + 2 * dm, sizeof(float) * dm);
+        }
+        rc = orc_attend(st, l, t, q, k, v, 1.0f / sqrtf((float)D), att, NULL);
+        if (rc) break;
+        orc_linear_f32(att, t, dm, blob + L->wout[l], NULL, dm, h);
+        for (size_t i = 0; i < (size_t)t * dm; i++) x[i] += h[i];
+        orc_layer_norm(x, t, dm, blob + L->ln2_w[l], blob + L->ln2_b[l], 1e-5f, ORC_F32, h);
+        orc_linear_f32(h, t, dm, blob + L->w1[l], NULL, ff, f);
+        for (size_t i = 0; i < (size_t)t * ff; i++) f[i] = orc_gelu(f[i], d->gelu);
+        orc_linear_f32(f, t, ff, blob + L->w2[l], NULL, dm, h);
+        for (size_t i = 0; i < (size_t)t * dm; i++) x[i] += h[i];
+    }
+    if (rc == 0) rc = orc_commit(st, t);
+    free(h); free(qkv); free(q); free(k); free(v); free(att); free(f);
+    return rc;
+}
+
+int orc_flow_lm_prompt_text(const orc_flow_lm_desc *d, const float *blob, orc_stream *st, const int *ids, int n) {
+    flow_layout L;
+    if (flow_layout_of(d, &L)) return -1;
+    if (n <= 0) return 0;
+    const int dm = d->d_model;
+    for (int i = 0; i < n; i++)
+        if (ids[i] < 0 || ids[i] > d->n_bins) return fail("token id %d is past the %d-entry embedding table", ids[i], d->n_bins + 1);
+    float *x = malloc(sizeof(float) * (size_t)n * dm);
+    for (int i = 0; i < n; i++) memcpy(x + (size_t)i * dm, blob + L.embed + (size_t)ids[i] * dm, sizeof(float) * dm);
+    int rc = flow_transformer(d, blob, &L, st, n, x); /* tts_model.rs:297-307, 455-466 */
+    free(x);
+    return rc;
+}
+
+int orc_flow_lm_step(const orc_flow_lm_desc *d, const float *blob, orc_stream *st, const float *latent_in,
+                     const float *noise, float *latent_out, float *eos_logit) {
+    flow_layout L;
+    if (flow_layout_of(d, &L)) return -1;
+    const int dm = d->d_model, F = d->flow_dim, ld = d->ldim;
+    float *x = malloc(sizeof(float) * dm), *t_out = malloc(sizeof(float) * dm), *temb = malloc(sizeof(float) * F);
+    float *cur = malloc(sizeof(float) * ld), *dir = malloc(sizeof(float) * ld);
+    /* input_linear of the previous latent, or of bos_emb on the first step (flow_lm.rs:314-324) */
+    orc_linear_f32(latent_in ? latent_in : blob + L.bos, 1, ld, blob + L.in_lin, NULL, dm, x);
+    int rc = flow_transformer(d, blob, &L, st, 1, x);
+    if (rc == 0) {
+        ln_mod(x, dm, blob + L.on_w, blob + L.on_b, 1e-5f, NULL, NULL, t_out); /* out_norm (flow_lm.rs:315) */
+        orc_linear_f32(t_out, 1, dm, blob + L.eos_w, blob + L.eos_b, 1, eos_logit);
+        memcpy(cur, noise, sizeof(float) * ld);
+        const float step_scale = 1.0f / (float)d->lsd_steps;
+        for (int i = 0; i < d->lsd_steps; i++) { /* lsd_decode (flow_lm.rs:97-110) */
+            orc_flow_time_embedding(d, blob, (float)i / (float)d->lsd_steps, (float)(i + 1) / (float)d->lsd_steps, temb);
+            orc_flow_net(d, blob, t_out, temb, cur, dir);
+            for (int j = 0; j < ld; j++) cur[j] = cur[j] + dir[j] * step_scale;
+        }
+        memcpy(latent_out, cur, sizeof(float) * ld);
+    }
+    free(x); free(t_out); free(temb); free(cur); free(dir);
+    return rc;
+}
+
+/* ---------------------------------------------------------------------------------------- */
 /* batched CPU step (the CPU baseline): one thread per stream, OpenMP across streams        */
 
 int orc_batch_attend(orc_stream **streams, int n, int layer, const float *q, const float *k,
@@ -704,6 +949,14 @@ int orc_batch_commit(orc_stream **streams, int n) {
     for (int i = 0; i < n; i++)
         if (orc_commit(streams[i], 1)) return -1;
     return 0;
+}
+
+void orc_set_threads(int n) {
+#ifdef _OPENMP
+    omp_set_num_threads(n);
+#else
+    (void)n;
+#endif
 }
 
 int orc_threads(void) {

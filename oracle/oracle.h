@@ -130,11 +130,50 @@ typedef struct orc_layer_weights {
 int orc_layer_step(orc_stream **streams, int n, int t, int layer, const orc_layer_weights *w,
                    float scale, float *x);
 
+/* --- the flow LM around the transformer (flow_lm.rs, mlp.rs, conditioners.rs), f32 ------------ */
+#define ORC_FREQ_DIM 256 /* the time embedders' frequency embedding (mlp.rs:186-193) */
+typedef struct orc_flow_lm_desc {
+    int d_model, num_heads, num_layers, ff;  /* the transformer (no GQA, no layer scale) */
+    int ldim, n_bins, flow_dim, flow_depth;  /* latent width, LUT rows - 1, flow net width, res blocks */
+    int lsd_steps;                           /* LSD solver steps (lsd_decode_steps) */
+    int gelu;                                /* 0 erf, 1 tanh */
+    int time_norm;                           /* 0 Rms, 1 RmsVar (mlp.rs:17-28) */
+} orc_flow_lm_desc;
+/* Floats of the weight blob: every tensor f32, row-major [out][in], in this order --
+ * conditioner.embed [n_bins+1][d]; input_linear [d][ldim]; bos_emb [ldim];
+ * per layer: norm1 w, b [d]; in_proj [3d][d]; out_proj [d][d]; norm2 w, b [d]; linear1 [ff][d];
+ *   linear2 [d][ff];
+ * out_norm w, b [d]; out_eos w [1][d], b [1];
+ * per time embedder (2): freqs [128]; mlp.0 w [F][256], b [F]; mlp.2 w [F][F], b [F]; alpha [F];
+ * cond_embed w [F][d], b [F]; input_proj w [F][ldim], b [F];
+ * per res block: in_ln w, b [F]; mlp.0 w [F][F], b [F]; mlp.2 w [F][F], b [F];
+ *   adaLN_modulation.1 w [3F][F], b [3F];
+ * final_layer: adaLN_modulation.1 w [2F][F], b [2F]; linear w [ldim][F], b [ldim].
+ * Returns -1 for a bad shape. */
+long long orc_flow_lm_size(const orc_flow_lm_desc *d);
+/* y[m][j] = sum_k x[m][k] w[j][k] (+ b[j] when b is not NULL), f32, k ascending. */
+void orc_linear_f32(const float *x, int rows, int k, const float *w, const float *b, int n, float *y);
+/* SimpleMLPAdaLN::time_embedding([s, t]) (mlp.rs:201-212): out [flow_dim]. */
+int orc_flow_time_embedding(const orc_flow_lm_desc *d, const float *blob, float s, float t, float *out);
+/* SimpleMLPAdaLN::forward (mlp.rs:214-238) on one row: c [d_model], t_emb [flow_dim], x0 [ldim]. */
+int orc_flow_net(const orc_flow_lm_desc *d, const float *blob, const float *c, const float *t_emb,
+                 const float *x0, float *out);
+/* TTSModel::prompt_text (tts_model.rs:297-307): the LUT rows of the tokens through the transformer
+ * (f32 stream), committed.  No text sink. */
+int orc_flow_lm_prompt_text(const orc_flow_lm_desc *d, const float *blob, orc_stream *st,
+                            const int *ids, int n);
+/* One frame (generate_step_parts, tts_model.rs:365-378): input_linear of latent_in (NULL: bos_emb),
+ * the transformer (committed), out_norm, the EOS logit (out_eos) and the LSD decode of noise
+ * [ldim] conditioned on the output: latent_out [ldim], eos_logit [1]. */
+int orc_flow_lm_step(const orc_flow_lm_desc *d, const float *blob, orc_stream *st,
+                     const float *latent_in, const float *noise, float *latent_out, float *eos_logit);
+
 /* Many streams, one layer: the CPU baseline's batched step (OpenMP over streams). */
 int orc_batch_attend(orc_stream **streams, int n, int layer, const float *q, const float *k,
                      const float *v, float scale, float *out);
 int orc_batch_commit(orc_stream **streams, int n);
 int orc_threads(void);
+void orc_set_threads(int n);
 
 const char *orc_last_error(void);
 

@@ -61,6 +61,13 @@ def lib():
                                                 _fp, _fp, _fp, ctypes.c_float, _fp]),
             "orc_batch_commit": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int]),
             "orc_threads": (ctypes.c_int, []),
+            "orc_set_threads": (None, [ctypes.c_int]),
+            "orc_flow_lm_size": (ctypes.c_longlong, [ctypes.c_void_p]),
+            "orc_linear_f32": (None, [_fp, ctypes.c_int, ctypes.c_int, _fp, _fp, ctypes.c_int, _fp]),
+            "orc_flow_time_embedding": (ctypes.c_int, [ctypes.c_void_p, _fp, ctypes.c_float, ctypes.c_float, _fp]),
+            "orc_flow_net": (ctypes.c_int, [ctypes.c_void_p, _fp, _fp, _fp, _fp, _fp]),
+            "orc_flow_lm_prompt_text": (ctypes.c_int, [ctypes.c_void_p, _fp, ctypes.c_void_p, _ip, ctypes.c_int]),
+            "orc_flow_lm_step": (ctypes.c_int, [ctypes.c_void_p, _fp, ctypes.c_void_p, _fp, _fp, _fp, _fp]),
             "orc_layer_norm": (None, [_fp, ctypes.c_int, ctypes.c_int, _fp, _fp, ctypes.c_float, ctypes.c_int, _fp]),
             "orc_quantize_rows": (None, [_fp, ctypes.c_int, ctypes.c_int, _i8p, _fp]),
             "orc_linear_q8": (None, [_fp, ctypes.c_int, ctypes.c_int, _i8p, _fp, ctypes.c_int, ctypes.c_int, _fp]),
@@ -247,6 +254,10 @@ def threads() -> int:
     return lib().orc_threads()
 
 
+def set_threads(n: int):
+    lib().orc_set_threads(n)
+
+
 # ---- the rest of the layer (transformer.rs:591-634) ------------------------------------------------
 def layer_norm(x, w, b, eps=1e-5, act="f32"):
     x, xp = _f32(x)
@@ -323,3 +334,59 @@ def layer_step(streams, layer, weights: LayerWeights, x, scale=0.125):
     _ok(lib().orc_layer_step(arr, n, t, layer, ctypes.cast(ctypes.pointer(cw), ctypes.c_void_p), scale,
                              x.ctypes.data_as(_fp)))
     return x
+
+
+# ---- the flow LM around the transformer (flow_lm.rs, mlp.rs, conditioners.rs), f32 -------------------
+class _FlowDescC(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("d_model", "num_heads", "num_layers", "ff", "ldim", "n_bins",
+                                            "flow_dim", "flow_depth", "lsd_steps", "gelu", "time_norm")]
+
+
+class FlowLM:
+    """The oracle's single-stream flow LM over a flat f32 weight blob (layout: oracle.h)."""
+
+    def __init__(self, cfg, blob):
+        self.cfg = cfg
+        self.d = _FlowDescC(cfg.d_model, cfg.num_heads, cfg.num_layers, cfg.dim_feedforward, cfg.ldim, cfg.n_bins,
+                            cfg.flow_dim, cfg.flow_depth, cfg.lsd_decode_steps, 0 if cfg.gelu == "erf" else 1,
+                            0 if cfg.time_rms_norm == "rms" else 1)
+        self.blob = np.ascontiguousarray(blob, np.float32)
+        n = lib().orc_flow_lm_size(self._dp())
+        if n != self.blob.size:
+            raise OracleError(f"the blob holds {self.blob.size} floats, the layout {n}")
+        self._bp = self.blob.ctypes.data_as(_fp)
+
+    def _dp(self):
+        return ctypes.cast(ctypes.pointer(self.d), ctypes.c_void_p)
+
+    def stream(self, capacity):
+        c = self.cfg
+        return Stream(c.num_layers, c.num_heads, c.d_model // c.num_heads, capacity, cache="f32", act="f32",
+                      max_period=c.max_period)
+
+    def time_embedding(self, s, t):
+        out = np.zeros(self.cfg.flow_dim, np.float32)
+        _ok(lib().orc_flow_time_embedding(self._dp(), self._bp, s, t, out.ctypes.data_as(_fp)))
+        return out
+
+    def flow_net(self, c, t_emb, x0):
+        c, cp = _f32(c)
+        t, tp = _f32(t_emb)
+        x, xp = _f32(x0)
+        out = np.zeros(self.cfg.ldim, np.float32)
+        _ok(lib().orc_flow_net(self._dp(), self._bp, cp, tp, xp, out.ctypes.data_as(_fp)))
+        return out
+
+    def prompt_text(self, st, ids):
+        ids = np.ascontiguousarray(ids, np.int32)
+        _ok(lib().orc_flow_lm_prompt_text(self._dp(), self._bp, st.h, ids.ctypes.data_as(_ip), ids.size))
+
+    def step(self, st, latent_in, noise):
+        """One frame: (latent [ldim], eos logit)."""
+        lat = None if latent_in is None else np.ascontiguousarray(latent_in, np.float32)
+        nz, nzp = _f32(noise)
+        out = np.zeros(self.cfg.ldim, np.float32)
+        eos = np.zeros(1, np.float32)
+        _ok(lib().orc_flow_lm_step(self._dp(), self._bp, st.h, lat.ctypes.data_as(_fp) if lat is not None else None,
+                                   nzp, out.ctypes.data_as(_fp), eos.ctypes.data_as(_fp)))
+        return out, float(eos[0])

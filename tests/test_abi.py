@@ -323,3 +323,25 @@ def test_layer_calls_refuse_bad_shapes_without_running_a_kernel():
     x = ctypes.c_uint16()
     assert lib.xnp_layer_step(pool._h, 0, ctypes.byref(w), ctypes.byref(x), None, 0, None) == 9  # no batch open
     assert pool.layer_workspace(2048, 512, 2048) >= 2048 * (512 * 5 + 2048) * 2
+
+
+def test_flow_lm_layout_agrees_between_the_library_and_the_package():
+    cfg = xnp.FlowLMConfig()
+    d = xnp.flow_lm.desc_of(cfg)
+    n = ctypes.c_int64()
+    assert xnp.load_library().xnp_flow_lm_weights_size(ctypes.byref(d), ctypes.byref(n)) == 0
+    assert n.value == xnp.flow_lm.blob_size(cfg)
+    small = xnp.FlowLMConfig(num_layers=2, flow_depth=3, n_bins=10, flow_dim=256, dim_feedforward=1024)
+    d = xnp.flow_lm.desc_of(small)
+    assert xnp.load_library().xnp_flow_lm_weights_size(ctypes.byref(d), ctypes.byref(n)) == 0
+    assert n.value == xnp.flow_lm.blob_size(small)
+
+
+def test_flow_lm_refuses_a_pool_it_does_not_fit():
+    cfg = xnp.FlowLMConfig(num_layers=2, flow_depth=1, n_bins=10)
+    pool = xnp.KvPool(num_layers=2, num_heads=8, num_blocks=8, max_streams=2, max_blocks_per_stream=4,
+                      host_only=True, cache_dtype="f32", act_dtype="f32")
+    with pytest.raises(xnp.XnpError):  # a host-only pool has no device
+        xnp.FlowLM(pool, cfg, np.zeros(xnp.flow_lm.blob_size(cfg), np.float32))
+    with pytest.raises(xnp.XnpError):  # the blob does not match the layout
+        xnp.FlowLM(pool, cfg, np.zeros(10, np.float32))

@@ -1,0 +1,95 @@
+"""GPU parity of the flow LM around the transformer (flow_lm.rs, mlp.rs, conditioners.rs,
+tts_model.rs:297-378) on f32 kernels and an f32 pool, through the C ABI, against the oracle on the
+same weights, tokens and noise.
+
+Bar: 1e-5 relative for fp32 (latents per frame, EOS logits against max(1, |logit|)).  Cache rows
+come from projections the GPU sums in its own order, so they are held to the same bar.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import oracle, xnp
+from helpers import rel_err
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+fl = xnp.flow_lm
+
+
+def run_pair(cfg, blob, tokens, frames, noise, cap):
+    n = tokens.shape[0]
+    H, D = cfg.num_heads, cfg.d_model // cfg.num_heads
+    mbps = (cap + 15) // 16
+    pool = xnp.KvPool(num_layers=cfg.num_layers, num_heads=H, num_blocks=n * mbps + 8, max_streams=n,
+                      max_blocks_per_stream=mbps, cache_dtype="f32", act_dtype="f32", max_pos=cap + 16, page_seed=3)
+    ids = [pool.init_state(cap) for _ in range(n)]
+    lm = xnp.FlowLM(pool, cfg, blob, max_rows=n * tokens.shape[1])
+    orc = oracle.FlowLM(cfg, blob)
+    sts = [orc.stream(cap) for _ in range(n)]
+    lm.prompt_text(ids, tokens)
+    for i in range(n):
+        orc.prompt_text(sts[i], tokens[i])
+    lat_in = None
+    out = torch.empty((n, cfg.ldim), dtype=torch.float32, device=DEV)
+    eos = torch.empty(n, dtype=torch.float32, device=DEV)
+    nz = torch.from_numpy(noise).to(DEV)
+    want_lat = [None] * n
+    worst = 0.0
+    for f in range(frames):
+        lm.step(ids, lat_in, nz[f], out, eos)
+        torch.cuda.synchronize()
+        got_lat, got_eos = out.cpu().numpy(), eos.cpu().numpy()
+        for i in range(n):
+            wl, we = orc.step(sts[i], want_lat[i], noise[f, i])
+            want_lat[i] = wl
+            e = max(rel_err(got_lat[i], wl), abs(got_eos[i] - we) / max(1.0, abs(we)))
+            worst = max(worst, e)
+            assert e <= 1e-5, (f, i, e)
+        lat_in = out.clone()
+    return pool, ids, sts, worst
+
+
+def test_flow_lm_prompt_and_frames_match_the_oracle():
+    cfg = fl.FlowLMConfig(num_layers=2, flow_depth=2, flow_dim=256, dim_feedforward=1024, n_bins=100)
+    blob = fl.random_weights(cfg, 90, std=0.05, unit_norms=False)
+    rng = np.random.default_rng(91)
+    tokens = rng.integers(0, cfg.n_bins + 1, (2, 5)).astype(np.int32)
+    noise = (0.5 * rng.standard_normal((6, 2, cfg.ldim))).astype(np.float32)
+    pool, ids, sts, _ = run_pair(cfg, blob, tokens, 6, noise, 32)
+    # the cache rows the prompt and the frames wrote, within the same bar
+    for i in range(2):
+        n = sts[i].current_end
+        assert n == 11
+        for layer in range(cfg.num_layers):
+            for kv in (0, 1):
+                rows = torch.empty((n, cfg.num_heads, 64), dtype=torch.float32, device=DEV)
+                pool.read_rows(ids[i], layer, kv, 0, rows)
+                torch.cuda.synchronize()
+                vals, _, _ = sts[i].read_rows(layer, kv, 0, n)
+                assert rel_err(rows.cpu().numpy(), vals) <= 1e-5, (i, layer, kv)
+
+
+def test_phonon_31m_shape_64_tokens_then_200_frames_at_temperature_0():
+    # the single-stream configuration: 6 layers x 512, 8 heads, FF 2048, ldim 32, 4001-row LUT,
+    # flow net 512 x 6, 1 LSD step; N(0, 0.02) linears, unit norms; 64 tokens, 200 greedy frames
+    cfg = fl.FlowLMConfig()
+    blob = fl.random_weights(cfg, 20261201)
+    rng = np.random.default_rng(20261201)
+    tokens = rng.integers(0, cfg.n_bins + 1, (1, 64)).astype(np.int32)
+    noise = np.zeros((200, 1, cfg.ldim), np.float32)  # temperature 0 (flow_lm.rs:494-500)
+    _, _, sts, worst = run_pair(cfg, blob, tokens, 200, noise, 868)
+    assert sts[0].current_end == 264
+    print(f"worst relative error over 200 frames: {worst:.2e}")
+
+
+def test_bad_tokens_are_refused_and_change_nothing():
+    cfg = fl.FlowLMConfig(num_layers=1, flow_depth=1, flow_dim=256, dim_feedforward=512, n_bins=10)
+    blob = fl.random_weights(cfg, 92)
+    pool = xnp.KvPool(num_layers=1, num_heads=8, num_blocks=8, max_streams=1, max_blocks_per_stream=4,
+                      cache_dtype="f32", act_dtype="f32")
+    sid = pool.init_state(64)
+    lm = xnp.FlowLM(pool, cfg, blob, max_rows=8)
+    with pytest.raises(xnp.XnpError):
+        lm.prompt_text([sid], np.array([[1, 2, 11]], np.int32))
+    assert pool.current_end(sid) == 0

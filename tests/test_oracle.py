@@ -493,3 +493,138 @@ def test_layer_step_is_the_reference_layer(KVH):
             assert rel_err(got[i], want) < 2e-5, (t, i)
         oracle.batch_commit_t(sts, t)
         pos += t
+
+
+# ---- the flow LM around the transformer (flow_lm.rs, mlp.rs, conditioners.rs) -------------------
+flow_lm = __import__("xn_ptts_amd.flow_lm", fromlist=["flow_lm"])
+
+
+def _small_flow_cfg(**kw):
+    base = dict(d_model=512, num_heads=8, num_layers=2, dim_feedforward=1024, ldim=32, n_bins=100,
+                flow_dim=256, flow_depth=2, lsd_decode_steps=1)
+    base.update(kw)
+    return flow_lm.FlowLMConfig(**base)
+
+
+def _t(a):
+    return torch.from_numpy(np.asarray(a, np.float64))
+
+
+def _torch_time_embed(W, i, t, kind):
+    p = f"time_embed.{i}."
+    args = t * _t(W[p + "freqs"])
+    emb = torch.cat([torch.cos(args), torch.sin(args)])
+    h = torch.nn.functional.silu(torch.nn.functional.linear(emb, _t(W[p + "mlp0.w"]), _t(W[p + "mlp0.b"])))
+    h = torch.nn.functional.linear(h, _t(W[p + "mlp2.w"]), _t(W[p + "mlp2.b"]))
+    if kind == "rms":
+        return torch.nn.functional.rms_norm(h, (h.shape[-1],), _t(W[p + "alpha"]), eps=1e-5)
+    return h / torch.sqrt(torch.var(h, unbiased=True) + 1e-5) * _t(W[p + "alpha"])
+
+
+def _torch_flow_net(W, cfg, c, temb, x0):
+    lin = lambda x, n: torch.nn.functional.linear(x, _t(W[n + ".w"]), _t(W[n + ".b"]))
+    F = cfg.flow_dim
+    x = lin(_t(x0), "input_proj")
+    ya = torch.nn.functional.silu(temb + lin(c, "cond_embed"))
+    for j in range(cfg.flow_depth):
+        p = f"res_blocks.{j}."
+        ada = lin(ya, p + "ada")
+        h = torch.nn.functional.layer_norm(x, (F,), _t(W[p + "in_ln.w"]), _t(W[p + "in_ln.b"]), eps=1e-6)
+        h = h * (1 + ada[F:2 * F]) + ada[:F]
+        h = lin(torch.nn.functional.silu(lin(h, p + "mlp0")), p + "mlp2")
+        x = x + ada[2 * F:] * h
+    ada = lin(ya, "final.ada")
+    h = torch.nn.functional.layer_norm(x, (F,), eps=1e-6) * (1 + ada[F:]) + ada[:F]
+    return lin(h, "final.linear")
+
+
+@pytest.mark.parametrize("kind", ["rms", "rms_var"])
+def test_flow_time_embedding_matches_torch(kind):
+    cfg = _small_flow_cfg(time_rms_norm=kind)
+    blob = flow_lm.random_weights(cfg, 80, unit_norms=False)
+    W = flow_lm.split(cfg, blob)
+    m = oracle.FlowLM(cfg, blob)
+    for s, t in [(0.0, 1.0), (0.25, 0.5)]:
+        want = (_torch_time_embed(W, 0, s, kind) + _torch_time_embed(W, 1, t, kind)) / 2
+        assert rel_err(m.time_embedding(s, t), want.numpy()) < 1e-5
+
+
+def test_flow_net_matches_torch():
+    cfg = _small_flow_cfg()
+    blob = flow_lm.random_weights(cfg, 81, std=0.05, unit_norms=False)
+    W = flow_lm.split(cfg, blob)
+    m = oracle.FlowLM(cfg, blob)
+    rng = np.random.default_rng(82)
+    c, x0 = rng.standard_normal(cfg.d_model), rng.standard_normal(cfg.ldim)
+    temb = m.time_embedding(0.0, 1.0)
+    want = _torch_flow_net(W, cfg, _t(c), _t(temb), x0)
+    assert rel_err(m.flow_net(c, temb, x0), want.numpy()) < 1e-5
+
+
+def _torch_flow_lm(cfg, W, ids, frames, noise):
+    """prompt_text then `frames` generate steps (flow_lm.rs:296-432, tts_model.rs:297-378) in torch f64."""
+    H, dm = cfg.num_heads, cfg.d_model
+    D = dm // H
+    hist = [{} for _ in range(cfg.num_layers)]
+
+    def rope(a, p):
+        c, s = oracle.rope_row(D, cfg.max_period, float(p), "f32")
+        out = a.clone()
+        out[..., 0::2] = a[..., 0::2] * _t(c) - a[..., 1::2] * _t(s)
+        out[..., 1::2] = a[..., 0::2] * _t(s) + a[..., 1::2] * _t(c)
+        return out
+
+    def transformer(x, pos):
+        T = x.shape[0]
+        for l in range(cfg.num_layers):
+            p = f"layers.{l}."
+            h = torch.nn.functional.layer_norm(x, (dm,), _t(W[p + "norm1.w"]), _t(W[p + "norm1.b"]), eps=1e-5)
+            qkv = h @ _t(W[p + "in_proj"]).T
+            q, k, v = (qkv[:, i * dm:(i + 1) * dm].reshape(T, H, D) for i in range(3))
+            q = torch.stack([rope(q[i], pos + i) for i in range(T)])
+            k = torch.stack([rope(k[i], pos + i) for i in range(T)])
+            hs = hist[l]
+            hs["k"] = torch.cat([hs["k"], k]) if "k" in hs else k
+            hs["v"] = torch.cat([hs["v"], v]) if "v" in hs else v
+            n = hs["k"].shape[0]
+            att = torch.einsum("thd,nhd->thn", q, hs["k"]) / math.sqrt(D)
+            causal = torch.arange(n)[None, :] <= (n - T + torch.arange(T))[:, None]
+            att = att.masked_fill(~causal[:, None, :], float("-inf")).softmax(-1)
+            x = x + torch.einsum("thn,nhd->thd", att, hs["v"]).reshape(T, dm) @ _t(W[p + "out_proj"]).T
+            h = torch.nn.functional.layer_norm(x, (dm,), _t(W[p + "norm2.w"]), _t(W[p + "norm2.b"]), eps=1e-5)
+            f = torch.nn.functional.gelu(h @ _t(W[p + "linear1"]).T)
+            x = x + f @ _t(W[p + "linear2"]).T
+        return x
+
+    transformer(_t(W["conditioner.embed"][ids]), 0)
+    pos, latent, outs = len(ids), _t(W["bos_emb"]), []
+    temb = (_torch_time_embed(W, 0, 0.0, cfg.time_rms_norm) + _torch_time_embed(W, 1, 1.0, cfg.time_rms_norm)) / 2
+    for f in range(frames):
+        x = transformer((_t(W["input_linear"]) @ latent)[None, :], pos)[0]
+        pos += 1
+        t_out = torch.nn.functional.layer_norm(x, (dm,), _t(W["out_norm.w"]), _t(W["out_norm.b"]), eps=1e-5)
+        eos = float(_t(W["out_eos.w"])[0] @ t_out + _t(W["out_eos.b"])[0])
+        latent = _t(noise[f]) + _torch_flow_net(W, cfg, t_out, temb, noise[f])
+        outs.append((latent.numpy().copy(), eos))
+    return outs
+
+
+def test_flow_lm_prompt_and_frames_match_torch():
+    # a 5-token prompt, then 4 frames (from bos_emb, then each frame's latent), noise N(0, 0.5)
+    cfg = _small_flow_cfg()
+    blob = flow_lm.random_weights(cfg, 83, std=0.05, unit_norms=False)
+    W = flow_lm.split(cfg, blob)
+    m = oracle.FlowLM(cfg, blob)
+    rng = np.random.default_rng(84)
+    ids = rng.integers(0, cfg.n_bins + 1, 5)
+    noise = (0.5 * rng.standard_normal((4, cfg.ldim))).astype(np.float32)
+    want = _torch_flow_lm(cfg, W, ids, 4, noise)
+    st = m.stream(32)
+    m.prompt_text(st, ids)
+    lat = None
+    for f in range(4):
+        lat, eos = m.step(st, lat, noise[f])
+        wl, we = want[f]
+        assert rel_err(lat, wl) < 2e-5, f
+        assert abs(eos - we) <= 2e-5 * max(1.0, abs(we)), f
+    assert st.current_end == 9

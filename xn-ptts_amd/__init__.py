@@ -6,7 +6,8 @@ so load it by path, e.g. importlib.util.spec_from_file_location("xn_ptts_amd", <
 """
 from .kv import (BF16, BLOCK, DTYPES, F32, I8, LIB_PATH, RING_ABSOLUTE, RING_SHIFT, KvPool, LayerWeights,
                  XnpError, frame_budget, layer_norm, linear_q8, load_library, quantize_rows, seq_budget)
+from .flow_lm import FlowLM, FlowLMConfig
 
-__all__ = ["KvPool", "LayerWeights", "XnpError", "load_library", "frame_budget", "seq_budget", "layer_norm",
+__all__ = ["KvPool", "FlowLM", "FlowLMConfig", "LayerWeights", "XnpError", "load_library", "frame_budget", "seq_budget", "layer_norm",
            "linear_q8", "quantize_rows", "LIB_PATH", "F32", "BF16", "I8", "BLOCK", "DTYPES", "RING_SHIFT",
            "RING_ABSOLUTE"]

@@ -1,0 +1,342 @@
+// Host side of the flow LM around the paged transformer (ptts/src/flow_lm.rs, mlp.rs,
+// conditioners.rs, tts_model.rs:297-378) on f32 kernels: weights uploaded once, then text
+// prompts and frames for batches of a pool's streams.  The transformer's attention is the
+// pool's (xnp_attend); everything else is kernels.hip's f32 linears, LayerNorms and gather.
+#include "../../include/xnp_kv.h"
+#include "xnp_internal.h"
+
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <vector>
+
+using namespace xnp;
+
+namespace {
+
+constexpr int kFreqDim = 256; // the time embedders' frequency embedding (mlp.rs:186-193)
+constexpr int kMaxLayers = 64;
+
+// Offsets (in floats) of the weight blob's tensors, in the order include/xnp_kv.h documents.
+struct Layout {
+    size_t embed, in_lin, bos;
+    size_t ln1_w[kMaxLayers], ln1_b[kMaxLayers], wqkv[kMaxLayers], wout[kMaxLayers];
+    size_t ln2_w[kMaxLayers], ln2_b[kMaxLayers], w1[kMaxLayers], w2[kMaxLayers];
+    size_t on_w, on_b, eos_w, eos_b;
+    size_t te_freqs[2], te_w1[2], te_b1[2], te_w2[2], te_b2[2], te_alpha[2];
+    size_t cond_w, cond_b, inp_w, inp_b;
+    size_t rb_lnw[kMaxLayers], rb_lnb[kMaxLayers], rb_w1[kMaxLayers], rb_b1[kMaxLayers];
+    size_t rb_w2[kMaxLayers], rb_b2[kMaxLayers], rb_aw[kMaxLayers], rb_ab[kMaxLayers];
+    size_t fin_aw, fin_ab, fin_w, fin_b;
+    size_t total;
+};
+
+bool layout_of(const xnp_flow_lm_desc &d, Layout &L) {
+    if (d.num_layers <= 0 || d.num_layers > kMaxLayers || d.flow_depth < 0 || d.flow_depth > kMaxLayers ||
+        d.d_model <= 0 || d.num_heads <= 0 || d.d_model % d.num_heads || d.ldim <= 0 || d.flow_dim <= 0 ||
+        d.ff <= 0 || d.n_bins <= 0 || d.lsd_steps <= 0)
+        return false;
+    const size_t dm = d.d_model, F = d.flow_dim, ld = d.ldim, ff = d.ff, fq = kFreqDim;
+    size_t o = 0;
+    auto take = [&](size_t &field, size_t n) { field = o, o += n; };
+    take(L.embed, ((size_t)d.n_bins + 1) * dm);
+    take(L.in_lin, dm * ld);
+    take(L.bos, ld);
+    for (int l = 0; l < d.num_layers; l++) {
+        take(L.ln1_w[l], dm), take(L.ln1_b[l], dm), take(L.wqkv[l], 3 * dm * dm), take(L.wout[l], dm * dm);
+        take(L.ln2_w[l], dm), take(L.ln2_b[l], dm), take(L.w1[l], ff * dm), take(L.w2[l], dm * ff);
+    }
+    take(L.on_w, dm), take(L.on_b, dm), take(L.eos_w, dm), take(L.eos_b, 1);
+    for (int i = 0; i < 2; i++) {
+        take(L.te_freqs[i], fq / 2), take(L.te_w1[i], F * fq), take(L.te_b1[i], F);
+        take(L.te_w2[i], F * F), take(L.te_b2[i], F), take(L.te_alpha[i], F);
+    }
+    take(L.cond_w, F * dm), take(L.cond_b, F), take(L.inp_w, F * ld), take(L.inp_b, F);
+    for (int j = 0; j < d.flow_depth; j++) {
+        take(L.rb_lnw[j], F), take(L.rb_lnb[j], F), take(L.rb_w1[j], F * F), take(L.rb_b1[j], F);
+        take(L.rb_w2[j], F * F), take(L.rb_b2[j], F), take(L.rb_aw[j], 3 * F * F), take(L.rb_ab[j], 3 * F);
+    }
+    take(L.fin_aw, 2 * F * F), take(L.fin_ab, 2 * F), take(L.fin_w, ld * F), take(L.fin_b, ld);
+    L.total = o;
+    return true;
+}
+
+// y = x W^T + b on the host, f32, k ascending (the time embedders, computed once at load).
+void host_linear(const float *x, int k, const float *w, const float *b, int n, float *y) {
+    for (int j = 0; j < n; j++) {
+        float acc = 0.f;
+        for (int i = 0; i < k; i++) acc += x[i] * w[(size_t)j * k + i];
+        y[j] = acc + b[j];
+    }
+}
+
+// TimestepEmbedder::forward and its norm (mlp.rs:55-86) for time t.
+void host_time_embed(const xnp_flow_lm_desc &d, const float *blob, const Layout &L, int i, float t, float *out) {
+    const int F = d.flow_dim, half = kFreqDim / 2;
+    float emb[kFreqDim];
+    for (int j = 0; j < half; j++) {
+        const float a = t * blob[L.te_freqs[i] + j];
+        emb[j] = cosf(a);
+        emb[half + j] = sinf(a);
+    }
+    std::vector<float> h(F);
+    host_linear(emb, kFreqDim, blob + L.te_w1[i], blob + L.te_b1[i], F, h.data());
+    for (int j = 0; j < F; j++) h[j] = h[j] / (1.0f + expf(-h[j]));
+    host_linear(h.data(), F, blob + L.te_w2[i], blob + L.te_b2[i], F, out);
+    const float *alpha = blob + L.te_alpha[i];
+    const float eps = 1e-5f, n = (float)F;
+    if (d.time_norm == XNP_TIME_RMS_VAR) { // centred, unbiased variance
+        float s = 0.f;
+        for (int j = 0; j < F; j++) s += out[j];
+        const float mean = s * (1.0f / n);
+        float v = 0.f;
+        for (int j = 0; j < F; j++) {
+            const float e = out[j] - mean;
+            v += e * e;
+        }
+        const float inv = 1.0f / sqrtf(v * (1.0f / (n - 1.0f)) + eps);
+        for (int j = 0; j < F; j++) out[j] = out[j] * inv * alpha[j];
+    } else { // x * alpha / sqrt(mean(x^2) + eps)
+        float s = 0.f;
+        for (int j = 0; j < F; j++) s += out[j] * out[j];
+        const float inv = 1.0f / sqrtf(s * (1.0f / n) + eps);
+        for (int j = 0; j < F; j++) out[j] = out[j] * inv * alpha[j];
+    }
+}
+
+} // namespace
+
+struct xnp_flow_lm {
+    xnp_pool *pool = nullptr;
+    xnp_flow_lm_desc d{};
+    Layout L{};
+    float *w = nullptr;    // the weight blob on the device
+    float *temb = nullptr; // [lsd_steps][F]: SimpleMLPAdaLN::time_embedding of each solver step
+    // scratch for max_rows rows
+    float *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *f = nullptr;
+    float *tout = nullptr, *ya = nullptr, *ada = nullptr, *xf = nullptr, *hf = nullptr, *h2 = nullptr;
+    int32_t *dids = nullptr;
+    int32_t *hids = nullptr; // pinned staging of token ids
+    std::vector<void *> allocs;
+    const float *W(size_t off) const { return w + off; }
+};
+
+static void fl_free(xnp_flow_lm *lm) {
+    for (void *p : lm->allocs) (void)hipFree(p);
+    if (lm->hids) (void)hipHostFree(lm->hids);
+    delete lm;
+}
+
+extern "C" xnp_status xnp_flow_lm_weights_size(const xnp_flow_lm_desc *desc, int64_t *nfloats) {
+    if (!desc || !nfloats) return pool_fail(XNP_E_INVALID, "null argument");
+    Layout L;
+    if (!layout_of(*desc, L)) return pool_fail(XNP_E_INVALID, "bad flow LM shape");
+    *nfloats = (int64_t)L.total;
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_flow_lm_create(xnp_pool *pool, const xnp_flow_lm_desc *desc, const float *weights,
+                                         int64_t nfloats, xnp_flow_lm **out) {
+    if (!pool || !desc || !weights || !out) return pool_fail(XNP_E_INVALID, "null argument");
+    *out = nullptr;
+    const xnp_pool_desc &pd = *pool_desc(pool);
+    const xnp_flow_lm_desc &d = *desc;
+    Layout L;
+    if (!layout_of(d, L)) return pool_fail(XNP_E_INVALID, "bad flow LM shape");
+    if ((int64_t)L.total != nfloats)
+        return pool_fail(XNP_E_INVALID, "the weights hold %lld floats; the layout needs %lld", (long long)nfloats,
+                         (long long)L.total);
+    if (pool_host_only(pool)) return pool_fail(XNP_E_STATE, "a host-only pool has no device");
+    if (pd.cache_dtype != XNP_F32 || pd.act_dtype != XNP_F32)
+        return pool_fail(XNP_E_INVALID, "the flow LM runs on an f32 pool (f32 cache and activations)");
+    if (pd.num_layers != d.num_layers || pd.num_heads != d.num_heads || pd.num_kv_heads != d.num_heads ||
+        pd.head_dim * d.num_heads != d.d_model)
+        return pool_fail(XNP_E_INVALID, "the pool's layers and heads do not match the flow LM's");
+    if (d.max_rows <= 0) return pool_fail(XNP_E_INVALID, "max_rows %d", d.max_rows);
+    if (d.d_model > 2048 || d.flow_dim > 2048 || d.ff > 2048 || d.ldim > 2048)
+        return pool_fail(XNP_E_INVALID, "widths above 2048 are not supported");
+    if (d.gelu != XNP_GELU_ERF && d.gelu != XNP_GELU_TANH) return pool_fail(XNP_E_INVALID, "gelu %d", d.gelu);
+    if (d.time_norm != XNP_TIME_RMS && d.time_norm != XNP_TIME_RMS_VAR)
+        return pool_fail(XNP_E_INVALID, "time norm %d", d.time_norm);
+
+    xnp_flow_lm *lm = new (std::nothrow) xnp_flow_lm();
+    if (!lm) return pool_fail(XNP_E_INVALID, "out of host memory");
+    lm->pool = pool;
+    lm->d = d;
+    lm->L = L;
+    hipError_t e = hipSetDevice(pd.device);
+    auto fail_hip = [&](hipError_t err, const char *what) {
+        fl_free(lm);
+        return pool_fail(XNP_E_HIP, "%s: %s", what, hipGetErrorString(err));
+    };
+    if (e != hipSuccess) return fail_hip(e, "hipSetDevice");
+    auto dalloc = [&](void **p, size_t bytes) {
+        hipError_t r = hipMalloc(p, bytes);
+        if (r == hipSuccess) lm->allocs.push_back(*p);
+        return r;
+    };
+    const size_t M = d.max_rows, dm = d.d_model, F = d.flow_dim;
+    struct {
+        float **p;
+        size_t n;
+    } bufs[] = {{&lm->w, L.total}, {&lm->temb, (size_t)d.lsd_steps * F}, {&lm->x, M * dm}, {&lm->h, M * dm},
+                {&lm->q, M * dm},  {&lm->k, M * dm},  {&lm->v, M * dm}, {&lm->att, M * dm},
+                {&lm->f, M * (size_t)d.ff}, {&lm->tout, M * dm}, {&lm->ya, M * F}, {&lm->ada, M * 3 * F},
+                {&lm->xf, M * F}, {&lm->hf, M * F}, {&lm->h2, M * F}};
+    for (auto &b : bufs)
+        if ((e = dalloc((void **)b.p, sizeof(float) * b.n)) != hipSuccess) return fail_hip(e, "flow LM buffers");
+    if ((e = dalloc((void **)&lm->dids, sizeof(int32_t) * M)) != hipSuccess) return fail_hip(e, "flow LM ids");
+    if ((e = hipHostMalloc((void **)&lm->hids, sizeof(int32_t) * M, hipHostMallocDefault)) != hipSuccess)
+        return fail_hip(e, "pinned ids");
+    if ((e = hipMemcpy(lm->w, weights, sizeof(float) * L.total, hipMemcpyHostToDevice)) != hipSuccess)
+        return fail_hip(e, "weight upload");
+    // lsd_time_embeddings (flow_lm.rs:82-95): times (i / steps, (i + 1) / steps), averaged over the
+    // two embedders (mlp.rs:201-212).  They depend on nothing but the weights: once, at load.
+    std::vector<float> temb((size_t)d.lsd_steps * F), b(F);
+    for (int i = 0; i < d.lsd_steps; i++) {
+        float *o = temb.data() + (size_t)i * F;
+        host_time_embed(d, weights, L, 0, (float)i / (float)d.lsd_steps, o);
+        host_time_embed(d, weights, L, 1, (float)(i + 1) / (float)d.lsd_steps, b.data());
+        for (size_t j = 0; j < F; j++) o[j] = (o[j] + b[j]) * 0.5f;
+    }
+    if ((e = hipMemcpy(lm->temb, temb.data(), sizeof(float) * temb.size(), hipMemcpyHostToDevice)) != hipSuccess)
+        return fail_hip(e, "time embedding upload");
+    *out = lm;
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_flow_lm_destroy(xnp_flow_lm *lm) {
+    if (!lm) return XNP_OK;
+    (void)hipSetDevice(pool_desc(lm->pool)->device);
+    fl_free(lm);
+    return XNP_OK;
+}
+
+#define FL_TRY(expr, what)                                                                         \
+    do {                                                                                           \
+        hipError_t e_ = (expr);                                                                    \
+        if (e_ != hipSuccess) return pool_fail(XNP_E_HIP, "%s: %s", what, hipGetErrorString(e_)); \
+    } while (0)
+
+// The transformer (StreamingTransformer::forward, transformer.rs:742-808, with the layers of
+// transformer.rs:591-634) over the M rows in lm->x, for the open batch.
+static xnp_status fl_transformer(xnp_flow_lm *lm, int M, void *hip_stream) {
+    const xnp_flow_lm_desc &d = lm->d;
+    const Layout &L = lm->L;
+    hipStream_t hs = (hipStream_t)hip_stream;
+    const int dm = d.d_model, ff = d.ff;
+    const float scale = 1.0f / std::sqrt((float)(dm / d.num_heads));
+    for (int l = 0; l < d.num_layers; l++) {
+        FL_TRY(launch_ln_f32(lm->x, M, dm, lm->W(L.ln1_w[l]), lm->W(L.ln1_b[l]), 1e-5f, nullptr, nullptr, 0, lm->h, hs),
+               "norm1");
+        LinOut qkv;
+        qkv.nseg = 3;
+        qkv.out[0] = lm->q, qkv.ld[0] = dm, qkv.col0[0] = 0;
+        qkv.out[1] = lm->k, qkv.ld[1] = dm, qkv.col0[1] = dm;
+        qkv.out[2] = lm->v, qkv.ld[2] = dm, qkv.col0[2] = 2 * dm;
+        FL_TRY(launch_linear_f32(lm->h, dm, M, dm, lm->W(L.wqkv[l]), nullptr, 3 * dm, kLinStore, qkv, hs), "in_proj");
+        if (xnp_status st = xnp_attend(lm->pool, l, lm->q, lm->k, lm->v, lm->att, scale, hip_stream)) return st;
+        LinOut res;
+        res.out[0] = lm->x, res.ld[0] = dm;
+        FL_TRY(launch_linear_f32(lm->att, dm, M, dm, lm->W(L.wout[l]), nullptr, dm, kLinResidual, res, hs), "out_proj");
+        FL_TRY(launch_ln_f32(lm->x, M, dm, lm->W(L.ln2_w[l]), lm->W(L.ln2_b[l]), 1e-5f, nullptr, nullptr, 0, lm->h, hs),
+               "norm2");
+        LinOut hid;
+        hid.out[0] = lm->f, hid.ld[0] = ff;
+        FL_TRY(launch_linear_f32(lm->h, dm, M, dm, lm->W(L.w1[l]), nullptr, ff,
+                                 d.gelu == XNP_GELU_ERF ? kLinGeluErf : kLinGeluTanh, hid, hs),
+               "linear1");
+        FL_TRY(launch_linear_f32(lm->f, ff, M, ff, lm->W(L.w2[l]), nullptr, dm, kLinResidual, res, hs), "linear2");
+    }
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_flow_lm_prompt_text(xnp_flow_lm *lm, const int32_t *ids, int32_t n, const int32_t *tokens,
+                                              int32_t t, void *hip_stream) {
+    if (!lm || (n > 0 && (!ids || !tokens))) return pool_fail(XNP_E_INVALID, "null argument");
+    if (n < 0 || t < 0) return pool_fail(XNP_E_INVALID, "%d streams of %d tokens", n, t);
+    if (n == 0 || t == 0) return XNP_OK;
+    const int64_t M = (int64_t)n * t;
+    if (M > lm->d.max_rows) return pool_fail(XNP_E_INVALID, "%lld rows; the flow LM holds %d", (long long)M, lm->d.max_rows);
+    for (int64_t i = 0; i < M; i++) // LUTConditioner::embed_tokens refuses ids past its table
+        if (tokens[i] < 0 || tokens[i] > lm->d.n_bins)
+            return pool_fail(XNP_E_INVALID, "token id %d is past this checkpoint's %d-entry embedding table", tokens[i],
+                             lm->d.n_bins + 1);
+    hipStream_t hs = (hipStream_t)hip_stream;
+    FL_TRY(hipSetDevice(pool_desc(lm->pool)->device), "hipSetDevice");
+    // the previous call's upload from the staging buffer has finished once the stream reaches here
+    FL_TRY(hipStreamSynchronize(hs), "staging");
+    std::memcpy(lm->hids, tokens, sizeof(int32_t) * M);
+    FL_TRY(hipMemcpyAsync(lm->dids, lm->hids, sizeof(int32_t) * M, hipMemcpyHostToDevice, hs), "token upload");
+    if (xnp_status st = xnp_batch_begin(lm->pool, ids, n, t, hip_stream)) return st;
+    FL_TRY(launch_embed_f32(lm->W(lm->L.embed), lm->dids, (int)M, lm->d.d_model, lm->x, hs), "embed");
+    if (xnp_status st = fl_transformer(lm, (int)M, hip_stream)) {
+        (void)xnp_batch_abort(lm->pool);
+        return st;
+    }
+    return xnp_batch_end(lm->pool);
+}
+
+extern "C" xnp_status xnp_flow_lm_step(xnp_flow_lm *lm, const int32_t *ids, int32_t n, const float *latent_in,
+                                       const float *noise, float *latent_out, float *eos_logit, void *hip_stream) {
+    if (!lm || (n > 0 && (!ids || !noise || !latent_out || !eos_logit))) return pool_fail(XNP_E_INVALID, "null argument");
+    if (n < 0 || n > lm->d.max_rows) return pool_fail(XNP_E_INVALID, "%d streams; the flow LM holds %d rows", n, lm->d.max_rows);
+    if (n == 0) return XNP_OK;
+    const xnp_flow_lm_desc &d = lm->d;
+    const Layout &L = lm->L;
+    hipStream_t hs = (hipStream_t)hip_stream;
+    const int dm = d.d_model, F = d.flow_dim, ld = d.ldim, M = n;
+    FL_TRY(hipSetDevice(pool_desc(lm->pool)->device), "hipSetDevice");
+    // input_linear of the previous latents, or of bos_emb for every row (flow_lm.rs:314-324, 423-427)
+    LinOut xo;
+    xo.out[0] = lm->x, xo.ld[0] = dm;
+    FL_TRY(launch_linear_f32(latent_in ? latent_in : lm->W(L.bos), latent_in ? ld : 0, M, ld, lm->W(L.in_lin), nullptr,
+                             dm, kLinStore, xo, hs),
+           "input_linear");
+    if (xnp_status st = xnp_batch_begin(lm->pool, ids, n, 1, hip_stream)) return st;
+    if (xnp_status st = fl_transformer(lm, M, hip_stream)) {
+        (void)xnp_batch_abort(lm->pool);
+        return st;
+    }
+    if (xnp_status st = xnp_batch_end(lm->pool)) return st;
+    // out_norm (flow_lm.rs:315), the EOS logit (flow_lm.rs:366)
+    FL_TRY(launch_ln_f32(lm->x, M, dm, lm->W(L.on_w), lm->W(L.on_b), 1e-5f, nullptr, nullptr, 0, lm->tout, hs), "out_norm");
+    LinOut eo;
+    eo.out[0] = eos_logit, eo.ld[0] = 1;
+    FL_TRY(launch_linear_f32(lm->tout, dm, M, dm, lm->W(L.eos_w), lm->W(L.eos_b), 1, kLinStore, eo, hs), "out_eos");
+    // lsd_decode (flow_lm.rs:97-110): each step x += flow_net(t_out, t_emb_i, x) / steps
+    for (int i = 0; i < d.lsd_steps; i++) {
+        const float *cur = i == 0 ? noise : latent_out;
+        LinOut y;
+        y.out[0] = lm->ya, y.ld[0] = F, y.aux = lm->temb + (size_t)i * F;
+        FL_TRY(launch_linear_f32(lm->tout, dm, M, dm, lm->W(L.cond_w), lm->W(L.cond_b), F, kLinSiluAddVec, y, hs),
+               "cond_embed");
+        LinOut xf;
+        xf.out[0] = lm->xf, xf.ld[0] = F;
+        FL_TRY(launch_linear_f32(cur, ld, M, ld, lm->W(L.inp_w), lm->W(L.inp_b), F, kLinStore, xf, hs), "input_proj");
+        for (int r = 0; r < d.flow_depth; r++) { // ResBlock (mlp.rs:113-131)
+            LinOut a;
+            a.out[0] = lm->ada, a.ld[0] = 3 * F;
+            FL_TRY(launch_linear_f32(lm->ya, F, M, F, lm->W(L.rb_aw[r]), lm->W(L.rb_ab[r]), 3 * F, kLinStore, a, hs),
+                   "adaLN_modulation");
+            FL_TRY(launch_ln_f32(lm->xf, M, F, lm->W(L.rb_lnw[r]), lm->W(L.rb_lnb[r]), 1e-6f, lm->ada, lm->ada + F, 3 * F,
+                                 lm->hf, hs),
+                   "in_ln");
+            LinOut s1;
+            s1.out[0] = lm->h2, s1.ld[0] = F;
+            FL_TRY(launch_linear_f32(lm->hf, F, M, F, lm->W(L.rb_w1[r]), lm->W(L.rb_b1[r]), F, kLinSilu, s1, hs), "mlp.0");
+            LinOut g;
+            g.out[0] = lm->xf, g.ld[0] = F, g.aux = lm->ada + 2 * F, g.ld_aux = 3 * F;
+            FL_TRY(launch_linear_f32(lm->h2, F, M, F, lm->W(L.rb_w2[r]), lm->W(L.rb_b2[r]), F, kLinGated, g, hs), "mlp.2");
+        }
+        LinOut a; // FinalLayer (mlp.rs:155-163)
+        a.out[0] = lm->ada, a.ld[0] = 2 * F;
+        FL_TRY(launch_linear_f32(lm->ya, F, M, F, lm->W(L.fin_aw), lm->W(L.fin_ab), 2 * F, kLinStore, a, hs),
+               "final adaLN_modulation");
+        FL_TRY(launch_ln_f32(lm->xf, M, F, nullptr, nullptr, 1e-6f, lm->ada, lm->ada + F, 2 * F, lm->hf, hs), "norm_final");
+        LinOut o;
+        o.out[0] = latent_out, o.ld[0] = ld, o.aux = cur, o.ld_aux = ld, o.alpha = 1.0f / (float)d.lsd_steps;
+        FL_TRY(launch_linear_f32(lm->hf, F, M, F, lm->W(L.fin_w), lm->W(L.fin_b), ld, kLinAxpy, o, hs), "final linear");
+    }
+    return XNP_OK;
+}

@@ -1193,4 +1193,159 @@ hipError_t launch_gemm_q8(const void *A, int M, int K, const int8_t *W, const fl
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------------------------
+// f32 pieces of the flow LM around the transformer (flow_lm.rs, mlp.rs, conditioners.rs):
+// linears with bias and fused epilogues, LayerNorm with the AdaLN modulation, the LUT gather.
+// Batch-1 frames make these matrix-vector products: one wave per output channel, the weight
+// row held in registers, each row of x reduced across the wave.
+
+template <int KC, int EPI>
+__global__ __launch_bounds__(256) void k_linear_f32(const float *x, int ldx, int M, int K, const float *W,
+                                                    const float *bias, int N, LinOut lo) {
+    const int n = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (n >= N) return;
+    float w[KC];
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+        const int k = c * 64 + lane;
+        w[c] = k < K ? W[(size_t)n * K + k] : 0.f;
+    }
+    const float b = bias ? bias[n] : 0.f;
+    for (int m = 0; m < M; ++m) {
+        const float *xr = x + (size_t)m * ldx;
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+            const int k = c * 64 + lane;
+            if (k < K) acc = __builtin_fmaf(w[c], xr[k], acc);
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
+        if (lane != 0) continue;
+        const float y = acc + b;
+        int seg = 0;
+        if (lo.nseg > 1 && n >= lo.col0[1]) seg = (lo.nseg > 2 && n >= lo.col0[2]) ? 2 : 1;
+        float *o = lo.out[seg] + (size_t)m * lo.ld[seg] + (n - lo.col0[seg]);
+        if constexpr (EPI == kLinStore) {
+            *o = y;
+        } else if constexpr (EPI == kLinGeluErf) {
+            *o = 0.5f * y * (1.0f + erff(y * 0.7071067811865476f));
+        } else if constexpr (EPI == kLinGeluTanh) {
+            const float c = 0.7978845608028654f;
+            *o = 0.5f * y * (1.0f + tanhf(c * (y + 0.044715f * y * y * y)));
+        } else if constexpr (EPI == kLinSilu) {
+            *o = y / (1.0f + expf(-y));
+        } else if constexpr (EPI == kLinSiluAddVec) {
+            const float z = y + lo.aux[n];
+            *o = z / (1.0f + expf(-z));
+        } else if constexpr (EPI == kLinResidual) {
+            *o = *o + y;
+        } else if constexpr (EPI == kLinGated) {
+            *o = *o + lo.aux[(size_t)m * lo.ld_aux + n] * y;
+        } else { // kLinAxpy
+            *o = lo.aux[(size_t)m * lo.ld_aux + n] + y * lo.alpha;
+        }
+    }
+}
+
+template <int KC>
+static hipError_t linear_f32_kc(const float *x, int ldx, int M, int K, const float *W, const float *b, int N, int epi,
+                                const LinOut &lo, hipStream_t stream) {
+    const dim3 grid((N + 3) / 4), block(256);
+#define XNP_LIN(E) hipLaunchKernelGGL((k_linear_f32<KC, E>), grid, block, 0, stream, x, ldx, M, K, W, b, N, lo)
+    switch (epi) {
+    case kLinStore: XNP_LIN(kLinStore); break;
+    case kLinGeluErf: XNP_LIN(kLinGeluErf); break;
+    case kLinGeluTanh: XNP_LIN(kLinGeluTanh); break;
+    case kLinSilu: XNP_LIN(kLinSilu); break;
+    case kLinSiluAddVec: XNP_LIN(kLinSiluAddVec); break;
+    case kLinResidual: XNP_LIN(kLinResidual); break;
+    case kLinGated: XNP_LIN(kLinGated); break;
+    case kLinAxpy: XNP_LIN(kLinAxpy); break;
+    default: return hipErrorInvalidValue;
+    }
+#undef XNP_LIN
+    return hipGetLastError();
+}
+
+hipError_t launch_linear_f32(const float *x, int ldx, int M, int K, const float *W, const float *b, int N, int epi,
+                             const LinOut &lo, hipStream_t stream) {
+    if (M <= 0 || N <= 0) return hipSuccess;
+    const int kc = (K + 63) / 64;
+    if (kc <= 1) return linear_f32_kc<1>(x, ldx, M, K, W, b, N, epi, lo, stream);
+    if (kc <= 4) return linear_f32_kc<4>(x, ldx, M, K, W, b, N, epi, lo, stream);
+    if (kc <= 8) return linear_f32_kc<8>(x, ldx, M, K, W, b, N, epi, lo, stream);
+    if (kc <= 16) return linear_f32_kc<16>(x, ldx, M, K, W, b, N, epi, lo, stream);
+    if (kc <= 32) return linear_f32_kc<32>(x, ldx, M, K, W, b, N, epi, lo, stream);
+    return hipErrorInvalidValue;
+}
+
+// LayerNorm of f32 rows (eps given; w, b optional), then, when shift is given, the AdaLN
+// modulation y * (1 + scale) + shift with per-row shift/scale (mlp.rs:4-11).  One wave per row.
+template <int CH>
+__global__ __launch_bounds__(256) void k_ln_f32(const float *x, int rows, int dim, const float *w, const float *b,
+                                                float eps, const float *shift, const float *scale, int ld_mod,
+                                                float *out) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float *xr = x + (size_t)row * dim;
+    float v[CH];
+    float sum = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int i = c * 64 + lane;
+        v[c] = i < dim ? xr[i] : 0.f;
+        sum += v[c];
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o);
+    const float mean = sum / (float)dim;
+    float sq = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const float d = c * 64 + lane < dim ? v[c] - mean : 0.f;
+        sq = __builtin_fmaf(d, d, sq);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
+    const float rstd = 1.0f / __builtin_sqrtf(sq / (float)dim + eps);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int i = c * 64 + lane;
+        if (i >= dim) continue;
+        float y = (v[c] - mean) * rstd;
+        if (w) y = y * w[i] + b[i];
+        if (shift) y = y * (scale[(size_t)row * ld_mod + i] + 1.0f) + shift[(size_t)row * ld_mod + i];
+        out[(size_t)row * dim + i] = y;
+    }
+}
+
+hipError_t launch_ln_f32(const float *x, int rows, int dim, const float *w, const float *b, float eps,
+                         const float *shift, const float *scale, int ld_mod, float *out, hipStream_t stream) {
+    if (rows <= 0) return hipSuccess;
+    const dim3 grid((rows + 3) / 4), block(256);
+    const int ch = (dim + 63) / 64;
+#define XNP_LN(C) hipLaunchKernelGGL(k_ln_f32<C>, grid, block, 0, stream, x, rows, dim, w, b, eps, shift, scale, ld_mod, out)
+    if (ch <= 4) XNP_LN(4);
+    else if (ch <= 8) XNP_LN(8);
+    else if (ch <= 16) XNP_LN(16);
+    else if (ch <= 32) XNP_LN(32);
+    else return hipErrorInvalidValue;
+#undef XNP_LN
+    return hipGetLastError();
+}
+
+// LUTConditioner::embed_tokens (conditioners.rs:239-262): out[r] = table[ids[r]], rows of dim f32.
+__global__ void k_embed_f32(const float *table, const int32_t *ids, int rows, int dim, float *out) {
+    const int r = blockIdx.x;
+    const float *src = table + (size_t)ids[r] * dim;
+    for (int i = threadIdx.x; i < dim; i += blockDim.x) out[(size_t)r * dim + i] = src[i];
+}
+
+hipError_t launch_embed_f32(const float *table, const int32_t *ids, int rows, int dim, float *out, hipStream_t stream) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_embed_f32, dim3(rows), dim3(256), 0, stream, table, ids, rows, dim, out);
+    return hipGetLastError();
+}
+
 } // namespace xnp

@@ -281,6 +281,20 @@ struct xnp_pool {
 
 extern "C" const char *xnp_last_error(void) { return g_err.c_str(); }
 
+namespace xnp {
+xnp_status pool_fail(xnp_status code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+const xnp_pool_desc *pool_desc(const xnp_pool *p) { return &p->d; }
+bool pool_host_only(const xnp_pool *p) { return p->host_only; }
+} // namespace xnp
+
 extern "C" int32_t xnp_frame_budget(int32_t num_tokens, double frame_rate) {
     // plan.rs:43-45
     return (int32_t)std::ceil(((double)num_tokens / 3.0 + 2.0) * frame_rate);

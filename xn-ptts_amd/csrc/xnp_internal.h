@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/xnp_kv.h"
+
 namespace xnp {
 
 constexpr int kBlock = 16;   // positions per page
@@ -78,6 +80,11 @@ struct LaunchTiming {
     hipEvent_t start = nullptr, stop = nullptr;
 };
 
+// The pool's description and the library's error reporting (pool.cpp), for the other host files.
+xnp_status pool_fail(xnp_status code, const char *fmt, ...);
+const xnp_pool_desc *pool_desc(const xnp_pool *p);
+bool pool_host_only(const xnp_pool *p);
+
 // Launchers (kernels.hip).  All asynchronous on `stream`; return the launch status.
 hipError_t launch_patch_tables(const PoolView &pv, const TablePatch *patches, int n,
                                hipStream_t stream);
@@ -114,6 +121,31 @@ hipError_t launch_layer_norm(const void *x, int rows, int dim, const float *w, c
                              hipStream_t stream);
 hipError_t launch_gemm_q8(const void *A, int M, int K, const int8_t *W, const float *s, int N, int epi,
                           const GemmOut &go, hipStream_t stream);
+// Epilogues of the f32 linear (launch_linear_f32), y = x W^T + b:
+//   kLinStore out = y; kLinGelu* out = gelu(y); kLinSilu out = silu(y); kLinSiluAddVec
+//   out = silu(y + aux[n]); kLinResidual out += y; kLinGated out += aux[m][n] * y; kLinAxpy
+//   out = aux[m][n] + alpha * y (aux may be out itself).
+enum : int32_t {
+    kLinStore = 0, kLinGeluErf = 1, kLinGeluTanh = 2, kLinSilu = 3, kLinSiluAddVec = 4, kLinResidual = 5,
+    kLinGated = 6, kLinAxpy = 7
+};
+
+// Where an f32 linear writes: columns [col0[j], col0[j+1]) to out[j] (row stride ld[j]).
+struct LinOut {
+    float *out[3] = {nullptr, nullptr, nullptr};
+    int32_t ld[3] = {0, 0, 0};
+    int32_t col0[3] = {0, 0, 0};
+    int32_t nseg = 1;
+    const float *aux = nullptr;
+    int32_t ld_aux = 0;
+    float alpha = 1.f;
+};
+
+hipError_t launch_linear_f32(const float *x, int ldx, int M, int K, const float *W, const float *b, int N, int epi,
+                             const LinOut &lo, hipStream_t stream);
+hipError_t launch_ln_f32(const float *x, int rows, int dim, const float *w, const float *b, float eps,
+                         const float *shift, const float *scale, int ld_mod, float *out, hipStream_t stream);
+hipError_t launch_embed_f32(const float *table, const int32_t *ids, int rows, int dim, float *out, hipStream_t stream);
 hipError_t launch_rows_io(const PoolView &pv, int sid, int layer, int kv, int slot0, int n,
                           void *rows, float *scales, bool write, hipStream_t stream);
 

@@ -105,6 +105,11 @@ SIGNATURES = {
     "xnp_layer_norm": (_i32, [_p, _i32, _i32, _p, _p, _c.c_float, _p, _p]),
     "xnp_linear_q8": (_i32, [_p, _i32, _i32, _p, _p, _i32, _i32, _p, _p, _p]),
     "xnp_quantize_rows": (_i32, [_p, _i32, _i32, _p, _p]),
+    "xnp_flow_lm_weights_size": (_i32, [_p, _c.POINTER(_c.c_int64)]),
+    "xnp_flow_lm_create": (_i32, [_p, _p, _p, _c.c_int64, _c.POINTER(_p)]),
+    "xnp_flow_lm_destroy": (_i32, [_p]),
+    "xnp_flow_lm_prompt_text": (_i32, [_p, _i32p, _i32, _p, _i32, _p]),
+    "xnp_flow_lm_step": (_i32, [_p, _i32p, _i32, _p, _p, _p, _p, _p]),
     "xnp_frame_budget": (_i32, [_i32, _c.c_double]),
     "xnp_seq_budget": (_i32, [_i32, _i32]),
     "xnp_last_error": (_c.c_char_p, []),
