@@ -24,8 +24,9 @@
 
 --workload flowlm: the single-stream flow LM (Phonon-31m shape, fp32): a 64-token text prompt, then
   greedy frames at temperature 0 through input_linear, the 6 layers, out_norm, the EOS head and the flow
-  net.  Value: frames/s at batch 1; the CPU oracle of the same stream beside it on 1 thread and on all
-  cores.
+  net.  Value: frames/s at batch 1 with each frame replayed from a hipGraph recording of its launches
+  (xnp_flow_lm_step_graph; the launched rate beside it); the CPU oracle of the same stream on 1 thread
+  and on all cores.
 
 --workload window: int8 K/V with fp32 scales per (page, head), 1024 streams, a sliding window of
   512 positions on rings of 528 slots whose write heads start at offsets U[0, 4096), each stream
@@ -595,8 +596,8 @@ def run_flowlm(args, xnp, torch):
     tokens = rng.integers(0, cfg.n_bins + 1, 64).astype(np.int32)
     frames = args.warmup + args.steps
     cap = xnp.seq_budget(64, xnp.frame_budget(64))  # plan.rs:52-54: 868
-    if 64 + frames > cap:
-        raise SystemExit(f"{frames} frames do not fit the {cap}-position budget of a 64-token prompt")
+    if 64 + 2 * frames > cap:
+        raise SystemExit(f"{frames} frames twice do not fit the {cap}-position budget of a 64-token prompt")
     mbps = (cap + 15) // 16
     pool = xnp.KvPool(num_layers=cfg.num_layers, num_heads=cfg.num_heads, num_blocks=mbps + 4, max_streams=1,
                       max_blocks_per_stream=mbps, cache_dtype="f32", act_dtype="f32", max_pos=cap + 16,
@@ -604,29 +605,32 @@ def run_flowlm(args, xnp, torch):
     sid = pool.init_state(cap)
     lm = xnp.FlowLM(pool, cfg, blob, max_rows=64)
     noise = torch.zeros((1, cfg.ldim), dtype=torch.float32, device=dev)  # temperature 0
-    lat = [torch.empty((1, cfg.ldim), dtype=torch.float32, device=dev) for _ in range(2)]
+    lat = torch.zeros((1, cfg.ldim), dtype=torch.float32, device=dev)  # read and overwritten in place
     eos = torch.empty(1, dtype=torch.float32, device=dev)
+    stream = torch.cuda.Stream()  # a recorded frame replays on a stream of the caller's
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    lm.prompt_text([sid], tokens[None, :])
-    torch.cuda.synchronize()
-    prompt_ms = (time.perf_counter() - t0) * 1000.0
-    cur = [None]
-    for f in range(args.warmup):
-        lm.step([sid], cur[0], noise, lat[f % 2], eos)
-        cur[0] = lat[f % 2]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for f in range(args.warmup, frames):
-        lm.step([sid], cur[0], noise, lat[f % 2], eos)
-        cur[0] = lat[f % 2]
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+    with torch.cuda.stream(stream):
+        t0 = time.perf_counter()
+        lm.prompt_text([sid], tokens[None, :])
+        stream.synchronize()
+        prompt_ms = (time.perf_counter() - t0) * 1000.0
+
+        def frames_ms(first, count, graph):
+            t = time.perf_counter()
+            for f in range(first, first + count):
+                lm.step([sid], None if f == 0 else lat, noise, lat, eos, graph=graph)
+            stream.synchronize()
+            return (time.perf_counter() - t) * 1000.0 / max(count, 1)
+
+        frames_ms(0, args.warmup, True)
+        ms = frames_ms(args.warmup, args.steps, True)  # the value: frames replayed from a recording
+        eager_ms = frames_ms(frames, min(args.steps, cap - 64 - frames), False)  # the same frames, launched
     fps = 1000.0 / ms
     bytes_mean = np.mean([flow_bytes(cfg, 64 + f) for f in range(args.warmup, frames)])
     gbs = bytes_mean / (ms * 1e-3) / 1e9
     cpu = None if args.no_cpu else cpu_flowlm(cfg, blob, tokens, args.cpu_seconds, 1)
-    extra = {"audio_sec_per_sec": round(fps * 0.08, 2), "prompt_ms": round(prompt_ms, 3)}
+    extra = {"audio_sec_per_sec": round(fps * 0.08, 2), "prompt_ms": round(prompt_ms, 3),
+             "eager_frames_per_s": round(1000.0 / eager_ms, 1)}
     if not args.no_cpu:
         oracle = _load("oracle", os.path.join(ROOT, "oracle", "oracle.py"))
         extra["cpu_baseline_all_cores"] = cpu_flowlm(cfg, blob, tokens, args.cpu_seconds, os.cpu_count() or 1)
@@ -639,7 +643,8 @@ def run_flowlm(args, xnp, torch):
     # f32 weight once plus the K/V attended) over its wall time, not one kernel's
     roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "whole frame: f32 linears, LayerNorms, k_decode<f32>, flow net (batch 1, launch-bound)",
+            "kernel": "whole frame replayed from a hipGraph: f32 linears, LayerNorms, k_decode<f32>, flow net "
+                      "(batch 1, launch-bound)",
             "bytes_per_frame": int(bytes_mean)}
     return line("frames/sec, single-stream flow LM (Phonon-31m shape, fp32)", fps, "frames/s", args, ms, "f32",
                 config, roof, cpu, extra=extra)

@@ -311,6 +311,15 @@ xnp_status xnp_flow_lm_prompt_text(xnp_flow_lm *lm, const int32_t *ids, int32_t 
  * f32 device memory.  The streams advance by one position. */
 xnp_status xnp_flow_lm_step(xnp_flow_lm *lm, const int32_t *ids, int32_t n, const float *latent_in,
                             const float *noise, float *latent_out, float *eos_logit, void *hip_stream);
+/* xnp_flow_lm_step with the frame's launches recorded once in a hipGraph and replayed, as
+ * StepGraph records one step and replays it per frame (step_graph.rs:111-122, 234-267).  The plan
+ * (positions, pages) is uploaded eagerly each call and read by the recorded kernels from the pool's
+ * device buffers, as DeviceStep keeps the position on the device (transformer.rs:111-140).  A new
+ * recording is made when n, a buffer or the stream changes; hip_stream must not be the null
+ * stream.  Results are those of xnp_flow_lm_step. */
+xnp_status xnp_flow_lm_step_graph(xnp_flow_lm *lm, const int32_t *ids, int32_t n, const float *latent_in,
+                                  const float *noise, float *latent_out, float *eos_logit,
+                                  void *hip_stream);
 
 /* ---- budgets (plan.rs:25, 43-54) --------------------------------------------------------- */
 int32_t xnp_frame_budget(int32_t num_tokens, double frame_rate);

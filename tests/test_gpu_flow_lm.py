@@ -93,3 +93,36 @@ def test_bad_tokens_are_refused_and_change_nothing():
     with pytest.raises(xnp.XnpError):
         lm.prompt_text([sid], np.array([[1, 2, 11]], np.int32))
     assert pool.current_end(sid) == 0
+
+
+def test_graph_recorded_frames_equal_eager_frames():
+    # StepGraph's analog (step_graph.rs:111-307): the frame's launches recorded once and replayed
+    # after each eager plan upload, against a twin model stepping eagerly -- bit for bit, every
+    # frame, with the host reading results back between replays.  The latent buffer is updated in
+    # place, so after the first frame (bos) one recording serves every later frame.
+    cfg = fl.FlowLMConfig(num_layers=2, flow_depth=2, flow_dim=256, dim_feedforward=1024, n_bins=100)
+    blob = fl.random_weights(cfg, 93, std=0.05, unit_norms=False)
+    rng = np.random.default_rng(94)
+    n = 2
+    tokens = rng.integers(0, cfg.n_bins + 1, (n, 4)).astype(np.int32)
+    s = torch.cuda.Stream()
+    runs = []
+    for _ in range(2):
+        pool = xnp.KvPool(num_layers=2, num_heads=8, num_blocks=16, max_streams=n, max_blocks_per_stream=4,
+                          cache_dtype="f32", act_dtype="f32", max_pos=128, page_seed=4)
+        ids = [pool.init_state(64) for _ in range(n)]
+        lm = xnp.FlowLM(pool, cfg, blob, max_rows=n * 4)
+        with torch.cuda.stream(s):
+            lm.prompt_text(ids, tokens)
+        lat = torch.zeros((n, cfg.ldim), dtype=torch.float32, device=DEV)
+        eos = torch.zeros(n, dtype=torch.float32, device=DEV)
+        runs.append((pool, ids, lm, lat, eos))
+    noise = torch.zeros((n, cfg.ldim), dtype=torch.float32, device=DEV)
+    for f in range(8):
+        with torch.cuda.stream(s):
+            noise.copy_(torch.from_numpy((0.5 * rng.standard_normal((n, cfg.ldim))).astype(np.float32)).to(DEV))
+            for g, (pool, ids, lm, lat, eos) in enumerate(runs):
+                lm.step(ids, None if f == 0 else lat, noise, lat, eos, stream=s.cuda_stream, graph=(g == 1))
+        s.synchronize()
+        assert torch.equal(runs[0][3], runs[1][3]) and torch.equal(runs[0][4], runs[1][4]), f
+    assert runs[1][0].current_end(runs[1][1][0]) == 12

@@ -431,3 +431,70 @@ def test_unwritten_rows_holding_nan_bytes_do_not_reach_the_output(cache, act):
     assert p.step() <= TOL[cache]
     for i in range(2):
         p.assert_cache_equal(i)
+
+
+def test_a_step_captured_in_a_hip_graph_replays_like_eager_steps():
+    # The per-layer launches of a batch allocate nothing and read positions and pages from the
+    # plan the step uploads, as DeviceStep keeps the position on the device (transformer.rs:111-140)
+    # so that StepGraph can record one step and replay it (step_graph.rs:111-307).  Capture the L
+    # attend launches once; each later step is begin (eager plan upload) + replay + end.  A twin
+    # pool runs the same steps eagerly: outputs and caches must agree bit for bit, every replay.
+    L, H, S = 2, 8, 6
+    lens = [0, 3, 15, 16, 40, 70]
+    rng = np.random.default_rng(27)
+    pools, idss = [], []
+    for _ in range(2):
+        pool = xnp.KvPool(num_layers=L, num_heads=H, num_blocks=S * 8 + 8, max_streams=S, max_blocks_per_stream=8,
+                          cache_dtype="bf16", act_dtype="bf16", max_pos=256, page_seed=13)
+        pools.append(pool)
+        idss.append([pool.init_state(128) for _ in range(S)])
+    for i, n in enumerate(lens):
+        if n == 0:
+            continue
+        k, v = dev(bf16_round(rng.standard_normal((n, H, 64))), "bf16"), dev(bf16_round(rng.standard_normal((n, H, 64))), "bf16")
+        for pool, ids in zip(pools, idss):
+            pool.begin([ids[i]], t=n)
+            for layer in range(L):
+                pool.append(layer, k, v)
+            pool.end()
+    s = torch.cuda.Stream()
+    q, k, v = ([torch.empty((S, H, 64), dtype=torch.bfloat16, device=DEV) for _ in range(L)] for _ in range(3))
+    outs = [[torch.empty((S, H, 64), dtype=torch.bfloat16, device=DEV) for _ in range(L)] for _ in range(2)]
+
+    def refill():
+        for t in q + k + v:
+            t.copy_(torch.from_numpy(bf16_round(rng.standard_normal((S, H, 64)))).to(DEV))
+
+    def launches(pool, out):
+        for layer in range(L):
+            pool.attend(layer, q[layer], k[layer], v[layer], out[layer], 0.125)
+
+    g = torch.cuda.CUDAGraph()
+    for step in range(6):
+        with torch.cuda.stream(s):
+            refill()
+            for p, (pool, ids) in enumerate(zip(pools, idss)):
+                pool.begin(ids, stream=s.cuda_stream)
+                if p == 0:
+                    launches(pool, outs[0])
+                elif step == 0:
+                    with torch.cuda.graph(g, stream=s):
+                        launches(pool, outs[1])
+                    g.replay()
+                else:
+                    g.replay()
+                pool.end()
+        s.synchronize()
+        for layer in range(L):
+            a, b = outs[0][layer].view(torch.int16), outs[1][layer].view(torch.int16)
+            assert torch.equal(a, b), (step, layer)
+        torch.cuda.synchronize()
+    for i in range(S):
+        n = lens[i] + 6
+        for layer in range(L):
+            for kvi in (0, 1):
+                rows = [torch.empty((n, H, 64), dtype=torch.bfloat16, device=DEV) for _ in range(2)]
+                for pool, ids, r in zip(pools, idss, rows):
+                    pool.read_rows(ids[i], layer, kvi, 0, r)
+                torch.cuda.synchronize()
+                assert torch.equal(rows[0].view(torch.int16), rows[1].view(torch.int16)), (i, layer, kvi)

@@ -106,15 +106,25 @@ void host_time_embed(const xnp_flow_lm_desc &d, const float *blob, const Layout 
 
 } // namespace
 
+// A recorded frame: the launches of xnp_flow_lm_step for one batch size and one set of buffers.
+struct FlowGraph {
+    hipGraphExec_t exec = nullptr;
+    int32_t n = 0;
+    const float *latent_in = nullptr, *noise = nullptr;
+    float *latent_out = nullptr, *eos = nullptr;
+    hipStream_t stream = nullptr;
+};
+
 struct xnp_flow_lm {
+    FlowGraph graph;
     xnp_pool *pool = nullptr;
     xnp_flow_lm_desc d{};
     Layout L{};
     float *w = nullptr;    // the weight blob on the device
     float *temb = nullptr; // [lsd_steps][F]: SimpleMLPAdaLN::time_embedding of each solver step
     // scratch for max_rows rows
-    float *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *f = nullptr;
-    float *tout = nullptr, *ya = nullptr, *ada = nullptr, *xf = nullptr, *hf = nullptr, *h2 = nullptr;
+    float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *f = nullptr;
+    float *ya = nullptr, *ada = nullptr, *xf = nullptr, *h2 = nullptr;
     int32_t *dids = nullptr;
     int32_t *hids = nullptr; // pinned staging of token ids
     std::vector<void *> allocs;
@@ -122,6 +132,7 @@ struct xnp_flow_lm {
 };
 
 static void fl_free(xnp_flow_lm *lm) {
+    if (lm->graph.exec) (void)hipGraphExecDestroy(lm->graph.exec);
     for (void *p : lm->allocs) (void)hipFree(p);
     if (lm->hids) (void)hipHostFree(lm->hids);
     delete lm;
@@ -179,10 +190,10 @@ extern "C" xnp_status xnp_flow_lm_create(xnp_pool *pool, const xnp_flow_lm_desc 
     struct {
         float **p;
         size_t n;
-    } bufs[] = {{&lm->w, L.total}, {&lm->temb, (size_t)d.lsd_steps * F}, {&lm->x, M * dm}, {&lm->h, M * dm},
+    } bufs[] = {{&lm->w, L.total}, {&lm->temb, (size_t)d.lsd_steps * F}, {&lm->x, M * dm},
                 {&lm->q, M * dm},  {&lm->k, M * dm},  {&lm->v, M * dm}, {&lm->att, M * dm},
-                {&lm->f, M * (size_t)d.ff}, {&lm->tout, M * dm}, {&lm->ya, M * F}, {&lm->ada, M * 3 * F},
-                {&lm->xf, M * F}, {&lm->hf, M * F}, {&lm->h2, M * F}};
+                {&lm->f, M * (size_t)d.ff}, {&lm->ya, M * F}, {&lm->ada, M * 3 * F},
+                {&lm->xf, M * F}, {&lm->h2, M * F}};
     for (auto &b : bufs)
         if ((e = dalloc((void **)b.p, sizeof(float) * b.n)) != hipSuccess) return fail_hip(e, "flow LM buffers");
     if ((e = dalloc((void **)&lm->dids, sizeof(int32_t) * M)) != hipSuccess) return fail_hip(e, "flow LM ids");
@@ -227,24 +238,24 @@ static xnp_status fl_transformer(xnp_flow_lm *lm, int M, void *hip_stream) {
     const int dm = d.d_model, ff = d.ff;
     const float scale = 1.0f / std::sqrt((float)(dm / d.num_heads));
     for (int l = 0; l < d.num_layers; l++) {
-        FL_TRY(launch_ln_f32(lm->x, M, dm, lm->W(L.ln1_w[l]), lm->W(L.ln1_b[l]), 1e-5f, nullptr, nullptr, 0, lm->h, hs),
-               "norm1");
+        LinNorm n1; // norm1, applied as in_proj reads x
+        n1.w = lm->W(L.ln1_w[l]), n1.b = lm->W(L.ln1_b[l]), n1.eps = 1e-5f;
         LinOut qkv;
         qkv.nseg = 3;
         qkv.out[0] = lm->q, qkv.ld[0] = dm, qkv.col0[0] = 0;
         qkv.out[1] = lm->k, qkv.ld[1] = dm, qkv.col0[1] = dm;
         qkv.out[2] = lm->v, qkv.ld[2] = dm, qkv.col0[2] = 2 * dm;
-        FL_TRY(launch_linear_f32(lm->h, dm, M, dm, lm->W(L.wqkv[l]), nullptr, 3 * dm, kLinStore, qkv, hs), "in_proj");
+        FL_TRY(launch_linear_f32(lm->x, dm, M, dm, lm->W(L.wqkv[l]), nullptr, 3 * dm, kLinStore, qkv, hs, &n1), "in_proj");
         if (xnp_status st = xnp_attend(lm->pool, l, lm->q, lm->k, lm->v, lm->att, scale, hip_stream)) return st;
         LinOut res;
         res.out[0] = lm->x, res.ld[0] = dm;
         FL_TRY(launch_linear_f32(lm->att, dm, M, dm, lm->W(L.wout[l]), nullptr, dm, kLinResidual, res, hs), "out_proj");
-        FL_TRY(launch_ln_f32(lm->x, M, dm, lm->W(L.ln2_w[l]), lm->W(L.ln2_b[l]), 1e-5f, nullptr, nullptr, 0, lm->h, hs),
-               "norm2");
+        LinNorm n2; // norm2, applied as linear1 reads x
+        n2.w = lm->W(L.ln2_w[l]), n2.b = lm->W(L.ln2_b[l]), n2.eps = 1e-5f;
         LinOut hid;
         hid.out[0] = lm->f, hid.ld[0] = ff;
-        FL_TRY(launch_linear_f32(lm->h, dm, M, dm, lm->W(L.w1[l]), nullptr, ff,
-                                 d.gelu == XNP_GELU_ERF ? kLinGeluErf : kLinGeluTanh, hid, hs),
+        FL_TRY(launch_linear_f32(lm->x, dm, M, dm, lm->W(L.w1[l]), nullptr, ff,
+                                 d.gelu == XNP_GELU_ERF ? kLinGeluErf : kLinGeluTanh, hid, hs, &n2),
                "linear1");
         FL_TRY(launch_linear_f32(lm->f, ff, M, ff, lm->W(L.w2[l]), nullptr, dm, kLinResidual, res, hs), "linear2");
     }
@@ -277,39 +288,34 @@ extern "C" xnp_status xnp_flow_lm_prompt_text(xnp_flow_lm *lm, const int32_t *id
     return xnp_batch_end(lm->pool);
 }
 
-extern "C" xnp_status xnp_flow_lm_step(xnp_flow_lm *lm, const int32_t *ids, int32_t n, const float *latent_in,
-                                       const float *noise, float *latent_out, float *eos_logit, void *hip_stream) {
-    if (!lm || (n > 0 && (!ids || !noise || !latent_out || !eos_logit))) return pool_fail(XNP_E_INVALID, "null argument");
-    if (n < 0 || n > lm->d.max_rows) return pool_fail(XNP_E_INVALID, "%d streams; the flow LM holds %d rows", n, lm->d.max_rows);
-    if (n == 0) return XNP_OK;
+// The frame's device work after the step's plan is uploaded: input_linear, the transformer, the
+// heads and the flow net, all launches on hip_stream (what a graph of the frame records).
+static xnp_status fl_frame_launches(xnp_flow_lm *lm, int M, const float *latent_in, const float *noise,
+                                    float *latent_out, float *eos_logit, void *hip_stream) {
     const xnp_flow_lm_desc &d = lm->d;
     const Layout &L = lm->L;
     hipStream_t hs = (hipStream_t)hip_stream;
-    const int dm = d.d_model, F = d.flow_dim, ld = d.ldim, M = n;
-    FL_TRY(hipSetDevice(pool_desc(lm->pool)->device), "hipSetDevice");
+    const int dm = d.d_model, F = d.flow_dim, ld = d.ldim;
     // input_linear of the previous latents, or of bos_emb for every row (flow_lm.rs:314-324, 423-427)
     LinOut xo;
     xo.out[0] = lm->x, xo.ld[0] = dm;
     FL_TRY(launch_linear_f32(latent_in ? latent_in : lm->W(L.bos), latent_in ? ld : 0, M, ld, lm->W(L.in_lin), nullptr,
                              dm, kLinStore, xo, hs),
            "input_linear");
-    if (xnp_status st = xnp_batch_begin(lm->pool, ids, n, 1, hip_stream)) return st;
-    if (xnp_status st = fl_transformer(lm, M, hip_stream)) {
-        (void)xnp_batch_abort(lm->pool);
-        return st;
-    }
-    if (xnp_status st = xnp_batch_end(lm->pool)) return st;
-    // out_norm (flow_lm.rs:315), the EOS logit (flow_lm.rs:366)
-    FL_TRY(launch_ln_f32(lm->x, M, dm, lm->W(L.on_w), lm->W(L.on_b), 1e-5f, nullptr, nullptr, 0, lm->tout, hs), "out_norm");
+    if (xnp_status st = fl_transformer(lm, M, hip_stream)) return st;
+    // out_norm (flow_lm.rs:315), applied as its two readers load x: the EOS logit (flow_lm.rs:366)
+    // and the flow net's cond_embed
+    LinNorm on;
+    on.w = lm->W(L.on_w), on.b = lm->W(L.on_b), on.eps = 1e-5f;
     LinOut eo;
     eo.out[0] = eos_logit, eo.ld[0] = 1;
-    FL_TRY(launch_linear_f32(lm->tout, dm, M, dm, lm->W(L.eos_w), lm->W(L.eos_b), 1, kLinStore, eo, hs), "out_eos");
+    FL_TRY(launch_linear_f32(lm->x, dm, M, dm, lm->W(L.eos_w), lm->W(L.eos_b), 1, kLinStore, eo, hs, &on), "out_eos");
     // lsd_decode (flow_lm.rs:97-110): each step x += flow_net(t_out, t_emb_i, x) / steps
     for (int i = 0; i < d.lsd_steps; i++) {
         const float *cur = i == 0 ? noise : latent_out;
         LinOut y;
         y.out[0] = lm->ya, y.ld[0] = F, y.aux = lm->temb + (size_t)i * F;
-        FL_TRY(launch_linear_f32(lm->tout, dm, M, dm, lm->W(L.cond_w), lm->W(L.cond_b), F, kLinSiluAddVec, y, hs),
+        FL_TRY(launch_linear_f32(lm->x, dm, M, dm, lm->W(L.cond_w), lm->W(L.cond_b), F, kLinSiluAddVec, y, hs, &on),
                "cond_embed");
         LinOut xf;
         xf.out[0] = lm->xf, xf.ld[0] = F;
@@ -319,12 +325,13 @@ extern "C" xnp_status xnp_flow_lm_step(xnp_flow_lm *lm, const int32_t *ids, int3
             a.out[0] = lm->ada, a.ld[0] = 3 * F;
             FL_TRY(launch_linear_f32(lm->ya, F, M, F, lm->W(L.rb_aw[r]), lm->W(L.rb_ab[r]), 3 * F, kLinStore, a, hs),
                    "adaLN_modulation");
-            FL_TRY(launch_ln_f32(lm->xf, M, F, lm->W(L.rb_lnw[r]), lm->W(L.rb_lnb[r]), 1e-6f, lm->ada, lm->ada + F, 3 * F,
-                                 lm->hf, hs),
-                   "in_ln");
+            LinNorm in; // in_ln and modulate(shift, scale), applied as mlp.0 reads x
+            in.w = lm->W(L.rb_lnw[r]), in.b = lm->W(L.rb_lnb[r]), in.eps = 1e-6f;
+            in.shift = lm->ada, in.scale = lm->ada + F, in.ld_mod = 3 * F;
             LinOut s1;
             s1.out[0] = lm->h2, s1.ld[0] = F;
-            FL_TRY(launch_linear_f32(lm->hf, F, M, F, lm->W(L.rb_w1[r]), lm->W(L.rb_b1[r]), F, kLinSilu, s1, hs), "mlp.0");
+            FL_TRY(launch_linear_f32(lm->xf, F, M, F, lm->W(L.rb_w1[r]), lm->W(L.rb_b1[r]), F, kLinSilu, s1, hs, &in),
+                   "mlp.0");
             LinOut g;
             g.out[0] = lm->xf, g.ld[0] = F, g.aux = lm->ada + 2 * F, g.ld_aux = 3 * F;
             FL_TRY(launch_linear_f32(lm->h2, F, M, F, lm->W(L.rb_w2[r]), lm->W(L.rb_b2[r]), F, kLinGated, g, hs), "mlp.2");
@@ -333,10 +340,74 @@ extern "C" xnp_status xnp_flow_lm_step(xnp_flow_lm *lm, const int32_t *ids, int3
         a.out[0] = lm->ada, a.ld[0] = 2 * F;
         FL_TRY(launch_linear_f32(lm->ya, F, M, F, lm->W(L.fin_aw), lm->W(L.fin_ab), 2 * F, kLinStore, a, hs),
                "final adaLN_modulation");
-        FL_TRY(launch_ln_f32(lm->xf, M, F, nullptr, nullptr, 1e-6f, lm->ada, lm->ada + F, 2 * F, lm->hf, hs), "norm_final");
+        LinNorm nf; // norm_final (no affine) and modulate, applied as the final linear reads x
+        nf.eps = 1e-6f, nf.shift = lm->ada, nf.scale = lm->ada + F, nf.ld_mod = 2 * F;
         LinOut o;
         o.out[0] = latent_out, o.ld[0] = ld, o.aux = cur, o.ld_aux = ld, o.alpha = 1.0f / (float)d.lsd_steps;
-        FL_TRY(launch_linear_f32(lm->hf, F, M, F, lm->W(L.fin_w), lm->W(L.fin_b), ld, kLinAxpy, o, hs), "final linear");
+        FL_TRY(launch_linear_f32(lm->xf, F, M, F, lm->W(L.fin_w), lm->W(L.fin_b), ld, kLinAxpy, o, hs, &nf),
+               "final linear");
     }
     return XNP_OK;
+}
+
+static xnp_status fl_step_check(xnp_flow_lm *lm, const int32_t *ids, int32_t n, const float *noise, float *latent_out,
+                                float *eos_logit) {
+    if (!lm || (n > 0 && (!ids || !noise || !latent_out || !eos_logit))) return pool_fail(XNP_E_INVALID, "null argument");
+    if (n < 0 || n > lm->d.max_rows) return pool_fail(XNP_E_INVALID, "%d streams; the flow LM holds %d rows", n, lm->d.max_rows);
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_flow_lm_step(xnp_flow_lm *lm, const int32_t *ids, int32_t n, const float *latent_in,
+                                       const float *noise, float *latent_out, float *eos_logit, void *hip_stream) {
+    if (xnp_status st = fl_step_check(lm, ids, n, noise, latent_out, eos_logit)) return st;
+    if (n == 0) return XNP_OK;
+    FL_TRY(hipSetDevice(pool_desc(lm->pool)->device), "hipSetDevice");
+    if (xnp_status st = xnp_batch_begin(lm->pool, ids, n, 1, hip_stream)) return st;
+    if (xnp_status st = fl_frame_launches(lm, n, latent_in, noise, latent_out, eos_logit, hip_stream)) {
+        (void)xnp_batch_abort(lm->pool);
+        return st;
+    }
+    return xnp_batch_end(lm->pool);
+}
+
+extern "C" xnp_status xnp_flow_lm_step_graph(xnp_flow_lm *lm, const int32_t *ids, int32_t n, const float *latent_in,
+                                             const float *noise, float *latent_out, float *eos_logit,
+                                             void *hip_stream) {
+    if (xnp_status st = fl_step_check(lm, ids, n, noise, latent_out, eos_logit)) return st;
+    if (n == 0) return XNP_OK;
+    if (!hip_stream) return pool_fail(XNP_E_INVALID, "a graph is recorded on a stream of the caller's, not the null stream");
+    hipStream_t hs = (hipStream_t)hip_stream;
+    FL_TRY(hipSetDevice(pool_desc(lm->pool)->device), "hipSetDevice");
+    // the plan (positions, pages) is uploaded eagerly; the frame's launches read it from the
+    // pool's device buffers, so one recording serves every step with the same rows and buffers
+    if (xnp_status st = xnp_batch_begin(lm->pool, ids, n, 1, hip_stream)) return st;
+    FlowGraph &G = lm->graph;
+    const bool same = G.exec && G.n == n && G.latent_in == latent_in && G.noise == noise && G.latent_out == latent_out &&
+                      G.eos == eos_logit && G.stream == hs;
+    if (!same) {
+        if (G.exec) (void)hipGraphExecDestroy(G.exec);
+        G = FlowGraph();
+        hipGraph_t graph = nullptr;
+        hipError_t e = hipStreamBeginCapture(hs, hipStreamCaptureModeThreadLocal);
+        if (e != hipSuccess) {
+            (void)xnp_batch_abort(lm->pool);
+            return pool_fail(XNP_E_HIP, "graph capture: %s", hipGetErrorString(e));
+        }
+        xnp_status st = fl_frame_launches(lm, n, latent_in, noise, latent_out, eos_logit, hip_stream);
+        e = hipStreamEndCapture(hs, &graph);
+        if (st == XNP_OK && e == hipSuccess) e = hipGraphInstantiate(&G.exec, graph, nullptr, nullptr, 0);
+        if (graph) (void)hipGraphDestroy(graph);
+        if (st != XNP_OK || e != hipSuccess) {
+            G = FlowGraph();
+            (void)xnp_batch_abort(lm->pool);
+            return st != XNP_OK ? st : pool_fail(XNP_E_HIP, "graph capture: %s", hipGetErrorString(e));
+        }
+        G.n = n, G.latent_in = latent_in, G.noise = noise, G.latent_out = latent_out, G.eos = eos_logit, G.stream = hs;
+    }
+    hipError_t e = hipGraphLaunch(G.exec, hs);
+    if (e != hipSuccess) {
+        (void)xnp_batch_abort(lm->pool);
+        return pool_fail(XNP_E_HIP, "graph launch: %s", hipGetErrorString(e));
+    }
+    return xnp_batch_end(lm->pool);
 }

@@ -14,6 +14,16 @@
 
 namespace xnp {
 
+// Launch a kernel; with timing events, through hipExtLaunchKernel so that the events bracket the
+// kernel alone.  Without them, a plain launch: the form a stream capture (hipGraph) records.
+#define XNP_LAUNCH(kernel, grid, block, stream, tm, ...)                                            \
+    do {                                                                                           \
+        if ((tm).start)                                                                            \
+            hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, (tm).start, (tm).stop, 0, __VA_ARGS__); \
+        else                                                                                       \
+            hipLaunchKernelGGL(kernel, grid, block, 0, stream, __VA_ARGS__);                       \
+    } while (0)
+
 // ---------------------------------------------------------------------------------------------
 // element helpers
 
@@ -536,8 +546,7 @@ static hipError_t decode_impl(const PoolView &pv, const BatchView &bv, int layer
     const dim3 grid(bv.n * pv.H);
     const int f = fused ? 1 : 0;
 #define XNP_DECODE(S, PFX)                                                                                          \
-    hipExtLaunchKernelGGL((k_decode<CDT, ABF, S, PFX>), grid, dim3(64 * S), 0, stream, tm.start, tm.stop, 0, pv, bv, \
-                          layer, q, k, v, out, qmul, f)
+    XNP_LAUNCH((k_decode<CDT, ABF, S, PFX>), grid, dim3(64 * S), stream, tm, pv, bv, layer, q, k, v, out, qmul, f)
     if (bv.prefix) {
         switch (bv.split) {
         case 1: XNP_DECODE(1, true); break;
@@ -960,10 +969,10 @@ static hipError_t prefill_rows_impl(const PoolView &pv, const BatchView &bv, int
     const float qmul = scale * 1.4426950408889634f;
     const dim3 grid(bv.n * bv.t * pv.H);
     switch (bv.split) {
-    case 1: hipExtLaunchKernelGGL((k_prefill_rows<CDT, ABF, 1>), grid, dim3(64), 0, stream, tm.start, tm.stop, 0, pv, bv, layer, q, out, qmul); break;
-    case 2: hipExtLaunchKernelGGL((k_prefill_rows<CDT, ABF, 2>), grid, dim3(128), 0, stream, tm.start, tm.stop, 0, pv, bv, layer, q, out, qmul); break;
-    case 4: hipExtLaunchKernelGGL((k_prefill_rows<CDT, ABF, 4>), grid, dim3(256), 0, stream, tm.start, tm.stop, 0, pv, bv, layer, q, out, qmul); break;
-    case 8: hipExtLaunchKernelGGL((k_prefill_rows<CDT, ABF, 8>), grid, dim3(512), 0, stream, tm.start, tm.stop, 0, pv, bv, layer, q, out, qmul); break;
+    case 1: XNP_LAUNCH((k_prefill_rows<CDT, ABF, 1>), grid, dim3(64), stream, tm, pv, bv, layer, q, out, qmul); break;
+    case 2: XNP_LAUNCH((k_prefill_rows<CDT, ABF, 2>), grid, dim3(128), stream, tm, pv, bv, layer, q, out, qmul); break;
+    case 4: XNP_LAUNCH((k_prefill_rows<CDT, ABF, 4>), grid, dim3(256), stream, tm, pv, bv, layer, q, out, qmul); break;
+    case 8: XNP_LAUNCH((k_prefill_rows<CDT, ABF, 8>), grid, dim3(512), stream, tm, pv, bv, layer, q, out, qmul); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -979,8 +988,8 @@ hipError_t launch_prefill(const PoolView &pv, const BatchView &bv, int layer, co
     switch (pv.cache_dt * 2 + pv.act_dt) {
     case DT_F32 * 2 + DT_F32: return prefill_rows_impl<DT_F32, false>(pv, bv, layer, q, out, scale, stream, tm);
     case DT_BF16 * 2 + DT_BF16:
-        hipExtLaunchKernelGGL(k_prefill_mfma, dim3(bv.n * pv.H), dim3(64 * kPfWaves), 0, stream, tm.start, tm.stop, 0,
-                              pv, bv, layer, q, k, v, out, scale * 1.4426950408889634f, fused ? 1 : 0);
+        XNP_LAUNCH(k_prefill_mfma, dim3(bv.n * pv.H), dim3(64 * kPfWaves), stream, tm, pv, bv, layer, q, k, v, out,
+                   scale * 1.4426950408889634f, fused ? 1 : 0);
         return hipGetLastError();
     case DT_I8 * 2 + DT_BF16: return prefill_rows_impl<DT_I8, true>(pv, bv, layer, q, out, scale, stream, tm);
     case DT_I8 * 2 + DT_F32: return prefill_rows_impl<DT_I8, false>(pv, bv, layer, q, out, scale, stream, tm);
@@ -1199,26 +1208,59 @@ hipError_t launch_gemm_q8(const void *A, int M, int K, const int8_t *W, const fl
 // Batch-1 frames make these matrix-vector products: one wave per output channel, the weight
 // row held in registers, each row of x reduced across the wave.
 
-template <int KC, int EPI>
+template <int KC, int EPI, bool NORM>
 __global__ __launch_bounds__(256) void k_linear_f32(const float *x, int ldx, int M, int K, const float *W,
-                                                    const float *bias, int N, LinOut lo) {
+                                                    const float *bias, int N, LinOut lo, LinNorm ln) {
     const int n = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (n >= N) return;
-    float w[KC];
+    // every load is issued unconditionally (the index clamped, the value then zeroed), so that all
+    // of them are in flight together rather than each behind a branch and a wait
+    float w[KC], nw[KC], nb[KC];
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
-        const int k = c * 64 + lane;
-        w[c] = k < K ? W[(size_t)n * K + k] : 0.f;
+        const int k = c * 64 + lane, kk = min(k, K - 1);
+        const float wv = W[(size_t)n * K + kk];
+        w[c] = k < K ? wv : 0.f;
+        if constexpr (NORM) {
+            nw[c] = ln.w ? ln.w[kk] : 1.f;
+            nb[c] = ln.w ? ln.b[kk] : 0.f;
+        }
     }
     const float b = bias ? bias[n] : 0.f;
     for (int m = 0; m < M; ++m) {
         const float *xr = x + (size_t)m * ldx;
+        float xv[KC];
+#pragma unroll
+        for (int c = 0; c < KC; ++c) xv[c] = xr[min(c * 64 + lane, K - 1)];
+        if constexpr (NORM) {
+            // LayerNorm of the row over K, then the AdaLN modulation y * (1 + scale) + shift (mlp.rs:4-11)
+            float sum = 0.f;
+#pragma unroll
+            for (int c = 0; c < KC; ++c) sum += c * 64 + lane < K ? xv[c] : 0.f;
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o);
+            const float mean = sum / (float)K;
+            float sq = 0.f;
+#pragma unroll
+            for (int c = 0; c < KC; ++c) {
+                const float d = c * 64 + lane < K ? xv[c] - mean : 0.f;
+                sq = __builtin_fmaf(d, d, sq);
+            }
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
+            const float rstd = 1.0f / __builtin_sqrtf(sq / (float)K + ln.eps);
+#pragma unroll
+            for (int c = 0; c < KC; ++c) {
+                const int kk = min(c * 64 + lane, K - 1);
+                float y = (xv[c] - mean) * rstd;
+                if (ln.w) y = y * nw[c] + nb[c];
+                if (ln.shift) y = y * (ln.scale[(size_t)m * ln.ld_mod + kk] + 1.0f) + ln.shift[(size_t)m * ln.ld_mod + kk];
+                xv[c] = y;
+            }
+        }
         float acc = 0.f;
 #pragma unroll
-        for (int c = 0; c < KC; ++c) {
-            const int k = c * 64 + lane;
-            if (k < K) acc = __builtin_fmaf(w[c], xr[k], acc);
-        }
+        for (int c = 0; c < KC; ++c) acc = __builtin_fmaf(w[c], xv[c], acc); // w is 0 past K
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
         if (lane != 0) continue;
@@ -1248,11 +1290,11 @@ __global__ __launch_bounds__(256) void k_linear_f32(const float *x, int ldx, int
     }
 }
 
-template <int KC>
+template <int KC, bool NORM>
 static hipError_t linear_f32_kc(const float *x, int ldx, int M, int K, const float *W, const float *b, int N, int epi,
-                                const LinOut &lo, hipStream_t stream) {
+                                const LinOut &lo, const LinNorm &ln, hipStream_t stream) {
     const dim3 grid((N + 3) / 4), block(256);
-#define XNP_LIN(E) hipLaunchKernelGGL((k_linear_f32<KC, E>), grid, block, 0, stream, x, ldx, M, K, W, b, N, lo)
+#define XNP_LIN(E) hipLaunchKernelGGL((k_linear_f32<KC, E, NORM>), grid, block, 0, stream, x, ldx, M, K, W, b, N, lo, ln)
     switch (epi) {
     case kLinStore: XNP_LIN(kLinStore); break;
     case kLinGeluErf: XNP_LIN(kLinGeluErf); break;
@@ -1268,71 +1310,23 @@ static hipError_t linear_f32_kc(const float *x, int ldx, int M, int K, const flo
     return hipGetLastError();
 }
 
-hipError_t launch_linear_f32(const float *x, int ldx, int M, int K, const float *W, const float *b, int N, int epi,
-                             const LinOut &lo, hipStream_t stream) {
-    if (M <= 0 || N <= 0) return hipSuccess;
+template <bool NORM>
+static hipError_t linear_f32_norm(const float *x, int ldx, int M, int K, const float *W, const float *b, int N, int epi,
+                                  const LinOut &lo, const LinNorm &ln, hipStream_t stream) {
     const int kc = (K + 63) / 64;
-    if (kc <= 1) return linear_f32_kc<1>(x, ldx, M, K, W, b, N, epi, lo, stream);
-    if (kc <= 4) return linear_f32_kc<4>(x, ldx, M, K, W, b, N, epi, lo, stream);
-    if (kc <= 8) return linear_f32_kc<8>(x, ldx, M, K, W, b, N, epi, lo, stream);
-    if (kc <= 16) return linear_f32_kc<16>(x, ldx, M, K, W, b, N, epi, lo, stream);
-    if (kc <= 32) return linear_f32_kc<32>(x, ldx, M, K, W, b, N, epi, lo, stream);
+    if (kc <= 1) return linear_f32_kc<1, NORM>(x, ldx, M, K, W, b, N, epi, lo, ln, stream);
+    if (kc <= 4) return linear_f32_kc<4, NORM>(x, ldx, M, K, W, b, N, epi, lo, ln, stream);
+    if (kc <= 8) return linear_f32_kc<8, NORM>(x, ldx, M, K, W, b, N, epi, lo, ln, stream);
+    if (kc <= 16) return linear_f32_kc<16, NORM>(x, ldx, M, K, W, b, N, epi, lo, ln, stream);
+    if (kc <= 32) return linear_f32_kc<32, NORM>(x, ldx, M, K, W, b, N, epi, lo, ln, stream);
     return hipErrorInvalidValue;
 }
 
-// LayerNorm of f32 rows (eps given; w, b optional), then, when shift is given, the AdaLN
-// modulation y * (1 + scale) + shift with per-row shift/scale (mlp.rs:4-11).  One wave per row.
-template <int CH>
-__global__ __launch_bounds__(256) void k_ln_f32(const float *x, int rows, int dim, const float *w, const float *b,
-                                                float eps, const float *shift, const float *scale, int ld_mod,
-                                                float *out) {
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (row >= rows) return;
-    const float *xr = x + (size_t)row * dim;
-    float v[CH];
-    float sum = 0.f;
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-        const int i = c * 64 + lane;
-        v[c] = i < dim ? xr[i] : 0.f;
-        sum += v[c];
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o);
-    const float mean = sum / (float)dim;
-    float sq = 0.f;
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-        const float d = c * 64 + lane < dim ? v[c] - mean : 0.f;
-        sq = __builtin_fmaf(d, d, sq);
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
-    const float rstd = 1.0f / __builtin_sqrtf(sq / (float)dim + eps);
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-        const int i = c * 64 + lane;
-        if (i >= dim) continue;
-        float y = (v[c] - mean) * rstd;
-        if (w) y = y * w[i] + b[i];
-        if (shift) y = y * (scale[(size_t)row * ld_mod + i] + 1.0f) + shift[(size_t)row * ld_mod + i];
-        out[(size_t)row * dim + i] = y;
-    }
-}
-
-hipError_t launch_ln_f32(const float *x, int rows, int dim, const float *w, const float *b, float eps,
-                         const float *shift, const float *scale, int ld_mod, float *out, hipStream_t stream) {
-    if (rows <= 0) return hipSuccess;
-    const dim3 grid((rows + 3) / 4), block(256);
-    const int ch = (dim + 63) / 64;
-#define XNP_LN(C) hipLaunchKernelGGL(k_ln_f32<C>, grid, block, 0, stream, x, rows, dim, w, b, eps, shift, scale, ld_mod, out)
-    if (ch <= 4) XNP_LN(4);
-    else if (ch <= 8) XNP_LN(8);
-    else if (ch <= 16) XNP_LN(16);
-    else if (ch <= 32) XNP_LN(32);
-    else return hipErrorInvalidValue;
-#undef XNP_LN
-    return hipGetLastError();
+hipError_t launch_linear_f32(const float *x, int ldx, int M, int K, const float *W, const float *b, int N, int epi,
+                             const LinOut &lo, hipStream_t stream, const LinNorm *ln) {
+    if (M <= 0 || N <= 0) return hipSuccess;
+    if (ln) return linear_f32_norm<true>(x, ldx, M, K, W, b, N, epi, lo, *ln, stream);
+    return linear_f32_norm<false>(x, ldx, M, K, W, b, N, epi, lo, LinNorm(), stream);
 }
 
 // LUTConditioner::embed_tokens (conditioners.rs:239-262): out[r] = table[ids[r]], rows of dim f32.

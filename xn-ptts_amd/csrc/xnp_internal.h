@@ -141,10 +141,19 @@ struct LinOut {
     float alpha = 1.f;
 };
 
+// A LayerNorm over each row of x applied as the linear reads it (mean, then the centred sum of
+// squares, rstd = 1 / sqrt(var + eps)): eps; the
+// affine w, b (both null: none); the AdaLN modulation y * (1 + scale) + shift with per-row
+// shift/scale of row stride ld_mod (shift null: none).
+struct LinNorm {
+    const float *w = nullptr, *b = nullptr;
+    float eps = 1e-5f;
+    const float *shift = nullptr, *scale = nullptr;
+    int32_t ld_mod = 0;
+};
+
 hipError_t launch_linear_f32(const float *x, int ldx, int M, int K, const float *W, const float *b, int N, int epi,
-                             const LinOut &lo, hipStream_t stream);
-hipError_t launch_ln_f32(const float *x, int rows, int dim, const float *w, const float *b, float eps,
-                         const float *shift, const float *scale, int ld_mod, float *out, hipStream_t stream);
+                             const LinOut &lo, hipStream_t stream, const LinNorm *ln = nullptr);
 hipError_t launch_embed_f32(const float *table, const int32_t *ids, int rows, int dim, float *out, hipStream_t stream);
 hipError_t launch_rows_io(const PoolView &pv, int sid, int layer, int kv, int slot0, int n,
                           void *rows, float *scales, bool write, hipStream_t stream);

@@ -146,9 +146,11 @@ class FlowLM:
         _check(self._lib.xnp_flow_lm_prompt_text(self._h, arr, len(ids), tokens.ctypes.data, tokens.shape[1],
                                                  _stream(stream)))
 
-    def step(self, ids, latent_in, noise, latent_out, eos_out, stream=None):
+    def step(self, ids, latent_in, noise, latent_out, eos_out, stream=None, graph: bool = False):
         """One frame for each stream: latent_in [n][ldim] (None: bos_emb), noise [n][ldim],
-        latent_out [n][ldim], eos_out [n] -- f32 device tensors."""
+        latent_out [n][ldim], eos_out [n] -- f32 device tensors.  graph: replay a recording of the
+        frame's launches (xnp_flow_lm_step_graph; needs a non-null stream)."""
         arr = (ctypes.c_int32 * len(ids))(*ids)
-        _check(self._lib.xnp_flow_lm_step(self._h, arr, len(ids), _ptr(latent_in), _ptr(noise), _ptr(latent_out),
-                                          _ptr(eos_out), _stream(stream)))
+        fn = self._lib.xnp_flow_lm_step_graph if graph else self._lib.xnp_flow_lm_step
+        _check(fn(self._h, arr, len(ids), _ptr(latent_in), _ptr(noise), _ptr(latent_out), _ptr(eos_out),
+                  _stream(stream)))

@@ -110,6 +110,7 @@ SIGNATURES = {
     "xnp_flow_lm_destroy": (_i32, [_p]),
     "xnp_flow_lm_prompt_text": (_i32, [_p, _i32p, _i32, _p, _i32, _p]),
     "xnp_flow_lm_step": (_i32, [_p, _i32p, _i32, _p, _p, _p, _p, _p]),
+    "xnp_flow_lm_step_graph": (_i32, [_p, _i32p, _i32, _p, _p, _p, _p, _p]),
     "xnp_frame_budget": (_i32, [_i32, _c.c_double]),
     "xnp_seq_budget": (_i32, [_i32, _i32]),
     "xnp_last_error": (_c.c_char_p, []),
