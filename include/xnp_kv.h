@@ -95,7 +95,8 @@ typedef struct xnp_pool_desc {
                              free list seeded with it (shuffled block tables) */
     int32_t device;       /* HIP device ordinal */
     int32_t decode_split; /* waves sharing one (stream, head) in decode: 1, 2, 4 or 8; a stream
-                             holds at most 60 * decode_split pages; 0: the fewest that fit */
+                             holds at most 60 * decode_split pages; 0: the fewest that fit, raised
+                             per batch (up to 8) while the batch has under 1024 waves */
 } xnp_pool_desc;
 
 typedef struct xnp_stream_info {

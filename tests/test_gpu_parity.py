@@ -163,9 +163,11 @@ class Pair:
 
 
 # ---- linear caches -----------------------------------------------------------------------------
+# split 0 lets the library choose: 8 waves per (stream, head) for batches as small as these
+@pytest.mark.parametrize("split", [0, 2])
 @pytest.mark.parametrize("cache,act", [("bf16", "bf16"), ("f32", "f32"), ("i8", "bf16"), ("i8", "f32")])
-def test_append_and_decode_match_the_oracle(cache, act):
-    p = Pair(cache=cache, act=act, streams=8, cap=300, seed=1, page_seed=7)
+def test_append_and_decode_match_the_oracle(cache, act, split):
+    p = Pair(cache=cache, act=act, streams=8, cap=300, seed=1, page_seed=7, split=split)
     lens = [0, 1, 15, 16, 17, 100, 200, 255]
     for i, n in enumerate(lens):
         p.fill(i, n)
@@ -245,10 +247,11 @@ def test_fork_shares_the_prefix_and_diverges():
 # ---- rings (transformer.rs:842-929) ----------------------------------------------------------------
 @pytest.mark.parametrize("cache,act,mode", [("f32", "f32", "shift"), ("bf16", "bf16", "shift"),
                                             ("bf16", "bf16", "absolute"), ("i8", "bf16", "absolute")])
-def test_ring_sessions_match_the_oracle(cache, act, mode):
+@pytest.mark.parametrize("split", [0, 2])
+def test_ring_sessions_match_the_oracle(cache, act, mode, split):
     # The s2s policy on several streams at once: a voice prefix, then frames in a context of 24
     # slots whose oldest third goes whenever it is full (s2s.rs:318-333).
-    p = Pair(cache=cache, act=act, streams=3, cap=64, seed=6)
+    p = Pair(cache=cache, act=act, streams=3, cap=64, seed=6, split=split)
     v, context = [5, 16, 0], 24
     for i in range(3):
         p.fill(i, v[i])

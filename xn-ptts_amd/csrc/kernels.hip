@@ -1208,7 +1208,12 @@ hipError_t launch_gemm_q8(const void *A, int M, int K, const int8_t *W, const fl
 // Batch-1 frames make these matrix-vector products: one wave per output channel, the weight
 // row held in registers, each row of x reduced across the wave.
 
-template <int KC, int EPI, bool NORM>
+// NORM: a bit set of kNormLn (LayerNorm the row of x over K), kNormAffine (then * w + b) and
+// kNormMod (then the AdaLN modulation y * (1 + scale) + shift, mlp.rs:4-11).  Compile-time, so
+// that the norm's operands load together with x instead of behind a branch after the reductions.
+constexpr int kNormLn = 1, kNormAffine = 2, kNormMod = 4;
+
+template <int KC, int EPI, int NORM>
 __global__ __launch_bounds__(256) void k_linear_f32(const float *x, int ldx, int M, int K, const float *W,
                                                     const float *bias, int N, LinOut lo, LinNorm ln) {
     const int n = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -1221,19 +1226,26 @@ __global__ __launch_bounds__(256) void k_linear_f32(const float *x, int ldx, int
         const int k = c * 64 + lane, kk = min(k, K - 1);
         const float wv = W[(size_t)n * K + kk];
         w[c] = k < K ? wv : 0.f;
-        if constexpr (NORM) {
-            nw[c] = ln.w ? ln.w[kk] : 1.f;
-            nb[c] = ln.w ? ln.b[kk] : 0.f;
+        if constexpr ((NORM & kNormAffine) != 0) {
+            nw[c] = ln.w[kk];
+            nb[c] = ln.b[kk];
         }
     }
     const float b = bias ? bias[n] : 0.f;
     for (int m = 0; m < M; ++m) {
         const float *xr = x + (size_t)m * ldx;
-        float xv[KC];
+        float xv[KC], sh[KC], sc[KC];
 #pragma unroll
-        for (int c = 0; c < KC; ++c) xv[c] = xr[min(c * 64 + lane, K - 1)];
-        if constexpr (NORM) {
-            // LayerNorm of the row over K, then the AdaLN modulation y * (1 + scale) + shift (mlp.rs:4-11)
+        for (int c = 0; c < KC; ++c) {
+            const int kk = min(c * 64 + lane, K - 1);
+            xv[c] = xr[kk];
+            if constexpr ((NORM & kNormMod) != 0) {
+                sh[c] = ln.shift[(size_t)m * ln.ld_mod + kk];
+                sc[c] = ln.scale[(size_t)m * ln.ld_mod + kk];
+            }
+        }
+        if constexpr ((NORM & kNormLn) != 0) {
+            // mean, then the centred sum of squares: the two passes of a textbook LayerNorm
             float sum = 0.f;
 #pragma unroll
             for (int c = 0; c < KC; ++c) sum += c * 64 + lane < K ? xv[c] : 0.f;
@@ -1251,10 +1263,9 @@ __global__ __launch_bounds__(256) void k_linear_f32(const float *x, int ldx, int
             const float rstd = 1.0f / __builtin_sqrtf(sq / (float)K + ln.eps);
 #pragma unroll
             for (int c = 0; c < KC; ++c) {
-                const int kk = min(c * 64 + lane, K - 1);
                 float y = (xv[c] - mean) * rstd;
-                if (ln.w) y = y * nw[c] + nb[c];
-                if (ln.shift) y = y * (ln.scale[(size_t)m * ln.ld_mod + kk] + 1.0f) + ln.shift[(size_t)m * ln.ld_mod + kk];
+                if constexpr ((NORM & kNormAffine) != 0) y = y * nw[c] + nb[c];
+                if constexpr ((NORM & kNormMod) != 0) y = y * (sc[c] + 1.0f) + sh[c];
                 xv[c] = y;
             }
         }
@@ -1290,7 +1301,7 @@ __global__ __launch_bounds__(256) void k_linear_f32(const float *x, int ldx, int
     }
 }
 
-template <int KC, bool NORM>
+template <int KC, int NORM>
 static hipError_t linear_f32_kc(const float *x, int ldx, int M, int K, const float *W, const float *b, int N, int epi,
                                 const LinOut &lo, const LinNorm &ln, hipStream_t stream) {
     const dim3 grid((N + 3) / 4), block(256);
@@ -1310,7 +1321,7 @@ static hipError_t linear_f32_kc(const float *x, int ldx, int M, int K, const flo
     return hipGetLastError();
 }
 
-template <bool NORM>
+template <int NORM>
 static hipError_t linear_f32_norm(const float *x, int ldx, int M, int K, const float *W, const float *b, int N, int epi,
                                   const LinOut &lo, const LinNorm &ln, hipStream_t stream) {
     const int kc = (K + 63) / 64;
@@ -1325,8 +1336,13 @@ static hipError_t linear_f32_norm(const float *x, int ldx, int M, int K, const f
 hipError_t launch_linear_f32(const float *x, int ldx, int M, int K, const float *W, const float *b, int N, int epi,
                              const LinOut &lo, hipStream_t stream, const LinNorm *ln) {
     if (M <= 0 || N <= 0) return hipSuccess;
-    if (ln) return linear_f32_norm<true>(x, ldx, M, K, W, b, N, epi, lo, *ln, stream);
-    return linear_f32_norm<false>(x, ldx, M, K, W, b, N, epi, lo, LinNorm(), stream);
+    if (!ln) return linear_f32_norm<0>(x, ldx, M, K, W, b, N, epi, lo, LinNorm(), stream);
+    if ((ln->w == nullptr) != (ln->b == nullptr) || (ln->shift == nullptr) != (ln->scale == nullptr))
+        return hipErrorInvalidValue;
+    if (ln->w && ln->shift) return linear_f32_norm<kNormLn | kNormAffine | kNormMod>(x, ldx, M, K, W, b, N, epi, lo, *ln, stream);
+    if (ln->w) return linear_f32_norm<kNormLn | kNormAffine>(x, ldx, M, K, W, b, N, epi, lo, *ln, stream);
+    if (ln->shift) return linear_f32_norm<kNormLn | kNormMod>(x, ldx, M, K, W, b, N, epi, lo, *ln, stream);
+    return linear_f32_norm<kNormLn>(x, ldx, M, K, W, b, N, epi, lo, *ln, stream);
 }
 
 // LUTConditioner::embed_tokens (conditioners.rs:239-262): out[r] = table[ids[r]], rows of dim f32.

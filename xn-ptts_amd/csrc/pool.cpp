@@ -996,7 +996,12 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
     B.bv.plans = (const StreamPlan *)(pool->dbatch + o_plans);
     B.bv.recs = pool->dbatch + o_recs;
     B.bv.rec_stride = pool->rec_stride;
+    // unless the caller fixed the split: a batch of few (stream, head) groups fills few CUs, so give
+    // each group more waves (a larger split only raises the pages a group can index) until the batch
+    // has about one wave per SIMD
     B.bv.split = pool->split;
+    while (!pool->d.decode_split && B.bv.split < 8 && (int64_t)n * t * pool->d.num_heads * B.bv.split < 1024)
+        B.bv.split *= 2;
     B.bv.prefix = 0;
     for (int32_t i = 0; i < n; i++) B.bv.prefix |= plans[i].prefix > 0;
     B.bv.masks = (const uint32_t *)(pool->dbatch + o_masks);
