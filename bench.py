@@ -639,12 +639,12 @@ def run_flowlm(args, xnp, torch):
                           "n_bins 4000, flow net 512 x 6, 1 LSD step), random-init f32 weights N(0, 0.02), unit "
                           "norms; 64 seeded tokens, then greedy frames at temperature 0 on an f32 paged cache",
               "streams": 1, "layers": cfg.num_layers, "prompt_tokens": 64, "frames_timed": args.steps}
-    # batch 1 is launch-bound (about 80 launches a frame): the roofline is the frame's bytes (every
-    # f32 weight once plus the K/V attended) over its wall time, not one kernel's
+    # batch 1 is bound by its chain of about 50 dependent kernels: the roofline is the frame's bytes
+    # (every f32 weight once plus the K/V attended) over its wall time, not one kernel's
     roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "whole frame replayed from a hipGraph: f32 linears, LayerNorms, k_decode<f32>, flow net "
-                      "(batch 1, launch-bound)",
+            "kernel": "whole frame replayed from a hipGraph: f32 linears (LayerNorms fused), k_decode<f32>, flow "
+                      "net (batch 1, bound by its chain of about 50 dependent kernels)",
             "bytes_per_frame": int(bytes_mean)}
     return line("frames/sec, single-stream flow LM (Phonon-31m shape, fp32)", fps, "frames/s", args, ms, "f32",
                 config, roof, cpu, extra=extra)

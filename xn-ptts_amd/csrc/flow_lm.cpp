@@ -122,6 +122,10 @@ struct xnp_flow_lm {
     Layout L{};
     float *w = nullptr;    // the weight blob on the device
     float *temb = nullptr; // [lsd_steps][F]: SimpleMLPAdaLN::time_embedding of each solver step
+    // every residual block's adaLN_modulation then the final layer's, stacked: [na][F] and [na].
+    // They all read the same conditioning vector, so one launch computes them together.
+    float *adaw = nullptr, *adab = nullptr;
+    int32_t na = 0; // flow_depth * 3F + 2F
     // scratch for max_rows rows
     float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *f = nullptr;
     float *ya = nullptr, *ada = nullptr, *xf = nullptr, *h2 = nullptr;
@@ -186,14 +190,15 @@ extern "C" xnp_status xnp_flow_lm_create(xnp_pool *pool, const xnp_flow_lm_desc 
         if (r == hipSuccess) lm->allocs.push_back(*p);
         return r;
     };
-    const size_t M = d.max_rows, dm = d.d_model, F = d.flow_dim;
+    const size_t M = d.max_rows, dm = d.d_model, F = d.flow_dim, na = (size_t)d.flow_depth * 3 * F + 2 * F;
+    lm->na = (int32_t)na;
     struct {
         float **p;
         size_t n;
     } bufs[] = {{&lm->w, L.total}, {&lm->temb, (size_t)d.lsd_steps * F}, {&lm->x, M * dm},
                 {&lm->q, M * dm},  {&lm->k, M * dm},  {&lm->v, M * dm}, {&lm->att, M * dm},
-                {&lm->f, M * (size_t)d.ff}, {&lm->ya, M * F}, {&lm->ada, M * 3 * F},
-                {&lm->xf, M * F}, {&lm->h2, M * F}};
+                {&lm->f, M * (size_t)d.ff}, {&lm->ya, M * F}, {&lm->ada, M * na},
+                {&lm->xf, M * F}, {&lm->h2, M * F}, {&lm->adaw, na * F}, {&lm->adab, na}};
     for (auto &b : bufs)
         if ((e = dalloc((void **)b.p, sizeof(float) * b.n)) != hipSuccess) return fail_hip(e, "flow LM buffers");
     if ((e = dalloc((void **)&lm->dids, sizeof(int32_t) * M)) != hipSuccess) return fail_hip(e, "flow LM ids");
@@ -201,6 +206,15 @@ extern "C" xnp_status xnp_flow_lm_create(xnp_pool *pool, const xnp_flow_lm_desc 
         return fail_hip(e, "pinned ids");
     if ((e = hipMemcpy(lm->w, weights, sizeof(float) * L.total, hipMemcpyHostToDevice)) != hipSuccess)
         return fail_hip(e, "weight upload");
+    for (int r = 0; r <= d.flow_depth; r++) { // the stacked adaLN_modulation rows
+        const bool fin = r == d.flow_depth;
+        const size_t rows = (fin ? 2 : 3) * F, row0 = (size_t)r * 3 * F;
+        if ((e = hipMemcpy(lm->adaw + row0 * F, weights + (fin ? L.fin_aw : L.rb_aw[r]), sizeof(float) * rows * F,
+                           hipMemcpyHostToDevice)) != hipSuccess ||
+            (e = hipMemcpy(lm->adab + row0, weights + (fin ? L.fin_ab : L.rb_ab[r]), sizeof(float) * rows,
+                           hipMemcpyHostToDevice)) != hipSuccess)
+            return fail_hip(e, "adaLN weight upload");
+    }
     // lsd_time_embeddings (flow_lm.rs:82-95): times (i / steps, (i + 1) / steps), averaged over the
     // two embedders (mlp.rs:201-212).  They depend on nothing but the weights: once, at load.
     std::vector<float> temb((size_t)d.lsd_steps * F), b(F);
@@ -320,28 +334,30 @@ static xnp_status fl_frame_launches(xnp_flow_lm *lm, int M, const float *latent_
         LinOut xf;
         xf.out[0] = lm->xf, xf.ld[0] = F;
         FL_TRY(launch_linear_f32(cur, ld, M, ld, lm->W(L.inp_w), lm->W(L.inp_b), F, kLinStore, xf, hs), "input_proj");
+        // every block's adaLN_modulation and the final layer's, in one launch: row m of lm->ada
+        // holds block r's (shift, scale, gate) at r * 3F and the final (shift, scale) at depth * 3F
+        const int na = lm->na;
+        LinOut a;
+        a.out[0] = lm->ada, a.ld[0] = na;
+        FL_TRY(launch_linear_f32(lm->ya, F, M, F, lm->adaw, lm->adab, na, kLinStore, a, hs), "adaLN_modulation");
         for (int r = 0; r < d.flow_depth; r++) { // ResBlock (mlp.rs:113-131)
-            LinOut a;
-            a.out[0] = lm->ada, a.ld[0] = 3 * F;
-            FL_TRY(launch_linear_f32(lm->ya, F, M, F, lm->W(L.rb_aw[r]), lm->W(L.rb_ab[r]), 3 * F, kLinStore, a, hs),
-                   "adaLN_modulation");
+            const float *mod = lm->ada + (size_t)r * 3 * F;
             LinNorm in; // in_ln and modulate(shift, scale), applied as mlp.0 reads x
             in.w = lm->W(L.rb_lnw[r]), in.b = lm->W(L.rb_lnb[r]), in.eps = 1e-6f;
-            in.shift = lm->ada, in.scale = lm->ada + F, in.ld_mod = 3 * F;
+            in.shift = mod, in.scale = mod + F, in.ld_mod = na;
             LinOut s1;
             s1.out[0] = lm->h2, s1.ld[0] = F;
             FL_TRY(launch_linear_f32(lm->xf, F, M, F, lm->W(L.rb_w1[r]), lm->W(L.rb_b1[r]), F, kLinSilu, s1, hs, &in),
                    "mlp.0");
             LinOut g;
-            g.out[0] = lm->xf, g.ld[0] = F, g.aux = lm->ada + 2 * F, g.ld_aux = 3 * F;
+            g.out[0] = lm->xf, g.ld[0] = F, g.aux = mod + 2 * F, g.ld_aux = na;
             FL_TRY(launch_linear_f32(lm->h2, F, M, F, lm->W(L.rb_w2[r]), lm->W(L.rb_b2[r]), F, kLinGated, g, hs), "mlp.2");
         }
-        LinOut a; // FinalLayer (mlp.rs:155-163)
-        a.out[0] = lm->ada, a.ld[0] = 2 * F;
-        FL_TRY(launch_linear_f32(lm->ya, F, M, F, lm->W(L.fin_aw), lm->W(L.fin_ab), 2 * F, kLinStore, a, hs),
-               "final adaLN_modulation");
-        LinNorm nf; // norm_final (no affine) and modulate, applied as the final linear reads x
-        nf.eps = 1e-6f, nf.shift = lm->ada, nf.scale = lm->ada + F, nf.ld_mod = 2 * F;
+        // FinalLayer (mlp.rs:155-163): norm_final (no affine) and modulate, applied as the final
+        // linear reads x
+        const float *fmod = lm->ada + (size_t)d.flow_depth * 3 * F;
+        LinNorm nf;
+        nf.eps = 1e-6f, nf.shift = fmod, nf.scale = fmod + F, nf.ld_mod = na;
         LinOut o;
         o.out[0] = latent_out, o.ld[0] = ld, o.aux = cur, o.ld_aux = ld, o.alpha = 1.0f / (float)d.lsd_steps;
         FL_TRY(launch_linear_f32(lm->xf, F, M, F, lm->W(L.fin_w), lm->W(L.fin_b), ld, kLinAxpy, o, hs, &nf),
