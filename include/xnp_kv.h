@@ -155,6 +155,15 @@ xnp_status xnp_write_rows(xnp_pool *pool, int32_t id, int32_t layer, int32_t kv,
                           int32_t n, const void *rows, const float *scales, void *hip_stream);
 xnp_status xnp_read_rows(const xnp_pool *pool, int32_t id, int32_t layer, int32_t kv,
                          int32_t slot0, int32_t n, void *rows, float *scales, void *hip_stream);
+/* voice_from_kv_cache, ptts-wasm/src/lib.rs:291-325: a voice stored as the flow LM's KV cache
+ * (`transformer.layers.{i}.self_attn/cache`, f32 [2, 1, n, H, D]: keys, already rotated, then
+ * values) becomes rows [0, n) of one layer of stream id, converted to the cache dtype on the
+ * device: bf16 rounded to nearest even; int8 with one scale per (page, head), amax / 127 over the
+ * page's rows, codes rint(x / s) clamped to +-127.  kv is device memory, [2][n][H][D] f32.  The
+ * stream must hold exactly n rows and no ring: open it, xnp_stream_advance(n), then load every
+ * layer.  Forks of it (xnp_stream_fork, with_seq_budget) then share its full pages. */
+xnp_status xnp_stream_load_kv(xnp_pool *pool, int32_t id, int32_t layer, const float *kv, int32_t n,
+                              void *hip_stream);
 
 /* ---- ring (transformer.rs:842-929) ------------------------------------------------------ */
 /* start_ring: valid[s] = s < current_end; write = filled = current_end.  `prefix` is used by

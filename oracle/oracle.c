@@ -578,6 +578,43 @@ int orc_write_rows(orc_stream *st, int layer, int kv, int slot0, int n, const fl
     return 0;
 }
 
+/* voice_from_kv_cache (ptts-wasm/src/lib.rs:291-325): the voice's f32 rows kv [2][n][H][D]
+ * (keys, already rotated, then values) become rows [0, n) of one layer, stored in the cache dtype.
+ * int8 has no counterpart in the reference; the policy here is one scale per (block, head),
+ * amax / 127 over the block's rows, and codes rint(x / s), as a block whose rows all arrive at
+ * once would take them. */
+int orc_load_kv(orc_stream *st, int layer, const float *kv, int n) {
+    if (check_rows(st, layer, 0, 0, n)) return -1;
+    if (st->ring != ORC_RING_NONE) return fail("a voice loads into a plain cache, not a ring");
+    if (n != st->current_end)
+        return fail("a %d-row voice loads into a stream holding exactly as many rows, not %d", n,
+                    st->current_end);
+    const int H = st->H, D = st->D;
+    for (int which = 0; which < 2; which++) {
+        const float *src = kv + (size_t)which * n * H * D;
+        if (st->cdt != ORC_I8) {
+            if (orc_write_rows(st, layer, which, 0, n, src, NULL, NULL)) return -1;
+            continue;
+        }
+        for (int b0 = 0; b0 < n; b0 += ORC_BLOCK) {
+            const int rows = n - b0 < ORC_BLOCK ? n - b0 : ORC_BLOCK;
+            for (int h = 0; h < H; h++) {
+                float amax = 0.f;
+                for (int r = 0; r < rows; r++)
+                    for (int d = 0; d < D; d++)
+                        amax = fmaxf(amax, fabsf(src[((size_t)(b0 + r) * H + h) * D + d]));
+                const float sc = amax / 127.0f;
+                for (int r = 0; r < rows; r++) {
+                    int8_t *dst = (int8_t *)st->kc[which] + idx(st, layer, b0 + r, h);
+                    for (int d = 0; d < D; d++) dst[d] = orc_quant(src[((size_t)(b0 + r) * H + h) * D + d], sc);
+                }
+                *scale_at(st, which, layer, b0 / ORC_BLOCK, h) = sc;
+            }
+        }
+    }
+    return 0;
+}
+
 /* ---------------------------------------------------------------------------------------- */
 /* the rest of the layer: transformer.rs:591-634                                            */
 

@@ -95,6 +95,10 @@ int orc_read_rows(const orc_stream *st, int layer, int kv, int slot0, int n, flo
                   int8_t *q8, float *scales);
 int orc_write_rows(orc_stream *st, int layer, int kv, int slot0, int n, const float *vals,
                    const int8_t *q8, const float *scales);
+/* voice_from_kv_cache (ptts-wasm/src/lib.rs:291-325): kv [2][n][H][D] f32 (keys, already
+ * rotated, then values) stored as rows [0, n) of one layer; the stream must hold exactly n rows
+ * and no ring.  int8: per (block, head) s = amax / 127 over the block's rows, q = rint(x / s). */
+int orc_load_kv(orc_stream *st, int layer, const float *kv, int n);
 
 /* --- the rest of a flow-LM transformer layer (transformer.rs:591-634) ------------------------ */
 /* LayerNorm over the last dimension, as norm1/norm2 (transformer.rs:547-548, eps 1e-5): per row,

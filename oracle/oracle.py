@@ -57,6 +57,7 @@ def lib():
                                              ctypes.c_int, _fp, _i8p, _fp]),
             "orc_write_rows": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                               ctypes.c_int, _fp, _i8p, _fp]),
+            "orc_load_kv": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _fp, ctypes.c_int]),
             "orc_batch_attend": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int, ctypes.c_int,
                                                 _fp, _fp, _fp, ctypes.c_float, _fp]),
             "orc_batch_commit": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int]),
@@ -224,6 +225,13 @@ class Stream:
         q = np.ascontiguousarray(q8 if q8 is not None else np.zeros((n, self.H, self.D), np.int8), np.int8)
         s, sp = _f32(scales if scales is not None else np.zeros((max(n // 16 + 2, 1), self.H), np.float32))
         _ok(lib().orc_write_rows(self.h, layer, kv, slot0, n, vp, q.ctypes.data_as(_i8p), sp))
+
+    def load_kv(self, layer, kv):
+        """voice_from_kv_cache (ptts-wasm/src/lib.rs:291-325): kv [2][n][H][D] f32 -> rows [0, n)."""
+        kv = np.ascontiguousarray(kv, np.float32)
+        assert kv.ndim == 4 and kv.shape[0] == 2, kv.shape
+        a, ap = _f32(kv)
+        _ok(lib().orc_load_kv(self.h, layer, ap, kv.shape[1]))
 
 
 def batch_attend(streams, layer, q, k, v, scale=0.125):

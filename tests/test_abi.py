@@ -345,3 +345,34 @@ def test_flow_lm_refuses_a_pool_it_does_not_fit():
         xnp.FlowLM(pool, cfg, np.zeros(xnp.flow_lm.blob_size(cfg), np.float32))
     with pytest.raises(xnp.XnpError):  # the blob does not match the layout
         xnp.FlowLM(pool, cfg, np.zeros(10, np.float32))
+
+
+# ---- voice files (ptts-wasm/src/lib.rs:291-325, 394-396) ------------------------------------------
+def test_voice_files_are_read_and_checked_as_the_reference_checks_them(tmp_path):
+    from safetensors.numpy import save_file
+    rng = np.random.default_rng(3)
+    names = [xnp.voice_kv_name(i) for i in range(2)]
+    assert names[1] == "transformer.layers.1.self_attn/cache"
+    good = {nm: rng.standard_normal((2, 1, 5, 4, 64)).astype(np.float32) for nm in names}
+    path = tmp_path / "voice.safetensors"
+    save_file(good, str(path))
+    frames, layers = xnp.voice_layers(xnp.read_voice_file(str(path)), 2, 4)
+    assert frames == 5
+    assert np.array_equal(layers[1], good[names[1]][:, 0])
+
+    def bad(name, arr, match):
+        t = dict(good)
+        if arr is None:
+            del t[name]
+        else:
+            t[name] = arr
+        with pytest.raises(ValueError, match=match):
+            xnp.voice_layers(t, 2, 4)
+
+    bad(names[1], None, "expected f32 tensor: transformer.layers.1.self_attn/cache")
+    bad(names[0], good[names[0]].astype(np.float16), "expected f32 tensor")
+    bad(names[0], np.zeros((3, 1, 5, 4, 64), np.float32), "expected a first dim of size 2, got 3")
+    bad(names[0], np.zeros((2, 2, 5, 4, 64), np.float32), "batch of 2")
+    bad(names[0], np.zeros((2, 1, 5, 8, 64), np.float32), "8 heads of 64, the pool holds 4")
+    bad(names[1], np.zeros((2, 1, 6, 4, 64), np.float32), "6 frames, layer 0 holds 5")
+    bad(names[0], np.zeros((2, 5, 4, 64), np.float32), "expected 5 dims")

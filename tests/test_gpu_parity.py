@@ -231,6 +231,45 @@ def test_empty_batch_is_a_no_op():
     assert p.pool.current_end(p.ids[0]) == 0
 
 
+# ---- voices stored as the KV cache (ptts-wasm/src/lib.rs:291-325) -------------------------------
+@pytest.mark.parametrize("cache,act", [("f32", "f32"), ("bf16", "bf16"), ("i8", "bf16")])
+def test_a_voice_file_loads_into_pages_and_its_forks_share_them(cache, act, tmp_path):
+    # An `embeddings_v2/` voice: per layer an f32 [2, 1, 37, H, D] cache (keys already rotated).
+    # Loaded once, then forked per generation (with_seq_budget): the forks share the two full
+    # pages, copy the 5-row tail page, and decode 20 frames each against the oracle.
+    from safetensors.numpy import save_file
+    p = Pair(cache=cache, act=act, streams=2, cap=128, seed=21)  # room for the voice and 3 forks
+    rng = np.random.default_rng(22)
+    n = 37
+    tensors = {xnp.voice_kv_name(l): (rng.standard_normal((2, 1, n, 8, 64)) * 2).astype(np.float32)
+               for l in range(p.L)}
+    path = tmp_path / "voice.safetensors"
+    save_file(tensors, str(path))
+    vid = p.pool.load_voice(str(path))
+    o = oracle.Stream(p.L, p.H, 64, n, cache=cache, act=act)
+    o.advance(n)
+    for l in range(p.L):
+        o.load_kv(l, tensors[xnp.voice_kv_name(l)][:, 0])
+    p.ids.append(vid)
+    p.orc.append(o)
+    assert p.pool.current_end(vid) == n
+    p.assert_cache_equal(2)
+    free0 = p.pool.stats()["free_blocks"]
+    for _ in range(3):
+        p.ids.append(p.pool.with_seq_budget(vid, 128))
+        p.orc.append(o.with_seq_budget(128))
+    assert free0 - p.pool.stats()["free_blocks"] == 3  # one copied tail page per fork
+    for _ in range(20):  # past the tail page: the forks take pages of their own
+        p.step(which=[3, 4, 5])
+    for i in range(2, 6):
+        p.assert_cache_equal(i)
+    # refusals: a stream of another length, and a ring
+    with pytest.raises(xnp.XnpError, match="exactly as many rows"):
+        p.pool.load_kv(p.ids[3], 0, torch.zeros((2, n, 8, 64), dtype=torch.float32, device=DEV))
+    with pytest.raises(ValueError, match="first dim of size 2"):
+        p.pool.load_voice({k: v[:1] for k, v in tensors.items()})
+
+
 # ---- with_seq_budget: shared pages ----------------------------------------------------------------
 def test_fork_shares_the_prefix_and_diverges():
     p = Pair(cache="bf16", act="bf16", streams=1, cap=128, seed=5)

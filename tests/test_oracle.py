@@ -377,6 +377,50 @@ def test_int8_rows_quantize_within_half_a_step():
     assert q8[0, 0, -1] == 127 and np.abs(vals[0, 0] - x[0, 0]).max() <= scales[0, 0] / 2 + 1e-7
 
 
+# ---- voices stored as the KV cache (ptts-wasm/src/lib.rs:291-325) -----------------------------
+@pytest.mark.parametrize("cache", ["f32", "bf16", "i8"])
+def test_a_voice_loads_as_its_rows_in_the_cache_dtype(cache):
+    rng = np.random.default_rng(31)
+    n, H = 37, 3  # two full blocks and a tail block of 5 rows
+    kv = (rng.standard_normal((2, n, H, 64)) * rng.uniform(0.1, 4.0, (1, n, H, 1))).astype(np.float32)
+    st = oracle.Stream(2, H, 64, 64, cache=cache, act="f32" if cache == "f32" else "bf16")
+    st.advance(n)
+    st.load_kv(1, kv)
+    assert st.current_end == n
+    for which in (0, 1):
+        vals, q8, scales = st.read_rows(1, which, 0, n)
+        x = kv[which]
+        if cache == "f32":
+            assert np.array_equal(vals.view(np.uint32), x.view(np.uint32))
+        elif cache == "bf16":
+            want = torch.from_numpy(x).to(torch.bfloat16).to(torch.float32).numpy()
+            assert np.array_equal(vals.view(np.uint32), want.view(np.uint32))
+        else:
+            for b in range(3):
+                blk, q = x[16 * b:16 * b + 16], q8[16 * b:16 * b + 16]
+                amax = np.abs(blk.astype(np.float64)).max(axis=(0, 2))  # [H], over the block's rows only
+                np.testing.assert_allclose(scales[b], amax / 127.0, rtol=1e-7)
+                # the largest magnitude of each (block, head) lands on code +-127, and every value
+                # is within half a step of what it dequantizes to
+                assert (np.abs(q.astype(int)).max(axis=(0, 2)) == 127).all()
+                err = np.abs(vals[16 * b:16 * b + 16].astype(np.float64) - blk)
+                assert (err <= scales[b][None, :, None] / 2 * (1 + 1e-6)).all()
+                np.testing.assert_array_equal(vals[16 * b:16 * b + 16], q * scales[b][None, :, None])
+    vals, _, _ = st.read_rows(0, 0, 0, n)  # layer 0 was not loaded
+    assert not vals.any()
+
+
+def test_a_voice_loads_only_into_a_plain_stream_of_its_length():
+    kv = np.zeros((2, 4, 2, 64), np.float32)
+    st = oracle.Stream(1, 2, 64, 32, cache="bf16", act="bf16")
+    with pytest.raises(oracle.OracleError, match="exactly as many rows"):
+        st.load_kv(0, kv)
+    st.advance(4)
+    st.start_ring("absolute")
+    with pytest.raises(oracle.OracleError, match="not a ring"):
+        st.load_kv(0, kv)
+
+
 # ---- the rest of the layer (transformer.rs:591-634) -------------------------------------------
 def test_layer_norm_matches_torch():
     # torch.nn.functional.layer_norm in f64 is the textbook definition (biased variance, eps inside

@@ -682,6 +682,63 @@ hipError_t launch_rows_io(const PoolView &pv, int sid, int layer, int kv, int sl
     return hipGetLastError();
 }
 
+// A voice stored as the KV cache (voice_from_kv_cache, ptts-wasm/src/lib.rs:291-325): rows
+// [0, n) of one layer from an f32 [2][n][H][D] tensor (keys, already rotated, then values),
+// converted to the cache dtype: f32 as is, bf16 rounded to nearest even, int8 with one scale per
+// (page, head), amax / 127 over the rows the page receives, and codes rint(x / s).  One wave per
+// (page, head, keys or values); lane d holds dimension d of each of the page's 16 rows, so every
+// row is one coalesced 256 B read.  Rows past n in the last page are left as they are.
+template <int CDT>
+__global__ __launch_bounds__(64) void k_load_kv(PoolView pv, int sid, int layer, const float *kv, int n) {
+    const int b = blockIdx.x, h = blockIdx.y, which = blockIdx.z, lane = threadIdx.x;
+    const int page = pv.tables[(size_t)sid * pv.mbps + b];
+    if (page < 0 || page >= pv.NB) return;
+    const int rows = min(kBlock, n - b * kBlock);
+    float x[kBlock];
+#pragma unroll
+    for (int r = 0; r < kBlock; ++r) { // all 16 loads in flight; rows past n re-read the last one
+        const int slot = b * kBlock + min(r, rows - 1);
+        x[r] = kv[(((size_t)which * n + slot) * pv.H + h) * kHeadDim + lane];
+    }
+    const size_t tile = tile_index(pv, layer, which, page, h);
+    if constexpr (CDT == DT_F32) {
+        float *pg = (float *)pv.pages + tile * (kBlock * kHeadDim);
+#pragma unroll
+        for (int r = 0; r < kBlock; ++r)
+            if (r < rows) pg[r * kHeadDim + lane] = x[r];
+    } else if constexpr (CDT == DT_BF16) {
+        uint16_t *pg = (uint16_t *)pv.pages + tile * (kBlock * kHeadDim);
+#pragma unroll
+        for (int r = 0; r < kBlock; ++r)
+            if (r < rows) pg[r * kHeadDim + lane] = (uint16_t)bf16_bits(x[r]);
+    } else {
+        float amax = 0.f;
+#pragma unroll
+        for (int r = 0; r < kBlock; ++r)
+            if (r < rows) amax = fmaxf(amax, fabsf(x[r]));
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+        const float sc = amax / 127.0f;
+        int8_t *pg = (int8_t *)pv.pages + tile * (kBlock * kHeadDim);
+#pragma unroll
+        for (int r = 0; r < kBlock; ++r)
+            if (r < rows) pg[r * kHeadDim + lane] = (int8_t)quant(x[r], sc);
+        if (lane == 0) pv.scales[tile] = sc;
+    }
+}
+
+hipError_t launch_load_kv(const PoolView &pv, int sid, int layer, const float *kv, int n, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    const dim3 grid((n + kBlock - 1) / kBlock, pv.H, 2);
+    switch (pv.cache_dt) {
+    case DT_F32: hipLaunchKernelGGL(k_load_kv<DT_F32>, grid, dim3(64), 0, stream, pv, sid, layer, kv, n); break;
+    case DT_BF16: hipLaunchKernelGGL(k_load_kv<DT_BF16>, grid, dim3(64), 0, stream, pv, sid, layer, kv, n); break;
+    case DT_I8: hipLaunchKernelGGL(k_load_kv<DT_I8>, grid, dim3(64), 0, stream, pv, sid, layer, kv, n); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------------------------
 // prompt prefill on MFMA (bf16 cache and activations), transformer.rs:231-248 batched, with the
 // append of the prompt's K/V rows (complete_kv, transformer.rs:84-91) fused in.

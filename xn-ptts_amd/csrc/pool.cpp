@@ -673,6 +673,25 @@ extern "C" xnp_status xnp_stream_advance(xnp_pool *pool, int32_t id, int32_t n) 
     return XNP_OK;
 }
 
+// Copy on write before rows [slot0, slot0 + n) of stream id are rewritten: a page shared with a
+// fork gets a copy of its own first.  Then the table patches reach the device.
+static xnp_status own_pages(xnp_pool *pool, int32_t id, int32_t slot0, int32_t n, hipStream_t hs) {
+    Stream &s = pool->streams[id];
+    const int32_t b0 = slot0 / kBlock, b1 = (slot0 + n - 1) / kBlock + 1;
+    int need = 0;
+    for (int32_t b = b0; b < b1; b++) need += pool->refcnt[s.blocks[b]] > 1;
+    if (need > (int)pool->free_pages.size())
+        return fail(XNP_E_OUT_OF_BLOCKS, "out of blocks: %d needed to copy shared pages", need);
+    for (int32_t b = b0; b < b1; b++) {
+        int32_t p = s.blocks[b];
+        if (pool->refcnt[p] <= 1) continue;
+        pool->refcnt[p]--;
+        int32_t q = pool->take_page(id, b);
+        HIP_TRY(launch_copy_page(pool->view(), p, q, hs), "page copy");
+    }
+    return pool->flush_patches(hs);
+}
+
 static xnp_status rows_check(const xnp_pool *pool, int32_t id, int32_t layer, int32_t kv, int32_t slot0,
                              int32_t n, const void *rows) {
     if (!pool || (!rows && n > 0)) return fail(XNP_E_INVALID, "null argument");
@@ -695,24 +714,27 @@ extern "C" xnp_status xnp_write_rows(xnp_pool *pool, int32_t id, int32_t layer, 
     if (n == 0) return XNP_OK;
     hipStream_t hs = (hipStream_t)hip_stream;
     HIP_TRY(hipSetDevice(pool->d.device), "hipSetDevice");
-    // Copy on write: a page shared with a fork gets a copy of its own first.
-    Stream &s = pool->streams[id];
-    const int32_t b0 = slot0 / kBlock, b1 = (slot0 + n - 1) / kBlock + 1;
-    int need = 0;
-    for (int32_t b = b0; b < b1; b++) need += pool->refcnt[s.blocks[b]] > 1;
-    if (need > (int)pool->free_pages.size())
-        return fail(XNP_E_OUT_OF_BLOCKS, "out of blocks: %d needed to copy shared pages", need);
-    for (int32_t b = b0; b < b1; b++) {
-        int32_t p = s.blocks[b];
-        if (pool->refcnt[p] <= 1) continue;
-        pool->refcnt[p]--;
-        int32_t q = pool->take_page(id, b);
-        HIP_TRY(launch_copy_page(pool->view(), p, q, hs), "page copy");
-    }
-    if (xnp_status st = pool->flush_patches(hs)) return st;
+    if (xnp_status st = own_pages(pool, id, slot0, n, hs)) return st;
     HIP_TRY(launch_rows_io(pool->view(), id, layer, kv, slot0, n, const_cast<void *>(rows),
                            const_cast<float *>(scales), true, hs),
             "row write");
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_stream_load_kv(xnp_pool *pool, int32_t id, int32_t layer, const float *kv, int32_t n,
+                                         void *hip_stream) {
+    if (xnp_status st = rows_check(pool, id, layer, 0, 0, n, kv)) return st;
+    if (xnp_status st = no_batch(pool)) return st;
+    const Stream &s = pool->streams[id];
+    if (s.ring != RING_NONE) return fail(XNP_E_RING, "a voice loads into a plain cache, not a ring");
+    if (n != s.current_end)
+        return fail(XNP_E_INVALID, "a %d-row voice loads into a stream holding exactly as many rows, not %d", n,
+                    s.current_end);
+    if (n == 0) return XNP_OK;
+    hipStream_t hs = (hipStream_t)hip_stream;
+    HIP_TRY(hipSetDevice(pool->d.device), "hipSetDevice");
+    if (xnp_status st = own_pages(pool, id, 0, n, hs)) return st;
+    HIP_TRY(launch_load_kv(pool->view(), id, layer, kv, n, hs), "voice load");
     return XNP_OK;
 }
 

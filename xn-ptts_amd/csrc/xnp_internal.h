@@ -155,6 +155,7 @@ struct LinNorm {
 hipError_t launch_linear_f32(const float *x, int ldx, int M, int K, const float *W, const float *b, int N, int epi,
                              const LinOut &lo, hipStream_t stream, const LinNorm *ln = nullptr);
 hipError_t launch_embed_f32(const float *table, const int32_t *ids, int rows, int dim, float *out, hipStream_t stream);
+hipError_t launch_load_kv(const PoolView &pv, int sid, int layer, const float *kv, int n, hipStream_t stream);
 hipError_t launch_rows_io(const PoolView &pv, int sid, int layer, int kv, int slot0, int n,
                           void *rows, float *scales, bool write, hipStream_t stream);
 

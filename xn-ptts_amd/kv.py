@@ -87,6 +87,7 @@ SIGNATURES = {
     "xnp_stream_blocks": (_i32, [_p, _i32, _i32p, _i32, _i32p]),
     "xnp_ring_valid": (_i32, [_p, _i32, _c.POINTER(_c.c_uint8), _i32]),
     "xnp_write_rows": (_i32, [_p, _i32, _i32, _i32, _i32, _i32, _p, _p, _p]),
+    "xnp_stream_load_kv": (_i32, [_p, _i32, _i32, _p, _i32, _p]),
     "xnp_read_rows": (_i32, [_p, _i32, _i32, _i32, _i32, _i32, _p, _p, _p]),
     "xnp_ring_start": (_i32, [_p, _i32, _i32, _i32, _p]),
     "xnp_ring_set_slot": (_i32, [_p, _i32, _i32]),
@@ -161,6 +162,43 @@ def frame_budget(num_tokens: int, frame_rate: float = 12.5) -> int:
 
 def seq_budget(num_tokens: int, frame_budget_: int) -> int:
     return load_library().xnp_seq_budget(num_tokens, frame_budget_)
+
+
+def voice_kv_name(layer: int) -> str:
+    """The tensor holding layer `layer` of a voice stored as the KV cache (ptts-wasm/src/lib.rs:394-396)."""
+    return f"transformer.layers.{layer}.self_attn/cache"
+
+
+def voice_layers(tensors, num_layers: int, num_heads: int, head_dim: int = 64):
+    """Check a KV-cache voice (voice_from_kv_cache, ptts-wasm/src/lib.rs:291-325) and return
+    (frames, [per layer: the f32 [2, frames, heads, head_dim] tensor]).  `tensors` maps names to
+    numpy arrays or torch tensors, as a safetensors file loads.  The errors are the reference's."""
+    layers, frames = [], None
+    for i in range(num_layers):
+        name = voice_kv_name(i)
+        t = tensors.get(name)
+        if t is None or str(t.dtype) not in ("float32", "torch.float32"):
+            raise ValueError(f"expected f32 tensor: {name}")
+        if len(t.shape) != 5:
+            raise ValueError(f"{name}: expected 5 dims [2, batch, seq, heads, head_dim], got {tuple(t.shape)}")
+        two, batch, seq, heads, hd = (int(d) for d in t.shape)
+        if two != 2:
+            raise ValueError(f"{name}: expected a first dim of size 2, got {two}")
+        if batch != 1:
+            raise ValueError(f"{name}: a stream holds one voice, got a batch of {batch}")
+        if heads != num_heads or hd != head_dim:
+            raise ValueError(f"{name}: {heads} heads of {hd}, the pool holds {num_heads} of {head_dim}")
+        if frames is not None and seq != frames:
+            raise ValueError(f"{name}: {seq} frames, layer 0 holds {frames}")
+        frames = seq
+        layers.append(t.reshape(2, seq, heads, hd))
+    return frames, layers
+
+
+def read_voice_file(path: str):
+    """The tensors of a safetensors voice file, as numpy arrays (read on the host)."""
+    from safetensors.numpy import load_file
+    return load_file(path)
 
 
 def _ptr(t) -> Optional[int]:
@@ -277,6 +315,32 @@ class KvPool:
         n = rows.shape[0] if rows is not None else 0
         _check(self._lib.xnp_write_rows(self._h, sid, layer, kv, slot0, n, _ptr(rows), _ptr(scales),
                                         _stream(stream)))
+
+    def load_kv(self, sid: int, layer: int, kv, stream=None):
+        """Rows [0, n) of one layer from a device f32 [2, n, H, D] tensor (xnp_stream_load_kv)."""
+        n = kv.shape[1]
+        _check(self._lib.xnp_stream_load_kv(self._h, sid, layer, _ptr(kv), n, _stream(stream)))
+
+    def load_voice(self, voice, capacity: Optional[int] = None, stream=None) -> int:
+        """A stream holding a voice stored as the KV cache (`embeddings_v2/` voices): a path to a
+        safetensors file, or its tensors by name.  The stream's capacity is the voice's length
+        unless given; give each generation its own budget with with_seq_budget, which shares
+        the voice's full pages instead of copying them (transformer.rs:350-392)."""
+        import torch
+        tensors = read_voice_file(voice) if isinstance(voice, (str, os.PathLike)) else voice
+        frames, layers = voice_layers(tensors, self.desc.num_layers, self.desc.num_heads, self.desc.head_dim)
+        sid = self.init_state(frames if capacity is None else capacity)
+        try:
+            self.advance(sid, frames)
+            dev = torch.device("cuda", self.desc.device)
+            staged = [torch.as_tensor(t).to(dev, torch.float32).contiguous() for t in layers]
+            for layer, t in enumerate(staged):
+                self.load_kv(sid, layer, t, stream)
+            torch.cuda.synchronize(dev)  # the staged copies are freed on return
+        except BaseException:
+            self.close(sid)
+            raise
+        return sid
 
     def read_rows(self, sid: int, layer: int, kv: int, slot0: int, rows, scales=None, stream=None):
         n = rows.shape[0]
