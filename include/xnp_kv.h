@@ -110,6 +110,7 @@ typedef struct xnp_stream_info {
     int32_t in_view;     /* valid ring slots */
     int32_t blocks;      /* pages the stream holds */
     int32_t shared;      /* of which shared with another stream */
+    int32_t window;      /* a window cache (xnp_window_open): its rows, else 0 */
 } xnp_stream_info;
 
 typedef struct xnp_pool_stats {
@@ -164,6 +165,16 @@ xnp_status xnp_read_rows(const xnp_pool *pool, int32_t id, int32_t layer, int32_
  * layer.  Forks of it (xnp_stream_fork, with_seq_budget) then share its full pages. */
 xnp_status xnp_stream_load_kv(xnp_pool *pool, int32_t id, int32_t layer, const float *kv, int32_t n,
                               void *hip_stream);
+
+/* ---- Mimi's window cache (transformer.rs:257-318,398-468) -------------------------------- */
+/* KvCache::new(context): a stream whose steps attend the last `window` positions, the causal
+ * window of Mimi's attention (delta < context, transformer.rs:764-781), keys rotated at their
+ * absolute position (KvCache::absolute_offset).  Its rows place themselves, row p in slot
+ * p % window over the row leaving the window, so no eviction call is needed.  A step takes t <= 4
+ * rows (Mimi's decoder takes 2 a frame): with t > 1 every stream of the batch must be a window
+ * cache, and xnp_attend, the only per-layer call such a batch takes, runs the rows in order.
+ * xnp_stream_fork clones a window as it is, every page copied (transformer.rs:348-354). */
+xnp_status xnp_window_open(xnp_pool *pool, int32_t window, int32_t *id);
 
 /* ---- ring (transformer.rs:842-929) ------------------------------------------------------ */
 /* start_ring: valid[s] = s < current_end; write = filled = current_end.  `prefix` is used by

@@ -616,6 +616,155 @@ int orc_load_kv(orc_stream *st, int layer, const float *kv, int n) {
 }
 
 /* ---------------------------------------------------------------------------------------- */
+/* Mimi's attention cache: KvCache (transformer.rs:257-318), MimiStreamingMultiheadAttention::  */
+/* forward (:428-468) and the window mask of StreamingTransformer::forward (:764-781)          */
+
+struct orc_window {
+    int L, H, D, context, rows_max, adt;
+    float theta;
+    float *k, *v; /* [L][context - 1 + rows_max][H][D]: the kept rows then this step's, in order */
+    int len;      /* KvCache::current_seq_len: rows kept between steps (at most context - 1) */
+    int offset;   /* KvCache::absolute_offset: rows appended so far */
+};
+
+orc_window *orc_window_open(int layers, int heads, int head_dim, int context, int rows_max, int act_dtype,
+                            float max_period) {
+    if (layers <= 0 || heads <= 0 || head_dim <= 0 || head_dim > 256 || (head_dim & 1) || context <= 0 ||
+        rows_max <= 0 || act_dtype < 0 || act_dtype > 1) {
+        fail("bad window shape");
+        return NULL;
+    }
+    orc_window *w = calloc(1, sizeof *w);
+    w->L = layers, w->H = heads, w->D = head_dim, w->context = context, w->rows_max = rows_max;
+    w->adt = act_dtype, w->theta = max_period;
+    const size_t n = (size_t)layers * (context - 1 + rows_max) * heads * head_dim;
+    w->k = calloc(n, sizeof(float));
+    w->v = calloc(n, sizeof(float));
+    return w;
+}
+
+void orc_window_close(orc_window *w) {
+    if (!w) return;
+    free(w->k);
+    free(w->v);
+    free(w);
+}
+
+int orc_window_len(const orc_window *w) { return w->len; }
+int orc_window_offset(const orc_window *w) { return w->offset; }
+
+static float *win_row(const orc_window *w, float *base, int layer, int r, int h) {
+    return base + (((size_t)layer * (w->context - 1 + w->rows_max) + r) * w->H + h) * w->D;
+}
+
+/* One layer of a step of t rows: append (KvCache::append, keys rotated at absolute_offset + i as
+ * RotaryEmbedding::new(head_dim, offset, t) gives them, stored in the activation dtype), then row
+ * i attends key j of the len + t rows when j <= len + i < j + context (:771-775; with t = 1 the
+ * reference passes no mask, and every row is inside the window).  Softmax in f32 in key order, as
+ * orc_attention; out64 (nullable) the f64 companion. */
+int orc_window_attend(orc_window *w, int layer, int t, const float *q, const float *k, const float *v, float scale,
+                      float *out, double *out64) {
+    if (layer < 0 || layer >= w->L) return fail("layer %d of %d", layer, w->L);
+    if (t <= 0 || t > w->rows_max) return fail("a step of %d rows, at most %d", t, w->rows_max);
+    const int H = w->H, D = w->D, n = w->len + t;
+    float cs[256], qr[256], x[256], kb[256];
+    float *sn = cs + D / 2;
+    float *sbuf = malloc(sizeof(float) * n);
+    double *dbuf = malloc(sizeof(double) * n);
+    for (int i = 0; i < t; i++) {
+        orc_rope_row(D, w->theta, (float)(w->offset + i), w->adt, cs, sn);
+        for (int h = 0; h < H; h++) {
+            memcpy(x, k + ((size_t)i * H + h) * D, D * 4);
+            orc_rotate(D, x, cs, sn, w->adt);
+            memcpy(win_row(w, w->k, layer, w->len + i, h), x, D * 4);
+            const float *vs = v + ((size_t)i * H + h) * D;
+            float *vd = win_row(w, w->v, layer, w->len + i, h);
+            for (int d = 0; d < D; d++) vd[d] = round_act(vs[d], w->adt);
+        }
+    }
+    for (int i = 0; i < t; i++) {
+        const int seq = w->len + i;
+        orc_rope_row(D, w->theta, (float)(w->offset + i), w->adt, cs, sn);
+        for (int h = 0; h < H; h++) {
+            memcpy(qr, q + ((size_t)i * H + h) * D, D * 4);
+            orc_rotate(D, qr, cs, sn, w->adt);
+            float m = -INFINITY;
+            double md = -INFINITY;
+            for (int j = 0; j < n; j++) {
+                if (!(j <= seq && seq < j + w->context)) {
+                    sbuf[j] = -INFINITY;
+                    dbuf[j] = -INFINITY;
+                    continue;
+                }
+                const float *kr = win_row(w, w->k, layer, j, h);
+                float sc = 0.0f;
+                double sd = 0.0;
+                for (int d = 0; d < D; d++) {
+                    sc = sc + qr[d] * kr[d];
+                    sd += (double)qr[d] * (double)kr[d];
+                }
+                sbuf[j] = sc * scale;
+                dbuf[j] = sd * (double)scale;
+                if (sbuf[j] > m) m = sbuf[j];
+                if (dbuf[j] > md) md = dbuf[j];
+            }
+            float l = 0.0f;
+            double ld = 0.0;
+            for (int j = 0; j < n; j++) {
+                sbuf[j] = sbuf[j] == -INFINITY ? 0.0f : expf(sbuf[j] - m);
+                dbuf[j] = dbuf[j] == -INFINITY ? 0.0 : exp(dbuf[j] - md);
+                l = l + sbuf[j];
+                ld += dbuf[j];
+            }
+            float o[256];
+            double od[256];
+            for (int d = 0; d < D; d++) o[d] = 0.0f, od[d] = 0.0;
+            for (int j = 0; j < n; j++) {
+                if (!(j <= seq && seq < j + w->context)) continue;
+                memcpy(kb, win_row(w, w->v, layer, j, h), D * 4);
+                for (int d = 0; d < D; d++) {
+                    o[d] = o[d] + sbuf[j] * kb[d];
+                    od[d] += dbuf[j] * (double)kb[d];
+                }
+            }
+            for (int d = 0; d < D; d++) {
+                out[((size_t)i * H + h) * D + d] = round_act(o[d] / l, w->adt);
+                if (out64) out64[((size_t)i * H + h) * D + d] = od[d] / ld;
+            }
+        }
+    }
+    free(sbuf);
+    free(dbuf);
+    return 0;
+}
+
+/* After every layer took the step: absolute_offset += t, then KvCache::trim (:300-316) keeps the
+ * last context - 1 rows. */
+int orc_window_commit(orc_window *w, int t) {
+    if (t <= 0 || t > w->rows_max) return fail("a step of %d rows, at most %d", t, w->rows_max);
+    w->offset += t;
+    const int n = w->len + t, keep = w->context - 1;
+    if (n <= keep) {
+        w->len = n;
+        return 0;
+    }
+    const int drop = n - keep;
+    for (int l = 0; l < w->L; l++) {
+        memmove(win_row(w, w->k, l, 0, 0), win_row(w, w->k, l, drop, 0), sizeof(float) * keep * w->H * w->D);
+        memmove(win_row(w, w->v, l, 0, 0), win_row(w, w->v, l, drop, 0), sizeof(float) * keep * w->H * w->D);
+    }
+    w->len = keep;
+    return 0;
+}
+
+/* The kept rows [len][H][D] of one layer, keys (kv 0) or values (1), oldest first. */
+int orc_window_rows(const orc_window *w, int layer, int kv, float *rows) {
+    if (layer < 0 || layer >= w->L || kv < 0 || kv > 1) return fail("bad layer or kv");
+    memcpy(rows, win_row(w, kv ? w->v : w->k, layer, 0, 0), sizeof(float) * w->len * w->H * w->D);
+    return 0;
+}
+
+/* ---------------------------------------------------------------------------------------- */
 /* the rest of the layer: transformer.rs:591-634                                            */
 
 void orc_layer_norm(const float *x, int rows, int dim, const float *w, const float *b, float eps,

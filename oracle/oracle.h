@@ -100,6 +100,21 @@ int orc_write_rows(orc_stream *st, int layer, int kv, int slot0, int n, const fl
  * and no ring.  int8: per (block, head) s = amax / 127 over the block's rows, q = rint(x / s). */
 int orc_load_kv(orc_stream *st, int layer, const float *kv, int n);
 
+/* --- Mimi's attention cache (transformer.rs:257-318, 428-468, 764-781) ------------------------ */
+/* KvCache with context `context`: between steps it keeps the last context - 1 rows; a step of t
+ * rows (at most rows_max) rotates them at absolute_offset + i and each attends the rows within
+ * `context` positions before it, itself included.  Values stored in the activation dtype. */
+typedef struct orc_window orc_window;
+orc_window *orc_window_open(int layers, int heads, int head_dim, int context, int rows_max, int act_dtype,
+                            float max_period);
+void orc_window_close(orc_window *w);
+int orc_window_attend(orc_window *w, int layer, int t, const float *q, const float *k, const float *v, float scale,
+                      float *out, double *out64);
+int orc_window_commit(orc_window *w, int t);
+int orc_window_len(const orc_window *w);
+int orc_window_offset(const orc_window *w);
+int orc_window_rows(const orc_window *w, int layer, int kv, float *rows);
+
 /* --- the rest of a flow-LM transformer layer (transformer.rs:591-634) ------------------------ */
 /* LayerNorm over the last dimension, as norm1/norm2 (transformer.rs:547-548, eps 1e-5): per row,
  * mean and biased variance in f32 (ascending sums), then (x - mean) * (1 / sqrt(var + eps)) * w + b,

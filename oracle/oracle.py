@@ -58,6 +58,14 @@ def lib():
             "orc_write_rows": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                               ctypes.c_int, _fp, _i8p, _fp]),
             "orc_load_kv": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _fp, ctypes.c_int]),
+            "orc_window_open": (ctypes.c_void_p, [ctypes.c_int] * 6 + [ctypes.c_float]),
+            "orc_window_close": (None, [ctypes.c_void_p]),
+            "orc_window_attend": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, _fp, _fp, _fp,
+                                                 ctypes.c_float, _fp, _dp]),
+            "orc_window_commit": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+            "orc_window_len": (ctypes.c_int, [ctypes.c_void_p]),
+            "orc_window_offset": (ctypes.c_int, [ctypes.c_void_p]),
+            "orc_window_rows": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, _fp]),
             "orc_batch_attend": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int, ctypes.c_int,
                                                 _fp, _fp, _fp, ctypes.c_float, _fp]),
             "orc_batch_commit": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int]),
@@ -232,6 +240,51 @@ class Stream:
         assert kv.ndim == 4 and kv.shape[0] == 2, kv.shape
         a, ap = _f32(kv)
         _ok(lib().orc_load_kv(self.h, layer, ap, kv.shape[1]))
+
+
+class Window:
+    """Mimi's KvCache over all layers (transformer.rs:257-318): the last context - 1 rows kept
+    between steps, a step of t rows attending the causal window of `context` positions."""
+
+    def __init__(self, layers, heads, head_dim, context, rows_max=4, act="f32", max_period=10000.0):
+        self.L, self.H, self.D, self.context = layers, heads, head_dim, context
+        self.h = lib().orc_window_open(layers, heads, head_dim, context, rows_max, DT[act], max_period)
+        if not self.h:
+            raise OracleError(lib().orc_last_error().decode())
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().orc_window_close(self.h)
+            self.h = None
+
+    @property
+    def len(self):
+        return lib().orc_window_len(self.h)
+
+    @property
+    def offset(self):
+        return lib().orc_window_offset(self.h)
+
+    def attend(self, layer, q, k, v, scale=0.125):
+        """q, k, v [t][H][D]; returns (out, out64)."""
+        q, qp = _f32(q)
+        k, kp = _f32(k)
+        v, vp = _f32(v)
+        t = q.shape[0]
+        out = np.zeros((t, self.H, self.D), np.float32)
+        out64 = np.zeros((t, self.H, self.D), np.float64)
+        _ok(lib().orc_window_attend(self.h, layer, t, qp, kp, vp, scale, out.ctypes.data_as(_fp),
+                                    out64.ctypes.data_as(_dp)))
+        return out, out64
+
+    def commit(self, t):
+        _ok(lib().orc_window_commit(self.h, t))
+
+    def rows(self, layer, kv):
+        """The kept rows [len][H][D], oldest first (keys rotated)."""
+        out = np.zeros((max(self.len, 1), self.H, self.D), np.float32)
+        _ok(lib().orc_window_rows(self.h, layer, kv, out.ctypes.data_as(_fp)))
+        return out[:self.len]
 
 
 def batch_attend(streams, layer, q, k, v, scale=0.125):

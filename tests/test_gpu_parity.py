@@ -231,6 +231,149 @@ def test_empty_batch_is_a_no_op():
     assert p.pool.current_end(p.ids[0]) == 0
 
 
+# ---- Mimi's window cache (transformer.rs:257-318, 428-468, 764-781) ------------------------------
+def _window_batch(pool, ids, orcs, t, L, H, act, cache, rng, twins=()):
+    """One step of t rows on `ids`, every layer checked against the oracle caches `orcs` (None:
+    not checked).  twins: (i, j) pairs whose stream j gets stream i's inputs and must answer alike."""
+    n = len(ids)
+    pool.begin(ids, t=t)
+    for layer in range(L):
+        q, k, v = (rng.standard_normal((n, t, H, 64)).astype(np.float32) for _ in range(3))
+        if act == "bf16":
+            q, k, v = bf16_round(q), bf16_round(k), bf16_round(v)
+        for i, j in twins:
+            q[j], k[j], v[j] = q[i], k[i], v[i]
+        out = torch.empty((n, t, H, 64), dtype=TORCH_DT[act], device=DEV)
+        pool.attend(layer, dev(q, act), dev(k, act), dev(v, act), out, 0.125)
+        torch.cuda.synchronize()
+        got = host(out)
+        for j, o in enumerate(orcs):
+            if o is not None:
+                want, _ = o.attend(layer, q[j], k[j], v[j])
+                assert rel_err(got[j], want) <= TOL[cache], (layer, j, t)
+        for i, j in twins:
+            assert np.array_equal(got[i], got[j]), (layer, i, j)
+    pool.end()
+    for o in orcs:
+        if o is not None:
+            o.commit(t)
+
+
+def _assert_window_rows(pool, sid, win, window, L, H, cache):
+    # the oracle keeps positions [offset - len, offset); the pool holds position p in slot p % window
+    filled = min(win.offset, window)
+    for layer in range(L):
+        for kv in (0, 1):
+            rows = torch.empty((filled, H, 64), dtype=CACHE_TORCH[cache], device=DEV)
+            pool.read_rows(sid, layer, kv, 0, rows)
+            torch.cuda.synchronize()
+            g = rows.float().cpu().numpy()
+            want = win.rows(layer, kv)
+            for i, p in enumerate(range(win.offset - win.len, win.offset)):
+                assert np.array_equal(g[p % window].view(np.uint32), want[i].view(np.uint32)), (layer, kv, p)
+
+
+@pytest.mark.parametrize("cache,act", [("bf16", "bf16"), ("f32", "f32")])
+def test_window_caches_match_mimis_kv_cache(cache, act):
+    # Three windows (KvCache::new(24), (24), (40)) and a plain stream in the same batches for 60
+    # single rows; then 15 steps of two rows (Mimi's decoder: two 25 Hz rows per 80 ms frame) on the
+    # windows and a clone of the first (with_seq_budget clones a window as it is), fed its inputs.
+    L, H = 2, 8
+    pool = xnp.KvPool(num_layers=L, num_heads=H, num_blocks=64, max_streams=8, max_blocks_per_stream=8,
+                      cache_dtype=cache, act_dtype=act, max_pos=4096, page_seed=3)
+    contexts = [24, 24, 40]
+    ids = [pool.init_window(c) for c in contexts]
+    orcs = [oracle.Window(L, H, 64, c, act=act) for c in contexts]
+    ids.append(pool.init_state(128))
+    orcs.append(oracle.Stream(L, H, 64, 128, cache=cache, act=act))
+    assert pool.info(ids[0])["window"] == 24 and pool.info(ids[3])["window"] == 0
+    rng = np.random.default_rng(50)
+    for s_ in range(60):
+        _window_batch(pool, ids, orcs, 1, L, H, act, cache, rng)
+        if s_ in (10, 23, 24, 59):
+            for i in range(3):
+                _assert_window_rows(pool, ids[i], orcs[i], contexts[i], L, H, cache)
+    clone = pool.with_seq_budget(ids[0], 999)
+    assert pool.info(clone)["window"] == 24
+    wids = ids[:3] + [clone]
+    for _ in range(15):
+        _window_batch(pool, wids, orcs[:3] + [None], 2, L, H, act, cache, rng, twins=[(0, 3)])
+    for i in range(3):
+        _assert_window_rows(pool, wids[i], orcs[i], contexts[i], L, H, cache)
+        assert pool.current_end(wids[i]) == contexts[i]  # rows held: the window, full
+
+
+def test_int8_window_cache_matches_the_ring_it_stands_for():
+    # An int8 window has no counterpart in the reference; it is an absolute ring of `context`
+    # slots whose every row evicts the oldest, so the oracle's ring driven that way is its bar:
+    # bit-exact codes and scales, outputs within 2e-2.  Single rows, then rows in pairs.
+    L, H, context = 2, 8, 24
+    pool = xnp.KvPool(num_layers=L, num_heads=H, num_blocks=16, max_streams=2, max_blocks_per_stream=2,
+                      cache_dtype="i8", act_dtype="bf16", max_pos=4096, page_seed=4)
+    wid = pool.init_window(context)
+    st = oracle.Stream(L, H, 64, context, cache="i8", act="bf16")
+    st.start_ring("absolute", prefix=0)
+    rng = np.random.default_rng(51)
+    p = 0
+    for t in [1] * 50 + [2] * 12:
+        q, k, v = (bf16_round(rng.standard_normal((L, 1, t, H, 64)).astype(np.float32) * 2) for _ in range(3))
+        pool.begin([wid], t=t)
+        got = []
+        for layer in range(L):
+            out = torch.empty((1, t, H, 64), dtype=torch.bfloat16, device=DEV)
+            pool.attend(layer, dev(q[layer], "bf16"), dev(k[layer], "bf16"), dev(v[layer], "bf16"), out, 0.125)
+            torch.cuda.synchronize()
+            got.append(host(out))
+        pool.end()
+        for i in range(t):  # the oracle's ring, one row at a time over every layer
+            if st.ring_info()["filled"] == context:
+                st.evict(0, [p % context])
+            st.set_ring_slot(p % context)
+            for layer in range(L):
+                want, _ = st.attend(layer, q[layer][0, i:i + 1], k[layer][0, i:i + 1], v[layer][0, i:i + 1])
+                assert rel_err(got[layer][0, i:i + 1], want) <= TOL["i8"], (p, layer)
+            st.commit(1)
+            p += 1
+        if p % 7 == 0 or t == 2:
+            n = min(p, context)
+            for layer in range(L):
+                for kv in (0, 1):
+                    rows = torch.empty((n, H, 64), dtype=torch.int8, device=DEV)
+                    nb = (n - 1) // 16 + 1
+                    sc = torch.zeros((nb, H), dtype=torch.float32, device=DEV)
+                    pool.read_rows(wid, layer, kv, 0, rows, sc)
+                    torch.cuda.synchronize()
+                    _, q8, osc = st.read_rows(layer, kv, 0, n)
+                    assert np.array_equal(rows.cpu().numpy(), q8), (p, layer, kv)
+                    assert np.array_equal(sc.cpu().numpy().view(np.uint32), osc.view(np.uint32)), (p, layer, kv)
+
+
+def test_window_misuse_is_refused():
+    pool = xnp.KvPool(num_layers=1, num_heads=8, num_blocks=16, max_streams=4, max_blocks_per_stream=4,
+                      cache_dtype="bf16", act_dtype="bf16", max_pos=1024)
+    wid, pid = pool.init_window(16), pool.init_state(64)
+    with pytest.raises(xnp.XnpError, match="window of 0"):
+        pool.init_window(0)
+    with pytest.raises(xnp.XnpError, match="at most 4 rows"):
+        pool.begin([wid], t=5)
+    with pytest.raises(xnp.XnpError, match="window caches only"):
+        pool.begin([wid, pid], t=2)
+    with pytest.raises(xnp.XnpError, match="places its rows itself"):
+        pool.set_ring_slot(wid, 3)
+    with pytest.raises(xnp.XnpError, match="places its rows itself"):
+        pool.evict(wid, 0, [0])
+    with pytest.raises(xnp.XnpError, match="not a ring"):
+        pool.load_kv(wid, 0, torch.zeros((2, 0, 8, 64), dtype=torch.float32, device=DEV))
+    pool.begin([wid], t=2)
+    x = torch.zeros((1, 2, 8, 64), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(xnp.XnpError, match="through xnp_attend alone"):
+        pool.decode(0, x, x, 0.125)
+    with pytest.raises(xnp.XnpError, match="through xnp_attend alone"):
+        pool.append(0, x, x)
+    pool.abort()
+    assert pool.current_end(wid) == 0
+
+
 # ---- voices stored as the KV cache (ptts-wasm/src/lib.rs:291-325) -------------------------------
 @pytest.mark.parametrize("cache,act", [("f32", "f32"), ("bf16", "bf16"), ("i8", "bf16")])
 def test_a_voice_file_loads_into_pages_and_its_forks_share_them(cache, act, tmp_path):

@@ -421,6 +421,96 @@ def test_a_voice_loads_only_into_a_plain_stream_of_its_length():
         st.load_kv(0, kv)
 
 
+# ---- Mimi's window cache (transformer.rs:257-318, 428-468, 764-781) ----------------------------
+def _window_run(win, steps, rng, H, act):
+    """Feed `steps` (rows per step) of seeded q, k, v through an oracle window; the outputs."""
+    outs = []
+    for t in steps:
+        q, k, v = (rng.standard_normal((t, H, 64)).astype(np.float32) for _ in range(3))
+        if act == "bf16":
+            q, k, v = bf16_round(q), bf16_round(k), bf16_round(v)
+        outs.append(win.attend(0, q, k, v))
+        win.commit(t)
+    return outs
+
+
+@pytest.mark.parametrize("act", ["f32", "bf16"])
+def test_a_window_wider_than_the_stream_is_plain_causal_attention(act):
+    # With context above every position the mask is the causal one: the flow LM's linear cache
+    # (pinned against textbook attention above) gives the same outputs bit for bit.
+    steps = [3, 1, 1, 2, 1, 4] + [1] * 10
+    win = oracle.Window(1, 2, 64, 200, act=act)
+    st = oracle.Stream(1, 2, 64, 64, cache=act, act=act)
+    got = _window_run(win, steps, np.random.default_rng(40), 2, act)
+    rng = np.random.default_rng(40)
+    for t, (o, _) in zip(steps, got):
+        q, k, v = (rng.standard_normal((t, 2, 64)).astype(np.float32) for _ in range(3))
+        if act == "bf16":
+            q, k, v = bf16_round(q), bf16_round(k), bf16_round(v)
+        want, _ = st.attend(0, q, k, v)
+        st.commit(t)
+        assert np.array_equal(o.view(np.uint32), want.view(np.uint32))
+    n = sum(steps)
+    assert win.len == n and win.offset == n
+    np.testing.assert_array_equal(win.rows(0, 0), st.read_rows(0, 0, 0, n)[0])
+
+
+def test_a_window_matches_textbook_windowed_attention():
+    # f64 RoPE from math.cos/sin at absolute positions, then softmax over keys p - context < j <= p
+    context, H = 5, 2
+    steps = [1, 2, 1, 3, 1, 1, 2, 1, 1, 1, 3]
+    win = oracle.Window(1, H, 64, context, act="f32")
+    rng = np.random.default_rng(41)
+    inv = np.array([THETA ** (-i / 32) for i in range(32)])
+
+    def rot(x, pos):
+        a = pos * inv
+        c, s_ = np.cos(a), np.sin(a)
+        x0, x1 = x[..., 0::2].astype(np.float64), x[..., 1::2].astype(np.float64)
+        y = np.empty(x.shape, np.float64)
+        y[..., 0::2], y[..., 1::2] = x0 * c - x1 * s_, x0 * s_ + x1 * c
+        return y
+
+    keys, vals, p = [], [], 0
+    for t in steps:
+        q, k, v = (rng.standard_normal((t, H, 64)).astype(np.float32) for _ in range(3))
+        _, out64 = win.attend(0, q, k, v, scale=0.125)
+        win.commit(t)
+        for i in range(t):
+            keys.append(rot(k[i], p + i))
+            vals.append(v[i].astype(np.float64))
+        for i in range(t):
+            pos = p + i
+            lo = max(0, pos - context + 1)
+            K, V = np.stack(keys[lo:pos + 1]), np.stack(vals[lo:pos + 1])  # [n][H][D]
+            sc = np.einsum("hd,nhd->hn", rot(q[i], pos), K) * 0.125
+            w = np.exp(sc - sc.max(axis=1, keepdims=True))
+            w /= w.sum(axis=1, keepdims=True)
+            want = np.einsum("hn,nhd->hd", w, V)
+            assert rel_err(out64[i], want) <= 1e-5, (p, i)
+        p += t
+    assert win.len == context - 1 and win.offset == p
+
+
+def test_a_chunk_attends_as_its_rows_one_at_a_time():
+    # Row i of a chunk sees what it would see as a step of its own, so a chunk of 3 equals three
+    # single rows, bit for bit, and leaves the same kept rows.
+    a = oracle.Window(1, 2, 64, 6, act="bf16")
+    b = oracle.Window(1, 2, 64, 6, act="bf16")
+    ra, rb = np.random.default_rng(42), np.random.default_rng(42)
+    for _ in range(7):
+        qa, ka, va = (bf16_round(ra.standard_normal((3, 2, 64)).astype(np.float32)) for _ in range(3))
+        qb, kb, vb = (bf16_round(rb.standard_normal((3, 2, 64)).astype(np.float32)) for _ in range(3))
+        oa, _ = a.attend(0, qa, ka, va)
+        a.commit(3)
+        for i in range(3):
+            ob, _ = b.attend(0, qb[i:i + 1], kb[i:i + 1], vb[i:i + 1])
+            b.commit(1)
+            assert np.array_equal(oa[i].view(np.uint32), ob[0].view(np.uint32))
+    assert a.len == b.len == 5
+    np.testing.assert_array_equal(a.rows(0, 1), b.rows(0, 1))
+
+
 # ---- the rest of the layer (transformer.rs:591-634) -------------------------------------------
 def test_layer_norm_matches_torch():
     # torch.nn.functional.layer_norm in f64 is the textbook definition (biased variance, eps inside

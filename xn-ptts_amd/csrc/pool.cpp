@@ -84,7 +84,13 @@ struct Stream {
     int32_t ring = RING_NONE, write = 0, filled = 0, prefix = 0, shift = 0;
     std::vector<uint8_t> valid;
     int32_t nvalid = 0; // valid slots of the ring
+    // Mimi's KvCache (transformer.rs:257-318): an absolute ring of `window` slots that places its
+    // rows itself, row p in slot p % window, each overwriting the row that just left the window
+    int32_t window = 0;
 };
+
+// rows a window stream takes in one step (Mimi's decoder: 2 per frame)
+constexpr int32_t kMaxWindowRows = 4;
 
 // A pinned host buffer an upload is composed in; reused once its copy has completed.
 struct Staging {
@@ -139,6 +145,7 @@ struct xnp_pool {
         std::vector<int32_t> ids;
         std::vector<std::pair<int32_t, int32_t>> taken; // (stream, block) pages taken by begin
         BatchView bv{};
+        bool wsteps = false; // a step of several rows on window caches: one decode per row
     } batch;
 
     PoolView view() const {
@@ -383,7 +390,8 @@ extern "C" xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out)
 
     // plan upload layout: plans, work items, masks (each 256-byte aligned)
     p->rec_stride = (int)align_up(sizeof(StreamRec) + sizeof(int32_t) * d.max_blocks_per_stream, 64);
-    p->batch_bytes = align_up(sizeof(StreamPlan) * d.max_streams, 256) + align_up((size_t)p->rec_stride * d.max_streams, 256) +
+    p->batch_bytes = align_up(sizeof(StreamPlan) * d.max_streams, 256) +
+                     align_up((size_t)p->rec_stride * d.max_streams * kMaxWindowRows, 256) +
                      align_up(sizeof(uint32_t) * (size_t)p->mask_words * d.max_streams, 256);
     p->aux_bytes = std::max<size_t>(sizeof(TablePatch) * 65536,
                                     align_up(sizeof(EvictRow) * d.max_blocks_per_stream * kBlock, 256) + 4096);
@@ -560,6 +568,29 @@ extern "C" xnp_status xnp_stream_fork(xnp_pool *pool, int32_t src, int32_t capac
     if (xnp_status st = no_batch(pool)) return st;
     Stream *s = pool->get(src);
     if (!s) return fail(XNP_E_STREAM, "no open stream %d", src);
+    if (s->window) {
+        // with_seq_budget clones a Mimi cache as it is (transformer.rs:348-354): a window rewrites
+        // its pages in place, so every page is copied, and the budget does not apply
+        int held = 0;
+        for (int32_t p : s->blocks) held += p >= 0;
+        if (held > (int)pool->free_pages.size())
+            return fail(XNP_E_OUT_OF_BLOCKS, "out of blocks: %d needed, %d free", held, (int)pool->free_pages.size());
+        int32_t dst;
+        if (xnp_status st = xnp_stream_open(pool, s->capacity, &dst)) return st;
+        s = pool->get(src);
+        Stream &t = pool->streams[dst];
+        t = *s;
+        t.blocks.assign(s->blocks.size(), -1);
+        if (!pool->host_only) HIP_TRY(hipSetDevice(pool->d.device), "hipSetDevice");
+        for (size_t b = 0; b < s->blocks.size(); b++) {
+            if (s->blocks[b] < 0) continue;
+            const int32_t q = pool->take_page(dst, (int32_t)b);
+            if (!pool->host_only)
+                HIP_TRY(launch_copy_page(pool->view(), s->blocks[b], q, (hipStream_t)hip_stream), "page copy");
+        }
+        *id = dst;
+        return XNP_OK;
+    }
     if (s->ring != RING_NONE) return fail(XNP_E_BUDGET, "a ring cache cannot be resized");
     const int32_t used = s->current_end;
     if (used > capacity)
@@ -605,6 +636,7 @@ extern "C" xnp_status xnp_stream_info_get(const xnp_pool *pool, int32_t id, xnp_
     out->ring_write = s->write;
     out->ring_filled = s->filled;
     out->ring_prefix = s->prefix;
+    out->window = s->window;
     out->ring_shift = s->shift;
     int32_t in_view = 0, blocks = 0, shared = 0;
     for (uint8_t v : s->valid) in_view += v;
@@ -782,6 +814,7 @@ extern "C" xnp_status xnp_ring_set_slot(xnp_pool *pool, int32_t id, int32_t slot
     Stream *s = pool->get(id);
     if (!s) return fail(XNP_E_STREAM, "no open stream %d", id);
     if (s->ring == RING_NONE) return fail(XNP_E_RING, "not a ring cache, see start_ring");
+    if (s->window) return fail(XNP_E_RING, "a window cache places its rows itself");
     if (slot < 0 || slot >= s->capacity) return fail(XNP_E_RING, "slot %d of a %d-slot ring", slot, s->capacity);
     s->write = slot;
     return XNP_OK;
@@ -794,6 +827,7 @@ extern "C" xnp_status xnp_ring_evict(xnp_pool *pool, int32_t id, int32_t prefix,
     Stream *s = pool->get(id);
     if (!s) return fail(XNP_E_STREAM, "no open stream %d", id);
     if (s->ring == RING_NONE) return fail(XNP_E_RING, "not a ring cache, see start_ring");
+    if (s->window) return fail(XNP_E_RING, "a window cache places its rows itself");
     if (count < 0 || count > s->current_end)
         return fail(XNP_E_EVICT, "cannot evict %d of %d positions", count, s->current_end);
     if (s->ring == RING_ABSOLUTE && prefix != s->prefix)
@@ -885,6 +919,24 @@ extern "C" xnp_status xnp_ring_slide_batch(xnp_pool *pool, const int32_t *ids, i
     return XNP_OK;
 }
 
+// KvCache::new(context) (transformer.rs:264-267) for Mimi's attention: an absolute ring of
+// `window` slots whose rows the batch calls place themselves (row p in slot p % window), so that
+// each step attends the last `window` positions, as KvCache::trim and the window mask of
+// transformer.rs:300-316,764-781 keep them.
+extern "C" xnp_status xnp_window_open(xnp_pool *pool, int32_t window, int32_t *id) {
+    if (!pool || !id) return fail(XNP_E_INVALID, "null argument");
+    if (window <= 0) return fail(XNP_E_INVALID, "a window of %d rows", window);
+    int32_t sid;
+    if (xnp_status st = xnp_stream_open(pool, window, &sid)) return st;
+    if (xnp_status st = xnp_ring_start(pool, sid, XNP_RING_ABSOLUTE, 0, nullptr)) {
+        (void)xnp_stream_close(pool, sid);
+        return st;
+    }
+    pool->streams[sid].window = window;
+    *id = sid;
+    return XNP_OK;
+}
+
 // ---------------------------------------------------------------------------------------------
 // batches
 
@@ -895,15 +947,30 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
     if (t <= 0) return fail(XNP_E_INVALID, "a step appends at least one row, not %d", t);
     // check everything first
     std::vector<uint8_t> seen(pool->streams.size(), 0);
-    int need = 0;
+    int need = 0, windows = 0;
     for (int32_t i = 0; i < n; i++) {
         const int32_t id = ids[i];
         const Stream *s = pool->get(id);
         if (!s) return fail(XNP_E_STREAM, "no open stream %d", id);
         if (seen[id]) return fail(XNP_E_INVALID, "stream %d appears twice in the batch", id);
         seen[id] = 1;
-        int32_t last_pos;
-        if (s->ring != RING_NONE) {
+        int64_t last_pos;
+        if (s->window) {
+            // row i of the step goes to slot (p + i) % window, over the row leaving the window
+            if (t > kMaxWindowRows)
+                return fail(XNP_E_RING, "a window cache takes at most %d rows a step, not %d", kMaxWindowRows, t);
+            const int64_t p = (int64_t)s->current_end + s->shift;
+            int32_t counted[kMaxWindowRows];
+            for (int32_t r = 0; r < t; r++) {
+                const int32_t b = (int32_t)((p + r) % s->window) / kBlock;
+                counted[r] = b;
+                bool dup = false;
+                for (int32_t q = 0; q < r; q++) dup |= counted[q] == b;
+                need += !dup && s->blocks[b] < 0;
+            }
+            last_pos = p + t - 1;
+            windows++;
+        } else if (s->ring != RING_NONE) {
             if (t != 1) return fail(XNP_E_RING, "a ring cache takes one row at a time, not %d", t);
             if (s->valid[s->write]) return fail(XNP_E_RING, "ring slot %d still holds a row, evict it first", s->write);
             need += s->blocks[s->write / kBlock] < 0;
@@ -915,8 +982,12 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
             last_pos = s->current_end + t - 1;
         }
         if (last_pos >= pool->d.max_pos)
-            return fail(XNP_E_INVALID, "position %d is beyond the RoPE table (%d rows)", last_pos, pool->d.max_pos);
+            return fail(XNP_E_INVALID, "position %lld is beyond the RoPE table (%d rows)", (long long)last_pos,
+                        pool->d.max_pos);
     }
+    if (t > 1 && windows && windows != n)
+        return fail(XNP_E_INVALID, "a step of %d rows holds window caches only, or none", t);
+    const bool wsteps = t > 1 && windows; // one decode per row, each over its own records
     if (need > (int)pool->free_pages.size())
         return fail(XNP_E_OUT_OF_BLOCKS, "out of blocks: %d needed, %d free", need, (int)pool->free_pages.size());
 
@@ -928,7 +999,13 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
     B.stream = (hipStream_t)hip_stream;
     for (int32_t i = 0; i < n; i++) {
         Stream &s = pool->streams[ids[i]];
-        if (s.ring != RING_NONE)
+        if (s.window) {
+            const int64_t p = (int64_t)s.current_end + s.shift;
+            for (int32_t r = 0; r < t; r++) {
+                const int32_t b = (int32_t)((p + r) % s.window) / kBlock;
+                take_range(pool, ids[i], b, b + 1, &B.taken);
+            }
+        } else if (s.ring != RING_NONE)
             take_range(pool, ids[i], s.write / kBlock, s.write / kBlock + 1, &B.taken);
         else
             take_range(pool, ids[i], s.current_end / kBlock, (s.current_end + t - 1) / kBlock + 1, &B.taken);
@@ -991,7 +1068,8 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
     if (xnp_status st = pool->stage_acquire(&sg)) return undo(st);
     const size_t o_plans = 0;
     const size_t o_recs = align_up(sizeof(StreamPlan) * n, 256);
-    const size_t o_masks = o_recs + align_up(t == 1 ? (size_t)pool->rec_stride * n : 0, 256);
+    const int32_t sets = t == 1 ? 1 : wsteps ? t : 0; // record sets: one per decode launch
+    const size_t o_masks = o_recs + align_up((size_t)pool->rec_stride * n * sets, 256);
     const size_t total = o_masks + sizeof(uint32_t) * masks.size();
     std::memcpy(sg->host + o_plans, plans.data(), sizeof(StreamPlan) * n);
     if (t == 1)
@@ -1013,6 +1091,32 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
             std::memcpy(dst, &R, sizeof R);
             std::memcpy(dst + sizeof R, pool->streams[P.sid].blocks.data(), sizeof(int32_t) * R.nblk);
         }
+    if (wsteps)
+        // Mimi's chunk (transformer.rs:764-781): row i attends positions (p + i - window, p + i], the
+        // causal window.  Per layer the rows run in order, each a decode of one row per stream: row
+        // i's key takes the slot of position p + i - window, which no later row sees, and every
+        // filled slot holds a position inside row i's window.  So row i sees slots [0, span).
+        for (int32_t r = 0; r < t; r++)
+            for (int32_t j = 0; j < n; j++) {
+                const Stream &st = pool->streams[plans[order[j]].sid];
+                const int64_t p = (int64_t)st.current_end + st.shift + r;
+                StreamRec R;
+                std::memset(&R, 0, sizeof R);
+                R.b = plans[order[j]].out_row * t + r;
+                R.write_slot = (int32_t)(p % st.window);
+                R.span = (int32_t)std::min<int64_t>(p + 1, st.window);
+                R.nblk = (R.span + kBlock - 1) / kBlock;
+                R.pos = R.pos_pre = R.key_pos = (int32_t)p;
+                R.mask_off = -1;
+                // int8: the write page starts afresh when no other slot of it holds a row yet
+                const int32_t b0 = R.write_slot / kBlock * kBlock, filled = (int32_t)std::min<int64_t>(p, st.window);
+                bool other = false;
+                for (int32_t sl = b0; sl < std::min(b0 + kBlock, filled); sl++) other |= sl != R.write_slot;
+                R.flags = 1 | (other ? 0 : 2);
+                char *dst = sg->host + o_recs + ((size_t)r * n + j) * pool->rec_stride;
+                std::memcpy(dst, &R, sizeof R);
+                std::memcpy(dst + sizeof R, st.blocks.data(), sizeof(int32_t) * R.nblk);
+            }
     std::memcpy(sg->host + o_masks, masks.data(), sizeof(uint32_t) * masks.size());
     if (xnp_status st = pool->upload(sg, pool->dbatch, total, hs)) return undo(st);
     B.bv.plans = (const StreamPlan *)(pool->dbatch + o_plans);
@@ -1029,19 +1133,26 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
     B.bv.masks = (const uint32_t *)(pool->dbatch + o_masks);
     B.bv.n = n;
     B.bv.t = t;
+    B.wsteps = wsteps;
     B.open = true;
     return XNP_OK;
 }
 
-static xnp_status batch_call(xnp_pool *pool, int32_t layer, void *hip_stream, bool decode) {
+// The checks of a per-layer call: `decode` for one row per stream, else several; `window_rows` for
+// the row-by-row attention of a window step of several rows, the only call such a batch takes.
+static xnp_status batch_call(xnp_pool *pool, int32_t layer, void *hip_stream, bool decode, bool window_rows = false) {
     if (!pool) return fail(XNP_E_INVALID, "null argument");
     if (!pool->batch.open) return fail(XNP_E_STATE, "no batch is open");
     if (pool->host_only) return fail(XNP_E_STATE, "a host-only pool runs no kernels");
     if (layer < 0 || layer >= pool->d.num_layers) return fail(XNP_E_INVALID, "layer %d of %d", layer, pool->d.num_layers);
     if ((hipStream_t)hip_stream != pool->batch.stream)
         return fail(XNP_E_INVALID, "a batch's calls go to the stream it began on");
-    if (decode && pool->batch.t != 1) return fail(XNP_E_INVALID, "decode takes one row per stream, not %d", pool->batch.t);
-    if (!decode && pool->batch.t == 1) return fail(XNP_E_INVALID, "prefill takes more than one row per stream");
+    if (pool->batch.wsteps != window_rows)
+        return fail(XNP_E_INVALID, "a window step of several rows runs through xnp_attend alone");
+    if (!window_rows && decode && pool->batch.t != 1)
+        return fail(XNP_E_INVALID, "decode takes one row per stream, not %d", pool->batch.t);
+    if (!window_rows && !decode && pool->batch.t == 1)
+        return fail(XNP_E_INVALID, "prefill takes more than one row per stream");
     HIP_TRY(hipSetDevice(pool->d.device), "hipSetDevice");
     return XNP_OK;
 }
@@ -1081,6 +1192,22 @@ extern "C" xnp_status xnp_prefill(xnp_pool *pool, int32_t layer, const void *q, 
 extern "C" xnp_status xnp_attend(xnp_pool *pool, int32_t layer, const void *q, const void *k, const void *v,
                                  void *out, float scale, void *hip_stream) {
     if (!pool) return fail(XNP_E_INVALID, "null argument");
+    if (pool->batch.open && pool->batch.wsteps) {
+        // window caches, several rows: row by row, each a fused append + decode over its records
+        auto &B = pool->batch;
+        if (xnp_status st = batch_call(pool, layer, hip_stream, false, true)) return st;
+        if (B.n > 0 && (!q || !k || !v || !out)) return fail(XNP_E_INVALID, "null q, k, v or out");
+        const LaunchTiming tm = pool->timing;
+        pool->timing = LaunchTiming();
+        BatchView bv = B.bv;
+        for (int32_t r = 0; r < B.t; r++) {
+            bv.recs = B.bv.recs + (size_t)r * B.n * B.bv.rec_stride;
+            HIP_TRY(launch_decode(pool->view(), bv, layer, q, k, v, out, scale, true, B.stream,
+                                  r == 0 ? tm : LaunchTiming()),
+                    "attend");
+        }
+        return XNP_OK;
+    }
     if (pool->batch.open && pool->batch.t > 1) {
         if (!prefill_fuses_append(pool->view())) {
             if (xnp_status st = xnp_append(pool, layer, k, v, hip_stream)) return st;
@@ -1110,7 +1237,16 @@ extern "C" xnp_status xnp_batch_end(xnp_pool *pool) {
     if (!B.open) return fail(XNP_E_STATE, "no batch is open");
     for (int32_t id : B.ids) {
         Stream &s = pool->streams[id];
-        if (s.ring != RING_NONE) {
+        if (s.window) {
+            // KvCache::append then trim (transformer.rs:280-316): the last `window` rows stay, the
+            // newest in slot p % window
+            const int64_t p = (int64_t)s.current_end + s.shift + B.t;
+            const int32_t held = (int32_t)std::min<int64_t>(p, s.window);
+            for (int32_t sl = s.filled; sl < held; sl++) s.valid[sl] = 1;
+            s.nvalid = s.filled = s.current_end = held;
+            s.shift = (int32_t)(p - held);
+            s.write = (int32_t)(p % s.window);
+        } else if (s.ring != RING_NONE) {
             // complete_kv's ring branch, transformer.rs:74-79 (begin refused a valid write slot)
             s.valid[s.write] = 1;
             s.nvalid++;

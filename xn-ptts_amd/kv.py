@@ -64,7 +64,7 @@ class LayerWeightsC(_c.Structure):
 class StreamInfo(_c.Structure):
     _fields_ = [(n, _i32) for n in (
         "current_end", "capacity", "ring_mode", "ring_write", "ring_filled", "ring_prefix",
-        "ring_shift", "in_view", "blocks", "shared")]
+        "ring_shift", "in_view", "blocks", "shared", "window")]
 
 
 class PoolStats(_c.Structure):
@@ -88,6 +88,7 @@ SIGNATURES = {
     "xnp_ring_valid": (_i32, [_p, _i32, _c.POINTER(_c.c_uint8), _i32]),
     "xnp_write_rows": (_i32, [_p, _i32, _i32, _i32, _i32, _i32, _p, _p, _p]),
     "xnp_stream_load_kv": (_i32, [_p, _i32, _i32, _p, _i32, _p]),
+    "xnp_window_open": (_i32, [_p, _i32, _i32p]),
     "xnp_read_rows": (_i32, [_p, _i32, _i32, _i32, _i32, _i32, _p, _p, _p]),
     "xnp_ring_start": (_i32, [_p, _i32, _i32, _i32, _p]),
     "xnp_ring_set_slot": (_i32, [_p, _i32, _i32]),
@@ -281,6 +282,13 @@ class KvPool:
 
     def close(self, sid: int):
         _check(self._lib.xnp_stream_close(self._h, sid))
+
+    def init_window(self, context: int) -> int:
+        """MimiStreamingMultiheadAttention::init_state (transformer.rs:416-418): a stream whose
+        steps attend the last `context` positions (KvCache::new(context)), rows placing themselves."""
+        sid = _i32()
+        _check(self._lib.xnp_window_open(self._h, context, ctypes.byref(sid)))
+        return sid.value
 
     def with_seq_budget(self, sid: int, budget: int, stream=None) -> int:
         out = _i32()
