@@ -278,10 +278,29 @@ xnp_status xnp_layer_norm(const void *x, int32_t rows, int32_t dim, const float 
  * y [rows][n], XNP_EPI_GELU_ERF / _TANH write gelu of it, XNP_EPI_RESIDUAL adds it (times ls[j],
  * rounded, when ls is not NULL) into y and rounds. */
 typedef enum xnp_epilogue {
-    XNP_EPI_STORE = 0, XNP_EPI_GELU_ERF = 1, XNP_EPI_GELU_TANH = 2, XNP_EPI_RESIDUAL = 3
+    XNP_EPI_STORE = 0, XNP_EPI_GELU_ERF = 1, XNP_EPI_GELU_TANH = 2, XNP_EPI_RESIDUAL = 3,
+    /* the flow net's (xnp_flow_linear_q8 only) */
+    XNP_EPI_SILU = 4, XNP_EPI_SILU_ADD = 5, XNP_EPI_GATED = 6, XNP_EPI_AXPY_F32 = 7, XNP_EPI_STORE_F32 = 8
 } xnp_epilogue;
 xnp_status xnp_linear_q8(const void *x, int32_t rows, int32_t k, const int8_t *w, const float *s,
                          int32_t n, int32_t epilogue, void *y, const float *ls, void *hip_stream);
+/* The flow net's pieces (SimpleMLPAdaLN, mlp.rs:4-11,113-163), as the q8 flow LM runs them:
+ * y = bf16(s[j] * sum_k x[m][k] w[j][k] (+ bias[j])) for x [rows][k] bf16 (x_f32: f32, rounded to
+ * bf16 as it is read; XNP_EPI_STORE only), w [n][k] int8, any n, k a multiple of 16, then
+ * XNP_EPI_STORE y; _GELU_* gelu(y); _RESIDUAL y += y; _SILU silu(y); _SILU_ADD silu(bf16(y +
+ * aux[j])) (aux f32 [n], the time embedding); _GATED y[m][j] = bf16(y[m][j] + bf16(aux[m][j] *
+ * y)) (aux bf16, the AdaLN gate); _AXPY_F32 y[m][j] = bf16(bf16(aux[m][j]) + bf16(y * alpha)) (aux
+ * and y f32: the solver step); _STORE_F32 y (f32).  Every result rounded to bf16 once; y rows of
+ * stride ldy, aux rows of stride ld_aux. */
+xnp_status xnp_flow_linear_q8(const void *x, int32_t x_f32, int32_t rows, int32_t k, const int8_t *w,
+                              const float *s, const float *bias, int32_t n, int32_t epilogue, void *y,
+                              int32_t ldy, const void *aux, int32_t ld_aux, float alpha, void *hip_stream);
+/* LayerNorm of bf16 rows (dim a multiple of 512; w, b both NULL for no affine) rounded to bf16,
+ * then when shift is given the AdaLN modulation in bf16 steps, bf16(bf16(y * bf16(scale + 1)) +
+ * shift), shift and scale bf16 rows of stride ld_mod (a multiple of 8). */
+xnp_status xnp_layer_norm_mod(const void *x, int32_t rows, int32_t dim, const float *w, const float *b,
+                              float eps, const void *shift, const void *scale, int32_t ld_mod, void *out,
+                              void *hip_stream);
 /* Per-row int8 weights on the host: s[r] = max |w[r][.]| / 127, q = rint(w / s) clamped to
  * +-127 (an all-zero row gets s = 0, q = 0). */
 xnp_status xnp_quantize_rows(const float *w, int32_t rows, int32_t cols, int8_t *q, float *scales);
@@ -294,6 +313,14 @@ xnp_status xnp_quantize_rows(const float *w, int32_t rows, int32_t cols, int8_t 
  * subset: no z_proj, no attn_dim override, no grouped heads, no layer scale, no conditions or
  * sinks. */
 typedef enum xnp_time_norm { XNP_TIME_RMS = 0, XNP_TIME_RMS_VAR = 1 } xnp_time_norm; /* mlp.rs:17-28 */
+/* FlowType (flow_lm.rs:372-381): the LSD solver over lsd_steps, or one flow-net call without time
+ * conditions (Drifting: the latent is its output; Pointwise: noise plus it). */
+typedef enum xnp_flow_type { XNP_FLOW_LSD = 0, XNP_FLOW_DRIFTING = 1, XNP_FLOW_POINTWISE = 2 } xnp_flow_type;
+/* XNP_FLOW_F32: f32 weights and activations on an f32 pool (one stream a frame, the reference's
+ * case).  XNP_FLOW_Q8: every linear's weights quantized at create as xnp_quantize_rows does
+ * (biases, norms f32), bf16 activations on a bf16 pool, the projections on MFMA (many streams a
+ * frame); each operation rounds its bf16 output once, as a bf16 tensor op does. */
+typedef enum xnp_flow_precision { XNP_FLOW_F32 = 0, XNP_FLOW_Q8 = 1 } xnp_flow_precision;
 
 typedef struct xnp_flow_lm_desc {
     int32_t d_model, num_heads, num_layers, ff; /* the transformer; the pool must match it */
@@ -302,24 +329,31 @@ typedef struct xnp_flow_lm_desc {
     int32_t gelu;                               /* xnp_gelu */
     int32_t time_norm;                          /* xnp_time_norm */
     int32_t max_rows;                           /* rows one call may hold: streams x prompt tokens */
+    int32_t z_dim;                              /* 0: no z_proj; else its width (flow_lm.rs:239-240) */
+    int32_t flow_type;                          /* xnp_flow_type */
+    int32_t precision;                          /* xnp_flow_precision */
 } xnp_flow_lm_desc;
 
 typedef struct xnp_flow_lm xnp_flow_lm;
 
-/* Floats of the weight blob: every tensor f32, row-major [out][in] for linears, in this order --
+/* Floats of the weight blob: every tensor f32, row-major [out][in] for linears, in this order (zd:
+ * z_dim when set, else d) --
  * conditioner.embed [n_bins+1][d]; input_linear [d][ldim]; bos_emb [ldim];
  * per layer: norm1 w, b [d]; in_proj [3d][d]; out_proj [d][d]; norm2 w, b [d]; linear1 [ff][d];
  *   linear2 [d][ff];
- * out_norm w, b [d]; out_eos w [1][d], b [1];
- * per time embedder (2): freqs [128]; mlp.0 w [F][256], b [F]; mlp.2 w [F][F], b [F]; alpha [F];
- * cond_embed w [F][d], b [F]; input_proj w [F][ldim], b [F];
+ * out_norm w, b [d]; z_proj [z][d] when z_dim; out_eos w [1][zd], b [1];
+ * per time embedder (2, XNP_FLOW_LSD only): freqs [128]; mlp.0 w [F][256], b [F]; mlp.2 w [F][F],
+ *   b [F]; alpha [F];
+ * cond_embed w [F][zd], b [F]; input_proj w [F][ldim], b [F];
  * per res block: in_ln w, b [F]; mlp.0 w [F][F], b [F]; mlp.2 w [F][F], b [F];
  *   adaLN_modulation.1 w [3F][F], b [3F];
  * final_layer: adaLN_modulation.1 w [2F][F], b [2F]; linear w [ldim][F], b [ldim]. */
 xnp_status xnp_flow_lm_weights_size(const xnp_flow_lm_desc *desc, int64_t *nfloats);
-/* Upload the weights (host memory) for a pool with f32 cache and activations whose layers and
- * heads match; the time embeddings of the solver steps are computed once here, as
- * lsd_time_embeddings does at load (flow_lm.rs:82-95). */
+/* Upload the weights (host memory; quantized here for XNP_FLOW_Q8) for a pool whose layers and
+ * heads match, with f32 cache and activations (XNP_FLOW_F32) or bf16 ones (XNP_FLOW_Q8: d_model
+ * and flow_dim multiples of 512, every linear's input width a multiple of 16); the time embeddings
+ * of the solver steps are computed once here, as lsd_time_embeddings does at load
+ * (flow_lm.rs:82-95). */
 xnp_status xnp_flow_lm_create(xnp_pool *pool, const xnp_flow_lm_desc *desc, const float *weights,
                               int64_t nfloats, xnp_flow_lm **out);
 xnp_status xnp_flow_lm_destroy(xnp_flow_lm *lm);

@@ -879,21 +879,25 @@ typedef struct {
     size_t embed, in_lin, bos;
     size_t ln1_w[ORC_MAXL], ln1_b[ORC_MAXL], wqkv[ORC_MAXL], wout[ORC_MAXL];
     size_t ln2_w[ORC_MAXL], ln2_b[ORC_MAXL], w1[ORC_MAXL], w2[ORC_MAXL];
-    size_t on_w, on_b, eos_w, eos_b;
+    size_t on_w, on_b, z_proj, eos_w, eos_b;
     size_t te_freqs[2], te_w1[2], te_b1[2], te_w2[2], te_b2[2], te_alpha[2];
     size_t cond_w, cond_b, inp_w, inp_b;
     size_t rb_lnw[ORC_MAXL], rb_lnb[ORC_MAXL], rb_w1[ORC_MAXL], rb_b1[ORC_MAXL];
     size_t rb_w2[ORC_MAXL], rb_b2[ORC_MAXL], rb_aw[ORC_MAXL], rb_ab[ORC_MAXL];
     size_t fin_aw, fin_ab, fin_w, fin_b;
     size_t total;
+    int zd; /* the width out_eos and cond_embed read: z_dim, else d_model */
 } flow_layout;
 
 static int flow_layout_of(const orc_flow_lm_desc *d, flow_layout *L) {
     if (d->num_layers <= 0 || d->num_layers > ORC_MAXL || d->flow_depth < 0 || d->flow_depth > ORC_MAXL ||
         d->d_model <= 0 || d->num_heads <= 0 || d->d_model % d->num_heads || d->ldim <= 0 || d->flow_dim <= 0 ||
-        d->ff <= 0 || d->n_bins <= 0 || d->lsd_steps <= 0)
+        d->ff <= 0 || d->n_bins <= 0 || d->z_dim < 0 || d->flow_type < 0 || d->flow_type > 2 ||
+        (d->flow_type == 0 && d->lsd_steps <= 0) || d->precision < 0 || d->precision > 1)
         return fail("bad flow LM shape");
     const size_t dm = d->d_model, F = d->flow_dim, ld = d->ldim, ff = d->ff, fq = ORC_FREQ_DIM;
+    const size_t zd = d->z_dim ? (size_t)d->z_dim : dm;
+    L->zd = (int)zd;
     size_t o = 0;
 #define TAKE(field, n) (L->field = o, o += (size_t)(n))
     TAKE(embed, (d->n_bins + 1) * dm);
@@ -906,12 +910,13 @@ static int flow_layout_of(const orc_flow_lm_desc *d, flow_layout *L) {
         TAKE(w1[l], ff * dm); TAKE(w2[l], dm * ff);
     }
     TAKE(on_w, dm); TAKE(on_b, dm);
-    TAKE(eos_w, dm); TAKE(eos_b, 1);
-    for (int i = 0; i < 2; i++) {
+    TAKE(z_proj, d->z_dim ? zd * dm : 0);
+    TAKE(eos_w, zd); TAKE(eos_b, 1);
+    for (int i = 0; i < (d->flow_type == 0 ? 2 : 0); i++) { /* num_time_conds: 2 for Lsd, else 0 */
         TAKE(te_freqs[i], fq / 2); TAKE(te_w1[i], F * fq); TAKE(te_b1[i], F);
         TAKE(te_w2[i], F * F); TAKE(te_b2[i], F); TAKE(te_alpha[i], F);
     }
-    TAKE(cond_w, F * dm); TAKE(cond_b, F);
+    TAKE(cond_w, F * zd); TAKE(cond_b, F);
     TAKE(inp_w, F * ld); TAKE(inp_b, F);
     for (int j = 0; j < d->flow_depth; j++) {
         TAKE(rb_lnw[j], F); TAKE(rb_lnb[j], F);
@@ -988,6 +993,7 @@ static void time_embed_one(const orc_flow_lm_desc *d, const float *blob, const f
 int orc_flow_time_embedding(const orc_flow_lm_desc *d, const float *blob, float s, float t, float *out) {
     flow_layout L;
     if (flow_layout_of(d, &L)) return -1;
+    if (d->flow_type != 0) return fail("a head without time conditions has no time embedding");
     const int F = d->flow_dim;
     float *b = malloc(sizeof(float) * F);
     time_embed_one(d, blob, &L, 0, s, out);
@@ -1022,12 +1028,12 @@ int orc_flow_net(const orc_flow_lm_desc *d, const float *blob, const float *c, c
                  const float *x0, float *out) {
     flow_layout L;
     if (flow_layout_of(d, &L)) return -1;
-    const int F = d->flow_dim, dm = d->d_model, ld = d->ldim;
+    const int F = d->flow_dim, ld = d->ldim;
     float *x = malloc(sizeof(float) * F), *y = malloc(sizeof(float) * F), *ya = malloc(sizeof(float) * F);
     float *ada = malloc(sizeof(float) * 3 * F), *h = malloc(sizeof(float) * F), *h2 = malloc(sizeof(float) * F);
     orc_linear_f32(x0, 1, ld, blob + L.inp_w, blob + L.inp_b, F, x);     /* input_proj */
-    orc_linear_f32(c, 1, dm, blob + L.cond_w, blob + L.cond_b, F, y);   /* cond_embed */
-    for (int j = 0; j < F; j++) ya[j] = silu(t_emb[j] + y[j]);           /* y = t + c; silu */
+    orc_linear_f32(c, 1, L.zd, blob + L.cond_w, blob + L.cond_b, F, y); /* cond_embed */
+    for (int j = 0; j < F; j++) ya[j] = silu(t_emb ? t_emb[j] + y[j] : y[j]); /* y = t + c (or c); silu */
     for (int r = 0; r < d->flow_depth; r++) {                            /* ResBlock (mlp.rs:113-131) */
         orc_linear_f32(ya, 1, F, blob + L.rb_aw[r], blob + L.rb_ab[r], 3 * F, ada);
         ln_mod(x, F, blob + L.rb_lnw[r], blob + L.rb_lnb[r], 1e-6f, ada, ada + F, h);
@@ -1093,25 +1099,261 @@ int orc_flow_lm_step(const orc_flow_lm_desc *d, const float *blob, orc_stream *s
                      const float *noise, float *latent_out, float *eos_logit) {
     flow_layout L;
     if (flow_layout_of(d, &L)) return -1;
+    if (d->precision != 0) return fail("a q8 flow LM steps through orc_flow_q8_step");
     const int dm = d->d_model, F = d->flow_dim, ld = d->ldim;
     float *x = malloc(sizeof(float) * dm), *t_out = malloc(sizeof(float) * dm), *temb = malloc(sizeof(float) * F);
     float *cur = malloc(sizeof(float) * ld), *dir = malloc(sizeof(float) * ld);
+    float *z = malloc(sizeof(float) * L.zd);
     /* input_linear of the previous latent, or of bos_emb on the first step (flow_lm.rs:314-324) */
     orc_linear_f32(latent_in ? latent_in : blob + L.bos, 1, ld, blob + L.in_lin, NULL, dm, x);
     int rc = flow_transformer(d, blob, &L, st, 1, x);
     if (rc == 0) {
         ln_mod(x, dm, blob + L.on_w, blob + L.on_b, 1e-5f, NULL, NULL, t_out); /* out_norm (flow_lm.rs:315) */
-        orc_linear_f32(t_out, 1, dm, blob + L.eos_w, blob + L.eos_b, 1, eos_logit);
+        if (d->z_dim) orc_linear_f32(t_out, 1, dm, blob + L.z_proj, NULL, d->z_dim, z); /* :320-323 */
+        else memcpy(z, t_out, sizeof(float) * dm);
+        orc_linear_f32(z, 1, L.zd, blob + L.eos_w, blob + L.eos_b, 1, eos_logit);
         memcpy(cur, noise, sizeof(float) * ld);
-        const float step_scale = 1.0f / (float)d->lsd_steps;
-        for (int i = 0; i < d->lsd_steps; i++) { /* lsd_decode (flow_lm.rs:97-110) */
-            orc_flow_time_embedding(d, blob, (float)i / (float)d->lsd_steps, (float)(i + 1) / (float)d->lsd_steps, temb);
-            orc_flow_net(d, blob, t_out, temb, cur, dir);
-            for (int j = 0; j < ld; j++) cur[j] = cur[j] + dir[j] * step_scale;
+        if (d->flow_type == 0) {
+            const float step_scale = 1.0f / (float)d->lsd_steps;
+            for (int i = 0; i < d->lsd_steps; i++) { /* lsd_decode (flow_lm.rs:97-110) */
+                orc_flow_time_embedding(d, blob, (float)i / (float)d->lsd_steps, (float)(i + 1) / (float)d->lsd_steps,
+                                        temb);
+                orc_flow_net(d, blob, z, temb, cur, dir);
+                for (int j = 0; j < ld; j++) cur[j] = cur[j] + dir[j] * step_scale;
+            }
+        } else { /* Drifting: flow_net(c, None, noise); Pointwise: noise + the same (:380-381) */
+            orc_flow_net(d, blob, z, NULL, noise, dir);
+            for (int j = 0; j < ld; j++) cur[j] = d->flow_type == 2 ? noise[j] + dir[j] : dir[j];
         }
         memcpy(latent_out, cur, sizeof(float) * ld);
     }
-    free(x); free(t_out); free(temb); free(cur); free(dir);
+    free(x); free(t_out); free(temb); free(cur); free(dir); free(z);
+    return rc;
+}
+
+/* ---------------------------------------------------------------------------------------- */
+/* the flow LM in q8 precision: int8 per-channel weights, bf16 activations                   */
+
+/* The flow net's q8 linear (the batched frame's GEMM and its epilogues): y = bf16(s[j] * sum_k
+ * bf16(x[m][k]) q[j][k] (+ b[j])), then epi 0 store; 4 silu; 5 silu(bf16(y + aux[j])); 6
+ * out = bf16(out + bf16(aux[m][j] * y)); 7 out = bf16(bf16(aux[m][j]) + bf16(y * alpha)); 8 store (the
+ * f32 output is the bf16 value).  out [rows][ldo] (read by 6), aux rows of stride ld_aux. */
+void orc_flow_linear_q8(const float *x, int rows, int k, const int8_t *q, const float *s, const float *b, int n,
+                        int epi, float *out, int ldo, const float *aux, int ld_aux, float alpha) {
+    for (int m = 0; m < rows; m++)
+        for (int j = 0; j < n; j++) {
+            const float *xr = x + (size_t)m * k;
+            const int8_t *qr = q + (size_t)j * k;
+            float acc = 0.f;
+            for (int i = 0; i < k; i++) acc += orc_bf16_round(xr[i]) * (float)qr[i];
+            const float y = orc_bf16_round(b ? s[j] * acc + b[j] : s[j] * acc);
+            float *o = out + (size_t)m * ldo + j;
+            switch (epi) {
+            case 4: *o = orc_bf16_round(silu(y)); break;
+            case 5: *o = orc_bf16_round(silu(orc_bf16_round(y + aux[j]))); break;
+            case 6: *o = orc_bf16_round(*o + orc_bf16_round(aux[(size_t)m * ld_aux + j] * y)); break;
+            case 7:
+                *o = orc_bf16_round(orc_bf16_round(aux[(size_t)m * ld_aux + j]) + orc_bf16_round(y * alpha));
+                break;
+            default: *o = y;
+            }
+        }
+}
+
+/* LayerNorm of bf16 rows (w, b: the affine, or NULL) rounded once, then, when shift is given, the
+ * AdaLN modulation in bf16 steps: bf16(bf16(y * bf16(scale + 1)) + shift) (shift and scale rows of
+ * stride ld_mod). */
+void orc_layer_norm_mod(const float *x, int rows, int dim, const float *w, const float *b, float eps,
+                        const float *shift, const float *scale, int ld_mod, float *out) {
+    for (int r = 0; r < rows; r++) {
+        const float *xr = x + (size_t)r * dim;
+        float sum = 0.f;
+        for (int i = 0; i < dim; i++) sum += xr[i];
+        const float mean = sum / (float)dim;
+        float q = 0.f;
+        for (int i = 0; i < dim; i++) {
+            float e = xr[i] - mean;
+            q += e * e;
+        }
+        const float rstd = 1.0f / sqrtf(q / (float)dim + eps);
+        for (int i = 0; i < dim; i++) {
+            float y = (xr[i] - mean) * rstd;
+            if (w) y = y * w[i] + b[i];
+            y = orc_bf16_round(y);
+            if (shift) {
+                const float sc1 = orc_bf16_round(scale[(size_t)r * ld_mod + i] + 1.0f);
+                y = orc_bf16_round(orc_bf16_round(y * sc1) + shift[(size_t)r * ld_mod + i]);
+            }
+            out[(size_t)r * dim + i] = y;
+        }
+    }
+}
+
+typedef struct {
+    int8_t *q;
+    float *s;
+    int n, k;
+} qlin;
+
+struct orc_flow_q8 {
+    orc_flow_lm_desc d;
+    flow_layout L;
+    const float *blob; /* the caller's: biases, norms, the LUT */
+    qlin in_lin, wqkv[ORC_MAXL], wout[ORC_MAXL], w1[ORC_MAXL], w2[ORC_MAXL], z, eos, cond, inp;
+    qlin rb1[ORC_MAXL], rb2[ORC_MAXL], rba[ORC_MAXL], fina, finw;
+    orc_layer_weights lw[ORC_MAXL];
+    float *temb; /* [steps][F], rounded to bf16 */
+};
+
+static void qlin_make(qlin *w, const float *src, int n, int k) {
+    w->n = n, w->k = k;
+    w->q = malloc((size_t)n * k);
+    w->s = malloc(sizeof(float) * n);
+    orc_quantize_rows(src, n, k, w->q, w->s);
+}
+
+static void qlin_free(qlin *w) {
+    free(w->q);
+    free(w->s);
+}
+
+/* the flow net's q8 linear on one prepared weight */
+static void q8lin_epi(const float *x, int rows, const qlin *w, const float *b, int epi, float *out, const float *aux,
+                      int ld_aux, float alpha) {
+    orc_flow_linear_q8(x, rows, w->k, w->q, w->s, b, w->n, epi, out, w->n, aux, ld_aux, alpha);
+}
+
+static void q8lin(const float *x, int rows, const qlin *w, const float *b, float *y) {
+    q8lin_epi(x, rows, w, b, 0, y, NULL, 0, 1.f);
+}
+
+orc_flow_q8 *orc_flow_q8_prepare(const orc_flow_lm_desc *d, const float *blob) {
+    flow_layout L;
+    if (flow_layout_of(d, &L)) return NULL;
+    if (d->precision != 1) {
+        fail("orc_flow_q8_prepare takes a q8 desc");
+        return NULL;
+    }
+    orc_flow_q8 *m = calloc(1, sizeof *m);
+    m->d = *d, m->L = L, m->blob = blob;
+    const int dm = d->d_model, F = d->flow_dim, ld = d->ldim, ff = d->ff, zd = L.zd;
+    qlin_make(&m->in_lin, blob + L.in_lin, dm, ld);
+    for (int l = 0; l < d->num_layers; l++) {
+        qlin_make(&m->wqkv[l], blob + L.wqkv[l], 3 * dm, dm);
+        qlin_make(&m->wout[l], blob + L.wout[l], dm, dm);
+        qlin_make(&m->w1[l], blob + L.w1[l], ff, dm);
+        qlin_make(&m->w2[l], blob + L.w2[l], dm, ff);
+        orc_layer_weights *w = &m->lw[l];
+        w->d_model = dm, w->ff = ff, w->gelu = d->gelu;
+        w->wqkv = m->wqkv[l].q, w->sqkv = m->wqkv[l].s, w->wout = m->wout[l].q, w->sout = m->wout[l].s;
+        w->w1 = m->w1[l].q, w->s1 = m->w1[l].s, w->w2 = m->w2[l].q, w->s2 = m->w2[l].s;
+        w->ln1_w = blob + L.ln1_w[l], w->ln1_b = blob + L.ln1_b[l];
+        w->ln2_w = blob + L.ln2_w[l], w->ln2_b = blob + L.ln2_b[l];
+    }
+    if (d->z_dim) qlin_make(&m->z, blob + L.z_proj, d->z_dim, dm);
+    qlin_make(&m->eos, blob + L.eos_w, 1, zd);
+    qlin_make(&m->cond, blob + L.cond_w, F, zd);
+    qlin_make(&m->inp, blob + L.inp_w, F, ld);
+    for (int r = 0; r < d->flow_depth; r++) {
+        qlin_make(&m->rb1[r], blob + L.rb_w1[r], F, F);
+        qlin_make(&m->rb2[r], blob + L.rb_w2[r], F, F);
+        qlin_make(&m->rba[r], blob + L.rb_aw[r], 3 * F, F);
+    }
+    qlin_make(&m->fina, blob + L.fin_aw, 2 * F, F);
+    qlin_make(&m->finw, blob + L.fin_w, ld, F);
+    const int steps = d->flow_type == 0 ? d->lsd_steps : 0;
+    m->temb = calloc((size_t)(steps ? steps : 1) * F, sizeof(float));
+    for (int i = 0; i < steps; i++) {
+        float *t = m->temb + (size_t)i * F;
+        orc_flow_time_embedding(d, blob, (float)i / (float)steps, (float)(i + 1) / (float)steps, t);
+        for (int j = 0; j < F; j++) t[j] = orc_bf16_round(t[j]);
+    }
+    return m;
+}
+
+void orc_flow_q8_free(orc_flow_q8 *m) {
+    if (!m) return;
+    qlin_free(&m->in_lin);
+    for (int l = 0; l < m->d.num_layers; l++) {
+        qlin_free(&m->wqkv[l]);
+        qlin_free(&m->wout[l]);
+        qlin_free(&m->w1[l]);
+        qlin_free(&m->w2[l]);
+    }
+    if (m->d.z_dim) qlin_free(&m->z);
+    qlin_free(&m->eos);
+    qlin_free(&m->cond);
+    qlin_free(&m->inp);
+    for (int r = 0; r < m->d.flow_depth; r++) {
+        qlin_free(&m->rb1[r]);
+        qlin_free(&m->rb2[r]);
+        qlin_free(&m->rba[r]);
+    }
+    qlin_free(&m->fina);
+    qlin_free(&m->finw);
+    free(m->temb);
+    free(m);
+}
+
+static int q8_transformer(orc_flow_q8 *m, orc_stream *st, int t, float *x) {
+    const float scale = 1.0f / sqrtf((float)(m->d.d_model / m->d.num_heads));
+    for (int l = 0; l < m->d.num_layers; l++)
+        if (layer_step_one(st, t, l, &m->lw[l], scale, x)) return -1;
+    return orc_commit(st, t);
+}
+
+int orc_flow_q8_prompt_text(orc_flow_q8 *m, orc_stream *st, const int *ids, int n) {
+    if (n <= 0) return 0;
+    const int dm = m->d.d_model;
+    for (int i = 0; i < n; i++)
+        if (ids[i] < 0 || ids[i] > m->d.n_bins)
+            return fail("token id %d is past the %d-entry embedding table", ids[i], m->d.n_bins + 1);
+    float *x = malloc(sizeof(float) * (size_t)n * dm);
+    for (int i = 0; i < n; i++)
+        for (int j = 0; j < dm; j++)
+            x[(size_t)i * dm + j] = orc_bf16_round(m->blob[m->L.embed + (size_t)ids[i] * dm + j]);
+    int rc = q8_transformer(m, st, n, x);
+    free(x);
+    return rc;
+}
+
+int orc_flow_q8_step(orc_flow_q8 *m, orc_stream *st, const float *latent_in, const float *noise,
+                     float *latent_out, float *eos_logit) {
+    const orc_flow_lm_desc *d = &m->d;
+    const flow_layout *L = &m->L;
+    const float *blob = m->blob;
+    const int dm = d->d_model, F = d->flow_dim, ld = d->ldim, zd = L->zd;
+    float *x = malloc(sizeof(float) * dm), *t_out = malloc(sizeof(float) * dm), *z = malloc(sizeof(float) * zd);
+    float *ya = malloc(sizeof(float) * F), *xf = malloc(sizeof(float) * F), *ada = malloc(sizeof(float) * 3 * F);
+    float *h = malloc(sizeof(float) * F), *h2 = malloc(sizeof(float) * F), *cur = malloc(sizeof(float) * ld);
+    q8lin(latent_in ? latent_in : blob + L->bos, 1, &m->in_lin, NULL, x); /* input_linear (flow_lm.rs:314-324) */
+    int rc = q8_transformer(m, st, 1, x);
+    if (rc == 0) {
+        orc_layer_norm_mod(x, 1, dm, blob + L->on_w, blob + L->on_b, 1e-5f, NULL, NULL, 0, t_out); /* out_norm */
+        if (d->z_dim) q8lin(t_out, 1, &m->z, NULL, z);
+        else memcpy(z, t_out, sizeof(float) * dm);
+        q8lin(z, 1, &m->eos, blob + L->eos_b, eos_logit);
+        memcpy(cur, noise, sizeof(float) * ld);
+        const int steps = d->flow_type == 0 ? d->lsd_steps : 1;
+        const float alpha = d->flow_type == 0 ? 1.0f / (float)steps : 1.0f;
+        for (int i = 0; i < steps; i++) {
+            /* cond_embed, then y = t + c (or c), silu (mlp.rs:214-238) */
+            q8lin_epi(z, 1, &m->cond, blob + L->cond_b, d->flow_type == 0 ? 5 : 4, ya, m->temb + (size_t)i * F, 0, 1.f);
+            q8lin(cur, 1, &m->inp, blob + L->inp_b, xf); /* input_proj (x rounded to bf16 as it is read) */
+            for (int r = 0; r < d->flow_depth; r++) {  /* ResBlock (mlp.rs:113-131) */
+                q8lin(ya, 1, &m->rba[r], blob + L->rb_ab[r], ada);
+                orc_layer_norm_mod(xf, 1, F, blob + L->rb_lnw[r], blob + L->rb_lnb[r], 1e-6f, ada, ada + F, 3 * F, h);
+                q8lin_epi(h, 1, &m->rb1[r], blob + L->rb_b1[r], 4, h2, NULL, 0, 1.f);
+                q8lin_epi(h2, 1, &m->rb2[r], blob + L->rb_b2[r], 6, xf, ada + 2 * F, 3 * F, 1.f);
+            }
+            q8lin(ya, 1, &m->fina, blob + L->fin_ab, ada); /* FinalLayer (mlp.rs:155-163) */
+            orc_layer_norm_mod(xf, 1, F, NULL, NULL, 1e-6f, ada, ada + F, 2 * F, h);
+            /* Lsd: x + v / steps; Pointwise: noise + v; Drifting: v */
+            q8lin_epi(h, 1, &m->finw, blob + L->fin_b, d->flow_type == 1 ? 8 : 7, cur, cur, ld, alpha);
+        }
+        memcpy(latent_out, cur, sizeof(float) * ld);
+    }
+    free(x); free(t_out); free(z); free(ya); free(xf); free(ada); free(h); free(h2); free(cur);
     return rc;
 }
 

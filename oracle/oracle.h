@@ -157,14 +157,19 @@ typedef struct orc_flow_lm_desc {
     int lsd_steps;                           /* LSD solver steps (lsd_decode_steps) */
     int gelu;                                /* 0 erf, 1 tanh */
     int time_norm;                           /* 0 Rms, 1 RmsVar (mlp.rs:17-28) */
+    int z_dim;                               /* 0: no z_proj; else its width (flow_lm.rs:135, 239-240) */
+    int flow_type;                           /* 0 Lsd, 1 Drifting, 2 Pointwise (flow_lm.rs:372-381) */
+    int precision;                           /* 0 f32; 1 q8: int8 weights, bf16 activations */
 } orc_flow_lm_desc;
-/* Floats of the weight blob: every tensor f32, row-major [out][in], in this order --
+/* Floats of the weight blob: every tensor f32, row-major [out][in], in this order (zd = z_dim when
+ * set, else d) --
  * conditioner.embed [n_bins+1][d]; input_linear [d][ldim]; bos_emb [ldim];
  * per layer: norm1 w, b [d]; in_proj [3d][d]; out_proj [d][d]; norm2 w, b [d]; linear1 [ff][d];
  *   linear2 [d][ff];
- * out_norm w, b [d]; out_eos w [1][d], b [1];
- * per time embedder (2): freqs [128]; mlp.0 w [F][256], b [F]; mlp.2 w [F][F], b [F]; alpha [F];
- * cond_embed w [F][d], b [F]; input_proj w [F][ldim], b [F];
+ * out_norm w, b [d]; z_proj [z][d] when z_dim; out_eos w [1][zd], b [1];
+ * per time embedder (2, Lsd only): freqs [128]; mlp.0 w [F][256], b [F]; mlp.2 w [F][F], b [F];
+ *   alpha [F];
+ * cond_embed w [F][zd], b [F]; input_proj w [F][ldim], b [F];
  * per res block: in_ln w, b [F]; mlp.0 w [F][F], b [F]; mlp.2 w [F][F], b [F];
  *   adaLN_modulation.1 w [3F][F], b [3F];
  * final_layer: adaLN_modulation.1 w [2F][F], b [2F]; linear w [ldim][F], b [ldim].
@@ -174,7 +179,8 @@ long long orc_flow_lm_size(const orc_flow_lm_desc *d);
 void orc_linear_f32(const float *x, int rows, int k, const float *w, const float *b, int n, float *y);
 /* SimpleMLPAdaLN::time_embedding([s, t]) (mlp.rs:201-212): out [flow_dim]. */
 int orc_flow_time_embedding(const orc_flow_lm_desc *d, const float *blob, float s, float t, float *out);
-/* SimpleMLPAdaLN::forward (mlp.rs:214-238) on one row: c [d_model], t_emb [flow_dim], x0 [ldim]. */
+/* SimpleMLPAdaLN::forward (mlp.rs:214-238) on one row, f32: c [zd], t_emb [flow_dim] (NULL: a head
+ * without time conditions), x0 [ldim]. */
 int orc_flow_net(const orc_flow_lm_desc *d, const float *blob, const float *c, const float *t_emb,
                  const float *x0, float *out);
 /* TTSModel::prompt_text (tts_model.rs:297-307): the LUT rows of the tokens through the transformer
@@ -182,10 +188,35 @@ int orc_flow_net(const orc_flow_lm_desc *d, const float *blob, const float *c, c
 int orc_flow_lm_prompt_text(const orc_flow_lm_desc *d, const float *blob, orc_stream *st,
                             const int *ids, int n);
 /* One frame (generate_step_parts, tts_model.rs:365-378): input_linear of latent_in (NULL: bos_emb),
- * the transformer (committed), out_norm, the EOS logit (out_eos) and the LSD decode of noise
- * [ldim] conditioned on the output: latent_out [ldim], eos_logit [1]. */
+ * the transformer (committed), out_norm, z_proj, the EOS logit (out_eos) and the flow head on noise
+ * [ldim] conditioned on the output (sample_from_noise, flow_lm.rs:363-384): latent_out [ldim],
+ * eos_logit [1].  f32 desc only. */
 int orc_flow_lm_step(const orc_flow_lm_desc *d, const float *blob, orc_stream *st,
                      const float *latent_in, const float *noise, float *latent_out, float *eos_logit);
+
+/* The q8 precision (desc->precision 1), the batched frame's definition: every linear's weight rows
+ * quantized as orc_quantize_rows does (biases, norms and the LUT stay f32, the LUT rows and bos
+ * rounded to bf16 when read), activations bf16, each op rounding its output once as a bf16 tensor
+ * op does -- linear: bf16(s * acc (+ b)); LayerNorm (affine inside): once; modulate:
+ * bf16(bf16(y * bf16(scale + 1)) + shift); y + t, silu, gate * h, x + gate * h, x + v / steps: once
+ * each.  The time embeddings are computed in f32 (as the f32 path) and rounded once.  The
+ * transformer is orc_layer_step's.  Streams are bf16 caches with bf16 activations. */
+/* Its pieces.  The q8 linear: y = bf16(s[j] * sum_k bf16(x[m][k]) q[j][k] (+ b[j])), then epi 0:
+ * store; 4: silu; 5: silu(bf16(y + aux[j])); 6: out = bf16(out + bf16(aux[m][j] * y)) (the AdaLN
+ * gate); 7: out = bf16(bf16(aux[m][j]) + bf16(y * alpha)) (the solver step); 8: store.  Every
+ * result is rounded to bf16 once.  out [rows][ldo], aux rows of stride ld_aux. */
+void orc_flow_linear_q8(const float *x, int rows, int k, const int8_t *q, const float *s, const float *b, int n,
+                        int epi, float *out, int ldo, const float *aux, int ld_aux, float alpha);
+/* LayerNorm of rows (affine w, b or NULL) rounded to bf16, then when shift is given the AdaLN
+ * modulation (mlp.rs:4-11) in bf16 steps: bf16(bf16(y * bf16(scale + 1)) + shift). */
+void orc_layer_norm_mod(const float *x, int rows, int dim, const float *w, const float *b, float eps,
+                        const float *shift, const float *scale, int ld_mod, float *out);
+typedef struct orc_flow_q8 orc_flow_q8;
+orc_flow_q8 *orc_flow_q8_prepare(const orc_flow_lm_desc *d, const float *blob);
+void orc_flow_q8_free(orc_flow_q8 *m);
+int orc_flow_q8_prompt_text(orc_flow_q8 *m, orc_stream *st, const int *ids, int n);
+int orc_flow_q8_step(orc_flow_q8 *m, orc_stream *st, const float *latent_in, const float *noise,
+                     float *latent_out, float *eos_logit);
 
 /* Many streams, one layer: the CPU baseline's batched step (OpenMP over streams). */
 int orc_batch_attend(orc_stream **streams, int n, int layer, const float *q, const float *k,

@@ -77,6 +77,14 @@ def lib():
             "orc_flow_net": (ctypes.c_int, [ctypes.c_void_p, _fp, _fp, _fp, _fp, _fp]),
             "orc_flow_lm_prompt_text": (ctypes.c_int, [ctypes.c_void_p, _fp, ctypes.c_void_p, _ip, ctypes.c_int]),
             "orc_flow_lm_step": (ctypes.c_int, [ctypes.c_void_p, _fp, ctypes.c_void_p, _fp, _fp, _fp, _fp]),
+            "orc_flow_linear_q8": (None, [_fp, ctypes.c_int, ctypes.c_int, _i8p, _fp, _fp, ctypes.c_int, ctypes.c_int,
+                                          _fp, ctypes.c_int, _fp, ctypes.c_int, ctypes.c_float]),
+            "orc_layer_norm_mod": (None, [_fp, ctypes.c_int, ctypes.c_int, _fp, _fp, ctypes.c_float, _fp, _fp,
+                                          ctypes.c_int, _fp]),
+            "orc_flow_q8_prepare": (ctypes.c_void_p, [ctypes.c_void_p, _fp]),
+            "orc_flow_q8_free": (None, [ctypes.c_void_p]),
+            "orc_flow_q8_prompt_text": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, _ip, ctypes.c_int]),
+            "orc_flow_q8_step": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, _fp, _fp, _fp, _fp]),
             "orc_layer_norm": (None, [_fp, ctypes.c_int, ctypes.c_int, _fp, _fp, ctypes.c_float, ctypes.c_int, _fp]),
             "orc_quantize_rows": (None, [_fp, ctypes.c_int, ctypes.c_int, _i8p, _fp]),
             "orc_linear_q8": (None, [_fp, ctypes.c_int, ctypes.c_int, _i8p, _fp, ctypes.c_int, ctypes.c_int, _fp]),
@@ -397,32 +405,85 @@ def layer_step(streams, layer, weights: LayerWeights, x, scale=0.125):
     return x
 
 
+FLOW_EPILOGUES = {"store": 0, "silu": 4, "silu_add": 5, "gated": 6, "axpy_f32": 7, "store_f32": 8}
+
+
+def flow_linear_q8(x, q, s, epilogue="store", bias=None, aux=None, out=None, alpha=1.0):
+    """The flow net's q8 linear (oracle.h): x [rows][k] (rounded to bf16 as read), q [n][k] int8,
+    s [n]; out [rows][n] is read by "gated" and returned."""
+    x, xp = _f32(x)
+    rows, k = x.shape
+    n = q.shape[0]
+    q = np.ascontiguousarray(q, np.int8)
+    o = np.zeros((rows, n), np.float32) if out is None else np.array(out, np.float32, copy=True, order="C")
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    a = None if aux is None else np.ascontiguousarray(aux, np.float32)
+    sv, sp = _f32(s)
+    lib().orc_flow_linear_q8(xp, rows, k, q.ctypes.data_as(_i8p), sp, b.ctypes.data_as(_fp) if b is not None else None,
+                             n, FLOW_EPILOGUES[epilogue], o.ctypes.data_as(_fp), n,
+                             a.ctypes.data_as(_fp) if a is not None else None,
+                             a.shape[-1] if a is not None and a.ndim > 1 else 0, alpha)
+    return o
+
+
+def layer_norm_mod(x, w=None, b=None, shift=None, scale=None, eps=1e-6):
+    """LayerNorm of rows rounded to bf16, then the AdaLN modulation in bf16 steps (oracle.h)."""
+    x, xp = _f32(x)
+    rows, dim = x.shape
+    out = np.zeros_like(x)
+    P = lambda a: np.ascontiguousarray(a, np.float32).ctypes.data_as(_fp) if a is not None else None
+    keep = [np.ascontiguousarray(a, np.float32) if a is not None else None for a in (w, b, shift, scale)]
+    lib().orc_layer_norm_mod(xp, rows, dim, *[k.ctypes.data_as(_fp) if k is not None else None for k in keep[:2]], eps,
+                             *[k.ctypes.data_as(_fp) if k is not None else None for k in keep[2:]],
+                             keep[2].shape[-1] if keep[2] is not None else 0, out.ctypes.data_as(_fp))
+    return out
+
+
 # ---- the flow LM around the transformer (flow_lm.rs, mlp.rs, conditioners.rs), f32 -------------------
 class _FlowDescC(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in ("d_model", "num_heads", "num_layers", "ff", "ldim", "n_bins",
-                                            "flow_dim", "flow_depth", "lsd_steps", "gelu", "time_norm")]
+                                            "flow_dim", "flow_depth", "lsd_steps", "gelu", "time_norm", "z_dim",
+                                            "flow_type", "precision")]
+
+
+FLOW_TYPES = {"lsd": 0, "drifting": 1, "pointwise": 2}
+PRECISIONS = {"f32": 0, "q8": 1}
 
 
 class FlowLM:
-    """The oracle's single-stream flow LM over a flat f32 weight blob (layout: oracle.h)."""
+    """The oracle's single-stream flow LM over a flat f32 weight blob (layout: oracle.h), in the
+    config's precision: f32, or q8 (int8 weights quantized here, bf16 activations)."""
 
     def __init__(self, cfg, blob):
         self.cfg = cfg
+        self.q8 = getattr(cfg, "precision", "f32") == "q8"
         self.d = _FlowDescC(cfg.d_model, cfg.num_heads, cfg.num_layers, cfg.dim_feedforward, cfg.ldim, cfg.n_bins,
                             cfg.flow_dim, cfg.flow_depth, cfg.lsd_decode_steps, 0 if cfg.gelu == "erf" else 1,
-                            0 if cfg.time_rms_norm == "rms" else 1)
+                            0 if cfg.time_rms_norm == "rms" else 1, getattr(cfg, "z_dim", 0),
+                            FLOW_TYPES[getattr(cfg, "flow_type", "lsd")], PRECISIONS[getattr(cfg, "precision", "f32")])
         self.blob = np.ascontiguousarray(blob, np.float32)
         n = lib().orc_flow_lm_size(self._dp())
         if n != self.blob.size:
             raise OracleError(f"the blob holds {self.blob.size} floats, the layout {n}")
         self._bp = self.blob.ctypes.data_as(_fp)
+        self._q = None
+        if self.q8:
+            self._q = lib().orc_flow_q8_prepare(self._dp(), self._bp)
+            if not self._q:
+                raise OracleError(lib().orc_last_error().decode())
+
+    def __del__(self):
+        if getattr(self, "_q", None):
+            lib().orc_flow_q8_free(self._q)
+            self._q = None
 
     def _dp(self):
         return ctypes.cast(ctypes.pointer(self.d), ctypes.c_void_p)
 
     def stream(self, capacity):
         c = self.cfg
-        return Stream(c.num_layers, c.num_heads, c.d_model // c.num_heads, capacity, cache="f32", act="f32",
+        dt = "bf16" if self.q8 else "f32"
+        return Stream(c.num_layers, c.num_heads, c.d_model // c.num_heads, capacity, cache=dt, act=dt,
                       max_period=c.max_period)
 
     def time_embedding(self, s, t):
@@ -440,14 +501,21 @@ class FlowLM:
 
     def prompt_text(self, st, ids):
         ids = np.ascontiguousarray(ids, np.int32)
-        _ok(lib().orc_flow_lm_prompt_text(self._dp(), self._bp, st.h, ids.ctypes.data_as(_ip), ids.size))
+        if self.q8:
+            _ok(lib().orc_flow_q8_prompt_text(self._q, st.h, ids.ctypes.data_as(_ip), ids.size))
+        else:
+            _ok(lib().orc_flow_lm_prompt_text(self._dp(), self._bp, st.h, ids.ctypes.data_as(_ip), ids.size))
 
     def step(self, st, latent_in, noise):
         """One frame: (latent [ldim], eos logit)."""
         lat = None if latent_in is None else np.ascontiguousarray(latent_in, np.float32)
+        latp = lat.ctypes.data_as(_fp) if lat is not None else None
         nz, nzp = _f32(noise)
         out = np.zeros(self.cfg.ldim, np.float32)
         eos = np.zeros(1, np.float32)
-        _ok(lib().orc_flow_lm_step(self._dp(), self._bp, st.h, lat.ctypes.data_as(_fp) if lat is not None else None,
-                                   nzp, out.ctypes.data_as(_fp), eos.ctypes.data_as(_fp)))
+        if self.q8:
+            _ok(lib().orc_flow_q8_step(self._q, st.h, latp, nzp, out.ctypes.data_as(_fp), eos.ctypes.data_as(_fp)))
+        else:
+            _ok(lib().orc_flow_lm_step(self._dp(), self._bp, st.h, latp, nzp, out.ctypes.data_as(_fp),
+                                       eos.ctypes.data_as(_fp)))
         return out, float(eos[0])

@@ -1,0 +1,101 @@
+"""GPU parity of the q8 flow net's pieces, through the C ABI (xnp_flow_linear_q8, xnp_layer_norm_mod),
+against the oracle's (orc_flow_linear_q8, orc_layer_norm_mod) on the same bf16 inputs.
+
+Bar: the same bf16 values, bit for bit, except where the GPU's summation order (MFMA for the
+product, a wave reduction for the norm's moments) moves an f32 result across a bf16 rounding
+boundary: then one bf16 step at most, and for at most 1 % of the elements.  These fix the rounding
+points of the q8 frame one by one; the end-to-end frame is held to its own bar in
+test_gpu_flow_lm.py.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import oracle, xnp
+from helpers import bf16_round
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _ulps(got, want):
+    want64 = np.abs(want.astype(np.float64))
+    spacing = np.exp2(np.floor(np.log2(np.maximum(want64, 1e-30))) - 7)
+    return np.abs(got.astype(np.float64) - want) / spacing
+
+
+def _close(got, want, what):
+    u = _ulps(got, want)
+    assert (u <= 1).all(), (what, float(u.max()))
+    assert (got != want).mean() <= 0.01, (what, float((got != want).mean()))
+
+
+def _bf(a):
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(DEV).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("rows,k,n", [(100, 48, 40), (130, 512, 600), (64, 1024, 1)])
+@pytest.mark.parametrize("epilogue", ["store", "silu", "silu_add", "gated", "axpy_f32", "store_f32"])
+def test_flow_linear_q8_matches_the_oracle(rows, k, n, epilogue):
+    rng = np.random.default_rng(rows * 7 + k + n)
+    x = bf16_round(rng.standard_normal((rows, k)).astype(np.float32))
+    q, s = oracle.quantize_rows((0.05 * rng.standard_normal((n, k))).astype(np.float32))
+    b = (0.1 * rng.standard_normal(n)).astype(np.float32)
+    aux = out0 = None
+    alpha = 1.0
+    if epilogue == "silu_add":
+        aux = bf16_round(rng.standard_normal(n).astype(np.float32))
+    elif epilogue == "gated":
+        aux = bf16_round(rng.standard_normal((rows, n)).astype(np.float32))
+        out0 = bf16_round(rng.standard_normal((rows, n)).astype(np.float32))
+    elif epilogue == "axpy_f32":
+        aux, alpha = rng.standard_normal((rows, n)).astype(np.float32), 0.5
+    want = oracle.flow_linear_q8(x, q, s, epilogue, bias=b, aux=aux, out=out0, alpha=alpha)
+    f32_out = epilogue in ("axpy_f32", "store_f32")
+    y = (torch.zeros((rows, n), dtype=torch.float32, device=DEV) if f32_out
+         else (_bf(out0) if out0 is not None else torch.zeros((rows, n), dtype=torch.bfloat16, device=DEV)))
+    if aux is None:
+        a = None
+    elif epilogue == "gated":
+        a = _bf(aux)
+    else:
+        a = torch.from_numpy(aux).to(DEV)
+    xnp.flow_linear_q8(_bf(x), torch.from_numpy(q).to(DEV), torch.from_numpy(s).to(DEV), y, epilogue,
+                       bias=torch.from_numpy(b).to(DEV), aux=a, alpha=alpha)
+    torch.cuda.synchronize()
+    _close(y.float().cpu().numpy(), want, epilogue)
+
+
+def test_flow_linear_q8_reads_f32_rows_rounded():
+    # input_linear / input_proj: K = 32 latents in f32, rounded to bf16 as they are staged
+    rng = np.random.default_rng(89)
+    x = rng.standard_normal((70, 32)).astype(np.float32)
+    q, s = oracle.quantize_rows((0.05 * rng.standard_normal((512, 32))).astype(np.float32))
+    b = (0.1 * rng.standard_normal(512)).astype(np.float32)
+    want = oracle.flow_linear_q8(x, q, s, "store", bias=b)
+    y = torch.zeros((70, 512), dtype=torch.bfloat16, device=DEV)
+    xnp.flow_linear_q8(torch.from_numpy(x).to(DEV), torch.from_numpy(q).to(DEV), torch.from_numpy(s).to(DEV), y,
+                       bias=torch.from_numpy(b).to(DEV))
+    torch.cuda.synchronize()
+    _close(y.float().cpu().numpy(), want, "f32 x")
+    with pytest.raises(xnp.XnpError, match="store epilogue"):
+        xnp.flow_linear_q8(torch.from_numpy(x).to(DEV), torch.from_numpy(q).to(DEV), torch.from_numpy(s).to(DEV), y,
+                           "silu")
+
+
+@pytest.mark.parametrize("affine,mod", [(True, True), (False, True), (True, False)])
+def test_layer_norm_mod_matches_the_oracle(affine, mod):
+    rng = np.random.default_rng(90 + 2 * affine + mod)
+    rows, dim = 75, 512
+    x = bf16_round((1 + 2 * rng.standard_normal((rows, dim))).astype(np.float32))
+    w = (1 + 0.1 * rng.standard_normal(dim)).astype(np.float32) if affine else None
+    b = (0.1 * rng.standard_normal(dim)).astype(np.float32) if affine else None
+    ada = bf16_round(rng.standard_normal((rows, 3 * dim)).astype(np.float32))  # (shift, scale, gate) rows
+    shift, scale = (ada[:, :dim], ada[:, dim:2 * dim]) if mod else (None, None)
+    want = oracle.layer_norm_mod(x, w, b, shift, scale)
+    out = torch.zeros((rows, dim), dtype=torch.bfloat16, device=DEV)
+    ada_d = _bf(ada)
+    T = lambda a: torch.from_numpy(a).to(DEV) if a is not None else None
+    xnp.layer_norm_mod(_bf(x), out, T(w), T(b), ada_d[:, :dim] if mod else None, ada_d[:, dim:2 * dim] if mod else None)
+    torch.cuda.synchronize()
+    _close(out.float().cpu().numpy(), want, (affine, mod))

@@ -659,7 +659,8 @@ def _torch_flow_net(W, cfg, c, temb, x0):
     lin = lambda x, n: torch.nn.functional.linear(x, _t(W[n + ".w"]), _t(W[n + ".b"]))
     F = cfg.flow_dim
     x = lin(_t(x0), "input_proj")
-    ya = torch.nn.functional.silu(temb + lin(c, "cond_embed"))
+    y = lin(c, "cond_embed")
+    ya = torch.nn.functional.silu(y if temb is None else temb + y)  # no time conditions: c alone
     for j in range(cfg.flow_depth):
         p = f"res_blocks.{j}."
         ada = lin(ya, p + "ada")
@@ -732,20 +733,29 @@ def _torch_flow_lm(cfg, W, ids, frames, noise):
 
     transformer(_t(W["conditioner.embed"][ids]), 0)
     pos, latent, outs = len(ids), _t(W["bos_emb"]), []
-    temb = (_torch_time_embed(W, 0, 0.0, cfg.time_rms_norm) + _torch_time_embed(W, 1, 1.0, cfg.time_rms_norm)) / 2
+    lsd = cfg.flow_type == "lsd"
+    assert not lsd or cfg.lsd_decode_steps == 1
+    temb = None
+    if lsd:
+        temb = (_torch_time_embed(W, 0, 0.0, cfg.time_rms_norm) + _torch_time_embed(W, 1, 1.0, cfg.time_rms_norm)) / 2
     for f in range(frames):
         x = transformer((_t(W["input_linear"]) @ latent)[None, :], pos)[0]
         pos += 1
         t_out = torch.nn.functional.layer_norm(x, (dm,), _t(W["out_norm.w"]), _t(W["out_norm.b"]), eps=1e-5)
+        if cfg.z_dim:  # z_proj, bias-free (flow_lm.rs:320-323)
+            t_out = _t(W["z_proj"]) @ t_out
         eos = float(_t(W["out_eos.w"])[0] @ t_out + _t(W["out_eos.b"])[0])
-        latent = _t(noise[f]) + _torch_flow_net(W, cfg, t_out, temb, noise[f])
+        v = _torch_flow_net(W, cfg, t_out, temb, noise[f])
+        # one LSD step: noise + v / 1; Drifting: v; Pointwise: noise + v (flow_lm.rs:372-381)
+        latent = v if cfg.flow_type == "drifting" else _t(noise[f]) + v
         outs.append((latent.numpy().copy(), eos))
     return outs
 
 
-def test_flow_lm_prompt_and_frames_match_torch():
+@pytest.mark.parametrize("flow_type,z_dim", [("lsd", 0), ("lsd", 48), ("drifting", 0), ("pointwise", 32)])
+def test_flow_lm_prompt_and_frames_match_torch(flow_type, z_dim):
     # a 5-token prompt, then 4 frames (from bos_emb, then each frame's latent), noise N(0, 0.5)
-    cfg = _small_flow_cfg()
+    cfg = _small_flow_cfg(flow_type=flow_type, z_dim=z_dim)
     blob = flow_lm.random_weights(cfg, 83, std=0.05, unit_norms=False)
     W = flow_lm.split(cfg, blob)
     m = oracle.FlowLM(cfg, blob)
@@ -762,3 +772,100 @@ def test_flow_lm_prompt_and_frames_match_torch():
         assert rel_err(lat, wl) < 2e-5, f
         assert abs(eos - we) <= 2e-5 * max(1.0, abs(we)), f
     assert st.current_end == 9
+
+
+def _q8_exact(cfg, blob):
+    """The blob with every linear's rows replaced by their int8 dequantization, so that quantizing
+    it again gives the same codes: the q8 precision then differs from f32 only in its bf16 rounding."""
+    blob = blob.copy()
+    W = flow_lm.split(cfg, blob)
+    for name, t in W.items():  # every linear the q8 precision quantizes: not the LUT, not the time embedders
+        if t.ndim == 2 and name != "conditioner.embed" and not name.startswith("time_embed"):
+            q, s = oracle.quantize_rows(t)
+            t[:] = q.astype(np.float32) * s[:, None]
+    return blob
+
+
+@pytest.mark.parametrize("flow_type,z_dim", [("lsd", 0), ("pointwise", 64)])
+def test_q8_flow_lm_is_the_f32_one_within_bf16_rounding(flow_type, z_dim):
+    # The q8 precision on weights its quantization reproduces exactly, against the f32 path (pinned
+    # against torch above): only the bf16 rounding of every activation separates them.
+    kw = dict(d_model=512, num_heads=8, num_layers=2, dim_feedforward=1024, flow_dim=512, flow_depth=2, n_bins=50,
+              flow_type=flow_type, z_dim=z_dim)
+    c32 = flow_lm.FlowLMConfig(**kw)
+    cq8 = flow_lm.FlowLMConfig(**kw, precision="q8")
+    blob = _q8_exact(c32, flow_lm.random_weights(c32, 85, std=0.05, unit_norms=False))
+    f32, q8 = oracle.FlowLM(c32, blob), oracle.FlowLM(cq8, blob)
+    s32, sq8 = f32.stream(64), q8.stream(64)
+    rng = np.random.default_rng(86)
+    ids = rng.integers(0, 51, 6)
+    f32.prompt_text(s32, ids)
+    q8.prompt_text(sq8, ids)
+    lat = None
+    worst = 0.0
+    for f in range(8):
+        noise = (0.5 * rng.standard_normal(c32.ldim)).astype(np.float32)
+        want, we = f32.step(s32, lat, noise)
+        got, ge = q8.step(sq8, lat, noise)  # both from the f32 path's latent: no drift between them
+        err = rel_err(got, want)
+        worst = max(worst, err)
+        assert err < 4e-2, (f, err)
+        assert abs(ge - we) <= 4e-2 * max(1.0, abs(we)), (f, ge, we)
+        assert np.array_equal(got, bf16_round(got))  # q8 latents are bf16 values
+        lat = want
+    assert worst > 1e-4  # the precisions do differ: the q8 path is not the f32 one
+
+
+def _ulps(got, want):
+    """|got - want| in units of the bf16 spacing at want (both bf16 values)."""
+    want64 = np.abs(want.astype(np.float64))
+    spacing = np.exp2(np.floor(np.log2(np.maximum(want64, 1e-30))) - 7)
+    return np.abs(got.astype(np.float64) - want) / spacing
+
+
+def test_flow_linear_q8_and_its_epilogues_match_torch_bf16_ops():
+    # y against an f64 product rounded by torch's cast; each epilogue against the same operation on
+    # torch bf16 tensors, which round every result once, from the oracle's own y
+    rng = np.random.default_rng(87)
+    rows, k, n = 9, 48, 40
+    x = bf16_round(rng.standard_normal((rows, k)).astype(np.float32))
+    q, s = oracle.quantize_rows(rng.standard_normal((n, k)).astype(np.float32) * 0.05)
+    b = (0.1 * rng.standard_normal(n)).astype(np.float32)
+    bt = lambda a: torch.from_numpy(np.asarray(a, np.float32)).to(torch.bfloat16)
+    y = oracle.flow_linear_q8(x, q, s, "store", bias=b)
+    ref = (torch.from_numpy(x.astype(np.float64)) @ torch.from_numpy(q.astype(np.float64) * s[:, None].astype(np.float64)).T
+           + torch.from_numpy(b.astype(np.float64))).to(torch.bfloat16).float().numpy()
+    assert (_ulps(y, ref) <= 1).all() and (y == ref).mean() > 0.97
+    assert np.array_equal(oracle.flow_linear_q8(x, q, s, "store_f32", bias=b), y)
+    yt = bt(y)
+    f = lambda t: t.float().numpy()
+    got = oracle.flow_linear_q8(x, q, s, "silu", bias=b)
+    assert (_ulps(got, f(torch.nn.functional.silu(yt))) <= 1).all()
+    temb = bf16_round(rng.standard_normal(n).astype(np.float32))
+    got = oracle.flow_linear_q8(x, q, s, "silu_add", bias=b, aux=temb)
+    assert (_ulps(got, f(torch.nn.functional.silu(yt + bt(temb)))) <= 1).all()
+    gate = bf16_round(rng.standard_normal((rows, n)).astype(np.float32))
+    x0 = bf16_round(rng.standard_normal((rows, n)).astype(np.float32))
+    got = oracle.flow_linear_q8(x, q, s, "gated", bias=b, aux=gate, out=x0)
+    assert np.array_equal(got, f(bt(x0) + bt(gate) * yt))
+    cur = rng.standard_normal((rows, n)).astype(np.float32)
+    got = oracle.flow_linear_q8(x, q, s, "axpy_f32", bias=b, aux=cur, alpha=0.25)
+    assert np.array_equal(got, f(bt(cur) + yt * 0.25))
+
+
+def test_layer_norm_mod_matches_torch_bf16_ops():
+    rng = np.random.default_rng(88)
+    rows, dim = 6, 512
+    x = bf16_round((2 + 3 * rng.standard_normal((rows, dim))).astype(np.float32))
+    w, b = (1 + 0.1 * rng.standard_normal(dim)).astype(np.float32), (0.1 * rng.standard_normal(dim)).astype(np.float32)
+    mod = bf16_round(rng.standard_normal((rows, 3 * dim)).astype(np.float32))
+    shift, scale = mod[:, :dim], mod[:, dim:2 * dim]
+    bt = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(torch.bfloat16)
+    ln = torch.nn.functional.layer_norm(torch.from_numpy(x.astype(np.float64)), (dim,), torch.from_numpy(w.astype(np.float64)),
+                                        torch.from_numpy(b.astype(np.float64)), eps=1e-6).to(torch.bfloat16)
+    want = ((ln * (bt(scale) + 1)) + bt(shift)).float().numpy()
+    got = oracle.layer_norm_mod(x, w, b, shift, scale)
+    assert (_ulps(got, want) <= 1).all() and (got == want).mean() > 0.97
+    ln0 = torch.nn.functional.layer_norm(torch.from_numpy(x.astype(np.float64)), (dim,), eps=1e-6).to(torch.bfloat16)
+    got = oracle.layer_norm_mod(x, shift=shift, scale=scale)
+    assert (_ulps(got, ((ln0 * (bt(scale) + 1)) + bt(shift)).float().numpy()) <= 1).all()

@@ -1060,10 +1060,15 @@ hipError_t launch_prefill(const PoolView &pv, const BatchView &bv, int layer, co
 
 // LayerNorm over rows of `dim` bf16 values (norm1, norm2: transformer.rs:547-548): one wave per
 // row, each lane holding dim / 64 values; mean and biased variance in f32 (two passes over the
-// registers), y = (x - mean) * (1 / sqrt(var + eps)) * w + b, rounded to bf16.
-template <int CH>
+// registers), y = (x - mean) * (1 / sqrt(var + eps)) (* w + b when MODE has kLnAffine), rounded
+// to bf16.  With kLnMod, then the AdaLN modulation (mlp.rs:4-11) as bf16 tensor operations round
+// it: bf16(bf16(y * bf16(scale + 1)) + shift), with shift and scale bf16 rows of stride ld_mod.
+constexpr int kLnAffine = 1, kLnMod = 2;
+
+template <int CH, int MODE>
 __global__ __launch_bounds__(256) void k_layer_norm(const uint16_t *x, int rows, int dim, const float *w,
-                                                    const float *b, float eps, uint16_t *out) {
+                                                    const float *b, float eps, const uint16_t *shift,
+                                                    const uint16_t *scale, int ld_mod, uint16_t *out) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= rows) return;
     const uint16_t *xr = x + (size_t)row * dim;
@@ -1080,6 +1085,14 @@ __global__ __launch_bounds__(256) void k_layer_norm(const uint16_t *x, int rows,
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) sum += v[c][i];
+    }
+    uint4 rsh[CH], rsc[CH]; // the modulation's rows, loaded with x
+    if constexpr ((MODE & kLnMod) != 0) {
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            rsh[c] = *(const uint4 *)(shift + (size_t)row * ld_mod + (c * 64 + lane) * 8);
+            rsc[c] = *(const uint4 *)(scale + (size_t)row * ld_mod + (c * 64 + lane) * 8);
+        }
     }
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) sum += __shfl_xor(sum, o);
@@ -1098,66 +1111,121 @@ __global__ __launch_bounds__(256) void k_layer_norm(const uint16_t *x, int rows,
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
         const int e0 = (c * 64 + lane) * 8;
-        const float4 w0 = *(const float4 *)(w + e0), w1 = *(const float4 *)(w + e0 + 4);
-        const float4 b0 = *(const float4 *)(b + e0), b1 = *(const float4 *)(b + e0 + 4);
-        const float ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-        const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+        float ww[8], bb[8];
+        if constexpr ((MODE & kLnAffine) != 0) {
+            const float4 w0 = *(const float4 *)(w + e0), w1 = *(const float4 *)(w + e0 + 4);
+            const float4 b0 = *(const float4 *)(b + e0), b1 = *(const float4 *)(b + e0 + 4);
+            const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+            const float bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ww[i] = wv[i], bb[i] = bv[i];
+        }
         uint32_t o4[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float y0 = ((v[c][2 * i] - mean) * rstd) * ww[2 * i] + bb[2 * i];
-            const float y1 = ((v[c][2 * i + 1] - mean) * rstd) * ww[2 * i + 1] + bb[2 * i + 1];
-            o4[i] = pack_bf16(y0, y1);
+            float y[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int e = 2 * i + j;
+                y[j] = (v[c][e] - mean) * rstd;
+                if constexpr ((MODE & kLnAffine) != 0) y[j] = y[j] * ww[e] + bb[e];
+                if constexpr ((MODE & kLnMod) != 0) {
+                    const uint32_t us = ((const uint32_t *)&rsc[c])[i], uh = ((const uint32_t *)&rsh[c])[i];
+                    const float sc1 = bf16_value(bf16_bits(bf16_value(j ? us >> 16 : us & 0xffffu) + 1.0f));
+                    const float p = bf16_value(bf16_bits(bf16_value(bf16_bits(y[j])) * sc1));
+                    y[j] = p + bf16_value(j ? uh >> 16 : uh & 0xffffu);
+                }
+            }
+            o4[i] = pack_bf16(y[0], y[1]);
         }
         *(uint4 *)(out + (size_t)row * dim + e0) = make_uint4(o4[0], o4[1], o4[2], o4[3]);
     }
 }
 
-hipError_t launch_layer_norm(const void *x, int rows, int dim, const float *w, const float *b, float eps, void *out,
-                             hipStream_t stream) {
-    if (rows <= 0) return hipSuccess;
+template <int MODE>
+static hipError_t layer_norm_mode(const void *x, int rows, int dim, const float *w, const float *b, float eps,
+                                  const void *shift, const void *scale, int ld_mod, void *out, hipStream_t stream) {
     const dim3 grid((rows + 3) / 4), block(256);
+    const uint16_t *xs = (const uint16_t *)x, *sh = (const uint16_t *)shift, *sc = (const uint16_t *)scale;
+    uint16_t *o = (uint16_t *)out;
+#define XNP_LN(C) hipLaunchKernelGGL((k_layer_norm<C, MODE>), grid, block, 0, stream, xs, rows, dim, w, b, eps, sh, sc, ld_mod, o)
     switch (dim / 512) {
-    case 1: hipLaunchKernelGGL(k_layer_norm<1>, grid, block, 0, stream, (const uint16_t *)x, rows, dim, w, b, eps, (uint16_t *)out); break;
-    case 2: hipLaunchKernelGGL(k_layer_norm<2>, grid, block, 0, stream, (const uint16_t *)x, rows, dim, w, b, eps, (uint16_t *)out); break;
-    case 3: hipLaunchKernelGGL(k_layer_norm<3>, grid, block, 0, stream, (const uint16_t *)x, rows, dim, w, b, eps, (uint16_t *)out); break;
-    case 4: hipLaunchKernelGGL(k_layer_norm<4>, grid, block, 0, stream, (const uint16_t *)x, rows, dim, w, b, eps, (uint16_t *)out); break;
+    case 1: XNP_LN(1); break;
+    case 2: XNP_LN(2); break;
+    case 3: XNP_LN(3); break;
+    case 4: XNP_LN(4); break;
     default: return hipErrorInvalidValue;
     }
+#undef XNP_LN
     return hipGetLastError();
+}
+
+hipError_t launch_layer_norm_mod(const void *x, int rows, int dim, const float *w, const float *b, float eps,
+                                 const void *shift, const void *scale, int ld_mod, void *out, hipStream_t stream) {
+    if (rows <= 0) return hipSuccess;
+    if (dim % 512 || (w == nullptr) != (b == nullptr) || (shift == nullptr) != (scale == nullptr) ||
+        (shift && ld_mod % 8))
+        return hipErrorInvalidValue;
+    if (w && shift) return layer_norm_mode<kLnAffine | kLnMod>(x, rows, dim, w, b, eps, shift, scale, ld_mod, out, stream);
+    if (w) return layer_norm_mode<kLnAffine>(x, rows, dim, w, b, eps, shift, scale, ld_mod, out, stream);
+    if (shift) return layer_norm_mode<kLnMod>(x, rows, dim, w, b, eps, shift, scale, ld_mod, out, stream);
+    return layer_norm_mode<0>(x, rows, dim, w, b, eps, shift, scale, ld_mod, out, stream);
+}
+
+hipError_t launch_layer_norm(const void *x, int rows, int dim, const float *w, const float *b, float eps, void *out,
+                             hipStream_t stream) {
+    return launch_layer_norm_mod(x, rows, dim, w, b, eps, nullptr, nullptr, 0, out, stream);
 }
 
 // y = epilogue(s[n] * sum_k A[m][k] W[n][k]): A [M][K] bf16, W [N][K] int8 with one f32 scale per
 // output channel (row of W), the sum on v_mfma_f32_16x16x32_bf16 with W widened to bf16 exactly
 // (|q| <= 127).  One work group of 4 waves per 64 x 64 tile of y, each wave 32 x 32 (2 x 2 MFMA
 // tiles); K in chunks of 64 staged through LDS, double-buffered, the next chunk's loads in flight
-// while one is multiplied.  The product is rounded to bf16 (the projection's output tensor),
-// then: kStore writes it (column ranges may go to separate outputs: q, k and v), kGelu* write
-// gelu(y) rounded, kResidual adds y (times the layer scale, rounded, when given) into X and
-// rounds: X + layer_scale(linear(..)) as transformer.rs:612-633 does.
+// while one is multiplied.  The product, plus the bias when given, is rounded to bf16 (the
+// projection's output tensor), then: kStore writes it (column ranges may go to separate outputs:
+// q, k and v), kGelu* write gelu(y) rounded, kResidual adds y (times the layer scale, rounded,
+// when given) into X and rounds: X + layer_scale(linear(..)) as transformer.rs:612-633 does; the
+// flow net's epilogues are listed with their enum.  N may be any width (columns past N are
+// neither loaded nor stored) and K any multiple of 16 (the last chunk's loads past K read zeros).
 constexpr int kGmT = 64;  // tile rows and columns
 constexpr int kGmK = 64;  // K chunk
 constexpr int kGmLd = 72; // LDS row length in bf16
 
-template <int EPI>
+template <int EPI, bool AF32>
 __global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K, const int8_t *W, const float *s,
                                                  int N, GemmOut go) {
     __shared__ __attribute__((aligned(16))) uint16_t As[2][kGmT][kGmLd];
     __shared__ __attribute__((aligned(16))) uint16_t Ws[2][kGmT][kGmLd];
-    const int ntn = N / kGmT;
+    const int ntn = (N + kGmT - 1) / kGmT;
     const int m0 = (blockIdx.x / ntn) * kGmT, n0 = (blockIdx.x % ntn) * kGmT;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, l16 = lane & 15;
     const int wm = w & 1, wn = w >> 1;
 
     // staging: A rows a_r and a_r + 32, 8 bf16 at k 8 a_k; W row w_r, 16 int8 at k 16 w_k
     const int a_r = tid >> 3, a_k = tid & 7, w_r = tid >> 2, w_k = tid & 3;
-    const int ar0 = min(m0 + a_r, M - 1), ar1 = min(m0 + a_r + 32, M - 1);
+    const int ar0 = min(m0 + a_r, M - 1), ar1 = min(m0 + a_r + 32, M - 1), wr = min(n0 + w_r, N - 1);
     uint4 ra0, ra1, rw;
     auto load = [&](int kc) {
         const int k0 = kc * kGmK;
-        ra0 = *(const uint4 *)(A + (size_t)ar0 * K + k0 + 8 * a_k);
-        ra1 = *(const uint4 *)(A + (size_t)ar1 * K + k0 + 8 * a_k);
-        rw = *(const uint4 *)(W + (size_t)(n0 + w_r) * K + k0 + 16 * w_k);
+        // past K (K % 16 == 0, so no 16-byte load straddles it): an in-bounds address, then zeros
+        const bool ain = k0 + 8 * a_k < K, win = k0 + 16 * w_k < K;
+        const int ka = ain ? k0 + 8 * a_k : 0, kw = win ? k0 + 16 * w_k : 0;
+        const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+        uint4 l0, l1;
+        if constexpr (AF32) { // 8 f32 of each row, rounded to bf16 pairs
+            const float *af = (const float *)A;
+            const float4 a0 = *(const float4 *)(af + (size_t)ar0 * K + ka), a1 = *(const float4 *)(af + (size_t)ar0 * K + ka + 4);
+            const float4 b0 = *(const float4 *)(af + (size_t)ar1 * K + ka), b1 = *(const float4 *)(af + (size_t)ar1 * K + ka + 4);
+            l0 = make_uint4(pack_bf16(a0.x, a0.y), pack_bf16(a0.z, a0.w), pack_bf16(a1.x, a1.y), pack_bf16(a1.z, a1.w));
+            l1 = make_uint4(pack_bf16(b0.x, b0.y), pack_bf16(b0.z, b0.w), pack_bf16(b1.x, b1.y), pack_bf16(b1.z, b1.w));
+        } else {
+            l0 = *(const uint4 *)(A + (size_t)ar0 * K + ka);
+            l1 = *(const uint4 *)(A + (size_t)ar1 * K + ka);
+        }
+        const uint4 lw = *(const uint4 *)(W + (size_t)wr * K + kw);
+        ra0 = ain ? l0 : z;
+        ra1 = ain ? l1 : z;
+        rw = win ? lw : z;
     };
     auto store = [&](int buf) {
         *(uint4 *)&As[buf][a_r][8 * a_k] = ra0;
@@ -1181,7 +1249,7 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    const int nk = K / kGmK;
+    const int nk = (K + kGmK - 1) / kGmK;
     load(0);
     store(0);
     __syncthreads();
@@ -1210,7 +1278,9 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K
 #pragma unroll
     for (int ni = 0; ni < 2; ++ni) {
         const int n = n0 + 32 * wn + 16 * ni + l16;
+        if (n >= N) continue;
         const float sc = s[n];
+        const float bn = go.bias ? go.bias[n] : 0.f;
         int seg = 0;
         if constexpr (EPI == kStore) {
             if (go.nseg > 1 && n >= go.col0[1]) seg = (go.nseg > 2 && n >= go.col0[2]) ? 2 : 1;
@@ -1222,7 +1292,7 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K
             for (int r = 0; r < 4; ++r) {
                 const int m = m0 + 32 * wm + 16 * mi + 4 * g + r;
                 if (m >= M) continue;
-                const float y = bf16_value(bf16_bits(acc[mi][ni][r] * sc));
+                const float y = bf16_value(bf16_bits(go.bias ? acc[mi][ni][r] * sc + bn : acc[mi][ni][r] * sc));
                 if constexpr (EPI == kStore) {
                     ((uint16_t *)go.out[seg])[(size_t)m * go.ld[seg] + (n - go.col0[seg])] = (uint16_t)bf16_bits(y);
                 } else if constexpr (EPI == kGeluErf || EPI == kGeluTanh) {
@@ -1234,10 +1304,25 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K
                         gv = 0.5f * y * (1.0f + tanhf(c * (y + 0.044715f * y * y * y)));
                     }
                     ((uint16_t *)go.out[0])[(size_t)m * go.ld[0] + n] = (uint16_t)bf16_bits(gv);
-                } else {
+                } else if constexpr (EPI == kResidual) {
                     const float a = go.ls ? bf16_value(bf16_bits(y * lsn)) : y;
                     uint16_t *xp = (uint16_t *)go.out[0] + (size_t)m * go.ld[0] + n;
                     *xp = (uint16_t)bf16_bits(bf16_value(*xp) + a);
+                } else if constexpr (EPI == kSilu) {
+                    ((uint16_t *)go.out[0])[(size_t)m * go.ld[0] + n] = (uint16_t)bf16_bits(y / (1.0f + expf(-y)));
+                } else if constexpr (EPI == kSiluAddVec) {
+                    const float z = bf16_value(bf16_bits(y + ((const float *)go.aux)[n]));
+                    ((uint16_t *)go.out[0])[(size_t)m * go.ld[0] + n] = (uint16_t)bf16_bits(z / (1.0f + expf(-z)));
+                } else if constexpr (EPI == kGated) {
+                    const float gate = bf16_value(((const uint16_t *)go.aux)[(size_t)m * go.ld_aux + n]);
+                    uint16_t *xp = (uint16_t *)go.out[0] + (size_t)m * go.ld[0] + n;
+                    *xp = (uint16_t)bf16_bits(bf16_value(*xp) + bf16_value(bf16_bits(gate * y)));
+                } else if constexpr (EPI == kAxpyF32) {
+                    const float cur = bf16_value(bf16_bits(((const float *)go.aux)[(size_t)m * go.ld_aux + n]));
+                    ((float *)go.out[0])[(size_t)m * go.ld[0] + n] =
+                        bf16_value(bf16_bits(cur + bf16_value(bf16_bits(y * go.alpha))));
+                } else { // kStoreF32
+                    ((float *)go.out[0])[(size_t)m * go.ld[0] + n] = y;
                 }
             }
     }
@@ -1246,16 +1331,28 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K
 hipError_t launch_gemm_q8(const void *A, int M, int K, const int8_t *W, const float *s, int N, int epi,
                           const GemmOut &go, hipStream_t stream) {
     if (M <= 0) return hipSuccess;
-    if (N % kGmT || K % kGmK) return hipErrorInvalidValue;
-    const dim3 grid((N / kGmT) * ((M + kGmT - 1) / kGmT)), block(256);
+    if (N <= 0 || K <= 0 || K % 16) return hipErrorInvalidValue;
+    const dim3 grid(((N + kGmT - 1) / kGmT) * ((M + kGmT - 1) / kGmT)), block(256);
     const uint16_t *a = (const uint16_t *)A;
+#define XNP_GEMM(E) hipLaunchKernelGGL((k_gemm_q8<E, false>), grid, block, 0, stream, a, M, K, W, s, N, go)
+    if (go.a_f32) {
+        if (epi != kStore) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((k_gemm_q8<kStore, true>), grid, block, 0, stream, a, M, K, W, s, N, go);
+        return hipGetLastError();
+    }
     switch (epi) {
-    case kStore: hipLaunchKernelGGL(k_gemm_q8<kStore>, grid, block, 0, stream, a, M, K, W, s, N, go); break;
-    case kGeluErf: hipLaunchKernelGGL(k_gemm_q8<kGeluErf>, grid, block, 0, stream, a, M, K, W, s, N, go); break;
-    case kGeluTanh: hipLaunchKernelGGL(k_gemm_q8<kGeluTanh>, grid, block, 0, stream, a, M, K, W, s, N, go); break;
-    case kResidual: hipLaunchKernelGGL(k_gemm_q8<kResidual>, grid, block, 0, stream, a, M, K, W, s, N, go); break;
+    case kStore: XNP_GEMM(kStore); break;
+    case kGeluErf: XNP_GEMM(kGeluErf); break;
+    case kGeluTanh: XNP_GEMM(kGeluTanh); break;
+    case kResidual: XNP_GEMM(kResidual); break;
+    case kSilu: XNP_GEMM(kSilu); break;
+    case kSiluAddVec: XNP_GEMM(kSiluAddVec); break;
+    case kGated: XNP_GEMM(kGated); break;
+    case kAxpyF32: XNP_GEMM(kAxpyF32); break;
+    case kStoreF32: XNP_GEMM(kStoreF32); break;
     default: return hipErrorInvalidValue;
     }
+#undef XNP_GEMM
     return hipGetLastError();
 }
 
@@ -1407,6 +1504,21 @@ __global__ void k_embed_f32(const float *table, const int32_t *ids, int rows, in
     const int r = blockIdx.x;
     const float *src = table + (size_t)ids[r] * dim;
     for (int i = threadIdx.x; i < dim; i += blockDim.x) out[(size_t)r * dim + i] = src[i];
+}
+
+__global__ void k_gather_rows(const uint4 *table, const int32_t *ids, int row_u4, uint4 *out) {
+    const int r = blockIdx.x;
+    const uint4 *src = table + (size_t)ids[r] * row_u4;
+    for (int i = threadIdx.x; i < row_u4; i += blockDim.x) out[(size_t)r * row_u4 + i] = src[i];
+}
+
+hipError_t launch_gather_rows(const void *table, const int32_t *ids, int rows, int row_bytes, void *out,
+                              hipStream_t stream) {
+    if (rows <= 0) return hipSuccess;
+    if (row_bytes % 16) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_gather_rows, dim3(rows), dim3(256), 0, stream, (const uint4 *)table, ids, row_bytes / 16,
+                       (uint4 *)out);
+    return hipGetLastError();
 }
 
 hipError_t launch_embed_f32(const float *table, const int32_t *ids, int rows, int dim, float *out, hipStream_t stream) {

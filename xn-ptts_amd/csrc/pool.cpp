@@ -46,20 +46,6 @@ uint64_t splitmix64(uint64_t &s) {
     return z ^ (z >> 31);
 }
 
-float bf16_round_host(float x) {
-    uint32_t u;
-    std::memcpy(&u, &x, 4);
-    if ((u & 0x7f800000u) == 0x7f800000u) {
-        if (u & 0x007fffffu) u |= 0x00400000u;
-        u &= 0xffff0000u;
-    } else {
-        u += 0x7fffu + ((u >> 16) & 1u);
-        u &= 0xffff0000u;
-    }
-    std::memcpy(&x, &u, 4);
-    return x;
-}
-
 // RotaryEmbedding::at_positions (rope.rs:37-63) for one position: cos/sin of pos * inv_freq[i],
 // inv_freq[i] = 1 / theta^(i / half), each rounded to the activation dtype (rope.rs:55-56).
 void rope_row(int D, float theta, float pos, bool act_bf16, float2 *out) {
@@ -289,6 +275,22 @@ struct xnp_pool {
 extern "C" const char *xnp_last_error(void) { return g_err.c_str(); }
 
 namespace xnp {
+
+// bf16 rounding on the host: to nearest even, NaN kept quiet (the kernels' rounding).
+float bf16_round_host(float x) {
+    uint32_t u;
+    std::memcpy(&u, &x, 4);
+    if ((u & 0x7f800000u) == 0x7f800000u) {
+        if (u & 0x007fffffu) u |= 0x00400000u;
+        u &= 0xffff0000u;
+    } else {
+        u += 0x7fffu + ((u >> 16) & 1u);
+        u &= 0xffff0000u;
+    }
+    std::memcpy(&x, &u, 4);
+    return x;
+}
+
 xnp_status pool_fail(xnp_status code, const char *fmt, ...) {
     char buf[512];
     va_list ap;
@@ -1317,6 +1319,39 @@ extern "C" xnp_status xnp_linear_q8(const void *x, int32_t rows, int32_t k, cons
     go.ld[0] = n;
     go.ls = epilogue == XNP_EPI_RESIDUAL ? ls : nullptr;
     HIP_TRY(launch_gemm_q8(x, rows, k, w, s, n, epilogue, go, (hipStream_t)hip_stream), "q8 linear");
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_flow_linear_q8(const void *x, int32_t x_f32, int32_t rows, int32_t k, const int8_t *w,
+                                         const float *s, const float *bias, int32_t n, int32_t epilogue, void *y,
+                                         int32_t ldy, const void *aux, int32_t ld_aux, float alpha,
+                                         void *hip_stream) {
+    if (rows < 0 || k <= 0 || n <= 0 || k % 16 || ldy < n)
+        return fail(XNP_E_INVALID, "a q8 linear of %d x %d by %d into rows of %d: k a multiple of 16", rows, k, n, ldy);
+    if (epilogue < XNP_EPI_STORE || epilogue > XNP_EPI_STORE_F32) return fail(XNP_E_INVALID, "epilogue %d", epilogue);
+    if (x_f32 && epilogue != XNP_EPI_STORE) return fail(XNP_E_INVALID, "an f32 x takes the store epilogue");
+    const bool needs_aux = epilogue == XNP_EPI_SILU_ADD || epilogue == XNP_EPI_GATED || epilogue == XNP_EPI_AXPY_F32;
+    if (rows > 0 && (!x || !w || !s || !y || (needs_aux && !aux))) return fail(XNP_E_INVALID, "null argument");
+    if ((epilogue == XNP_EPI_GATED || epilogue == XNP_EPI_AXPY_F32) && ld_aux < n)
+        return fail(XNP_E_INVALID, "aux rows of %d for %d columns", ld_aux, n);
+    GemmOut go;
+    go.out[0] = y, go.ld[0] = ldy, go.bias = bias, go.aux = aux, go.ld_aux = ld_aux, go.alpha = alpha;
+    go.a_f32 = x_f32 != 0;
+    HIP_TRY(launch_gemm_q8(x, rows, k, w, s, n, epilogue, go, (hipStream_t)hip_stream), "q8 linear");
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_layer_norm_mod(const void *x, int32_t rows, int32_t dim, const float *w, const float *b,
+                                         float eps, const void *shift, const void *scale, int32_t ld_mod, void *out,
+                                         void *hip_stream) {
+    if (rows < 0 || dim <= 0 || dim % 512 || dim > 2048)
+        return fail(XNP_E_INVALID, "layer norm over %d rows of %d: rows of a multiple of 512 up to 2048", rows, dim);
+    if ((w == nullptr) != (b == nullptr) || (shift == nullptr) != (scale == nullptr))
+        return fail(XNP_E_INVALID, "the affine takes w and b, the modulation shift and scale");
+    if (shift && (ld_mod < dim || ld_mod % 8)) return fail(XNP_E_INVALID, "modulation rows of %d", ld_mod);
+    if (rows > 0 && (!x || !out)) return fail(XNP_E_INVALID, "null argument");
+    HIP_TRY(launch_layer_norm_mod(x, rows, dim, w, b, eps, shift, scale, ld_mod, out, (hipStream_t)hip_stream),
+            "layer norm");
     return XNP_OK;
 }
 

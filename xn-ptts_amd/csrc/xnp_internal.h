@@ -104,7 +104,15 @@ hipError_t launch_evict_rotate(const PoolView &pv, const EvictRow *rows, int n,
                                const float *cos_row, const float *sin_row, hipStream_t stream);
 hipError_t launch_copy_page(const PoolView &pv, int src_page, int dst_page, hipStream_t stream);
 // Epilogues of the q8 projection GEMM (launch_gemm_q8).
-enum : int32_t { kStore = 0, kGeluErf = 1, kGeluTanh = 2, kResidual = 3 };
+// Epilogues of the q8 projection (launch_gemm_q8), y = bf16(s[n] * acc (+ bias[n])):
+//   kStore out = y; kGelu* out = bf16(gelu(y)); kResidual out = bf16(out + y (* ls[n], rounded));
+//   kSilu out = bf16(silu(y)); kSiluAddVec z = bf16(y + aux[n]) (f32), out = bf16(silu(z));
+//   kGated out = bf16(out + bf16(aux[m][n] * y)) (aux bf16, the AdaLN gate); kAxpyF32 out (f32) =
+//   bf16(bf16(aux[m][n]) + bf16(y * alpha)) (aux f32); kStoreF32 out (f32) = y.
+enum : int32_t {
+    kStore = 0, kGeluErf = 1, kGeluTanh = 2, kResidual = 3, kSilu = 4, kSiluAddVec = 5, kGated = 6, kAxpyF32 = 7,
+    kStoreF32 = 8
+};
 
 // Where a q8 projection writes.  kStore: columns [col0[j], col0[j+1]) go to out[j] (row stride
 // ld[j], column n - col0[j]), j < nseg; the others: out[0] with stride ld[0] (kResidual reads and
@@ -115,10 +123,20 @@ struct GemmOut {
     int32_t col0[3] = {0, 0, 0};
     int32_t nseg = 1;
     const float *ls = nullptr;
+    const float *bias = nullptr; // per output channel, added before the rounding to bf16
+    const void *aux = nullptr;   // the epilogue's operand (see above)
+    int32_t ld_aux = 0;
+    float alpha = 1.f;
+    bool a_f32 = false;          // A holds f32, rounded to bf16 as it is staged (kStore only)
 };
 
 hipError_t launch_layer_norm(const void *x, int rows, int dim, const float *w, const float *b, float eps, void *out,
                              hipStream_t stream);
+// LayerNorm of bf16 rows (w, b: the affine, both null for none), rounded, then when shift is
+// given the AdaLN modulation of mlp.rs:4-11 in bf16 steps: bf16(bf16(y * bf16(scale + 1)) + shift),
+// shift and scale bf16 rows of stride ld_mod.
+hipError_t launch_layer_norm_mod(const void *x, int rows, int dim, const float *w, const float *b, float eps,
+                                 const void *shift, const void *scale, int ld_mod, void *out, hipStream_t stream);
 hipError_t launch_gemm_q8(const void *A, int M, int K, const int8_t *W, const float *s, int N, int epi,
                           const GemmOut &go, hipStream_t stream);
 // Epilogues of the f32 linear (launch_linear_f32), y = x W^T + b:
@@ -155,6 +173,10 @@ struct LinNorm {
 hipError_t launch_linear_f32(const float *x, int ldx, int M, int K, const float *W, const float *b, int N, int epi,
                              const LinOut &lo, hipStream_t stream, const LinNorm *ln = nullptr);
 hipError_t launch_embed_f32(const float *table, const int32_t *ids, int rows, int dim, float *out, hipStream_t stream);
+// out[r] = table[ids[r]] for rows of row_bytes bytes (a multiple of 16)
+hipError_t launch_gather_rows(const void *table, const int32_t *ids, int rows, int row_bytes, void *out,
+                              hipStream_t stream);
+float bf16_round_host(float x); // to nearest even, NaN kept quiet: the kernels' rounding on the host
 hipError_t launch_load_kv(const PoolView &pv, int sid, int layer, const float *kv, int n, hipStream_t stream);
 hipError_t launch_rows_io(const PoolView &pv, int sid, int layer, int kv, int slot0, int n,
                           void *rows, float *scales, bool write, hipStream_t stream);

@@ -1,6 +1,7 @@
-"""The flow LM around the paged transformer (ptts/src/flow_lm.rs, mlp.rs, conditioners.rs), on the
-library's f32 kernels: the tensor layout of its weights, and FlowLM, the binding of the
-xnp_flow_lm_* entry points of include/xnp_kv.h.
+"""The flow LM around the paged transformer (ptts/src/flow_lm.rs, mlp.rs, conditioners.rs): the
+tensor layout of its weights, and FlowLM, the binding of the xnp_flow_lm_* entry points of
+include/xnp_kv.h.  Two precisions: f32 throughout (one stream at a time, the reference's own
+case), or q8 -- int8 per-channel weights on MFMA with bf16 activations, for many streams a frame.
 
     TTSModel::prompt_text          tts_model.rs:297-307    FlowLM.prompt_text
     TTSModel::generate_step_parts  tts_model.rs:365-378    FlowLM.step
@@ -19,10 +20,14 @@ from .kv import _check, _ptr, _stream, load_library
 FREQ_DIM = 256  # the time embedders' frequency embedding (mlp.rs:186-193)
 
 
+FLOW_TYPES = {"lsd": 0, "drifting": 1, "pointwise": 2}  # FlowType (flow_lm.rs:372-381)
+PRECISIONS = {"f32": 0, "q8": 1}
+
+
 @dataclass
 class FlowLMConfig:
-    """FlowLMConfig (flow_lm.rs:114-146) restricted to what this build runs: no z_proj, no
-    attn_dim override, no grouped heads, no layer scale, no conditions or sinks."""
+    """FlowLMConfig (flow_lm.rs:114-146) restricted to what this build runs: no attn_dim override,
+    no grouped heads, no layer scale, no conditions or sinks.  z_dim 0: no z_proj."""
     d_model: int = 512
     num_heads: int = 8
     num_layers: int = 6
@@ -35,6 +40,9 @@ class FlowLMConfig:
     gelu: str = "erf"
     time_rms_norm: str = "rms"
     max_period: float = 10000.0
+    z_dim: int = 0
+    flow_type: str = "lsd"
+    precision: str = "f32"
 
 
 def layout(cfg: FlowLMConfig):
@@ -46,12 +54,16 @@ def layout(cfg: FlowLMConfig):
         p = f"layers.{i}."
         out += [(p + "norm1.w", (d,)), (p + "norm1.b", (d,)), (p + "in_proj", (3 * d, d)), (p + "out_proj", (d, d)),
                 (p + "norm2.w", (d,)), (p + "norm2.b", (d,)), (p + "linear1", (ff, d)), (p + "linear2", (d, ff))]
-    out += [("out_norm.w", (d,)), ("out_norm.b", (d,)), ("out_eos.w", (1, d)), ("out_eos.b", (1,))]
-    for i in range(2):
+    zd = cfg.z_dim or d
+    out += [("out_norm.w", (d,)), ("out_norm.b", (d,))]
+    if cfg.z_dim:
+        out += [("z_proj", (cfg.z_dim, d))]
+    out += [("out_eos.w", (1, zd)), ("out_eos.b", (1,))]
+    for i in range(2 if cfg.flow_type == "lsd" else 0):  # num_time_conds (flow_lm.rs:225-228)
         p = f"time_embed.{i}."
         out += [(p + "freqs", (FREQ_DIM // 2,)), (p + "mlp0.w", (F, FREQ_DIM)), (p + "mlp0.b", (F,)),
                 (p + "mlp2.w", (F, F)), (p + "mlp2.b", (F,)), (p + "alpha", (F,))]
-    out += [("cond_embed.w", (F, d)), ("cond_embed.b", (F,)), ("input_proj.w", (F, ld)), ("input_proj.b", (F,))]
+    out += [("cond_embed.w", (F, zd)), ("cond_embed.b", (F,)), ("input_proj.w", (F, ld)), ("input_proj.b", (F,))]
     for j in range(cfg.flow_depth):
         p = f"res_blocks.{j}."
         out += [(p + "in_ln.w", (F,)), (p + "in_ln.b", (F,)), (p + "mlp0.w", (F, F)), (p + "mlp0.b", (F,)),
@@ -102,7 +114,7 @@ def random_weights(cfg: FlowLMConfig, seed: int, std: float = 0.02, unit_norms: 
 class FlowLMDesc(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in (
         "d_model", "num_heads", "num_layers", "ff", "ldim", "n_bins", "flow_dim", "flow_depth", "lsd_steps",
-        "gelu", "time_norm", "max_rows")]
+        "gelu", "time_norm", "max_rows", "z_dim", "flow_type", "precision")]
 
 
 def desc_of(cfg: FlowLMConfig, max_rows: int = 1) -> FlowLMDesc:
@@ -110,12 +122,14 @@ def desc_of(cfg: FlowLMConfig, max_rows: int = 1) -> FlowLMDesc:
                       ff=cfg.dim_feedforward, ldim=cfg.ldim, n_bins=cfg.n_bins, flow_dim=cfg.flow_dim,
                       flow_depth=cfg.flow_depth, lsd_steps=cfg.lsd_decode_steps,
                       gelu=0 if cfg.gelu == "erf" else 1, time_norm=0 if cfg.time_rms_norm == "rms" else 1,
-                      max_rows=max_rows)
+                      max_rows=max_rows, z_dim=cfg.z_dim, flow_type=FLOW_TYPES[cfg.flow_type],
+                      precision=PRECISIONS[cfg.precision])
 
 
 class FlowLM:
-    """The flow LM on one pool (f32 cache and activations): weights uploaded once, then prompts
-    and frames for batches of that pool's streams."""
+    """The flow LM on one pool (f32 cache and activations for the f32 precision, bf16 for q8):
+    weights uploaded once (quantized on the host for q8), then prompts and frames for batches of
+    that pool's streams."""
 
     def __init__(self, pool, cfg: FlowLMConfig, blob: np.ndarray, max_rows: int = 1):
         self._lib = load_library()

@@ -89,6 +89,8 @@ SIGNATURES = {
     "xnp_write_rows": (_i32, [_p, _i32, _i32, _i32, _i32, _i32, _p, _p, _p]),
     "xnp_stream_load_kv": (_i32, [_p, _i32, _i32, _p, _i32, _p]),
     "xnp_window_open": (_i32, [_p, _i32, _i32p]),
+    "xnp_flow_linear_q8": (_i32, [_p, _i32, _i32, _i32, _p, _p, _p, _i32, _i32, _p, _i32, _p, _i32, _c.c_float, _p]),
+    "xnp_layer_norm_mod": (_i32, [_p, _i32, _i32, _p, _p, _c.c_float, _p, _p, _i32, _p, _p]),
     "xnp_read_rows": (_i32, [_p, _i32, _i32, _i32, _i32, _i32, _p, _p, _p]),
     "xnp_ring_start": (_i32, [_p, _i32, _i32, _i32, _p]),
     "xnp_ring_set_slot": (_i32, [_p, _i32, _i32]),
@@ -419,7 +421,8 @@ class KvPool:
 
 # ---- the rest of the layer (transformer.rs:591-634) ---------------------------------------------
 GELU = {"erf": 0, "tanh": 1}
-EPILOGUES = {"store": 0, "gelu_erf": 1, "gelu_tanh": 2, "residual": 3}
+EPILOGUES = {"store": 0, "gelu_erf": 1, "gelu_tanh": 2, "residual": 3, "silu": 4, "silu_add": 5, "gated": 6,
+             "axpy_f32": 7, "store_f32": 8}
 
 
 class LayerWeights:
@@ -456,3 +459,24 @@ def linear_q8(x, w, s, y, epilogue: str = "store", ls=None, stream=None):
     k = x.shape[-1]
     _check(load_library().xnp_linear_q8(_ptr(x), x.numel() // k, k, _ptr(w), _ptr(s), w.shape[0],
                                         EPILOGUES[epilogue], _ptr(y), _ptr(ls), _stream(stream)))
+
+
+def flow_linear_q8(x, w, s, y, epilogue: str = "store", bias=None, aux=None, alpha: float = 1.0, stream=None):
+    """xnp_flow_linear_q8: x [rows][k] bf16 or f32 (f32: rounded as read, store only), w [n][k] int8,
+    s [n], y [rows][>= n] (bf16, or f32 for axpy_f32 / store_f32); aux per the epilogue."""
+    k = x.shape[-1]
+    rows = x.numel() // k
+    n = w.shape[0]
+    ld_aux = aux.shape[-1] if aux is not None and aux.dim() > 1 else 0
+    _check(load_library().xnp_flow_linear_q8(_ptr(x), int(x.dtype.is_floating_point and x.element_size() == 4),
+                                             rows, k, _ptr(w), _ptr(s), _ptr(bias), n, EPILOGUES[epilogue], _ptr(y),
+                                             y.shape[-1], _ptr(aux), ld_aux, alpha, _stream(stream)))
+
+
+def layer_norm_mod(x, out, w=None, b=None, shift=None, scale=None, eps: float = 1e-6, stream=None):
+    """xnp_layer_norm_mod on bf16 rows: LayerNorm (affine optional), then the AdaLN modulation when
+    shift and scale (bf16 views whose rows have the stride of their base tensor) are given."""
+    dim = x.shape[-1]
+    ld_mod = shift.stride(0) if shift is not None else 0
+    _check(load_library().xnp_layer_norm_mod(_ptr(x), x.numel() // dim, dim, _ptr(w), _ptr(b), eps, _ptr(shift),
+                                             _ptr(scale), ld_mod, _ptr(out), _stream(stream)))
