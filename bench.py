@@ -52,6 +52,12 @@ SEED = 20261201
 H, D = 8, 64
 
 
+def host_threads():
+    """The host threads a CPU baseline may use: OMP_NUM_THREADS when set (the GPU box's share of
+    its host), else every core."""
+    return int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+
+
 def _load(name, path):
     if name in sys.modules:
         return sys.modules[name]
@@ -557,6 +563,118 @@ def run_step(args, xnp, torch):
                 "frames/s", args, ms, "bf16", config, roof, cpu, extra={"audio_sec_per_sec": round(fps * 0.08, 1)})
 
 
+# ---- the batched frame: the q8 flow LM at 2048 streams ----------------------------------------------
+def cpu_frame(cfg, blob, lens, seconds, threads):
+    """The oracle's q8 frame on a sample of the streams, one stream per host thread (each call
+    releases the interpreter lock): frames/s over the sample."""
+    from concurrent.futures import ThreadPoolExecutor
+    oracle = _load("oracle", os.path.join(ROOT, "oracle", "oracle.py"))
+    m = oracle.FlowLM(cfg, blob)
+    rng = np.random.default_rng(SEED + 11)
+    sample = [int(n) for n in lens[:2 * threads]]
+    sts = []
+    for n in sample:
+        st = m.stream(n + 256)
+        for layer in range(cfg.num_layers):
+            for kv in (0, 1):
+                st.write_rows(layer, kv, 0, rng.standard_normal((n, H, D)).astype(np.float32))
+        st.advance(n)
+        sts.append(st)
+    zero = np.zeros(cfg.ldim, np.float32)
+
+    def run(i):
+        m.step(sts[i], None, zero)
+
+    frames, t0 = 0, time.perf_counter()
+    with ThreadPoolExecutor(threads) as ex:
+        while time.perf_counter() - t0 < seconds and frames < 200 * len(sts):
+            list(ex.map(run, range(len(sts))))
+            frames += len(sts)
+    el = time.perf_counter() - t0
+    return {"value": round(frames / el, 2), "unit": "frames/s", "cores": threads, "kind": "port",
+            "sample": f"{len(sts)} streams of the same length draw, {frames // len(sts)} frames each, the q8 frame "
+                      f"(oracle, one stream per thread), {el:.1f} s"}
+
+
+def run_frame(args, xnp, torch):
+    dev = torch.device("cuda:0")
+    fl = xnp.flow_lm
+    S, L = args.step_streams, args.layers
+    cfg = fl.FlowLMConfig(num_layers=L, precision="q8")  # 9 x 512, 8 heads, FF 2048; flow net 512 x 6; ldim 32
+    blob = fl.random_weights(cfg, SEED + 10)
+    rng = np.random.default_rng(SEED + 5)
+    lens = rng.integers(1, args.step_max_len + 1, S)
+    total = args.warmup + 2 * args.steps + 8
+    cap = args.step_max_len + total + 1
+    mbps = (cap + 15) // 16
+    nblocks = int(sum((n + total + 16) // 16 + 1 for n in lens)) + 16
+    pool = xnp.KvPool(num_layers=L, num_heads=H, num_blocks=nblocks, max_streams=S, max_blocks_per_stream=mbps,
+                      cache_dtype="bf16", act_dtype="bf16", max_pos=cap + 16, page_seed=SEED + 6)
+    ids = [pool.init_state(cap) for _ in range(S)]
+    gen = torch.Generator(device=dev).manual_seed(SEED + 7)
+    maxn = int(lens.max())
+    for layer in range(L):
+        for kvi in (0, 1):
+            rows = torch.randn((maxn, H, D), generator=gen, device=dev).to(torch.bfloat16)
+            for sid, n in zip(ids, lens):
+                if layer == 0 and kvi == 0:
+                    pool.advance(sid, int(n))
+                pool.write_rows(sid, layer, kvi, 0, rows[:n])
+    lm = xnp.FlowLM(pool, cfg, blob, max_rows=S)
+    lat = torch.zeros((S, cfg.ldim), dtype=torch.float32, device=dev)
+    eos = torch.empty(S, dtype=torch.float32, device=dev)
+    noise = torch.zeros((S, cfg.ldim), dtype=torch.float32, device=dev)  # temperature 0
+    stream = torch.cuda.Stream()
+    cur = lens.copy()
+    with torch.cuda.stream(stream):
+        lm.step(ids, None, noise, lat, eos, graph=True)  # the bos frame, then frames from the latents
+        cur += 1
+        for _ in range(args.warmup):
+            lm.step(ids, lat, noise, lat, eos, graph=True)
+            cur += 1
+        stream.synchronize()
+        bytes0 = decode_bytes(cur)
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            lm.step(ids, lat, noise, lat, eos, graph=True)
+        stream.synchronize()
+        ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+        cur += args.steps
+        # the dominant kernel: layer 0's fused append + decode, timed by its launch's events over
+        # eager frames (an event recorded inside a graph replay is not the launch's own)
+        hip = HipEvents()
+        evs, bts = [], []
+        for _ in range(args.steps):
+            e = (hip.create(), hip.create())
+            bts.append(decode_bytes(cur))
+            pool.time_next(*e)
+            lm.step(ids, lat, noise, lat, eos)
+            evs.append(e)
+            cur += 1
+        stream.synchronize()
+        kern = np.array([hip.elapsed_ms(*e) for e in evs])
+        for e in evs:
+            hip.destroy(e[0])
+            hip.destroy(e[1])
+    avg_ms = float(kern.mean())
+    achieved = float(np.mean(bts)) / (avg_ms * 1e-3) / 1e9
+    fps = S / (ms / 1000.0)
+    cpu = None if args.no_cpu else cpu_frame(cfg, blob, lens, args.cpu_seconds, host_threads())
+    config = {"workload": f"full batched flow-LM frame at {S} streams, q8: input_linear, {L} transformer layers "
+                          f"({DM} wide, {H} heads x {D}, FF {FF}, int8 per-channel weights on MFMA, bf16 activations, "
+                          f"paged bf16 KV append + decode over cache lengths U[1,{args.step_max_len}]), out_norm, the "
+                          f"EOS head and the flow net (512 x 6, one LSD step) at temperature 0; every frame replayed "
+                          f"from one hipGraph after its plan upload",
+              "streams": S, "layers": L, "d_model": DM, "ff": FF, "flow": "512 x 6"}
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "k_decode<bf16> (fused append + RoPE + decode) of layer 0, timed in eager frames",
+            "avg_kernel_us": round(avg_ms * 1000.0, 2), "bytes_per_launch": int(np.mean(bts)),
+            "decode_share_of_frame": round(L * avg_ms / ms, 3)}
+    return line("frames/sec, full batched flow-LM frame at 2048 streams (q8 transformer + flow net)", fps,
+                "frames/s", args, ms, "bf16", config, roof, cpu, extra={"audio_sec_per_sec": round(fps * 0.08, 1)})
+
+
 # ---- the single-stream flow LM (configuration 1) ----------------------------------------------------
 def flow_bytes(cfg, n):
     """Algorithmic bytes of one frame at batch 1: every f32 weight of the transformer, the heads and
@@ -633,8 +751,8 @@ def run_flowlm(args, xnp, torch):
              "eager_frames_per_s": round(1000.0 / eager_ms, 1)}
     if not args.no_cpu:
         oracle = _load("oracle", os.path.join(ROOT, "oracle", "oracle.py"))
-        extra["cpu_baseline_all_cores"] = cpu_flowlm(cfg, blob, tokens, args.cpu_seconds, os.cpu_count() or 1)
-        oracle.set_threads(os.cpu_count() or 1)
+        extra["cpu_baseline_all_cores"] = cpu_flowlm(cfg, blob, tokens, args.cpu_seconds, host_threads())
+        oracle.set_threads(host_threads())
     config = {"workload": "single-stream flow LM, Phonon-31m shape (6 x 512, 8 heads x 64, FF 2048, ldim 32, "
                           "n_bins 4000, flow net 512 x 6, 1 LSD step), random-init f32 weights N(0, 0.02), unit "
                           "norms; 64 seeded tokens, then greedy frames at temperature 0 on an f32 paged cache",
@@ -655,7 +773,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=["decode", "prefill", "window", "step", "flowlm"], default="decode")
+    ap.add_argument("--workload", choices=["decode", "prefill", "window", "step", "flowlm", "frame"], default="decode")
     ap.add_argument("--step-streams", type=int, default=2048)
     ap.add_argument("--step-max-len", type=int, default=1500)
     ap.add_argument("--streams", type=int, default=1024)
@@ -690,7 +808,7 @@ def main():
     xnp = _load("xn_ptts_amd", os.path.join(ROOT, "xn-ptts_amd"))
     xnp.load_library()
     run = {"decode": run_decode, "prefill": run_prefill, "window": run_window, "step": run_step,
-           "flowlm": run_flowlm}[args.workload]
+           "flowlm": run_flowlm, "frame": run_frame}[args.workload]
     print(json.dumps(run(args, xnp, torch)))
 
 
