@@ -119,26 +119,28 @@ def window_bytes(attended):
     return int((2 * a * H * D + 2 * H * 4 * pages + H * D * 2 * (1 + 2 + 1) + 2 * H * D + 4 * pages).sum())
 
 
-def timed_steps(step, steps, warmup, L):
+def timed_steps(step, steps, warmup, L, every=5):
     """Run warmup then `steps` steps; wall ms per step, and the durations (ms) of the timed launches.
 
-    Step s times one launch, layer s % L, with HIP events its launch records around the kernel:
-    a recorded event costs about 17 us of issue time, so timing every launch would slow the very
-    steps the wall clock measures.  Layers are alike, so the rotating sample's mean is the mean
-    launch duration."""
+    Every `every`-th step times one launch, layer (s / every) % L, with HIP events its launch
+    records around the kernel: a launch that records events issues more slowly (and the steps
+    around it with it), so timing every step would slow the very steps the wall clock measures.
+    Layers are alike, so the rotating sample's mean is the mean launch duration."""
     import torch
     for _ in range(warmup):
         step(None)
     torch.cuda.synchronize()
     hip = HipEvents()
-    ev = [[(hip.create(), hip.create()) if l == s % L else None for l in range(L)] for s in range(steps)]
+    timed = {s: (s // every) % L for s in range(0, steps, every)}
+    ev = [[(hip.create(), hip.create()) if timed.get(s) == l else None for l in range(L)] if s in timed else None
+          for s in range(steps)]
     t0 = time.perf_counter()
     for s in range(steps):
         step(ev[s])
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    kern = np.array([hip.elapsed_ms(*ev[s][s % L]) for s in range(steps)])
-    for pair in (p_ for s_ in ev for p_ in s_ if p_ is not None):
+    kern = np.array([hip.elapsed_ms(*ev[s][timed[s]]) for s in timed])
+    for pair in (p_ for s_ in ev if s_ is not None for p_ in s_ if p_ is not None):
         for e in pair:
             hip.destroy(e)
     return (t1 - t0) * 1000.0 / steps, kern
@@ -214,11 +216,12 @@ def run_decode(args, xnp, torch):
     out = [torch.empty((S, H, D), dtype=torch.bfloat16, device=dev) for _ in range(L)]
     torch.cuda.synchronize()
     cur = lens.copy()
-    bytes_timed = [0]
+    bytes_timed = [0, 0]  # bytes of the timed launches, their count
 
     def step(events):
         if events is not None:
-            bytes_timed[0] += L * decode_bytes(cur)
+            bytes_timed[0] += decode_bytes(cur)  # the one launch this step times
+            bytes_timed[1] += 1
         pool.begin(ids)
         for layer in range(L):
             if events is not None and events[layer] is not None:  # recorded by the launch itself
@@ -229,7 +232,7 @@ def run_decode(args, xnp, torch):
 
     ms, kern = timed_steps(step, args.steps, args.warmup, L)
     avg_ms = float(kern.mean())
-    bytes_per_launch = bytes_timed[0] / (args.steps * L)  # every layer of a step moves the same bytes
+    bytes_per_launch = bytes_timed[0] / bytes_timed[1]  # every layer of a step moves the same bytes
     achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
     fps = S / (ms / 1000.0)
     # HBM traffic per launch from the FETCH_SIZE / WRITE_SIZE counter runs of this same command,
@@ -407,12 +410,13 @@ def run_window(args, xnp, torch):
         pool.end()
         written[act] += 1
     torch.cuda.synchronize()
-    bytes_timed = [0]
+    bytes_timed = [0, 0]  # bytes of the timed launches, their count
 
     def step(events):
         att = np.minimum(written + 1, WINDOW)
         if events is not None:
-            bytes_timed[0] += L * window_bytes(att)
+            bytes_timed[0] += window_bytes(att)  # the one launch this step times
+            bytes_timed[1] += 1
         pool.slide_batch(ids, 0, SPAN, WINDOW, 1, heads + written)
         pool.begin(ids)
         for layer in range(L):
@@ -424,7 +428,7 @@ def run_window(args, xnp, torch):
 
     ms, kern = timed_steps(step, args.steps, args.warmup, L)
     avg_ms = float(kern.mean())
-    bytes_per_launch = bytes_timed[0] / (args.steps * L)  # every layer of a step moves the same bytes
+    bytes_per_launch = bytes_timed[0] / bytes_timed[1]  # every layer of a step moves the same bytes
     achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
     fps = S / (ms / 1000.0)
     cpu = None if args.no_cpu else cpu_window(L, lens, args.cpu_seconds)
@@ -526,11 +530,12 @@ def run_step(args, xnp, torch):
     ws = torch.empty(pool.layer_workspace(S, DM, FF), dtype=torch.uint8, device=dev)
     torch.cuda.synchronize()
     cur = lens.copy()
-    bytes_timed = [0]
+    bytes_timed = [0, 0]  # bytes of the timed launches, their count
 
     def step(events):
         if events is not None:
-            bytes_timed[0] += L * decode_bytes(cur)
+            bytes_timed[0] += decode_bytes(cur)  # the one launch this step times
+            bytes_timed[1] += 1
         x.copy_(x0)  # the step's input rows (synthetic; the model's would come from its embeddings)
         pool.begin(ids)
         for layer in range(L):
@@ -542,7 +547,7 @@ def run_step(args, xnp, torch):
 
     ms, kern = timed_steps(step, args.steps, args.warmup, L)
     avg_ms = float(kern.mean())
-    bytes_per_launch = bytes_timed[0] / (args.steps * L)  # every layer of a step moves the same bytes
+    bytes_per_launch = bytes_timed[0] / bytes_timed[1]  # every layer of a step moves the same bytes
     achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
     fps = S / (ms / 1000.0)
     rest_ms = ms / L - avg_ms  # per layer: norms, projections, plan, launch gaps

@@ -33,9 +33,12 @@
  *   q, out          [n][t][H][D]     activation dtype (f32 or bf16)
  *   k, v            [n][t][KVH][D]   activation dtype; KV head j serves query heads
  *                                    j*H/KVH .. (j+1)*H/KVH-1 (transformer.rs:199-211)
- *   pages           [L][2][num_blocks][H][16][D]   cache dtype; one (page, head) is a
- *                                    contiguous 16 x D tile
- *   int8 scales     [L][2][num_blocks][H]          f32, one per (page, head), K and V apart
+ *   pages           [L][2][num_blocks][KVH][16][D] cache dtype; one (page, kv head) is a
+ *                                    contiguous 16 x D tile.  The cache stores the KVH heads,
+ *                                    not the H repeated ones the reference's cache holds
+ *                                    (transformer.rs:199-211): the query heads of a group read
+ *                                    the same tiles
+ *   int8 scales     [L][2][num_blocks][KVH]        f32, one per (page, kv head), K and V apart
  */
 #ifndef XNP_KV_H
 #define XNP_KV_H
@@ -149,8 +152,8 @@ xnp_status xnp_stream_blocks(const xnp_pool *pool, int32_t id, int32_t *pages, i
 /* The seen map attention uses at the next step: valid[slot] for slot < capacity. */
 xnp_status xnp_ring_valid(const xnp_pool *pool, int32_t id, uint8_t *valid, int32_t cap);
 
-/* Raw rows [slot0, slot0 + n) of one layer, kv 0 = keys, 1 = values: rows [n][H][D] in the
- * cache dtype (device memory); for int8 also scales [nb][H] for the nb pages the rows touch.
+/* Raw rows [slot0, slot0 + n) of one layer, kv 0 = keys, 1 = values: rows [n][KVH][D] in the
+ * cache dtype (device memory); for int8 also scales [nb][KVH] for the nb pages the rows touch.
  * No RoPE, no quantization: a voice cache loaded as is, or a cache read back. */
 xnp_status xnp_write_rows(xnp_pool *pool, int32_t id, int32_t layer, int32_t kv, int32_t slot0,
                           int32_t n, const void *rows, const float *scales, void *hip_stream);

@@ -130,12 +130,13 @@ def test_layer_steps_match_the_oracle(cache, KVH, ls):
         n = sts[i].current_end
         for layer in range(L):
             for kv in (0, 1):
-                rows = torch.empty((n, H, D), dtype=torch.bfloat16 if cache == "bf16" else torch.int8, device=DEV)
+                # the pool stores each kv head once; the oracle repeats it over its group
+                rows = torch.empty((n, KVH, D), dtype=torch.bfloat16 if cache == "bf16" else torch.int8, device=DEV)
                 nb = (n + 15) // 16
-                sc = torch.zeros((nb, H), dtype=torch.float32, device=DEV)
+                sc = torch.zeros((nb, KVH), dtype=torch.float32, device=DEV)
                 pool.read_rows(ids[i], layer, kv, 0, rows, sc if cache == "i8" else None)
                 torch.cuda.synchronize()
-                vals, _, _ = sts[i].read_rows(layer, kv, 0, n)
+                vals = sts[i].read_rows(layer, kv, 0, n)[0][:, ::H // KVH]
                 if cache == "i8":
                     got_rows = rows.float().cpu().numpy() * np.repeat(sc.cpu().numpy(), 16, axis=0)[:n, :, None]
                     bar = 6e-2  # one int8 step of a row whose scale came from slightly different inputs

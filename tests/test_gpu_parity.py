@@ -142,14 +142,16 @@ class Pair:
         if n == 0:
             return
         valid = st.ring_info()["valid"] if st.ring_info()["mode"] else np.ones(st.capacity, bool)
+        G = self.H // self.KVH  # the pool stores kv head j once; the oracle repeats it at heads j*G ..
         for layer in range(self.L):
             for kv in (0, 1):
-                rows = torch.empty((n, self.H, 64), dtype=CACHE_TORCH[self.cache], device=DEV)
+                rows = torch.empty((n, self.KVH, 64), dtype=CACHE_TORCH[self.cache], device=DEV)
                 nb = (n - 1) // 16 + 1
-                scales = torch.zeros((nb, self.H), dtype=torch.float32, device=DEV)
+                scales = torch.zeros((nb, self.KVH), dtype=torch.float32, device=DEV)
                 self.pool.read_rows(sid, layer, kv, 0, rows, scales if self.cache == "i8" else None)
                 torch.cuda.synchronize()
                 vals, q8, osc = st.read_rows(layer, kv, 0, n)
+                vals, q8, osc = vals[:, ::G], q8[:, ::G], osc[:, ::G]
                 m = valid[:n]
                 if self.cache == "i8":
                     g = rows.cpu().numpy()
@@ -212,13 +214,50 @@ def test_split_chunks_and_separate_calls_agree():
     assert np.array_equal(outs[1], outs[3])  # the fused append changes nothing but the launch
 
 
-def test_grouped_kv_heads():
-    p = Pair(cache="bf16", act="bf16", H=8, KVH=2, streams=4, cap=128, seed=4)
-    for i, n in enumerate([3, 40, 64, 100]):
+# ---- grouped heads, stored once per kv head (transformer.rs:199-211) ----------------------------
+@pytest.mark.parametrize("kvh", [4, 2, 1])
+@pytest.mark.parametrize("cache,act", [("bf16", "bf16"), ("f32", "f32"), ("i8", "bf16")])
+def test_grouped_kv_heads(cache, act, kvh):
+    # 8 query heads over 4, 2 or 1 stored kv heads: appends of t rows, prompts, then decode steps
+    # (an int8 pool appends in a kernel of its own before each decode)
+    p = Pair(cache=cache, act=act, H=8, KVH=kvh, streams=5, cap=160, seed=4 + kvh)
+    for i, n in enumerate([0, 3, 40, 64, 100]):
         p.fill(i, n)
-    p.step()
-    p.step()
-    for i in range(4):
+    p.prefill(9, which=[0, 2])
+    for _ in range(3):
+        p.step()
+    for i in range(5):
+        p.assert_cache_equal(i)
+
+
+def test_grouped_heads_store_a_kv_head_once():
+    # the pages hold KVH heads: a pool of 2 kv heads takes a quarter of one of 8
+    def pages_bytes(kvh):
+        pool = xnp.KvPool(num_layers=2, num_heads=8, num_kv_heads=kvh, num_blocks=64, max_streams=4,
+                          max_blocks_per_stream=8, cache_dtype="bf16", act_dtype="bf16", max_pos=256)
+        return pool.stats()["device_bytes"]
+    page = 2 * 2 * 64 * 16 * 64 * 2  # layers x (K, V) x blocks x 16 rows x 64 dims x 2 bytes, per kv head
+    assert pages_bytes(8) - pages_bytes(2) == 6 * page
+
+
+@pytest.mark.parametrize("cache,act,mode", [("bf16", "bf16", "shift"), ("i8", "bf16", "absolute")])
+def test_grouped_heads_on_rings(cache, act, mode):
+    p = Pair(cache=cache, act=act, H=8, KVH=2, streams=2, cap=48, seed=31)
+    context = 20
+    for i in range(2):
+        p.fill(i, 4)
+        p.pool.start_ring(p.ids[i], mode, prefix=4)
+        p.orc[i].start_ring(mode, prefix=4)
+    for steps in range(50):
+        for i in range(2):  # a 4-row prefix, then frames sliding over 20 slots, the oldest evicted
+            slot = 4 + steps % context
+            if p.orc[i].ring_info()["valid"][slot]:
+                p.orc[i].evict(4, [slot])
+                p.pool.evict(p.ids[i], 4, [slot])
+            p.orc[i].set_ring_slot(slot)
+            p.pool.set_ring_slot(p.ids[i], slot)
+        p.step()
+    for i in range(2):
         p.assert_cache_equal(i)
 
 

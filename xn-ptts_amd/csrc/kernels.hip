@@ -61,8 +61,10 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 template <int CDT> constexpr int esize() { return CDT == DT_F32 ? 4 : CDT == DT_BF16 ? 2 : 1; }
 
 // Element offset of row 0 of tile (layer, kv, page, head).
-__device__ __forceinline__ size_t tile_index(const PoolView &pv, int layer, int kv, int page, int h) {
-    return (((size_t)layer * 2 + kv) * pv.NB + page) * pv.H + h;
+// The (page, kv head) tile: pages hold the KVH heads a layer stores (query heads h share kv head
+// h / (H / KVH), transformer.rs:199-211), not the H repeated ones.
+__device__ __forceinline__ size_t tile_index(const PoolView &pv, int layer, int kv, int page, int j) {
+    return (((size_t)layer * 2 + kv) * pv.NB + page) * pv.KVH + j;
 }
 
 // Two activation values (dims 2i, 2i+1) of a head row.
@@ -167,7 +169,7 @@ __global__ __launch_bounds__(1024) void k_append(PoolView pv, BatchView bv, int 
                                                  const void *v, int nseg) {
     const int b = blockIdx.x / nseg, seg = blockIdx.x % nseg;
     const StreamPlan P = bv.plans[b];
-    const int h = threadIdx.x >> 6;
+    const int j = threadIdx.x >> 6; // kv head
     const int t = bv.t;
     const int ws = P.write_slot;
     const int blk = (ws >> 4) + seg;
@@ -175,13 +177,12 @@ __global__ __launch_bounds__(1024) void k_append(PoolView pv, BatchView bv, int 
     if (i0 >= i1) return;
     const int page = pv.tables[(size_t)P.sid * pv.mbps + blk];
     if (page < 0 || page >= pv.NB) return; // begin took this page; never index the pool without one
-    const int group = pv.H / pv.KVH;
     constexpr int AE = ABF ? 2 : 4;
     for (int i = i0; i < i1; ++i) {
         const int slot = ws + i;
-        const size_t arow = ((size_t)P.out_row * t + i) * pv.KVH + h / group;
+        const size_t arow = ((size_t)P.out_row * t + i) * pv.KVH + j;
         const bool fresh = P.ring ? (P.fresh != 0) : ((slot & 15) == 0);
-        append_row_wave<CDT, ABF>(pv, layer, page, slot & 15, h, P.key_pos + i,
+        append_row_wave<CDT, ABF>(pv, layer, page, slot & 15, j, P.key_pos + i,
                                   (const char *)k + arow * kHeadDim * AE, (const char *)v + arow * kHeadDim * AE,
                                   fresh);
         __syncthreads();
@@ -265,6 +266,7 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
 
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int nb = R.nblk > w ? (R.nblk - w + SPLIT - 1) / SPLIT : 0; // this wave's pages
+    const int kvh = h / (pv.H / pv.KVH);                               // the tiles query head h reads
 
     // Per-page metadata, lane j holding page w + j * SPLIT: page id, seen rows, int8 scales.
     // Past the wave's last page the lanes hold page 0 with no row seen.
@@ -286,8 +288,8 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
         my_page = ok ? pg : 0;
         my_seen = seen;
         if constexpr (CDT == DT_I8) {
-            my_sk = pv.scales[tile_index(pv, layer, 0, my_page, h)];
-            my_sv = pv.scales[tile_index(pv, layer, 1, my_page, h)];
+            my_sk = pv.scales[tile_index(pv, layer, 0, my_page, kvh)];
+            my_sv = pv.scales[tile_index(pv, layer, 1, my_page, kvh)];
         }
     }
 
@@ -309,9 +311,9 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
         }
     }
 
-    const uint4 *kbase = (const uint4 *)((const char *)pv.pages + tile_index(pv, layer, 0, 0, h) * (kBlock * kHeadDim * esize<CDT>()));
-    const uint4 *vbase = (const uint4 *)((const char *)pv.pages + tile_index(pv, layer, 1, 0, h) * (kBlock * kHeadDim * esize<CDT>()));
-    const size_t page_u4 = (size_t)pv.H * (kBlock * kHeadDim * esize<CDT>() / 16);
+    const uint4 *kbase = (const uint4 *)((const char *)pv.pages + tile_index(pv, layer, 0, 0, kvh) * (kBlock * kHeadDim * esize<CDT>()));
+    const uint4 *vbase = (const uint4 *)((const char *)pv.pages + tile_index(pv, layer, 1, 0, kvh) * (kBlock * kHeadDim * esize<CDT>()));
+    const size_t page_u4 = (size_t)pv.KVH * (kBlock * kHeadDim * esize<CDT>() / 16);
 
     float m = -1e30f, l = 0.f;
     float acc[DPL];
@@ -405,16 +407,18 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
     }
     if (owner) {
         const int slot = R.write_slot;
-        const size_t arow = (size_t)R.b * pv.KVH + h / (pv.H / pv.KVH);
+        const size_t arow = (size_t)R.b * pv.KVH + kvh;
         const bool fresh = (R.flags & 1) ? (R.flags & 2) != 0 : ((slot & 15) == 0);
-        append_row_wave<CDT, ABF>(pv, layer, __builtin_amdgcn_readlane(my_page, wj), slot & 15, h, R.key_pos,
+        // with grouped heads every query head of the group writes the same row (the same bytes);
+        // int8 pools append in a kernel of their own first, since their append rewrites the page
+        append_row_wave<CDT, ABF>(pv, layer, __builtin_amdgcn_readlane(my_page, wj), slot & 15, kvh, R.key_pos,
                                   (const char *)knew + arow * kHeadDim * AE, (const char *)vnew + arow * kHeadDim * AE,
                                   fresh);
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
         if constexpr (CDT == DT_I8) {
             if (lane == wj) { // the append may have raised this page's scales
-                my_sk = pv.scales[tile_index(pv, layer, 0, my_page, h)];
-                my_sv = pv.scales[tile_index(pv, layer, 1, my_page, h)];
+                my_sk = pv.scales[tile_index(pv, layer, 0, my_page, kvh)];
+                my_sv = pv.scales[tile_index(pv, layer, 1, my_page, kvh)];
             }
         }
     }
@@ -483,10 +487,24 @@ template <int CDT, bool ABF, int SPLIT, bool PREFIX>
 __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(Lanes<CDT>::WAVES))) void k_decode(
     PoolView pv, BatchView bv, int layer, const void *q, const void *knew, const void *vnew, void *out, float qmul,
     int fused) {
-    const char *rec = bv.recs + (size_t)(blockIdx.x / pv.H) * bv.rec_stride;
+    // Work groups go to the 8 XCDs in turn (group b to XCD b % 8).  The G = H / KVH query heads
+    // of one (stream, kv head) read the same tiles: in runs of 8 G groups, XCD x takes the G heads
+    // of pair x of the run, one after another, so their reads meet in that XCD's L2.  With G = 1
+    // this is group b -> (record b / H, head b % H).
+    const int G = pv.H / pv.KVH, b = blockIdx.x;
+    const int full = bv.n * pv.KVH / 8 * 8; // (stream, kv head) pairs in whole runs
+    int pair, gi;
+    if (b < full * G) {
+        pair = b / (8 * G) * 8 + b % 8;
+        gi = b % (8 * G) / 8;
+    } else {
+        pair = full + (b - full * G) / G;
+        gi = (b - full * G) % G;
+    }
+    const char *rec = bv.recs + (size_t)(pair / pv.KVH) * bv.rec_stride;
     const StreamRec R = *(const StreamRec *)rec;
     attend_core<CDT, ABF, SPLIT, PREFIX>(pv, bv, layer, R, (const int32_t *)(rec + sizeof(StreamRec)),
-                                         blockIdx.x % pv.H, q, knew, vnew, out, qmul, fused);
+                                         pair % pv.KVH * G + gi, q, knew, vnew, out, qmul, fused);
 }
 
 // Prompt rows (transformer.rs:231-248), after k_append has written all t rows: row i of a stream
@@ -521,7 +539,7 @@ template <int CDT, bool ABF>
 static hipError_t append_impl(const PoolView &pv, const BatchView &bv, int layer, const void *k,
                               const void *v, hipStream_t stream) {
     const int nseg = (bv.t + kBlock - 1) / kBlock + 1;
-    hipLaunchKernelGGL((k_append<CDT, ABF>), dim3(bv.n * nseg), dim3(64 * pv.H), 0, stream, pv, bv, layer, k,
+    hipLaunchKernelGGL((k_append<CDT, ABF>), dim3(bv.n * nseg), dim3(64 * pv.KVH), 0, stream, pv, bv, layer, k,
                        v, nseg);
     return hipGetLastError();
 }
@@ -588,10 +606,10 @@ template <int CDT, bool ABF>
 __global__ void k_evict_rotate(PoolView pv, const EvictRow *rows, const float2 *cs_row) {
     const EvictRow R = rows[blockIdx.x / pv.L];
     const int layer = blockIdx.x % pv.L;
-    const int h = threadIdx.x >> 5, pr = threadIdx.x & 31;
+    const int j = threadIdx.x >> 5, pr = threadIdx.x & 31; // kv head, dim pair
     const int page = pv.tables[(size_t)R.sid * pv.mbps + (R.slot >> 4)];
     if (page < 0 || page >= pv.NB) return;
-    const size_t e = tile_index(pv, layer, 0, page, h) * (kBlock * kHeadDim) + (R.slot & 15) * kHeadDim + 2 * pr;
+    const size_t e = tile_index(pv, layer, 0, page, j) * (kBlock * kHeadDim) + (R.slot & 15) * kHeadDim + 2 * pr;
     float2 x;
     if constexpr (CDT == DT_F32) {
         x = *(const float2 *)((const float *)pv.pages + e);
@@ -612,7 +630,7 @@ __global__ void k_evict_rotate(PoolView pv, const EvictRow *rows, const float2 *
 hipError_t launch_evict_rotate(const PoolView &pv, const EvictRow *rows, int n, const float *cs,
                                const float *, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
-    const dim3 grid(n * pv.L), block(32 * pv.H);
+    const dim3 grid(n * pv.L), block(32 * pv.KVH);
     const float2 *csr = (const float2 *)cs;
     switch (pv.cache_dt * 2 + pv.act_dt) {
     case DT_F32 * 2 + DT_F32: hipLaunchKernelGGL((k_evict_rotate<DT_F32, false>), grid, block, 0, stream, pv, rows, csr); break;
@@ -629,9 +647,9 @@ __global__ void k_copy_page(PoolView pv, int src, int dst, int tile_u4) {
     const int layer = blockIdx.x >> 1, kv = blockIdx.x & 1;
     const uint4 *s = (const uint4 *)pv.pages + tile_index(pv, layer, kv, src, 0) * tile_u4;
     uint4 *d = (uint4 *)pv.pages + tile_index(pv, layer, kv, dst, 0) * tile_u4;
-    const int n = tile_u4 * pv.H;
+    const int n = tile_u4 * pv.KVH;
     for (int i = threadIdx.x; i < n; i += blockDim.x) d[i] = s[i];
-    if (pv.scales && threadIdx.x < pv.H)
+    if (pv.scales && threadIdx.x < pv.KVH)
         pv.scales[tile_index(pv, layer, kv, dst, threadIdx.x)] = pv.scales[tile_index(pv, layer, kv, src, threadIdx.x)];
 }
 
@@ -651,7 +669,7 @@ __global__ void k_rows_io(PoolView pv, int sid, int layer, int kv, int slot0, vo
     const int slot = slot0 + s;
     const int page = pv.tables[(size_t)sid * pv.mbps + (slot >> 4)];
     if (page < 0 || page >= pv.NB) return;
-    const int per_head = row_u4 / pv.H;
+    const int per_head = row_u4 / pv.KVH;
     for (int i = threadIdx.x; i < row_u4; i += blockDim.x) {
         const int h = i / per_head, w = i % per_head;
         uint4 *pg = (uint4 *)pv.pages + tile_index(pv, layer, kv, page, h) * (kBlock * per_head) + (slot & 15) * per_head + w;
@@ -661,10 +679,10 @@ __global__ void k_rows_io(PoolView pv, int sid, int layer, int kv, int slot0, vo
         else
             *rw = *pg;
     }
-    if (scales && ((slot & 15) == 0 || s == 0) && threadIdx.x < pv.H) {
+    if (scales && ((slot & 15) == 0 || s == 0) && threadIdx.x < pv.KVH) {
         const int bi = (slot >> 4) - (slot0 >> 4);
         float *ps = pv.scales + tile_index(pv, layer, kv, page, threadIdx.x);
-        float *us = scales + (size_t)bi * pv.H + threadIdx.x;
+        float *us = scales + (size_t)bi * pv.KVH + threadIdx.x;
         if (write)
             *ps = *us;
         else
@@ -676,7 +694,7 @@ hipError_t launch_rows_io(const PoolView &pv, int sid, int layer, int kv, int sl
                           float *scales, bool write, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
     const int es = pv.cache_dt == DT_F32 ? 4 : pv.cache_dt == DT_BF16 ? 2 : 1;
-    const int row_u4 = pv.H * kHeadDim * es / 16;
+    const int row_u4 = pv.KVH * kHeadDim * es / 16;
     hipLaunchKernelGGL(k_rows_io, dim3(n), dim3(256), 0, stream, pv, sid, layer, kv, slot0, rows,
                        pv.cache_dt == DT_I8 ? scales : nullptr, write ? 1 : 0, row_u4);
     return hipGetLastError();
@@ -690,7 +708,8 @@ hipError_t launch_rows_io(const PoolView &pv, int sid, int layer, int kv, int sl
 // row is one coalesced 256 B read.  Rows past n in the last page are left as they are.
 template <int CDT>
 __global__ __launch_bounds__(64) void k_load_kv(PoolView pv, int sid, int layer, const float *kv, int n) {
-    const int b = blockIdx.x, h = blockIdx.y, which = blockIdx.z, lane = threadIdx.x;
+    const int b = blockIdx.x, j = blockIdx.y, which = blockIdx.z, lane = threadIdx.x;
+    const int h = j * (pv.H / pv.KVH); // the voice repeats kv head j over its group's query heads
     const int page = pv.tables[(size_t)sid * pv.mbps + b];
     if (page < 0 || page >= pv.NB) return;
     const int rows = min(kBlock, n - b * kBlock);
@@ -700,7 +719,7 @@ __global__ __launch_bounds__(64) void k_load_kv(PoolView pv, int sid, int layer,
         const int slot = b * kBlock + min(r, rows - 1);
         x[r] = kv[(((size_t)which * n + slot) * pv.H + h) * kHeadDim + lane];
     }
-    const size_t tile = tile_index(pv, layer, which, page, h);
+    const size_t tile = tile_index(pv, layer, which, page, j);
     if constexpr (CDT == DT_F32) {
         float *pg = (float *)pv.pages + tile * (kBlock * kHeadDim);
 #pragma unroll
@@ -729,7 +748,7 @@ __global__ __launch_bounds__(64) void k_load_kv(PoolView pv, int sid, int layer,
 
 hipError_t launch_load_kv(const PoolView &pv, int sid, int layer, const float *kv, int n, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
-    const dim3 grid((n + kBlock - 1) / kBlock, pv.H, 2);
+    const dim3 grid((n + kBlock - 1) / kBlock, pv.KVH, 2);
     switch (pv.cache_dt) {
     case DT_F32: hipLaunchKernelGGL(k_load_kv<DT_F32>, grid, dim3(64), 0, stream, pv, sid, layer, kv, n); break;
     case DT_BF16: hipLaunchKernelGGL(k_load_kv<DT_BF16>, grid, dim3(64), 0, stream, pv, sid, layer, kv, n); break;
@@ -806,9 +825,9 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, l16 = lane & 15;
     const int c0 = P.write_slot; // slot (= position) of prompt row 0
     const int kvh = h / (pv.H / pv.KVH);
-    const size_t page_elems = (size_t)pv.H * kBlock * kHeadDim;
-    uint16_t *kpages = (uint16_t *)pv.pages + tile_index(pv, layer, 0, 0, h) * (kBlock * kHeadDim);
-    uint16_t *vpages = (uint16_t *)pv.pages + tile_index(pv, layer, 1, 0, h) * (kBlock * kHeadDim);
+    const size_t page_elems = (size_t)pv.KVH * kBlock * kHeadDim;
+    uint16_t *kpages = (uint16_t *)pv.pages + tile_index(pv, layer, 0, 0, kvh) * (kBlock * kHeadDim);
+    uint16_t *vpages = (uint16_t *)pv.pages + tile_index(pv, layer, 1, 0, kvh) * (kBlock * kHeadDim);
     // the stream's page ids for every key any round sees, read once
     for (int i = tid; i < min((c0 + t + kBlock - 1) / kBlock, kPfMaxPages); i += 64 * kPfWaves) spages[i] = tab[i];
     // this thread's share of a chunk: 16 bytes (8 dims) of one key's K and V

@@ -410,7 +410,8 @@ extern "C" xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out)
     };
     hipError_t e = hipSetDevice(d.device);
     if (e != hipSuccess) return dev_fail(e, "hipSetDevice");
-    const size_t page_elems = (size_t)d.num_heads * kBlock * d.head_dim;
+    // a page holds the num_kv_heads heads a layer stores, not the repeated query heads
+    const size_t page_elems = (size_t)d.num_kv_heads * kBlock * d.head_dim;
     const size_t page_bytes = page_elems * p->esz;
     const size_t pages_bytes = page_bytes * d.num_blocks * 2 * d.num_layers;
     struct {
@@ -419,7 +420,7 @@ extern "C" xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out)
         const char *what;
     } allocs[] = {
         {&p->pages, pages_bytes, "pages"},
-        {(void **)&p->scales, d.cache_dtype == XNP_I8 ? sizeof(float) * d.num_heads * (size_t)d.num_blocks * 2 * d.num_layers : 0, "scales"},
+        {(void **)&p->scales, d.cache_dtype == XNP_I8 ? sizeof(float) * d.num_kv_heads * (size_t)d.num_blocks * 2 * d.num_layers : 0, "scales"},
         {(void **)&p->tables, sizeof(int32_t) * (size_t)d.max_streams * d.max_blocks_per_stream, "block tables"},
         {(void **)&p->rope, sizeof(float2) * p->rope_host.size(), "rope table"},
         {(void **)&p->rope16, d.act_dtype == XNP_BF16 ? sizeof(uint32_t) * p->rope_host.size() : 0, "bf16 rope table"},
@@ -435,7 +436,7 @@ extern "C" xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out)
     e = hipMemset(p->tables, 0xff, sizeof(int32_t) * (size_t)d.max_streams * d.max_blocks_per_stream);
     if (e != hipSuccess) return dev_fail(e, "table init");
     if (p->scales) {
-        e = hipMemset(p->scales, 0, sizeof(float) * d.num_heads * (size_t)d.num_blocks * 2 * d.num_layers);
+        e = hipMemset(p->scales, 0, sizeof(float) * d.num_kv_heads * (size_t)d.num_blocks * 2 * d.num_layers);
         if (e != hipSuccess) return dev_fail(e, "scale init");
     }
     e = hipMemcpy(p->rope, p->rope_host.data(), sizeof(float2) * p->rope_host.size(), hipMemcpyHostToDevice);
@@ -990,6 +991,8 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
     if (t > 1 && windows && windows != n)
         return fail(XNP_E_INVALID, "a step of %d rows holds window caches only, or none", t);
     const bool wsteps = t > 1 && windows; // one decode per row, each over its own records
+    if (wsteps && pool->d.cache_dtype == XNP_I8 && pool->d.num_kv_heads < pool->d.num_heads)
+        return fail(XNP_E_INVALID, "an int8 window cache with grouped heads takes one row a step");
     if (need > (int)pool->free_pages.size())
         return fail(XNP_E_OUT_OF_BLOCKS, "out of blocks: %d needed, %d free", need, (int)pool->free_pages.size());
 
@@ -1228,7 +1231,11 @@ extern "C" xnp_status xnp_attend(xnp_pool *pool, int32_t layer, const void *q, c
     if (pool->batch.n > 0 && (!q || !k || !v || !out)) return fail(XNP_E_INVALID, "null q, k, v or out");
     const LaunchTiming tm = pool->timing;
     pool->timing = LaunchTiming();
-    HIP_TRY(launch_decode(pool->view(), pool->batch.bv, layer, q, k, v, out, scale, true, pool->batch.stream, tm),
+    // grouped heads: every query head of a group would append its kv head's row; on an int8 pool,
+    // whose append rewrites the page, one kernel appends first and the decode only reads
+    const bool fuse = !(pool->d.cache_dtype == XNP_I8 && pool->d.num_kv_heads < pool->d.num_heads);
+    if (!fuse) HIP_TRY(launch_append(pool->view(), pool->batch.bv, layer, k, v, pool->batch.stream), "append");
+    HIP_TRY(launch_decode(pool->view(), pool->batch.bv, layer, q, k, v, out, scale, fuse, pool->batch.stream, tm),
             "attend");
     return XNP_OK;
 }
