@@ -103,11 +103,12 @@ def bf16_np(a):
     return ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32).view(np.float32).reshape(a.shape)
 
 
-def decode_bytes(lens, elem=2):
-    """Bytes one layer's append + decode must move for streams with cached lengths `lens`."""
+def decode_bytes(lens, elem=2, kvh=H):
+    """Bytes one layer's append + decode must move for streams with cached lengths `lens`: each
+    stored kv head's K/V rows once (kvh of them), q and out for every query head."""
     lens = np.asarray(lens, np.int64)
-    kv = 2 * (lens + 1) * H * D * elem
-    fixed = (H * D * 2) * (1 + 2 + 1) + 2 * H * D * elem  # q, new k/v, out (bf16); append write
+    kv = 2 * (lens + 1) * kvh * D * elem
+    fixed = (H * D * 2) * 2 + (kvh * D * 2) * 2 + 2 * kvh * D * elem  # q, out; new k/v (bf16); append write
     table = 4 * ((lens + 1 + 15) // 16)
     return int((kv + fixed + table).sum())
 
@@ -197,22 +198,23 @@ def run_decode(args, xnp, torch):
     cap = args.max_len + total_steps + 1
     mbps = (cap + 15) // 16
     nblocks = int(sum((n + total_steps + 16) // 16 + 1 for n in lens)) + 16
-    pool = xnp.KvPool(num_layers=L, num_heads=H, num_blocks=nblocks, max_streams=S, max_blocks_per_stream=mbps,
-                      cache_dtype="bf16", act_dtype="bf16", max_pos=cap + 16, page_seed=SEED + 2,
-                      decode_split=args.split)
+    kvh = args.kv_heads or H
+    pool = xnp.KvPool(num_layers=L, num_heads=H, num_kv_heads=kvh, num_blocks=nblocks, max_streams=S,
+                      max_blocks_per_stream=mbps, cache_dtype="bf16", act_dtype="bf16", max_pos=cap + 16,
+                      page_seed=SEED + 2, decode_split=args.split)
     ids = [pool.init_state(cap) for _ in range(S)]
     gen = torch.Generator(device=dev).manual_seed(SEED + 3)
     maxn = int(lens.max())
     for layer in range(L):
         for kvi in (0, 1):
-            rows = torch.randn((maxn, H, D), generator=gen, device=dev).to(torch.bfloat16)
+            rows = torch.randn((maxn, kvh, D), generator=gen, device=dev).to(torch.bfloat16)
             for sid, n in zip(ids, lens):
                 if layer == 0 and kvi == 0:
                     pool.advance(sid, int(n))
                 pool.write_rows(sid, layer, kvi, 0, rows[:n])
     q = [torch.randn((S, H, D), generator=gen, device=dev).to(torch.bfloat16) for _ in range(L)]
-    k = [torch.randn((S, H, D), generator=gen, device=dev).to(torch.bfloat16) for _ in range(L)]
-    v = [torch.randn((S, H, D), generator=gen, device=dev).to(torch.bfloat16) for _ in range(L)]
+    k = [torch.randn((S, kvh, D), generator=gen, device=dev).to(torch.bfloat16) for _ in range(L)]
+    v = [torch.randn((S, kvh, D), generator=gen, device=dev).to(torch.bfloat16) for _ in range(L)]
     out = [torch.empty((S, H, D), dtype=torch.bfloat16, device=dev) for _ in range(L)]
     torch.cuda.synchronize()
     cur = lens.copy()
@@ -220,7 +222,7 @@ def run_decode(args, xnp, torch):
 
     def step(events):
         if events is not None:
-            bytes_timed[0] += decode_bytes(cur)  # the one launch this step times
+            bytes_timed[0] += decode_bytes(cur, kvh=kvh)  # the one launch this step times
             bytes_timed[1] += 1
         pool.begin(ids)
         for layer in range(L):
@@ -243,13 +245,15 @@ def run_decode(args, xnp, torch):
         with open(tpath) as f:
             tr = json.load(f)
         if tr.get("workload") == {"streams": S, "layers": L, "max_len": args.max_len, "steps": args.steps,
-                                  "warmup": args.warmup, "fixed_len": args.fixed_len, "split": args.split}:
+                                  "warmup": args.warmup, "fixed_len": args.fixed_len, "split": args.split} \
+                and kvh == H:
             traffic = int(tr["traffic_bytes_per_launch"])
     cpu = None if args.no_cpu else cpu_decode(L, lens, args.cpu_seconds)
+    grouped = "" if kvh == H else f", {kvh} kv heads stored (grouped query heads)"
     config = {"workload": f"batched paged decode attention + KV append: {S} streams, Phonon-40m layers "
-                          f"({L} x {H} heads x {D}), bf16 K/V in 16-position pages, shuffled block tables, "
-                          f"cache length U[1,{args.max_len}] growing one row per step",
-              "streams": S, "layers": L, "heads": H, "head_dim": D, "page": 16,
+                          f"({L} x {H} heads x {D}{grouped}), bf16 K/V in 16-position pages, shuffled block "
+                          f"tables, cache length U[1,{args.max_len}] growing one row per step",
+              "streams": S, "layers": L, "heads": H, "kv_heads": kvh, "head_dim": D, "page": 16,
               "mean_cached_len": round(float(cur.mean()) - (args.steps + 1) / 2.0, 1)}
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
@@ -787,6 +791,8 @@ def main():
     ap.add_argument("--fixed-len", type=int, default=0,
                     help="decode: every stream at this cached length instead of U[1, max-len] (a balance check)")
     ap.add_argument("--split", type=int, default=0, help="decode: waves per (stream, head): 1, 2, 4, 8 (0: default)")
+    ap.add_argument("--kv-heads", type=int, default=0,
+                    help="decode: kv heads stored (grouped query heads; 0: one per query head)")
     ap.add_argument("--prefill-streams", type=int, default=64)
     ap.add_argument("--prompt", type=int, default=256)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
