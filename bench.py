@@ -12,6 +12,7 @@
   records as the kernel starts and ends (hipExtLaunchKernel, via xnp_pool_time_next), on the
   stream the kernel runs on: one launch per timed step, layer s % 9 at step s (an event pair
   costs about 17 us of issue time, so timing all nine would slow the steps being measured).
+  step_ms: the median and 95th percentile of the step periods, from one event per step start.
 
 --workload prefill: prompt prefill, 64 streams x 256-position prompts, 9 layers, bf16, RoPE
   theta 10000, causal, K/V written into the pages.  Value: prompt positions/s.  Roofline: causal
@@ -120,8 +121,28 @@ def window_bytes(attended):
     return int((2 * a * H * D + 2 * H * 4 * pages + H * D * 2 * (1 + 2 + 1) + 2 * H * D + 4 * pages).sum())
 
 
+class StepMarks:
+    """A timing event recorded on the current stream at the start of every timed step and after the
+    last one: the steps' periods on the GPU's clock, whose median and 95th percentile go in the
+    line beside the wall-clock mean."""
+
+    def __init__(self, steps):
+        import torch
+        self.ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+        self.n = 0
+
+    def mark(self):
+        self.ev[self.n].record()
+        self.n += 1
+
+    def percentiles(self):
+        d = np.array([a.elapsed_time(b) for a, b in zip(self.ev[:self.n - 1], self.ev[1:self.n])])
+        return {"p50": round(float(np.percentile(d, 50)), 4), "p95": round(float(np.percentile(d, 95)), 4)}
+
+
 def timed_steps(step, steps, warmup, L, every=5):
-    """Run warmup then `steps` steps; wall ms per step, and the durations (ms) of the timed launches.
+    """Run warmup then `steps` steps; wall ms per step, the durations (ms) of the timed launches,
+    and the steps' p50 / p95 periods (StepMarks).
 
     Every `every`-th step times one launch, layer (s / every) % L, with HIP events its launch
     records around the kernel: a launch that records events issues more slowly (and the steps
@@ -135,22 +156,27 @@ def timed_steps(step, steps, warmup, L, every=5):
     timed = {s: (s // every) % L for s in range(0, steps, every)}
     ev = [[(hip.create(), hip.create()) if timed.get(s) == l else None for l in range(L)] if s in timed else None
           for s in range(steps)]
+    marks = StepMarks(steps)
     t0 = time.perf_counter()
     for s in range(steps):
+        marks.mark()
         step(ev[s])
+    marks.mark()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     kern = np.array([hip.elapsed_ms(*ev[s][timed[s]]) for s in timed])
     for pair in (p_ for s_ in ev if s_ is not None for p_ in s_ if p_ is not None):
         for e in pair:
             hip.destroy(e)
-    return (t1 - t0) * 1000.0 / steps, kern
+    return (t1 - t0) * 1000.0 / steps, kern, marks.percentiles()
 
 
-def line(metric, value, unit, args, ms, dtype, config, roofline, cpu, higher=True, extra=None):
+def line(metric, value, unit, args, ms, dtype, config, roofline, cpu, higher=True, extra=None, pct=None):
     out = {"metric": metric, "value": round(value, 1), "unit": unit, "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": higher, "scaling": "weak",
            "vs_baseline": None, "dtype": dtype, "data": "synthetic", "config": config}
+    if pct:
+        out["step_ms"] = pct
     if extra:
         out.update(extra)
     out["roofline"] = roofline
@@ -232,7 +258,7 @@ def run_decode(args, xnp, torch):
         pool.end()
         cur[:] += 1
 
-    ms, kern = timed_steps(step, args.steps, args.warmup, L)
+    ms, kern, pct = timed_steps(step, args.steps, args.warmup, L)
     avg_ms = float(kern.mean())
     bytes_per_launch = bytes_timed[0] / bytes_timed[1]  # every layer of a step moves the same bytes
     achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
@@ -260,7 +286,7 @@ def run_decode(args, xnp, torch):
             "kernel": "k_decode<bf16> (fused append + RoPE + decode), one launch per layer",
             "avg_kernel_us": round(avg_ms * 1000.0, 2), "bytes_per_launch": int(bytes_per_launch)}
     return line("frames/sec (audio-sec/sec) at 1024 streams; decode-attn HBM GB/s % peak", fps, "frames/s", args,
-                ms, "bf16", config, roof, cpu, extra={"audio_sec_per_sec": round(fps * 0.08, 1)})
+                ms, "bf16", config, roof, cpu, extra={"audio_sec_per_sec": round(fps * 0.08, 1)}, pct=pct)
 
 
 # ---- prompt prefill (configuration 3) ---------------------------------------------------------------
@@ -309,7 +335,7 @@ def run_prefill(args, xnp, torch):
             pool.close(sid)
             ids[i] = pool.init_state(T)
 
-    ms, kern = timed_steps(step, args.steps, args.warmup, L)
+    ms, kern, pct = timed_steps(step, args.steps, args.warmup, L)
     avg_ms = float(kern.mean())
     flops = 2.0 * D * T * (T + 1) * H * S
     tflops = flops / (avg_ms * 1e-3) / 1e12
@@ -332,7 +358,7 @@ def run_prefill(args, xnp, torch):
             "mfma": {"achieved": round(tflops, 2), "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4), "flops_per_launch": flops}}
     return line("prompt prefill positions/sec (64 streams x 256); MFMA TFLOP/s % peak", S * T / (ms / 1000.0),
-                "positions/s", args, ms, "bf16", config, roof, cpu)
+                "positions/s", args, ms, "bf16", config, roof, cpu, pct=pct)
 
 
 # ---- int8 sliding window (configuration 4) ------------------------------------------------------------
@@ -430,7 +456,7 @@ def run_window(args, xnp, torch):
         pool.end()
         written[:] += 1
 
-    ms, kern = timed_steps(step, args.steps, args.warmup, L)
+    ms, kern, pct = timed_steps(step, args.steps, args.warmup, L)
     avg_ms = float(kern.mean())
     bytes_per_launch = bytes_timed[0] / bytes_timed[1]  # every layer of a step moves the same bytes
     achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
@@ -445,7 +471,8 @@ def run_window(args, xnp, torch):
             "kernel": "k_decode<int8> (fused append + quantize + RoPE + dequant decode), one launch per layer",
             "avg_kernel_us": round(avg_ms * 1000.0, 2), "bytes_per_launch": int(bytes_per_launch)}
     return line("frames/sec, int8 KV sliding window (512) at 1024 streams; decode HBM GB/s % peak", fps,
-                "frames/s", args, ms, "int8", config, roof, cpu, extra={"audio_sec_per_sec": round(fps * 0.08, 1)})
+                "frames/s", args, ms, "int8", config, roof, cpu, extra={"audio_sec_per_sec": round(fps * 0.08, 1)},
+                pct=pct)
 
 
 # ---- the full per-frame layer step (configuration 5) ---------------------------------------------
@@ -549,7 +576,7 @@ def run_step(args, xnp, torch):
         pool.end()
         cur[:] += 1
 
-    ms, kern = timed_steps(step, args.steps, args.warmup, L)
+    ms, kern, pct = timed_steps(step, args.steps, args.warmup, L)
     avg_ms = float(kern.mean())
     bytes_per_launch = bytes_timed[0] / bytes_timed[1]  # every layer of a step moves the same bytes
     achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
@@ -569,7 +596,8 @@ def run_step(args, xnp, torch):
             "rest_of_layer_us": round(rest_ms * 1000.0, 2), "gemm_gop_per_layer": round(flops / 1e9, 2),
             "gemm_tops_upper_bound": round(flops / (rest_ms * 1e-3) / 1e12, 2)}
     return line("frames/sec, full per-frame layer step at 2048 streams; decode-attn HBM GB/s % peak", fps,
-                "frames/s", args, ms, "bf16", config, roof, cpu, extra={"audio_sec_per_sec": round(fps * 0.08, 1)})
+                "frames/s", args, ms, "bf16", config, roof, cpu, extra={"audio_sec_per_sec": round(fps * 0.08, 1)},
+                pct=pct)
 
 
 # ---- the batched frame: the q8 flow LM at 2048 streams ----------------------------------------------
@@ -643,9 +671,12 @@ def run_frame(args, xnp, torch):
             cur += 1
         stream.synchronize()
         bytes0 = decode_bytes(cur)
+        marks = StepMarks(args.steps)
         t0 = time.perf_counter()
         for _ in range(args.steps):
+            marks.mark()
             lm.step(ids, lat, noise, lat, eos, graph=True)
+        marks.mark()
         stream.synchronize()
         ms = (time.perf_counter() - t0) * 1000.0 / args.steps
         cur += args.steps
@@ -681,7 +712,8 @@ def run_frame(args, xnp, torch):
             "avg_kernel_us": round(avg_ms * 1000.0, 2), "bytes_per_launch": int(np.mean(bts)),
             "decode_share_of_frame": round(L * avg_ms / ms, 3)}
     return line("frames/sec, full batched flow-LM frame at 2048 streams (q8 transformer + flow net)", fps,
-                "frames/s", args, ms, "bf16", config, roof, cpu, extra={"audio_sec_per_sec": round(fps * 0.08, 1)})
+                "frames/s", args, ms, "bf16", config, roof, cpu, extra={"audio_sec_per_sec": round(fps * 0.08, 1)},
+                pct=marks.percentiles())
 
 
 # ---- the single-stream flow LM (configuration 1) ----------------------------------------------------
@@ -742,16 +774,26 @@ def run_flowlm(args, xnp, torch):
         stream.synchronize()
         prompt_ms = (time.perf_counter() - t0) * 1000.0
 
-        def frames_ms(first, count, graph):
+        def frames_ms(first, count, graph, marks=None):
             t = time.perf_counter()
             for f in range(first, first + count):
+                if marks:
+                    marks.mark()
                 lm.step([sid], None if f == 0 else lat, noise, lat, eos, graph=graph)
+            if marks:
+                marks.mark()
             stream.synchronize()
             return (time.perf_counter() - t) * 1000.0 / max(count, 1)
 
         frames_ms(0, args.warmup, True)
         ms = frames_ms(args.warmup, args.steps, True)  # the value: frames replayed from a recording
-        eager_ms = frames_ms(frames, min(args.steps, cap - 64 - frames), False)  # the same frames, launched
+        n_eager = min(args.steps, cap - 64 - frames)
+        eager_ms = frames_ms(frames, n_eager, False)  # the same frames, launched
+        # the frame periods' percentiles come from a replayed pass of their own: an event recorded
+        # between frames costs a visible share of a 0.2 ms frame at batch 1
+        n_pct = min(args.steps, cap - 64 - frames - n_eager)
+        marks = StepMarks(n_pct)
+        frames_ms(frames + n_eager, n_pct, True, marks)
     fps = 1000.0 / ms
     bytes_mean = np.mean([flow_bytes(cfg, 64 + f) for f in range(args.warmup, frames)])
     gbs = bytes_mean / (ms * 1e-3) / 1e9
@@ -774,7 +816,7 @@ def run_flowlm(args, xnp, torch):
                       "net (batch 1, bound by its chain of about 50 dependent kernels)",
             "bytes_per_frame": int(bytes_mean)}
     return line("frames/sec, single-stream flow LM (Phonon-31m shape, fp32)", fps, "frames/s", args, ms, "f32",
-                config, roof, cpu, extra=extra)
+                config, roof, cpu, extra=extra, pct=marks.percentiles() if n_pct >= 2 else None)
 
 
 def main():

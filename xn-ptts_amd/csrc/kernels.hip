@@ -354,15 +354,22 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
         float smax = s[0];
 #pragma unroll
         for (int p = 1; p < NP; ++p) smax = fmaxf(smax, s[p]);
+        // Lazy rescaling: the accumulators move to a new max only when some lane's max grew by
+        // more than 8 (log2 units).  Until then exponents are taken against the older max and
+        // stay below 2^8, and the final l and acc keep the same ratio.  Most pages skip the
+        // rescale, the branch being uniform over the wave.
         const float m_new = fmaxf(m, smax);
-        const float alpha = fast_exp2(m - m_new);
-        l *= alpha;
+        if (__any(m_new > m + 8.f)) {
+            const float alpha = fast_exp2(m - m_new);
+            l *= alpha;
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) acc[i] *= alpha;
-        if constexpr (CDT == DT_I8) vbias *= alpha;
+            for (int i = 0; i < DPL; ++i) acc[i] *= alpha;
+            if constexpr (CDT == DT_I8) vbias *= alpha;
+            m = m_new;
+        }
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-            const float e = fast_exp2(s[p] - m_new);
+            const float e = fast_exp2(s[p] - m);
             l += e;
             // an unseen row weighs 0, but its bytes may be anything (a page's unwritten rows
             // hold what the memory held before): zero them, since 0 * NaN would still be NaN
@@ -375,7 +382,6 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
 #pragma unroll
             for (int i = 0; i < DPL; ++i) acc[i] = __builtin_fmaf(ev, x[i], acc[i]);
         }
-        m = m_new;
     };
     auto load = [&](uint4 (&kr)[NP], uint4 (&vr)[NP], int j) {
         const int pg = __builtin_amdgcn_readlane(my_page, j);
