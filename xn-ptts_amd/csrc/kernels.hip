@@ -295,10 +295,21 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
 
     const int c = lane % LPR, g = lane / LPR;
     const char *qrow = (const char *)q + ((size_t)R.b * pv.H + h) * kHeadDim * AE;
+    // bf16 pages and queries: scores by v_dot2_f32_bf16 on packed bf16 pairs (the page words as
+    // they are, no unpacking), with the query's scale applied to each row's sum
+    constexpr bool DOT2 = CDT == DT_BF16 && ABF;
     float qw[DPL], qp[DPL];
-    rotated_q<DPL, ABF>(pv, qrow, c, R.pos, qmul, qw);
+    rotated_q<DPL, ABF>(pv, qrow, c, R.pos, DOT2 ? 1.f : qmul, qw);
     const bool two_q = PREFIX && R.prefix > 0; // PREFIX: some stream of the batch keeps a prefix
-    if (two_q) rotated_q<DPL, ABF>(pv, qrow, c, R.pos_pre, qmul, qp);
+    if (two_q) rotated_q<DPL, ABF>(pv, qrow, c, R.pos_pre, DOT2 ? 1.f : qmul, qp);
+    uint32_t qh[DPL / 2], ph[DPL / 2]; // DOT2: the rotated query's bf16 pairs
+    if constexpr (DOT2) {
+#pragma unroll
+        for (int i = 0; i < DPL / 2; ++i) {
+            qh[i] = (__float_as_uint(qw[2 * i]) >> 16) | (__float_as_uint(qw[2 * i + 1]) & 0xffff0000u);
+            ph[i] = (__float_as_uint(qp[2 * i]) >> 16) | (__float_as_uint(qp[2 * i + 1]) & 0xffff0000u);
+        }
+    }
     // int8: unpack hands out q + 128, so a dot product is sum(qw (q + 128)) - 128 sum(qw) and a
     // value accumulator carries -128 sum(e sv) on every dim (vbias, taken out after the loop)
     float qwsum = 0.f, qpsum = 0.f, vbias = 0.f;
@@ -332,23 +343,33 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
         float s[NP];
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-            float x[DPL];
-            unpack<CDT>(kr[p], x);
-            float dw = 0.f;
-#pragma unroll
-            for (int i = 0; i < DPL; ++i) dw = __builtin_fmaf(qw[i], x[i], dw);
-            if constexpr (CDT == DT_I8) dw = __builtin_fmaf(-128.f, qwsum, dw);
             const int r = g + RPP * p;
-            if (two_q && base + r < R.prefix) {
-                float dp = 0.f;
+            const bool pre = two_q && base + r < R.prefix; // a prefix row: the query at pos_pre
+            float dw = 0.f;
+            if constexpr (DOT2) {
+                const uint32_t *u = (const uint32_t *)&kr[p];
 #pragma unroll
-                for (int i = 0; i < DPL; ++i) dp = __builtin_fmaf(qp[i], x[i], dp);
-                if constexpr (CDT == DT_I8) dp = __builtin_fmaf(-128.f, qpsum, dp);
-                dw = dp;
+                for (int i = 0; i < DPL / 2; ++i)
+                    dw = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v_t, pre ? ph[i] : qh[i]),
+                                                         __builtin_bit_cast(bf16x2v_t, u[i]), dw, false);
+            } else {
+                float x[DPL];
+                unpack<CDT>(kr[p], x);
+#pragma unroll
+                for (int i = 0; i < DPL; ++i) dw = __builtin_fmaf(qw[i], x[i], dw);
+                if constexpr (CDT == DT_I8) dw = __builtin_fmaf(-128.f, qwsum, dw);
+                if (pre) {
+                    float dp = 0.f;
+#pragma unroll
+                    for (int i = 0; i < DPL; ++i) dp = __builtin_fmaf(qp[i], x[i], dp);
+                    if constexpr (CDT == DT_I8) dp = __builtin_fmaf(-128.f, qpsum, dp);
+                    dw = dp;
+                }
             }
 #pragma unroll
             for (int o = 1; o < LPR; o <<= 1) dw += __shfl_xor(dw, o);
             if constexpr (CDT == DT_I8) dw *= sk;
+            if constexpr (DOT2) dw *= qmul;
             s[p] = ((seen >> r) & 1u) ? dw : -INFINITY;
         }
         float smax = s[0];
@@ -372,9 +393,11 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
             const float e = fast_exp2(s[p] - m);
             l += e;
             // an unseen row weighs 0, but its bytes may be anything (a page's unwritten rows
-            // hold what the memory held before): zero them, since 0 * NaN would still be NaN
+            // hold what the memory held before): zero them, since 0 * NaN would still be NaN.
+            // int8 bytes always convert to finite values (scales start at 0 and are amax / 127),
+            // so int8 rows need no zeroing.
             const bool rs = (seen >> (g + RPP * p)) & 1u;
-            const uint4 vv = rs ? vr[p] : make_uint4(0, 0, 0, 0);
+            const uint4 vv = (CDT == DT_I8 || rs) ? vr[p] : make_uint4(0, 0, 0, 0);
             float x[DPL];
             unpack<CDT>(vv, x);
             const float ev = (CDT == DT_I8) ? e * sv : e;
