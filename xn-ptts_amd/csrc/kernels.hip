@@ -1228,8 +1228,8 @@ hipError_t launch_layer_norm(const void *x, int rows, int dim, const float *w, c
 // y = epilogue(s[n] * sum_k A[m][k] W[n][k]): A [M][K] bf16, W [N][K] int8 with one f32 scale per
 // output channel (row of W), the sum on v_mfma_f32_16x16x32_bf16 with W widened to bf16 exactly
 // (|q| <= 127).  One work group of 4 waves per 64 x 64 tile of y, each wave 32 x 32 (2 x 2 MFMA
-// tiles); K in chunks of 64 staged through LDS, double-buffered, the next chunk's loads in flight
-// while one is multiplied.  The product, plus the bias when given, is rounded to bf16 (the
+// tiles); K in chunks of 64 staged through LDS, double-buffered, with the loads of the next three
+// chunks in flight while one is multiplied.  The product, plus the bias when given, is rounded to bf16 (the
 // projection's output tensor), then: kStore writes it (column ranges may go to separate outputs:
 // q, k and v), kGelu* write gelu(y) rounded, kResidual adds y (times the layer scale, rounded,
 // when given) into X and rounds: X + layer_scale(linear(..)) as transformer.rs:612-633 does; the
@@ -1238,6 +1238,7 @@ hipError_t launch_layer_norm(const void *x, int rows, int dim, const float *w, c
 constexpr int kGmT = 64;  // tile rows and columns
 constexpr int kGmK = 64;  // K chunk
 constexpr int kGmLd = 72; // LDS row length in bf16
+constexpr int kGmPD = 3;  // K chunks of loads in flight
 
 template <int EPI, bool AF32>
 __global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K, const int8_t *W, const float *s,
@@ -1249,47 +1250,71 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, l16 = lane & 15;
     const int wm = w & 1, wn = w >> 1;
 
-    // staging: A rows a_r and a_r + 32, 8 bf16 at k 8 a_k; W row w_r, 16 int8 at k 16 w_k
+    // staging: A rows a_r and a_r + 32, 8 values at k 8 a_k; W row w_r, 16 int8 at k 16 w_k.
+    // kGmPD chunks of loads are in flight: set c % kGmPD holds chunk c from its load until it is
+    // written to LDS.  The words stay as loaded until then -- zeroing past K, rounding f32 A rows
+    // and widening W happen at the LDS store, since any use at the load would make the wave wait
+    // for it there.
     const int a_r = tid >> 3, a_k = tid & 7, w_r = tid >> 2, w_k = tid & 3;
     const int ar0 = min(m0 + a_r, M - 1), ar1 = min(m0 + a_r + 32, M - 1), wr = min(n0 + w_r, N - 1);
-    uint4 ra0, ra1, rw;
-    auto load = [&](int kc) {
+    constexpr int AW = AF32 ? 2 : 1; // uint4 per 8 A values
+    uint4 ra0[kGmPD][AW], ra1[kGmPD][AW], rw[kGmPD];
+    auto load = [&](int kc, int set) {
+        // past K (K % 16 == 0, so no 16-byte load straddles it): an in-bounds address, zeroed at
+        // the store
         const int k0 = kc * kGmK;
-        // past K (K % 16 == 0, so no 16-byte load straddles it): an in-bounds address, then zeros
-        const bool ain = k0 + 8 * a_k < K, win = k0 + 16 * w_k < K;
-        const int ka = ain ? k0 + 8 * a_k : 0, kw = win ? k0 + 16 * w_k : 0;
-        const uint4 z = make_uint4(0u, 0u, 0u, 0u);
-        uint4 l0, l1;
-        if constexpr (AF32) { // 8 f32 of each row, rounded to bf16 pairs
+        const int ka = k0 + 8 * a_k < K ? k0 + 8 * a_k : 0, kw = k0 + 16 * w_k < K ? k0 + 16 * w_k : 0;
+        if constexpr (AF32) {
             const float *af = (const float *)A;
-            const float4 a0 = *(const float4 *)(af + (size_t)ar0 * K + ka), a1 = *(const float4 *)(af + (size_t)ar0 * K + ka + 4);
-            const float4 b0 = *(const float4 *)(af + (size_t)ar1 * K + ka), b1 = *(const float4 *)(af + (size_t)ar1 * K + ka + 4);
-            l0 = make_uint4(pack_bf16(a0.x, a0.y), pack_bf16(a0.z, a0.w), pack_bf16(a1.x, a1.y), pack_bf16(a1.z, a1.w));
-            l1 = make_uint4(pack_bf16(b0.x, b0.y), pack_bf16(b0.z, b0.w), pack_bf16(b1.x, b1.y), pack_bf16(b1.z, b1.w));
+            ra0[set][0] = *(const uint4 *)(af + (size_t)ar0 * K + ka);
+            ra0[set][AW - 1] = *(const uint4 *)(af + (size_t)ar0 * K + ka + 4);
+            ra1[set][0] = *(const uint4 *)(af + (size_t)ar1 * K + ka);
+            ra1[set][AW - 1] = *(const uint4 *)(af + (size_t)ar1 * K + ka + 4);
         } else {
-            l0 = *(const uint4 *)(A + (size_t)ar0 * K + ka);
-            l1 = *(const uint4 *)(A + (size_t)ar1 * K + ka);
+            ra0[set][0] = *(const uint4 *)(A + (size_t)ar0 * K + ka);
+            ra1[set][0] = *(const uint4 *)(A + (size_t)ar1 * K + ka);
         }
-        const uint4 lw = *(const uint4 *)(W + (size_t)wr * K + kw);
-        ra0 = ain ? l0 : z;
-        ra1 = ain ? l1 : z;
-        rw = win ? lw : z;
+        rw[set] = *(const uint4 *)(W + (size_t)wr * K + kw);
     };
-    auto store = [&](int buf) {
-        *(uint4 *)&As[buf][a_r][8 * a_k] = ra0;
-        *(uint4 *)&As[buf][a_r + 32][8 * a_k] = ra1;
-        const uint32_t *u = (const uint32_t *)&rw;
-        uint32_t p[8];
+    auto masked = [](const uint4 &u, uint32_t m) { return make_uint4(u.x & m, u.y & m, u.z & m, u.w & m); };
+    auto bf16_row = [&](const uint4 (&u)[AW]) { // 8 A values as bf16 pairs
+        if constexpr (AF32) {
+            return make_uint4(pack_bf16(__uint_as_float(u[0].x), __uint_as_float(u[0].y)),
+                              pack_bf16(__uint_as_float(u[0].z), __uint_as_float(u[0].w)),
+                              pack_bf16(__uint_as_float(u[AW - 1].x), __uint_as_float(u[AW - 1].y)),
+                              pack_bf16(__uint_as_float(u[AW - 1].z), __uint_as_float(u[AW - 1].w)));
+        } else {
+            return u[0];
+        }
+    };
+    auto widen2 = [](uint32_t u, int sh) { // two int8 -> a bf16 pair (exact: |q| <= 127)
+        return pack_bf16((float)(int8_t)((u >> sh) & 0xffu), (float)(int8_t)((u >> (sh + 8)) & 0xffu));
+    };
+    auto store = [&](int buf, int set, int kc) {
+        uint4 a0 = bf16_row(ra0[set]), a1 = bf16_row(ra1[set]), wq = rw[set];
+        if ((kc + 1) * kGmK > K) { // the chunk reaches past K (uniform over the group)
+            const int k0 = kc * kGmK;
+            const uint32_t ma = k0 + 8 * a_k < K ? ~0u : 0u, mw = k0 + 16 * w_k < K ? ~0u : 0u;
+            a0 = masked(a0, ma);
+            a1 = masked(a1, ma);
+            wq = masked(wq, mw);
+        }
+        *(uint4 *)&As[buf][a_r][8 * a_k] = a0;
+        *(uint4 *)&As[buf][a_r + 32][8 * a_k] = a1;
+        *(uint4 *)&Ws[buf][w_r][16 * w_k] = make_uint4(widen2(wq.x, 0), widen2(wq.x, 16), widen2(wq.y, 0), widen2(wq.y, 16));
+        *(uint4 *)&Ws[buf][w_r][16 * w_k + 8] =
+            make_uint4(widen2(wq.z, 0), widen2(wq.z, 16), widen2(wq.w, 0), widen2(wq.w, 16));
+    };
+
+    // the epilogue's per-column operands, loaded before the loop so that they arrive with it
+    float sc[2], bn[2], lsn[2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float q0 = (float)(int8_t)(u[i] & 0xffu), q1 = (float)(int8_t)((u[i] >> 8) & 0xffu);
-            const float q2 = (float)(int8_t)((u[i] >> 16) & 0xffu), q3 = (float)(int8_t)(u[i] >> 24);
-            p[2 * i] = pack_bf16(q0, q1);
-            p[2 * i + 1] = pack_bf16(q2, q3);
-        }
-        *(uint4 *)&Ws[buf][w_r][16 * w_k] = make_uint4(p[0], p[1], p[2], p[3]);
-        *(uint4 *)&Ws[buf][w_r][16 * w_k + 8] = make_uint4(p[4], p[5], p[6], p[7]);
-    };
+    for (int ni = 0; ni < 2; ++ni) {
+        const int n = min(n0 + 32 * wn + 16 * ni + l16, N - 1);
+        sc[ni] = s[n];
+        bn[ni] = go.bias ? go.bias[n] : 0.f;
+        lsn[ni] = (EPI == kResidual && go.ls) ? go.ls[n] : 1.f;
+    }
 
     f32x4_t acc[2][2];
 #pragma unroll
@@ -1298,28 +1323,37 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K
         for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     const int nk = (K + kGmK - 1) / kGmK;
-    load(0);
-    store(0);
+    load(0, 0);
+#pragma unroll
+    for (int c = 1; c < kGmPD; ++c)
+        if (c < nk) load(c, c);
+    store(0, 0, 0);
     __syncthreads();
-    for (int kc = 0; kc < nk; ++kc) {
-        const int buf = kc & 1;
-        if (kc + 1 < nk) load(kc + 1);
+    for (int kb = 0; kb < nk; kb += kGmPD) {
 #pragma unroll
-        for (int ks = 0; ks < kGmK / 32; ++ks) {
-            bf16x8_t a[2], bw[2];
+        for (int u = 0; u < kGmPD; ++u) { // set indices stay constants
+            const int kc = kb + u;
+            if (kc >= nk) break;
+            const int buf = kc & 1;
+            if (kc + kGmPD < nk) load(kc + kGmPD, u); // set u held chunk kc, already in LDS
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                a[i] = as_bf16x8(*(const uint4 *)&As[buf][32 * wm + 16 * i + l16][32 * ks + 8 * g]);
-                bw[i] = as_bf16x8(*(const uint4 *)&Ws[buf][32 * wn + 16 * i + l16][32 * ks + 8 * g]);
+            for (int ks = 0; ks < kGmK / 32; ++ks) {
+                bf16x8_t a[2], bw[2];
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    a[i] = as_bf16x8(*(const uint4 *)&As[buf][32 * wm + 16 * i + l16][32 * ks + 8 * g]);
+                    bw[i] = as_bf16x8(*(const uint4 *)&Ws[buf][32 * wn + 16 * i + l16][32 * ks + 8 * g]);
+                }
+#pragma unroll
+                for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                    for (int ni = 0; ni < 2; ++ni)
+                        acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mi], bw[ni], acc[mi][ni], 0, 0, 0);
             }
-#pragma unroll
-            for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-                for (int ni = 0; ni < 2; ++ni)
-                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mi], bw[ni], acc[mi][ni], 0, 0, 0);
+            // buffer buf ^ 1's last readers finished before the previous barrier
+            if (kc + 1 < nk) store(buf ^ 1, (u + 1) % kGmPD, kc + 1);
+            __syncthreads();
         }
-        if (kc + 1 < nk) store(buf ^ 1); // its last readers finished before the previous barrier
-        __syncthreads();
     }
 
     // lane: column n0 + 32 wn + 16 ni + l16, rows m0 + 32 wm + 16 mi + 4 g + r
@@ -1327,20 +1361,17 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K
     for (int ni = 0; ni < 2; ++ni) {
         const int n = n0 + 32 * wn + 16 * ni + l16;
         if (n >= N) continue;
-        const float sc = s[n];
-        const float bn = go.bias ? go.bias[n] : 0.f;
         int seg = 0;
         if constexpr (EPI == kStore) {
             if (go.nseg > 1 && n >= go.col0[1]) seg = (go.nseg > 2 && n >= go.col0[2]) ? 2 : 1;
         }
-        const float lsn = (EPI == kResidual && go.ls) ? go.ls[n] : 1.f;
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = m0 + 32 * wm + 16 * mi + 4 * g + r;
                 if (m >= M) continue;
-                const float y = bf16_value(bf16_bits(go.bias ? acc[mi][ni][r] * sc + bn : acc[mi][ni][r] * sc));
+                const float y = bf16_value(bf16_bits(go.bias ? acc[mi][ni][r] * sc[ni] + bn[ni] : acc[mi][ni][r] * sc[ni]));
                 if constexpr (EPI == kStore) {
                     ((uint16_t *)go.out[seg])[(size_t)m * go.ld[seg] + (n - go.col0[seg])] = (uint16_t)bf16_bits(y);
                 } else if constexpr (EPI == kGeluErf || EPI == kGeluTanh) {
@@ -1353,7 +1384,7 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K
                     }
                     ((uint16_t *)go.out[0])[(size_t)m * go.ld[0] + n] = (uint16_t)bf16_bits(gv);
                 } else if constexpr (EPI == kResidual) {
-                    const float a = go.ls ? bf16_value(bf16_bits(y * lsn)) : y;
+                    const float a = go.ls ? bf16_value(bf16_bits(y * lsn[ni])) : y;
                     uint16_t *xp = (uint16_t *)go.out[0] + (size_t)m * go.ld[0] + n;
                     *xp = (uint16_t)bf16_bits(bf16_value(*xp) + a);
                 } else if constexpr (EPI == kSilu) {
