@@ -38,6 +38,7 @@ CPU baseline: the oracle (the C restatement, OpenMP over streams) on a bounded s
 workload, timed on this host's cores.
 """
 import argparse
+import gc
 import importlib.util
 import json
 import os
@@ -121,6 +122,19 @@ def window_bytes(attended):
     return int((2 * a * H * D + 2 * H * 4 * pages + H * D * 2 * (1 + 2 + 1) + 2 * H * D + 4 * pages).sum())
 
 
+class NoGC:
+    """Python's cyclic garbage collector off over a timed region, collected just before: its pauses
+    belong to this harness, not to the path, and one landing inside a timed step leaves the GPU idle
+    for a millisecond or more."""
+
+    def __enter__(self):
+        gc.collect()
+        gc.disable()
+
+    def __exit__(self, *exc):
+        gc.enable()
+
+
 class StepMarks:
     """A timing event recorded on the current stream at the start of every timed step and after the
     last one: the steps' periods on the GPU's clock, whose median and 95th percentile go in the
@@ -157,13 +171,14 @@ def timed_steps(step, steps, warmup, L, every=5):
     ev = [[(hip.create(), hip.create()) if timed.get(s) == l else None for l in range(L)] if s in timed else None
           for s in range(steps)]
     marks = StepMarks(steps)
-    t0 = time.perf_counter()
-    for s in range(steps):
+    with NoGC():
+        t0 = time.perf_counter()
+        for s in range(steps):
+            marks.mark()
+            step(ev[s])
         marks.mark()
-        step(ev[s])
-    marks.mark()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
     kern = np.array([hip.elapsed_ms(*ev[s][timed[s]]) for s in timed])
     for pair in (p_ for s_ in ev if s_ is not None for p_ in s_ if p_ is not None):
         for e in pair:
@@ -672,12 +687,13 @@ def run_frame(args, xnp, torch):
         stream.synchronize()
         bytes0 = decode_bytes(cur)
         marks = StepMarks(args.steps)
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
+        with NoGC():
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                marks.mark()
+                lm.step(ids, lat, noise, lat, eos, graph=True)
             marks.mark()
-            lm.step(ids, lat, noise, lat, eos, graph=True)
-        marks.mark()
-        stream.synchronize()
+            stream.synchronize()
         ms = (time.perf_counter() - t0) * 1000.0 / args.steps
         cur += args.steps
         # the dominant kernel: layer 0's fused append + decode, timed by its launch's events over
@@ -775,15 +791,16 @@ def run_flowlm(args, xnp, torch):
         prompt_ms = (time.perf_counter() - t0) * 1000.0
 
         def frames_ms(first, count, graph, marks=None):
-            t = time.perf_counter()
-            for f in range(first, first + count):
+            with NoGC():
+                t = time.perf_counter()
+                for f in range(first, first + count):
+                    if marks:
+                        marks.mark()
+                    lm.step([sid], None if f == 0 else lat, noise, lat, eos, graph=graph)
                 if marks:
                     marks.mark()
-                lm.step([sid], None if f == 0 else lat, noise, lat, eos, graph=graph)
-            if marks:
-                marks.mark()
-            stream.synchronize()
-            return (time.perf_counter() - t) * 1000.0 / max(count, 1)
+                stream.synchronize()
+                return (time.perf_counter() - t) * 1000.0 / max(count, 1)
 
         frames_ms(0, args.warmup, True)
         ms = frames_ms(args.warmup, args.steps, True)  # the value: frames replayed from a recording

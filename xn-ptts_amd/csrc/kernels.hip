@@ -160,6 +160,30 @@ hipError_t launch_patch_tables(const PoolView &pv, const TablePatch *patches, in
     return hipGetLastError();
 }
 
+// The batch plan, read straight from the pinned staging buffer the host composed it in, and the
+// block-table patches staged behind it: one launch, where copies would take a copy engine per
+// part plus a patch kernel, with a hand-off between engines before each.  The launch boundary
+// makes the host's writes to the buffer visible.
+__global__ __launch_bounds__(256) void k_pull_plan(const uint4 *src, uint4 *dst, int n16, const TablePatch *patches,
+                                                   int np, int32_t *tables, int mbps) {
+    const int stride = gridDim.x * blockDim.x, i0 = blockIdx.x * blockDim.x + threadIdx.x;
+    for (int i = i0; i < n16; i += stride) dst[i] = src[i];
+    for (int i = i0; i < np; i += stride) {
+        const TablePatch t = patches[i];
+        tables[(size_t)t.sid * mbps + t.blk] = t.page;
+    }
+}
+
+hipError_t launch_pull_plan(const PoolView &pv, const void *src, void *dst, size_t bytes, const TablePatch *patches,
+                            int np, hipStream_t stream) {
+    const int n16 = (int)((bytes + 15) / 16), work = std::max(n16, np);
+    if (work <= 0) return hipSuccess;
+    const int blocks = std::min((work + 255) / 256, 1024);
+    hipLaunchKernelGGL(k_pull_plan, dim3(blocks), dim3(256), 0, stream, (const uint4 *)src, (uint4 *)dst, n16, patches,
+                       np, pv.tables, pv.mbps);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------------------------
 // standalone append of t rows per stream.  Work item = (stream, page the rows touch); one wave
 // per head walks the page's rows in order, since int8 rows of one page depend on each other.

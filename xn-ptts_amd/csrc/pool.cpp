@@ -80,7 +80,8 @@ constexpr int32_t kMaxWindowRows = 4;
 
 // A pinned host buffer an upload is composed in; reused once its copy has completed.
 struct Staging {
-    char *host = nullptr;
+    char *host = nullptr; // pinned
+    char *dev = nullptr;  // the same bytes as the device sees them
     hipEvent_t done = nullptr;
     bool pending = false;
 };
@@ -188,6 +189,16 @@ struct xnp_pool {
             s.pending = false;
         }
         *out = &s;
+        return XNP_OK;
+    }
+
+    // A batch plan (bytes at the start of s) into dst, with np table patches staged at o_patch:
+    // one kernel reads both from the pinned buffer.
+    xnp_status pull(Staging *s, char *dst, size_t bytes, size_t o_patch, int np, hipStream_t stream) {
+        HIP_TRY(launch_pull_plan(view(), s->dev, dst, bytes, (const TablePatch *)(s->dev + o_patch), np, stream),
+                "plan pull");
+        HIP_TRY(hipEventRecord(s->done, stream), "recording a plan pull");
+        s->pending = true;
         return XNP_OK;
     }
 
@@ -453,10 +464,13 @@ extern "C" xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out)
         e = hipMemcpy(p->rope16, packed.data(), sizeof(uint32_t) * packed.size(), hipMemcpyHostToDevice);
         if (e != hipSuccess) return dev_fail(e, "bf16 rope table upload");
     }
-    const size_t stage_bytes = std::max(p->batch_bytes, p->aux_bytes);
+    // a plan with the table patches behind it, or an aux upload
+    const size_t stage_bytes = p->batch_bytes + p->aux_bytes;
     for (auto &s : p->stage) {
         e = hipHostMalloc((void **)&s.host, stage_bytes, hipHostMallocDefault);
         if (e != hipSuccess) return dev_fail(e, "pinned staging");
+        e = hipHostGetDevicePointer((void **)&s.dev, s.host, 0);
+        if (e != hipSuccess) return dev_fail(e, "pinned staging's device address");
         e = hipEventCreateWithFlags(&s.done, hipEventDisableTiming);
         if (e != hipSuccess) return dev_fail(e, "staging event");
     }
@@ -1068,7 +1082,11 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
     };
     hipError_t he = hipSetDevice(pool->d.device);
     if (he != hipSuccess) return undo(hip_fail(he, "hipSetDevice"));
-    if (xnp_status st = pool->flush_patches(hs)) return undo(st);
+    // the table patches ride behind the plan when they fit (a step takes a few pages), so one
+    // kernel pulls both; a longer list goes ahead by itself
+    pool->coalesce_patches();
+    if (pool->patches.size() * sizeof(TablePatch) > pool->aux_bytes)
+        if (xnp_status st = pool->flush_patches(hs)) return undo(st);
     Staging *sg;
     if (xnp_status st = pool->stage_acquire(&sg)) return undo(st);
     const size_t o_plans = 0;
@@ -1123,7 +1141,11 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
                 std::memcpy(dst + sizeof R, st.blocks.data(), sizeof(int32_t) * R.nblk);
             }
     std::memcpy(sg->host + o_masks, masks.data(), sizeof(uint32_t) * masks.size());
-    if (xnp_status st = pool->upload(sg, pool->dbatch, total, hs)) return undo(st);
+    const size_t o_patch = pool->batch_bytes;
+    const int np = (int)pool->patches.size();
+    std::memcpy(sg->host + o_patch, pool->patches.data(), sizeof(TablePatch) * np);
+    if (xnp_status st = pool->pull(sg, pool->dbatch, total, o_patch, np, hs)) return undo(st);
+    pool->patches.clear();
     B.bv.plans = (const StreamPlan *)(pool->dbatch + o_plans);
     B.bv.recs = pool->dbatch + o_recs;
     B.bv.rec_stride = pool->rec_stride;

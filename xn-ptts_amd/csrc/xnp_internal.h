@@ -88,6 +88,10 @@ bool pool_host_only(const xnp_pool *p);
 // Launchers (kernels.hip).  All asynchronous on `stream`; return the launch status.
 hipError_t launch_patch_tables(const PoolView &pv, const TablePatch *patches, int n,
                                hipStream_t stream);
+// Copies `bytes` (rounded up to 16) from src, a device view of pinned host memory, to dst, and
+// applies np table patches read from host memory too: a batch plan's upload in one launch.
+hipError_t launch_pull_plan(const PoolView &pv, const void *src, void *dst, size_t bytes, const TablePatch *patches,
+                            int np, hipStream_t stream);
 hipError_t launch_append(const PoolView &pv, const BatchView &bv, int layer, const void *k,
                          const void *v, hipStream_t stream);
 hipError_t launch_decode(const PoolView &pv, const BatchView &bv, int layer, const void *q,
