@@ -1264,23 +1264,27 @@ constexpr int kGmK = 64;  // K chunk
 constexpr int kGmLd = 72; // LDS row length in bf16
 constexpr int kGmPD = 3;  // K chunks of loads in flight
 
-template <int EPI, bool AF32>
+// MI: 16-row MFMA tiles per wave in M, so tiles of 32 MI rows.  MI = 1 doubles the work groups of a
+// narrow projection (N = 512 at 2048 rows gives 256 groups of 64 rows: one wave per SIMD).
+template <int EPI, bool AF32, int MI>
 __global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K, const int8_t *W, const float *s,
                                                  int N, GemmOut go) {
-    __shared__ __attribute__((aligned(16))) uint16_t As[2][kGmT][kGmLd];
+    constexpr int BM = 32 * MI;
+    __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][kGmLd];
     __shared__ __attribute__((aligned(16))) uint16_t Ws[2][kGmT][kGmLd];
     const int ntn = (N + kGmT - 1) / kGmT;
-    const int m0 = (blockIdx.x / ntn) * kGmT, n0 = (blockIdx.x % ntn) * kGmT;
+    const int m0 = (blockIdx.x / ntn) * BM, n0 = (blockIdx.x % ntn) * kGmT;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, l16 = lane & 15;
     const int wm = w & 1, wn = w >> 1;
 
-    // staging: A rows a_r and a_r + 32, 8 values at k 8 a_k; W row w_r, 16 int8 at k 16 w_k.
+    // staging: A rows a_r (and a_r + 32 when MI = 2), 8 values at k 8 a_k; W row w_r, 16 int8 at
+    // k 16 w_k.
     // kGmPD chunks of loads are in flight: set c % kGmPD holds chunk c from its load until it is
     // written to LDS.  The words stay as loaded until then -- zeroing past K, rounding f32 A rows
     // and widening W happen at the LDS store, since any use at the load would make the wave wait
     // for it there.
     const int a_r = tid >> 3, a_k = tid & 7, w_r = tid >> 2, w_k = tid & 3;
-    const int ar0 = min(m0 + a_r, M - 1), ar1 = min(m0 + a_r + 32, M - 1), wr = min(n0 + w_r, N - 1);
+    const int ar0 = min(m0 + a_r, M - 1), ar1 = min(m0 + a_r + 32 * (MI - 1), M - 1), wr = min(n0 + w_r, N - 1);
     constexpr int AW = AF32 ? 2 : 1; // uint4 per 8 A values
     uint4 ra0[kGmPD][AW], ra1[kGmPD][AW], rw[kGmPD];
     auto load = [&](int kc, int set) {
@@ -1292,11 +1296,13 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K
             const float *af = (const float *)A;
             ra0[set][0] = *(const uint4 *)(af + (size_t)ar0 * K + ka);
             ra0[set][AW - 1] = *(const uint4 *)(af + (size_t)ar0 * K + ka + 4);
-            ra1[set][0] = *(const uint4 *)(af + (size_t)ar1 * K + ka);
-            ra1[set][AW - 1] = *(const uint4 *)(af + (size_t)ar1 * K + ka + 4);
+            if constexpr (MI == 2) {
+                ra1[set][0] = *(const uint4 *)(af + (size_t)ar1 * K + ka);
+                ra1[set][AW - 1] = *(const uint4 *)(af + (size_t)ar1 * K + ka + 4);
+            }
         } else {
             ra0[set][0] = *(const uint4 *)(A + (size_t)ar0 * K + ka);
-            ra1[set][0] = *(const uint4 *)(A + (size_t)ar1 * K + ka);
+            if constexpr (MI == 2) ra1[set][0] = *(const uint4 *)(A + (size_t)ar1 * K + ka);
         }
         rw[set] = *(const uint4 *)(W + (size_t)wr * K + kw);
     };
@@ -1315,7 +1321,8 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K
         return pack_bf16((float)(int8_t)((u >> sh) & 0xffu), (float)(int8_t)((u >> (sh + 8)) & 0xffu));
     };
     auto store = [&](int buf, int set, int kc) {
-        uint4 a0 = bf16_row(ra0[set]), a1 = bf16_row(ra1[set]), wq = rw[set];
+        uint4 a0 = bf16_row(ra0[set]), a1 = a0, wq = rw[set];
+        if constexpr (MI == 2) a1 = bf16_row(ra1[set]);
         if ((kc + 1) * kGmK > K) { // the chunk reaches past K (uniform over the group)
             const int k0 = kc * kGmK;
             const uint32_t ma = k0 + 8 * a_k < K ? ~0u : 0u, mw = k0 + 16 * w_k < K ? ~0u : 0u;
@@ -1324,7 +1331,7 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K
             wq = masked(wq, mw);
         }
         *(uint4 *)&As[buf][a_r][8 * a_k] = a0;
-        *(uint4 *)&As[buf][a_r + 32][8 * a_k] = a1;
+        if constexpr (MI == 2) *(uint4 *)&As[buf][a_r + 32][8 * a_k] = a1;
         *(uint4 *)&Ws[buf][w_r][16 * w_k] = make_uint4(widen2(wq.x, 0), widen2(wq.x, 16), widen2(wq.y, 0), widen2(wq.y, 16));
         *(uint4 *)&Ws[buf][w_r][16 * w_k + 8] =
             make_uint4(widen2(wq.z, 0), widen2(wq.z, 16), widen2(wq.w, 0), widen2(wq.w, 16));
@@ -1340,9 +1347,9 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K
         lsn[ni] = (EPI == kResidual && go.ls) ? go.ls[n] : 1.f;
     }
 
-    f32x4_t acc[2][2];
+    f32x4_t acc[MI][2];
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
+    for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
@@ -1362,14 +1369,15 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K
             if (kc + kGmPD < nk) load(kc + kGmPD, u); // set u held chunk kc, already in LDS
 #pragma unroll
             for (int ks = 0; ks < kGmK / 32; ++ks) {
-                bf16x8_t a[2], bw[2];
+                bf16x8_t a[MI], bw[2];
 #pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    a[i] = as_bf16x8(*(const uint4 *)&As[buf][32 * wm + 16 * i + l16][32 * ks + 8 * g]);
+                for (int i = 0; i < MI; ++i)
+                    a[i] = as_bf16x8(*(const uint4 *)&As[buf][16 * MI * wm + 16 * i + l16][32 * ks + 8 * g]);
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
                     bw[i] = as_bf16x8(*(const uint4 *)&Ws[buf][32 * wn + 16 * i + l16][32 * ks + 8 * g]);
-                }
 #pragma unroll
-                for (int mi = 0; mi < 2; ++mi)
+                for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
                     for (int ni = 0; ni < 2; ++ni)
                         acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mi], bw[ni], acc[mi][ni], 0, 0, 0);
@@ -1380,7 +1388,7 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K
         }
     }
 
-    // lane: column n0 + 32 wn + 16 ni + l16, rows m0 + 32 wm + 16 mi + 4 g + r
+    // lane: column n0 + 32 wn + 16 ni + l16, rows m0 + 16 MI wm + 16 mi + 4 g + r
 #pragma unroll
     for (int ni = 0; ni < 2; ++ni) {
         const int n = n0 + 32 * wn + 16 * ni + l16;
@@ -1390,10 +1398,10 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K
             if (go.nseg > 1 && n >= go.col0[1]) seg = (go.nseg > 2 && n >= go.col0[2]) ? 2 : 1;
         }
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
+        for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int m = m0 + 32 * wm + 16 * mi + 4 * g + r;
+                const int m = m0 + 16 * MI * wm + 16 * mi + 4 * g + r;
                 if (m >= M) continue;
                 const float y = bf16_value(bf16_bits(go.bias ? acc[mi][ni][r] * sc[ni] + bn[ni] : acc[mi][ni][r] * sc[ni]));
                 if constexpr (EPI == kStore) {
@@ -1431,16 +1439,15 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K
     }
 }
 
-hipError_t launch_gemm_q8(const void *A, int M, int K, const int8_t *W, const float *s, int N, int epi,
-                          const GemmOut &go, hipStream_t stream) {
-    if (M <= 0) return hipSuccess;
-    if (N <= 0 || K <= 0 || K % 16) return hipErrorInvalidValue;
-    const dim3 grid(((N + kGmT - 1) / kGmT) * ((M + kGmT - 1) / kGmT)), block(256);
+template <int MI>
+static hipError_t gemm_q8_mi(const void *A, int M, int K, const int8_t *W, const float *s, int N, int epi,
+                             const GemmOut &go, hipStream_t stream) {
+    const dim3 grid(((N + kGmT - 1) / kGmT) * ((M + 32 * MI - 1) / (32 * MI))), block(256);
     const uint16_t *a = (const uint16_t *)A;
-#define XNP_GEMM(E) hipLaunchKernelGGL((k_gemm_q8<E, false>), grid, block, 0, stream, a, M, K, W, s, N, go)
+#define XNP_GEMM(E) hipLaunchKernelGGL((k_gemm_q8<E, false, MI>), grid, block, 0, stream, a, M, K, W, s, N, go)
     if (go.a_f32) {
         if (epi != kStore) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((k_gemm_q8<kStore, true>), grid, block, 0, stream, a, M, K, W, s, N, go);
+        hipLaunchKernelGGL((k_gemm_q8<kStore, true, MI>), grid, block, 0, stream, a, M, K, W, s, N, go);
         return hipGetLastError();
     }
     switch (epi) {
@@ -1457,6 +1464,16 @@ hipError_t launch_gemm_q8(const void *A, int M, int K, const int8_t *W, const fl
     }
 #undef XNP_GEMM
     return hipGetLastError();
+}
+
+hipError_t launch_gemm_q8(const void *A, int M, int K, const int8_t *W, const float *s, int N, int epi,
+                          const GemmOut &go, hipStream_t stream) {
+    if (M <= 0) return hipSuccess;
+    if (N <= 0 || K <= 0 || K % 16) return hipErrorInvalidValue;
+    // 32-row tiles when 64-row ones would leave the chip's 1024 SIMDs under two waves each
+    const int64_t groups64 = (int64_t)((N + kGmT - 1) / kGmT) * ((M + kGmT - 1) / kGmT);
+    return groups64 < 512 ? gemm_q8_mi<1>(A, M, K, W, s, N, epi, go, stream)
+                          : gemm_q8_mi<2>(A, M, K, W, s, N, epi, go, stream);
 }
 
 // ---------------------------------------------------------------------------------------------
