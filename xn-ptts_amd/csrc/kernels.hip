@@ -276,21 +276,23 @@ __device__ __forceinline__ void rotated_q(const PoolView &pv, const void *qrow, 
     }
 }
 
-// One query row of one head against pages [0, R.nblk) of its stream, by a group of SPLIT waves:
-// the body of the decode kernel and of the prompt-row kernel.  `pages` lists the stream's page
-// ids by logical block (a decode record's copy, or the block table).
-template <int CDT, bool ABF, int SPLIT, bool PREFIX>
+// One query row of GQ query heads h .. h + GQ - 1 (all of one kv head) against pages
+// [0, R.nblk) of its stream, by a group of SPLIT waves: the body of the decode kernel and of the
+// prompt-row kernel.  `pages` lists the stream's page ids by logical block (a decode record's
+// copy, or the block table).  With GQ > 1 each page is read once for the GQ heads: K is unpacked
+// (or taken by dot2) once per row, V once, and each head keeps its own online softmax.
+template <int CDT, bool ABF, int SPLIT, bool PREFIX, int GQ = 1>
 __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView &bv, int layer, const StreamRec &R,
                                             const int32_t *rec_pages, int h, const void *q, const void *knew,
                                             const void *vnew, void *out, float qmul, int fused) {
     using LN = Lanes<CDT>;
     constexpr int DPL = LN::DPL, LPR = LN::LPR, RPP = LN::RPP, NP = LN::NP, DEPTH = LN::DEPTH;
     constexpr int AE = ABF ? 2 : 4;
-    __shared__ float part[SPLIT][kPartStride];
+    __shared__ float part[SPLIT][GQ][kPartStride];
 
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int nb = R.nblk > w ? (R.nblk - w + SPLIT - 1) / SPLIT : 0; // this wave's pages
-    const int kvh = h / (pv.H / pv.KVH);                               // the tiles query head h reads
+    const int kvh = h / (pv.H / pv.KVH);                               // the tiles the heads read
 
     // Per-page metadata, lane j holding page w + j * SPLIT: page id, seen rows, int8 scales.
     // Past the wave's last page the lanes hold page 0 with no row seen.
@@ -318,31 +320,35 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
     }
 
     const int c = lane % LPR, g = lane / LPR;
-    const char *qrow = (const char *)q + ((size_t)R.b * pv.H + h) * kHeadDim * AE;
     // bf16 pages and queries: scores by v_dot2_f32_bf16 on packed bf16 pairs (the page words as
     // they are, no unpacking), with the query's scale applied to each row's sum
     constexpr bool DOT2 = CDT == DT_BF16 && ABF;
-    float qw[DPL], qp[DPL];
-    rotated_q<DPL, ABF>(pv, qrow, c, R.pos, DOT2 ? 1.f : qmul, qw);
     const bool two_q = PREFIX && R.prefix > 0; // PREFIX: some stream of the batch keeps a prefix
-    if (two_q) rotated_q<DPL, ABF>(pv, qrow, c, R.pos_pre, DOT2 ? 1.f : qmul, qp);
-    uint32_t qh[DPL / 2], ph[DPL / 2]; // DOT2: the rotated query's bf16 pairs
-    if constexpr (DOT2) {
-#pragma unroll
-        for (int i = 0; i < DPL / 2; ++i) {
-            qh[i] = (__float_as_uint(qw[2 * i]) >> 16) | (__float_as_uint(qw[2 * i + 1]) & 0xffff0000u);
-            ph[i] = (__float_as_uint(qp[2 * i]) >> 16) | (__float_as_uint(qp[2 * i + 1]) & 0xffff0000u);
-        }
-    }
+    float qw[GQ][DPL], qp[GQ][DPL];
+    uint32_t qh[GQ][DPL / 2], ph[GQ][DPL / 2]; // DOT2: the rotated queries' bf16 pairs
     // int8: unpack hands out q + 128, so a dot product is sum(qw (q + 128)) - 128 sum(qw) and a
     // value accumulator carries -128 sum(e sv) on every dim (vbias, taken out after the loop)
-    float qwsum = 0.f, qpsum = 0.f, vbias = 0.f;
-    if constexpr (CDT == DT_I8) {
+    float qwsum[GQ], qpsum[GQ], vbias[GQ];
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) qwsum += qw[i];
-        if (two_q) {
+    for (int e = 0; e < GQ; ++e) {
+        const char *qrow = (const char *)q + ((size_t)R.b * pv.H + h + e) * kHeadDim * AE;
+        rotated_q<DPL, ABF>(pv, qrow, c, R.pos, DOT2 ? 1.f : qmul, qw[e]);
+        if (two_q) rotated_q<DPL, ABF>(pv, qrow, c, R.pos_pre, DOT2 ? 1.f : qmul, qp[e]);
+        if constexpr (DOT2) {
 #pragma unroll
-            for (int i = 0; i < DPL; ++i) qpsum += qp[i];
+            for (int i = 0; i < DPL / 2; ++i) {
+                qh[e][i] = (__float_as_uint(qw[e][2 * i]) >> 16) | (__float_as_uint(qw[e][2 * i + 1]) & 0xffff0000u);
+                ph[e][i] = (__float_as_uint(qp[e][2 * i]) >> 16) | (__float_as_uint(qp[e][2 * i + 1]) & 0xffff0000u);
+            }
+        }
+        qwsum[e] = qpsum[e] = vbias[e] = 0.f;
+        if constexpr (CDT == DT_I8) {
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) qwsum[e] += qw[e][i];
+            if (two_q) {
+#pragma unroll
+                for (int i = 0; i < DPL; ++i) qpsum[e] += qp[e][i];
+            }
         }
     }
 
@@ -350,10 +356,14 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
     const uint4 *vbase = (const uint4 *)((const char *)pv.pages + tile_index(pv, layer, 1, 0, kvh) * (kBlock * kHeadDim * esize<CDT>()));
     const size_t page_u4 = (size_t)pv.KVH * (kBlock * kHeadDim * esize<CDT>() / 16);
 
-    float m = -1e30f, l = 0.f;
-    float acc[DPL];
+    float m[GQ], l[GQ], acc[GQ][DPL];
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
+    for (int e = 0; e < GQ; ++e) {
+        m[e] = -1e30f;
+        l[e] = 0.f;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) acc[e][i] = 0.f;
+    }
 
     // One page's scores and softmax/accumulator update from its K and V registers.
     auto process = [&](const uint4 (&kr)[NP], const uint4 (&vr)[NP], int j) {
@@ -364,58 +374,76 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
             sk = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(my_sk), j));
             sv = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(my_sv), j));
         }
-        float s[NP];
+        float s[GQ][NP];
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
             const int r = g + RPP * p;
-            const bool pre = two_q && base + r < R.prefix; // a prefix row: the query at pos_pre
-            float dw = 0.f;
+            const bool pre = two_q && base + r < R.prefix; // a prefix row: the queries at pos_pre
+            float dw[GQ];
             if constexpr (DOT2) {
                 const uint32_t *u = (const uint32_t *)&kr[p];
 #pragma unroll
-                for (int i = 0; i < DPL / 2; ++i)
-                    dw = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v_t, pre ? ph[i] : qh[i]),
-                                                         __builtin_bit_cast(bf16x2v_t, u[i]), dw, false);
+                for (int e = 0; e < GQ; ++e) {
+                    dw[e] = 0.f;
+#pragma unroll
+                    for (int i = 0; i < DPL / 2; ++i)
+                        dw[e] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v_t, pre ? ph[e][i] : qh[e][i]),
+                                                                __builtin_bit_cast(bf16x2v_t, u[i]), dw[e], false);
+                }
             } else {
                 float x[DPL];
                 unpack<CDT>(kr[p], x);
 #pragma unroll
-                for (int i = 0; i < DPL; ++i) dw = __builtin_fmaf(qw[i], x[i], dw);
-                if constexpr (CDT == DT_I8) dw = __builtin_fmaf(-128.f, qwsum, dw);
-                if (pre) {
-                    float dp = 0.f;
+                for (int e = 0; e < GQ; ++e) {
+                    dw[e] = 0.f;
 #pragma unroll
-                    for (int i = 0; i < DPL; ++i) dp = __builtin_fmaf(qp[i], x[i], dp);
-                    if constexpr (CDT == DT_I8) dp = __builtin_fmaf(-128.f, qpsum, dp);
-                    dw = dp;
+                    for (int i = 0; i < DPL; ++i) dw[e] = __builtin_fmaf(qw[e][i], x[i], dw[e]);
+                    if constexpr (CDT == DT_I8) dw[e] = __builtin_fmaf(-128.f, qwsum[e], dw[e]);
+                    if (pre) {
+                        float dp = 0.f;
+#pragma unroll
+                        for (int i = 0; i < DPL; ++i) dp = __builtin_fmaf(qp[e][i], x[i], dp);
+                        if constexpr (CDT == DT_I8) dp = __builtin_fmaf(-128.f, qpsum[e], dp);
+                        dw[e] = dp;
+                    }
                 }
             }
 #pragma unroll
-            for (int o = 1; o < LPR; o <<= 1) dw += __shfl_xor(dw, o);
-            if constexpr (CDT == DT_I8) dw *= sk;
-            if constexpr (DOT2) dw *= qmul;
-            s[p] = ((seen >> r) & 1u) ? dw : -INFINITY;
-        }
-        float smax = s[0];
+            for (int e = 0; e < GQ; ++e) {
 #pragma unroll
-        for (int p = 1; p < NP; ++p) smax = fmaxf(smax, s[p]);
+                for (int o = 1; o < LPR; o <<= 1) dw[e] += __shfl_xor(dw[e], o);
+                if constexpr (CDT == DT_I8) dw[e] *= sk;
+                if constexpr (DOT2) dw[e] *= qmul;
+                s[e][p] = ((seen >> r) & 1u) ? dw[e] : -INFINITY;
+            }
+        }
         // Lazy rescaling: the accumulators move to a new max only when some lane's max grew by
         // more than 8 (log2 units).  Until then exponents are taken against the older max and
         // stay below 2^8, and the final l and acc keep the same ratio.  Most pages skip the
         // rescale, the branch being uniform over the wave.
-        const float m_new = fmaxf(m, smax);
-        if (__any(m_new > m + 8.f)) {
-            const float alpha = fast_exp2(m - m_new);
-            l *= alpha;
+        float m_new[GQ];
+        bool grow = false;
 #pragma unroll
-            for (int i = 0; i < DPL; ++i) acc[i] *= alpha;
-            if constexpr (CDT == DT_I8) vbias *= alpha;
-            m = m_new;
+        for (int e = 0; e < GQ; ++e) {
+            float smax = s[e][0];
+#pragma unroll
+            for (int p = 1; p < NP; ++p) smax = fmaxf(smax, s[e][p]);
+            m_new[e] = fmaxf(m[e], smax);
+            grow |= m_new[e] > m[e] + 8.f;
+        }
+        if (__any(grow)) {
+#pragma unroll
+            for (int e = 0; e < GQ; ++e) {
+                const float alpha = fast_exp2(m[e] - m_new[e]);
+                l[e] *= alpha;
+#pragma unroll
+                for (int i = 0; i < DPL; ++i) acc[e][i] *= alpha;
+                if constexpr (CDT == DT_I8) vbias[e] *= alpha;
+                m[e] = m_new[e];
+            }
         }
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-            const float e = fast_exp2(s[p] - m);
-            l += e;
             // an unseen row weighs 0, but its bytes may be anything (a page's unwritten rows
             // hold what the memory held before): zero them, since 0 * NaN would still be NaN.
             // int8 bytes always convert to finite values (scales start at 0 and are amax / 127),
@@ -424,10 +452,15 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
             const uint4 vv = (CDT == DT_I8 || rs) ? vr[p] : make_uint4(0, 0, 0, 0);
             float x[DPL];
             unpack<CDT>(vv, x);
-            const float ev = (CDT == DT_I8) ? e * sv : e;
-            if constexpr (CDT == DT_I8) vbias += ev;
 #pragma unroll
-            for (int i = 0; i < DPL; ++i) acc[i] = __builtin_fmaf(ev, x[i], acc[i]);
+            for (int e = 0; e < GQ; ++e) {
+                const float pe = fast_exp2(s[e][p] - m[e]);
+                l[e] += pe;
+                const float ev = (CDT == DT_I8) ? pe * sv : pe;
+                if constexpr (CDT == DT_I8) vbias[e] += ev;
+#pragma unroll
+                for (int i = 0; i < DPL; ++i) acc[e][i] = __builtin_fmaf(ev, x[i], acc[e][i]);
+            }
         }
     };
     auto load = [&](uint4 (&kr)[NP], uint4 (&vr)[NP], int j) {
@@ -462,7 +495,7 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
         const int slot = R.write_slot;
         const size_t arow = (size_t)R.b * pv.KVH + kvh;
         const bool fresh = (R.flags & 1) ? (R.flags & 2) != 0 : ((slot & 15) == 0);
-        // with grouped heads every query head of the group writes the same row (the same bytes);
+        // with grouped heads every work group of the kv head writes the same row (the same bytes);
         // int8 pools append in a kernel of their own first, since their append rewrites the page
         append_row_wave<CDT, ABF>(pv, layer, __builtin_amdgcn_readlane(my_page, wj), slot & 15, kvh, R.key_pos,
                                   (const char *)knew + arow * kHeadDim * AE, (const char *)vnew + arow * kHeadDim * AE,
@@ -487,64 +520,71 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
         }
     }
 
-    if constexpr (CDT == DT_I8) {
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) acc[i] = __builtin_fmaf(-128.f, vbias, acc[i]);
-    }
-    // Merge the row groups: lanes c, c + LPR, c + 2 LPR, ... hold the same dims.
+    for (int e = 0; e < GQ; ++e) {
+        if constexpr (CDT == DT_I8) {
 #pragma unroll
-    for (int o = LPR; o < 64; o <<= 1) {
-        const float mo = __shfl_xor(m, o), lo = __shfl_xor(l, o);
-        const float mn = fmaxf(m, mo);
-        const float a = fast_exp2(m - mn), bb = fast_exp2(mo - mn);
-        l = l * a + lo * bb;
-#pragma unroll
-        for (int i = 0; i < DPL; ++i) {
-            const float ao = __shfl_xor(acc[i], o);
-            acc[i] = acc[i] * a + ao * bb;
+            for (int i = 0; i < DPL; ++i) acc[e][i] = __builtin_fmaf(-128.f, vbias[e], acc[e][i]);
         }
-        m = mn;
-    }
-    // Merge the waves through LDS; wave 0 writes the head's output, lane d owning dim d.
-    if (g == 0) {
+        // Merge the row groups: lanes c, c + LPR, c + 2 LPR, ... hold the same dims.
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) part[w][c * DPL + i] = acc[i];
-        if (lane == 0) {
-            part[w][64] = m;
-            part[w][65] = l;
+        for (int o = LPR; o < 64; o <<= 1) {
+            const float mo = __shfl_xor(m[e], o), lo = __shfl_xor(l[e], o);
+            const float mn = fmaxf(m[e], mo);
+            const float a = fast_exp2(m[e] - mn), bb = fast_exp2(mo - mn);
+            l[e] = l[e] * a + lo * bb;
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) {
+                const float ao = __shfl_xor(acc[e][i], o);
+                acc[e][i] = acc[e][i] * a + ao * bb;
+            }
+            m[e] = mn;
+        }
+        // the waves' shares of head h + e go through LDS
+        if (g == 0) {
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) part[w][e][c * DPL + i] = acc[e][i];
+            if (lane == 0) {
+                part[w][e][64] = m[e];
+                part[w][e][65] = l[e];
+            }
         }
     }
     __syncthreads();
     if (w != 0) return;
-    float M = -1e30f;
+    // wave 0 writes the heads' outputs, lane d owning dim d
 #pragma unroll
-    for (int k = 0; k < SPLIT; ++k) M = fmaxf(M, part[k][64]);
-    float L = 0.f, A = 0.f;
+    for (int e = 0; e < GQ; ++e) {
+        float M = -1e30f;
 #pragma unroll
-    for (int k = 0; k < SPLIT; ++k) {
-        const float a = fast_exp2(part[k][64] - M);
-        L = __builtin_fmaf(part[k][65], a, L);
-        A = __builtin_fmaf(part[k][lane], a, A);
+        for (int k = 0; k < SPLIT; ++k) M = fmaxf(M, part[k][e][64]);
+        float L = 0.f, A = 0.f;
+#pragma unroll
+        for (int k = 0; k < SPLIT; ++k) {
+            const float a = fast_exp2(part[k][e][64] - M);
+            L = __builtin_fmaf(part[k][e][65], a, L);
+            A = __builtin_fmaf(part[k][e][lane], a, A);
+        }
+        const float r = A / L;
+        const size_t o = ((size_t)R.b * pv.H + h + e) * kHeadDim + lane;
+        if constexpr (ABF)
+            ((uint16_t *)out)[o] = (uint16_t)bf16_bits(r);
+        else
+            ((float *)out)[o] = r;
     }
-    const float r = A / L;
-    const size_t o = ((size_t)R.b * pv.H + h) * kHeadDim + lane;
-    if constexpr (ABF)
-        ((uint16_t *)out)[o] = (uint16_t)bf16_bits(r);
-    else
-        ((float *)out)[o] = r;
 }
 
-// Decode: one work group per (stream, head), streams longest first.  The stream record carries
-// everything the group needs, its page ids included.
-template <int CDT, bool ABF, int SPLIT, bool PREFIX>
+// Decode: one work group per (stream, GQ query heads of one kv head), streams longest first.  The
+// stream record carries everything the group needs, its page ids included.
+template <int CDT, bool ABF, int SPLIT, bool PREFIX, int GQ>
 __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(Lanes<CDT>::WAVES))) void k_decode(
     PoolView pv, BatchView bv, int layer, const void *q, const void *knew, const void *vnew, void *out, float qmul,
     int fused) {
-    // Work groups go to the 8 XCDs in turn (group b to XCD b % 8).  The G = H / KVH query heads
-    // of one (stream, kv head) read the same tiles: in runs of 8 G groups, XCD x takes the G heads
+    // Work groups go to the 8 XCDs in turn (group b to XCD b % 8).  The G = H / (KVH GQ) groups
+    // of one (stream, kv head) read the same tiles: in runs of 8 G groups, XCD x takes the G groups
     // of pair x of the run, one after another, so their reads meet in that XCD's L2.  With G = 1
-    // this is group b -> (record b / H, head b % H).
-    const int G = pv.H / pv.KVH, b = blockIdx.x;
+    // this is group b -> (record b / (H / GQ), heads GQ (b % (H / GQ)) ..).
+    const int G = pv.H / (pv.KVH * GQ), b = blockIdx.x;
     const int full = bv.n * pv.KVH / 8 * 8; // (stream, kv head) pairs in whole runs
     int pair, gi;
     if (b < full * G) {
@@ -556,8 +596,8 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(Lane
     }
     const char *rec = bv.recs + (size_t)(pair / pv.KVH) * bv.rec_stride;
     const StreamRec R = *(const StreamRec *)rec;
-    attend_core<CDT, ABF, SPLIT, PREFIX>(pv, bv, layer, R, (const int32_t *)(rec + sizeof(StreamRec)),
-                                         pair % pv.KVH * G + gi, q, knew, vnew, out, qmul, fused);
+    attend_core<CDT, ABF, SPLIT, PREFIX, GQ>(pv, bv, layer, R, (const int32_t *)(rec + sizeof(StreamRec)),
+                                             (pair % pv.KVH * G + gi) * GQ, q, knew, vnew, out, qmul, fused);
 }
 
 // Prompt rows (transformer.rs:231-248), after k_append has written all t rows: row i of a stream
@@ -609,15 +649,21 @@ hipError_t launch_append(const PoolView &pv, const BatchView &bv, int layer, con
     }
 }
 
-template <int CDT, bool ABF>
+int decode_heads_per_group(const PoolView &pv) {
+    // two query heads of one kv head share a group's page reads; int8 keeps one (its registers
+    // hold no second head at four waves per SIMD)
+    return pv.cache_dt != DT_I8 && (pv.H / pv.KVH) % 2 == 0 ? 2 : 1;
+}
+
+template <int CDT, bool ABF, int GQ>
 static hipError_t decode_impl(const PoolView &pv, const BatchView &bv, int layer, const void *q, const void *k,
                               const void *v, void *out, float scale, bool fused, hipStream_t stream,
                               const LaunchTiming &tm) {
     const float qmul = scale * 1.4426950408889634f;
-    const dim3 grid(bv.n * pv.H);
+    const dim3 grid(bv.n * pv.H / GQ);
     const int f = fused ? 1 : 0;
 #define XNP_DECODE(S, PFX)                                                                                          \
-    XNP_LAUNCH((k_decode<CDT, ABF, S, PFX>), grid, dim3(64 * S), stream, tm, pv, bv, layer, q, k, v, out, qmul, f)
+    XNP_LAUNCH((k_decode<CDT, ABF, S, PFX, GQ>), grid, dim3(64 * S), stream, tm, pv, bv, layer, q, k, v, out, qmul, f)
     if (bv.prefix) {
         switch (bv.split) {
         case 1: XNP_DECODE(1, true); break;
@@ -644,10 +690,16 @@ hipError_t launch_decode(const PoolView &pv, const BatchView &bv, int layer, con
                          const LaunchTiming &tm) {
     if (bv.n == 0) return hipSuccess;
     switch (pv.cache_dt * 2 + pv.act_dt) {
-    case DT_F32 * 2 + DT_F32: return decode_impl<DT_F32, false>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
-    case DT_BF16 * 2 + DT_BF16: return decode_impl<DT_BF16, true>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
-    case DT_I8 * 2 + DT_BF16: return decode_impl<DT_I8, true>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
-    case DT_I8 * 2 + DT_F32: return decode_impl<DT_I8, false>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
+    case DT_F32 * 2 + DT_F32:
+        return decode_heads_per_group(pv) == 2
+                   ? decode_impl<DT_F32, false, 2>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm)
+                   : decode_impl<DT_F32, false, 1>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
+    case DT_BF16 * 2 + DT_BF16:
+        return decode_heads_per_group(pv) == 2
+                   ? decode_impl<DT_BF16, true, 2>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm)
+                   : decode_impl<DT_BF16, true, 1>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
+    case DT_I8 * 2 + DT_BF16: return decode_impl<DT_I8, true, 1>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
+    case DT_I8 * 2 + DT_F32: return decode_impl<DT_I8, false, 1>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
     default: return hipErrorInvalidValue;
     }
 }
