@@ -240,8 +240,11 @@ def test_grouped_heads_store_a_kv_head_once():
     assert pages_bytes(8) - pages_bytes(2) == 6 * page
 
 
-@pytest.mark.parametrize("cache,act,mode", [("bf16", "bf16", "shift"), ("i8", "bf16", "absolute")])
+@pytest.mark.parametrize("cache,act,mode", [("bf16", "bf16", "shift"), ("i8", "bf16", "absolute"),
+                                            ("bf16", "bf16", "absolute"), ("f32", "f32", "absolute")])
 def test_grouped_heads_on_rings(cache, act, mode):
+    # 4 query heads per kv head; an absolute ring's prefix gives the batch a second query position,
+    # with which bf16 and f32 decode take two heads per work group instead of four
     p = Pair(cache=cache, act=act, H=8, KVH=2, streams=2, cap=48, seed=31)
     context = 20
     for i in range(2):

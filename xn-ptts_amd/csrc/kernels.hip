@@ -649,10 +649,13 @@ hipError_t launch_append(const PoolView &pv, const BatchView &bv, int layer, con
     }
 }
 
-int decode_heads_per_group(const PoolView &pv) {
-    // two query heads of one kv head share a group's page reads; int8 keeps one (its registers
-    // hold no second head at four waves per SIMD)
-    return pv.cache_dt != DT_I8 && (pv.H / pv.KVH) % 2 == 0 ? 2 : 1;
+int decode_heads_per_group(const PoolView &pv, bool prefix) {
+    // query heads of one kv head share a group's page reads: four when four divide the group and
+    // no stream of the batch keeps a ring prefix (whose second query would spill them), else two;
+    // int8 keeps one (its registers hold no second head at four waves per SIMD)
+    const int G = pv.H / pv.KVH;
+    if (pv.cache_dt == DT_I8) return 1;
+    return G % 4 == 0 && !prefix ? 4 : G % 2 == 0 ? 2 : 1;
 }
 
 template <int CDT, bool ABF, int GQ>
@@ -665,12 +668,16 @@ static hipError_t decode_impl(const PoolView &pv, const BatchView &bv, int layer
 #define XNP_DECODE(S, PFX)                                                                                          \
     XNP_LAUNCH((k_decode<CDT, ABF, S, PFX, GQ>), grid, dim3(64 * S), stream, tm, pv, bv, layer, q, k, v, out, qmul, f)
     if (bv.prefix) {
-        switch (bv.split) {
-        case 1: XNP_DECODE(1, true); break;
-        case 2: XNP_DECODE(2, true); break;
-        case 4: XNP_DECODE(4, true); break;
-        case 8: XNP_DECODE(8, true); break;
-        default: return hipErrorInvalidValue;
+        if constexpr (GQ >= 4) {
+            return hipErrorInvalidValue; // four heads per group are built without a prefix
+        } else {
+            switch (bv.split) {
+            case 1: XNP_DECODE(1, true); break;
+            case 2: XNP_DECODE(2, true); break;
+            case 4: XNP_DECODE(4, true); break;
+            case 8: XNP_DECODE(8, true); break;
+            default: return hipErrorInvalidValue;
+            }
         }
     } else {
         switch (bv.split) {
@@ -691,13 +698,17 @@ hipError_t launch_decode(const PoolView &pv, const BatchView &bv, int layer, con
     if (bv.n == 0) return hipSuccess;
     switch (pv.cache_dt * 2 + pv.act_dt) {
     case DT_F32 * 2 + DT_F32:
-        return decode_heads_per_group(pv) == 2
-                   ? decode_impl<DT_F32, false, 2>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm)
-                   : decode_impl<DT_F32, false, 1>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
+        switch (decode_heads_per_group(pv, bv.prefix != 0)) {
+        case 4: return decode_impl<DT_F32, false, 4>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
+        case 2: return decode_impl<DT_F32, false, 2>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
+        default: return decode_impl<DT_F32, false, 1>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
+        }
     case DT_BF16 * 2 + DT_BF16:
-        return decode_heads_per_group(pv) == 2
-                   ? decode_impl<DT_BF16, true, 2>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm)
-                   : decode_impl<DT_BF16, true, 1>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
+        switch (decode_heads_per_group(pv, bv.prefix != 0)) {
+        case 4: return decode_impl<DT_BF16, true, 4>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
+        case 2: return decode_impl<DT_BF16, true, 2>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
+        default: return decode_impl<DT_BF16, true, 1>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
+        }
     case DT_I8 * 2 + DT_BF16: return decode_impl<DT_I8, true, 1>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
     case DT_I8 * 2 + DT_F32: return decode_impl<DT_I8, false, 1>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
     default: return hipErrorInvalidValue;

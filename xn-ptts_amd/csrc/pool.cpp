@@ -1152,12 +1152,13 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
     // unless the caller fixed the split: a batch of few (stream, head) groups fills few CUs, so give
     // each group more waves (a larger split only raises the pages a group can index) until the batch
     // has about one wave per SIMD
-    B.bv.split = pool->split;
-    const int64_t groups = (int64_t)n * t * pool->d.num_heads / (t == 1 ? decode_heads_per_group(pool->view()) : 1);
-    while (!pool->d.decode_split && B.bv.split < 8 && groups * B.bv.split < 1024)
-        B.bv.split *= 2;
     B.bv.prefix = 0;
     for (int32_t i = 0; i < n; i++) B.bv.prefix |= plans[i].prefix > 0;
+    B.bv.split = pool->split;
+    const int gq = t == 1 ? decode_heads_per_group(pool->view(), B.bv.prefix != 0) : 1;
+    const int64_t groups = (int64_t)n * t * pool->d.num_heads / gq;
+    while (!pool->d.decode_split && B.bv.split < 8 && groups * B.bv.split < 1024)
+        B.bv.split *= 2;
     B.bv.masks = (const uint32_t *)(pool->dbatch + o_masks);
     B.bv.n = n;
     B.bv.t = t;

@@ -94,9 +94,10 @@ hipError_t launch_pull_plan(const PoolView &pv, const void *src, void *dst, size
                             int np, hipStream_t stream);
 hipError_t launch_append(const PoolView &pv, const BatchView &bv, int layer, const void *k,
                          const void *v, hipStream_t stream);
-// Query heads one decode work group covers (all of one kv head): 2 when a pool stores grouped
-// heads in a bf16 or f32 cache with an even group, else 1.
-int decode_heads_per_group(const PoolView &pv);
+// Query heads one decode work group covers (all of one kv head), for a pool that stores grouped
+// heads in a bf16 or f32 cache: 4 when 4 divide the group and the batch keeps no ring prefix, 2
+// when 2 do, else 1 (always 1 for int8).
+int decode_heads_per_group(const PoolView &pv, bool prefix);
 hipError_t launch_decode(const PoolView &pv, const BatchView &bv, int layer, const void *q,
                          const void *k, const void *v, void *out, float scale, bool fused,
                          hipStream_t stream, const LaunchTiming &timing);
