@@ -8,10 +8,11 @@
   frames/s = streams / step time; audio-s/s = frames/s * 0.08 (12.5 Hz frames).
   Roofline: algorithmic bytes per decode launch (per stream: 2 (n+1) H D 2 B of K/V read, 1 KB q,
   2 KB new k/v, 1 KB out, 2 KB append write, 4 ceil((n+1)/16) B of page ids) over the kernel's
-  average duration, against 8 TB/s.  The duration comes from HIP events that the launch itself
-  records as the kernel starts and ends (hipExtLaunchKernel, via xnp_pool_time_next), on the
-  stream the kernel runs on: one launch per timed step, layer s % 9 at step s (an event pair
-  costs about 17 us of issue time, so timing all nine would slow the steps being measured).
+  average duration, against 8 TB/s.  The duration comes from HIP events that the launches
+  themselves record (hipExtLaunchKernel, via xnp_pool_time_next), on the stream the kernels run
+  on: on every fifth step, layer 0's launch records the start as its kernel starts and layer 8's
+  the stop as its kernel ends; the span / 9 is the mean launch (the nine launches run back to
+  back; one event pair per step keeps the event overhead off the steps and off short kernels).
   step_ms: the median and 95th percentile of the step periods, from one event per step start.
 
 --workload prefill: prompt prefill, 64 streams x 256-position prompts, 9 layers, bf16, RoPE
@@ -154,22 +155,36 @@ class StepMarks:
         return {"p50": round(float(np.percentile(d, 50)), 4), "p95": round(float(np.percentile(d, 95)), 4)}
 
 
-def timed_steps(step, steps, warmup, L, every=5):
+def timed_steps(step, steps, warmup, L, every=5, span=False):
     """Run warmup then `steps` steps; wall ms per step, the durations (ms) of the timed launches,
     and the steps' p50 / p95 periods (StepMarks).
 
-    Every `every`-th step times one launch, layer (s / every) % L, with HIP events its launch
-    records around the kernel: a launch that records events issues more slowly (and the steps
-    around it with it), so timing every step would slow the very steps the wall clock measures.
-    Layers are alike, so the rotating sample's mean is the mean launch duration."""
+    Every `every`-th step times the kernel with HIP events its launches record (hipExtLaunchKernel):
+    a launch that records events issues more slowly (and the steps around it with it), so timing
+    every step would slow the very steps the wall clock measures.
+    - span=False: one launch, layer (s / every) % L, records both events around its kernel.  Layers
+      are alike, so the rotating sample's mean is the mean launch duration.
+    - span=True, for steps that launch nothing but the L layers' kernels back to back: layer 0's
+      launch records the start and layer L - 1's the stop, and the span / L is the mean launch
+      duration.  An event pair costs the kernel it brackets about 5 us; spread over L launches it
+      stops inflating short kernels, at the price of the (about 1 us) gaps between launches."""
     import torch
     for _ in range(warmup):
         step(None)
     torch.cuda.synchronize()
     hip = HipEvents()
     timed = {s: (s // every) % L for s in range(0, steps, every)}
-    ev = [[(hip.create(), hip.create()) if timed.get(s) == l else None for l in range(L)] if s in timed else None
-          for s in range(steps)]
+    ev, pairs = [None] * steps, {}
+    for s in timed:
+        a, b = hip.create(), hip.create()
+        pairs[s] = (a, b)
+        ev[s] = [None] * L
+        if span:
+            ev[s][0] = (a, b) if L == 1 else (a, None)
+            if L > 1:
+                ev[s][L - 1] = (None, b)
+        else:
+            ev[s][timed[s]] = (a, b)
     marks = StepMarks(steps)
     with NoGC():
         t0 = time.perf_counter()
@@ -179,10 +194,10 @@ def timed_steps(step, steps, warmup, L, every=5):
         marks.mark()
         torch.cuda.synchronize()
         t1 = time.perf_counter()
-    kern = np.array([hip.elapsed_ms(*ev[s][timed[s]]) for s in timed])
-    for pair in (p_ for s_ in ev if s_ is not None for p_ in s_ if p_ is not None):
-        for e in pair:
-            hip.destroy(e)
+    kern = np.array([hip.elapsed_ms(*pairs[s]) / (L if span else 1) for s in timed])
+    for a, b in pairs.values():
+        hip.destroy(a)
+        hip.destroy(b)
     return (t1 - t0) * 1000.0 / steps, kern, marks.percentiles()
 
 
@@ -273,7 +288,7 @@ def run_decode(args, xnp, torch):
         pool.end()
         cur[:] += 1
 
-    ms, kern, pct = timed_steps(step, args.steps, args.warmup, L)
+    ms, kern, pct = timed_steps(step, args.steps, args.warmup, L, span=True)
     avg_ms = float(kern.mean())
     bytes_per_launch = bytes_timed[0] / bytes_timed[1]  # every layer of a step moves the same bytes
     achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
@@ -350,7 +365,7 @@ def run_prefill(args, xnp, torch):
             pool.close(sid)
             ids[i] = pool.init_state(T)
 
-    ms, kern, pct = timed_steps(step, args.steps, args.warmup, L)
+    ms, kern, pct = timed_steps(step, args.steps, args.warmup, L, span=True)
     avg_ms = float(kern.mean())
     flops = 2.0 * D * T * (T + 1) * H * S
     tflops = flops / (avg_ms * 1e-3) / 1e12
@@ -471,7 +486,7 @@ def run_window(args, xnp, torch):
         pool.end()
         written[:] += 1
 
-    ms, kern, pct = timed_steps(step, args.steps, args.warmup, L)
+    ms, kern, pct = timed_steps(step, args.steps, args.warmup, L, span=True)
     avg_ms = float(kern.mean())
     bytes_per_launch = bytes_timed[0] / bytes_timed[1]  # every layer of a step moves the same bytes
     achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9

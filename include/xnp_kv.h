@@ -235,7 +235,9 @@ xnp_status xnp_pool_check_tables(xnp_pool *pool, int32_t *mismatches, void *hip_
 
 /* Measurement hook (no counterpart in the reference): the pool's next decode or prefill launch
  * records HIP events `start` and `stop` (hipEvent_t, created by the caller) as the kernel starts
- * and ends (hipExtLaunchKernel), so that the kernel alone is timed.  Applies to one launch. */
+ * and ends (hipExtLaunchKernel), so that the kernel alone is timed.  Either may be null: a start
+ * recorded by one launch and a stop by a later one time the launches between them.  Applies to
+ * one launch. */
 xnp_status xnp_pool_time_next(xnp_pool *pool, void *start_event, void *stop_event);
 
 /* ---- the rest of a flow-LM layer (transformer.rs:591-634) --------------------------------- */

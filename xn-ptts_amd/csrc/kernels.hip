@@ -18,7 +18,7 @@ namespace xnp {
 // kernel alone.  Without them, a plain launch: the form a stream capture (hipGraph) records.
 #define XNP_LAUNCH(kernel, grid, block, stream, tm, ...)                                            \
     do {                                                                                           \
-        if ((tm).start)                                                                            \
+        if ((tm).start || (tm).stop)                                                               \
             hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, (tm).start, (tm).stop, 0, __VA_ARGS__); \
         else                                                                                       \
             hipLaunchKernelGGL(kernel, grid, block, 0, stream, __VA_ARGS__);                       \

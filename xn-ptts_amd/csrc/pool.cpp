@@ -499,7 +499,6 @@ extern "C" xnp_status xnp_pool_stats_get(const xnp_pool *pool, xnp_pool_stats *o
 
 extern "C" xnp_status xnp_pool_time_next(xnp_pool *pool, void *start_event, void *stop_event) {
     if (!pool) return fail(XNP_E_INVALID, "null argument");
-    if (!start_event != !stop_event) return fail(XNP_E_INVALID, "give both events or neither");
     pool->timing.start = (hipEvent_t)start_event;
     pool->timing.stop = (hipEvent_t)stop_event;
     return XNP_OK;

@@ -266,8 +266,9 @@ class KvPool:
         _check(self._lib.xnp_pool_check_tables(self._h, ctypes.byref(bad), _stream(stream)))
         return bad.value
 
-    def time_next(self, start_event: int, stop_event: int):
-        """Have the next decode/prefill launch record these hipEvent_t handles around its kernel."""
+    def time_next(self, start_event, stop_event):
+        """Have the next decode/prefill launch record these hipEvent_t handles around its kernel
+        (either may be None: a start from one launch and a stop from a later one)."""
         _check(self._lib.xnp_pool_time_next(self._h, start_event, stop_event))
 
     def rope_rows(self, pos0: int, n: int):
