@@ -1095,9 +1095,20 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
                     mx = fmaxf(mx, fmaxf(fmaxf(s[kg][0], s[kg][1]), fmaxf(s[kg][2], s[kg][3])));
                 mx = fmaxf(mx, __shfl_xor(mx, 16));
                 mx = fmaxf(mx, __shfl_xor(mx, 32));
+                // lazy rescaling, as in decode: the row's sum and accumulators move to a new max only
+                // when some row of the wave saw its max grow by more than 8 (log2 units); until then
+                // exponents are taken against the older max and stay below 2^8
                 const float mn = fmaxf(m[j], mx * qmul);
-                const float alpha = fast_exp2(m[j] - mn);
-                m[j] = mn;
+                if (__any(mn > m[j] + 8.f)) {
+                    const float alpha = fast_exp2(m[j] - mn);
+                    lsum[j] *= alpha;
+#pragma unroll
+                    for (int dg = 0; dg < 4; ++dg)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) o[j][dg][r] *= alpha;
+                    m[j] = mn;
+                }
+                const float mref = m[j];
                 float psum = 0.f;
                 uint32_t pk[4][2];
 #pragma unroll
@@ -1105,17 +1116,13 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
                     float p[4];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        p[r] = fast_exp2(__builtin_fmaf(s[kg][r], qmul, -mn));
+                        p[r] = fast_exp2(__builtin_fmaf(s[kg][r], qmul, -mref));
                         psum += p[r];
                     }
                     pk[kg][0] = pack_bf16(p[0], p[1]);
                     pk[kg][1] = pack_bf16(p[2], p[3]);
                 }
-                lsum[j] = __builtin_fmaf(lsum[j], alpha, psum);
-#pragma unroll
-                for (int dg = 0; dg < 4; ++dg)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) o[j][dg][r] *= alpha;
+                lsum[j] += psum;
 #pragma unroll
                 for (int kp = 0; kp < 2; ++kp) {
                     // k slots: keys 32 kp + 4 g .. +3 (elements 0-3) and 32 kp + 16 + 4 g .. +3 (4-7)
