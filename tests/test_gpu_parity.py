@@ -230,6 +230,20 @@ def test_grouped_kv_heads(cache, act, kvh):
         p.assert_cache_equal(i)
 
 
+@pytest.mark.parametrize("h,kvh", [(6, 2), (12, 2), (12, 3)])
+@pytest.mark.parametrize("cache,act", [("bf16", "bf16"), ("f32", "f32")])
+def test_grouped_heads_of_other_ratios(cache, act, h, kvh):
+    # 3, 6 and 4 query heads per kv head: a decode work group then takes one, two or four of them,
+    # and 3 kv heads leave the grid's runs of 8 (stream, kv head) pairs with a partial tail
+    p = Pair(cache=cache, act=act, H=h, KVH=kvh, streams=7, cap=96, seed=40 + h + kvh)
+    for i, n in enumerate([0, 5, 16, 17, 40, 63, 90]):
+        p.fill(i, n)
+    for _ in range(3):
+        p.step()
+    for i in range(7):
+        p.assert_cache_equal(i)
+
+
 def test_grouped_heads_store_a_kv_head_once():
     # the pages hold KVH heads: a pool of 2 kv heads takes a quarter of one of 8
     def pages_bytes(kvh):
