@@ -34,6 +34,7 @@ __device__ __forceinline__ float bf16_value(uint32_t bits16) { return __uint_as_
 // bits, exact ties, denormals, NaN and infinities).
 typedef float f32x2v_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+typedef __fp16 f16x2v_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
     const bf16x2v_t h = __builtin_convertvector((f32x2v_t){a, b}, bf16x2v_t);
@@ -323,22 +324,34 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
     // bf16 pages and queries: scores by v_dot2_f32_bf16 on packed bf16 pairs (the page words as
     // they are, no unpacking), with the query's scale applied to each row's sum
     constexpr bool DOT2 = CDT == DT_BF16 && ABF;
+    // int8 pages and bf16 queries: the query as f16 pairs (a bf16 value converts exactly), each
+    // code byte b (q + 128) under the f16 exponent of 1024 by one byte permute, so that
+    // v_dot2_f32_f16 sums q (1024 + b) = q (1152 + code) exactly per product; 1152 sum(q) comes
+    // back out once per row
+    constexpr bool H16 = CDT == DT_I8 && ABF;
     const bool two_q = PREFIX && R.prefix > 0; // PREFIX: some stream of the batch keeps a prefix
     float qw[GQ][DPL], qp[GQ][DPL];
-    uint32_t qh[GQ][DPL / 2], ph[GQ][DPL / 2]; // DOT2: the rotated queries' bf16 pairs
+    uint32_t qh[GQ][DPL / 2], ph[GQ][DPL / 2]; // DOT2, H16: the rotated queries' bf16 / f16 pairs
     // int8: unpack hands out q + 128, so a dot product is sum(qw (q + 128)) - 128 sum(qw) and a
     // value accumulator carries -128 sum(e sv) on every dim (vbias, taken out after the loop)
     float qwsum[GQ], qpsum[GQ], vbias[GQ];
 #pragma unroll
     for (int e = 0; e < GQ; ++e) {
         const char *qrow = (const char *)q + ((size_t)R.b * pv.H + h + e) * kHeadDim * AE;
-        rotated_q<DPL, ABF>(pv, qrow, c, R.pos, DOT2 ? 1.f : qmul, qw[e]);
-        if (two_q) rotated_q<DPL, ABF>(pv, qrow, c, R.pos_pre, DOT2 ? 1.f : qmul, qp[e]);
+        rotated_q<DPL, ABF>(pv, qrow, c, R.pos, DOT2 || H16 ? 1.f : qmul, qw[e]);
+        if (two_q) rotated_q<DPL, ABF>(pv, qrow, c, R.pos_pre, DOT2 || H16 ? 1.f : qmul, qp[e]);
         if constexpr (DOT2) {
 #pragma unroll
             for (int i = 0; i < DPL / 2; ++i) {
                 qh[e][i] = (__float_as_uint(qw[e][2 * i]) >> 16) | (__float_as_uint(qw[e][2 * i + 1]) & 0xffff0000u);
                 ph[e][i] = (__float_as_uint(qp[e][2 * i]) >> 16) | (__float_as_uint(qp[e][2 * i + 1]) & 0xffff0000u);
+            }
+        }
+        if constexpr (H16) {
+#pragma unroll
+            for (int i = 0; i < DPL / 2; ++i) {
+                qh[e][i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(qw[e][2 * i], qw[e][2 * i + 1]));
+                ph[e][i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(qp[e][2 * i], qp[e][2 * i + 1]));
             }
         }
         qwsum[e] = qpsum[e] = vbias[e] = 0.f;
@@ -390,6 +403,26 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
                         dw[e] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v_t, pre ? ph[e][i] : qh[e][i]),
                                                                 __builtin_bit_cast(bf16x2v_t, u[i]), dw[e], false);
                 }
+            } else if constexpr (H16) {
+                const uint32_t *u = (const uint32_t *)&kr[p];
+#pragma unroll
+                for (int e = 0; e < GQ; ++e) dw[e] = 0.f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t x = u[i] ^ 0x80808080u;
+                    // bytes 0, 1 (then 2, 3) of x as the low bytes of two f16 whose high bytes are 0x64
+                    const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u);
+                    const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u);
+#pragma unroll
+                    for (int e = 0; e < GQ; ++e) {
+                        dw[e] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2v_t, pre ? ph[e][2 * i] : qh[e][2 * i]),
+                                                       __builtin_bit_cast(f16x2v_t, lo), dw[e], false);
+                        dw[e] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2v_t, pre ? ph[e][2 * i + 1] : qh[e][2 * i + 1]),
+                                                       __builtin_bit_cast(f16x2v_t, hi), dw[e], false);
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < GQ; ++e) dw[e] = __builtin_fmaf(-1152.f, pre ? qpsum[e] : qwsum[e], dw[e]);
             } else {
                 float x[DPL];
                 unpack<CDT>(kr[p], x);
@@ -413,7 +446,7 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
 #pragma unroll
                 for (int o = 1; o < LPR; o <<= 1) dw[e] += __shfl_xor(dw[e], o);
                 if constexpr (CDT == DT_I8) dw[e] *= sk;
-                if constexpr (DOT2) dw[e] *= qmul;
+                if constexpr (DOT2 || H16) dw[e] *= qmul;
                 s[e][p] = ((seen >> r) & 1u) ? dw[e] : -INFINITY;
             }
         }
