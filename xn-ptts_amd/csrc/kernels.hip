@@ -682,12 +682,25 @@ hipError_t launch_append(const PoolView &pv, const BatchView &bv, int layer, con
     }
 }
 
+// bf16 pools with 2 to 16 query heads per kv head decode a whole kv head per work group on MFMA
+// (k_decode_gqa), unless a stream of the batch keeps a ring prefix (a second query position)
+static bool decode_on_mfma(const PoolView &pv, bool prefix) {
+    const int G = pv.H / pv.KVH;
+    return pv.cache_dt == DT_BF16 && pv.act_dt == DT_BF16 && G >= 2 && G <= 16 && !prefix;
+}
+
+static hipError_t decode_gqa_impl(const PoolView &pv, const BatchView &bv, int layer, const void *q, const void *k,
+                                  const void *v, void *out, float scale, bool fused, hipStream_t stream,
+                                  const LaunchTiming &tm);
+
 int decode_heads_per_group(const PoolView &pv, bool prefix) {
-    // query heads of one kv head share a group's page reads: four when four divide the group and
-    // no stream of the batch keeps a ring prefix (whose second query would spill them), else two;
-    // int8 keeps one (its registers hold no second head at four waves per SIMD)
+    // query heads of one kv head share a group's page reads: all of them on MFMA; else four when
+    // four divide the group and no stream of the batch keeps a ring prefix (whose second query
+    // would spill them), else two; int8 keeps one (its registers hold no second head at four
+    // waves per SIMD)
     const int G = pv.H / pv.KVH;
     if (pv.cache_dt == DT_I8) return 1;
+    if (decode_on_mfma(pv, prefix)) return G;
     return G % 4 == 0 && !prefix ? 4 : G % 2 == 0 ? 2 : 1;
 }
 
@@ -737,6 +750,8 @@ hipError_t launch_decode(const PoolView &pv, const BatchView &bv, int layer, con
         default: return decode_impl<DT_F32, false, 1>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
         }
     case DT_BF16 * 2 + DT_BF16:
+        if (decode_on_mfma(pv, bv.prefix != 0))
+            return decode_gqa_impl(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
         switch (decode_heads_per_group(pv, bv.prefix != 0)) {
         case 4: return decode_impl<DT_BF16, true, 4>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
         case 2: return decode_impl<DT_BF16, true, 2>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
@@ -1193,6 +1208,213 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
                                                                 pack_bf16(o[j][dg][2] * inv, o[j][dg][3] * inv));
         }
     }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Grouped-head decode on MFMA: bf16 pages and queries, 2 to 16 query heads per kv head, no ring
+// prefix.  One work group per (stream, kv head), whose G query heads are the 16 columns of the
+// MFMA tiles (columns past G hold zeros), so that each page is read once and its 16 keys meet all
+// G heads in a few instructions.  The contractions are the prompt prefill's, transposed so that P
+// never leaves registers:
+//   S^T = K Q^T      v_mfma_f32_16x16x32_bf16, A = the page's K rows straight from memory (lane:
+//                    key l16, dims 32 kc + 8 g .. +7), B = the rotated query rows; lane (l16, g)
+//                    gets the scores of keys 4 g .. 4 g + 3 for query head l16;
+//   softmax          online per query column, its max and sum over the 4 lanes of the column;
+//   O^T += V^T P^T   v_mfma_f32_16x16x16_bf16, B = P^T straight from the S^T registers, A = V^T by
+//                    transposed reads (ds_read_b64_tr_b16) of the page's V, copied into a
+//                    wave-private LDS tile.
+// Pages, SPLIT waves per group, the fused append and the LDS merge are attend_core's.
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+template <int SPLIT>
+__global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4))) void k_decode_gqa(
+    PoolView pv, BatchView bv, int layer, const void *q, const void *knew, const void *vnew, void *out, float qmul,
+    int fused) {
+    constexpr int DEPTH = 2; // pages in flight ahead of the one being reduced
+    __shared__ __attribute__((aligned(16))) uint16_t vt[SPLIT][kBlock][kPfLd]; // each wave's V tile, [key][dim]
+    __shared__ float part[SPLIT][16][kPartStride];
+    const int G = pv.H / pv.KVH;
+    const int kvh = blockIdx.x % pv.KVH;
+    const char *rec = bv.recs + (size_t)(blockIdx.x / pv.KVH) * bv.rec_stride;
+    const StreamRec R = *(const StreamRec *)rec;
+    const int32_t *rec_pages = (const int32_t *)(rec + sizeof(StreamRec));
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, l16 = lane & 15;
+    const int nb = R.nblk > w ? (R.nblk - w + SPLIT - 1) / SPLIT : 0; // this wave's pages
+
+    // per-page metadata, lane j holding page w + j * SPLIT (as attend_core)
+    int my_page = 0;
+    uint32_t my_seen = 0;
+    const int pg_raw = w + lane * SPLIT < pv.mbps ? rec_pages[w + lane * SPLIT] : -1;
+    if (lane < nb) {
+        const int base = (w + lane * SPLIT) * kBlock;
+        uint32_t seen = 0xffffu;
+        if (R.mask_off >= 0) seen = (bv.masks[R.mask_off + (base >> 5)] >> (base & 16)) & 0xffffu;
+        const int nvalid = R.span - base;
+        if (nvalid < kBlock) seen &= (1u << max(nvalid, 0)) - 1u;
+        const bool ok = pg_raw >= 0 && pg_raw < pv.NB;
+        my_page = ok ? pg_raw : 0;
+        my_seen = ok ? seen : 0;
+    }
+
+    // B operands of S^T: query head kvh G + l16, dims 32 kc + 8 g .. +7, rotated at R.pos and
+    // rounded to bf16 (zeros past G)
+    bf16x8_t qb[2];
+    {
+        const bool live = l16 < G;
+        const int hq = kvh * G + min(l16, G - 1);
+        const uint16_t *qp = (const uint16_t *)q + ((size_t)R.b * pv.H + hq) * kHeadDim;
+        const float4 *cs = (const float4 *)(pv.rope + (size_t)R.pos * (kHeadDim / 2));
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) {
+            const uint4 raw = *(const uint4 *)(qp + 32 * kc + 8 * g);
+            const float4 ca = cs[(32 * kc + 8 * g) / 4], cb = cs[(32 * kc + 8 * g) / 4 + 1];
+            const float cf[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w}; // cos, sin of 4 pairs
+            const uint32_t *u = (const uint32_t *)&raw;
+            uint32_t o4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float x0 = bf16_value(u[i] & 0xffffu), x1 = bf16_value(u[i] >> 16);
+                const float c = cf[2 * i], s = cf[2 * i + 1];
+                const float a = x0 * c, bb = x1 * s, e = x0 * s, f = x1 * c;
+                o4[i] = live ? pack_bf16(a - bb, e + f) : 0u;
+            }
+            qb[kc] = as_bf16x8(make_uint4(o4[0], o4[1], o4[2], o4[3]));
+        }
+    }
+
+    const uint16_t *kbase = (const uint16_t *)pv.pages + tile_index(pv, layer, 0, 0, kvh) * (kBlock * kHeadDim);
+    const uint16_t *vbase = (const uint16_t *)pv.pages + tile_index(pv, layer, 1, 0, kvh) * (kBlock * kHeadDim);
+    const size_t page_elems = (size_t)pv.KVH * kBlock * kHeadDim;
+
+    float m = -1e30f, lsum = 0.f; // running max (scaled, log2 units) and this lane's share of the sum
+    f32x4_t o[4];                 // O^T: dims 16 dg + 4 g + r, query head l16
+#pragma unroll
+    for (int dg = 0; dg < 4; ++dg) o[dg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    // a page's K in A-operand layout (key l16, dims 32 kc + 8 g) and this lane's 32 bytes of its V
+    auto load = [&](uint4 (&kr)[2], uint4 (&vr)[2], int j) {
+        const size_t pe = (size_t)__builtin_amdgcn_readlane(my_page, j) * page_elems;
+        kr[0] = *(const uint4 *)(kbase + pe + l16 * kHeadDim + 8 * g);
+        kr[1] = *(const uint4 *)(kbase + pe + l16 * kHeadDim + 32 + 8 * g);
+        vr[0] = *(const uint4 *)(vbase + pe + 16 * lane);
+        vr[1] = *(const uint4 *)(vbase + pe + 16 * lane + 8);
+    };
+    auto process = [&](const uint4 (&kr)[2], const uint4 (&vr)[2], int j) {
+        const uint32_t seen = __builtin_amdgcn_readlane(my_seen, j);
+        f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kr[kc]), qb[kc], s, 0, 0, 0);
+        // lane: query head l16 against keys 4 g + r of the page
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (!((seen >> (4 * g + r)) & 1u)) s[r] = -INFINITY;
+        float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        // lazy rescaling, as in attend_core
+        const float mn = fmaxf(m, mx * qmul);
+        if (__any(mn > m + 8.f)) {
+            const float alpha = fast_exp2(m - mn);
+            lsum *= alpha;
+#pragma unroll
+            for (int dg = 0; dg < 4; ++dg)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) o[dg][r] *= alpha;
+            m = mn;
+        }
+        float p[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            p[r] = fast_exp2(__builtin_fmaf(s[r], qmul, -m));
+            lsum += p[r];
+        }
+        const s16x4_t pt = __builtin_bit_cast(s16x4_t, make_uint2(pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3])));
+        // the page's V into this wave's LDS tile (row lane / 4, dims 16 (lane % 4) ..); an unseen row
+        // weighs 0 but its bytes may be anything, so it goes in as zeros (0 * NaN would be NaN)
+        const uint32_t keep = ((seen >> (lane >> 2)) & 1u) ? ~0u : 0u;
+        uint16_t *vrow = &vt[w][lane >> 2][16 * (lane & 3)];
+        *(uint4 *)vrow = make_uint4(vr[0].x & keep, vr[0].y & keep, vr[0].z & keep, vr[0].w & keep);
+        *(uint4 *)(vrow + 8) = make_uint4(vr[1].x & keep, vr[1].y & keep, vr[1].z & keep, vr[1].w & keep);
+#pragma unroll
+        for (int dg = 0; dg < 4; ++dg) {
+            // V^T: lane gets dim 16 dg + l16 of keys 4 g .. 4 g + 3
+            const uint2 a = lds_read_tr16(&vt[w][4 * g + (l16 >> 2)][16 * dg + 4 * (l16 & 3)]);
+            o[dg] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, a), pt, o[dg], 0, 0, 0);
+        }
+    };
+
+    uint4 kb[DEPTH + 1][2], vb[DEPTH + 1][2];
+    // complete_kv: the wave that owns the write page appends the kv head's new row, as in attend_core
+    const int wblk = R.write_slot >> 4, wj = wblk / SPLIT;
+    const bool owner = fused && w == wblk % SPLIT;
+    const bool early = !owner || wj >= DEPTH;
+    if (early) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) load(kb[d], vb[d], d);
+    }
+    if (owner) {
+        const int slot = R.write_slot;
+        const size_t arow = (size_t)R.b * pv.KVH + kvh;
+        const bool fresh = (R.flags & 1) ? (R.flags & 2) != 0 : ((slot & 15) == 0);
+        append_row_wave<DT_BF16, true>(pv, layer, __builtin_amdgcn_readlane(my_page, wj), slot & 15, kvh, R.key_pos,
+                                       (const char *)knew + arow * kHeadDim * 2, (const char *)vnew + arow * kHeadDim * 2,
+                                       fresh);
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+    }
+    if (!early) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) load(kb[d], vb[d], d);
+    }
+    for (int j = 0; j < nb; j += DEPTH + 1) {
+#pragma unroll
+        for (int u = 0; u <= DEPTH; ++u) {
+            load(kb[(u + DEPTH) % (DEPTH + 1)], vb[(u + DEPTH) % (DEPTH + 1)], j + u + DEPTH);
+            process(kb[u], vb[u], j + u);
+        }
+    }
+
+    // the column's sum over its 4 lanes; the waves' shares through LDS; wave 0 writes the G heads
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+#pragma unroll
+    for (int dg = 0; dg < 4; ++dg)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) part[w][l16][16 * dg + 4 * g + r] = o[dg][r];
+    if (g == 0) {
+        part[w][l16][64] = m;
+        part[w][l16][65] = lsum;
+    }
+    __syncthreads();
+    if (w != 0) return;
+    for (int e = 0; e < G; ++e) {
+        float M = -1e30f;
+#pragma unroll
+        for (int k = 0; k < SPLIT; ++k) M = fmaxf(M, part[k][e][64]);
+        float L = 0.f, A = 0.f;
+#pragma unroll
+        for (int k = 0; k < SPLIT; ++k) {
+            const float a = fast_exp2(part[k][e][64] - M);
+            L = __builtin_fmaf(part[k][e][65], a, L);
+            A = __builtin_fmaf(part[k][e][lane], a, A);
+        }
+        ((uint16_t *)out)[((size_t)R.b * pv.H + kvh * G + e) * kHeadDim + lane] = (uint16_t)bf16_bits(A / L);
+    }
+}
+
+static hipError_t decode_gqa_impl(const PoolView &pv, const BatchView &bv, int layer, const void *q, const void *k,
+                                  const void *v, void *out, float scale, bool fused, hipStream_t stream,
+                                  const LaunchTiming &tm) {
+    const float qmul = scale * 1.4426950408889634f;
+    const dim3 grid(bv.n * pv.KVH);
+    const int f = fused ? 1 : 0;
+    switch (bv.split) {
+    case 1: XNP_LAUNCH((k_decode_gqa<1>), grid, dim3(64), stream, tm, pv, bv, layer, q, k, v, out, qmul, f); break;
+    case 2: XNP_LAUNCH((k_decode_gqa<2>), grid, dim3(128), stream, tm, pv, bv, layer, q, k, v, out, qmul, f); break;
+    case 4: XNP_LAUNCH((k_decode_gqa<4>), grid, dim3(256), stream, tm, pv, bv, layer, q, k, v, out, qmul, f); break;
+    case 8: XNP_LAUNCH((k_decode_gqa<8>), grid, dim3(512), stream, tm, pv, bv, layer, q, k, v, out, qmul, f); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 template <int CDT, bool ABF>

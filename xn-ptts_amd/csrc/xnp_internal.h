@@ -95,8 +95,9 @@ hipError_t launch_pull_plan(const PoolView &pv, const void *src, void *dst, size
 hipError_t launch_append(const PoolView &pv, const BatchView &bv, int layer, const void *k,
                          const void *v, hipStream_t stream);
 // Query heads one decode work group covers (all of one kv head), for a pool that stores grouped
-// heads in a bf16 or f32 cache: 4 when 4 divide the group and the batch keeps no ring prefix, 2
-// when 2 do, else 1 (always 1 for int8).
+// heads in a bf16 or f32 cache: the whole group on MFMA for bf16 with 2 to 16 of them and no ring
+// prefix in the batch; else 4 when 4 divide the group and no prefix, 2 when 2 do, else 1 (always
+// 1 for int8).
 int decode_heads_per_group(const PoolView &pv, bool prefix);
 hipError_t launch_decode(const PoolView &pv, const BatchView &bv, int layer, const void *q,
                          const void *k, const void *v, void *out, float scale, bool fused,
