@@ -313,7 +313,9 @@ def run_decode(args, xnp, torch):
               "mean_cached_len": round(float(cur.mean()) - (args.steps + 1) / 2.0, 1)}
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel": "k_decode<bf16> (fused append + RoPE + decode), one launch per layer",
+            "kernel": ("k_decode<bf16> (fused append + RoPE + decode)" if kvh == H or H // kvh > 16 else
+                       "k_decode_gqa (fused append + RoPE + decode, the query heads of a kv head on MFMA)")
+                      + ", one launch per layer",
             "avg_kernel_us": round(avg_ms * 1000.0, 2), "bytes_per_launch": int(bytes_per_launch)}
     return line("frames/sec (audio-sec/sec) at 1024 streams; decode-attn HBM GB/s % peak", fps, "frames/s", args,
                 ms, "bf16", config, roof, cpu, extra={"audio_sec_per_sec": round(fps * 0.08, 1)}, pct=pct)
