@@ -613,24 +613,26 @@ template <int CDT, bool ABF, int SPLIT, bool PREFIX, int GQ>
 __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(Lanes<CDT>::WAVES))) void k_decode(
     PoolView pv, BatchView bv, int layer, const void *q, const void *knew, const void *vnew, void *out, float qmul,
     int fused) {
-    // Work groups go to the 8 XCDs in turn (group b to XCD b % 8).  The G = H / (KVH GQ) groups
-    // of one (stream, kv head) read the same tiles: in runs of 8 G groups, XCD x takes the G groups
-    // of pair x of the run, one after another, so their reads meet in that XCD's L2.  With G = 1
-    // this is group b -> (record b / (H / GQ), heads GQ (b % (H / GQ)) ..).
-    const int G = pv.H / (pv.KVH * GQ), b = blockIdx.x;
-    const int full = bv.n * pv.KVH / 8 * 8; // (stream, kv head) pairs in whole runs
-    int pair, gi;
-    if (b < full * G) {
-        pair = b / (8 * G) * 8 + b % 8;
-        gi = b % (8 * G) / 8;
+    // Work groups go to the 8 XCDs in turn (group b to XCD b % 8).  A stream has P = H / GQ groups
+    // (slot s: query heads GQ s ..).  In runs of 8 P groups, XCD x takes the P groups of stream x of
+    // the run, one after another: the heads of one page block (adjacent tiles in HBM) are read from
+    // one XCD at about the same time, and the groups that share a kv head (consecutive slots) meet
+    // in its L2.  Measured against one head per XCD: int8 window 107.5 -> 105.6 us, bf16 decode
+    // 192.2 -> 191.8 us.
+    const int P = pv.H / GQ, b = blockIdx.x;
+    const int full = bv.n / 8 * 8; // streams in whole runs
+    int sidx, slot;
+    if (b < full * P) {
+        sidx = b / (8 * P) * 8 + b % 8;
+        slot = b % (8 * P) / 8;
     } else {
-        pair = full + (b - full * G) / G;
-        gi = (b - full * G) % G;
+        sidx = full + (b - full * P) / P;
+        slot = (b - full * P) % P;
     }
-    const char *rec = bv.recs + (size_t)(pair / pv.KVH) * bv.rec_stride;
+    const char *rec = bv.recs + (size_t)sidx * bv.rec_stride;
     const StreamRec R = *(const StreamRec *)rec;
-    attend_core<CDT, ABF, SPLIT, PREFIX, GQ>(pv, bv, layer, R, (const int32_t *)(rec + sizeof(StreamRec)),
-                                             (pair % pv.KVH * G + gi) * GQ, q, knew, vnew, out, qmul, fused);
+    attend_core<CDT, ABF, SPLIT, PREFIX, GQ>(pv, bv, layer, R, (const int32_t *)(rec + sizeof(StreamRec)), slot * GQ,
+                                             q, knew, vnew, out, qmul, fused);
 }
 
 // Prompt rows (transformer.rs:231-248), after k_append has written all t rows: row i of a stream
@@ -1234,8 +1236,11 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
     __shared__ __attribute__((aligned(16))) uint16_t vt[SPLIT][kBlock][kPfLd]; // each wave's V tile, [key][dim]
     __shared__ float part[SPLIT][16][kPartStride];
     const int G = pv.H / pv.KVH;
-    const int kvh = blockIdx.x % pv.KVH;
-    const char *rec = bv.recs + (size_t)(blockIdx.x / pv.KVH) * bv.rec_stride;
+    // XCD runs as in k_decode: in runs of 8 KVH groups, XCD x takes the kv heads of stream x of the run
+    const int b = blockIdx.x, full = bv.n / 8 * 8;
+    const int sidx = b < full * pv.KVH ? b / (8 * pv.KVH) * 8 + b % 8 : full + (b - full * pv.KVH) / pv.KVH;
+    const int kvh = b < full * pv.KVH ? b % (8 * pv.KVH) / 8 : (b - full * pv.KVH) % pv.KVH;
+    const char *rec = bv.recs + (size_t)sidx * bv.rec_stride;
     const StreamRec R = *(const StreamRec *)rec;
     const int32_t *rec_pages = (const int32_t *)(rec + sizeof(StreamRec));
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, l16 = lane & 15;
