@@ -587,6 +587,59 @@ def test_many_streams_at_the_config2_length_distribution(split):
         p.assert_cache_equal(i)
 
 
+def test_the_decode_configuration_at_full_size_spot_checked():
+    # The batched decode workload at its full size: 1024 streams x 9 layers x 8 heads x 64, bf16
+    # pages of 16 on shuffled block tables, cache lengths U[1, 1024], the library's own split.
+    # Every stream runs; 18 of them, spread over the longest-first order (the longest and the
+    # shortest included), are checked against the oracle over two steps: outputs within 2e-2,
+    # then every cache row bit-exact.
+    import types
+    S, L, H, cap = 1024, 9, 8, 1040
+    rng = np.random.default_rng(20261203)
+    lens = rng.integers(1, 1025, S)
+    order = np.argsort(-lens, kind="stable")
+    sample = sorted(set(order[::64].tolist()) | {int(order[0]), int(order[-1])})
+    mbps = (cap + 15) // 16
+    pool = xnp.KvPool(num_layers=L, num_heads=H, num_blocks=S * mbps + 8, max_streams=S, max_blocks_per_stream=mbps,
+                      cache_dtype="bf16", act_dtype="bf16", max_pos=8192, page_seed=13)
+    ids = [pool.init_state(cap) for _ in range(S)]
+    orc = {i: oracle.Stream(L, H, 64, cap, cache="bf16", act="bf16") for i in sample}
+    g = torch.Generator(device=DEV).manual_seed(20261203)
+
+    def randn(*shape):
+        return torch.randn(shape, device=DEV, generator=g).to(torch.bfloat16)
+
+    for i, n in enumerate(lens.tolist()):
+        # each stream's history through the voice load (f32 rows rounded to bf16 on the device)
+        pool.advance(ids[i], n)
+        if i in orc:
+            orc[i].advance(n)
+        for layer in range(L):
+            kv = torch.randn((2, n, H, 64), device=DEV, generator=g)
+            pool.load_kv(ids[i], layer, kv)
+            if i in orc:
+                orc[i].load_kv(layer, host(kv))
+        torch.cuda.synchronize()  # the staged rows are freed on the next iteration
+    for _ in range(2):
+        pool.begin(ids)
+        for layer in range(L):
+            q, k, v = randn(S, H, 64), randn(S, H, 64), randn(S, H, 64)
+            out = torch.empty((S, H, 64), dtype=torch.bfloat16, device=DEV)
+            pool.attend(layer, q, k, v, out, 0.125)
+            torch.cuda.synchronize()
+            got, qh, kh, vh = host(out[sample]), host(q[sample]), host(k[sample]), host(v[sample])
+            for j, i in enumerate(sample):
+                want, _ = orc[i].attend(layer, qh[j:j + 1], kh[j:j + 1], vh[j:j + 1])
+                assert rel_err(got[j:j + 1], want) <= 2e-2, (layer, i, int(lens[i]))
+        pool.end()
+        for i in sample:
+            orc[i].commit(1)
+    shim = types.SimpleNamespace(pool=pool, ids=ids, orc=orc, L=L, H=H, KVH=H, cache="bf16")
+    for i in sample:
+        Pair.assert_cache_equal(shim, i)
+    assert pool.check_tables() == 0
+
+
 # ---- prompt prefill (transformer.rs:231-248) ------------------------------------------------------
 @pytest.mark.parametrize("cache,act", [("bf16", "bf16"), ("f32", "f32"), ("i8", "bf16")])
 def test_prefill_matches_the_oracle(cache, act):
