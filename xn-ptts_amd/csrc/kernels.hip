@@ -59,6 +59,17 @@ __device__ __forceinline__ int quant(float y, float s) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// 16 bytes with the non-temporal hint.  A decode launch reads each K/V tile once: streamed, the
+// tiles stop displacing what the launch does reuse in L2 and the memory-side cache (records,
+// tables, queries).  Measured on attend_core's page loads: bf16 decode at 1024 streams 192 ->
+// 171 us, int8 window 104.4 -> 95.0 us; on the prefill's key/value staging 32.8 -> 32.2 us.  Only
+// where one load instruction covers whole 128-byte lines (attend_core: 1 KB contiguous per wave).
+__device__ __forceinline__ uint4 ld_stream(const void *p) {
+    typedef unsigned u32x4_nt __attribute__((ext_vector_type(4)));
+    const u32x4_nt a = __builtin_nontemporal_load((const u32x4_nt *)p);
+    return make_uint4(a.x, a.y, a.z, a.w);
+}
+
 template <int CDT> constexpr int esize() { return CDT == DT_F32 ? 4 : CDT == DT_BF16 ? 2 : 1; }
 
 // Element offset of row 0 of tile (layer, kv, page, head).
@@ -501,14 +512,14 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
         const size_t off = (size_t)pg * page_u4 + lane;
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-            kr[p] = kbase[off + 64 * p];
-            vr[p] = vbase[off + 64 * p];
+            kr[p] = ld_stream(kbase + off + 64 * p);
+            vr[p] = ld_stream(vbase + off + 64 * p);
         }
     };
 
     // DEPTH pages in flight ahead of the one being reduced.  The loop body has no branch: past
-    // the wave's last page the lanes' page is page 0, whose tile every wave shares and finds in
-    // L2, and its rows are unseen, so reducing it changes nothing.  Each wait then only covers
+    // the wave's last page the lanes' page is page 0, a tile every wave shares (so mostly a cache
+    // hit), and its rows are unseen, so reducing it changes nothing.  Each wait then only covers
     // the oldest page's loads.
     uint4 kb[DEPTH + 1][NP], vb[DEPTH + 1][NP];
 
@@ -1078,11 +1089,11 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
             const size_t arow = (((size_t)P.out_row * t + i) * pv.KVH + kvh) * kHeadDim + 8 * spart;
             st.k = st.v = make_uint4(0, 0, 0, 0);
             if (in && fresh) {
-                st.k = *(const uint4 *)((const uint16_t *)knew + arow);
-                st.v = *(const uint4 *)((const uint16_t *)vnew + arow);
+                st.k = ld_stream((const uint16_t *)knew + arow);
+                st.v = ld_stream((const uint16_t *)vnew + arow);
             } else if (in && ok) {
-                st.k = *(const uint4 *)(kpages + poff);
-                st.v = *(const uint4 *)(vpages + poff);
+                st.k = ld_stream(kpages + poff);
+                st.v = ld_stream(vpages + poff);
             }
             st.rope = *(const uint4 *)(pv.rope16 + (size_t)(P.key_pos + i) * (kHeadDim / 2) + 4 * spart);
             st.info = (in && fresh ? 1 : 0) | (in && fresh && ok && last ? 2 : 0) | ((ok ? page : 0) << 2);
@@ -1218,9 +1229,10 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
 // MFMA tiles (columns past G hold zeros), so that each page is read once and its 16 keys meet all
 // G heads in a few instructions.  The contractions are the prompt prefill's, transposed so that P
 // never leaves registers:
-//   S^T = K Q^T      v_mfma_f32_16x16x32_bf16, A = the page's K rows straight from memory (lane:
-//                    key l16, dims 32 kc + 8 g .. +7), B = the rotated query rows; lane (l16, g)
-//                    gets the scores of keys 4 g .. 4 g + 3 for query head l16;
+//   S^T = K Q^T      v_mfma_f32_16x16x32_bf16, A = the page's K rows (lane: key l16, dims
+//                    32 kc + 8 g .. +7) from a wave-private LDS tile that streamed whole-line loads
+//                    fill, B = the rotated query rows; lane (l16, g) gets the scores of keys
+//                    4 g .. 4 g + 3 for query head l16;
 //   softmax          online per query column, its max and sum over the 4 lanes of the column;
 //   O^T += V^T P^T   v_mfma_f32_16x16x16_bf16, B = P^T straight from the S^T registers, A = V^T by
 //                    transposed reads (ds_read_b64_tr_b16) of the page's V, copied into a
@@ -1234,6 +1246,7 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
     int fused) {
     constexpr int DEPTH = 2; // pages in flight ahead of the one being reduced
     __shared__ __attribute__((aligned(16))) uint16_t vt[SPLIT][kBlock][kPfLd]; // each wave's V tile, [key][dim]
+    __shared__ __attribute__((aligned(16))) uint16_t kt[SPLIT][kBlock][kPfLd]; // each wave's K tile, [key][dim]
     __shared__ float part[SPLIT][16][kPartStride];
     const int G = pv.H / pv.KVH;
     // XCD runs as in k_decode: in runs of 8 KVH groups, XCD x takes the kv heads of stream x of the run
@@ -1296,19 +1309,30 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
 #pragma unroll
     for (int dg = 0; dg < 4; ++dg) o[dg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    // a page's K in A-operand layout (key l16, dims 32 kc + 8 g) and this lane's 32 bytes of its V
+    // a page's K and V tiles, each in two streamed 1 KB loads (keys lane / 8 and 8 + lane / 8,
+    // dims 8 (lane % 8) ..): every load covers whole 128-byte lines.  Loaded straight in the MFMA's
+    // A layout, each load would take half of every line, and a streamed line is gone before the
+    // other half is read (33 -> 36.6 us at 1 kv head); K therefore goes through an LDS tile too.
+    // Measured against plain loads in A layout: 1 kv head 33.4 -> 28.8 us, 2: 56.5 -> 50.5, 4:
+    // 101.5 -> 89 us.
     auto load = [&](uint4 (&kr)[2], uint4 (&vr)[2], int j) {
         const size_t pe = (size_t)__builtin_amdgcn_readlane(my_page, j) * page_elems;
-        kr[0] = *(const uint4 *)(kbase + pe + l16 * kHeadDim + 8 * g);
-        kr[1] = *(const uint4 *)(kbase + pe + l16 * kHeadDim + 32 + 8 * g);
-        vr[0] = *(const uint4 *)(vbase + pe + 16 * lane);
-        vr[1] = *(const uint4 *)(vbase + pe + 16 * lane + 8);
+        kr[0] = ld_stream(kbase + pe + 8 * lane);
+        kr[1] = ld_stream(kbase + pe + 512 + 8 * lane);
+        vr[0] = ld_stream(vbase + pe + 8 * lane);
+        vr[1] = ld_stream(vbase + pe + 512 + 8 * lane);
     };
     auto process = [&](const uint4 (&kr)[2], const uint4 (&vr)[2], int j) {
         const uint32_t seen = __builtin_amdgcn_readlane(my_seen, j);
         f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        // K through the wave's LDS tile into A layout (key l16, dims 32 kc + 8 g); a wave's LDS
+        // accesses complete in order, so no barrier
+        *(uint4 *)&kt[w][lane >> 3][8 * (lane & 7)] = kr[0];
+        *(uint4 *)&kt[w][8 + (lane >> 3)][8 * (lane & 7)] = kr[1];
 #pragma unroll
-        for (int kc = 0; kc < 2; ++kc) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kr[kc]), qb[kc], s, 0, 0, 0);
+        for (int kc = 0; kc < 2; ++kc)
+            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(*(const uint4 *)&kt[w][l16][32 * kc + 8 * g]), qb[kc],
+                                                       s, 0, 0, 0);
         // lane: query head l16 against keys 4 g + r of the page
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -1334,12 +1358,15 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
             lsum += p[r];
         }
         const s16x4_t pt = __builtin_bit_cast(s16x4_t, make_uint2(pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3])));
-        // the page's V into this wave's LDS tile (row lane / 4, dims 16 (lane % 4) ..); an unseen row
-        // weighs 0 but its bytes may be anything, so it goes in as zeros (0 * NaN would be NaN)
-        const uint32_t keep = ((seen >> (lane >> 2)) & 1u) ? ~0u : 0u;
-        uint16_t *vrow = &vt[w][lane >> 2][16 * (lane & 3)];
-        *(uint4 *)vrow = make_uint4(vr[0].x & keep, vr[0].y & keep, vr[0].z & keep, vr[0].w & keep);
-        *(uint4 *)(vrow + 8) = make_uint4(vr[1].x & keep, vr[1].y & keep, vr[1].z & keep, vr[1].w & keep);
+        // the page's V into this wave's LDS tile (rows lane / 8 and 8 + lane / 8, dims 8 (lane % 8) ..);
+        // an unseen row weighs 0 but its bytes may be anything, so it goes in as zeros (0 * NaN would
+        // be NaN)
+        const uint32_t keep0 = ((seen >> (lane >> 3)) & 1u) ? ~0u : 0u;
+        const uint32_t keep1 = ((seen >> (8 + (lane >> 3))) & 1u) ? ~0u : 0u;
+        *(uint4 *)&vt[w][lane >> 3][8 * (lane & 7)] =
+            make_uint4(vr[0].x & keep0, vr[0].y & keep0, vr[0].z & keep0, vr[0].w & keep0);
+        *(uint4 *)&vt[w][8 + (lane >> 3)][8 * (lane & 7)] =
+            make_uint4(vr[1].x & keep1, vr[1].y & keep1, vr[1].z & keep1, vr[1].w & keep1);
 #pragma unroll
         for (int dg = 0; dg < 4; ++dg) {
             // V^T: lane gets dim 16 dg + l16 of keys 4 g .. 4 g + 3
