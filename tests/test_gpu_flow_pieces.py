@@ -66,6 +66,31 @@ def test_flow_linear_q8_matches_the_oracle(rows, k, n, epilogue):
     _close(y.float().cpu().numpy(), want, epilogue)
 
 
+# Long K: K >= 2048 runs the GEMM's two-half groups (alternate K chunks, summed in LDS); 2064 leaves
+# the halves 17 and 16 chunks, the last one partial; 1024 x 2048 x 2048 takes 64-row tiles.  Over
+# thousands of terms the f32 sum's order matters beyond one bf16 step for outputs near zero (the
+# oracle's own sequential sum lies up to 4 steps from the exact one at K = 2064), so each element
+# may also differ by the recursive-summation bound of both sums, 2 K 2^-24 s sum|x q|.
+@pytest.mark.parametrize("rows,k,n", [(70, 2048, 96), (600, 2064, 520), (1024, 2048, 2048)])
+@pytest.mark.parametrize("epilogue", ["store", "store_f32"])
+def test_flow_linear_q8_long_k_within_the_summation_bound(rows, k, n, epilogue):
+    rng = np.random.default_rng(rows + k + n)
+    x = bf16_round(rng.standard_normal((rows, k)).astype(np.float32))
+    q, s = oracle.quantize_rows((0.05 * rng.standard_normal((n, k))).astype(np.float32))
+    b = (0.1 * rng.standard_normal(n)).astype(np.float32)
+    want = oracle.flow_linear_q8(x, q, s, epilogue, bias=b)
+    y = torch.zeros((rows, n), dtype=torch.float32 if epilogue == "store_f32" else torch.bfloat16, device=DEV)
+    xnp.flow_linear_q8(_bf(x), torch.from_numpy(q).to(DEV), torch.from_numpy(s).to(DEV), y, epilogue,
+                       bias=torch.from_numpy(b).to(DEV))
+    torch.cuda.synchronize()
+    got = y.float().cpu().numpy()
+    bound = 2.0 * k * 2.0 ** -24 * (np.abs(x) @ np.abs(q.astype(np.float32)).T) * s[None, :]
+    want64 = np.abs(want.astype(np.float64))
+    spacing = np.exp2(np.floor(np.log2(np.maximum(want64, 1e-30))) - 7)
+    assert (np.abs(got.astype(np.float64) - want) <= spacing + bound).all(), epilogue
+    assert (got != want).mean() <= 0.01, (epilogue, float((got != want).mean()))
+
+
 def test_flow_linear_q8_reads_f32_rows_rounded():
     # input_linear / input_proj: K = 32 latents in f32, rounded to bf16 as they are staged
     rng = np.random.default_rng(89)

@@ -86,12 +86,14 @@ def make_weights(rng, H=8, KVH=8, D=64, dm=512, ff=2048, ls=False):
     return orc, xnp.LayerWeights(**d)
 
 
-@pytest.mark.parametrize("cache,KVH,ls", [("bf16", 8, False), ("bf16", 2, True), ("i8", 8, False)])
-def test_layer_steps_match_the_oracle(cache, KVH, ls):
+# ff 2048 (Phonon-40m's): linear2's K = 2048 runs the GEMM's two-half groups
+@pytest.mark.parametrize("cache,KVH,ls,ff", [("bf16", 8, False, 1024), ("bf16", 2, True, 1024), ("i8", 8, False, 1024),
+                                             ("bf16", 8, False, 2048)])
+def test_layer_steps_match_the_oracle(cache, KVH, ls, ff):
     # 5 streams with prior caches of 0..40 rows; a 7-row prompt on all, then 3 single-row steps,
     # through 2 layers each
-    rng = np.random.default_rng(61 + KVH)
-    L, H, D, dm, ff = 2, 8, 64, 512, 1024
+    rng = np.random.default_rng(61 + KVH + ff)
+    L, H, D, dm = 2, 8, 64, 512
     W = [make_weights(rng, H=H, KVH=KVH, ff=ff, ls=ls) for _ in range(L)]
     S, cap = 5, 96
     pool = xnp.KvPool(num_layers=L, num_heads=H, num_kv_heads=KVH, num_blocks=S * 8 + 8, max_streams=S,

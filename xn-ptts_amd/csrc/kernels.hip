@@ -1623,15 +1623,22 @@ constexpr int kGmPD = 3;  // K chunks of loads in flight
 
 // MI: 16-row MFMA tiles per wave in M, so tiles of 32 MI rows.  MI = 1 doubles the work groups of a
 // narrow projection (N = 512 at 2048 rows gives 256 groups of 64 rows: one wave per SIMD).
-template <int EPI, bool AF32, int MI>
-__global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K, const int8_t *W, const float *s,
-                                                 int N, GemmOut go) {
+//
+// KS: groups of KS x 256 threads.  Half h (256 threads, the tile's 4 waves) takes K chunks h, h + KS,
+// .. into its own LDS buffers; at the end half 1 hands its sums to half 0 through LDS, which adds
+// them and runs the epilogue.  For long K (linear2: K = 2048), where a group's chunks run one
+// after another.
+template <int EPI, bool AF32, int MI, int KS>
+__global__ __launch_bounds__(256 * KS) void k_gemm_q8(const uint16_t *A, int M, int K, const int8_t *W, const float *s,
+                                                      int N, GemmOut go) {
     constexpr int BM = 32 * MI;
-    __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][kGmLd];
-    __shared__ __attribute__((aligned(16))) uint16_t Ws[2][kGmT][kGmLd];
+    static_assert(KS == 1 || KS == 2, "one or two halves");
+    __shared__ __attribute__((aligned(16))) uint16_t As[KS][2][BM][kGmLd];
+    __shared__ __attribute__((aligned(16))) uint16_t Ws[KS][2][kGmT][kGmLd];
     const int ntn = (N + kGmT - 1) / kGmT;
     const int m0 = (blockIdx.x / ntn) * BM, n0 = (blockIdx.x % ntn) * kGmT;
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, l16 = lane & 15;
+    const int tid = threadIdx.x & 255, h = KS > 1 ? (int)(threadIdx.x >> 8) : 0;
+    const int w = tid >> 6, lane = tid & 63, g = lane >> 4, l16 = lane & 15;
     const int wm = w & 1, wn = w >> 1;
 
     // staging: A rows a_r (and a_r + 32 when MI = 2), 8 values at k 8 a_k; W row w_r, 16 int8 at
@@ -1687,10 +1694,10 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K
             a1 = masked(a1, ma);
             wq = masked(wq, mw);
         }
-        *(uint4 *)&As[buf][a_r][8 * a_k] = a0;
-        if constexpr (MI == 2) *(uint4 *)&As[buf][a_r + 32][8 * a_k] = a1;
-        *(uint4 *)&Ws[buf][w_r][16 * w_k] = make_uint4(widen2(wq.x, 0), widen2(wq.x, 16), widen2(wq.y, 0), widen2(wq.y, 16));
-        *(uint4 *)&Ws[buf][w_r][16 * w_k + 8] =
+        *(uint4 *)&As[h][buf][a_r][8 * a_k] = a0;
+        if constexpr (MI == 2) *(uint4 *)&As[h][buf][a_r + 32][8 * a_k] = a1;
+        *(uint4 *)&Ws[h][buf][w_r][16 * w_k] = make_uint4(widen2(wq.x, 0), widen2(wq.x, 16), widen2(wq.y, 0), widen2(wq.y, 16));
+        *(uint4 *)&Ws[h][buf][w_r][16 * w_k + 8] =
             make_uint4(widen2(wq.z, 0), widen2(wq.z, 16), widen2(wq.w, 0), widen2(wq.w, 16));
     };
 
@@ -1710,39 +1717,66 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+    // this half's chunks: c = 0 .. nkh - 1 is chunk h + KS c.  Both halves run nkmax rounds, one
+    // barrier each, whatever their own count (the launcher takes KS = 2 only when nk >= 2 KS).
     const int nk = (K + kGmK - 1) / kGmK;
-    load(0, 0);
+    const int nkh = (nk - h + KS - 1) / KS, nkmax = (nk + KS - 1) / KS;
+    load(h, 0);
 #pragma unroll
     for (int c = 1; c < kGmPD; ++c)
-        if (c < nk) load(c, c);
-    store(0, 0, 0);
+        if (c < nkh) load(h + KS * c, c);
+    store(0, 0, h);
     __syncthreads();
-    for (int kb = 0; kb < nk; kb += kGmPD) {
+    for (int cb = 0; cb < nkmax; cb += kGmPD) {
 #pragma unroll
         for (int u = 0; u < kGmPD; ++u) { // set indices stay constants
-            const int kc = kb + u;
-            if (kc >= nk) break;
-            const int buf = kc & 1;
-            if (kc + kGmPD < nk) load(kc + kGmPD, u); // set u held chunk kc, already in LDS
+            const int c = cb + u;
+            if (c >= nkmax) break; // uniform over the group
+            const int buf = c & 1;
+            if (c + kGmPD < nkh) load(h + KS * (c + kGmPD), u); // set u held chunk c, already in LDS
+            if (c < nkh) {
 #pragma unroll
-            for (int ks = 0; ks < kGmK / 32; ++ks) {
-                bf16x8_t a[MI], bw[2];
+                for (int ks = 0; ks < kGmK / 32; ++ks) {
+                    bf16x8_t a[MI], bw[2];
 #pragma unroll
-                for (int i = 0; i < MI; ++i)
-                    a[i] = as_bf16x8(*(const uint4 *)&As[buf][16 * MI * wm + 16 * i + l16][32 * ks + 8 * g]);
+                    for (int i = 0; i < MI; ++i)
+                        a[i] = as_bf16x8(*(const uint4 *)&As[h][buf][16 * MI * wm + 16 * i + l16][32 * ks + 8 * g]);
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
-                    bw[i] = as_bf16x8(*(const uint4 *)&Ws[buf][32 * wn + 16 * i + l16][32 * ks + 8 * g]);
+                    for (int i = 0; i < 2; ++i)
+                        bw[i] = as_bf16x8(*(const uint4 *)&Ws[h][buf][32 * wn + 16 * i + l16][32 * ks + 8 * g]);
 #pragma unroll
-                for (int mi = 0; mi < MI; ++mi)
+                    for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-                    for (int ni = 0; ni < 2; ++ni)
-                        acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mi], bw[ni], acc[mi][ni], 0, 0, 0);
+                        for (int ni = 0; ni < 2; ++ni)
+                            acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mi], bw[ni], acc[mi][ni], 0, 0, 0);
+                }
             }
             // buffer buf ^ 1's last readers finished before the previous barrier
-            if (kc + 1 < nk) store(buf ^ 1, (u + 1) % kGmPD, kc + 1);
+            if (c + 1 < nkh) store(buf ^ 1, (u + 1) % kGmPD, h + KS * (c + 1));
             __syncthreads();
         }
+    }
+    if constexpr (KS > 1) {
+        // half 1's sums to half 0 through LDS (the tiles are free: every half passed the loop's
+        // last barrier after its last read); half 0 adds them, in the same order in every group
+        static_assert(sizeof(As) >= 256 * MI * 8 * sizeof(float), "room for half 1's sums");
+        float *red = (float *)&As[0][0][0][0];
+        if (h == 1) {
+#pragma unroll
+            for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) red[((mi * 2 + ni) * 4 + r) * 256 + tid] = acc[mi][ni][r];
+        }
+        __syncthreads();
+        if (h == 1) return;
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[mi][ni][r] += red[((mi * 2 + ni) * 4 + r) * 256 + tid];
     }
 
     // lane: column n0 + 32 wn + 16 ni + l16, rows m0 + 16 MI wm + 16 mi + 4 g + r
@@ -1796,15 +1830,15 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const uint16_t *A, int M, int K
     }
 }
 
-template <int MI>
+template <int MI, int KS>
 static hipError_t gemm_q8_mi(const void *A, int M, int K, const int8_t *W, const float *s, int N, int epi,
                              const GemmOut &go, hipStream_t stream) {
-    const dim3 grid(((N + kGmT - 1) / kGmT) * ((M + 32 * MI - 1) / (32 * MI))), block(256);
+    const dim3 grid(((N + kGmT - 1) / kGmT) * ((M + 32 * MI - 1) / (32 * MI))), block(256 * KS);
     const uint16_t *a = (const uint16_t *)A;
-#define XNP_GEMM(E) hipLaunchKernelGGL((k_gemm_q8<E, false, MI>), grid, block, 0, stream, a, M, K, W, s, N, go)
+#define XNP_GEMM(E) hipLaunchKernelGGL((k_gemm_q8<E, false, MI, KS>), grid, block, 0, stream, a, M, K, W, s, N, go)
     if (go.a_f32) {
         if (epi != kStore) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((k_gemm_q8<kStore, true, MI>), grid, block, 0, stream, a, M, K, W, s, N, go);
+        hipLaunchKernelGGL((k_gemm_q8<kStore, true, MI, KS>), grid, block, 0, stream, a, M, K, W, s, N, go);
         return hipGetLastError();
     }
     switch (epi) {
@@ -1829,8 +1863,12 @@ hipError_t launch_gemm_q8(const void *A, int M, int K, const int8_t *W, const fl
     if (N <= 0 || K <= 0 || K % 16) return hipErrorInvalidValue;
     // 32-row tiles when 64-row ones would leave the chip's 1024 SIMDs under two waves each
     const int64_t groups64 = (int64_t)((N + kGmT - 1) / kGmT) * ((M + kGmT - 1) / kGmT);
-    return groups64 < 512 ? gemm_q8_mi<1>(A, M, K, W, s, N, epi, go, stream)
-                          : gemm_q8_mi<2>(A, M, K, W, s, N, epi, go, stream);
+    // two halves per group on alternate K chunks when K is long (32 chunks and more)
+    if (K >= 32 * kGmK)
+        return groups64 < 512 ? gemm_q8_mi<1, 2>(A, M, K, W, s, N, epi, go, stream)
+                              : gemm_q8_mi<2, 2>(A, M, K, W, s, N, epi, go, stream);
+    return groups64 < 512 ? gemm_q8_mi<1, 1>(A, M, K, W, s, N, epi, go, stream)
+                          : gemm_q8_mi<2, 1>(A, M, K, W, s, N, epi, go, stream);
 }
 
 // ---------------------------------------------------------------------------------------------
