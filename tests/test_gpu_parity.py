@@ -540,6 +540,101 @@ def test_int8_sliding_window_with_random_write_heads():
         p.assert_cache_equal(i)
 
 
+def test_the_int8_window_configuration_at_full_size_spot_checked():
+    # The int8 sliding-window workload at its full size: 1024 streams x 9 layers x 8 heads x 64, int8
+    # pages with a scale per (page, head), window 512 on 528-slot absolute rings, write heads
+    # U[0,4096), histories of U[64,1100] rows (the long ones wrap their ring twice), each row
+    # through the batched append with one slide per step, then two attend steps.  10 streams spread
+    # over the lengths (the longest and the shortest included) are mirrored on the oracle: outputs
+    # within 2e-2, then every live cache row, code and scale bit-exact.
+    S, L, H, SPAN, WIN = 1024, 9, 8, 528, 512
+    rng = np.random.default_rng(20261204)
+    heads = rng.integers(0, 4096, S)
+    lens = rng.integers(64, 1101, S)
+    order = np.argsort(-lens, kind="stable")
+    sample = sorted(set(order[::128].tolist()) | {int(order[0]), int(order[-1])})
+    mbps = SPAN // 16
+    pool = xnp.KvPool(num_layers=L, num_heads=H, num_blocks=S * mbps + 16, max_streams=S, max_blocks_per_stream=mbps,
+                      cache_dtype="i8", act_dtype="bf16", max_pos=1200, page_seed=17)
+    ids = [pool.init_state(SPAN) for _ in range(S)]
+    for sid in ids:
+        pool.start_ring(sid, "absolute", prefix=0)
+    orc = {i: oracle.Stream(L, H, 64, SPAN, cache="i8", act="bf16") for i in sample}
+    for i in sample:
+        orc[i].start_ring("absolute", prefix=0)
+    in_view = {i: 0 for i in sample}
+    written = np.zeros(S, np.int64)
+    g = torch.Generator(device=DEV).manual_seed(20261204)
+
+    def randn(*shape):
+        return torch.randn(shape, device=DEV, generator=g).to(torch.bfloat16)
+
+    def slide(i):  # xnp_ring_slide(prefix 0, span 528, window 512, drop 1, step) restated on the oracle
+        step = int(heads[i] + written[i])
+        if in_view[i] == WIN:
+            orc[i].evict(0, [(step - WIN) % SPAN])
+            in_view[i] -= 1
+        orc[i].set_ring_slot(step % SPAN)
+
+    kv = [randn(S, H, 64) for _ in range(2 * L)]
+    kvh = [host(t) for t in kv]
+    N = int(lens.max())
+    start = N - lens
+    for s in range(N):  # stream i joins at step N - lens[i] and appends one row per step
+        act = np.nonzero(start <= s)[0]
+        pool.slide_batch([ids[i] for i in act], 0, SPAN, WIN, 1, heads[act] + written[act])
+        pool.begin([ids[i] for i in act])
+        for layer in range(L):
+            pool.append(layer, kv[2 * layer][:len(act)], kv[2 * layer + 1][:len(act)])
+        pool.end()
+        for i in sample:
+            if start[i] <= s:
+                slide(i)
+                j = int(np.searchsorted(act, i))
+                for layer in range(L):
+                    orc[i].append(layer, kvh[2 * layer][j:j + 1], kvh[2 * layer + 1][j:j + 1])
+                orc[i].commit(1)
+                in_view[i] += 1
+        written[act] += 1
+    torch.cuda.synchronize()
+    for _ in range(2):
+        pool.slide_batch(ids, 0, SPAN, WIN, 1, heads + written)
+        for i in sample:
+            slide(i)
+        pool.begin(ids)
+        for layer in range(L):
+            q, k, v = randn(S, H, 64), randn(S, H, 64), randn(S, H, 64)
+            out = torch.empty((S, H, 64), dtype=torch.bfloat16, device=DEV)
+            pool.attend(layer, q, k, v, out, 0.125)
+            torch.cuda.synchronize()
+            got, qh, kh, vh = host(out[sample]), host(q[sample]), host(k[sample]), host(v[sample])
+            for j, i in enumerate(sample):
+                want, _ = orc[i].attend(layer, qh[j:j + 1], kh[j:j + 1], vh[j:j + 1])
+                assert rel_err(got[j:j + 1], want) <= 2e-2, (layer, i, int(lens[i]))
+        pool.end()
+        for i in sample:
+            orc[i].commit(1)
+            in_view[i] += 1
+        written += 1
+    # page by page: a ring written from an arbitrary head holds pages only where it has written
+    for i in sample:
+        valid = orc[i].ring_info()["valid"]
+        for pg in range(mbps):
+            live = valid[16 * pg:16 * pg + 16]
+            if not live.any():
+                continue
+            for layer in range(L):
+                for kvi in (0, 1):
+                    rows = torch.empty((16, H, 64), dtype=torch.int8, device=DEV)
+                    sc = torch.zeros((1, H), dtype=torch.float32, device=DEV)
+                    pool.read_rows(ids[i], layer, kvi, 16 * pg, rows, sc)
+                    torch.cuda.synchronize()
+                    _, q8, osc = orc[i].read_rows(layer, kvi, 16 * pg, 16)
+                    assert np.array_equal(rows.cpu().numpy()[live], q8[live]), (i, pg, layer, kvi)
+                    assert np.array_equal(sc.cpu().numpy().view(np.uint32), osc.view(np.uint32)), (i, pg, layer, kvi)
+    assert pool.check_tables() == 0
+
+
 # ---- raw rows ------------------------------------------------------------------------------------
 @pytest.mark.parametrize("cache", ["bf16", "i8"])
 def test_rows_written_raw_read_back_the_same(cache):
