@@ -5,6 +5,8 @@ oracle's bit for bit; attention outputs are within 1e-5 relative (f32) or 2e-2 r
 int8 KV) of the oracle's f32 outputs, where relative error is max|got - want| / max|want| over
 each (row, head) vector.
 """
+import types
+
 import numpy as np
 import pytest
 import torch
@@ -690,7 +692,6 @@ def test_the_decode_configuration_at_full_size_spot_checked():
     # Every stream runs; 18 of them, spread over the longest-first order (the longest and the
     # shortest included), are checked against the oracle over two steps: outputs within 2e-2,
     # then every cache row bit-exact.
-    import types
     S, L, H, cap = 1024, 9, 8, 1040
     rng = np.random.default_rng(20261203)
     lens = rng.integers(1, 1025, S)
@@ -761,6 +762,35 @@ def test_prefill_of_a_grouped_head_prompt_at_config3_shape_sample():
     assert p.prefill(256) <= 2e-2
     for i in range(0, 8, 3):
         p.assert_cache_equal(i)
+
+
+def test_the_prefill_configuration_at_full_size_spot_checked():
+    # The prefill workload at its full size: 64 streams x 256-position prompts x 9 layers, bf16,
+    # shuffled pages; every stream runs, 8 of them go through the oracle: outputs within 2e-2, then
+    # every cache row the prompt wrote bit-exact.
+    S, L, H, T = 64, 9, 8, 256
+    pool = xnp.KvPool(num_layers=L, num_heads=H, num_blocks=S * 17 + 8, max_streams=S, max_blocks_per_stream=17,
+                      cache_dtype="bf16", act_dtype="bf16", max_pos=1024, page_seed=21)
+    ids = [pool.init_state(272) for _ in range(S)]
+    sample = list(range(0, S, 9))
+    orc = {i: oracle.Stream(L, H, 64, 272, cache="bf16", act="bf16") for i in sample}
+    g = torch.Generator(device=DEV).manual_seed(20261206)
+    pool.begin(ids, t=T)
+    for layer in range(L):
+        q, k, v = (torch.randn((S, T, H, 64), device=DEV, generator=g).to(torch.bfloat16) for _ in range(3))
+        out = torch.empty((S, T, H, 64), dtype=torch.bfloat16, device=DEV)
+        pool.attend(layer, q, k, v, out, 0.125)
+        torch.cuda.synchronize()
+        got, qh, kh, vh = host(out[sample]), host(q[sample]), host(k[sample]), host(v[sample])
+        for j, i in enumerate(sample):
+            want, _ = orc[i].attend(layer, qh[j], kh[j], vh[j])
+            assert rel_err(got[j], want) <= 2e-2, (layer, i)
+    pool.end()
+    for i in sample:
+        orc[i].commit(T)
+    shim = types.SimpleNamespace(pool=pool, ids=ids, orc=orc, L=L, H=H, KVH=H, cache="bf16")
+    for i in sample:
+        Pair.assert_cache_equal(shim, i)
 
 
 def test_prompts_on_reopened_streams_use_live_pages():
