@@ -1,6 +1,6 @@
 // Host side of the flow LM around the paged transformer (ptts/src/flow_lm.rs, mlp.rs,
 // conditioners.rs, tts_model.rs:297-378): weights uploaded once, then text prompts and frames for
-// batches of a pool's streams.  Two precisions: f32 (kernels.hip's f32 linears with the norms
+// batches of a pool's streams.  Two precisions: f32 (k_layer.hip's f32 linears with the norms
 // fused, the pool's xnp_attend), and q8 (int8 weights on the MFMA GEMM with its epilogues, bf16
 // activations, the transformer as xnp_layer_step).
 #include "../../include/xnp_kv.h"

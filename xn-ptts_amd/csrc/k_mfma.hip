@@ -1,0 +1,507 @@
+// Attention on MFMA (bf16): the causal prompt prefill with its fused append (k_prefill_mfma) and the
+// grouped-head decode (k_decode_gqa).
+#include "kernels_common.h"
+
+namespace xnp {
+
+// ---------------------------------------------------------------------------------------------
+// prompt prefill on MFMA (bf16 cache and activations), transformer.rs:231-248 batched, with the
+// append of the prompt's K/V rows (complete_kv, transformer.rs:84-91) fused in.
+//
+// One work group of 8 waves per (stream, head).  Query rows are taken in rounds of 256: 16 tiles
+// of 16 rows, wave w owning tiles w and 15 - w of the round, so that every wave sees about the
+// same number of causal keys.  Keys are staged through LDS in chunks of 64 (four pages), K and
+// V both as [key][dim], double-buffered, with the next chunk's loads in flight while one is
+// attended over.  Keys before the prompt come from the pages; the prompt's own keys come
+// from the k/v inputs, rotated at their position and rounded to bf16, and are written into
+// their pages during the last round, so that each is written exactly once and never read back
+// from HBM.
+//
+// Both contractions are computed transposed so that P never leaves registers:
+//   S^T = K Q^T   v_mfma_f32_16x16x32_bf16, A = K rows from LDS (lane: key lane%16, 8 dims),
+//                 B = the wave's rotated query rows (registers; lane: query lane%16, 8 dims);
+//                 the result holds, per lane, query row lane%16 against keys 4(lane/16) .. +3;
+//   softmax       online per query row; its max and sum reduce over the 4 lanes of a row;
+//   O^T += V^T P^T  B = P^T straight from the S^T registers (lane: query lane%16, 8 keys),
+//                 A = V^T by transposed LDS reads of the same 8 keys (ds_read_b64_tr_b16).
+// A and B always hold the same key (or dim) in the same (lane / 16, element) slot, so each
+// contraction is right whatever order the instruction walks k in.
+
+
+constexpr int kPfKeys = 64;      // keys per chunk (four pages)
+constexpr int kPfLd = 72;        // LDS row length in bf16: 64 + 8 of padding, rows 16-byte aligned
+constexpr int kPfWaves = 8;      // waves per work group
+constexpr int kPfRound = 256;    // query rows per round: 8 waves x 2 tiles x 16 rows
+constexpr int kPfMaxPages = 512; // page ids a work group keeps in LDS
+static_assert(kPfMaxPages >= kLaneBlocks * 8, "every page of a stream fits (a pool refuses more than 60 x 8)");
+static_assert(64 * kPfWaves == kPfKeys * 8, "one thread stages 16 bytes of one key per chunk");
+
+__global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4))) void k_prefill_mfma(
+    PoolView pv, BatchView bv, int layer, const void *q, const void *knew, const void *vnew, void *out, float qmul,
+    int fused) {
+    __shared__ __attribute__((aligned(16))) uint16_t ks[2 * kPfKeys][kPfLd]; // K of two chunks, [key][dim]
+    __shared__ __attribute__((aligned(16))) uint16_t vs[2 * kPfKeys][kPfLd]; // V of two chunks, [key][dim]
+    __shared__ int32_t spages[kPfMaxPages];
+    const int t = bv.t;
+    const int h = blockIdx.x % pv.H, b = blockIdx.x / pv.H;
+    const StreamPlan P = bv.plans[b];
+    const int32_t *tab = pv.tables + (size_t)P.sid * pv.mbps;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, l16 = lane & 15;
+    const int c0 = P.write_slot; // slot (= position) of prompt row 0
+    const int kvh = h / (pv.H / pv.KVH);
+    const size_t page_elems = (size_t)pv.KVH * kBlock * kHeadDim;
+    uint16_t *kpages = (uint16_t *)pv.pages + tile_index(pv, layer, 0, 0, kvh) * (kBlock * kHeadDim);
+    uint16_t *vpages = (uint16_t *)pv.pages + tile_index(pv, layer, 1, 0, kvh) * (kBlock * kHeadDim);
+    // the stream's page ids for every key any round sees, read once
+    for (int i = tid; i < min((c0 + t + kBlock - 1) / kBlock, kPfMaxPages); i += 64 * kPfWaves) spages[i] = tab[i];
+    // this thread's share of a chunk: 16 bytes (8 dims) of one key's K and V
+    const int skey = tid >> 3, spart = tid & 7;
+
+    const int nqt = (t + 15) / 16;
+    for (int tq0 = 0; tq0 < nqt; tq0 += kPfRound / 16) {
+        const int nq = min(kPfRound / 16, nqt - tq0);
+        const bool last = tq0 + nq == nqt;
+        // this wave's tiles: (w, nq-1-w) for w < nq/2; the middle one alone when nq is odd
+        int tile[2] = {-1, -1};
+        if (w < nq / 2) {
+            tile[0] = tq0 + w;
+            tile[1] = tq0 + nq - 1 - w;
+        } else if (w == nq / 2 && (nq & 1)) {
+            tile[0] = tq0 + w;
+        }
+        const int kend = c0 + min(t, 16 * (tq0 + nq)); // the round's rows see keys [0, kend)
+        const int nch = (kend + kPfKeys - 1) / kPfKeys;
+
+        // B operands of S^T: query row 16 tile + l16, dims 32 kc + 8 g .. +7, rotated at its
+        // position and rounded to bf16 as the reference's bf16 q is.  Every load is issued
+        // before any is used (rows past the prompt read row t - 1 and are zeroed after).
+        bf16x8_t qb[2][2];
+        float m[2], lsum[2]; // running max (scaled, log2 units) and this lane's share of the sum
+        f32x4_t o[2][4];
+        {
+            uint4 qraw[2][2];
+            float4 qcs[2][2][2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int qr = min(16 * max(tile[j], 0) + l16, t - 1);
+                const uint16_t *qp = (const uint16_t *)q + (((size_t)P.out_row * t + qr) * pv.H + h) * kHeadDim;
+                const float4 *cs = (const float4 *)(pv.rope + (size_t)(P.pos + qr) * (kHeadDim / 2));
+#pragma unroll
+                for (int kc = 0; kc < 2; ++kc) {
+                    qraw[j][kc] = *(const uint4 *)(qp + 32 * kc + 8 * g);
+                    qcs[j][kc][0] = cs[(32 * kc + 8 * g) / 4];
+                    qcs[j][kc][1] = cs[(32 * kc + 8 * g) / 4 + 1];
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                m[j] = -1e30f;
+                lsum[j] = 0.f;
+#pragma unroll
+                for (int dg = 0; dg < 4; ++dg) o[j][dg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                const bool live = tile[j] >= 0 && 16 * tile[j] + l16 < t;
+#pragma unroll
+                for (int kc = 0; kc < 2; ++kc) {
+                    const uint32_t *u = (const uint32_t *)&qraw[j][kc];
+                    const float4 ca = qcs[j][kc][0], cb = qcs[j][kc][1];
+                    const float cf[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w}; // cos, sin of 4 pairs
+                    uint32_t o4[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float x0 = bf16_value(u[i] & 0xffffu), x1 = bf16_value(u[i] >> 16);
+                        const float c = cf[2 * i], s = cf[2 * i + 1];
+                        const float a = x0 * c, bb = x1 * s, e = x0 * s, f = x1 * c;
+                        o4[i] = live ? pack_bf16(a - bb, e + f) : 0u;
+                    }
+                    qb[j][kc] = as_bf16x8(make_uint4(o4[0], o4[1], o4[2], o4[3]));
+                }
+            }
+        }
+        __syncthreads(); // spages written
+
+        // Loads run one chunk ahead: chunk c's registers are consumed (rotated, stored to LDS
+        // buffer c & 1) at step c, which then issues chunk c + 1's loads into them.
+        struct Stage {
+            uint4 k, v, rope; // the key's K and V pieces, 4 (cos, sin) pairs as packed bf16
+            int info;         // bit 0: a prompt key, bit 1: write it to its page; page id above
+        };
+        auto issue = [&](int c, Stage &st) {
+            const int slot = c * kPfKeys + skey;
+            const bool in = c < nch && slot < kend;
+            const bool fresh = fused && slot >= c0; // a prompt key: from the inputs, rotated here
+            const int page = in ? spages[min(slot >> 4, kPfMaxPages - 1)] : -1;
+            const bool ok = page >= 0 && page < pv.NB;
+            const size_t poff = (size_t)(ok ? page : 0) * page_elems + (slot & 15) * kHeadDim + 8 * spart;
+            const int i = fresh ? min(slot - c0, t - 1) : 0;
+            const size_t arow = (((size_t)P.out_row * t + i) * pv.KVH + kvh) * kHeadDim + 8 * spart;
+            st.k = st.v = make_uint4(0, 0, 0, 0);
+            if (in && fresh) {
+                st.k = ld_stream((const uint16_t *)knew + arow);
+                st.v = ld_stream((const uint16_t *)vnew + arow);
+            } else if (in && ok) {
+                st.k = ld_stream(kpages + poff);
+                st.v = ld_stream(vpages + poff);
+            }
+            st.rope = *(const uint4 *)(pv.rope16 + (size_t)(P.key_pos + i) * (kHeadDim / 2) + 4 * spart);
+            st.info = (in && fresh ? 1 : 0) | (in && fresh && ok && last ? 2 : 0) | ((ok ? page : 0) << 2);
+        };
+        auto step = [&](int c, Stage &st) {
+            const int buf = c & 1, kbase = c * kPfKeys, lb = buf * kPfKeys;
+            // rotate a prompt key at its position; store this thread's piece of the chunk
+            {
+                uint4 kk = st.k;
+                if (st.info & 1) {
+                    const uint32_t *r = (const uint32_t *)&st.rope;
+                    const uint32_t *u = (const uint32_t *)&st.k;
+                    uint32_t o4[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float x0 = bf16_value(u[e] & 0xffffu), x1 = bf16_value(u[e] >> 16);
+                        const float cc = bf16_value(r[e] & 0xffffu), sn = bf16_value(r[e] >> 16);
+                        const float a = x0 * cc, bb = x1 * sn, ee = x0 * sn, f = x1 * cc;
+                        o4[e] = pack_bf16(a - bb, ee + f);
+                    }
+                    kk = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+                }
+                if (st.info & 2) { // complete_kv: the prompt's rows go into their pages once
+                    const size_t poff = (size_t)(st.info >> 2) * page_elems + ((kbase + skey) & 15) * kHeadDim + 8 * spart;
+                    *(uint4 *)(kpages + poff) = kk;
+                    *(uint4 *)(vpages + poff) = st.v;
+                }
+                *(uint4 *)&ks[lb + skey][8 * spart] = kk;
+                *(uint4 *)&vs[lb + skey][8 * spart] = st.v;
+            }
+            issue(c + 1, st);
+            __syncthreads(); // chunk c is in LDS; every reader of chunk c - 2 (same buffer) is done
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int r0 = c0 + 16 * tile[j]; // slot of the tile's first row
+                // skip a tile when every key of the chunk comes after all of its rows
+                if (tile[j] < 0 || kbase > r0 + 15) continue;
+                f32x4_t s[4];
+#pragma unroll
+                for (int kg = 0; kg < 4; ++kg) {
+                    s[kg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int kc = 0; kc < 2; ++kc) {
+                        const bf16x8_t a = as_bf16x8(*(const uint4 *)&ks[lb + 16 * kg + l16][32 * kc + 8 * g]);
+                        s[kg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qb[j][kc], s[kg], 0, 0, 0);
+                    }
+                }
+                // lane: query slot r0 + l16 against key slots kbase + 16 kg + 4 g + r
+                if (kbase + kPfKeys - 1 > r0) { // the chunk reaches past the tile's first row: mask
+                    const int qs = r0 + l16;
+#pragma unroll
+                    for (int kg = 0; kg < 4; ++kg)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (kbase + 16 * kg + 4 * g + r > qs) s[kg][r] = -INFINITY;
+                }
+                float mx = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
+#pragma unroll
+                for (int kg = 1; kg < 4; ++kg)
+                    mx = fmaxf(mx, fmaxf(fmaxf(s[kg][0], s[kg][1]), fmaxf(s[kg][2], s[kg][3])));
+                mx = fmaxf(mx, __shfl_xor(mx, 16));
+                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                // lazy rescaling, as in decode: the row's sum and accumulators move to a new max only
+                // when some row of the wave saw its max grow by more than 8 (log2 units); until then
+                // exponents are taken against the older max and stay below 2^8
+                const float mn = fmaxf(m[j], mx * qmul);
+                if (__any(mn > m[j] + 8.f)) {
+                    const float alpha = fast_exp2(m[j] - mn);
+                    lsum[j] *= alpha;
+#pragma unroll
+                    for (int dg = 0; dg < 4; ++dg)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) o[j][dg][r] *= alpha;
+                    m[j] = mn;
+                }
+                const float mref = m[j];
+                float psum = 0.f;
+                uint32_t pk[4][2];
+#pragma unroll
+                for (int kg = 0; kg < 4; ++kg) {
+                    float p[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        p[r] = fast_exp2(__builtin_fmaf(s[kg][r], qmul, -mref));
+                        psum += p[r];
+                    }
+                    pk[kg][0] = pack_bf16(p[0], p[1]);
+                    pk[kg][1] = pack_bf16(p[2], p[3]);
+                }
+                lsum[j] += psum;
+#pragma unroll
+                for (int kp = 0; kp < 2; ++kp) {
+                    // k slots: keys 32 kp + 4 g .. +3 (elements 0-3) and 32 kp + 16 + 4 g .. +3 (4-7)
+                    const bf16x8_t pb =
+                        as_bf16x8(make_uint4(pk[2 * kp][0], pk[2 * kp][1], pk[2 * kp + 1][0], pk[2 * kp + 1][1]));
+#pragma unroll
+                    for (int dg = 0; dg < 4; ++dg) {
+                        // V^T: lane gets dim 16 dg + l16 of the same eight keys, by two transposed reads
+                        const uint16_t *vp = &vs[lb + 32 * kp + 4 * g + (l16 >> 2)][16 * dg + 4 * (l16 & 3)];
+                        const uint2 lo = lds_read_tr16(vp), hi = lds_read_tr16(vp + 16 * kPfLd);
+                        const bf16x8_t a = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+                        o[j][dg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, o[j][dg], 0, 0, 0);
+                    }
+                }
+            }
+        };
+        Stage st;
+        issue(0, st);
+        for (int c = 0; c < nch; ++c) step(c, st);
+        __syncthreads(); // the next round's staging overwrites both buffers
+
+        // out[row][h][16 dg + 4 g .. +3] = O / l, the row's sum reduced over its 4 lanes
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            float l = lsum[j];
+            l += __shfl_xor(l, 16);
+            l += __shfl_xor(l, 32);
+            const int qrow = 16 * tile[j] + l16;
+            if (tile[j] < 0 || qrow >= t) continue;
+            const float inv = 1.0f / l;
+            uint16_t *orow = (uint16_t *)out + (((size_t)P.out_row * t + qrow) * pv.H + h) * kHeadDim;
+#pragma unroll
+            for (int dg = 0; dg < 4; ++dg)
+                *(uint2 *)(orow + 16 * dg + 4 * g) = make_uint2(pack_bf16(o[j][dg][0] * inv, o[j][dg][1] * inv),
+                                                                pack_bf16(o[j][dg][2] * inv, o[j][dg][3] * inv));
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Grouped-head decode on MFMA: bf16 pages and queries, 2 to 16 query heads per kv head, no ring
+// prefix.  One work group per (stream, kv head), whose G query heads are the 16 columns of the
+// MFMA tiles (columns past G hold zeros), so that each page is read once and its 16 keys meet all
+// G heads in a few instructions.  The contractions are the prompt prefill's, transposed so that P
+// never leaves registers:
+//   S^T = K Q^T      v_mfma_f32_16x16x32_bf16, A = the page's K rows (lane: key l16, dims
+//                    32 kc + 8 g .. +7) from a wave-private LDS tile that streamed whole-line loads
+//                    fill, B = the rotated query rows; lane (l16, g) gets the scores of keys
+//                    4 g .. 4 g + 3 for query head l16;
+//   softmax          online per query column, its max and sum over the 4 lanes of the column;
+//   O^T += V^T P^T   v_mfma_f32_16x16x16_bf16, B = P^T straight from the S^T registers, A = V^T by
+//                    transposed reads (ds_read_b64_tr_b16) of the page's V, copied into a
+//                    wave-private LDS tile.
+// Pages, SPLIT waves per group, the fused append and the LDS merge are attend_core's.
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+template <int SPLIT>
+__global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4))) void k_decode_gqa(
+    PoolView pv, BatchView bv, int layer, const void *q, const void *knew, const void *vnew, void *out, float qmul,
+    int fused) {
+    constexpr int DEPTH = 2; // pages in flight ahead of the one being reduced
+    __shared__ __attribute__((aligned(16))) uint16_t vt[SPLIT][kBlock][kPfLd]; // each wave's V tile, [key][dim]
+    __shared__ __attribute__((aligned(16))) uint16_t kt[SPLIT][kBlock][kPfLd]; // each wave's K tile, [key][dim]
+    __shared__ float part[SPLIT][16][kPartStride];
+    const int G = pv.H / pv.KVH;
+    // XCD runs as in k_decode: in runs of 8 KVH groups, XCD x takes the kv heads of stream x of the run
+    const int b = blockIdx.x, full = bv.n / 8 * 8;
+    const int sidx = b < full * pv.KVH ? b / (8 * pv.KVH) * 8 + b % 8 : full + (b - full * pv.KVH) / pv.KVH;
+    const int kvh = b < full * pv.KVH ? b % (8 * pv.KVH) / 8 : (b - full * pv.KVH) % pv.KVH;
+    const char *rec = bv.recs + (size_t)sidx * bv.rec_stride;
+    const StreamRec R = *(const StreamRec *)rec;
+    const int32_t *rec_pages = (const int32_t *)(rec + sizeof(StreamRec));
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, l16 = lane & 15;
+    const int nb = R.nblk > w ? (R.nblk - w + SPLIT - 1) / SPLIT : 0; // this wave's pages
+
+    // per-page metadata, lane j holding page w + j * SPLIT (as attend_core)
+    int my_page = 0;
+    uint32_t my_seen = 0;
+    const int pg_raw = w + lane * SPLIT < pv.mbps ? rec_pages[w + lane * SPLIT] : -1;
+    if (lane < nb) {
+        const int base = (w + lane * SPLIT) * kBlock;
+        uint32_t seen = 0xffffu;
+        if (R.mask_off >= 0) seen = (bv.masks[R.mask_off + (base >> 5)] >> (base & 16)) & 0xffffu;
+        const int nvalid = R.span - base;
+        if (nvalid < kBlock) seen &= (1u << max(nvalid, 0)) - 1u;
+        const bool ok = pg_raw >= 0 && pg_raw < pv.NB;
+        my_page = ok ? pg_raw : 0;
+        my_seen = ok ? seen : 0;
+    }
+
+    // B operands of S^T: query head kvh G + l16, dims 32 kc + 8 g .. +7, rotated at R.pos and
+    // rounded to bf16 (zeros past G)
+    bf16x8_t qb[2];
+    {
+        const bool live = l16 < G;
+        const int hq = kvh * G + min(l16, G - 1);
+        const uint16_t *qp = (const uint16_t *)q + ((size_t)R.b * pv.H + hq) * kHeadDim;
+        const float4 *cs = (const float4 *)(pv.rope + (size_t)R.pos * (kHeadDim / 2));
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) {
+            const uint4 raw = *(const uint4 *)(qp + 32 * kc + 8 * g);
+            const float4 ca = cs[(32 * kc + 8 * g) / 4], cb = cs[(32 * kc + 8 * g) / 4 + 1];
+            const float cf[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w}; // cos, sin of 4 pairs
+            const uint32_t *u = (const uint32_t *)&raw;
+            uint32_t o4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float x0 = bf16_value(u[i] & 0xffffu), x1 = bf16_value(u[i] >> 16);
+                const float c = cf[2 * i], s = cf[2 * i + 1];
+                const float a = x0 * c, bb = x1 * s, e = x0 * s, f = x1 * c;
+                o4[i] = live ? pack_bf16(a - bb, e + f) : 0u;
+            }
+            qb[kc] = as_bf16x8(make_uint4(o4[0], o4[1], o4[2], o4[3]));
+        }
+    }
+
+    const uint16_t *kbase = (const uint16_t *)pv.pages + tile_index(pv, layer, 0, 0, kvh) * (kBlock * kHeadDim);
+    const uint16_t *vbase = (const uint16_t *)pv.pages + tile_index(pv, layer, 1, 0, kvh) * (kBlock * kHeadDim);
+    const size_t page_elems = (size_t)pv.KVH * kBlock * kHeadDim;
+
+    float m = -1e30f, lsum = 0.f; // running max (scaled, log2 units) and this lane's share of the sum
+    f32x4_t o[4];                 // O^T: dims 16 dg + 4 g + r, query head l16
+#pragma unroll
+    for (int dg = 0; dg < 4; ++dg) o[dg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    // a page's K and V tiles, each in two streamed 1 KB loads (keys lane / 8 and 8 + lane / 8,
+    // dims 8 (lane % 8) ..): every load covers whole 128-byte lines.  Loaded straight in the MFMA's
+    // A layout, each load would take half of every line, and a streamed line is gone before the
+    // other half is read (33 -> 36.6 us at 1 kv head); K therefore goes through an LDS tile too.
+    // Measured against plain loads in A layout: 1 kv head 33.4 -> 28.8 us, 2: 56.5 -> 50.5, 4:
+    // 101.5 -> 89 us.
+    auto load = [&](uint4 (&kr)[2], uint4 (&vr)[2], int j) {
+        const size_t pe = (size_t)__builtin_amdgcn_readlane(my_page, j) * page_elems;
+        kr[0] = ld_stream(kbase + pe + 8 * lane);
+        kr[1] = ld_stream(kbase + pe + 512 + 8 * lane);
+        vr[0] = ld_stream(vbase + pe + 8 * lane);
+        vr[1] = ld_stream(vbase + pe + 512 + 8 * lane);
+    };
+    auto process = [&](const uint4 (&kr)[2], const uint4 (&vr)[2], int j) {
+        const uint32_t seen = __builtin_amdgcn_readlane(my_seen, j);
+        f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        // K through the wave's LDS tile into A layout (key l16, dims 32 kc + 8 g); a wave's LDS
+        // accesses complete in order, so no barrier
+        *(uint4 *)&kt[w][lane >> 3][8 * (lane & 7)] = kr[0];
+        *(uint4 *)&kt[w][8 + (lane >> 3)][8 * (lane & 7)] = kr[1];
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc)
+            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(*(const uint4 *)&kt[w][l16][32 * kc + 8 * g]), qb[kc],
+                                                       s, 0, 0, 0);
+        // lane: query head l16 against keys 4 g + r of the page
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (!((seen >> (4 * g + r)) & 1u)) s[r] = -INFINITY;
+        float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        // lazy rescaling, as in attend_core
+        const float mn = fmaxf(m, mx * qmul);
+        if (__any(mn > m + 8.f)) {
+            const float alpha = fast_exp2(m - mn);
+            lsum *= alpha;
+#pragma unroll
+            for (int dg = 0; dg < 4; ++dg)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) o[dg][r] *= alpha;
+            m = mn;
+        }
+        float p[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            p[r] = fast_exp2(__builtin_fmaf(s[r], qmul, -m));
+            lsum += p[r];
+        }
+        const s16x4_t pt = __builtin_bit_cast(s16x4_t, make_uint2(pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3])));
+        // the page's V into this wave's LDS tile (rows lane / 8 and 8 + lane / 8, dims 8 (lane % 8) ..);
+        // an unseen row weighs 0 but its bytes may be anything, so it goes in as zeros (0 * NaN would
+        // be NaN)
+        const uint32_t keep0 = ((seen >> (lane >> 3)) & 1u) ? ~0u : 0u;
+        const uint32_t keep1 = ((seen >> (8 + (lane >> 3))) & 1u) ? ~0u : 0u;
+        *(uint4 *)&vt[w][lane >> 3][8 * (lane & 7)] =
+            make_uint4(vr[0].x & keep0, vr[0].y & keep0, vr[0].z & keep0, vr[0].w & keep0);
+        *(uint4 *)&vt[w][8 + (lane >> 3)][8 * (lane & 7)] =
+            make_uint4(vr[1].x & keep1, vr[1].y & keep1, vr[1].z & keep1, vr[1].w & keep1);
+#pragma unroll
+        for (int dg = 0; dg < 4; ++dg) {
+            // V^T: lane gets dim 16 dg + l16 of keys 4 g .. 4 g + 3
+            const uint2 a = lds_read_tr16(&vt[w][4 * g + (l16 >> 2)][16 * dg + 4 * (l16 & 3)]);
+            o[dg] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, a), pt, o[dg], 0, 0, 0);
+        }
+    };
+
+    uint4 kb[DEPTH + 1][2], vb[DEPTH + 1][2];
+    // complete_kv: the wave that owns the write page appends the kv head's new row, as in attend_core
+    const int wblk = R.write_slot >> 4, wj = wblk / SPLIT;
+    const bool owner = fused && w == wblk % SPLIT;
+    const bool early = !owner || wj >= DEPTH;
+    if (early) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) load(kb[d], vb[d], d);
+    }
+    if (owner) {
+        const int slot = R.write_slot;
+        const size_t arow = (size_t)R.b * pv.KVH + kvh;
+        const bool fresh = (R.flags & 1) ? (R.flags & 2) != 0 : ((slot & 15) == 0);
+        append_row_wave<DT_BF16, true>(pv, layer, __builtin_amdgcn_readlane(my_page, wj), slot & 15, kvh, R.key_pos,
+                                       (const char *)knew + arow * kHeadDim * 2, (const char *)vnew + arow * kHeadDim * 2,
+                                       fresh);
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+    }
+    if (!early) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) load(kb[d], vb[d], d);
+    }
+    for (int j = 0; j < nb; j += DEPTH + 1) {
+#pragma unroll
+        for (int u = 0; u <= DEPTH; ++u) {
+            load(kb[(u + DEPTH) % (DEPTH + 1)], vb[(u + DEPTH) % (DEPTH + 1)], j + u + DEPTH);
+            process(kb[u], vb[u], j + u);
+        }
+    }
+
+    // the column's sum over its 4 lanes; the waves' shares through LDS; wave 0 writes the G heads
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+#pragma unroll
+    for (int dg = 0; dg < 4; ++dg)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) part[w][l16][16 * dg + 4 * g + r] = o[dg][r];
+    if (g == 0) {
+        part[w][l16][64] = m;
+        part[w][l16][65] = lsum;
+    }
+    __syncthreads();
+    if (w != 0) return;
+    for (int e = 0; e < G; ++e) {
+        float M = -1e30f;
+#pragma unroll
+        for (int k = 0; k < SPLIT; ++k) M = fmaxf(M, part[k][e][64]);
+        float L = 0.f, A = 0.f;
+#pragma unroll
+        for (int k = 0; k < SPLIT; ++k) {
+            const float a = fast_exp2(part[k][e][64] - M);
+            L = __builtin_fmaf(part[k][e][65], a, L);
+            A = __builtin_fmaf(part[k][e][lane], a, A);
+        }
+        ((uint16_t *)out)[((size_t)R.b * pv.H + kvh * G + e) * kHeadDim + lane] = (uint16_t)bf16_bits(A / L);
+    }
+}
+
+hipError_t launch_decode_gqa(const PoolView &pv, const BatchView &bv, int layer, const void *q, const void *k,
+                             const void *v, void *out, float scale, bool fused, hipStream_t stream,
+                             const LaunchTiming &tm) {
+    const float qmul = scale * 1.4426950408889634f;
+    const dim3 grid(bv.n * pv.KVH);
+    const int f = fused ? 1 : 0;
+    switch (bv.split) {
+    case 1: XNP_LAUNCH((k_decode_gqa<1>), grid, dim3(64), stream, tm, pv, bv, layer, q, k, v, out, qmul, f); break;
+    case 2: XNP_LAUNCH((k_decode_gqa<2>), grid, dim3(128), stream, tm, pv, bv, layer, q, k, v, out, qmul, f); break;
+    case 4: XNP_LAUNCH((k_decode_gqa<4>), grid, dim3(256), stream, tm, pv, bv, layer, q, k, v, out, qmul, f); break;
+    case 8: XNP_LAUNCH((k_decode_gqa<8>), grid, dim3(512), stream, tm, pv, bv, layer, q, k, v, out, qmul, f); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill_mfma(const PoolView &pv, const BatchView &bv, int layer, const void *q, const void *k,
+                               const void *v, void *out, float scale, bool fused, hipStream_t stream,
+                               const LaunchTiming &tm) {
+    XNP_LAUNCH(k_prefill_mfma, dim3(bv.n * pv.H), dim3(64 * kPfWaves), stream, tm, pv, bv, layer, q, k, v, out,
+               scale * 1.4426950408889634f, fused ? 1 : 0);
+    return hipGetLastError();
+}
+
+} // namespace xnp

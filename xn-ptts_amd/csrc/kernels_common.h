@@ -1,0 +1,245 @@
+// Device helpers shared by the HIP kernel files of the paged flow-LM KV cache (gfx950, wave64).
+//
+// Bit-exactness contract with the CPU restatement: the library is built with
+// -ffp-contract=off, RoPE rotates with host-computed cos/sin tables, bf16 rounding is
+// round-to-nearest-even on the f32 bits, int8 quantization is rint(y / s) clamped to +-127 with
+// IEEE division.  The attention arithmetic (dots, softmax, weighted sums) is f32 in an order of
+// its own and is checked to a tolerance, not bit for bit.
+#pragma once
+
+#include "xnp_internal.h"
+
+#include <hip/hip_ext.h>
+
+#include <algorithm>
+
+namespace xnp {
+
+
+// Launch a kernel; with timing events, through hipExtLaunchKernel so that the events bracket the
+// kernel alone.  Without them, a plain launch: the form a stream capture (hipGraph) records.
+#define XNP_LAUNCH(kernel, grid, block, stream, tm, ...)                                            \
+    do {                                                                                           \
+        if ((tm).start || (tm).stop)                                                               \
+            hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, (tm).start, (tm).stop, 0, __VA_ARGS__); \
+        else                                                                                       \
+            hipLaunchKernelGGL(kernel, grid, block, 0, stream, __VA_ARGS__);                       \
+    } while (0)
+
+// ---------------------------------------------------------------------------------------------
+// element helpers
+
+__device__ __forceinline__ float bf16_value(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+// Round to bf16 with v_cvt_pk_bf16_f32: round to nearest even, NaN kept quiet.  The same bits as
+// the CPU restatement's software rounding (checked on this hardware over 4M inputs: random
+// bits, exact ties, denormals, NaN and infinities).
+typedef float f32x2v_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+typedef __fp16 f16x2v_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+    const bf16x2v_t h = __builtin_convertvector((f32x2v_t){a, b}, bf16x2v_t);
+    uint32_t u;
+    __builtin_memcpy(&u, &h, 4);
+    return u;
+}
+
+__device__ __forceinline__ uint32_t bf16_bits(float x) { return pack_bf16(x, 0.f) & 0xffffu; }
+
+template <bool ABF> __device__ __forceinline__ float round_act(float x) {
+    if constexpr (ABF) return bf16_value(bf16_bits(x));
+    return x;
+}
+
+__device__ __forceinline__ int quant(float y, float s) {
+    if (!(s > 0.0f)) return 0;
+    float r = __builtin_rintf(y / s);
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    return (int)r;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// 16 bytes with the non-temporal hint.  A decode launch reads each K/V tile once: streamed, the
+// tiles stop displacing what the launch does reuse in L2 and the memory-side cache (records,
+// tables, queries).  Measured on attend_core's page loads: bf16 decode at 1024 streams 192 ->
+// 171 us, int8 window 104.4 -> 95.0 us; on the prefill's key/value staging 32.8 -> 32.2 us.  Only
+// where one load instruction covers whole 128-byte lines (attend_core: 1 KB contiguous per wave).
+__device__ __forceinline__ uint4 ld_stream(const void *p) {
+    typedef unsigned u32x4_nt __attribute__((ext_vector_type(4)));
+    const u32x4_nt a = __builtin_nontemporal_load((const u32x4_nt *)p);
+    return make_uint4(a.x, a.y, a.z, a.w);
+}
+
+template <int CDT> constexpr int esize() { return CDT == DT_F32 ? 4 : CDT == DT_BF16 ? 2 : 1; }
+
+// Element offset of row 0 of tile (layer, kv, page, head).
+// The (page, kv head) tile: pages hold the KVH heads a layer stores (query heads h share kv head
+// h / (H / KVH), transformer.rs:199-211), not the H repeated ones.
+__device__ __forceinline__ size_t tile_index(const PoolView &pv, int layer, int kv, int page, int j) {
+    return (((size_t)layer * 2 + kv) * pv.NB + page) * pv.KVH + j;
+}
+
+// Two activation values (dims 2i, 2i+1) of a head row.
+template <bool ABF> __device__ __forceinline__ float2 load_pair(const void *row, int i) {
+    if constexpr (ABF) {
+        uint32_t w = ((const uint32_t *)row)[i];
+        return make_float2(bf16_value(w & 0xffffu), bf16_value(w >> 16));
+    } else {
+        return ((const float2 *)row)[i];
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// append: one wave writes one new row of one head, keys (lanes 0-31, RoPE'd) and values
+// (lanes 32-63), each lane one pair of dims.  complete_kv, transformer.rs:61-92, with the k
+// rotation of rope.rs:74-95 fused in.
+
+template <int CDT, bool ABF>
+__device__ void append_row_wave(const PoolView &pv, int layer, int page, int row, int h, int key_pos,
+                                const void *krow, const void *vrow, bool fresh) {
+    const int lane = threadIdx.x & 63;
+    const int kv = lane >> 5;
+    const int pr = lane & 31;
+    float2 x = load_pair<ABF>(kv ? vrow : krow, pr);
+    if (kv == 0) {
+        float2 cs = pv.rope[(size_t)key_pos * (pv.D / 2) + pr];
+        float a = x.x * cs.x, b = x.y * cs.y, e = x.x * cs.y, f = x.y * cs.x;
+        x.x = round_act<ABF>(a - b);
+        x.y = round_act<ABF>(e + f);
+    }
+    const size_t tile = tile_index(pv, layer, kv, page, h);
+    if constexpr (CDT == DT_F32) {
+        ((float2 *)pv.pages)[tile * (kBlock * kHeadDim / 2) + row * (kHeadDim / 2) + pr] = x;
+    } else if constexpr (CDT == DT_BF16) {
+        ((uint32_t *)pv.pages)[tile * (kBlock * kHeadDim / 2) + row * (kHeadDim / 2) + pr] =
+            bf16_bits(x.x) | (bf16_bits(x.y) << 16);
+    } else {
+        // int8: per-(page, head) scale amax / 127.  A page holding another live row keeps its
+        // scale unless this row needs a larger one; then its other rows are requantized.
+        float amax = fmaxf(fabsf(x.x), fabsf(x.y));
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+        const float s_row = amax / 127.0f;
+        float *sp = pv.scales + tile;
+        const float s_old = *sp;
+        const float s_new = fresh ? s_row : fmaxf(s_old, s_row);
+        const int req = (!fresh && s_new > s_old) ? 1 : 0;
+        int8_t *pages8 = (int8_t *)pv.pages;
+#pragma unroll
+        for (int which = 0; which < 2; ++which) {
+            const int rq = __shfl(req, which * 32);
+            if (rq) {
+                const float so = __shfl(s_old, which * 32), sn = __shfl(s_new, which * 32);
+                const size_t wt = tile_index(pv, layer, which, page, h);
+                uint4 *tp = (uint4 *)(pages8 + wt * (kBlock * kHeadDim)) + lane;
+                if ((lane >> 2) != row) { // 4 lanes per 64-byte row
+                    uint4 w = *tp;
+                    uint32_t *wv = (uint32_t *)&w;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        uint32_t o = 0;
+#pragma unroll
+                        for (int bt = 0; bt < 4; ++bt) {
+                            int qv = (int)(int8_t)((wv[j] >> (8 * bt)) & 0xffu);
+                            int nq = quant((float)qv * so, sn);
+                            o |= ((uint32_t)(nq & 0xff)) << (8 * bt);
+                        }
+                        wv[j] = o;
+                    }
+                    *tp = w;
+                }
+            }
+        }
+        const uint32_t q0 = (uint32_t)(quant(x.x, s_new) & 0xff), q1 = (uint32_t)(quant(x.y, s_new) & 0xff);
+        ((uint16_t *)(pages8 + tile * (kBlock * kHeadDim)))[row * (kHeadDim / 2) + pr] =
+            (uint16_t)(q0 | (q1 << 8));
+        if (pr == 0) *sp = s_new;
+    }
+}
+
+template <int CDT> struct Lanes {
+    static constexpr int DPL = 16 / esize<CDT>();
+    static constexpr int LPR = kHeadDim / DPL;
+    static constexpr int RPP = 64 / LPR;
+    static constexpr int NP = kBlock / RPP;
+    // blocks in flight per wave: 4 KB (f32), 8 KB (bf16), 4 KB (int8) of K and V
+    static constexpr int DEPTH = CDT == DT_F32 ? 1 : 2;
+    // waves per SIMD the register budget is sized for (512 VGPRs / waves)
+    static constexpr int WAVES = CDT == DT_F32 ? 3 : 4;
+};
+
+template <int CDT>
+__device__ __forceinline__ void unpack(const uint4 &w, float (&x)[Lanes<CDT>::DPL]) {
+    const uint32_t *u = (const uint32_t *)&w;
+    if constexpr (CDT == DT_F32) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = __uint_as_float(u[i]);
+    } else if constexpr (CDT == DT_BF16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x[2 * i] = bf16_value(u[i] & 0xffffu);
+            x[2 * i + 1] = bf16_value(u[i] >> 16);
+        }
+    } else {
+        // int8 codes q as q + 128: flipping the top bit of each byte makes it unsigned, and an
+        // unsigned byte converts to f32 in one instruction (v_cvt_f32_ubyte0..3).  The callers
+        // take the 128 back out once per dot product / per accumulator.
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t b = u[i] ^ 0x80808080u;
+#pragma unroll
+            for (int bt = 0; bt < 4; ++bt) x[4 * i + bt] = (float)((b >> (8 * bt)) & 0xffu);
+        }
+    }
+}
+
+// Rotated query slice (dims DPL*c .. DPL*c+DPL-1) at `pos`, rounded to the activation dtype and
+// prescaled.
+template <int DPL, bool ABF>
+__device__ __forceinline__ void rotated_q(const PoolView &pv, const void *qrow, int c, int pos, float mul,
+                                          float (&out)[DPL]) {
+#pragma unroll
+    for (int i = 0; i < DPL / 2; ++i) {
+        const int pr = c * (DPL / 2) + i;
+        float2 x = load_pair<ABF>(qrow, pr);
+        float2 cs = pv.rope[(size_t)pos * (pv.D / 2) + pr];
+        float a = x.x * cs.x, b = x.y * cs.y, e = x.x * cs.y, f = x.y * cs.x;
+        out[2 * i] = round_act<ABF>(a - b) * mul;
+        out[2 * i + 1] = round_act<ABF>(e + f) * mul;
+    }
+}
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(const uint4 &u) {
+    bf16x8_t r;
+    __builtin_memcpy(&r, &u, 16);
+    return r;
+}
+
+typedef short v4s_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s_t lds_v4s_t;
+
+// ds_read_b64_tr_b16 (gfx950).  Within each group of 16 lanes, lane j supplies the address of
+// four consecutive b16 values D[j][0..3], and lane i receives D[4 s + i / 4][i % 4] as element
+// s.  Pointing lane j at row r0 + j / 4, columns c0 + 4 (j % 4) of a row-major b16 matrix thus
+// hands lane i column c0 + i of rows r0 .. r0 + 3: a transposed read.
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t *p) {
+    const v4s_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t *)(__attribute__((address_space(3))) uint16_t *)p);
+    uint2 u;
+    __builtin_memcpy(&u, &r, 8);
+    return u;
+}
+
+// Launchers one kernel file provides to another.
+hipError_t launch_decode_gqa(const PoolView &pv, const BatchView &bv, int layer, const void *q, const void *k,
+                             const void *v, void *out, float scale, bool fused, hipStream_t stream,
+                             const LaunchTiming &tm);
+hipError_t launch_prefill_mfma(const PoolView &pv, const BatchView &bv, int layer, const void *q, const void *k,
+                               const void *v, void *out, float scale, bool fused, hipStream_t stream,
+                               const LaunchTiming &tm);
+
+} // namespace xnp

@@ -1,5 +1,5 @@
 // Host side of the paged flow-LM KV cache: the page allocator, per-stream state (current_end,
-// ring slots), batch plans and the C ABI of include/xnp_kv.h.  Kernels are in kernels.hip.
+// ring slots), batch plans and the C ABI of include/xnp_kv.h.  Kernels are in k_*.hip.
 #include "../../include/xnp_kv.h"
 #include "xnp_internal.h"
 

@@ -1,4 +1,4 @@
-// Structures shared by the host library (pool.cpp) and the HIP kernels (kernels.hip).
+// Structures shared by the host library (pool.cpp, flow_lm.cpp) and the HIP kernel files (k_*.hip).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -85,7 +85,7 @@ xnp_status pool_fail(xnp_status code, const char *fmt, ...);
 const xnp_pool_desc *pool_desc(const xnp_pool *p);
 bool pool_host_only(const xnp_pool *p);
 
-// Launchers (kernels.hip).  All asynchronous on `stream`; return the launch status.
+// Launchers (k_*.hip).  All asynchronous on `stream`; return the launch status.
 hipError_t launch_patch_tables(const PoolView &pv, const TablePatch *patches, int n,
                                hipStream_t stream);
 // Copies `bytes` (rounded up to 16) from src, a device view of pinned host memory, to dst, and
