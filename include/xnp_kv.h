@@ -78,6 +78,7 @@ typedef enum xnp_status {
 typedef enum xnp_ring_mode { XNP_RING_SHIFT = 1, XNP_RING_ABSOLUTE = 2 } xnp_ring_mode;
 
 #define XNP_POOL_HOST_ONLY 1 /* metadata only: no device memory; device calls return XNP_E_STATE */
+#define XNP_MAX_ROPE_ROWS (1 << 24) /* positions a pool's RoPE tables may grow to */
 
 typedef struct xnp_pool xnp_pool;
 
@@ -92,7 +93,8 @@ typedef struct xnp_pool_desc {
     int32_t cache_dtype;  /* xnp_dtype of the cached K/V */
     int32_t act_dtype;    /* xnp_dtype of q/k/v/out: XNP_F32 or XNP_BF16 */
     float max_period;     /* RoPE theta (rope.rs:47) */
-    int32_t max_pos;      /* RoPE table rows: every position used must be below it */
+    int32_t max_pos;      /* RoPE table rows to start with; a batch whose positions reach past the
+                             table's rows grows it (doubling, up to XNP_MAX_ROPE_ROWS) */
     int32_t flags;        /* XNP_POOL_* */
     uint64_t page_seed;   /* 0: pages are handed out in order; else a Fisher-Yates shuffle of the
                              free list seeded with it (shuffled block tables) */
@@ -122,6 +124,8 @@ typedef struct xnp_pool_stats {
     int32_t batch_open; /* streams in the open batch, 0 if none */
     int32_t work_items; /* decode work groups of the open batch: one per (stream, head) */
     int64_t device_bytes;
+    int32_t rope_rows;  /* rows of the RoPE tables now (positions 0 .. rope_rows - 1) */
+    int32_t pad;
 } xnp_pool_stats;
 
 /* ---- pool ------------------------------------------------------------------------------ */
@@ -129,7 +133,15 @@ xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out);
 xnp_status xnp_pool_destroy(xnp_pool *pool);
 xnp_status xnp_pool_stats_get(const xnp_pool *pool, xnp_pool_stats *out);
 /* Rows pos0 .. pos0+n-1 of the pool's RoPE table as [n][D/2] (cos, sin) pairs: the values the
- * kernels rotate with, built on the host as rope.rs:44-58 does (RotaryEmbedding::new). */
+ * kernels rotate with, built on the host as rope.rs:44-58 does (RotaryEmbedding::new).  Rows past
+ * the table's current size (xnp_pool_stats.rope_rows) are refused.
+ *
+ * The tables grow in xnp_batch_begin when a step's positions reach their end (absolute rings and
+ * window caches count positions on after their evictions, as the reference builds RoPE rows at any
+ * offset, transformer.rs:794-803): the device tables are reallocated and the old ones freed, which
+ * waits for the device.  Launches recorded before (a hipGraph of xnp_attend) read the old tables
+ * and must be recorded again; xnp_flow_lm_step_graph does so itself.  Angles are pos * inv_freq in
+ * f32, as the reference computes them, so large positions carry the same f32 rounding there. */
 xnp_status xnp_pool_rope_rows(const xnp_pool *pool, int32_t pos0, int32_t n, float *cos_sin);
 
 /* ---- streams ---------------------------------------------------------------------------- */
@@ -232,6 +244,12 @@ xnp_status xnp_batch_abort(xnp_pool *pool);
  * read the device tables back (synchronizes hip_stream) and count the entries of open streams
  * that differ from the host's page map.  0 is the only right answer. */
 xnp_status xnp_pool_check_tables(xnp_pool *pool, int32_t *mismatches, void *hip_stream);
+
+/* Test hook (no counterpart in the reference): on a host-only pool, set stream id's page map
+ * entry for logical block blk to `page` as given, without the allocator's bookkeeping, so that tests
+ * can plant the broken maps xnp_batch_begin refuses.  Device pools refuse it (XNP_E_STATE).  Put the
+ * entry back before closing the stream. */
+xnp_status xnp_debug_set_block(xnp_pool *pool, int32_t id, int32_t blk, int32_t page);
 
 /* Measurement hook (no counterpart in the reference): the pool's next decode or prefill launch
  * records HIP events `start` and `stop` (hipEvent_t, created by the caller) as the kernel starts
@@ -375,8 +393,10 @@ xnp_status xnp_flow_lm_step(xnp_flow_lm *lm, const int32_t *ids, int32_t n, cons
  * StepGraph records one step and replays it per frame (step_graph.rs:111-122, 234-267).  The plan
  * (positions, pages) is uploaded eagerly each call and read by the recorded kernels from the pool's
  * device buffers, as DeviceStep keeps the position on the device (transformer.rs:111-140).  A new
- * recording is made when n, a buffer or the stream changes; hip_stream must not be the null
- * stream.  Results are those of xnp_flow_lm_step. */
+ * recording is made when n, a buffer or the stream changes, or when the batch's plan picks other
+ * kernels than the recorded ones (a stream of the batch took up a ring prefix, another split, a
+ * regrown RoPE table); hip_stream must not be the null stream.  Results are those of
+ * xnp_flow_lm_step. */
 xnp_status xnp_flow_lm_step_graph(xnp_flow_lm *lm, const int32_t *ids, int32_t n, const float *latent_in,
                                   const float *noise, float *latent_out, float *eos_logit,
                                   void *hip_stream);

@@ -11,7 +11,8 @@ import os
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "liboracle.so")
+# XNP_ORACLE_LIB names another build of the oracle (the sanitizer build of `make -C oracle asan`)
+LIB_PATH = os.environ.get("XNP_ORACLE_LIB") or os.path.join(_HERE, "liboracle.so")
 F32, BF16, I8 = 0, 1, 2
 RING_NONE, RING_SHIFT, RING_ABSOLUTE = 0, 1, 2
 DT = {"f32": F32, "bf16": BF16, "i8": I8}

@@ -63,6 +63,59 @@ def test_rope_table_is_the_oracles_bit_for_bit(act):
         assert np.array_equal(table[pos, :, 1].view(np.uint32), s.view(np.uint32))
 
 
+@pytest.mark.parametrize("act", ["f32", "bf16"])
+def test_rope_tables_grow_when_positions_reach_their_end(act):
+    # An absolute ring counts positions on after its evictions (the reference rotates at any offset,
+    # transformer.rs:794-803): a batch reaching past the table's rows grows it, doubling, and the new
+    # rows are the oracle's bit for bit.
+    p = pool(cache_dtype=act, act_dtype=act, max_pos=64)
+    s = p.init_state(48)
+    p.begin([s], t=32)
+    p.end()
+    p.start_ring(s, "absolute", prefix=0)
+    for step in range(32, 232):  # a window of 32 on 48 slots, one row evicted per step
+        p.slide(s, 0, 48, 32, 1, step)
+        p.begin([s])
+        p.end()
+    info = p.info(s)
+    assert info["current_end"] == 32 and info["ring_shift"] == 200  # the last step wrote position 231
+    assert p.stats()["rope_rows"] == 256
+    table = p.rope_rows(0, 256)
+    for pos in [0, 63, 64, 127, 128, 200, 231, 255]:
+        c, sn = oracle.rope_row(64, 10000.0, float(pos), act)
+        assert np.array_equal(table[pos, :, 0].view(np.uint32), c.view(np.uint32)), pos
+        assert np.array_equal(table[pos, :, 1].view(np.uint32), sn.view(np.uint32)), pos
+    with pytest.raises(xnp.XnpError, match="256-row table"):
+        p.rope_rows(200, 100)
+
+
+def test_a_broken_page_map_is_refused_before_anything_changes():
+    # Every block a step writes must hold a page of the stream's own: planted on a host-only pool, an
+    # id past the pool, a free page, a page shared with a fork (with_seq_budget shares full pages,
+    # transformer.rs:350-392) and the page another stream of the batch takes for its own row (pages
+    # are handed out in order: a's next is page 2) are each refused, the pool left as it was; the
+    # repaired map steps.
+    p = pool()
+    a = p.init_state(64)
+    p.begin([a], t=32)
+    p.end()
+    b = p.with_seq_budget(a, 64)
+    shared = p.blocks(a)[1]
+    assert p.blocks(b)[:2] == p.blocks(a)[:2] and p.info(b)["shared"] == 2
+    free0 = p.stats()["free_blocks"]
+    for page in (64 + 5, 60, shared, 2):
+        p.debug_set_block(b, 2, page)
+        with pytest.raises(xnp.XnpError) as e:
+            p.begin([a, b], t=1)
+        assert e.value.name == "XNP_E_STATE" and "page map is broken" in e.value.message, page
+        p.debug_set_block(b, 2, -1)  # put back before anything reads the map
+        assert p.stats()["free_blocks"] == free0 and p.stats()["batch_open"] == 0
+        assert p.current_end(a) == 32 and p.current_end(b) == 32
+    p.begin([a, b], t=1)
+    p.end()
+    assert p.current_end(b) == 33 and p.stats()["free_blocks"] == free0 - 2
+
+
 def test_pages_are_taken_as_rows_arrive_and_returned_on_close():
     p = pool()
     a = p.init_state(100)

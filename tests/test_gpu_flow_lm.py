@@ -197,6 +197,45 @@ def test_q8_graph_recorded_frames_equal_eager_frames():
         assert torch.equal(runs[0][3], runs[1][3]) and torch.equal(runs[0][4], runs[1][4]), f
 
 
+def test_q8_graph_is_recorded_again_when_a_stream_takes_up_a_ring_prefix():
+    # A recording made while no stream keeps a ring prefix holds the decode built without the
+    # prefix's second query rotation.  When one stream then turns into an absolute ring that keeps
+    # its prompt (s2s.rs:174) and evicts (s2s.rs:324-333), replayed frames must still equal eager
+    # frames bit for bit: the plan picks the prefix decode, and the graph is recorded again.
+    cfg = fl.FlowLMConfig(num_layers=2, flow_depth=2, flow_dim=512, dim_feedforward=1024, n_bins=100, precision="q8")
+    blob = fl.random_weights(cfg, 103, std=0.05, unit_norms=False)
+    rng = np.random.default_rng(104)
+    n, P, span, drop = 3, 4, 12, 4
+    tokens = rng.integers(0, cfg.n_bins + 1, (n, P)).astype(np.int32)
+    s = torch.cuda.Stream()
+    runs = []
+    for _ in range(2):
+        pool = xnp.KvPool(num_layers=2, num_heads=8, num_blocks=24, max_streams=n, max_blocks_per_stream=4,
+                          cache_dtype="bf16", act_dtype="bf16", max_pos=128, page_seed=6)
+        ids = [pool.init_state(64) for _ in range(n)]
+        lm = xnp.FlowLM(pool, cfg, blob, max_rows=n * P)
+        with torch.cuda.stream(s):
+            lm.prompt_text(ids, tokens)
+        lat = torch.zeros((n, cfg.ldim), dtype=torch.float32, device=DEV)
+        eos = torch.zeros(n, dtype=torch.float32, device=DEV)
+        runs.append((pool, ids, lm, lat, eos))
+    noise = torch.zeros((n, cfg.ldim), dtype=torch.float32, device=DEV)
+    plain = 3  # frames before stream 0 becomes a ring; its frames sit at slots P, P + 1, ...
+    for f in range(plain + 21):
+        with torch.cuda.stream(s):
+            noise.copy_(torch.from_numpy((0.5 * rng.standard_normal((n, cfg.ldim))).astype(np.float32)).to(DEV))
+            for g, (pool, ids, lm, lat, eos) in enumerate(runs):
+                if f == plain:
+                    pool.start_ring(ids[0], "absolute", prefix=P, stream=s.cuda_stream)
+                if f >= plain:
+                    pool.slide(ids[0], P, span, span, drop, f, stream=s.cuda_stream)
+                lm.step(ids, None if f == 0 else lat, noise, lat, eos, stream=s.cuda_stream, graph=(g == 1))
+        s.synchronize()
+        assert torch.equal(runs[0][3], runs[1][3]) and torch.equal(runs[0][4], runs[1][4]), f
+    info = runs[1][0].info(runs[1][1][0])
+    assert info["ring_shift"] == 12 and info["ring_prefix"] == P  # three evictions of 4 rows
+
+
 def test_q8_refuses_an_f32_pool_and_odd_widths():
     cfg = fl.FlowLMConfig(num_layers=1, flow_depth=1, flow_dim=512, dim_feedforward=512, n_bins=10, precision="q8")
     blob = fl.random_weights(cfg, 101)

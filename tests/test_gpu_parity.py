@@ -34,14 +34,14 @@ class Pair:
     """A GPU pool and one oracle stream per GPU stream, driven in lockstep."""
 
     def __init__(self, *, L=2, H=8, KVH=None, cache="bf16", act="bf16", streams=8, cap=256,
-                 split=0, seed=0, page_seed=0):
+                 split=0, seed=0, page_seed=0, max_pos=8192):
         self.L, self.H, self.KVH = L, H, KVH or H
         self.cache, self.act = cache, act
         self.rng = np.random.default_rng(seed)
         mbps = (cap + 15) // 16
         self.pool = xnp.KvPool(num_layers=L, num_heads=H, num_kv_heads=self.KVH, num_blocks=streams * mbps * 2 + 8,
                                max_streams=streams * 2 + 2, max_blocks_per_stream=mbps, cache_dtype=cache,
-                               act_dtype=act, max_pos=8192, page_seed=page_seed, decode_split=split)
+                               act_dtype=act, max_pos=max_pos, page_seed=page_seed, decode_split=split)
         self.ids, self.orc = [], []
         for _ in range(streams):
             self.add(cap)
@@ -542,22 +542,124 @@ def test_int8_sliding_window_with_random_write_heads():
         p.assert_cache_equal(i)
 
 
+def test_shifting_and_absolute_rings_agree_over_a_long_session():
+    # The s2s policy (s2s.rs:318-333) for 1000 frames on a bf16 ring of each mode, fed the same
+    # inputs: a voice prefix, a context of 96 slots, the oldest third evicted whenever it is full.
+    # The shifting ring is the reference's (keys rotated back in place on every eviction,
+    # transformer.rs:905-926); the absolute one keeps keys as written and rotates the query twice.
+    # Each is held to its own oracle -- outputs within 2e-2, cache rows bit-exact -- and their
+    # outputs agree within 2e-2: RoPE scores depend only on position differences.
+    v, context, drop, frames = [16, 5, 0], 96, 32, 1000
+    pairs = {m: Pair(cache="bf16", act="bf16", streams=3, cap=128, seed=12, L=2) for m in ("shift", "absolute")}
+    for m, p in pairs.items():
+        for i in range(3):
+            p.fill(i, v[i])
+            p.pool.start_ring(p.ids[i], m, prefix=v[i])
+            p.orc[i].start_ring(m, prefix=v[i])
+    in_view, worst_between = [0, 0, 0], 0.0
+    rng = np.random.default_rng(13)
+    for step in range(frames):
+        for p in pairs.values():
+            for i in range(3):
+                if in_view[i] == context:
+                    oldest = step - in_view[i]
+                    p.orc[i].evict(v[i], [v[i] + (oldest + j) % context for j in range(drop)])
+                p.orc[i].set_ring_slot(v[i] + step % context)
+                p.pool.slide(p.ids[i], v[i], context, context, drop, step)
+        for i in range(3):
+            if in_view[i] == context:
+                in_view[i] -= drop
+        for p in pairs.values():
+            p.pool.begin(p.ids)
+        for layer in range(2):
+            q, k, v_ = (bf16_round(rng.standard_normal((3, 8, 64)).astype(np.float32)) for _ in range(3))
+            outs = {}
+            for m, p in pairs.items():
+                out = torch.empty((3, 8, 64), dtype=torch.bfloat16, device=DEV)
+                p.pool.attend(layer, dev(q, "bf16"), dev(k, "bf16"), dev(v_, "bf16"), out, 0.125)
+                torch.cuda.synchronize()
+                outs[m] = host(out)
+                for i in range(3):
+                    want, _ = p.orc[i].attend(layer, q[i:i + 1], k[i:i + 1], v_[i:i + 1])
+                    assert rel_err(outs[m][i:i + 1], want) <= 2e-2, (m, step, layer, i)
+            e = rel_err(outs["shift"], outs["absolute"])
+            worst_between = max(worst_between, e)
+            assert e <= 2e-2, (step, layer, e)
+        for p in pairs.values():
+            p.pool.end()
+            for i in range(3):
+                p.orc[i].commit(1)
+        for i in range(3):
+            in_view[i] += 1
+        if step % 250 == 249:
+            for p in pairs.values():
+                for i in range(3):
+                    p.assert_cache_equal(i)
+    assert pairs["absolute"].pool.info(pairs["absolute"].ids[2])["ring_shift"] == frames - in_view[2]
+    print(f"shift vs absolute over {frames} frames: worst relative difference {worst_between:.2e}")
+
+
+def test_an_int8_absolute_ring_runs_past_the_initial_rope_table():
+    # An absolute ring counts positions on after its evictions (the reference rotates at any
+    # offset, transformer.rs:794-803): a 64-row table grows as the ring's positions pass it, and the
+    # ring stays bit-exact with the oracle, outputs within 2e-2.
+    p = Pair(cache="i8", act="bf16", streams=3, cap=80, seed=14, L=2, max_pos=64)
+    heads = [0, 17, 70]
+    for i in range(3):
+        p.pool.start_ring(p.ids[i], "absolute", prefix=0)
+        p.orc[i].start_ring("absolute", prefix=0)
+    in_view = [0] * 3
+    for n in range(300):
+        for i in range(3):
+            step = heads[i] + n
+            if in_view[i] == 64:
+                p.orc[i].evict(0, [(step - 64) % 80])
+                in_view[i] -= 1
+            p.orc[i].set_ring_slot(step % 80)
+            p.pool.slide(p.ids[i], 0, 80, 64, 1, step)
+        p.step()
+        for i in range(3):
+            in_view[i] += 1
+        if n in (63, 64, 130, 299):
+            for i in range(3):
+                p.assert_cache_equal(i)
+    assert p.pool.stats()["rope_rows"] == 512  # positions up to 299: 64 -> 128 -> 256 -> 512
+
+
+@pytest.mark.parametrize("cache,act", [("bf16", "bf16"), ("f32", "f32")])
+def test_a_window_cache_runs_past_the_initial_rope_table(cache, act):
+    # Mimi's KvCache builds RoPE rows at its absolute offset on every call (transformer.rs:794-803):
+    # a window's positions grow without bound.  A 32-row table grows under a 24-row window over
+    # 120 rows, single then paired, held to the oracle's KvCache.
+    L, H = 2, 8
+    pool = xnp.KvPool(num_layers=L, num_heads=H, num_blocks=16, max_streams=2, max_blocks_per_stream=2,
+                      cache_dtype=cache, act_dtype=act, max_pos=32, page_seed=5)
+    wid = pool.init_window(24)
+    win = oracle.Window(L, H, 64, 24, act=act)
+    rng = np.random.default_rng(52)
+    for t in [1] * 80 + [2] * 20:
+        _window_batch(pool, [wid], [win], t, L, H, act, cache, rng)
+    _assert_window_rows(pool, wid, win, 24, L, H, cache)
+    assert win.offset == 120 and pool.stats()["rope_rows"] == 128
+
+
 def test_the_int8_window_configuration_at_full_size_spot_checked():
     # The int8 sliding-window workload at its full size: 1024 streams x 9 layers x 8 heads x 64, int8
     # pages with a scale per (page, head), window 512 on 528-slot absolute rings, write heads
-    # U[0,4096), histories of U[64,1100] rows (the long ones wrap their ring twice), each row
-    # through the batched append with one slide per step, then two attend steps.  10 streams spread
-    # over the lengths (the longest and the shortest included) are mirrored on the oracle: outputs
-    # within 2e-2, then every live cache row, code and scale bit-exact.
+    # U[0,4096), histories of U[64,2048] rows as the workload draws them (the long ones wrap their
+    # ring four times, each page's scale only growing once the ring has wrapped), each row through
+    # the batched append with one slide per step, then two attend steps.  10 streams spread over the
+    # lengths (the longest and the shortest included) are mirrored on the oracle: outputs within
+    # 2e-2, then every live cache row, code and scale bit-exact.
     S, L, H, SPAN, WIN = 1024, 9, 8, 528, 512
     rng = np.random.default_rng(20261204)
     heads = rng.integers(0, 4096, S)
-    lens = rng.integers(64, 1101, S)
+    lens = rng.integers(64, 2049, S)
     order = np.argsort(-lens, kind="stable")
     sample = sorted(set(order[::128].tolist()) | {int(order[0]), int(order[-1])})
     mbps = SPAN // 16
     pool = xnp.KvPool(num_layers=L, num_heads=H, num_blocks=S * mbps + 16, max_streams=S, max_blocks_per_stream=mbps,
-                      cache_dtype="i8", act_dtype="bf16", max_pos=1200, page_seed=17)
+                      cache_dtype="i8", act_dtype="bf16", max_pos=int(lens.max()) + 8, page_seed=17)
     ids = [pool.init_state(SPAN) for _ in range(S)]
     for sid in ids:
         pool.start_ring(sid, "absolute", prefix=0)

@@ -134,6 +134,7 @@ struct FlowGraph {
     const float *latent_in = nullptr, *noise = nullptr;
     float *latent_out = nullptr, *eos = nullptr;
     hipStream_t stream = nullptr;
+    BatchLaunchKey key; // the batch's kernel choice when recorded
 };
 
 struct xnp_flow_lm {
@@ -613,8 +614,11 @@ extern "C" xnp_status xnp_flow_lm_step_graph(xnp_flow_lm *lm, const int32_t *ids
     // pool's device buffers, so one recording serves every step with the same rows and buffers
     if (xnp_status st = xnp_batch_begin(lm->pool, ids, n, 1, hip_stream)) return st;
     FlowGraph &G = lm->graph;
+    // the recorded kernels were chosen by the batch that recorded them: a ring prefix taken up since
+    // (s2s.rs:174) changes the decode's template, and the plan sets the waves per group
+    const BatchLaunchKey key = batch_launch_key(lm->pool);
     const bool same = G.exec && G.n == n && G.latent_in == latent_in && G.noise == noise && G.latent_out == latent_out &&
-                      G.eos == eos_logit && G.stream == hs;
+                      G.eos == eos_logit && G.stream == hs && G.key == key;
     if (!same) {
         if (G.exec) (void)hipGraphExecDestroy(G.exec);
         G = FlowGraph();
@@ -634,6 +638,7 @@ extern "C" xnp_status xnp_flow_lm_step_graph(xnp_flow_lm *lm, const int32_t *ids
             return st != XNP_OK ? st : pool_fail(XNP_E_HIP, "graph capture: %s", hipGetErrorString(e));
         }
         G.n = n, G.latent_in = latent_in, G.noise = noise, G.latent_out = latent_out, G.eos = eos_logit, G.stream = hs;
+        G.key = key;
     }
     hipError_t e = hipGraphLaunch(G.exec, hs);
     if (e != hipSuccess) {

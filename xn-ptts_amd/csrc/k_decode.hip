@@ -36,7 +36,7 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
 
     // Per-page metadata, lane j holding page w + j * SPLIT: page id, seen rows, int8 scales.
     // Past the wave's last page the lanes hold page 0 with no row seen.
-    int my_page = 0;
+    int my_page = 0, my_ok = 0;
     uint32_t my_seen = 0;
     float my_sk = 0.f, my_sv = 0.f;
     // issued with the header load: record slots past nblk hold stale ids and are masked below
@@ -52,6 +52,7 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
         const bool ok = pg >= 0 && pg < pv.NB;
         if (!ok) seen = 0;
         my_page = ok ? pg : 0;
+        my_ok = ok ? 1 : 0;
         my_seen = seen;
         if constexpr (CDT == DT_I8) {
             my_sk = pv.scales[tile_index(pv, layer, 0, my_page, kvh)];
@@ -256,8 +257,10 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
     // A workgroup-scope fence orders the stores before the later loads on the same CU; nothing
     // waits for the stores to reach memory.  When the write page is not among the wave's first
     // DEPTH pages, those are loaded before the append, so the append's round trips overlap them.
+    // An invalid write page id (never handed out by the host, which checks it) appends nothing, as
+    // k_append skips it: the row would otherwise land in page 0, another stream's tile.
     const int wblk = R.write_slot >> 4, wj = wblk / SPLIT;
-    const bool owner = fused && w == wblk % SPLIT;
+    const bool owner = fused && w == wblk % SPLIT && __builtin_amdgcn_readlane(my_ok, wj) != 0;
     const bool early = !owner || wj >= DEPTH;
     if (early) {
 #pragma unroll

@@ -307,7 +307,7 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
     const int nb = R.nblk > w ? (R.nblk - w + SPLIT - 1) / SPLIT : 0; // this wave's pages
 
     // per-page metadata, lane j holding page w + j * SPLIT (as attend_core)
-    int my_page = 0;
+    int my_page = 0, my_ok = 0;
     uint32_t my_seen = 0;
     const int pg_raw = w + lane * SPLIT < pv.mbps ? rec_pages[w + lane * SPLIT] : -1;
     if (lane < nb) {
@@ -318,6 +318,7 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
         if (nvalid < kBlock) seen &= (1u << max(nvalid, 0)) - 1u;
         const bool ok = pg_raw >= 0 && pg_raw < pv.NB;
         my_page = ok ? pg_raw : 0;
+        my_ok = ok ? 1 : 0;
         my_seen = ok ? seen : 0;
     }
 
@@ -424,8 +425,9 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
 
     uint4 kb[DEPTH + 1][2], vb[DEPTH + 1][2];
     // complete_kv: the wave that owns the write page appends the kv head's new row, as in attend_core
+    // an invalid write page id appends nothing, as in attend_core
     const int wblk = R.write_slot >> 4, wj = wblk / SPLIT;
-    const bool owner = fused && w == wblk % SPLIT;
+    const bool owner = fused && w == wblk % SPLIT && __builtin_amdgcn_readlane(my_ok, wj) != 0;
     const bool early = !owner || wj >= DEPTH;
     if (early) {
 #pragma unroll

@@ -115,7 +115,8 @@ struct xnp_pool {
     int64_t device_bytes = 0;
 
     // host
-    std::vector<float2> rope_host;
+    std::vector<float2> rope_host; // [rope_rows][D/2]
+    int32_t rope_rows = 0;         // rows of the RoPE tables: desc.max_pos at first, grown as positions reach it
     std::vector<Stream> streams;
     std::vector<int32_t> free_ids;
     std::vector<int32_t> free_pages;
@@ -124,6 +125,7 @@ struct xnp_pool {
     std::vector<uint32_t> patch_mark; // [max_streams * mbps]: generation an entry was last coalesced in
     uint32_t patch_gen = 0;
     std::vector<int32_t> shadow_tables; // host-only pools: what the device tables would hold
+    std::vector<int32_t> writer;        // [num_blocks] during xnp_batch_begin's check: the stream writing each page, -1 none
 
     struct Batch {
         bool open = false;
@@ -148,7 +150,7 @@ struct xnp_pool {
         pv.D = d.head_dim;
         pv.NB = d.num_blocks;
         pv.mbps = d.max_blocks_per_stream;
-        pv.max_pos = d.max_pos;
+        pv.max_pos = rope_rows;
         pv.cache_dt = d.cache_dtype;
         pv.act_dt = d.act_dtype;
         return pv;
@@ -257,6 +259,64 @@ struct xnp_pool {
         return XNP_OK;
     }
 
+    // The device RoPE tables from rope_host: the f32 (cos, sin) pairs and, for bf16 activations, the
+    // same values packed as bf16 pairs (they are bf16 already: no rounding here).
+    xnp_status upload_rope(float2 *dst, uint32_t *dst16) {
+        HIP_TRY(hipMemcpy(dst, rope_host.data(), sizeof(float2) * rope_host.size(), hipMemcpyHostToDevice),
+                "rope table upload");
+        if (dst16) {
+            std::vector<uint32_t> packed(rope_host.size());
+            for (size_t i = 0; i < packed.size(); i++) {
+                uint32_t c, sn;
+                std::memcpy(&c, &rope_host[i].x, 4);
+                std::memcpy(&sn, &rope_host[i].y, 4);
+                packed[i] = (c >> 16) | (sn & 0xffff0000u);
+            }
+            HIP_TRY(hipMemcpy(dst16, packed.data(), sizeof(uint32_t) * packed.size(), hipMemcpyHostToDevice),
+                    "bf16 rope table upload");
+        }
+        return XNP_OK;
+    }
+
+    // Positions below `need` get RoPE rows.  The reference builds its rows at any offset on every
+    // call (transformer.rs:794-803), and an absolute ring or a window cache keeps counting positions
+    // after its evictions, so the tables grow (doubling) when a batch reaches their end: new rows are
+    // built on the host as at creation, the device tables reallocated and the old ones freed (which
+    // waits for the device).  Recordings of earlier launches read the old tables: the pool's launch
+    // key changes (batch_launch_key), so they are recorded again.
+    xnp_status grow_rope(int64_t need) {
+        if (need <= rope_rows) return XNP_OK;
+        if (need > kMaxRopeRows)
+            return fail(XNP_E_INVALID, "position %lld is beyond the largest RoPE table (%d rows)", (long long)need - 1,
+                        kMaxRopeRows);
+        const int64_t rows = std::max<int64_t>(need, std::min<int64_t>(2 * (int64_t)rope_rows, kMaxRopeRows));
+        const int half = d.head_dim / 2;
+        const size_t old = rope_host.size();
+        rope_host.resize((size_t)rows * half);
+        for (int64_t pos = rope_rows; pos < rows; pos++)
+            rope_row(d.head_dim, d.max_period, (float)pos, d.act_dtype == XNP_BF16, &rope_host[(size_t)pos * half]);
+        if (!host_only) {
+            float2 *nr = nullptr;
+            uint32_t *n16 = nullptr;
+            hipError_t e = hipMalloc(&nr, sizeof(float2) * rope_host.size());
+            if (e == hipSuccess && rope16) e = hipMalloc(&n16, sizeof(uint32_t) * rope_host.size());
+            xnp_status st = e == hipSuccess ? upload_rope(nr, n16) : hip_fail(e, "rope table growth");
+            if (st != XNP_OK) {
+                if (nr) (void)hipFree(nr);
+                if (n16) (void)hipFree(n16);
+                rope_host.resize(old);
+                return st;
+            }
+            HIP_TRY(hipFree(rope), "freeing the old rope table");
+            if (rope16) HIP_TRY(hipFree(rope16), "freeing the old bf16 rope table");
+            device_bytes += (int64_t)((rope_host.size() - old) * (sizeof(float2) + (rope16 ? sizeof(uint32_t) : 0)));
+            rope = nr;
+            rope16 = n16;
+        }
+        rope_rows = (int32_t)rows;
+        return XNP_OK;
+    }
+
     // Give `sid` its own copy of every page it shares (before in-place writes).
     xnp_status unshare(int32_t sid, hipStream_t stream) {
         Stream &s = streams[sid];
@@ -312,6 +372,14 @@ xnp_status pool_fail(xnp_status code, const char *fmt, ...) {
     return code;
 }
 const xnp_pool_desc *pool_desc(const xnp_pool *p) { return &p->d; }
+BatchLaunchKey batch_launch_key(const xnp_pool *p) {
+    BatchLaunchKey k;
+    k.prefix = p->batch.bv.prefix;
+    k.split = p->batch.bv.split;
+    k.rope = p->rope;
+    k.rope16 = p->rope16;
+    return k;
+}
 bool pool_host_only(const xnp_pool *p) { return p->host_only; }
 } // namespace xnp
 
@@ -396,7 +464,9 @@ extern "C" xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out)
     }
     p->free_pages.assign(order.rbegin(), order.rend()); // pop_back hands out order[0] first
 
+    if (d.max_pos > kMaxRopeRows) return fail(XNP_E_INVALID, "max_pos %d: the RoPE table holds at most %d rows", d.max_pos, kMaxRopeRows);
     const int half = d.head_dim / 2;
+    p->rope_rows = d.max_pos;
     p->rope_host.resize((size_t)d.max_pos * half);
     for (int32_t pos = 0; pos < d.max_pos; pos++)
         rope_row(d.head_dim, d.max_period, (float)pos, d.act_dtype == XNP_BF16, &p->rope_host[(size_t)pos * half]);
@@ -450,19 +520,9 @@ extern "C" xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out)
         e = hipMemset(p->scales, 0, sizeof(float) * d.num_kv_heads * (size_t)d.num_blocks * 2 * d.num_layers);
         if (e != hipSuccess) return dev_fail(e, "scale init");
     }
-    e = hipMemcpy(p->rope, p->rope_host.data(), sizeof(float2) * p->rope_host.size(), hipMemcpyHostToDevice);
-    if (e != hipSuccess) return dev_fail(e, "rope table upload");
-    if (p->rope16) {
-        // the bf16 table's values are the f32 table's, which were rounded to bf16: no rounding here
-        std::vector<uint32_t> packed(p->rope_host.size());
-        for (size_t i = 0; i < packed.size(); i++) {
-            uint32_t c, sn;
-            std::memcpy(&c, &p->rope_host[i].x, 4);
-            std::memcpy(&sn, &p->rope_host[i].y, 4);
-            packed[i] = (c >> 16) | (sn & 0xffff0000u);
-        }
-        e = hipMemcpy(p->rope16, packed.data(), sizeof(uint32_t) * packed.size(), hipMemcpyHostToDevice);
-        if (e != hipSuccess) return dev_fail(e, "bf16 rope table upload");
+    if (xnp_status st = p->upload_rope(p->rope, p->rope16)) {
+        pool_free(p);
+        return st;
     }
     // a plan with the table patches behind it, or an aux upload
     const size_t stage_bytes = p->batch_bytes + p->aux_bytes;
@@ -494,6 +554,18 @@ extern "C" xnp_status xnp_pool_stats_get(const xnp_pool *pool, xnp_pool_stats *o
     out->batch_open = pool->batch.open ? std::max(pool->batch.n, 1) : 0;
     out->work_items = pool->batch.open && pool->batch.t == 1 ? pool->batch.n * pool->d.num_heads : 0;
     out->device_bytes = pool->device_bytes;
+    out->rope_rows = pool->rope_rows;
+    out->pad = 0;
+    return XNP_OK;
+}
+
+extern "C" xnp_status xnp_debug_set_block(xnp_pool *pool, int32_t id, int32_t blk, int32_t page) {
+    if (!pool) return fail(XNP_E_INVALID, "null argument");
+    if (!pool->host_only) return fail(XNP_E_STATE, "only a host-only pool takes a planted page map");
+    Stream *s = pool->get(id);
+    if (!s) return fail(XNP_E_STREAM, "no open stream %d", id);
+    if (blk < 0 || blk >= (int32_t)s->blocks.size()) return fail(XNP_E_INVALID, "block %d of %d", blk, (int)s->blocks.size());
+    s->blocks[blk] = page;
     return XNP_OK;
 }
 
@@ -534,8 +606,8 @@ extern "C" xnp_status xnp_pool_check_tables(xnp_pool *pool, int32_t *mismatches,
 
 extern "C" xnp_status xnp_pool_rope_rows(const xnp_pool *pool, int32_t pos0, int32_t n, float *cos_sin) {
     if (!pool || !cos_sin) return fail(XNP_E_INVALID, "null argument");
-    if (pos0 < 0 || n < 0 || pos0 + n > pool->d.max_pos)
-        return fail(XNP_E_INVALID, "rows %d..%d of a %d-row table", pos0, pos0 + n, pool->d.max_pos);
+    if (pos0 < 0 || n < 0 || (int64_t)pos0 + n > pool->rope_rows)
+        return fail(XNP_E_INVALID, "rows %d..%d of a %d-row table", pos0, pos0 + n, pool->rope_rows);
     const size_t half = pool->d.head_dim / 2;
     std::memcpy(cos_sin, pool->rope_host.data() + (size_t)pos0 * half, sizeof(float2) * half * n);
     return XNP_OK;
@@ -712,9 +784,6 @@ extern "C" xnp_status xnp_stream_advance(xnp_pool *pool, int32_t id, int32_t n) 
     if (n < 0 || s->current_end + n > s->capacity)
         return fail(XNP_E_NO_ROOM, "no room left: the stream holds %d positions", s->capacity);
     if (n == 0) return XNP_OK;
-    if (s->current_end + n > pool->d.max_pos)
-        return fail(XNP_E_INVALID, "position %d is beyond the RoPE table (%d rows)", s->current_end + n - 1,
-                    pool->d.max_pos);
     const int32_t b0 = s->current_end / kBlock, b1 = (s->current_end + n - 1) / kBlock + 1;
     if (xnp_status st = take_range(pool, id, b0, b1, nullptr)) return st;
     s->current_end += n;
@@ -964,6 +1033,7 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
     // check everything first
     std::vector<uint8_t> seen(pool->streams.size(), 0);
     int need = 0, windows = 0;
+    int64_t max_pos = -1; // the step's largest RoPE position
     for (int32_t i = 0; i < n; i++) {
         const int32_t id = ids[i];
         const Stream *s = pool->get(id);
@@ -997,9 +1067,10 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
             for (int32_t b = s->current_end / kBlock; b <= (s->current_end + t - 1) / kBlock; b++) need += s->blocks[b] < 0;
             last_pos = s->current_end + t - 1;
         }
-        if (last_pos >= pool->d.max_pos)
-            return fail(XNP_E_INVALID, "position %lld is beyond the RoPE table (%d rows)", (long long)last_pos,
-                        pool->d.max_pos);
+        if (last_pos >= kMaxRopeRows)
+            return fail(XNP_E_INVALID, "position %lld is beyond the largest RoPE table (%d rows)", (long long)last_pos,
+                        kMaxRopeRows);
+        max_pos = std::max(max_pos, last_pos);
     }
     if (t > 1 && windows && windows != n)
         return fail(XNP_E_INVALID, "a step of %d rows holds window caches only, or none", t);
@@ -1008,6 +1079,8 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
         return fail(XNP_E_INVALID, "an int8 window cache with grouped heads takes one row a step");
     if (need > (int)pool->free_pages.size())
         return fail(XNP_E_OUT_OF_BLOCKS, "out of blocks: %d needed, %d free", need, (int)pool->free_pages.size());
+    if (!pool->host_only) HIP_TRY(hipSetDevice(pool->d.device), "hipSetDevice");
+    if (xnp_status st = pool->grow_rope(max_pos + 1)) return st;
 
     auto &B = pool->batch;
     B.ids.assign(ids, ids + n);
@@ -1028,6 +1101,49 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
         else
             take_range(pool, ids[i], s.current_end / kBlock, (s.current_end + t - 1) / kBlock + 1, &B.taken);
     }
+    // Every block a row of the step goes into must hold a page of this stream's own: a live page
+    // id, not shared with a fork (copy on write ran before).  The kernels would write a bad id's row
+    // nowhere (or, were the check absent, into another stream's page), so a broken page map stops
+    // here, before anything is uploaded.
+    pool->writer.resize(pool->d.num_blocks, -1);
+    std::vector<int32_t> written; // pages marked in pool->writer, unmarked below
+    auto unmark = [&] {
+        for (int32_t pg : written) pool->writer[pg] = -1;
+    };
+    for (int32_t i = 0; i < n; i++) {
+        const Stream &s = pool->streams[ids[i]];
+        int32_t bad = -1; // the first block written without a page of its own
+        auto check = [&](int32_t b) {
+            const int32_t pg = s.blocks[b];
+            const bool ok = pg >= 0 && pg < pool->d.num_blocks && pool->refcnt[pg] == 1 &&
+                            (pool->writer[pg] < 0 || pool->writer[pg] == ids[i]);
+            if (ok && pool->writer[pg] < 0) {
+                pool->writer[pg] = ids[i];
+                written.push_back(pg);
+            }
+            if (bad < 0 && !ok) bad = b;
+        };
+        if (s.window) {
+            const int64_t p = (int64_t)s.current_end + s.shift;
+            for (int32_t r = 0; r < t; r++) check((int32_t)((p + r) % s.window) / kBlock);
+        } else if (s.ring != RING_NONE) {
+            check(s.write / kBlock);
+        } else {
+            for (int32_t b = s.current_end / kBlock; b <= (s.current_end + t - 1) / kBlock; b++) check(b);
+        }
+        if (bad >= 0) {
+            const int32_t pg = s.blocks[bad];
+            const bool live = pg >= 0 && pg < pool->d.num_blocks;
+            const int32_t refs = live ? pool->refcnt[pg] : 0, other = live ? pool->writer[pg] : -1;
+            unmark();
+            for (auto it = B.taken.rbegin(); it != B.taken.rend(); ++it) pool->drop_page(it->first, it->second);
+            B.taken.clear();
+            return fail(XNP_E_STATE,
+                        "stream %d writes block %d, whose page %d is not its own (%d holders, written by stream %d "
+                        "of the batch too): the page map is broken", ids[i], bad, pg, refs, other);
+        }
+    }
+    unmark();
 
     // the plan, composed in host memory laid out as the device buffer
     std::vector<StreamPlan> plans(n);
@@ -1420,8 +1536,8 @@ extern "C" xnp_status xnp_layer_workspace(const xnp_pool *pool, int32_t rows, in
     return XNP_OK;
 }
 
-extern "C" xnp_status xnp_layer_step(xnp_pool *pool, int32_t layer, const xnp_layer_weights *w, void *x,
-                                     void *workspace, uint64_t workspace_bytes, void *hip_stream) {
+static xnp_status layer_step_impl(xnp_pool *pool, int32_t layer, const xnp_layer_weights *w, void *x, void *workspace,
+                                  uint64_t workspace_bytes, void *hip_stream) {
     if (!pool || !w || !x) return fail(XNP_E_INVALID, "null argument");
     if (xnp_status st = batch_call(pool, layer, hip_stream, pool->batch.t == 1)) return st;
     if (pool->d.act_dtype != XNP_BF16) return fail(XNP_E_INVALID, "the layer step runs on bf16 activations");
@@ -1466,3 +1582,9 @@ extern "C" xnp_status xnp_layer_step(xnp_pool *pool, int32_t layer, const xnp_la
     HIP_TRY(launch_gemm_q8(S.f, M, ff, w->w2, w->s2, dm, kResidual, res, hs), "linear2");
     return XNP_OK;
 }
+
+extern "C" xnp_status xnp_layer_step(xnp_pool *pool, int32_t layer, const xnp_layer_weights *w, void *x,
+                                     void *workspace, uint64_t workspace_bytes, void *hip_stream) {
+    return layer_step_impl(pool, layer, w, x, workspace, workspace_bytes, hip_stream);
+}
+

@@ -13,6 +13,7 @@ constexpr int kHeadDim = 64; // the kernels' head dimension
 constexpr int kMaxHeads = 16;
 constexpr int kPartStride = 68; // floats per wave partial: acc[64], m, l, pad
 constexpr int kLaneBlocks = 60;  // pages one wave's lanes index: 64 minus the prefetch overrun
+constexpr int32_t kMaxRopeRows = XNP_MAX_ROPE_ROWS; // positions the RoPE tables may grow to
 
 enum : int32_t { DT_F32 = 0, DT_BF16 = 1, DT_I8 = 2 };
 enum : int32_t { RING_NONE = 0, RING_SHIFT = 1, RING_ABSOLUTE = 2 };
@@ -22,7 +23,7 @@ struct PoolView {
     void *pages;          // [L][2][NB][H][16][D], cache dtype
     float *scales;        // [L][2][NB][H] (int8 only)
     int32_t *tables;      // [max_streams][mbps] page ids, -1 where none
-    const float2 *rope;   // [max_pos][D/2] (cos, sin), rounded to the activation dtype
+    const float2 *rope;   // [max_pos][D/2] (cos, sin), rounded to the activation dtype; max_pos: its rows now
     const uint32_t *rope16; // bf16 activations only: the same table as packed bf16 (cos | sin << 16)
     int32_t L, H, KVH, D, NB, mbps, max_pos;
     int32_t cache_dt, act_dt;
@@ -79,6 +80,19 @@ struct EvictRow {
 struct LaunchTiming {
     hipEvent_t start = nullptr, stop = nullptr;
 };
+
+// What the open batch's kernel launches are chosen by beyond its size and the caller's buffers: the
+// decode template (a ring prefix in the batch), the waves per work group, and the RoPE tables the
+// kernels read.  A recording of the launches (a hipGraph) replays right only for a batch with the
+// same key.
+struct BatchLaunchKey {
+    int32_t prefix = -1, split = 0;
+    const void *rope = nullptr, *rope16 = nullptr;
+    bool operator==(const BatchLaunchKey &o) const {
+        return prefix == o.prefix && split == o.split && rope == o.rope && rope16 == o.rope16;
+    }
+};
+BatchLaunchKey batch_launch_key(const xnp_pool *p);
 
 // The pool's description and the library's error reporting (pool.cpp), for the other host files.
 xnp_status pool_fail(xnp_status code, const char *fmt, ...);

@@ -21,7 +21,9 @@ import os
 from typing import Iterable, Optional, Sequence
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libxnp_kv.so")
+# XNP_KV_LIB names another build of the same library: the host-sanitizer build that
+# `make -C xn-ptts_amd/csrc asan-check` runs the CPU tests against.
+LIB_PATH = os.environ.get("XNP_KV_LIB") or os.path.join(_HERE, "libxnp_kv.so")
 
 F32, BF16, I8 = 0, 1, 2
 DTYPES = {"f32": F32, "bf16": BF16, "i8": I8}
@@ -69,7 +71,7 @@ class StreamInfo(_c.Structure):
 
 class PoolStats(_c.Structure):
     _fields_ = [("free_blocks", _i32), ("open_streams", _i32), ("batch_open", _i32),
-                ("work_items", _i32), ("device_bytes", _c.c_int64)]
+                ("work_items", _i32), ("device_bytes", _c.c_int64), ("rope_rows", _i32), ("pad", _i32)]
 
 
 SIGNATURES = {
@@ -106,6 +108,7 @@ SIGNATURES = {
     "xnp_batch_abort": (_i32, [_p]),
     "xnp_layer_workspace": (_i32, [_p, _i32, _i32, _i32, _c.POINTER(_c.c_uint64)]),
     "xnp_layer_step": (_i32, [_p, _i32, _p, _p, _p, _c.c_uint64, _p]),
+    "xnp_debug_set_block": (_i32, [_p, _i32, _i32, _i32]),
     "xnp_layer_norm": (_i32, [_p, _i32, _i32, _p, _p, _c.c_float, _p, _p]),
     "xnp_linear_q8": (_i32, [_p, _i32, _i32, _p, _p, _i32, _i32, _p, _p, _p]),
     "xnp_quantize_rows": (_i32, [_p, _i32, _i32, _p, _p]),
@@ -270,6 +273,10 @@ class KvPool:
         """Have the next decode/prefill launch record these hipEvent_t handles around its kernel
         (either may be None: a start from one launch and a stop from a later one)."""
         _check(self._lib.xnp_pool_time_next(self._h, start_event, stop_event))
+
+    def debug_set_block(self, sid: int, blk: int, page: int):
+        """Test hook, host-only pools: plant a page map entry (xnp_debug_set_block)."""
+        _check(self._lib.xnp_debug_set_block(self._h, sid, blk, page))
 
     def rope_rows(self, pos0: int, n: int):
         import numpy as np
