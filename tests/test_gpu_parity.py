@@ -547,8 +547,14 @@ def test_shifting_and_absolute_rings_agree_over_a_long_session():
     # inputs: a voice prefix, a context of 96 slots, the oldest third evicted whenever it is full.
     # The shifting ring is the reference's (keys rotated back in place on every eviction,
     # transformer.rs:905-926); the absolute one keeps keys as written and rotates the query twice.
-    # Each is held to its own oracle -- outputs within 2e-2, cache rows bit-exact -- and their
-    # outputs agree within 2e-2: RoPE scores depend only on position differences.
+    # Each is held to its own oracle -- outputs within 2e-2, cache rows bit-exact.  RoPE scores
+    # depend only on position differences, so the two modes agree up to their own roundings: the
+    # shifting ring rounds its keys to bf16 again on every rotation, the absolute one rounds a query
+    # rotated elsewhere.  The oracle's two modes, both in f32 on the same inputs, differ by up to
+    # 2.05e-2 over this session (8.7e-3 on average); the GPU's modes must differ by no more than the
+    # oracle's at the same frame plus their outputs' rounding: each bf16 output may sit one bf16 step
+    # from its oracle's rounded one (when the two f32 values straddle a rounding boundary), up to
+    # 2^-7 of the largest output, so 2 x 2^-7 for the pair.
     v, context, drop, frames = [16, 5, 0], 96, 32, 1000
     pairs = {m: Pair(cache="bf16", act="bf16", streams=3, cap=128, seed=12, L=2) for m in ("shift", "absolute")}
     for m, p in pairs.items():
@@ -556,7 +562,7 @@ def test_shifting_and_absolute_rings_agree_over_a_long_session():
             p.fill(i, v[i])
             p.pool.start_ring(p.ids[i], m, prefix=v[i])
             p.orc[i].start_ring(m, prefix=v[i])
-    in_view, worst_between = [0, 0, 0], 0.0
+    in_view, worst_between, worst_oracle = [0, 0, 0], 0.0, 0.0
     rng = np.random.default_rng(13)
     for step in range(frames):
         for p in pairs.values():
@@ -573,18 +579,21 @@ def test_shifting_and_absolute_rings_agree_over_a_long_session():
             p.pool.begin(p.ids)
         for layer in range(2):
             q, k, v_ = (bf16_round(rng.standard_normal((3, 8, 64)).astype(np.float32)) for _ in range(3))
-            outs = {}
+            outs, wants = {}, {}
             for m, p in pairs.items():
                 out = torch.empty((3, 8, 64), dtype=torch.bfloat16, device=DEV)
                 p.pool.attend(layer, dev(q, "bf16"), dev(k, "bf16"), dev(v_, "bf16"), out, 0.125)
                 torch.cuda.synchronize()
                 outs[m] = host(out)
+                wants[m] = np.concatenate([p.orc[i].attend(layer, q[i:i + 1], k[i:i + 1], v_[i:i + 1])[0]
+                                           for i in range(3)])
                 for i in range(3):
-                    want, _ = p.orc[i].attend(layer, q[i:i + 1], k[i:i + 1], v_[i:i + 1])
-                    assert rel_err(outs[m][i:i + 1], want) <= 2e-2, (m, step, layer, i)
-            e = rel_err(outs["shift"], outs["absolute"])
-            worst_between = max(worst_between, e)
-            assert e <= 2e-2, (step, layer, e)
+                    assert rel_err(outs[m][i:i + 1], wants[m][i:i + 1]) <= 2e-2, (m, step, layer, i)
+            for i in range(3):
+                e = rel_err(outs["shift"][i:i + 1], outs["absolute"][i:i + 1])
+                eo = rel_err(wants["shift"][i:i + 1], wants["absolute"][i:i + 1])
+                worst_between, worst_oracle = max(worst_between, e), max(worst_oracle, eo)
+                assert e <= eo + 2 * 2.0 ** -7, (step, layer, i, e, eo)
         for p in pairs.values():
             p.pool.end()
             for i in range(3):
@@ -596,7 +605,9 @@ def test_shifting_and_absolute_rings_agree_over_a_long_session():
                 for i in range(3):
                     p.assert_cache_equal(i)
     assert pairs["absolute"].pool.info(pairs["absolute"].ids[2])["ring_shift"] == frames - in_view[2]
-    print(f"shift vs absolute over {frames} frames: worst relative difference {worst_between:.2e}")
+    assert worst_oracle <= 2.5e-2
+    print(f"shift vs absolute over {frames} frames: worst relative difference {worst_between:.2e} "
+          f"(the oracle's modes: {worst_oracle:.2e})")
 
 
 def test_an_int8_absolute_ring_runs_past_the_initial_rope_table():
