@@ -292,6 +292,18 @@ xnp_status xnp_layer_workspace(const xnp_pool *pool, int32_t rows, int32_t d_mod
 xnp_status xnp_layer_step(xnp_pool *pool, int32_t layer, const xnp_layer_weights *w, void *x,
                           void *workspace, uint64_t workspace_bytes, void *hip_stream);
 
+/* xnp_layer_step without a workspace argument (no counterpart in the reference): for callers that
+ * cannot allocate device memory -- code under hipGraph capture, tight serving loops, hosts that
+ * forbid hipMalloc.  The scratch is a fixed array of XNP_STATIC_SCRATCH_BYTES inside the library,
+ * one per device, held until the process ends; a step needing more (xnp_layer_workspace) is refused
+ * with XNP_E_INVALID.  The call allocates nothing, host or device.  Every call on one device shares
+ * that device's array: calls that overlap on one GPU (two pools, two host threads, two streams)
+ * race, so the caller orders them.  Nothing in the array needs to start at zero (every byte a step
+ * reads it wrote first in the same call), so the previous call's contents do not matter. */
+#define XNP_STATIC_SCRATCH_BYTES (24u << 20) /* the 2048-row step of a 512-wide, FF 2048 layer takes 18 MiB */
+xnp_status xnp_layer_step_static(xnp_pool *pool, int32_t layer, const xnp_layer_weights *w, void *x,
+                                 void *hip_stream);
+
 /* The pieces, on caller buffers (the current HIP device):
  * LayerNorm of rows of `dim` bf16 values (dim a multiple of 512, at most 2048). */
 xnp_status xnp_layer_norm(const void *x, int32_t rows, int32_t dim, const float *w, const float *b,

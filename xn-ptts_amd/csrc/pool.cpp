@@ -491,6 +491,8 @@ extern "C" xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out)
     };
     hipError_t e = hipSetDevice(d.device);
     if (e != hipSuccess) return dev_fail(e, "hipSetDevice");
+    e = static_scratch_init(d.device); // the static scratch's address on this device, once per device
+    if (e != hipSuccess) return dev_fail(e, "static scratch address");
     // a page holds the num_kv_heads heads a layer stores, not the repeated query heads
     const size_t page_elems = (size_t)d.num_kv_heads * kBlock * d.head_dim;
     const size_t page_bytes = page_elems * p->esz;
@@ -1588,3 +1590,19 @@ extern "C" xnp_status xnp_layer_step(xnp_pool *pool, int32_t layer, const xnp_la
     return layer_step_impl(pool, layer, w, x, workspace, workspace_bytes, hip_stream);
 }
 
+extern "C" xnp_status xnp_layer_step_static(xnp_pool *pool, int32_t layer, const xnp_layer_weights *w, void *x,
+                                            void *hip_stream) {
+    if (!pool) return fail(XNP_E_INVALID, "null argument");
+    if (pool->host_only) return fail(XNP_E_STATE, "a host-only pool runs no kernels");
+    void *scr = static_scratch(pool->d.device); // the array's address on the pool's device
+    if (!scr) return fail(XNP_E_STATE, "the static scratch of device %d is not set up", pool->d.device);
+    if (w && pool->batch.open) {
+        const int64_t rows = (int64_t)pool->batch.n * pool->batch.t;
+        const int64_t qd = (int64_t)pool->d.num_heads * pool->d.head_dim, kd = (int64_t)pool->d.num_kv_heads * pool->d.head_dim;
+        const uint64_t need = layer_scratch(nullptr, rows, w->d_model, qd, kd, w->ff).bytes;
+        if (need > kStaticScratchBytes)
+            return fail(XNP_E_INVALID, "the step of %lld rows needs %llu bytes of scratch; the static scratch holds %llu",
+                        (long long)rows, (unsigned long long)need, (unsigned long long)kStaticScratchBytes);
+    }
+    return layer_step_impl(pool, layer, w, x, scr, kStaticScratchBytes, hip_stream);
+}

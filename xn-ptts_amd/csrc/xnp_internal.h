@@ -81,6 +81,13 @@ struct LaunchTiming {
     hipEvent_t start = nullptr, stop = nullptr;
 };
 
+// The library's static scratch (k_scratch.hip), one array per device: xnp_layer_step_static's
+// workspace.  static_scratch_init takes the array's address on `device`, which must be current;
+// pool creation calls it.  static_scratch returns that address (null before the init).
+constexpr uint64_t kStaticScratchBytes = XNP_STATIC_SCRATCH_BYTES;
+hipError_t static_scratch_init(int device);
+void *static_scratch(int device);
+
 // What the open batch's kernel launches are chosen by beyond its size and the caller's buffers: the
 // decode template (a ring prefix in the batch), the waves per work group, and the RoPE tables the
 // kernels read.  A recording of the launches (a hipGraph) replays right only for a batch with the

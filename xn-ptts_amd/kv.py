@@ -108,6 +108,7 @@ SIGNATURES = {
     "xnp_batch_abort": (_i32, [_p]),
     "xnp_layer_workspace": (_i32, [_p, _i32, _i32, _i32, _c.POINTER(_c.c_uint64)]),
     "xnp_layer_step": (_i32, [_p, _i32, _p, _p, _p, _c.c_uint64, _p]),
+    "xnp_layer_step_static": (_i32, [_p, _i32, _p, _p, _p]),
     "xnp_debug_set_block": (_i32, [_p, _i32, _i32, _i32]),
     "xnp_layer_norm": (_i32, [_p, _i32, _i32, _p, _p, _c.c_float, _p, _p]),
     "xnp_linear_q8": (_i32, [_p, _i32, _i32, _p, _p, _i32, _i32, _p, _p, _p]),
@@ -419,6 +420,10 @@ class KvPool:
         batch: x [n][t][d_model] bf16 is the residual stream, updated in place."""
         _check(self._lib.xnp_layer_step(self._h, layer, _c.byref(weights.c), _ptr(x), _ptr(workspace),
                                         workspace.numel() * workspace.element_size(), self._stream_h))
+
+    def layer_step_static(self, layer: int, weights: "LayerWeights", x):
+        """layer_step with the library's static scratch instead of a workspace: allocates nothing."""
+        _check(self._lib.xnp_layer_step_static(self._h, layer, _c.byref(weights.c), _ptr(x), self._stream_h))
 
     def end(self):
         _check(self._lib.xnp_batch_end(self._h))
