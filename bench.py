@@ -106,6 +106,22 @@ def bf16_np(a):
     return ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32).view(np.float32).reshape(a.shape)
 
 
+def traffic_of(workload, match, bytes_per_launch):
+    """HBM bytes per launch of a workload's dominant kernel, from its FETCH_SIZE / WRITE_SIZE counter
+    runs (profiles/traffic.json: each counter scaled by what it reads for a 1 GiB copy): the counter
+    bytes per algorithmic byte of the profiled run, times this run's algorithmic bytes per launch.
+    The ratio belongs to the kernel at that workload, so it carries over to any --steps / --warmup;
+    None when the workload (streams, layers, lengths, ...) is not the profiled one."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        entry = json.load(f).get(workload)
+    if not entry or entry.get("workload") != match:
+        return None
+    return int(round(entry["traffic_per_algorithmic_byte"] * bytes_per_launch))
+
+
 def decode_bytes(lens, elem=2, kvh=H):
     """Bytes one layer's append + decode must move for streams with cached lengths `lens`: each
     stored kv head's K/V rows once (kvh of them), q and out for every query head."""
@@ -293,17 +309,8 @@ def run_decode(args, xnp, torch):
     bytes_per_launch = bytes_timed[0] / bytes_timed[1]  # every layer of a step moves the same bytes
     achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
     fps = S / (ms / 1000.0)
-    # HBM traffic per launch from the FETCH_SIZE / WRITE_SIZE counter runs of this same command,
-    # scaled by the factors a copy of known size gives (profiles/decode_traffic.json).
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "decode_traffic.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            tr = json.load(f)
-        if tr.get("workload") == {"streams": S, "layers": L, "max_len": args.max_len, "steps": args.steps,
-                                  "warmup": args.warmup, "fixed_len": args.fixed_len, "split": args.split} \
-                and kvh == H:
-            traffic = int(tr["traffic_bytes_per_launch"])
+    traffic = traffic_of("decode", {"streams": S, "layers": L, "max_len": args.max_len, "fixed_len": args.fixed_len,
+                                    "split": args.split, "kv_heads": kvh}, bytes_per_launch)
     cpu = None if args.no_cpu else cpu_decode(L, lens, args.cpu_seconds)
     grouped = "" if kvh == H else f", {kvh} kv heads stored (grouped query heads)"
     config = {"workload": f"batched paged decode attention + KV append: {S} streams, Phonon-40m layers "
@@ -383,7 +390,8 @@ def run_prefill(args, xnp, torch):
     # far below the MFMA ridge (2.5 PFLOP/s / 8 TB/s ~ 312), so HBM bounds it; MFMA use is reported
     # beside it.
     roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic_of("prefill", {"streams": S, "prompt": T, "layers": L}, hbm),
             "kernel": "k_prefill_mfma (fused append + RoPE + causal attention on v_mfma_f32_16x16x32_bf16), "
                       "one launch per layer",
             "avg_kernel_us": round(avg_ms * 1000.0, 2), "bytes_per_launch": hbm,
@@ -499,7 +507,8 @@ def run_window(args, xnp, torch):
                           f"rows written U[64,2048]; evict + append + dequant-on-gather decode per step",
               "streams": S, "layers": L, "window": WINDOW, "ring_slots": SPAN}
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic_of("window", {"streams": S, "layers": L}, bytes_per_launch),
             "kernel": "k_decode<int8> (fused append + quantize + RoPE + dequant decode), one launch per layer",
             "avg_kernel_us": round(avg_ms * 1000.0, 2), "bytes_per_launch": int(bytes_per_launch)}
     return line("frames/sec, int8 KV sliding window (512) at 1024 streams; decode HBM GB/s % peak", fps,
@@ -622,7 +631,8 @@ def run_step(args, xnp, torch):
                           f"length U[1,{args.step_max_len}]",
               "streams": S, "layers": L, "d_model": DM, "ff": FF}
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic_of("step", {"streams": S, "layers": L, "max_len": args.step_max_len}, bytes_per_launch),
             "kernel": "k_decode<bf16> (fused append + RoPE + decode), one launch per layer",
             "avg_kernel_us": round(avg_ms * 1000.0, 2), "bytes_per_launch": int(bytes_per_launch),
             "rest_of_layer_us": round(rest_ms * 1000.0, 2), "gemm_gop_per_layer": round(flops / 1e9, 2),
@@ -873,6 +883,10 @@ def main():
     ap.add_argument("--prompt", type=int, default=256)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="decode: only the headline, without the other configurations' entries")
+    ap.add_argument("--nested-steps", type=int, default=20, help="timed steps of each nested configuration")
+    ap.add_argument("--nested-cpu-seconds", type=float, default=5.0)
     ap.add_argument("--calibrate", action="store_true",
                     help="only copy 1 GiB device to device 5 times: the known-size kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters")
@@ -894,9 +908,44 @@ def main():
     import torch
     xnp = _load("xn_ptts_amd", os.path.join(ROOT, "xn-ptts_amd"))
     xnp.load_library()
-    run = {"decode": run_decode, "prefill": run_prefill, "window": run_window, "step": run_step,
-           "flowlm": run_flowlm, "frame": run_frame}[args.workload]
-    print(json.dumps(run(args, xnp, torch)))
+    runs = {"decode": run_decode, "prefill": run_prefill, "window": run_window, "step": run_step,
+            "flowlm": run_flowlm, "frame": run_frame}
+    out = runs[args.workload](args, xnp, torch)
+    if args.workload == "decode" and not args.headline_only and headline_args(args):
+        out["configs"] = nested_configs(args, xnp, torch, runs)
+    print(json.dumps(out))
+
+
+# The other configurations of the same run, each an entry of the headline's line: the workload's
+# own value, step time, roofline and CPU baseline, timed as its own --workload run times it.
+NESTED = [("flowlm", 1, "single-stream flow LM, Phonon-31m shape, f32 (batch 1)"),
+          ("prefill", 3, "prompt prefill, 64 streams x 256 positions"),
+          ("window", 4, "int8 KV sliding window (512), 1024 streams"),
+          ("step", 5, "full per-frame layer step, 2048 streams"),
+          ("frame", 5, "the batched q8 flow-LM frame around configuration 5's layers (flow net and heads included)")]
+
+
+def headline_args(args):
+    """The default headline workload (the nested entries describe the configurations as drawn)."""
+    return (args.streams, args.layers, args.max_len, args.fixed_len, args.split, args.kv_heads) == (1024, 9, 1024, 0, 0, 0)
+
+
+def nested_configs(args, xnp, torch, runs):
+    entries = {}
+    for name, cfg_index, what in NESTED:
+        sub = argparse.Namespace(**vars(args))
+        sub.workload, sub.steps, sub.cpu_seconds = name, args.nested_steps, args.nested_cpu_seconds
+        gc.collect()
+        torch.cuda.empty_cache()
+        t0 = time.perf_counter()
+        res = runs[name](sub, xnp, torch)
+        keep = {k: v for k, v in res.items() if k not in ("n_gpus", "scaling", "vs_baseline", "data")}
+        keep["baseline_config"] = cfg_index
+        keep["what"] = what
+        keep["wall_s"] = round(time.perf_counter() - t0, 1)
+        entries[name] = keep
+        print(f"# {name}: {res['value']} {res['unit']} ({keep['wall_s']} s)", file=sys.stderr, flush=True)
+    return entries
 
 
 if __name__ == "__main__":
