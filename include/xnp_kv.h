@@ -185,10 +185,14 @@ xnp_status xnp_stream_load_kv(xnp_pool *pool, int32_t id, int32_t layer, const f
 /* KvCache::new(context): a stream whose steps attend the last `window` positions, the causal
  * window of Mimi's attention (delta < context, transformer.rs:764-781), keys rotated at their
  * absolute position (KvCache::absolute_offset).  Its rows place themselves, row p in slot
- * p % window over the row leaving the window, so no eviction call is needed.  A step takes t <= 4
- * rows (Mimi's decoder takes 2 a frame): with t > 1 every stream of the batch must be a window
- * cache, and xnp_attend, the only per-layer call such a batch takes, runs the rows in order.
- * xnp_stream_fork clones a window as it is, every page copied (transformer.rs:348-354). */
+ * p % window over the row leaving the window, so no eviction call is needed.  A step takes any
+ * number of rows t, more than the window included (Mimi's encoder over a whole voice clip,
+ * tts_model.rs:509-515; its decoder takes 2 a frame): with t > 1 every stream of the batch must be
+ * a window cache, and xnp_attend is the only per-layer call such a batch takes.  On a bf16 pool a
+ * step of more than 4 rows runs every row's windowed attention in one MFMA launch, then writes the
+ * last min(t, window) rows into their slots; shorter steps, and every step on f32 and int8 pools,
+ * run row by row.  xnp_stream_fork clones a window as it is, every page copied
+ * (transformer.rs:348-354). */
 xnp_status xnp_window_open(xnp_pool *pool, int32_t window, int32_t *id);
 
 /* ---- ring (transformer.rs:842-929) ------------------------------------------------------ */

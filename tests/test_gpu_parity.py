@@ -408,14 +408,65 @@ def test_int8_window_cache_matches_the_ring_it_stands_for():
                     assert np.array_equal(sc.cpu().numpy().view(np.uint32), osc.view(np.uint32)), (p, layer, kv)
 
 
+@pytest.mark.parametrize("cache,act,kvh", [("bf16", "bf16", 8), ("bf16", "bf16", 2), ("f32", "f32", 8)])
+def test_a_long_mimi_chunk_matches_the_kv_cache(cache, act, kvh):
+    # Mimi's encoder pushes a whole voice clip through its transformer in one call
+    # (tts_model.rs:509-515, mimi.rs:162-167): a chunk longer than the window (context 250) attends
+    # under the window mask of transformer.rs:764-781, then KvCache::trim keeps the last rows
+    # (transformer.rs:302-317).  Here: a 300-row chunk, 40 single rows, 10 steps of 2 rows and a
+    # 100-row chunk over the held rows, on two windows of the same batch, each against the oracle's
+    # KvCache: outputs within the dtype's bar every step, every held row bit for bit at the end.
+    # bf16 chunks of more than 4 rows take the windowed MFMA prefill and its append; f32 runs row
+    # by row.  With grouped heads the pool stores each kv head once; the oracle gets it repeated.
+    L, H, context = 2, 8, 250
+    G = H // kvh
+    pool = xnp.KvPool(num_layers=L, num_heads=H, num_kv_heads=kvh, num_blocks=48, max_streams=4,
+                      max_blocks_per_stream=16, cache_dtype=cache, act_dtype=act, max_pos=1024, page_seed=6)
+    ids = [pool.init_window(context) for _ in range(2)]
+    orcs = [oracle.Window(L, H, 64, context, rows_max=300, act=act) for _ in range(2)]
+    rng = np.random.default_rng(53 + kvh)
+
+    def step(t):
+        pool.begin(ids, t=t)
+        for layer in range(L):
+            q = rng.standard_normal((2, t, H, 64)).astype(np.float32)
+            k = rng.standard_normal((2, t, kvh, 64)).astype(np.float32)
+            v = rng.standard_normal((2, t, kvh, 64)).astype(np.float32)
+            if act == "bf16":
+                q, k, v = bf16_round(q), bf16_round(k), bf16_round(v)
+            out = torch.empty((2, t, H, 64), dtype=TORCH_DT[act], device=DEV)
+            pool.attend(layer, dev(q, act), dev(k, act), dev(v, act), out, 0.125)
+            torch.cuda.synchronize()
+            got = host(out)
+            for j in range(2):
+                want, _ = orcs[j].attend(layer, q[j], np.repeat(k[j], G, axis=1), np.repeat(v[j], G, axis=1))
+                assert rel_err(got[j], want) <= TOL[cache], (t, layer, j)
+        pool.end()
+        for o in orcs:
+            o.commit(t)
+
+    for t in [300] + [1] * 40 + [2] * 10 + [100]:
+        step(t)
+    for j in range(2):
+        assert orcs[j].offset == 460 and pool.current_end(ids[j]) == context
+        win = orcs[j]
+        for layer in range(L):
+            for kv in (0, 1):
+                rows = torch.empty((context, kvh, 64), dtype=CACHE_TORCH[cache], device=DEV)
+                pool.read_rows(ids[j], layer, kv, 0, rows)
+                torch.cuda.synchronize()
+                g = rows.float().cpu().numpy()
+                want = win.rows(layer, kv)[:, ::G]
+                for i, p in enumerate(range(win.offset - win.len, win.offset)):
+                    assert np.array_equal(g[p % context].view(np.uint32), want[i].view(np.uint32)), (j, layer, kv, p)
+
+
 def test_window_misuse_is_refused():
     pool = xnp.KvPool(num_layers=1, num_heads=8, num_blocks=16, max_streams=4, max_blocks_per_stream=4,
                       cache_dtype="bf16", act_dtype="bf16", max_pos=1024)
     wid, pid = pool.init_window(16), pool.init_state(64)
     with pytest.raises(xnp.XnpError, match="window of 0"):
         pool.init_window(0)
-    with pytest.raises(xnp.XnpError, match="at most 4 rows"):
-        pool.begin([wid], t=5)
     with pytest.raises(xnp.XnpError, match="window caches only"):
         pool.begin([wid, pid], t=2)
     with pytest.raises(xnp.XnpError, match="places its rows itself"):

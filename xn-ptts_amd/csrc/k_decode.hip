@@ -372,7 +372,8 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(Lane
         slot = (b - full * P) % P;
     }
     const char *rec = bv.recs + (size_t)sidx * bv.rec_stride;
-    const StreamRec R = *(const StreamRec *)rec;
+    StreamRec R = *(const StreamRec *)rec;
+    if (bv.wrow >= 0) window_row(R, bv.wrow);
     attend_core<CDT, ABF, SPLIT, PREFIX, GQ>(pv, bv, layer, R, (const int32_t *)(rec + sizeof(StreamRec)), slot * GQ,
                                              q, knew, vnew, out, qmul, fused);
 }
@@ -494,6 +495,13 @@ static hipError_t prefill_rows_impl(const PoolView &pv, const BatchView &bv, int
     return hipGetLastError();
 }
 
+hipError_t launch_window_prefill(const PoolView &pv, const BatchView &bv, int layer, const void *q, const void *k,
+                                 const void *v, void *out, float scale, hipStream_t stream, const LaunchTiming &tm) {
+    if (bv.n == 0) return hipSuccess;
+    if (pv.cache_dt != DT_BF16 || pv.act_dt != DT_BF16) return hipErrorInvalidValue;
+    return launch_prefill_mfma(pv, bv, layer, q, k, v, out, scale, false, true, stream, tm);
+}
+
 bool prefill_fuses_append(const PoolView &pv) { return pv.cache_dt == DT_BF16 && pv.act_dt == DT_BF16; }
 
 hipError_t launch_prefill(const PoolView &pv, const BatchView &bv, int layer, const void *q, const void *k,
@@ -504,7 +512,7 @@ hipError_t launch_prefill(const PoolView &pv, const BatchView &bv, int layer, co
     switch (pv.cache_dt * 2 + pv.act_dt) {
     case DT_F32 * 2 + DT_F32: return prefill_rows_impl<DT_F32, false>(pv, bv, layer, q, out, scale, stream, tm);
     case DT_BF16 * 2 + DT_BF16:
-        return launch_prefill_mfma(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
+        return launch_prefill_mfma(pv, bv, layer, q, k, v, out, scale, fused, false, stream, tm);
     case DT_I8 * 2 + DT_BF16: return prefill_rows_impl<DT_I8, true>(pv, bv, layer, q, out, scale, stream, tm);
     case DT_I8 * 2 + DT_F32: return prefill_rows_impl<DT_I8, false>(pv, bv, layer, q, out, scale, stream, tm);
     default: return hipErrorInvalidValue;

@@ -1,5 +1,5 @@
-// Attention on MFMA (bf16): the causal prompt prefill with its fused append (k_prefill_mfma) and the
-// grouped-head decode (k_decode_gqa).
+// Attention on MFMA (bf16): the causal prompt prefill with its fused append (k_prefill_mfma), the
+// windowed attention of a Mimi chunk (k_prefill_window) and the grouped-head decode (k_decode_gqa).
 #include "kernels_common.h"
 
 namespace xnp {
@@ -35,6 +35,7 @@ constexpr int kPfRound = 256;    // query rows per round: 8 waves x 2 tiles x 16
 constexpr int kPfMaxPages = 512; // page ids a work group keeps in LDS
 static_assert(kPfMaxPages >= kLaneBlocks * 8, "every page of a stream fits (a pool refuses more than 60 x 8)");
 static_assert(64 * kPfWaves == kPfKeys * 8, "one thread stages 16 bytes of one key per chunk");
+static_assert(2 * kPfKeys * kPfLd >= kPfWaves / 2 * 32 * kHeadDim, "half the waves' output tiles fit in each buffer");
 
 __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4))) void k_prefill_mfma(
     PoolView pv, BatchView bv, int layer, const void *q, const void *knew, const void *vnew, void *out, float qmul,
@@ -250,22 +251,400 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
         Stage st;
         issue(0, st);
         for (int c = 0; c < nch; ++c) step(c, st);
-        __syncthreads(); // the next round's staging overwrites both buffers
+        __syncthreads(); // every wave is done with both buffers
 
-        // out[row][h][16 dg + 4 g .. +3] = O / l, the row's sum reduced over its 4 lanes
+        // The output leaves as whole 128-byte rows: each wave writes its tiles' O / l (l: the row's
+        // sum over its 4 lanes), rounded to bf16, into 4 KB of the buffers of its own as
+        // [16 j + l16][unit ^ (row & 7)], and stores 8 rows at a time.
+        uint16_t *stage = w < kPfWaves / 2 ? &ks[0][0] + w * 32 * kHeadDim : &vs[0][0] + (w - kPfWaves / 2) * 32 * kHeadDim;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             float l = lsum[j];
             l += __shfl_xor(l, 16);
             l += __shfl_xor(l, 32);
-            const int qrow = 16 * tile[j] + l16;
-            if (tile[j] < 0 || qrow >= t) continue;
-            const float inv = 1.0f / l;
-            uint16_t *orow = (uint16_t *)out + (((size_t)P.out_row * t + qrow) * pv.H + h) * kHeadDim;
+            const float inv = 1.0f / l; // not stored for a tile past the round
+            const int row = 16 * j + l16;
 #pragma unroll
             for (int dg = 0; dg < 4; ++dg)
-                *(uint2 *)(orow + 16 * dg + 4 * g) = make_uint2(pack_bf16(o[j][dg][0] * inv, o[j][dg][1] * inv),
-                                                                pack_bf16(o[j][dg][2] * inv, o[j][dg][3] * inv));
+                *(uint2 *)(stage + row * kHeadDim + 8 * ((2 * dg + (g >> 1)) ^ (row & 7)) + 4 * (g & 1)) =
+                    make_uint2(pack_bf16(o[j][dg][0] * inv, o[j][dg][1] * inv),
+                               pack_bf16(o[j][dg][2] * inv, o[j][dg][3] * inv));
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int row = 8 * k + (lane >> 3), unit = lane & 7, j = row >> 4;
+            const int qrow = 16 * tile[j] + (row & 15);
+            if (tile[j] >= 0 && qrow < t)
+                *(uint4 *)((uint16_t *)out + (((size_t)P.out_row * t + qrow) * pv.H + h) * kHeadDim + 8 * unit) =
+                    *(const uint4 *)(stage + row * kHeadDim + 8 * (unit ^ (row & 7)));
+        }
+        __syncthreads(); // the next round's staging overwrites both buffers
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Windowed attention of a Mimi chunk on MFMA (bf16 window cache and activations),
+// transformer.rs:764-781: t query rows over a window cache of W rows (slot p mod W holds position
+// p) and the chunk's own rows, each row seeing the W keys up to itself, for chunks of any length.
+//
+// One work group of 4 waves per (stream, head), two work groups per CU.  Keys are indexed
+// virtually: the window's held rows first (j < ncache, oldest first, at slot (wbase + j) mod W),
+// then the chunk's rows (j = ncache + i: input row i, rotated at its position and rounded to bf16).
+// Query row i has virtual index ncache + i and sees key j when ncache + i - W < j <= ncache + i.
+// The chunk's rows reach the window by their own append (k_window_append); this kernel only reads.
+//
+// Query rows are taken in rounds of 256: 8 pairs of 16-row tiles, pair i rows 32 i .. 32 i + 31 of
+// the round, wave w owning pairs w and 7 - w.  A round's keys (from the window of its first row to
+// its last row) stream through a ring of 3 LDS slots in chunks of 64 (K and V as
+// [key][unit ^ swz(key)], K's rope pieces beside them), loaded straight into LDS
+// (global_load_lds_dwordx4) 2 chunks ahead of the one attended, so that no register holds them.
+// At each chunk a lane waits for its own loads of it, rotates the chunk's own keys among them in
+// place, and one barrier hands the chunk to every wave.
+//
+// The two tiles of a pair are the 32 columns of v_mfma_f32_32x32x16_bf16, and each K and V piece a
+// wave reads from LDS serves both of its pairs: 64 queries.  At two waves per SIMD a wave holds
+// 256 registers: its pairs' queries and accumulators.  Both contractions are computed transposed
+// so that P never leaves registers:
+//   S^T = K Q^T      A = 32 keys of K from LDS (lane: key lane % 32, dims 16 kk + 8 (lane / 32)),
+//                    B = the pair's rotated queries (lane: query column lane % 32, same dims);
+//                    lane l holds column l % 32 against keys 8 (r / 4) + 4 (l / 32) + r % 4;
+//   softmax          online per column; its max and sum pair lanes l and l ^ 32 (permlane32_swap);
+//   O^T += V^T P^T   B = P^T straight from the S^T registers (16 keys a step), A = V^T by
+//                    transposed LDS reads (ds_read_b64_tr_b16) of the same keys.
+// A and B always hold the same key (or dim) in the same (lane / 32, element) slot, so each
+// contraction is right whatever order the instruction walks k in.
+
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
+
+constexpr int kWpChunk = 64;  // keys of a chunk
+constexpr int kWpSlots = 3;   // chunk slots of the LDS ring: 2 chunks load while one is attended
+constexpr int kWpWaves = 4;   // waves per work group
+constexpr int kWpPairs = 2;   // tile pairs per wave
+constexpr int kWpRound = 256; // query rows per round: 4 waves x 2 pairs x 32 rows
+// A chunk is 24 direct loads of 1 KB (8 keys each), 6 a wave: 2 each of K, V and K's rope pieces.
+constexpr int kWpLoadsC = kWpChunk / 8 / kWpWaves; // loads of K (of V, of rope pieces) per wave per chunk
+static_assert(kWpRound == kWpWaves * kWpPairs * 32, "a round is the waves' pairs");
+static_assert(kWpLoadsC == 2 && kWpSlots == 3, "the waits below count 6 loads a chunk, 2 chunks ahead");
+
+// K's and V's LDS rows are 128 bytes, their 16-byte units placed at unit ^ swz(key): for 16 keys in
+// a row (the reads of K's pieces) and for keys 4a .. 4a + 3 with two adjacent units each (the
+// transposed reads of V), every unit of a read falls in its own banks.
+__device__ __forceinline__ int swz(int key) {
+    const int x = (key >> 1) & 7;
+    return ((x & 1) << 1) | (((x >> 1) & 1) << 2) | ((x >> 2) & 1);
+}
+
+// the pair of a lane's value: lanes l and l ^ 32 exchange (both halves of the result hold both)
+__device__ __forceinline__ float pair_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Rotate 8 bf16 values (4 pairs) with 4 packed bf16 (cos, sin) pairs, rounded to bf16 (rope.rs:74-95).
+__device__ __forceinline__ uint4 rotate8(const uint4 &x, const uint4 &cs) {
+    const uint32_t *u = (const uint32_t *)&x, *r = (const uint32_t *)&cs;
+    uint32_t o4[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float x0 = bf16_value(u[e] & 0xffffu), x1 = bf16_value(u[e] >> 16);
+        const float c = bf16_value(r[e] & 0xffffu), s = bf16_value(r[e] >> 16);
+        const float a = x0 * c, bb = x1 * s, ee = x0 * s, f = x1 * c;
+        o4[e] = pack_bf16(a - bb, ee + f);
+    }
+    return make_uint4(o4[0], o4[1], o4[2], o4[3]);
+}
+
+// Vector-memory loads of a wave complete in the order issued (one counter, vmcnt), so a wave waits
+// for chunk c by letting only the `ahead` chunks it issued after it (6 loads each) stay in flight.
+// The loads land in LDS, which the compiler does not track: this wait is the only one they get.
+__device__ __forceinline__ void wait_chunks(int ahead) {
+    if (ahead <= 0)
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else if (ahead == 1)
+        asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+    else
+        asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+}
+
+// The lane index, recomputed where it is used: the address pieces of a chunk's loads would otherwise be kept in registers across the whole loop, which the attention needs.
+__device__ __forceinline__ int lane_here(int lane) {
+    int x;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(x) : "v"(lane));
+    return x;
+}
+
+// A work-group barrier for LDS alone: __syncthreads also waits for every global access of the wave
+// in flight, which would drain the chunk loads issued ahead.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// A 1 KB load of the wave straight into LDS: lane l's 16 bytes at src go to lds + 16 l
+// (global_load_lds_dwordx4, LDS base in M0).  Written out here because the compiler makes every LDS
+// access after its own form of this load wait for all loads in flight (vmcnt(0)), which would drain
+// the chunks issued ahead; wait_chunks is the wait these loads get.  Every wait the compiler places
+// for its own loads stays correct, as vector-memory accesses complete in the order issued.
+__device__ __forceinline__ void dma16(const void *src, void *lds) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)lds);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base) : "memory", "m0");
+}
+
+__global__ __launch_bounds__(64 * kWpWaves) __attribute__((amdgpu_waves_per_eu(2))) void k_prefill_window(
+    PoolView pv, BatchView bv, int layer, const void *q, const void *knew, const void *vnew, void *out, float qmul) {
+    __shared__ __attribute__((aligned(16))) uint16_t ks[kWpSlots][kWpChunk][kHeadDim]; // K, [key][unit ^ swz]
+    __shared__ __attribute__((aligned(16))) uint16_t vs[kWpSlots][kWpChunk][kHeadDim]; // V, [key][unit ^ swz]
+    __shared__ __attribute__((aligned(16))) uint4 rs[kWpSlots][kWpWaves][kWpLoadsC][64]; // the lanes' rope pieces
+    __shared__ int32_t spages[kPfMaxPages];
+    const int t = bv.t;
+    const int h = blockIdx.x % pv.H, b = blockIdx.x / pv.H;
+    const StreamPlan P = bv.plans[b];
+    const int32_t *tab = pv.tables + (size_t)P.sid * pv.mbps;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hi = lane >> 5, col = lane & 31;
+    const int W = P.window;
+    const int ncache = P.pos_pre; // the window's held rows; keys from the pages are these
+    const int nfrom = ncache;
+    const int kvh = h / (pv.H / pv.KVH);
+    const size_t page_elems = (size_t)pv.KVH * kBlock * kHeadDim;
+    uint16_t *kpages = (uint16_t *)pv.pages + tile_index(pv, layer, 0, 0, kvh) * (kBlock * kHeadDim);
+    uint16_t *vpages = (uint16_t *)pv.pages + tile_index(pv, layer, 1, 0, kvh) * (kBlock * kHeadDim);
+
+    // A chunk's keys j0 + key go straight into LDS slot `slot` by 1 KB loads: lane l of load i of
+    // wave w takes key 16 w + 8 i + l / 8 and holds its unit (l % 8) ^ swz(key), and the rope piece
+    // of a step's own key to its own place (every load is issued, so that each chunk is 6 loads of
+    // the lane, and nothing of it sits in registers).  Keys past the round (j >= khi) read the
+    // round's last key, so that LDS only ever holds finite values where P is 0.
+    auto issue = [&](int j0, int khi, int slot) {
+        const int ln = lane_here(lane);
+#pragma unroll
+        for (int i = 0; i < kWpLoadsC; ++i) {
+            const int row = 16 * w + 8 * i, key = row + (ln >> 3), j = min(j0 + key, khi - 1);
+            const int unit = (ln & 7) ^ swz(key);
+            const uint16_t *ksrc, *vsrc;
+            if (j >= nfrom) {
+                const size_t arow = (((size_t)P.out_row * t + (j - ncache)) * pv.KVH + kvh) * kHeadDim + 8 * unit;
+                ksrc = (const uint16_t *)knew + arow;
+                vsrc = (const uint16_t *)vnew + arow;
+            } else {
+                int s = P.wbase + j;
+                if (s >= W) s -= W;
+                const int pg = spages[s >> 4];
+                const size_t poff = (size_t)(pg >= 0 && pg < pv.NB ? pg : 0) * page_elems + (s & 15) * kHeadDim + 8 * unit;
+                ksrc = kpages + poff;
+                vsrc = vpages + poff;
+            }
+            dma16(ksrc, &ks[slot][row][0]);
+            dma16(vsrc, &vs[slot][row][0]);
+            const int r = max(j - ncache, 0);
+            dma16(pv.rope16 + (size_t)(P.key_pos + r) * (kHeadDim / 2) + 4 * unit, &rs[slot][w][i][0]);
+        }
+    };
+    // ...then, once they have landed, the step's own keys rotated in place by the lane that loaded
+    // them
+    auto settle = [&](int j0, int khi, int slot) {
+        const int ln = lane_here(lane);
+#pragma unroll
+        for (int i = 0; i < kWpLoadsC; ++i) {
+            const int key = 16 * w + 8 * i + (ln >> 3), j = j0 + key;
+            if (j >= khi || j < nfrom) continue;
+            uint4 *kp = (uint4 *)&ks[slot][key][8 * (ln & 7)]; // this lane's own pieces
+            *kp = rotate8(*kp, rs[slot][w][i][ln]);
+        }
+    };
+    const int nqt = (t + 15) / 16;
+    for (int tq0 = 0; tq0 < nqt; tq0 += kWpRound / 16) {
+        const int nq = min(kWpRound / 16, nqt - tq0);
+        // the round's keys: from the window of its first row to its last row
+        const int khi = ncache + min(t, 16 * (tq0 + nq));
+        const int klo = max(0, (ncache + 16 * tq0 - W + 1) / kWpChunk * kWpChunk);
+        const int nch = (khi - klo + kWpChunk - 1) / kWpChunk;
+
+        // the wave's pairs: pair i = w (p = 0) and 7 - w (p = 1) hold the round's tiles 2 i and 2 i + 1,
+        // rows 32 i .. 32 i + 31 (a tile past the round's last is not stored)
+        int vq[kWpPairs], vq_min[kWpPairs], vq_max[kWpPairs], qr[kWpPairs];
+        bool act[kWpPairs];
+        bf16x8_t qb[kWpPairs][4];
+        // chunk loads write LDS, so a later round's wait until every reader of the previous round is
+        // done.  The round's first chunk goes out ahead of the queries when it reads no page (keys of
+        // the step itself), the rest of the ring once the queries are in.
+        if (tq0 > 0) __syncthreads();
+        const bool early = klo >= nfrom;
+        if (early) issue(klo, khi, 0);
+        {
+            uint4 qraw[kWpPairs][4], qcs[kWpPairs][4];
+#pragma unroll
+            for (int p = 0; p < kWpPairs; ++p) {
+                const int i = p == 0 ? w : kWpRound / 32 - 1 - w, r0 = 16 * tq0 + 32 * i;
+                act[p] = 32 * i < 16 * nq;
+                // column col: query row r0 + col, dims 16 kk + 8 hi .. +7, rotated at its position and
+                // rounded to bf16 as the reference's bf16 q is; rows past the step read row t - 1 and
+                // are never stored
+                qr[p] = min(r0 + col, t - 1);
+                vq[p] = ncache + qr[p];
+                vq_min[p] = ncache + r0;
+                vq_max[p] = ncache + min(r0 + 31, t - 1);
+                const uint16_t *qp = (const uint16_t *)q + (((size_t)P.out_row * t + qr[p]) * pv.H + h) * kHeadDim;
+                const uint32_t *cs = pv.rope16 + (size_t)(P.pos + qr[p]) * (kHeadDim / 2);
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    qraw[p][kk] = *(const uint4 *)(qp + 16 * kk + 8 * hi);
+                    qcs[p][kk] = *(const uint4 *)(cs + 8 * kk + 4 * hi);
+                }
+            }
+            if (tq0 == 0) {
+                // the stream's page ids, read once: the pages of cached keys and of the rows written
+                for (int i = tid; i < min(pv.mbps, kPfMaxPages); i += 64 * kWpWaves) spages[i] = tab[i];
+            }
+#pragma unroll
+            for (int p = 0; p < kWpPairs; ++p)
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    qb[p][kk] = as_bf16x8(rotate8(qraw[p][kk], qcs[p][kk]));
+                    // rotated here: the compiler's waits for these loads, placed after the chunk loads
+                    // below, would count those too and wait for them
+                    asm volatile("" ::"v"(qb[p][kk]));
+                }
+            wait_chunks(0); // this lane's loads so far (the first chunk, the page ids) have landed
+            __syncthreads(); // ...and every lane's: the page ids and the first chunk are in LDS
+#pragma unroll
+            for (int c = early ? 1 : 0; c < kWpSlots; ++c)
+                if (c < nch) issue(klo + kWpChunk * c, khi, c);
+        }
+        // the last key any query of the wave sees (pair 1 holds the later rows)
+        const int wq_max = act[1] ? vq_max[1] : act[0] ? vq_max[0] : -1;
+
+        float m[kWpPairs], lsum[kWpPairs]; // running max (scaled, log2 units), this lane's share of the sum
+        f32x16_t o[kWpPairs][2];           // O^T: dims 32 hh + 8 (r / 4) + 4 hi + r % 4, column col
+#pragma unroll
+        for (int p = 0; p < kWpPairs; ++p) {
+            m[p] = -1e30f;
+            lsum[p] = 0.f;
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[p][hh][r] = 0.f;
+        }
+
+        for (int cb = 0; cb < nch; cb += kWpSlots) {
+#pragma unroll
+            for (int u = 0; u < kWpSlots; ++u) { // slot and ring indices stay constants
+                const int c = cb + u;
+                if (c >= nch) break;
+                const int j0 = klo + kWpChunk * c;
+                // this lane's loads of chunk c have landed: after them it issued chunk c + 1 (chunks
+                // 0 .. 2 went out first, then one a step)
+                wait_chunks(min(c == 0 ? kWpSlots - 1 : kWpSlots - 2, nch - 1 - c));
+                settle(j0, khi, u);
+                lds_barrier(); // chunk c is in LDS; every wave is done with chunk c - 1's slot
+                if (c > 0 && c + kWpSlots - 1 < nch)
+                    issue(j0 + kWpChunk * (kWpSlots - 1), khi, (u + kWpSlots - 1) % kWpSlots);
+                for (int kb = 0; kb < kWpChunk; kb += 32) {
+                    const int jb = j0 + kb; // the block's first key
+                    if (jb > wq_max) break; // after every query of the wave
+                    // S^T for each pair that sees some key of the block; the K pieces serve both
+                    bf16x8_t ka[4];
+#pragma unroll
+                    for (int kk = 0; kk < 4; ++kk)
+                        ka[kk] = as_bf16x8(*(const uint4 *)&ks[u][kb + col][8 * ((2 * kk + hi) ^ swz(kb + col))]);
+                    bool need[kWpPairs];
+                    uint32_t pk[kWpPairs][8];
+#pragma unroll
+                    for (int p = 0; p < kWpPairs; ++p) {
+                        // uniform: a pair skips a block after its last row or before its first row's window
+                        need[p] = act[p] && jb <= vq_max[p] && !(jb + 31 <= vq_min[p] - W);
+                        if (!need[p]) continue;
+                        f32x16_t s;
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) s[r] = 0.f;
+#pragma unroll
+                        for (int kk = 0; kk < 4; ++kk) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[kk], qb[p][kk], s, 0, 0, 0);
+                        // mask unless every key of the block is visible to every query of the pair: key
+                        // jb + 4 hi + kr(r) (kr = 8 (r / 4) + r % 4) is seen when kr(r) <= lim, and on a
+                        // window when kr(r) > lim - W
+                        if (jb + 31 > vq_min[p] || jb <= vq_max[p] - W) {
+                            const int lim = vq[p] - jb - 4 * hi;
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) {
+                                const int kr = 8 * (r >> 2) + (r & 3);
+                                if (kr > lim || kr <= lim - W) s[r] = -INFINITY;
+                            }
+                        }
+                        float mx = s[0];
+#pragma unroll
+                        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+                        mx = pair_max(mx);
+                        // lazy rescaling, as in decode: the column's sum and accumulators move to a new
+                        // max only when some column of the pair saw its max grow by more than 8 (log2
+                        // units); until then exponents are taken against the older max
+                        const float mn = fmaxf(m[p], mx * qmul);
+                        if (__any(mn > m[p] + 8.f)) {
+                            const float alpha = fast_exp2(m[p] - mn);
+                            lsum[p] *= alpha;
+#pragma unroll
+                            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                                for (int r = 0; r < 16; ++r) o[p][hh][r] *= alpha;
+                            m[p] = mn;
+                        }
+                        float psum = 0.f;
+#pragma unroll
+                        for (int r = 0; r < 16; r += 2) {
+                            const float p0 = fast_exp2(__builtin_fmaf(s[r], qmul, -m[p]));
+                            const float p1 = fast_exp2(__builtin_fmaf(s[r + 1], qmul, -m[p]));
+                            psum += p0 + p1;
+                            pk[p][r >> 1] = pack_bf16(p0, p1);
+                        }
+                        lsum[p] += psum;
+                    }
+#pragma unroll
+                    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+                        for (int hh = 0; hh < 2; ++hh) {
+                            // V^T: lane gets dim 32 hh + col of keys 16 kh + 4 hi .. +3 and 16 kh + 8 + 4 hi ..
+                            // +3, by two transposed reads; B = P^T of the same k slots
+                            const int vr = kb + 16 * kh + 4 * hi + ((lane & 15) >> 2);
+                            const int vu = 4 * hh + 2 * (col >> 4) + ((lane & 3) >> 1), vo = 4 * (lane & 1);
+                            const uint2 lo = lds_read_tr16(&vs[u][vr][8 * (vu ^ swz(vr)) + vo]);
+                            const uint2 up = lds_read_tr16(&vs[u][vr + 8][8 * (vu ^ swz(vr + 8)) + vo]);
+                            const bf16x8_t va = as_bf16x8(make_uint4(lo.x, lo.y, up.x, up.y));
+#pragma unroll
+                            for (int p = 0; p < kWpPairs; ++p) {
+                                if (!need[p]) continue;
+                                const bf16x8_t pb = as_bf16x8(make_uint4(pk[p][4 * kh], pk[p][4 * kh + 1], pk[p][4 * kh + 2],
+                                                                         pk[p][4 * kh + 3]));
+                                o[p][hh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, o[p][hh], 0, 0, 0);
+                            }
+                        }
+                }
+            }
+        }
+        // The output leaves as whole 128-byte rows: once every wave is done attending, each wave
+        // writes its pairs' O / l (l: the column's sum over its lane pair), rounded to bf16, into 8 KB
+        // of the ring of its own, as [row 32 p + col][unit ^ (row & 7)], and stores 8 rows at a time.
+        lds_barrier();
+        uint16_t *stage = w < kWpSlots ? &ks[w][0][0] : &vs[w - kWpSlots][0][0];
+#pragma unroll
+        for (int p = 0; p < kWpPairs; ++p) {
+            const float inv = 1.0f / pair_sum(lsum[p]); // not stored for a pair past the round
+            const int row = 32 * p + col;
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr)
+                    *(uint2 *)(stage + row * kHeadDim + 8 * ((4 * hh + rr) ^ (row & 7)) + 4 * hi) =
+                        make_uint2(pack_bf16(o[p][hh][4 * rr] * inv, o[p][hh][4 * rr + 1] * inv),
+                                   pack_bf16(o[p][hh][4 * rr + 2] * inv, o[p][hh][4 * rr + 3] * inv));
+        }
+        lds_barrier();
+#pragma unroll
+        for (int k = 0; k < 2 * kWpPairs * 32 / 16; ++k) {
+            const int row = 8 * k + (lane >> 3), unit = lane & 7, p = row >> 5;
+            const int qrow = 16 * tq0 + 32 * (p == 0 ? w : kWpRound / 32 - 1 - w) + (row & 31);
+            if (act[p] && qrow < t)
+                *(uint4 *)((uint16_t *)out + (((size_t)P.out_row * t + qrow) * pv.H + h) * kHeadDim + 8 * unit) =
+                    *(const uint4 *)(stage + row * kHeadDim + 8 * (unit ^ (row & 7)));
         }
     }
 }
@@ -301,7 +680,8 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
     const int sidx = b < full * pv.KVH ? b / (8 * pv.KVH) * 8 + b % 8 : full + (b - full * pv.KVH) / pv.KVH;
     const int kvh = b < full * pv.KVH ? b % (8 * pv.KVH) / 8 : (b - full * pv.KVH) % pv.KVH;
     const char *rec = bv.recs + (size_t)sidx * bv.rec_stride;
-    const StreamRec R = *(const StreamRec *)rec;
+    StreamRec R = *(const StreamRec *)rec;
+    if (bv.wrow >= 0) window_row(R, bv.wrow);
     const int32_t *rec_pages = (const int32_t *)(rec + sizeof(StreamRec));
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, l16 = lane & 15;
     const int nb = R.nblk > w ? (R.nblk - w + SPLIT - 1) / SPLIT : 0; // this wave's pages
@@ -499,10 +879,16 @@ hipError_t launch_decode_gqa(const PoolView &pv, const BatchView &bv, int layer,
 }
 
 hipError_t launch_prefill_mfma(const PoolView &pv, const BatchView &bv, int layer, const void *q, const void *k,
-                               const void *v, void *out, float scale, bool fused, hipStream_t stream,
+                               const void *v, void *out, float scale, bool fused, bool window, hipStream_t stream,
                                const LaunchTiming &tm) {
-    XNP_LAUNCH(k_prefill_mfma, dim3(bv.n * pv.H), dim3(64 * kPfWaves), stream, tm, pv, bv, layer, q, k, v, out,
-               scale * 1.4426950408889634f, fused ? 1 : 0);
+    if ((fused || window) && (!k || !v)) return hipErrorInvalidValue; // the step's own rows are read from k, v
+    const float qmul = scale * 1.4426950408889634f;
+    if (window)
+        XNP_LAUNCH(k_prefill_window, dim3(bv.n * pv.H), dim3(64 * kWpWaves), stream, tm, pv, bv, layer, q, k, v, out,
+                   qmul);
+    else
+        XNP_LAUNCH(k_prefill_mfma, dim3(bv.n * pv.H), dim3(64 * kPfWaves), stream, tm, pv, bv, layer, q, k, v, out,
+                   qmul, fused ? 1 : 0);
     return hipGetLastError();
 }
 

@@ -94,6 +94,44 @@ hipError_t launch_append(const PoolView &pv, const BatchView &bv, int layer, con
 }
 
 // ---------------------------------------------------------------------------------------------
+// A window step's rows into the window after its attention (Mimi's chunk, bf16 and f32 pools):
+// slot s takes the step's last row i with (p + i) % window == s; a row that a later row of the
+// step overwrites is never written.  One work group per (stream, page of the window), one wave per
+// kv head walking the page's slots.
+
+template <int CDT, bool ABF>
+__global__ __launch_bounds__(1024) void k_window_append(PoolView pv, BatchView bv, int layer, const void *k,
+                                                        const void *v) {
+    const int b = blockIdx.x / pv.mbps, blk = blockIdx.x % pv.mbps;
+    const StreamPlan P = bv.plans[b];
+    const int W = P.window, t = bv.t, j = threadIdx.x >> 6;
+    if (W <= 0 || kBlock * blk >= W) return;
+    const int page = pv.tables[(size_t)P.sid * pv.mbps + blk];
+    if (page < 0 || page >= pv.NB) return; // begin took this page; never index the pool without one
+    constexpr int AE = ABF ? 2 : 4;
+    for (int s = kBlock * blk; s < min(kBlock * blk + kBlock, W); ++s) {
+        const int r = ((s - P.pos) % W + W) % W; // the first row of the step in slot s
+        if (r >= t) continue;
+        const int i = r + W * ((t - 1 - r) / W); // the last
+        const size_t arow = ((size_t)P.out_row * t + i) * pv.KVH + j;
+        append_row_wave<CDT, ABF>(pv, layer, page, s & 15, j, P.key_pos + i, (const char *)k + arow * kHeadDim * AE,
+                                  (const char *)v + arow * kHeadDim * AE, false);
+    }
+}
+
+hipError_t launch_window_append(const PoolView &pv, const BatchView &bv, int layer, const void *k, const void *v,
+                                hipStream_t stream) {
+    if (bv.n == 0) return hipSuccess;
+    const dim3 grid(bv.n * pv.mbps), block(64 * pv.KVH);
+    switch (pv.cache_dt * 2 + pv.act_dt) {
+    case DT_F32 * 2 + DT_F32: hipLaunchKernelGGL((k_window_append<DT_F32, false>), grid, block, 0, stream, pv, bv, layer, k, v); break;
+    case DT_BF16 * 2 + DT_BF16: hipLaunchKernelGGL((k_window_append<DT_BF16, true>), grid, block, 0, stream, pv, bv, layer, k, v); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------
 // eviction on a shifting ring: rotate one kept key row by -count in place (transformer.rs:905-926)
 
 template <int CDT, bool ABF>

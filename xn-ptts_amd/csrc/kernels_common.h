@@ -234,12 +234,29 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t *p) {
     return u;
 }
 
+// Row r of a window step run row by row, from the step's record (row 0's, every page of the window
+// listed): position p + r in slot (p + r) % window; it sees slots [0, min(p + r + 1, window)) (the
+// slot it takes held position p + r - window, which left its window), and an int8 page starts
+// afresh when no other slot of it holds a row yet.
+__device__ __forceinline__ void window_row(StreamRec &R, int r) {
+    const int W = R.window, p = R.pos + r;
+    R.b += r;
+    R.pos = R.pos_pre = R.key_pos = p;
+    R.write_slot = p % W;
+    R.span = min(p + 1, W);
+    R.nblk = (R.span + kBlock - 1) / kBlock;
+    const int filled = min(p, W), b0 = R.write_slot & ~(kBlock - 1), e = min(b0 + kBlock, filled);
+    const int others = max(0, e - b0) - (R.write_slot < e ? 1 : 0);
+    R.flags = 1 | (others > 0 ? 0 : 2);
+}
+
 // Launchers one kernel file provides to another.
 hipError_t launch_decode_gqa(const PoolView &pv, const BatchView &bv, int layer, const void *q, const void *k,
                              const void *v, void *out, float scale, bool fused, hipStream_t stream,
                              const LaunchTiming &tm);
+// window: the windowed attention of a Mimi chunk over a window cache (no rows written)
 hipError_t launch_prefill_mfma(const PoolView &pv, const BatchView &bv, int layer, const void *q, const void *k,
-                               const void *v, void *out, float scale, bool fused, hipStream_t stream,
+                               const void *v, void *out, float scale, bool fused, bool window, hipStream_t stream,
                                const LaunchTiming &tm);
 
 } // namespace xnp

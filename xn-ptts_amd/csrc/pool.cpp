@@ -75,8 +75,24 @@ struct Stream {
     int32_t window = 0;
 };
 
-// rows a window stream takes in one step (Mimi's decoder: 2 per frame)
-constexpr int32_t kMaxWindowRows = 4;
+// Window steps of more rows than this on a bf16 pool run as one windowed prefill on MFMA plus an
+// append; shorter ones (Mimi's decoder takes 2 a frame), and every window step on f32 and int8 pools,
+// run row by row through the decode kernel.
+constexpr int32_t kWindowRowByRow = 4;
+
+// The window's blocks a step of t rows from position p writes: those of the slots the last
+// min(t, window) rows land in, (p + i) % window (an earlier row's slot is taken again by a later one).
+template <class F> void window_blocks(const Stream &s, int64_t p, int32_t t, F &&each) {
+    const int32_t nb = (s.window + kBlock - 1) / kBlock;
+    std::vector<uint8_t> hit(nb, 0);
+    for (int64_t r = std::max<int64_t>(0, t - s.window); r < t; r++) {
+        const int32_t b = (int32_t)((p + r) % s.window) / kBlock;
+        if (!hit[b]) {
+            hit[b] = 1;
+            each(b);
+        }
+    }
+}
 
 // A pinned host buffer an upload is composed in; reused once its copy has completed.
 struct Staging {
@@ -474,7 +490,7 @@ extern "C" xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out)
     // plan upload layout: plans, work items, masks (each 256-byte aligned)
     p->rec_stride = (int)align_up(sizeof(StreamRec) + sizeof(int32_t) * d.max_blocks_per_stream, 64);
     p->batch_bytes = align_up(sizeof(StreamPlan) * d.max_streams, 256) +
-                     align_up((size_t)p->rec_stride * d.max_streams * kMaxWindowRows, 256) +
+                     align_up((size_t)p->rec_stride * d.max_streams, 256) +
                      align_up(sizeof(uint32_t) * (size_t)p->mask_words * d.max_streams, 256);
     p->aux_bytes = std::max<size_t>(sizeof(TablePatch) * 65536,
                                     align_up(sizeof(EvictRow) * d.max_blocks_per_stream * kBlock, 256) + 4096);
@@ -1045,17 +1061,8 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
         int64_t last_pos;
         if (s->window) {
             // row i of the step goes to slot (p + i) % window, over the row leaving the window
-            if (t > kMaxWindowRows)
-                return fail(XNP_E_RING, "a window cache takes at most %d rows a step, not %d", kMaxWindowRows, t);
             const int64_t p = (int64_t)s->current_end + s->shift;
-            int32_t counted[kMaxWindowRows];
-            for (int32_t r = 0; r < t; r++) {
-                const int32_t b = (int32_t)((p + r) % s->window) / kBlock;
-                counted[r] = b;
-                bool dup = false;
-                for (int32_t q = 0; q < r; q++) dup |= counted[q] == b;
-                need += !dup && s->blocks[b] < 0;
-            }
+            window_blocks(*s, p, t, [&](int32_t b) { need += s->blocks[b] < 0; });
             last_pos = p + t - 1;
             windows++;
         } else if (s->ring != RING_NONE) {
@@ -1093,11 +1100,8 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
     for (int32_t i = 0; i < n; i++) {
         Stream &s = pool->streams[ids[i]];
         if (s.window) {
-            const int64_t p = (int64_t)s.current_end + s.shift;
-            for (int32_t r = 0; r < t; r++) {
-                const int32_t b = (int32_t)((p + r) % s.window) / kBlock;
-                take_range(pool, ids[i], b, b + 1, &B.taken);
-            }
+            window_blocks(s, (int64_t)s.current_end + s.shift, t,
+                          [&](int32_t b) { take_range(pool, ids[i], b, b + 1, &B.taken); });
         } else if (s.ring != RING_NONE)
             take_range(pool, ids[i], s.write / kBlock, s.write / kBlock + 1, &B.taken);
         else
@@ -1126,8 +1130,7 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
             if (bad < 0 && !ok) bad = b;
         };
         if (s.window) {
-            const int64_t p = (int64_t)s.current_end + s.shift;
-            for (int32_t r = 0; r < t; r++) check((int32_t)((p + r) % s.window) / kBlock);
+            window_blocks(s, (int64_t)s.current_end + s.shift, t, check);
         } else if (s.ring != RING_NONE) {
             check(s.write / kBlock);
         } else {
@@ -1180,6 +1183,11 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
             int other = 0;
             for (int32_t sl = b0; sl < b1; sl++) other |= (sl != s.write && s.valid[sl]);
             P.fresh = !other;
+            if (s.window) {
+                // the held rows are positions p - held .. p - 1, the oldest in slot (p - held) % window
+                P.window = s.window;
+                P.wbase = s.shift % s.window;
+            }
         }
     }
     // decode order: longest streams first, so the short ones fill the tail of the launch
@@ -1208,7 +1216,7 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
     if (xnp_status st = pool->stage_acquire(&sg)) return undo(st);
     const size_t o_plans = 0;
     const size_t o_recs = align_up(sizeof(StreamPlan) * n, 256);
-    const int32_t sets = t == 1 ? 1 : wsteps ? t : 0; // record sets: one per decode launch
+    const int32_t sets = t == 1 || wsteps ? 1 : 0; // a window step's rows derive theirs from row 0's
     const size_t o_masks = o_recs + align_up((size_t)pool->rec_stride * n * sets, 256);
     const size_t total = o_masks + sizeof(uint32_t) * masks.size();
     std::memcpy(sg->host + o_plans, plans.data(), sizeof(StreamPlan) * n);
@@ -1233,30 +1241,27 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
         }
     if (wsteps)
         // Mimi's chunk (transformer.rs:764-781): row i attends positions (p + i - window, p + i], the
-        // causal window.  Per layer the rows run in order, each a decode of one row per stream: row
-        // i's key takes the slot of position p + i - window, which no later row sees, and every
-        // filled slot holds a position inside row i's window.  So row i sees slots [0, span).
-        for (int32_t r = 0; r < t; r++)
-            for (int32_t j = 0; j < n; j++) {
-                const Stream &st = pool->streams[plans[order[j]].sid];
-                const int64_t p = (int64_t)st.current_end + st.shift + r;
-                StreamRec R;
-                std::memset(&R, 0, sizeof R);
-                R.b = plans[order[j]].out_row * t + r;
-                R.write_slot = (int32_t)(p % st.window);
-                R.span = (int32_t)std::min<int64_t>(p + 1, st.window);
-                R.nblk = (R.span + kBlock - 1) / kBlock;
-                R.pos = R.pos_pre = R.key_pos = (int32_t)p;
-                R.mask_off = -1;
-                // int8: the write page starts afresh when no other slot of it holds a row yet
-                const int32_t b0 = R.write_slot / kBlock * kBlock, filled = (int32_t)std::min<int64_t>(p, st.window);
-                bool other = false;
-                for (int32_t sl = b0; sl < std::min(b0 + kBlock, filled); sl++) other |= sl != R.write_slot;
-                R.flags = 1 | (other ? 0 : 2);
-                char *dst = sg->host + o_recs + ((size_t)r * n + j) * pool->rec_stride;
-                std::memcpy(dst, &R, sizeof R);
-                std::memcpy(dst + sizeof R, st.blocks.data(), sizeof(int32_t) * R.nblk);
-            }
+        // causal window.  Row by row, each row's key takes the slot of position p + i - window, which
+        // no later row sees, and every filled slot holds a position inside row i's window, so row i
+        // sees slots [0, min(p + i + 1, window)).  The record is row 0's, with every page of the
+        // window; the decode kernel derives row i's from it (window_row).
+        for (int32_t j = 0; j < n; j++) {
+            const Stream &st = pool->streams[plans[order[j]].sid];
+            const int64_t p = (int64_t)st.current_end + st.shift;
+            StreamRec R;
+            std::memset(&R, 0, sizeof R);
+            R.b = plans[order[j]].out_row * t;
+            R.pos = R.pos_pre = R.key_pos = (int32_t)p;
+            R.write_slot = (int32_t)(p % st.window);
+            R.span = (int32_t)std::min<int64_t>(p + 1, st.window);
+            R.nblk = (st.window + kBlock - 1) / kBlock;
+            R.mask_off = -1;
+            R.flags = 1;
+            R.window = st.window;
+            char *dst = sg->host + o_recs + (size_t)j * pool->rec_stride;
+            std::memcpy(dst, &R, sizeof R);
+            std::memcpy(dst + sizeof R, st.blocks.data(), sizeof(int32_t) * R.nblk);
+        }
     std::memcpy(sg->host + o_masks, masks.data(), sizeof(uint32_t) * masks.size());
     const size_t o_patch = pool->batch_bytes;
     const int np = (int)pool->patches.size();
@@ -1277,6 +1282,7 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
     while (!pool->d.decode_split && B.bv.split < 8 && groups * B.bv.split < 1024)
         B.bv.split *= 2;
     B.bv.masks = (const uint32_t *)(pool->dbatch + o_masks);
+    B.bv.wrow = -1;
     B.bv.n = n;
     B.bv.t = t;
     B.wsteps = wsteps;
@@ -1345,9 +1351,16 @@ extern "C" xnp_status xnp_attend(xnp_pool *pool, int32_t layer, const void *q, c
         if (B.n > 0 && (!q || !k || !v || !out)) return fail(XNP_E_INVALID, "null q, k, v or out");
         const LaunchTiming tm = pool->timing;
         pool->timing = LaunchTiming();
+        if (pool->d.cache_dtype == XNP_BF16 && B.t > kWindowRowByRow) {
+            // every row's windowed attention in one MFMA launch (the held rows from the pages, the
+            // step's own from k and v), then the rows that stay into their slots
+            HIP_TRY(launch_window_prefill(pool->view(), B.bv, layer, q, k, v, out, scale, B.stream, tm), "window attend");
+            HIP_TRY(launch_window_append(pool->view(), B.bv, layer, k, v, B.stream), "window append");
+            return XNP_OK;
+        }
         BatchView bv = B.bv;
         for (int32_t r = 0; r < B.t; r++) {
-            bv.recs = B.bv.recs + (size_t)r * B.n * B.bv.rec_stride;
+            bv.wrow = r; // the kernel derives row r's record from the step's
             HIP_TRY(launch_decode(pool->view(), bv, layer, q, k, v, out, scale, true, B.stream,
                                   r == 0 ? tm : LaunchTiming()),
                     "attend");

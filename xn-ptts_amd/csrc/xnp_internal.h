@@ -42,7 +42,9 @@ struct StreamPlan {
     int32_t ring;       // 1 on a ring: int8 freshness comes from `fresh`, not from the slot
     int32_t fresh;      // ring + int8: the write slot's page holds no other live row
     int32_t out_row;    // row of q/k/v/out (= index in the batch)
-    int32_t pad[5];
+    int32_t window;     // a window cache: its slots (rows at slot position % window), else 0
+    int32_t wbase;      // a window cache: the slot of its oldest held row
+    int32_t pad[3];
 };
 
 // One stream of a decode batch, as its work groups read it: 64 bytes, followed in the record by
@@ -53,7 +55,8 @@ struct StreamRec {
     int32_t pos, pos_pre, prefix; // as StreamPlan
     int32_t write_slot, key_pos, span, mask_off;
     int32_t flags;      // 1: ring (int8 freshness from bit 2), 2: the write page starts afresh
-    int32_t pad[6];
+    int32_t window;     // a window step's base record: the window's slots (row r derives its own)
+    int32_t pad[5];
 };
 
 // Everything a batch's kernels read, in one device buffer.
@@ -64,6 +67,7 @@ struct BatchView {
     int32_t n, t, rec_stride;
     int32_t split;  // waves per (stream, head) work group
     int32_t prefix; // 1 if some stream of the batch is an absolute ring keeping a prefix
+    int32_t wrow;   // a window step run row by row: the row this launch attends (-1 otherwise)
 };
 
 // A table entry to set before the batch's kernels run.
@@ -130,6 +134,13 @@ bool prefill_fuses_append(const PoolView &pv);
 hipError_t launch_prefill(const PoolView &pv, const BatchView &bv, int layer, const void *q,
                           const void *k, const void *v, void *out, float scale, bool fused,
                           hipStream_t stream, const LaunchTiming &timing);
+// A window step of t rows on a bf16 pool (Mimi's chunk, transformer.rs:764-781): the windowed
+// attention of every row on MFMA over the held rows (pages) and the step's own (k, v), then the
+// append of the last min(t, window) rows into their slots, (p + i) % window.
+hipError_t launch_window_prefill(const PoolView &pv, const BatchView &bv, int layer, const void *q, const void *k,
+                                 const void *v, void *out, float scale, hipStream_t stream, const LaunchTiming &timing);
+hipError_t launch_window_append(const PoolView &pv, const BatchView &bv, int layer, const void *k, const void *v,
+                                hipStream_t stream);
 hipError_t launch_evict_rotate(const PoolView &pv, const EvictRow *rows, int n,
                                const float *cos_row, const float *sin_row, hipStream_t stream);
 hipError_t launch_copy_page(const PoolView &pv, int src_page, int dst_page, hipStream_t stream);
