@@ -35,7 +35,6 @@ constexpr int kPfRound = 256;    // query rows per round: 8 waves x 2 tiles x 16
 constexpr int kPfMaxPages = 512; // page ids a work group keeps in LDS
 static_assert(kPfMaxPages >= kLaneBlocks * 8, "every page of a stream fits (a pool refuses more than 60 x 8)");
 static_assert(64 * kPfWaves == kPfKeys * 8, "one thread stages 16 bytes of one key per chunk");
-static_assert(2 * kPfKeys * kPfLd >= kPfWaves / 2 * 32 * kHeadDim, "half the waves' output tiles fit in each buffer");
 
 __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4))) void k_prefill_mfma(
     PoolView pv, BatchView bv, int layer, const void *q, const void *knew, const void *vnew, void *out, float qmul,
@@ -251,35 +250,23 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
         Stage st;
         issue(0, st);
         for (int c = 0; c < nch; ++c) step(c, st);
-        __syncthreads(); // every wave is done with both buffers
+        __syncthreads(); // the next round's staging overwrites both buffers
 
-        // The output leaves as whole 128-byte rows: each wave writes its tiles' O / l (l: the row's
-        // sum over its 4 lanes), rounded to bf16, into 4 KB of the buffers of its own as
-        // [16 j + l16][unit ^ (row & 7)], and stores 8 rows at a time.
-        uint16_t *stage = w < kPfWaves / 2 ? &ks[0][0] + w * 32 * kHeadDim : &vs[0][0] + (w - kPfWaves / 2) * 32 * kHeadDim;
+        // out[row][h][16 dg + 4 g .. +3] = O / l, the row's sum reduced over its 4 lanes
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             float l = lsum[j];
             l += __shfl_xor(l, 16);
             l += __shfl_xor(l, 32);
-            const float inv = 1.0f / l; // not stored for a tile past the round
-            const int row = 16 * j + l16;
+            const int qrow = 16 * tile[j] + l16;
+            if (tile[j] < 0 || qrow >= t) continue;
+            const float inv = 1.0f / l;
+            uint16_t *orow = (uint16_t *)out + (((size_t)P.out_row * t + qrow) * pv.H + h) * kHeadDim;
 #pragma unroll
             for (int dg = 0; dg < 4; ++dg)
-                *(uint2 *)(stage + row * kHeadDim + 8 * ((2 * dg + (g >> 1)) ^ (row & 7)) + 4 * (g & 1)) =
-                    make_uint2(pack_bf16(o[j][dg][0] * inv, o[j][dg][1] * inv),
-                               pack_bf16(o[j][dg][2] * inv, o[j][dg][3] * inv));
+                *(uint2 *)(orow + 16 * dg + 4 * g) = make_uint2(pack_bf16(o[j][dg][0] * inv, o[j][dg][1] * inv),
+                                                                pack_bf16(o[j][dg][2] * inv, o[j][dg][3] * inv));
         }
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int row = 8 * k + (lane >> 3), unit = lane & 7, j = row >> 4;
-            const int qrow = 16 * tile[j] + (row & 15);
-            if (tile[j] >= 0 && qrow < t)
-                *(uint4 *)((uint16_t *)out + (((size_t)P.out_row * t + qrow) * pv.H + h) * kHeadDim + 8 * unit) =
-                    *(const uint4 *)(stage + row * kHeadDim + 8 * (unit ^ (row & 7)));
-        }
-        __syncthreads(); // the next round's staging overwrites both buffers
     }
 }
 
