@@ -159,6 +159,32 @@ __device__ void append_row_wave(const PoolView &pv, int layer, int page, int row
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// direct-to-LDS loads with hand-placed waits (the window prefill's ring, the q8 GEMM's ring)
+
+// The lane index, recomputed where it is used: the address pieces of a chunk's loads would
+// otherwise be kept in registers across the whole loop, which the loop's own work needs.
+__device__ __forceinline__ int lane_here(int lane) {
+    int x;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(x) : "v"(lane));
+    return x;
+}
+
+// A work-group barrier for LDS alone: __syncthreads also waits for every global access of the wave
+// in flight, which would drain the chunk loads issued ahead.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// A 1 KB load of the wave straight into LDS: lane l's 16 bytes at src go to lds + 16 l
+// (global_load_lds_dwordx4, LDS base in M0).  Written out here because the compiler makes every LDS
+// access after its own form of this load wait for all loads in flight (vmcnt(0)), which would drain
+// the chunks issued ahead; the caller's own `s_waitcnt vmcnt(n)` is the wait these loads get.  Every
+// wait the compiler places for its own loads stays correct, as vector-memory accesses complete in
+// the order issued (they can only wait longer).
+__device__ __forceinline__ void dma16(const void *src, void *lds) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)lds);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base) : "memory", "m0");
+}
+
 template <int CDT> struct Lanes {
     static constexpr int DPL = 16 / esize<CDT>();
     static constexpr int LPR = kHeadDim / DPL;
