@@ -282,6 +282,35 @@ def test_grouped_heads_on_rings(cache, act, mode):
         p.assert_cache_equal(i)
 
 
+@pytest.mark.parametrize("h", [8, 16])
+def test_grouped_heads_on_prefix_rings_take_the_mfma_decode(h):
+    # 8 and 16 query heads over one kv head (the MFMA decode of a whole kv head) on absolute rings
+    # with voice prefixes of 0, 5 and 20 rows (20: the prefix ends inside the second page), so that
+    # the batch keeps a second query position: keys before a stream's prefix are scored against its
+    # query at pos_pre (transformer.rs:879-929 restated as the absolute ring), the others at pos.
+    # Frames slide over a context of 40 slots with the oldest evicted, 60 steps, every output held to
+    # the oracle and every cache row bit-exact.
+    p = Pair(cache="bf16", act="bf16", H=h, KVH=1, streams=3, cap=96, seed=70 + h)
+    prefixes, context = [0, 5, 20], 40
+    for i, pre in enumerate(prefixes):
+        p.fill(i, pre)
+        p.pool.start_ring(p.ids[i], "absolute", prefix=pre)
+        p.orc[i].start_ring("absolute", prefix=pre)
+    worst = 0.0
+    for steps in range(60):
+        for i, pre in enumerate(prefixes):
+            slot = pre + steps % context
+            if p.orc[i].ring_info()["valid"][slot]:
+                p.orc[i].evict(pre, [slot])
+                p.pool.evict(p.ids[i], pre, [slot])
+            p.orc[i].set_ring_slot(slot)
+            p.pool.set_ring_slot(p.ids[i], slot)
+        worst = max(worst, p.step())
+    for i in range(3):
+        p.assert_cache_equal(i)
+    assert worst <= TOL["bf16"]
+
+
 def test_empty_batch_is_a_no_op():
     p = Pair(streams=1, cap=16)
     p.pool.begin([])

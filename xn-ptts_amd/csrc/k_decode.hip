@@ -404,10 +404,11 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(Lane
 }
 
 // bf16 pools with 2 to 16 query heads per kv head decode a whole kv head per work group on MFMA
-// (k_decode_gqa), unless a stream of the batch keeps a ring prefix (a second query position)
+// (k_decode_gqa), a ring prefix (a second query position) included
 static bool decode_on_mfma(const PoolView &pv, bool prefix) {
+    (void)prefix;
     const int G = pv.H / pv.KVH;
-    return pv.cache_dt == DT_BF16 && pv.act_dt == DT_BF16 && G >= 2 && G <= 16 && !prefix;
+    return pv.cache_dt == DT_BF16 && pv.act_dt == DT_BF16 && G >= 2 && G <= 16;
 }
 
 int decode_heads_per_group(const PoolView &pv, bool prefix) {

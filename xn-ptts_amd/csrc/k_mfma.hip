@@ -616,8 +616,8 @@ __global__ __launch_bounds__(64 * kWpWaves) __attribute__((amdgpu_waves_per_eu(2
 }
 
 // ---------------------------------------------------------------------------------------------
-// Grouped-head decode on MFMA: bf16 pages and queries, 2 to 16 query heads per kv head, no ring
-// prefix.  One work group per (stream, kv head), whose G query heads are the 16 columns of the
+// Grouped-head decode on MFMA: bf16 pages and queries, 2 to 16 query heads per kv head.  One work
+// group per (stream, kv head), whose G query heads are the 16 columns of the
 // MFMA tiles (columns past G hold zeros), so that each page is read once and its 16 keys meet all
 // G heads in a few instructions.  The contractions are the prompt prefill's, transposed so that P
 // never leaves registers:
@@ -629,10 +629,13 @@ __global__ __launch_bounds__(64 * kWpWaves) __attribute__((amdgpu_waves_per_eu(2
 //   O^T += V^T P^T   v_mfma_f32_16x16x16_bf16, B = P^T straight from the S^T registers, A = V^T by
 //                    transposed reads (ds_read_b64_tr_b16) of the page's V, copied into a
 //                    wave-private LDS tile.
-// Pages, SPLIT waves per group, the fused append and the LDS merge are attend_core's.
+// Pages, SPLIT waves per group, the fused append and the LDS merge are attend_core's.  PREFIX (some
+// stream of the batch keeps an absolute ring's prefix): the keys before the prefix are scored
+// against the queries rotated at pos_pre (attend_core's second query position), a second S^T of
+// the same K operand on the pages that hold prefix rows, taken row by row in the same lanes.
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 
-template <int SPLIT>
+template <int SPLIT, bool PREFIX>
 __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4))) void k_decode_gqa(
     PoolView pv, BatchView bv, int layer, const void *q, const void *knew, const void *vnew, void *out, float qmul,
     int fused) {
@@ -668,14 +671,14 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
         my_seen = ok ? seen : 0;
     }
 
-    // B operands of S^T: query head kvh G + l16, dims 32 kc + 8 g .. +7, rotated at R.pos and
-    // rounded to bf16 (zeros past G)
-    bf16x8_t qb[2];
-    {
+    // B operands of S^T: query head kvh G + l16, dims 32 kc + 8 g .. +7, rotated at R.pos (PREFIX:
+    // and at R.pos_pre) and rounded to bf16 (zeros past G)
+    bf16x8_t qb[2], qpre[2];
+    auto rotated = [&](int pos, bf16x8_t (&dst)[2]) {
         const bool live = l16 < G;
         const int hq = kvh * G + min(l16, G - 1);
         const uint16_t *qp = (const uint16_t *)q + ((size_t)R.b * pv.H + hq) * kHeadDim;
-        const float4 *cs = (const float4 *)(pv.rope + (size_t)R.pos * (kHeadDim / 2));
+        const float4 *cs = (const float4 *)(pv.rope + (size_t)pos * (kHeadDim / 2));
 #pragma unroll
         for (int kc = 0; kc < 2; ++kc) {
             const uint4 raw = *(const uint4 *)(qp + 32 * kc + 8 * g);
@@ -690,9 +693,11 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
                 const float a = x0 * c, bb = x1 * s, e = x0 * s, f = x1 * c;
                 o4[i] = live ? pack_bf16(a - bb, e + f) : 0u;
             }
-            qb[kc] = as_bf16x8(make_uint4(o4[0], o4[1], o4[2], o4[3]));
+            dst[kc] = as_bf16x8(make_uint4(o4[0], o4[1], o4[2], o4[3]));
         }
-    }
+    };
+    rotated(R.pos, qb);
+    if constexpr (PREFIX) rotated(R.prefix > 0 ? R.pos_pre : R.pos, qpre);
 
     const uint16_t *kbase = (const uint16_t *)pv.pages + tile_index(pv, layer, 0, 0, kvh) * (kBlock * kHeadDim);
     const uint16_t *vbase = (const uint16_t *)pv.pages + tile_index(pv, layer, 1, 0, kvh) * (kBlock * kHeadDim);
@@ -723,10 +728,24 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
         // accesses complete in order, so no barrier
         *(uint4 *)&kt[w][lane >> 3][8 * (lane & 7)] = kr[0];
         *(uint4 *)&kt[w][8 + (lane >> 3)][8 * (lane & 7)] = kr[1];
+        bf16x8_t ka[2];
 #pragma unroll
-        for (int kc = 0; kc < 2; ++kc)
-            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(*(const uint4 *)&kt[w][l16][32 * kc + 8 * g]), qb[kc],
-                                                       s, 0, 0, 0);
+        for (int kc = 0; kc < 2; ++kc) {
+            ka[kc] = as_bf16x8(*(const uint4 *)&kt[w][l16][32 * kc + 8 * g]);
+            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[kc], qb[kc], s, 0, 0, 0);
+        }
+        if constexpr (PREFIX) {
+            // a page holding prefix rows (uniform): those rows take the scores of the queries at pos_pre
+            const int base = (w + j * SPLIT) * kBlock;
+            if (base < R.prefix) {
+                f32x4_t sp = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kc = 0; kc < 2; ++kc) sp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[kc], qpre[kc], sp, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (base + 4 * g + r < R.prefix) s[r] = sp[r];
+            }
+        }
         // lane: query head l16 against keys 4 g + r of the page
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -834,13 +853,22 @@ hipError_t launch_decode_gqa(const PoolView &pv, const BatchView &bv, int layer,
     const float qmul = scale * 1.4426950408889634f;
     const dim3 grid(bv.n * pv.KVH);
     const int f = fused ? 1 : 0;
-    switch (bv.split) {
-    case 1: XNP_LAUNCH((k_decode_gqa<1>), grid, dim3(64), stream, tm, pv, bv, layer, q, k, v, out, qmul, f); break;
-    case 2: XNP_LAUNCH((k_decode_gqa<2>), grid, dim3(128), stream, tm, pv, bv, layer, q, k, v, out, qmul, f); break;
-    case 4: XNP_LAUNCH((k_decode_gqa<4>), grid, dim3(256), stream, tm, pv, bv, layer, q, k, v, out, qmul, f); break;
-    case 8: XNP_LAUNCH((k_decode_gqa<8>), grid, dim3(512), stream, tm, pv, bv, layer, q, k, v, out, qmul, f); break;
-    default: return hipErrorInvalidValue;
+#define XNP_GQA(S, PFX) XNP_LAUNCH((k_decode_gqa<S, PFX>), grid, dim3(64 * S), stream, tm, pv, bv, layer, q, k, v, out, qmul, f)
+#define XNP_GQA_SPLIT(PFX)                                                                                          \
+    switch (bv.split) {                                                                                            \
+    case 1: XNP_GQA(1, PFX); break;                                                                                \
+    case 2: XNP_GQA(2, PFX); break;                                                                                \
+    case 4: XNP_GQA(4, PFX); break;                                                                                \
+    case 8: XNP_GQA(8, PFX); break;                                                                                \
+    default: return hipErrorInvalidValue;                                                                          \
     }
+    if (bv.prefix) {
+        XNP_GQA_SPLIT(true);
+    } else {
+        XNP_GQA_SPLIT(false);
+    }
+#undef XNP_GQA_SPLIT
+#undef XNP_GQA
     return hipGetLastError();
 }
 
