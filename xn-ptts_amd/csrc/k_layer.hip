@@ -156,15 +156,15 @@ constexpr int kGmPD = 3;  // K chunks of loads in flight
 // 2048 rows: the epilogue took 2.4-3.1 us of each projection with 2-byte stores.
 constexpr int kGsLd = 72; // the staged epilogue's LDS row in bf16
 
-template <int EPI, bool AF32, int MI, int KS, bool STG>
+template <int EPI, bool AF32, int MI, int KS, bool STG, int NKC>
 __global__ __launch_bounds__(256 * KS) void k_gemm_q8(const uint16_t *A, int M, int K, const int8_t *W, const float *s,
                                                       int N, GemmOut go) {
     constexpr int BM = 32 * MI;
     static_assert(KS == 1 || KS == 2, "one or two halves");
     __shared__ __attribute__((aligned(16))) uint16_t As[KS][2][BM][kGmLd];
     __shared__ __attribute__((aligned(16))) uint16_t Ws[KS][2][kGmT][kGmLd];
-    const int ntn = (N + kGmT - 1) / kGmT;
-    const int m0 = (blockIdx.x / ntn) * BM, n0 = (blockIdx.x % ntn) * kGmT;
+    const int ntn = (N + kGmT - 1) / kGmT, tile = xcd_tile(blockIdx.x, gridDim.x);
+    const int m0 = (tile / ntn) * BM, n0 = (tile % ntn) * kGmT;
     const int tid = threadIdx.x & 255, h = KS > 1 ? (int)(threadIdx.x >> 8) : 0;
     const int w = tid >> 6, lane = tid & 63, g = lane >> 4, l16 = lane & 15;
     const int wm = w & 1, wn = w >> 1;
@@ -215,13 +215,14 @@ __global__ __launch_bounds__(256 * KS) void k_gemm_q8(const uint16_t *A, int M, 
     auto store = [&](int buf, int set, int kc) {
         uint4 a0 = bf16_row(ra0[set]), a1 = a0, wq = rw[set];
         if constexpr (MI == 2) a1 = bf16_row(ra1[set]);
-        if ((kc + 1) * kGmK > K) { // the chunk reaches past K (uniform over the group)
-            const int k0 = kc * kGmK;
-            const uint32_t ma = k0 + 8 * a_k < K ? ~0u : 0u, mw = k0 + 16 * w_k < K ? ~0u : 0u;
-            a0 = masked(a0, ma);
-            a1 = masked(a1, ma);
-            wq = masked(wq, mw);
-        }
+        // words past K zeroed with masks rather than under a branch: a branch here splits the
+        // loop, and past the join the compiler no longer knows which loads are still in flight
+        // (it then waits for all of them before the next load)
+        const int k0 = kc * kGmK;
+        const uint32_t ma = k0 + 8 * a_k < K ? ~0u : 0u, mw = k0 + 16 * w_k < K ? ~0u : 0u;
+        a0 = masked(a0, ma);
+        a1 = masked(a1, ma);
+        wq = masked(wq, mw);
         *(uint4 *)&As[h][buf][a_r][8 * a_k] = a0;
         if constexpr (MI == 2) *(uint4 *)&As[h][buf][a_r + 32][8 * a_k] = a1;
         *(uint4 *)&Ws[h][buf][w_r][16 * w_k] = make_uint4(widen2(wq.x, 0), widen2(wq.x, 16), widen2(wq.y, 0), widen2(wq.y, 16));
@@ -279,41 +280,52 @@ __global__ __launch_bounds__(256 * KS) void k_gemm_q8(const uint16_t *A, int M, 
 
     // this half's chunks: c = 0 .. nkh - 1 is chunk h + KS c.  Both halves run nkmax rounds, one
     // barrier each, whatever their own count (the launcher takes KS = 2 only when nk >= 2 KS).
-    const int nk = (K + kGmK - 1) / kGmK;
-    const int nkh = (nk - h + KS - 1) / KS, nkmax = (nk + KS - 1) / KS;
-    load(h, 0);
+    // Every round loads and stores unconditionally, past this half's last chunk its last chunk
+    // again (a duplicate nobody reads): loads under a branch leave the compiler unsure which loads
+    // are in flight after it, and it then drains them all before the next one.  NKC > 0: K is
+    // NKC x KS chunks exactly, and the rounds are unrolled whole -- the back edge of a loop makes
+    // the compiler copy load registers still in flight, which waits for them.
+    const int nk = NKC > 0 ? NKC * KS : (K + kGmK - 1) / kGmK;
+    const int nkh = NKC > 0 ? NKC : (nk - h + KS - 1) / KS, nkmax = NKC > 0 ? NKC : (nk + KS - 1) / KS;
+    auto chunk = [&](int c) { return h + KS * min(c, nkh - 1); };
+    auto round = [&](int c, int u) { // u = c % kGmPD: set indices stay constants
+        const int buf = c & 1;
+        load(chunk(c + kGmPD), u); // set u held chunk c, already in LDS
+        if (c < nkh) {
 #pragma unroll
-    for (int c = 1; c < kGmPD; ++c)
-        if (c < nkh) load(h + KS * c, c);
+            for (int ks = 0; ks < kGmK / 32; ++ks) {
+                bf16x8_t a[MI], bw[2];
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+                    a[i] = as_bf16x8(*(const uint4 *)&As[h][buf][16 * MI * wm + 16 * i + l16][32 * ks + 8 * g]);
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    bw[i] = as_bf16x8(*(const uint4 *)&Ws[h][buf][32 * wn + 16 * i + l16][32 * ks + 8 * g]);
+#pragma unroll
+                for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+                    for (int ni = 0; ni < 2; ++ni)
+                        acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mi], bw[ni], acc[mi][ni], 0, 0, 0);
+            }
+        }
+        // buffer buf ^ 1's last readers finished before the previous barrier
+        store(buf ^ 1, (u + 1) % kGmPD, chunk(c + 1));
+        __syncthreads();
+    };
+#pragma unroll
+    for (int c = 0; c < kGmPD; ++c) load(chunk(c), c);
     store(0, 0, h);
     __syncthreads();
-    for (int cb = 0; cb < nkmax; cb += kGmPD) {
+    if constexpr (NKC > 0) {
 #pragma unroll
-        for (int u = 0; u < kGmPD; ++u) { // set indices stay constants
-            const int c = cb + u;
-            if (c >= nkmax) break; // uniform over the group
-            const int buf = c & 1;
-            if (c + kGmPD < nkh) load(h + KS * (c + kGmPD), u); // set u held chunk c, already in LDS
-            if (c < nkh) {
+        for (int c = 0; c < NKC; ++c) round(c, c % kGmPD);
+    } else {
+        for (int cb = 0; cb < nkmax; cb += kGmPD) {
 #pragma unroll
-                for (int ks = 0; ks < kGmK / 32; ++ks) {
-                    bf16x8_t a[MI], bw[2];
-#pragma unroll
-                    for (int i = 0; i < MI; ++i)
-                        a[i] = as_bf16x8(*(const uint4 *)&As[h][buf][16 * MI * wm + 16 * i + l16][32 * ks + 8 * g]);
-#pragma unroll
-                    for (int i = 0; i < 2; ++i)
-                        bw[i] = as_bf16x8(*(const uint4 *)&Ws[h][buf][32 * wn + 16 * i + l16][32 * ks + 8 * g]);
-#pragma unroll
-                    for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-                        for (int ni = 0; ni < 2; ++ni)
-                            acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mi], bw[ni], acc[mi][ni], 0, 0, 0);
-                }
+            for (int u = 0; u < kGmPD; ++u) {
+                if (cb + u >= nkmax) break; // uniform over the group
+                round(cb + u, u);
             }
-            // buffer buf ^ 1's last readers finished before the previous barrier
-            if (c + 1 < nkh) store(buf ^ 1, (u + 1) % kGmPD, h + KS * (c + 1));
-            __syncthreads();
         }
     }
     if constexpr (KS > 1) {
@@ -487,15 +499,15 @@ static bool gemm_staged(int N, int epi, const GemmOut &go) {
     return true;
 }
 
-template <int MI, int KS, bool STG>
+template <int MI, int KS, bool STG, int NKC>
 static hipError_t gemm_q8_stg(const void *A, int M, int K, const int8_t *W, const float *s, int N, int epi,
                               const GemmOut &go, hipStream_t stream) {
     const dim3 grid(((N + kGmT - 1) / kGmT) * ((M + 32 * MI - 1) / (32 * MI))), block(256 * KS);
     const uint16_t *a = (const uint16_t *)A;
-#define XNP_GEMM(E) hipLaunchKernelGGL((k_gemm_q8<E, false, MI, KS, STG>), grid, block, 0, stream, a, M, K, W, s, N, go)
+#define XNP_GEMM(E) hipLaunchKernelGGL((k_gemm_q8<E, false, MI, KS, STG, NKC>), grid, block, 0, stream, a, M, K, W, s, N, go)
     if (go.a_f32) {
-        if (epi != kStore) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((k_gemm_q8<kStore, true, MI, KS, STG>), grid, block, 0, stream, a, M, K, W, s, N, go);
+        if (epi != kStore || NKC != 0) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((k_gemm_q8<kStore, true, MI, KS, STG, 0>), grid, block, 0, stream, a, M, K, W, s, N, go);
         return hipGetLastError();
     }
     switch (epi) {
@@ -514,11 +526,15 @@ static hipError_t gemm_q8_stg(const void *A, int M, int K, const int8_t *W, cons
     return hipGetLastError();
 }
 
+// The staged epilogue's kernels come unrolled whole for K of 8 or 16 chunks per half (the flow
+// LM's 512-2048 wide projections); others run the rounds in a loop.
 template <int MI, int KS>
 static hipError_t gemm_q8_mi(const void *A, int M, int K, const int8_t *W, const float *s, int N, int epi,
                              const GemmOut &go, hipStream_t stream) {
-    if (gemm_staged(N, epi, go)) return gemm_q8_stg<MI, KS, true>(A, M, K, W, s, N, epi, go, stream);
-    return gemm_q8_stg<MI, KS, false>(A, M, K, W, s, N, epi, go, stream);
+    if (!gemm_staged(N, epi, go)) return gemm_q8_stg<MI, KS, false, 0>(A, M, K, W, s, N, epi, go, stream);
+    if (!go.a_f32 && K == 8 * KS * kGmK) return gemm_q8_stg<MI, KS, true, 8>(A, M, K, W, s, N, epi, go, stream);
+    if (!go.a_f32 && K == 16 * KS * kGmK) return gemm_q8_stg<MI, KS, true, 16>(A, M, K, W, s, N, epi, go, stream);
+    return gemm_q8_stg<MI, KS, true, 0>(A, M, K, W, s, N, epi, go, stream);
 }
 
 hipError_t launch_gemm_q8(const void *A, int M, int K, const int8_t *W, const float *s, int N, int epi,
@@ -527,12 +543,11 @@ hipError_t launch_gemm_q8(const void *A, int M, int K, const int8_t *W, const fl
     if (N <= 0 || K <= 0 || K % 16) return hipErrorInvalidValue;
     // 32-row tiles when 64-row ones would leave the chip's 1024 SIMDs under two waves each
     const int64_t groups64 = (int64_t)((N + kGmT - 1) / kGmT) * ((M + kGmT - 1) / kGmT);
+    const bool mi1 = groups64 < 512;
     // two halves per group on alternate K chunks when K is long (32 chunks and more)
     if (K >= 32 * kGmK)
-        return groups64 < 512 ? gemm_q8_mi<1, 2>(A, M, K, W, s, N, epi, go, stream)
-                              : gemm_q8_mi<2, 2>(A, M, K, W, s, N, epi, go, stream);
-    return groups64 < 512 ? gemm_q8_mi<1, 1>(A, M, K, W, s, N, epi, go, stream)
-                          : gemm_q8_mi<2, 1>(A, M, K, W, s, N, epi, go, stream);
+        return mi1 ? gemm_q8_mi<1, 2>(A, M, K, W, s, N, epi, go, stream) : gemm_q8_mi<2, 2>(A, M, K, W, s, N, epi, go, stream);
+    return mi1 ? gemm_q8_mi<1, 1>(A, M, K, W, s, N, epi, go, stream) : gemm_q8_mi<2, 1>(A, M, K, W, s, N, epi, go, stream);
 }
 
 // ---------------------------------------------------------------------------------------------

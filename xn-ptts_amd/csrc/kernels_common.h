@@ -159,6 +159,15 @@ __device__ void append_row_wave(const PoolView &pv, int layer, int page, int row
     }
 }
 
+// The dispatcher hands work group b of a grid to XCD b % 8, and each XCD has its own L2.  A tile
+// grid numbered row-major would give every XCD every eighth tile, so each XCD would read nearly
+// all of the tiles' shared operand rows.  xcd_tile renumbers group b of G so that XCD x takes one
+// contiguous run of about G / 8 tiles (XCDs below G % 8 one more), which share their rows.
+__device__ __forceinline__ int xcd_tile(int b, int G) {
+    const int q = G >> 3, r = G & 7, x = b & 7, i = b >> 3;
+    return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + i;
+}
+
 // ---------------------------------------------------------------------------------------------
 // direct-to-LDS loads with hand-placed waits (the window prefill's ring, the q8 GEMM's ring)
 
