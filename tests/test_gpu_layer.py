@@ -39,7 +39,7 @@ def test_layer_norm_matches_the_oracle(rows, dim):
     assert rel_err(host(out), oracle.layer_norm(x, w, b, act="bf16")) <= TOL
 
 
-@pytest.mark.parametrize("rows,k,n", [(1, 512, 64), (37, 512, 1536), (200, 512, 2048), (70, 2048, 512)])
+@pytest.mark.parametrize("rows,k,n", [(1, 512, 64), (37, 512, 1536), (200, 512, 2048), (300, 1024, 512), (70, 2048, 512)])
 @pytest.mark.parametrize("epi", ["store", "gelu_erf", "gelu_tanh", "residual"])
 def test_linear_q8_matches_the_oracle(rows, k, n, epi):
     rng = np.random.default_rng(rows * 7 + n)
