@@ -132,11 +132,13 @@ def decode_bytes(lens, elem=2, kvh=H):
     return int((kv + fixed + table).sum())
 
 
-def window_bytes(attended):
-    """int8 window: K/V rows attended, one scale per (page, head) for K and V, bf16 q/out/new rows."""
+def window_bytes(attended, kvh=H):
+    """int8 window: K/V rows attended and one scale per (page, kv head) for K and V (kvh stored kv
+    heads), bf16 q and out for every query head, the new bf16 k/v rows and their int8 append."""
     a = np.asarray(attended, np.int64)
     pages = (a + 15) // 16 + 1
-    return int((2 * a * H * D + 2 * H * 4 * pages + H * D * 2 * (1 + 2 + 1) + 2 * H * D + 4 * pages).sum())
+    return int((2 * a * kvh * D + 2 * kvh * 4 * pages + H * D * 2 * 2 + kvh * D * 2 * 2 + 2 * kvh * D
+                + 4 * pages).sum())
 
 
 class NoGC:
@@ -453,13 +455,15 @@ def run_window(args, xnp, torch):
     lens = rng.integers(64, 2049, S)
     mbps = SPAN // 16
     total = int(lens.max()) + args.warmup + args.steps + 2
-    pool = xnp.KvPool(num_layers=L, num_heads=H, num_blocks=S * mbps + 16, max_streams=S, max_blocks_per_stream=mbps,
-                      cache_dtype="i8", act_dtype="bf16", max_pos=total + 16, page_seed=SEED + 5)
+    kvh = args.kv_heads or H
+    pool = xnp.KvPool(num_layers=L, num_heads=H, num_kv_heads=kvh, num_blocks=S * mbps + 16, max_streams=S,
+                      max_blocks_per_stream=mbps, cache_dtype="i8", act_dtype="bf16", max_pos=total + 16,
+                      page_seed=SEED + 5)
     ids = [pool.init_state(SPAN) for _ in range(S)]
     for sid in ids:
         pool.start_ring(sid, "absolute", prefix=0)
     gen = torch.Generator(device=dev).manual_seed(SEED + 6)
-    kv_new = [torch.randn((S, H, D), generator=gen, device=dev).to(torch.bfloat16) for _ in range(2 * L)]
+    kv_new = [torch.randn((S, kvh, D), generator=gen, device=dev).to(torch.bfloat16) for _ in range(2 * L)]
     q = [torch.randn((S, H, D), generator=gen, device=dev).to(torch.bfloat16) for _ in range(L)]
     out = [torch.empty((S, H, D), dtype=torch.bfloat16, device=dev) for _ in range(L)]
     torch.cuda.synchronize()
@@ -485,7 +489,7 @@ def run_window(args, xnp, torch):
     def step(events):
         att = np.minimum(written + 1, WINDOW)
         if events is not None:
-            bytes_timed[0] += window_bytes(att)  # the one launch this step times
+            bytes_timed[0] += window_bytes(att, kvh)  # the one launch this step times
             bytes_timed[1] += 1
         pool.slide_batch(ids, 0, SPAN, WINDOW, 1, heads + written)
         pool.begin(ids)
@@ -501,14 +505,15 @@ def run_window(args, xnp, torch):
     bytes_per_launch = bytes_timed[0] / bytes_timed[1]  # every layer of a step moves the same bytes
     achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
     fps = S / (ms / 1000.0)
-    cpu = None if args.no_cpu else cpu_window(L, lens, args.cpu_seconds)
+    cpu = None if args.no_cpu or kvh != H else cpu_window(L, lens, args.cpu_seconds)  # the oracle leg keeps H kv heads
     config = {"workload": f"int8 K/V sliding window: {S} streams, {L} layers x {H} heads x {D}, fp32 scales per "
                           f"(page, head), window {WINDOW} on {SPAN}-slot rings, write heads U[0,4096), "
                           f"rows written U[64,2048]; evict + append + dequant-on-gather decode per step",
-              "streams": S, "layers": L, "window": WINDOW, "ring_slots": SPAN}
+              "streams": S, "layers": L, "window": WINDOW, "ring_slots": SPAN, "kv_heads": kvh}
+    wkey = {"streams": S, "layers": L} if kvh == H else {"streams": S, "layers": L, "kv_heads": kvh}
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic_of("window", {"streams": S, "layers": L}, bytes_per_launch),
+            "traffic": traffic_of("window", wkey, bytes_per_launch),
             "kernel": "k_decode<int8> (fused append + quantize + RoPE + dequant decode), one launch per layer",
             "avg_kernel_us": round(avg_ms * 1000.0, 2), "bytes_per_launch": int(bytes_per_launch)}
     return line("frames/sec, int8 KV sliding window (512) at 1024 streams; decode HBM GB/s % peak", fps,

@@ -233,11 +233,11 @@ def test_grouped_kv_heads(cache, act, kvh):
 
 
 @pytest.mark.parametrize("h,kvh", [(6, 2), (12, 2), (12, 3), (8, 8), (8, 2)])
-@pytest.mark.parametrize("cache,act", [("bf16", "bf16"), ("f32", "f32")])
+@pytest.mark.parametrize("cache,act", [("bf16", "bf16"), ("f32", "f32"), ("i8", "bf16")])
 def test_grouped_heads_of_other_ratios(cache, act, h, kvh):
     # 3, 6, 4, 1 and 4 query heads per kv head: a decode work group then takes one, two or four of
-    # them (or, bf16, the whole kv head on MFMA).  13 streams: the grid's XCD runs of 8 streams,
-    # one whole run and a tail of 5.
+    # them (or, bf16 and int8, the whole kv head on MFMA).  13 streams: the grid's XCD runs of 8
+    # streams, one whole run and a tail of 5.
     lens = [0, 5, 16, 17, 40, 63, 90, 1, 33, 48, 2, 79, 15]
     p = Pair(cache=cache, act=act, H=h, KVH=kvh, streams=len(lens), cap=96, seed=40 + h + kvh)
     for i, n in enumerate(lens):

@@ -405,20 +405,25 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(Lane
 
 // bf16 pools with 2 to 16 query heads per kv head decode a whole kv head per work group on MFMA
 // (k_decode_gqa), a ring prefix (a second query position) included
+// The MFMA decode (k_decode_gqa): 2 to 16 query heads per kv head, bf16 pages, or int8 pages with
+// no ring prefix in the batch (its f16 scores take one query position).  One head per kv head
+// stays on the VALU: on MFMA each lane would carry four scores of which one is live, and the
+// int8 window measured 108.6 us there against 99.5 us (at 4 and 8 heads per kv head: 34 and 23.7
+// us against 70 and 68).
 static bool decode_on_mfma(const PoolView &pv, bool prefix) {
-    (void)prefix;
     const int G = pv.H / pv.KVH;
-    return pv.cache_dt == DT_BF16 && pv.act_dt == DT_BF16 && G >= 2 && G <= 16;
+    if (pv.act_dt != DT_BF16 || G < 2 || G > 16) return false;
+    return pv.cache_dt == DT_BF16 || (pv.cache_dt == DT_I8 && !prefix);
 }
 
 int decode_heads_per_group(const PoolView &pv, bool prefix) {
     // query heads of one kv head share a group's page reads: all of them on MFMA; else four when
     // four divide the group and no stream of the batch keeps a ring prefix (whose second query
-    // would spill them), else two; int8 keeps one (its registers hold no second head at four
-    // waves per SIMD)
+    // would spill them), else two; int8 on the VALU keeps one (its registers hold no second head
+    // at four waves per SIMD)
     const int G = pv.H / pv.KVH;
-    if (pv.cache_dt == DT_I8) return 1;
     if (decode_on_mfma(pv, prefix)) return G;
+    if (pv.cache_dt == DT_I8) return 1;
     return G % 4 == 0 && !prefix ? 4 : G % 2 == 0 ? 2 : 1;
 }
 
@@ -475,7 +480,10 @@ hipError_t launch_decode(const PoolView &pv, const BatchView &bv, int layer, con
         case 2: return decode_impl<DT_BF16, true, 2>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
         default: return decode_impl<DT_BF16, true, 1>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
         }
-    case DT_I8 * 2 + DT_BF16: return decode_impl<DT_I8, true, 1>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
+    case DT_I8 * 2 + DT_BF16:
+        if (decode_on_mfma(pv, bv.prefix != 0))
+            return launch_decode_gqa(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
+        return decode_impl<DT_I8, true, 1>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
     case DT_I8 * 2 + DT_F32: return decode_impl<DT_I8, false, 1>(pv, bv, layer, q, k, v, out, scale, fused, stream, tm);
     default: return hipErrorInvalidValue;
     }

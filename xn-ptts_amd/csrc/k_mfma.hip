@@ -616,7 +616,8 @@ __global__ __launch_bounds__(64 * kWpWaves) __attribute__((amdgpu_waves_per_eu(2
 }
 
 // ---------------------------------------------------------------------------------------------
-// Grouped-head decode on MFMA: bf16 pages and queries, 2 to 16 query heads per kv head.  One work
+// Grouped-head decode on MFMA: bf16 or int8 pages, bf16 queries, 2 to 16 query heads per kv head
+// (the kernel takes any G from 1; the launcher sends G = 1 to the VALU decode).  One work
 // group per (stream, kv head), whose G query heads are the 16 columns of the
 // MFMA tiles (columns past G hold zeros), so that each page is read once and its 16 keys meet all
 // G heads in a few instructions.  The contractions are the prompt prefill's, transposed so that P
@@ -633,13 +634,25 @@ __global__ __launch_bounds__(64 * kWpWaves) __attribute__((amdgpu_waves_per_eu(2
 // stream of the batch keeps an absolute ring's prefix): the keys before the prefix are scored
 // against the queries rotated at pos_pre (attend_core's second query position), a second S^T of
 // the same K operand on the pages that hold prefix rows, taken row by row in the same lanes.
+//
+// CDT = DT_I8 (int8 pages with f32 scales per (page, kv head), no prefix; the fused append is
+// attend_core's, re-reading the write page's scales after it): the VALU decode's arithmetic moved
+// onto the MFMA.  A code byte c goes
+// to f16 as 1024 + (c + 128) = 1152 + c by one byte permute (c ^ 0x80 under the f16 exponent of
+// 1024), the rotated bf16 queries convert to f16 exactly, so v_mfma_f32_16x16x32_f16 sums
+// q (1152 + c) and the score is sk (that sum - 1152 sum(q)).  V codes widen to bf16 exactly
+// (|c| <= 127) and P^T carries p sv rounded to bf16, so O needs no bias; the softmax sum keeps p.
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 
-template <int SPLIT, bool PREFIX>
+template <int SPLIT, bool PREFIX, int CDT>
 __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4))) void k_decode_gqa(
     PoolView pv, BatchView bv, int layer, const void *q, const void *knew, const void *vnew, void *out, float qmul,
     int fused) {
-    constexpr int DEPTH = 2; // pages in flight ahead of the one being reduced
+    static_assert(CDT == DT_BF16 || (CDT == DT_I8 && !PREFIX), "bf16 pages, or int8 pages without a prefix");
+    constexpr bool I8 = CDT == DT_I8;
+    constexpr int NL = I8 ? 1 : 2; // 1 KB loads per K or V tile of a page
+    constexpr int DEPTH = 2;       // pages in flight ahead of the one being reduced
     __shared__ __attribute__((aligned(16))) uint16_t vt[SPLIT][kBlock][kPfLd]; // each wave's V tile, [key][dim]
     __shared__ __attribute__((aligned(16))) uint16_t kt[SPLIT][kBlock][kPfLd]; // each wave's K tile, [key][dim]
     __shared__ float part[SPLIT][16][kPartStride];
@@ -658,6 +671,7 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
     // per-page metadata, lane j holding page w + j * SPLIT (as attend_core)
     int my_page = 0, my_ok = 0;
     uint32_t my_seen = 0;
+    float my_sk = 0.f, my_sv = 0.f; // int8: the page's K and V scales
     const int pg_raw = w + lane * SPLIT < pv.mbps ? rec_pages[w + lane * SPLIT] : -1;
     if (lane < nb) {
         const int base = (w + lane * SPLIT) * kBlock;
@@ -669,6 +683,10 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
         my_page = ok ? pg_raw : 0;
         my_ok = ok ? 1 : 0;
         my_seen = ok ? seen : 0;
+        if constexpr (I8) {
+            my_sk = pv.scales[tile_index(pv, layer, 0, my_page, kvh)];
+            my_sv = pv.scales[tile_index(pv, layer, 1, my_page, kvh)];
+        }
     }
 
     // B operands of S^T: query head kvh G + l16, dims 32 kc + 8 g .. +7, rotated at R.pos (PREFIX:
@@ -698,10 +716,33 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
     };
     rotated(R.pos, qb);
     if constexpr (PREFIX) rotated(R.prefix > 0 ? R.pos_pre : R.pos, qpre);
+    // int8: the same queries as f16 (exact) and their sum over the 64 dims of the lane's column
+    f16x8_t qh[2];
+    float qsum = 0.f;
+    if constexpr (I8) {
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) {
+            uint4 u;
+            __builtin_memcpy(&u, &qb[kc], 16);
+            const uint32_t *w4 = (const uint32_t *)&u;
+            uint32_t h4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float x0 = bf16_value(w4[i] & 0xffffu), x1 = bf16_value(w4[i] >> 16);
+                h4[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x0, x1));
+                qsum += x0;
+                qsum += x1;
+            }
+            qh[kc] = __builtin_bit_cast(f16x8_t, make_uint4(h4[0], h4[1], h4[2], h4[3]));
+        }
+        qsum += __shfl_xor(qsum, 16);
+        qsum += __shfl_xor(qsum, 32);
+    }
 
-    const uint16_t *kbase = (const uint16_t *)pv.pages + tile_index(pv, layer, 0, 0, kvh) * (kBlock * kHeadDim);
-    const uint16_t *vbase = (const uint16_t *)pv.pages + tile_index(pv, layer, 1, 0, kvh) * (kBlock * kHeadDim);
-    const size_t page_elems = (size_t)pv.KVH * kBlock * kHeadDim;
+    constexpr int ES = I8 ? 1 : 2; // bytes per cached value
+    const char *kbase = (const char *)pv.pages + tile_index(pv, layer, 0, 0, kvh) * (kBlock * kHeadDim * ES);
+    const char *vbase = (const char *)pv.pages + tile_index(pv, layer, 1, 0, kvh) * (kBlock * kHeadDim * ES);
+    const size_t page_bytes = (size_t)pv.KVH * kBlock * kHeadDim * ES;
 
     float m = -1e30f, lsum = 0.f; // running max (scaled, log2 units) and this lane's share of the sum
     f32x4_t o[4];                 // O^T: dims 16 dg + 4 g + r, query head l16
@@ -714,25 +755,47 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
     // other half is read (33 -> 36.6 us at 1 kv head); K therefore goes through an LDS tile too.
     // Measured against plain loads in A layout: 1 kv head 33.4 -> 28.8 us, 2: 56.5 -> 50.5, 4:
     // 101.5 -> 89 us.
-    auto load = [&](uint4 (&kr)[2], uint4 (&vr)[2], int j) {
-        const size_t pe = (size_t)__builtin_amdgcn_readlane(my_page, j) * page_elems;
-        kr[0] = ld_stream(kbase + pe + 8 * lane);
-        kr[1] = ld_stream(kbase + pe + 512 + 8 * lane);
-        vr[0] = ld_stream(vbase + pe + 8 * lane);
-        vr[1] = ld_stream(vbase + pe + 512 + 8 * lane);
+    // int8: a tile is 1 KB, lane l's 16 bytes being key l / 4, dims 16 (l % 4) ..
+    auto load = [&](uint4 (&kr)[NL], uint4 (&vr)[NL], int j) {
+        const size_t pe = (size_t)__builtin_amdgcn_readlane(my_page, j) * page_bytes;
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            kr[i] = ld_stream(kbase + pe + 1024 * i + 16 * lane);
+            vr[i] = ld_stream(vbase + pe + 1024 * i + 16 * lane);
+        }
     };
-    auto process = [&](const uint4 (&kr)[2], const uint4 (&vr)[2], int j) {
+    auto process = [&](const uint4 (&kr)[NL], const uint4 (&vr)[NL], int j) {
         const uint32_t seen = __builtin_amdgcn_readlane(my_seen, j);
         f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
         // K through the wave's LDS tile into A layout (key l16, dims 32 kc + 8 g); a wave's LDS
         // accesses complete in order, so no barrier
-        *(uint4 *)&kt[w][lane >> 3][8 * (lane & 7)] = kr[0];
-        *(uint4 *)&kt[w][8 + (lane >> 3)][8 * (lane & 7)] = kr[1];
         bf16x8_t ka[2];
+        if constexpr (I8) {
+            const uint32_t *u = (const uint32_t *)&kr[0];
+            uint32_t hv[8];
 #pragma unroll
-        for (int kc = 0; kc < 2; ++kc) {
-            ka[kc] = as_bf16x8(*(const uint4 *)&kt[w][l16][32 * kc + 8 * g]);
-            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[kc], qb[kc], s, 0, 0, 0);
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t x = u[i] ^ 0x80808080u;
+                hv[2 * i] = __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u);     // dims 4i, 4i + 1
+                hv[2 * i + 1] = __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u); // dims 4i + 2, 4i + 3
+            }
+            *(uint4 *)&kt[w][lane >> 2][16 * (lane & 3)] = make_uint4(hv[0], hv[1], hv[2], hv[3]);
+            *(uint4 *)&kt[w][lane >> 2][16 * (lane & 3) + 8] = make_uint4(hv[4], hv[5], hv[6], hv[7]);
+#pragma unroll
+            for (int kc = 0; kc < 2; ++kc)
+                s = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    __builtin_bit_cast(f16x8_t, *(const uint4 *)&kt[w][l16][32 * kc + 8 * g]), qh[kc], s, 0, 0, 0);
+            const float sk = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(my_sk), j));
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s[r] = __builtin_fmaf(-1152.f, qsum, s[r]) * sk;
+        } else {
+            *(uint4 *)&kt[w][lane >> 3][8 * (lane & 7)] = kr[0];
+            *(uint4 *)&kt[w][8 + (lane >> 3)][8 * (lane & 7)] = kr[1];
+#pragma unroll
+            for (int kc = 0; kc < 2; ++kc) {
+                ka[kc] = as_bf16x8(*(const uint4 *)&kt[w][l16][32 * kc + 8 * g]);
+                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[kc], qb[kc], s, 0, 0, 0);
+            }
         }
         if constexpr (PREFIX) {
             // a page holding prefix rows (uniform): those rows take the scores of the queries at pos_pre
@@ -770,16 +833,33 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
             p[r] = fast_exp2(__builtin_fmaf(s[r], qmul, -m));
             lsum += p[r];
         }
-        const s16x4_t pt = __builtin_bit_cast(s16x4_t, make_uint2(pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3])));
-        // the page's V into this wave's LDS tile (rows lane / 8 and 8 + lane / 8, dims 8 (lane % 8) ..);
-        // an unseen row weighs 0 but its bytes may be anything, so it goes in as zeros (0 * NaN would
-        // be NaN)
-        const uint32_t keep0 = ((seen >> (lane >> 3)) & 1u) ? ~0u : 0u;
-        const uint32_t keep1 = ((seen >> (8 + (lane >> 3))) & 1u) ? ~0u : 0u;
-        *(uint4 *)&vt[w][lane >> 3][8 * (lane & 7)] =
-            make_uint4(vr[0].x & keep0, vr[0].y & keep0, vr[0].z & keep0, vr[0].w & keep0);
-        *(uint4 *)&vt[w][8 + (lane >> 3)][8 * (lane & 7)] =
-            make_uint4(vr[1].x & keep1, vr[1].y & keep1, vr[1].z & keep1, vr[1].w & keep1);
+        s16x4_t pt;
+        if constexpr (I8) {
+            // p sv in P^T; the V codes into this wave's LDS tile as bf16 (row lane / 4, dims
+            // 16 (lane % 4) ..).  int8 codes are finite, so unseen rows (p = 0) need no zeroing.
+            const float sv = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(my_sv), j));
+            pt = __builtin_bit_cast(s16x4_t, make_uint2(pack_bf16(p[0] * sv, p[1] * sv), pack_bf16(p[2] * sv, p[3] * sv)));
+            const uint32_t *u = (const uint32_t *)&vr[0];
+            uint32_t bw[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                bw[2 * i] = pack_bf16((float)(int8_t)(u[i] & 0xffu), (float)(int8_t)((u[i] >> 8) & 0xffu));
+                bw[2 * i + 1] = pack_bf16((float)(int8_t)((u[i] >> 16) & 0xffu), (float)(int8_t)(u[i] >> 24));
+            }
+            *(uint4 *)&vt[w][lane >> 2][16 * (lane & 3)] = make_uint4(bw[0], bw[1], bw[2], bw[3]);
+            *(uint4 *)&vt[w][lane >> 2][16 * (lane & 3) + 8] = make_uint4(bw[4], bw[5], bw[6], bw[7]);
+        } else {
+            pt = __builtin_bit_cast(s16x4_t, make_uint2(pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3])));
+            // the page's V into this wave's LDS tile (rows lane / 8 and 8 + lane / 8, dims 8 (lane % 8) ..);
+            // an unseen row weighs 0 but its bytes may be anything, so it goes in as zeros (0 * NaN would
+            // be NaN)
+            const uint32_t keep0 = ((seen >> (lane >> 3)) & 1u) ? ~0u : 0u;
+            const uint32_t keep1 = ((seen >> (8 + (lane >> 3))) & 1u) ? ~0u : 0u;
+            *(uint4 *)&vt[w][lane >> 3][8 * (lane & 7)] =
+                make_uint4(vr[0].x & keep0, vr[0].y & keep0, vr[0].z & keep0, vr[0].w & keep0);
+            *(uint4 *)&vt[w][8 + (lane >> 3)][8 * (lane & 7)] =
+                make_uint4(vr[1].x & keep1, vr[1].y & keep1, vr[1].z & keep1, vr[1].w & keep1);
+        }
 #pragma unroll
         for (int dg = 0; dg < 4; ++dg) {
             // V^T: lane gets dim 16 dg + l16 of keys 4 g .. 4 g + 3
@@ -788,7 +868,7 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
         }
     };
 
-    uint4 kb[DEPTH + 1][2], vb[DEPTH + 1][2];
+    uint4 kb[DEPTH + 1][NL], vb[DEPTH + 1][NL];
     // complete_kv: the wave that owns the write page appends the kv head's new row, as in attend_core
     // an invalid write page id appends nothing, as in attend_core
     const int wblk = R.write_slot >> 4, wj = wblk / SPLIT;
@@ -802,10 +882,16 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
         const int slot = R.write_slot;
         const size_t arow = (size_t)R.b * pv.KVH + kvh;
         const bool fresh = (R.flags & 1) ? (R.flags & 2) != 0 : ((slot & 15) == 0);
-        append_row_wave<DT_BF16, true>(pv, layer, __builtin_amdgcn_readlane(my_page, wj), slot & 15, kvh, R.key_pos,
-                                       (const char *)knew + arow * kHeadDim * 2, (const char *)vnew + arow * kHeadDim * 2,
-                                       fresh);
+        append_row_wave<CDT, true>(pv, layer, __builtin_amdgcn_readlane(my_page, wj), slot & 15, kvh, R.key_pos,
+                                   (const char *)knew + arow * kHeadDim * 2, (const char *)vnew + arow * kHeadDim * 2,
+                                   fresh);
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+        if constexpr (I8) {
+            if (lane == wj) { // an int8 append may have raised this page's scales (and rewritten its codes)
+                my_sk = pv.scales[tile_index(pv, layer, 0, my_page, kvh)];
+                my_sv = pv.scales[tile_index(pv, layer, 1, my_page, kvh)];
+            }
+        }
     }
     if (!early) {
 #pragma unroll
@@ -853,19 +939,23 @@ hipError_t launch_decode_gqa(const PoolView &pv, const BatchView &bv, int layer,
     const float qmul = scale * 1.4426950408889634f;
     const dim3 grid(bv.n * pv.KVH);
     const int f = fused ? 1 : 0;
-#define XNP_GQA(S, PFX) XNP_LAUNCH((k_decode_gqa<S, PFX>), grid, dim3(64 * S), stream, tm, pv, bv, layer, q, k, v, out, qmul, f)
-#define XNP_GQA_SPLIT(PFX)                                                                                          \
+    if (pv.act_dt != DT_BF16 || (pv.cache_dt != DT_BF16 && pv.cache_dt != DT_I8)) return hipErrorInvalidValue;
+    if (pv.cache_dt == DT_I8 && bv.prefix) return hipErrorInvalidValue; // int8 pages: no prefix
+#define XNP_GQA(S, PFX, C) XNP_LAUNCH((k_decode_gqa<S, PFX, C>), grid, dim3(64 * S), stream, tm, pv, bv, layer, q, k, v, out, qmul, f)
+#define XNP_GQA_SPLIT(PFX, C)                                                                                       \
     switch (bv.split) {                                                                                            \
-    case 1: XNP_GQA(1, PFX); break;                                                                                \
-    case 2: XNP_GQA(2, PFX); break;                                                                                \
-    case 4: XNP_GQA(4, PFX); break;                                                                                \
-    case 8: XNP_GQA(8, PFX); break;                                                                                \
+    case 1: XNP_GQA(1, PFX, C); break;                                                                             \
+    case 2: XNP_GQA(2, PFX, C); break;                                                                             \
+    case 4: XNP_GQA(4, PFX, C); break;                                                                             \
+    case 8: XNP_GQA(8, PFX, C); break;                                                                             \
     default: return hipErrorInvalidValue;                                                                          \
     }
-    if (bv.prefix) {
-        XNP_GQA_SPLIT(true);
+    if (pv.cache_dt == DT_I8) {
+        XNP_GQA_SPLIT(false, DT_I8);
+    } else if (bv.prefix) {
+        XNP_GQA_SPLIT(true, DT_BF16);
     } else {
-        XNP_GQA_SPLIT(false);
+        XNP_GQA_SPLIT(false, DT_BF16);
     }
 #undef XNP_GQA_SPLIT
 #undef XNP_GQA

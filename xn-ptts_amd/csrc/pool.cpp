@@ -1385,9 +1385,12 @@ extern "C" xnp_status xnp_attend(xnp_pool *pool, int32_t layer, const void *q, c
     if (pool->batch.n > 0 && (!q || !k || !v || !out)) return fail(XNP_E_INVALID, "null q, k, v or out");
     const LaunchTiming tm = pool->timing;
     pool->timing = LaunchTiming();
-    // grouped heads: every query head of a group would append its kv head's row; on an int8 pool,
-    // whose append rewrites the page, one kernel appends first and the decode only reads
-    const bool fuse = !(pool->d.cache_dtype == XNP_I8 && pool->d.num_kv_heads < pool->d.num_heads);
+    // grouped heads on the VALU decode: every query head's group would append its kv head's row; on
+    // an int8 pool, whose append rewrites the page, one kernel appends first and the decode only
+    // reads.  The MFMA decode takes a whole kv head per group, so it appends once itself.
+    const int G = pool->d.num_heads / pool->d.num_kv_heads;
+    const bool fuse = !(pool->d.cache_dtype == XNP_I8 && G > 1) ||
+                      decode_heads_per_group(pool->view(), pool->batch.bv.prefix != 0) == G;
     if (!fuse) HIP_TRY(launch_append(pool->view(), pool->batch.bv, layer, k, v, pool->batch.stream), "append");
     HIP_TRY(launch_decode(pool->view(), pool->batch.bv, layer, q, k, v, out, scale, fuse, pool->batch.stream, tm),
             "attend");
