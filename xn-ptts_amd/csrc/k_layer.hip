@@ -154,6 +154,9 @@ constexpr int kGmPD = 3;  // K chunks of loads in flight
 // a row, so that its accesses to the output (and to x, the gate, aux) are 16 bytes (32 for f32
 // rows) instead of 2, with its operands loaded before the K loop.  Measured in the layer step at
 // 2048 rows: the epilogue took 2.4-3.1 us of each projection with 2-byte stores.
+// NKC: K is exactly NKC x KS chunks (8 or 16 per half: the flow LM's 512-2048 wide projections),
+// so the rounds run unrolled whole and without the past-K clamps and masks; 0: any K, in a loop.
+// Tiles go to the XCDs in contiguous runs (xcd_tile), so each XCD's L2 holds about an eighth of A.
 constexpr int kGsLd = 72; // the staged epilogue's LDS row in bf16
 
 template <int EPI, bool AF32, int MI, int KS, bool STG, int NKC>
