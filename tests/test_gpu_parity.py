@@ -598,10 +598,13 @@ def test_ring_sessions_match_the_oracle(cache, act, mode, split):
                 p.assert_cache_equal(i)
 
 
-def test_int8_sliding_window_with_random_write_heads():
+@pytest.mark.parametrize("kvh", [8, 2, 1])
+def test_int8_sliding_window_with_random_write_heads(kvh):
     # A window of 64 rows on a ring of 80 slots (window + one page), write heads at random
-    # offsets, one eviction per step once the window is full.
-    p = Pair(cache="i8", act="bf16", streams=4, cap=80, seed=7, L=1)
+    # offsets, one eviction per step once the window is full.  8 kv heads: the VALU decode; 2 and
+    # 1 (4 and 8 query heads per kv head): the MFMA decode of whole kv heads, which appends once
+    # per kv head and requantizes the write page as its scales grow.
+    p = Pair(cache="i8", act="bf16", H=8, KVH=kvh, streams=4, cap=80, seed=7, L=1)
     heads = [0, 5, 33, 79]
     for i in range(4):
         p.pool.start_ring(p.ids[i], "absolute", prefix=0)
