@@ -514,7 +514,9 @@ def run_window(args, xnp, torch):
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic_of("window", wkey, bytes_per_launch),
-            "kernel": "k_decode<int8> (fused append + quantize + RoPE + dequant decode), one launch per layer",
+            "kernel": ("k_decode<int8> (fused append + quantize + RoPE + dequant decode)" if kvh == H else
+                       "k_decode_gqa<int8> (MFMA over whole kv heads, fused append + quantize + RoPE + dequant "
+                       "decode)") + ", one launch per layer",
             "avg_kernel_us": round(avg_ms * 1000.0, 2), "bytes_per_launch": int(bytes_per_launch)}
     return line("frames/sec, int8 KV sliding window (512) at 1024 streams; decode HBM GB/s % peak", fps,
                 "frames/s", args, ms, "int8", config, roof, cpu, extra={"audio_sec_per_sec": round(fps * 0.08, 1)},
