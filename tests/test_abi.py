@@ -429,3 +429,97 @@ def test_voice_files_are_read_and_checked_as_the_reference_checks_them(tmp_path)
     bad(names[0], np.zeros((2, 1, 5, 8, 64), np.float32), "8 heads of 64, the pool holds 4")
     bad(names[1], np.zeros((2, 1, 6, 4, 64), np.float32), "6 frames, layer 0 holds 5")
     bad(names[0], np.zeros((2, 5, 4, 64), np.float32), "expected 5 dims")
+
+
+def test_random_stream_lifecycles_keep_the_page_accounting():
+    # Seeded random sequences of open, advance, batched appends (ended or aborted), forks
+    # (with_seq_budget: full pages shared, the partial one copied) and closes on a small pool, so
+    # that refusals (no free page, no free stream, capacity) are frequent.  After every call: the
+    # free pages are the pool's pages minus the distinct pages the streams hold; a stream holds
+    # exactly ceil(end / 16) pages, in [0, NB); a page held twice is a full page of both holders; a
+    # refused call changes neither ends nor the free count.
+    NB, S, MB = 24, 6, 6
+    rng = np.random.default_rng(20261202)
+    p = pool(num_blocks=NB, max_streams=S, max_blocks_per_stream=MB)
+    model = {}  # sid -> [end, capacity]
+
+    def pages_needed(end, t):
+        return (end + t + 15) // 16 - (end + 15) // 16
+
+    def check():
+        held = {}
+        for sid, (end, cap) in model.items():
+            assert p.current_end(sid) == end
+            blk = p.blocks(sid)
+            live = [(b, pg) for b, pg in enumerate(blk) if pg >= 0]
+            assert len(live) == (end + 15) // 16 and [b for b, _ in live] == list(range(len(live))), (sid, blk, end)
+            for b, pg in live:
+                assert 0 <= pg < NB
+                held.setdefault(pg, []).append((sid, b, end))
+        for pg, owners in held.items():
+            if len(owners) > 1:  # shared by a fork: a full page for every holder
+                assert all((b + 1) * 16 <= end for _, b, end in owners), (pg, owners)
+        assert p.stats()["free_blocks"] == NB - len(held)
+        assert p.stats()["open_streams"] == len(model)
+
+    def refused(call):
+        before = ({s: p.current_end(s) for s in model}, p.stats()["free_blocks"])
+        with pytest.raises(xnp.XnpError):
+            call()
+        assert before == ({s: p.current_end(s) for s in model}, p.stats()["free_blocks"])
+
+    for _ in range(3000):
+        op = rng.integers(0, 6)
+        free = p.stats()["free_blocks"]
+        sids = list(model)
+        if op == 0 or not sids:  # open
+            cap = int(rng.integers(1, MB * 16 + 1))
+            if len(model) < S:
+                model[p.init_state(cap)] = [0, cap]
+            else:
+                refused(lambda: p.init_state(cap))
+        elif op == 1:  # advance
+            sid = sids[rng.integers(len(sids))]
+            end, cap = model[sid]
+            n = int(rng.integers(0, cap - end + 1))
+            if pages_needed(end, n) <= free:
+                p.advance(sid, n)
+                model[sid][0] += n
+            else:
+                refused(lambda: p.advance(sid, n))
+        elif op == 2:  # a batch of t rows on some streams, ended or aborted
+            pick = [s for s in sids if rng.random() < 0.5] or sids[:1]
+            t = int(rng.integers(1, 40))
+            need = sum(pages_needed(model[s][0], t) for s in pick)
+            if any(model[s][0] + t > model[s][1] for s in pick) or need > free:
+                refused(lambda: p.begin(pick, t=t))
+            else:
+                p.begin(pick, t=t)
+                assert p.stats()["free_blocks"] == free - need
+                if rng.random() < 0.3:
+                    p.abort()
+                else:
+                    p.end()
+                    for s in pick:
+                        model[s][0] += t
+        elif op == 3:  # fork
+            sid = sids[rng.integers(len(sids))]
+            end = model[sid][0]
+            budget = int(rng.integers(end, MB * 16 + 1)) if end <= MB * 16 else end
+            tail = end % 16 != 0
+            if len(model) < S and (not tail or free > 0):
+                model[p.with_seq_budget(sid, budget)] = [end, budget]
+            else:
+                refused(lambda: p.with_seq_budget(sid, budget))
+        elif op == 4:  # a budget below the filled rows is refused
+            sid = sids[rng.integers(len(sids))]
+            if model[sid][0] > 0:
+                refused(lambda: p.with_seq_budget(sid, model[sid][0] - 1))
+        else:  # close
+            sid = sids[rng.integers(len(sids))]
+            p.close(sid)
+            del model[sid]
+        check()
+    for sid in list(model):
+        p.close(sid)
+    assert p.stats()["free_blocks"] == NB
