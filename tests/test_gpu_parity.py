@@ -66,14 +66,15 @@ class Pair:
         self.pool.end()
         self.orc[i].commit(n)
 
-    def prefill(self, t, which=None):
-        """A prompt step: t rows on every stream in `which`, through xnp_attend (append + causal)."""
+    def prefill(self, t, which=None, qscale=1.0):
+        """A prompt step: t rows on every stream in `which`, through xnp_attend (append + causal);
+        qscale (a power of two) scales the queries."""
         which = list(range(len(self.ids))) if which is None else which
         n = len(which)
         self.pool.begin([self.ids[i] for i in which], t=t)
         worst = 0.0
         for layer in range(self.L):
-            q, k, v = self.x(n, t, self.H, 64), self.x(n, t, self.KVH, 64), self.x(n, t, self.KVH, 64)
+            q, k, v = self.x(n, t, self.H, 64) * qscale, self.x(n, t, self.KVH, 64), self.x(n, t, self.KVH, 64)
             out = torch.empty((n, t, self.H, 64), dtype=TORCH_DT[self.act], device=DEV)
             self.pool.attend(layer, dev(q, self.act), dev(k, self.act), dev(v, self.act), out, 0.125)
             torch.cuda.synchronize()
@@ -111,13 +112,13 @@ class Pair:
             self.orc[i].commit(t)
         return worst
 
-    def step(self, which=None, fused=True, check=True):
+    def step(self, which=None, fused=True, check=True, qscale=1.0):
         which = list(range(len(self.ids))) if which is None else which
         n = len(which)
         self.pool.begin([self.ids[i] for i in which])
         errs = []
         for layer in range(self.L):
-            q, k, v = self.x(n, self.H, 64), self.x(n, self.KVH, 64), self.x(n, self.KVH, 64)
+            q, k, v = self.x(n, self.H, 64) * qscale, self.x(n, self.KVH, 64), self.x(n, self.KVH, 64)
             out = torch.empty((n, self.H, 64), dtype=TORCH_DT[self.act], device=DEV)
             if fused:
                 self.pool.attend(layer, dev(q, self.act), dev(k, self.act), dev(v, self.act), out, 0.125)
@@ -596,6 +597,23 @@ def test_ring_sessions_match_the_oracle(cache, act, mode, split):
         if steps % 23 == 0 or steps == 69:
             for i in range(3):
                 p.assert_cache_equal(i)
+
+
+@pytest.mark.parametrize("kvh", [8, 2])
+@pytest.mark.parametrize("qscale", [2.0 ** 17, 2.0 ** -20])
+def test_int8_pools_take_queries_beyond_the_f16_range(kvh, qscale):
+    # int8 pages with bf16 activations take the query as f16, scaled by a power of two that fits
+    # it: queries of N(0, 1) x 2^17 (components past f16's 65504) and x 2^-20 (below its normal
+    # range) on the VALU decode (8 kv heads) and the MFMA one (2 kv heads, 4 query heads each),
+    # after a 9-row prompt through the prompt-row kernel: outputs to the oracle, caches bit-exact
+    p = Pair(cache="i8", act="bf16", H=8, KVH=kvh, streams=3, cap=96, seed=50)
+    for i, n in enumerate([0, 20, 47]):
+        p.fill(i, n)
+    p.prefill(9, qscale=qscale)
+    for _ in range(3):
+        p.step(qscale=qscale)
+    for i in range(3):
+        p.assert_cache_equal(i)
 
 
 @pytest.mark.parametrize("kvh", [8, 2, 1])

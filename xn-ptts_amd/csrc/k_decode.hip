@@ -75,6 +75,7 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
     // int8: unpack hands out q + 128, so a dot product is sum(qw (q + 128)) - 128 sum(qw) and a
     // value accumulator carries -128 sum(e sv) on every dim (vbias, taken out after the loop)
     float qwsum[GQ], qpsum[GQ], vbias[GQ];
+    float qpow[GQ], ppow[GQ]; // H16: the power of two each query was scaled down by (f16_fit_exponent)
 #pragma unroll
     for (int e = 0; e < GQ; ++e) {
         const char *qrow = (const char *)q + ((size_t)R.b * pv.H + h + e) * kHeadDim * AE;
@@ -87,7 +88,18 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
                 ph[e][i] = (__float_as_uint(qp[e][2 * i]) >> 16) | (__float_as_uint(qp[e][2 * i + 1]) & 0xffff0000u);
             }
         }
+        qpow[e] = ppow[e] = 1.f;
         if constexpr (H16) {
+            const int xq = f16_fit_exponent<DPL, 1, 2>(qw[e]); // the row's 4 lanes: c = lane % 4
+            const int xp = two_q ? f16_fit_exponent<DPL, 1, 2>(qp[e]) : 0;
+            qpow[e] = pow2i(xq);
+            ppow[e] = pow2i(xp);
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) qw[e][i] *= pow2i(-xq);
+            if (two_q) {
+#pragma unroll
+                for (int i = 0; i < DPL; ++i) qp[e][i] *= pow2i(-xp);
+            }
 #pragma unroll
             for (int i = 0; i < DPL / 2; ++i) {
                 qh[e][i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(qw[e][2 * i], qw[e][2 * i + 1]));
@@ -186,6 +198,7 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
 #pragma unroll
                 for (int o = 1; o < LPR; o <<= 1) dw[e] += __shfl_xor(dw[e], o);
                 if constexpr (CDT == DT_I8) dw[e] *= sk;
+                if constexpr (H16) dw[e] *= pre ? ppow[e] : qpow[e];
                 if constexpr (DOT2 || H16) dw[e] *= qmul;
                 s[e][p] = ((seen >> r) & 1u) ? dw[e] : -INFINITY;
             }

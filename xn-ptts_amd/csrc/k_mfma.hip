@@ -716,19 +716,31 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
     };
     rotated(R.pos, qb);
     if constexpr (PREFIX) rotated(R.prefix > 0 ? R.pos_pre : R.pos, qpre);
-    // int8: the same queries as f16 (exact) and their sum over the 64 dims of the lane's column
+    // int8: the same queries as f16, scaled by a power of two that fits the column into f16
+    // (f16_fit_exponent: exact), and their sum over the 64 dims of the lane's column
     f16x8_t qh[2];
-    float qsum = 0.f;
+    float qsum = 0.f, qpow = 1.f;
     if constexpr (I8) {
+        float xv[16];
 #pragma unroll
         for (int kc = 0; kc < 2; ++kc) {
             uint4 u;
             __builtin_memcpy(&u, &qb[kc], 16);
             const uint32_t *w4 = (const uint32_t *)&u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                xv[8 * kc + 2 * i] = bf16_value(w4[i] & 0xffffu);
+                xv[8 * kc + 2 * i + 1] = bf16_value(w4[i] >> 16);
+            }
+        }
+        const int xq = f16_fit_exponent<16, 16, 2>(xv); // the column's 4 lanes: g = lane / 16
+        qpow = pow2i(xq);
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) {
             uint32_t h4[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float x0 = bf16_value(w4[i] & 0xffffu), x1 = bf16_value(w4[i] >> 16);
+                const float x0 = xv[8 * kc + 2 * i] * pow2i(-xq), x1 = xv[8 * kc + 2 * i + 1] * pow2i(-xq);
                 h4[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x0, x1));
                 qsum += x0;
                 qsum += x1;
@@ -787,7 +799,7 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
                     __builtin_bit_cast(f16x8_t, *(const uint4 *)&kt[w][l16][32 * kc + 8 * g]), qh[kc], s, 0, 0, 0);
             const float sk = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(my_sk), j));
 #pragma unroll
-            for (int r = 0; r < 4; ++r) s[r] = __builtin_fmaf(-1152.f, qsum, s[r]) * sk;
+            for (int r = 0; r < 4; ++r) s[r] = __builtin_fmaf(-1152.f, qsum, s[r]) * sk * qpow;
         } else {
             *(uint4 *)&kt[w][lane >> 3][8 * (lane & 7)] = kr[0];
             *(uint4 *)&kt[w][8 + (lane >> 3)][8 * (lane & 7)] = kr[1];

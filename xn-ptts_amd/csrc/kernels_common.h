@@ -246,6 +246,26 @@ __device__ __forceinline__ void rotated_q(const PoolView &pv, const void *qrow, 
     }
 }
 
+// A query taken as f16 (int8 pages with bf16 activations) is first scaled by a power of two 2^-x
+// that puts the row's largest |value| into [2^14, 2^15): every bf16 value then fits f16 (whose
+// largest is 65504, while bf16 reaches 3.4e38) with the largest at full precision.  Scaling by a
+// power of two is exact, the products of f16 values are exact in f32, and f32 sums round alike at
+// any power-of-two scale, so scores taken with the scaled query and multiplied by 2^x are those of
+// the unscaled query wherever that one fits f16.  The row's DPL values of this lane are reduced
+// over the N lanes XOR-distant by O0, 2 O0, ..; returns x.
+template <int DPL, int O0, int N>
+__device__ __forceinline__ int f16_fit_exponent(const float (&x)[DPL]) {
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) m = fmaxf(m, fabsf(x[i]));
+#pragma unroll
+    for (int k = 0, o = O0; k < N; ++k, o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+    const int ex = (int)((__float_as_uint(m) >> 23) & 0xffu) - 127; // floor(log2 m) for a normal m
+    return m > 0.f ? min(max(ex - 14, -100), 100) : 0;
+}
+// 2^x for |x| <= 126
+__device__ __forceinline__ float pow2i(int x) { return __uint_as_float((uint32_t)(127 + x) << 23); }
+
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 
