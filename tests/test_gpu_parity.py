@@ -1046,6 +1046,36 @@ def test_long_prompts_take_several_rounds():
     p.step()
 
 
+# The longest stream a pool takes: 480 pages of 16 rows (60 page ids per wave's lanes, 8 waves per
+# (stream, head)).  Streams one row short of full and one page short of full decode their last row
+# into the last slot and into a fresh last page; a short stream rides along in the same batch.
+# The grouped-head rows take the MFMA decode.
+@pytest.mark.parametrize("cache,act,kvh", [("bf16", "bf16", 8), ("i8", "bf16", 8), ("f32", "f32", 8),
+                                           ("bf16", "bf16", 1), ("i8", "bf16", 2)])
+def test_streams_at_the_longest_a_pool_takes(cache, act, kvh):
+    cap = 480 * 16
+    p = Pair(cache=cache, act=act, KVH=kvh, streams=3, cap=cap, seed=31, L=1, page_seed=12)
+    for i, n in enumerate([cap - 1, cap - 16, 3]):
+        p.fill(i, n)
+    assert p.step() <= TOL[cache]
+    for i in range(3):
+        p.assert_cache_equal(i)
+    assert p.orc[0].current_end == cap
+
+
+@pytest.mark.parametrize("cache,act", [("bf16", "bf16"), ("i8", "bf16"), ("f32", "f32")])
+def test_a_prompt_that_fills_the_longest_stream(cache, act):
+    # 7580 rows (ending mid-page), then a 100-row prompt ending on the last slot of page 480: the
+    # prompt reads every page id of the stream (the MFMA prefill keeps them in LDS; int8 and f32
+    # take the row-by-row prompt kernel after the append)
+    cap = 480 * 16
+    p = Pair(cache=cache, act=act, streams=1, cap=cap, seed=32, L=1, page_seed=13)
+    p.fill(0, cap - 100)
+    assert p.prefill(100) <= TOL[cache]
+    p.assert_cache_equal(0)
+    assert p.orc[0].current_end == cap
+
+
 @pytest.mark.parametrize("cache,act", [("bf16", "bf16"), ("f32", "f32")])
 def test_unwritten_rows_holding_nan_bytes_do_not_reach_the_output(cache, act):
     # A page's rows past current_end are never attended, but the kernels read whole tiles: rows
