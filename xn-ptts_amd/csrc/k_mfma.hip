@@ -2,6 +2,8 @@
 // windowed attention of a Mimi chunk (k_prefill_window) and the grouped-head decode (k_decode_gqa).
 #include "kernels_common.h"
 
+#include <type_traits>
+
 namespace xnp {
 
 // ---------------------------------------------------------------------------------------------
@@ -28,6 +30,20 @@ namespace xnp {
 // contraction is right whatever order the instruction walks k in.
 
 
+// Rotate 8 bf16 values (4 pairs) with 4 packed bf16 (cos, sin) pairs, rounded to bf16 (rope.rs:74-95).
+__device__ __forceinline__ uint4 rotate8(const uint4 &x, const uint4 &cs) {
+    const uint32_t *u = (const uint32_t *)&x, *r = (const uint32_t *)&cs;
+    uint32_t o4[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float x0 = bf16_value(u[e] & 0xffffu), x1 = bf16_value(u[e] >> 16);
+        const float c = bf16_value(r[e] & 0xffffu), s = bf16_value(r[e] >> 16);
+        const float a = x0 * c, bb = x1 * s, ee = x0 * s, f = x1 * c;
+        o4[e] = pack_bf16(a - bb, ee + f);
+    }
+    return make_uint4(o4[0], o4[1], o4[2], o4[3]);
+}
+
 constexpr int kPfKeys = 64;      // keys per chunk (four pages)
 constexpr int kPfLd = 72;        // LDS row length in bf16: 64 + 8 of padding, rows 16-byte aligned
 constexpr int kPfWaves = 8;      // waves per work group
@@ -43,6 +59,8 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
     __shared__ __attribute__((aligned(16))) uint16_t vs[2 * kPfKeys][kPfLd]; // V of two chunks, [key][dim]
     __shared__ int32_t spages[kPfMaxPages];
     const int t = bv.t;
+    // plan b is the batch's row b (its out_row): the inputs' and the output's rows are b's, so their
+    // addresses do not wait for the plan
     const int h = blockIdx.x % pv.H, b = blockIdx.x / pv.H;
     const StreamPlan P = bv.plans[b];
     const int32_t *tab = pv.tables + (size_t)P.sid * pv.mbps;
@@ -52,8 +70,12 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
     const size_t page_elems = (size_t)pv.KVH * kBlock * kHeadDim;
     uint16_t *kpages = (uint16_t *)pv.pages + tile_index(pv, layer, 0, 0, kvh) * (kBlock * kHeadDim);
     uint16_t *vpages = (uint16_t *)pv.pages + tile_index(pv, layer, 1, 0, kvh) * (kBlock * kHeadDim);
-    // the stream's page ids for every key any round sees, read once
-    for (int i = tid; i < min((c0 + t + kBlock - 1) / kBlock, kPfMaxPages); i += 64 * kPfWaves) spages[i] = tab[i];
+    // the stream's page ids for every key any round sees, at most one per thread: loaded here and
+    // put into LDS only once the first round's queries and first chunk are on their way, so that
+    // those loads go out together instead of each waiting for the one before
+    const int npg = min((c0 + t + kBlock - 1) / kBlock, kPfMaxPages);
+    static_assert(kPfMaxPages <= 64 * kPfWaves, "one page id per thread");
+    const int my_pg = tab[min(tid, npg - 1)];
     // this thread's share of a chunk: 16 bytes (8 dims) of one key's K and V
     const int skey = tid >> 3, spart = tid & 7;
 
@@ -72,27 +94,67 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
         const int kend = c0 + min(t, 16 * (tq0 + nq)); // the round's rows see keys [0, kend)
         const int nch = (kend + kPfKeys - 1) / kPfKeys;
 
+        // Loads run one chunk ahead: chunk c's registers are consumed (rotated, stored to LDS
+        // buffer c & 1) at step c, which then issues chunk c + 1's loads into them.
+        struct Stage {
+            uint4 k, v, rope; // the key's K and V pieces, 4 (cos, sin) pairs as packed bf16
+            int info;         // bit 0: a prompt key, bit 1: write it to its page
+        };
+        // LDS: the page ids are in LDS (all but the first round's first chunk, which reads the
+        // table itself); a compile-time choice, so that no pointer is selected between the two
+        auto issue = [&](int c, Stage &st, auto LDS) {
+            const int slot = c * kPfKeys + skey;
+            const bool in = c < nch && slot < kend;
+            const bool fresh = fused && slot >= c0; // a prompt key: from the inputs, rotated here
+            const int i = fresh ? min(slot - c0, t - 1) : 0;
+            const size_t arow = (((size_t)b * t + i) * pv.KVH + kvh) * kHeadDim + 8 * spart;
+            st.k = st.v = make_uint4(0, 0, 0, 0);
+            if (in && fresh) {
+                st.k = ld_stream((const uint16_t *)knew + arow);
+                st.v = ld_stream((const uint16_t *)vnew + arow);
+            } else if (in) {
+                const int blk = min(slot >> 4, kPfMaxPages - 1);
+                int page;
+                if constexpr (decltype(LDS)::value)
+                    page = spages[blk];
+                else
+                    page = tab[blk];
+                if (page >= 0 && page < pv.NB) {
+                    const size_t poff = (size_t)page * page_elems + (slot & 15) * kHeadDim + 8 * spart;
+                    st.k = ld_stream(kpages + poff);
+                    st.v = ld_stream(vpages + poff);
+                }
+            }
+            st.rope = *(const uint4 *)(pv.rope16 + (size_t)(P.key_pos + i) * (kHeadDim / 2) + 4 * spart);
+            st.info = (in && fresh ? 1 : 0) | (in && fresh && last ? 2 : 0);
+        };
+
         // B operands of S^T: query row 16 tile + l16, dims 32 kc + 8 g .. +7, rotated at its
-        // position and rounded to bf16 as the reference's bf16 q is.  Every load is issued
-        // before any is used (rows past the prompt read row t - 1 and are zeroed after).
+        // position and rounded to bf16 as the reference's bf16 q is.  The queries' loads and the
+        // first chunk's go out before any is used (rows past the prompt read row t - 1 and are
+        // zeroed after).
         bf16x8_t qb[2][2];
         float m[2], lsum[2]; // running max (scaled, log2 units) and this lane's share of the sum
         f32x4_t o[2][4];
+        Stage st;
         {
-            uint4 qraw[2][2];
-            float4 qcs[2][2][2];
+            uint4 qraw[2][2], qcs[2][2]; // q pieces; their 4 (cos, sin) pairs as packed bf16
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const int qr = min(16 * max(tile[j], 0) + l16, t - 1);
-                const uint16_t *qp = (const uint16_t *)q + (((size_t)P.out_row * t + qr) * pv.H + h) * kHeadDim;
-                const float4 *cs = (const float4 *)(pv.rope + (size_t)(P.pos + qr) * (kHeadDim / 2));
+                const uint16_t *qp = (const uint16_t *)q + (((size_t)b * t + qr) * pv.H + h) * kHeadDim;
+                const uint32_t *cs = pv.rope16 + (size_t)(P.pos + qr) * (kHeadDim / 2);
 #pragma unroll
                 for (int kc = 0; kc < 2; ++kc) {
                     qraw[j][kc] = *(const uint4 *)(qp + 32 * kc + 8 * g);
-                    qcs[j][kc][0] = cs[(32 * kc + 8 * g) / 4];
-                    qcs[j][kc][1] = cs[(32 * kc + 8 * g) / 4 + 1];
+                    qcs[j][kc] = *(const uint4 *)(cs + 16 * kc + 4 * g);
                 }
             }
+            if (tq0 > 0)
+                issue(0, st, std::true_type{});
+            else
+                issue(0, st, std::false_type{});
+            if (tq0 == 0 && tid < npg) spages[tid] = my_pg;
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 m[j] = -1e30f;
@@ -102,76 +164,31 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
                 const bool live = tile[j] >= 0 && 16 * tile[j] + l16 < t;
 #pragma unroll
                 for (int kc = 0; kc < 2; ++kc) {
-                    const uint32_t *u = (const uint32_t *)&qraw[j][kc];
-                    const float4 ca = qcs[j][kc][0], cb = qcs[j][kc][1];
-                    const float cf[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w}; // cos, sin of 4 pairs
-                    uint32_t o4[4];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float x0 = bf16_value(u[i] & 0xffffu), x1 = bf16_value(u[i] >> 16);
-                        const float c = cf[2 * i], s = cf[2 * i + 1];
-                        const float a = x0 * c, bb = x1 * s, e = x0 * s, f = x1 * c;
-                        o4[i] = live ? pack_bf16(a - bb, e + f) : 0u;
-                    }
-                    qb[j][kc] = as_bf16x8(make_uint4(o4[0], o4[1], o4[2], o4[3]));
+                    const uint4 r = rotate8(qraw[j][kc], qcs[j][kc]);
+                    qb[j][kc] = as_bf16x8(live ? r : make_uint4(0, 0, 0, 0));
                 }
             }
         }
         __syncthreads(); // spages written
 
-        // Loads run one chunk ahead: chunk c's registers are consumed (rotated, stored to LDS
-        // buffer c & 1) at step c, which then issues chunk c + 1's loads into them.
-        struct Stage {
-            uint4 k, v, rope; // the key's K and V pieces, 4 (cos, sin) pairs as packed bf16
-            int info;         // bit 0: a prompt key, bit 1: write it to its page; page id above
-        };
-        auto issue = [&](int c, Stage &st) {
-            const int slot = c * kPfKeys + skey;
-            const bool in = c < nch && slot < kend;
-            const bool fresh = fused && slot >= c0; // a prompt key: from the inputs, rotated here
-            const int page = in ? spages[min(slot >> 4, kPfMaxPages - 1)] : -1;
-            const bool ok = page >= 0 && page < pv.NB;
-            const size_t poff = (size_t)(ok ? page : 0) * page_elems + (slot & 15) * kHeadDim + 8 * spart;
-            const int i = fresh ? min(slot - c0, t - 1) : 0;
-            const size_t arow = (((size_t)P.out_row * t + i) * pv.KVH + kvh) * kHeadDim + 8 * spart;
-            st.k = st.v = make_uint4(0, 0, 0, 0);
-            if (in && fresh) {
-                st.k = ld_stream((const uint16_t *)knew + arow);
-                st.v = ld_stream((const uint16_t *)vnew + arow);
-            } else if (in && ok) {
-                st.k = ld_stream(kpages + poff);
-                st.v = ld_stream(vpages + poff);
-            }
-            st.rope = *(const uint4 *)(pv.rope16 + (size_t)(P.key_pos + i) * (kHeadDim / 2) + 4 * spart);
-            st.info = (in && fresh ? 1 : 0) | (in && fresh && ok && last ? 2 : 0) | ((ok ? page : 0) << 2);
-        };
         auto step = [&](int c, Stage &st) {
             const int buf = c & 1, kbase = c * kPfKeys, lb = buf * kPfKeys;
             // rotate a prompt key at its position; store this thread's piece of the chunk
             {
-                uint4 kk = st.k;
-                if (st.info & 1) {
-                    const uint32_t *r = (const uint32_t *)&st.rope;
-                    const uint32_t *u = (const uint32_t *)&st.k;
-                    uint32_t o4[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float x0 = bf16_value(u[e] & 0xffffu), x1 = bf16_value(u[e] >> 16);
-                        const float cc = bf16_value(r[e] & 0xffffu), sn = bf16_value(r[e] >> 16);
-                        const float a = x0 * cc, bb = x1 * sn, ee = x0 * sn, f = x1 * cc;
-                        o4[e] = pack_bf16(a - bb, ee + f);
-                    }
-                    kk = make_uint4(o4[0], o4[1], o4[2], o4[3]);
-                }
+                const uint4 kk = st.info & 1 ? rotate8(st.k, st.rope) : st.k;
                 if (st.info & 2) { // complete_kv: the prompt's rows go into their pages once
-                    const size_t poff = (size_t)(st.info >> 2) * page_elems + ((kbase + skey) & 15) * kHeadDim + 8 * spart;
-                    *(uint4 *)(kpages + poff) = kk;
-                    *(uint4 *)(vpages + poff) = st.v;
+                    const int slot = kbase + skey;
+                    const int page = spages[min(slot >> 4, kPfMaxPages - 1)];
+                    if (page >= 0 && page < pv.NB) {
+                        const size_t poff = (size_t)page * page_elems + (slot & 15) * kHeadDim + 8 * spart;
+                        *(uint4 *)(kpages + poff) = kk;
+                        *(uint4 *)(vpages + poff) = st.v;
+                    }
                 }
                 *(uint4 *)&ks[lb + skey][8 * spart] = kk;
                 *(uint4 *)&vs[lb + skey][8 * spart] = st.v;
             }
-            issue(c + 1, st);
+            issue(c + 1, st, std::true_type{});
             __syncthreads(); // chunk c is in LDS; every reader of chunk c - 2 (same buffer) is done
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
@@ -247,8 +264,6 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
                 }
             }
         };
-        Stage st;
-        issue(0, st);
         for (int c = 0; c < nch; ++c) step(c, st);
         __syncthreads(); // the next round's staging overwrites both buffers
 
@@ -261,7 +276,7 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
             const int qrow = 16 * tile[j] + l16;
             if (tile[j] < 0 || qrow >= t) continue;
             const float inv = 1.0f / l;
-            uint16_t *orow = (uint16_t *)out + (((size_t)P.out_row * t + qrow) * pv.H + h) * kHeadDim;
+            uint16_t *orow = (uint16_t *)out + (((size_t)b * t + qrow) * pv.H + h) * kHeadDim;
 #pragma unroll
             for (int dg = 0; dg < 4; ++dg)
                 *(uint2 *)(orow + 16 * dg + 4 * g) = make_uint2(pack_bf16(o[j][dg][0] * inv, o[j][dg][1] * inv),
@@ -330,20 +345,6 @@ __device__ __forceinline__ float pair_max(float x) {
 __device__ __forceinline__ float pair_sum(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-// Rotate 8 bf16 values (4 pairs) with 4 packed bf16 (cos, sin) pairs, rounded to bf16 (rope.rs:74-95).
-__device__ __forceinline__ uint4 rotate8(const uint4 &x, const uint4 &cs) {
-    const uint32_t *u = (const uint32_t *)&x, *r = (const uint32_t *)&cs;
-    uint32_t o4[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const float x0 = bf16_value(u[e] & 0xffffu), x1 = bf16_value(u[e] >> 16);
-        const float c = bf16_value(r[e] & 0xffffu), s = bf16_value(r[e] >> 16);
-        const float a = x0 * c, bb = x1 * s, ee = x0 * s, f = x1 * c;
-        o4[e] = pack_bf16(a - bb, ee + f);
-    }
-    return make_uint4(o4[0], o4[1], o4[2], o4[3]);
 }
 
 // Vector-memory loads of a wave complete in the order issued (one counter, vmcnt), so a wave waits
