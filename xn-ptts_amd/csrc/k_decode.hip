@@ -54,7 +54,42 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
         my_page = ok ? pg : 0;
         my_ok = ok ? 1 : 0;
         my_seen = seen;
-        if constexpr (CDT == DT_I8) {
+    }
+
+    const uint4 *kbase = (const uint4 *)((const char *)pv.pages + tile_index(pv, layer, 0, 0, kvh) * (kBlock * kHeadDim * esize<CDT>()));
+    const uint4 *vbase = (const uint4 *)((const char *)pv.pages + tile_index(pv, layer, 1, 0, kvh) * (kBlock * kHeadDim * esize<CDT>()));
+    const size_t page_u4 = (size_t)pv.KVH * (kBlock * kHeadDim * esize<CDT>() / 16);
+    auto load = [&](uint4 (&kr)[NP], uint4 (&vr)[NP], int j) {
+        const int pg = __builtin_amdgcn_readlane(my_page, j);
+        const size_t off = (size_t)pg * page_u4 + lane;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            kr[p] = ld_stream(kbase + off + 64 * p);
+            vr[p] = ld_stream(vbase + off + 64 * p);
+        }
+    };
+
+    // DEPTH pages in flight ahead of the one being reduced.  The loop body has no branch: past
+    // the wave's last page the lanes' page is page 0, a tile every wave shares (so mostly a cache
+    // hit), and its rows are unseen, so reducing it changes nothing.  Each wait then only covers
+    // the oldest page's loads.
+    uint4 kb[DEPTH + 1][NP], vb[DEPTH + 1][NP];
+
+    // The first DEPTH pages' loads go out before the queries are rotated, so that a group's first
+    // K/V bytes are one round trip behind its page ids, not two (the rotation waits for the query
+    // and RoPE rows).  The wave that owns the write page loads them after its append instead when
+    // the write page is among them; otherwise before it, so the append's round trips overlap them.
+    const int wblk = R.write_slot >> 4, wj = wblk / SPLIT;
+    const bool owner = fused && w == wblk % SPLIT && __builtin_amdgcn_readlane(my_ok, wj) != 0;
+    const bool early = !owner || wj >= DEPTH;
+    if (early) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) load(kb[d], vb[d], d);
+    }
+    // int8: the pages' scales, after the first pages' loads (a wait for the page ids before those
+    // would otherwise wait for these too)
+    if constexpr (CDT == DT_I8) {
+        if (lane < nb) {
             my_sk = pv.scales[tile_index(pv, layer, 0, my_page, kvh)];
             my_sv = pv.scales[tile_index(pv, layer, 1, my_page, kvh)];
         }
@@ -117,9 +152,6 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
         }
     }
 
-    const uint4 *kbase = (const uint4 *)((const char *)pv.pages + tile_index(pv, layer, 0, 0, kvh) * (kBlock * kHeadDim * esize<CDT>()));
-    const uint4 *vbase = (const uint4 *)((const char *)pv.pages + tile_index(pv, layer, 1, 0, kvh) * (kBlock * kHeadDim * esize<CDT>()));
-    const size_t page_u4 = (size_t)pv.KVH * (kBlock * kHeadDim * esize<CDT>() / 16);
 
     float m[GQ], l[GQ], acc[GQ][DPL];
 #pragma unroll
@@ -249,36 +281,13 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
             }
         }
     };
-    auto load = [&](uint4 (&kr)[NP], uint4 (&vr)[NP], int j) {
-        const int pg = __builtin_amdgcn_readlane(my_page, j);
-        const size_t off = (size_t)pg * page_u4 + lane;
-#pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            kr[p] = ld_stream(kbase + off + 64 * p);
-            vr[p] = ld_stream(vbase + off + 64 * p);
-        }
-    };
 
-    // DEPTH pages in flight ahead of the one being reduced.  The loop body has no branch: past
-    // the wave's last page the lanes' page is page 0, a tile every wave shares (so mostly a cache
-    // hit), and its rows are unseen, so reducing it changes nothing.  Each wait then only covers
-    // the oldest page's loads.
-    uint4 kb[DEPTH + 1][NP], vb[DEPTH + 1][NP];
-
-    // complete_kv: the wave that owns the write page appends this head's new row, then reads it
-    // back with the rest of its pages (its own lanes' stores; no other wave touches the page).
-    // A workgroup-scope fence orders the stores before the later loads on the same CU; nothing
-    // waits for the stores to reach memory.  When the write page is not among the wave's first
-    // DEPTH pages, those are loaded before the append, so the append's round trips overlap them.
-    // An invalid write page id (never handed out by the host, which checks it) appends nothing, as
-    // k_append skips it: the row would otherwise land in page 0, another stream's tile.
-    const int wblk = R.write_slot >> 4, wj = wblk / SPLIT;
-    const bool owner = fused && w == wblk % SPLIT && __builtin_amdgcn_readlane(my_ok, wj) != 0;
-    const bool early = !owner || wj >= DEPTH;
-    if (early) {
-#pragma unroll
-        for (int d = 0; d < DEPTH; ++d) load(kb[d], vb[d], d);
-    }
+    // complete_kv: the wave that owns the write page (above) appends this head's new row, then
+    // reads it back with the rest of its pages (its own lanes' stores; no other wave touches the
+    // page).  A workgroup-scope fence orders the stores before the later loads on the same CU;
+    // nothing waits for the stores to reach memory.  An invalid write page id (never handed out by
+    // the host, which checks it) appends nothing, as k_append skips it: the row would otherwise
+    // land in page 0, another stream's tile.
     if (owner) {
         const int slot = R.write_slot;
         const size_t arow = (size_t)R.b * pv.KVH + kvh;

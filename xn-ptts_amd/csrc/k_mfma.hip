@@ -684,39 +684,74 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
         my_page = ok ? pg_raw : 0;
         my_ok = ok ? 1 : 0;
         my_seen = ok ? seen : 0;
-        if constexpr (I8) {
+    }
+
+    // B operands of S^T: query head kvh G + l16, dims 32 kc + 8 g .. +7, rotated at R.pos (PREFIX:
+    // and at R.pos_pre) with the packed bf16 RoPE rows and rounded to bf16 (zeros past G).  The
+    // query and RoPE pieces are loaded here, unconditionally (head clamped), and rotated once the
+    // first pages' loads are out (below), so that those wait for nothing but the page ids.
+    uint4 qraw[2], qcs[2], pcs[2];
+    {
+        const int hq = kvh * G + min(l16, G - 1);
+        const uint16_t *qp = (const uint16_t *)q + ((size_t)R.b * pv.H + hq) * kHeadDim;
+        const uint32_t *cs = pv.rope16 + (size_t)R.pos * (kHeadDim / 2);
+        const uint32_t *ps = pv.rope16 + (size_t)(PREFIX && R.prefix > 0 ? R.pos_pre : R.pos) * (kHeadDim / 2);
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) {
+            qraw[kc] = *(const uint4 *)(qp + 32 * kc + 8 * g);
+            qcs[kc] = *(const uint4 *)(cs + 16 * kc + 4 * g);
+            if constexpr (PREFIX) pcs[kc] = *(const uint4 *)(ps + 16 * kc + 4 * g);
+        }
+    }
+
+    constexpr int ES = I8 ? 1 : 2; // bytes per cached value
+    const char *kbase = (const char *)pv.pages + tile_index(pv, layer, 0, 0, kvh) * (kBlock * kHeadDim * ES);
+    const char *vbase = (const char *)pv.pages + tile_index(pv, layer, 1, 0, kvh) * (kBlock * kHeadDim * ES);
+    const size_t page_bytes = (size_t)pv.KVH * kBlock * kHeadDim * ES;
+    // a page's K and V tiles, each in two streamed 1 KB loads (keys lane / 8 and 8 + lane / 8,
+    // dims 8 (lane % 8) ..): every load covers whole 128-byte lines.  Loaded straight in the MFMA's
+    // A layout, each load would take half of every line, and a streamed line is gone before the
+    // other half is read (33 -> 36.6 us at 1 kv head); K therefore goes through an LDS tile too.
+    // Measured against plain loads in A layout: 1 kv head 33.4 -> 28.8 us, 2: 56.5 -> 50.5, 4:
+    // 101.5 -> 89 us.
+    // int8: a tile is 1 KB, lane l's 16 bytes being key l / 4, dims 16 (l % 4) ..
+    auto load = [&](uint4 (&kr)[NL], uint4 (&vr)[NL], int j) {
+        const size_t pe = (size_t)__builtin_amdgcn_readlane(my_page, j) * page_bytes;
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            kr[i] = ld_stream(kbase + pe + 1024 * i + 16 * lane);
+            vr[i] = ld_stream(vbase + pe + 1024 * i + 16 * lane);
+        }
+    };
+    // The first DEPTH pages' loads go out before the queries are rotated; the wave that owns the
+    // write page loads them after its append instead when the write page is among them (as in
+    // attend_core).
+    uint4 kb[DEPTH + 1][NL], vb[DEPTH + 1][NL];
+    const int wblk = R.write_slot >> 4, wj = wblk / SPLIT;
+    const bool owner = fused && w == wblk % SPLIT && __builtin_amdgcn_readlane(my_ok, wj) != 0;
+    const bool early = !owner || wj >= DEPTH;
+    if (early) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) load(kb[d], vb[d], d);
+    }
+    // int8: the pages' scales, after those loads (a wait for the page ids before them would
+    // otherwise wait for these too)
+    if constexpr (I8) {
+        if (lane < nb) {
             my_sk = pv.scales[tile_index(pv, layer, 0, my_page, kvh)];
             my_sv = pv.scales[tile_index(pv, layer, 1, my_page, kvh)];
         }
     }
 
-    // B operands of S^T: query head kvh G + l16, dims 32 kc + 8 g .. +7, rotated at R.pos (PREFIX:
-    // and at R.pos_pre) and rounded to bf16 (zeros past G)
     bf16x8_t qb[2], qpre[2];
-    auto rotated = [&](int pos, bf16x8_t (&dst)[2]) {
+    {
         const bool live = l16 < G;
-        const int hq = kvh * G + min(l16, G - 1);
-        const uint16_t *qp = (const uint16_t *)q + ((size_t)R.b * pv.H + hq) * kHeadDim;
-        const float4 *cs = (const float4 *)(pv.rope + (size_t)pos * (kHeadDim / 2));
 #pragma unroll
         for (int kc = 0; kc < 2; ++kc) {
-            const uint4 raw = *(const uint4 *)(qp + 32 * kc + 8 * g);
-            const float4 ca = cs[(32 * kc + 8 * g) / 4], cb = cs[(32 * kc + 8 * g) / 4 + 1];
-            const float cf[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w}; // cos, sin of 4 pairs
-            const uint32_t *u = (const uint32_t *)&raw;
-            uint32_t o4[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float x0 = bf16_value(u[i] & 0xffffu), x1 = bf16_value(u[i] >> 16);
-                const float c = cf[2 * i], s = cf[2 * i + 1];
-                const float a = x0 * c, bb = x1 * s, e = x0 * s, f = x1 * c;
-                o4[i] = live ? pack_bf16(a - bb, e + f) : 0u;
-            }
-            dst[kc] = as_bf16x8(make_uint4(o4[0], o4[1], o4[2], o4[3]));
+            qb[kc] = as_bf16x8(live ? rotate8(qraw[kc], qcs[kc]) : make_uint4(0, 0, 0, 0));
+            if constexpr (PREFIX) qpre[kc] = as_bf16x8(live ? rotate8(qraw[kc], pcs[kc]) : make_uint4(0, 0, 0, 0));
         }
-    };
-    rotated(R.pos, qb);
-    if constexpr (PREFIX) rotated(R.prefix > 0 ? R.pos_pre : R.pos, qpre);
+    }
     // int8: the same queries as f16, scaled by a power of two that fits the column into f16
     // (f16_fit_exponent: exact), and their sum over the 64 dims of the lane's column
     f16x8_t qh[2];
@@ -752,31 +787,11 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
         qsum += __shfl_xor(qsum, 32);
     }
 
-    constexpr int ES = I8 ? 1 : 2; // bytes per cached value
-    const char *kbase = (const char *)pv.pages + tile_index(pv, layer, 0, 0, kvh) * (kBlock * kHeadDim * ES);
-    const char *vbase = (const char *)pv.pages + tile_index(pv, layer, 1, 0, kvh) * (kBlock * kHeadDim * ES);
-    const size_t page_bytes = (size_t)pv.KVH * kBlock * kHeadDim * ES;
-
     float m = -1e30f, lsum = 0.f; // running max (scaled, log2 units) and this lane's share of the sum
     f32x4_t o[4];                 // O^T: dims 16 dg + 4 g + r, query head l16
 #pragma unroll
     for (int dg = 0; dg < 4; ++dg) o[dg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    // a page's K and V tiles, each in two streamed 1 KB loads (keys lane / 8 and 8 + lane / 8,
-    // dims 8 (lane % 8) ..): every load covers whole 128-byte lines.  Loaded straight in the MFMA's
-    // A layout, each load would take half of every line, and a streamed line is gone before the
-    // other half is read (33 -> 36.6 us at 1 kv head); K therefore goes through an LDS tile too.
-    // Measured against plain loads in A layout: 1 kv head 33.4 -> 28.8 us, 2: 56.5 -> 50.5, 4:
-    // 101.5 -> 89 us.
-    // int8: a tile is 1 KB, lane l's 16 bytes being key l / 4, dims 16 (l % 4) ..
-    auto load = [&](uint4 (&kr)[NL], uint4 (&vr)[NL], int j) {
-        const size_t pe = (size_t)__builtin_amdgcn_readlane(my_page, j) * page_bytes;
-#pragma unroll
-        for (int i = 0; i < NL; ++i) {
-            kr[i] = ld_stream(kbase + pe + 1024 * i + 16 * lane);
-            vr[i] = ld_stream(vbase + pe + 1024 * i + 16 * lane);
-        }
-    };
     auto process = [&](const uint4 (&kr)[NL], const uint4 (&vr)[NL], int j) {
         const uint32_t seen = __builtin_amdgcn_readlane(my_seen, j);
         f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -881,16 +896,8 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
         }
     };
 
-    uint4 kb[DEPTH + 1][NL], vb[DEPTH + 1][NL];
     // complete_kv: the wave that owns the write page appends the kv head's new row, as in attend_core
     // an invalid write page id appends nothing, as in attend_core
-    const int wblk = R.write_slot >> 4, wj = wblk / SPLIT;
-    const bool owner = fused && w == wblk % SPLIT && __builtin_amdgcn_readlane(my_ok, wj) != 0;
-    const bool early = !owner || wj >= DEPTH;
-    if (early) {
-#pragma unroll
-        for (int d = 0; d < DEPTH; ++d) load(kb[d], vb[d], d);
-    }
     if (owner) {
         const int slot = R.write_slot;
         const size_t arow = (size_t)R.b * pv.KVH + kvh;
