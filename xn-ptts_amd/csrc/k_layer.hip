@@ -44,6 +44,20 @@ __global__ __launch_bounds__(256) void k_layer_norm(const uint16_t *x, int rows,
             rsc[c] = *(const uint4 *)(scale + (size_t)row * ld_mod + (c * 64 + lane) * 8);
         }
     }
+    float4 aw[CH][2], ab[CH][2]; // the affine's weights and biases, loaded with x too
+    if constexpr ((MODE & kLnAffine) != 0) {
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int e0 = (c * 64 + lane) * 8;
+            aw[c][0] = *(const float4 *)(w + e0);
+            aw[c][1] = *(const float4 *)(w + e0 + 4);
+            ab[c][0] = *(const float4 *)(b + e0);
+            ab[c][1] = *(const float4 *)(b + e0 + 4);
+        }
+    }
+    // a scheduling barrier: keeps the loads above here, issued together with x's, rather than
+    // sunk to their uses after the row's reductions (a second round trip)
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) sum += __shfl_xor(sum, o);
     const float mean = sum / (float)dim;
@@ -63,8 +77,7 @@ __global__ __launch_bounds__(256) void k_layer_norm(const uint16_t *x, int rows,
         const int e0 = (c * 64 + lane) * 8;
         float ww[8], bb[8];
         if constexpr ((MODE & kLnAffine) != 0) {
-            const float4 w0 = *(const float4 *)(w + e0), w1 = *(const float4 *)(w + e0 + 4);
-            const float4 b0 = *(const float4 *)(b + e0), b1 = *(const float4 *)(b + e0 + 4);
+            const float4 w0 = aw[c][0], w1 = aw[c][1], b0 = ab[c][0], b1 = ab[c][1];
             const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
             const float bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
 #pragma unroll
@@ -574,14 +587,15 @@ __global__ __launch_bounds__(256) void k_linear_f32(const float *x, int ldx, int
                                                     const float *bias, int N, LinOut lo, LinNorm ln) {
     const int n = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (n >= N) return;
-    // every load is issued unconditionally (the index clamped, the value then zeroed), so that all
-    // of them are in flight together rather than each behind a branch and a wait
+    // every load is issued unconditionally (the index clamped), so that all of them are in flight
+    // together rather than each behind a branch and a wait.  Columns past K are zeroed on the x side,
+    // inside the row loop: a select on w would be hoisted out of the loop, and every w load would
+    // then be waited for before any x load is issued.
     float w[KC], nw[KC], nb[KC];
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
-        const int k = c * 64 + lane, kk = min(k, K - 1);
-        const float wv = W[(size_t)n * K + kk];
-        w[c] = k < K ? wv : 0.f;
+        const int kk = min(c * 64 + lane, K - 1);
+        w[c] = W[(size_t)n * K + kk];
         if constexpr ((NORM & kNormAffine) != 0) {
             nw[c] = ln.w[kk];
             nb[c] = ln.b[kk];
@@ -600,6 +614,24 @@ __global__ __launch_bounds__(256) void k_linear_f32(const float *x, int ldx, int
                 sc[c] = ln.scale[(size_t)m * ln.ld_mod + kk];
             }
         }
+        // the output's address (segments picked with constant indices, so the kernel arguments are
+        // read as scalars), and the epilogue's operand loaded with x (every lane, the same word)
+        float *o = lo.out[0] + (size_t)m * lo.ld[0] + (n - lo.col0[0]);
+        if (lo.nseg > 1 && n >= lo.col0[1]) {
+            if (lo.nseg > 2 && n >= lo.col0[2])
+                o = lo.out[2] + (size_t)m * lo.ld[2] + (n - lo.col0[2]);
+            else
+                o = lo.out[1] + (size_t)m * lo.ld[1] + (n - lo.col0[1]);
+        }
+        float eo = 0.f, er = 0.f; // the auxiliary operand; the residual (the output's old value)
+        if constexpr (EPI == kLinResidual || EPI == kLinGated) er = *o;
+        if constexpr (EPI == kLinSiluAddVec)
+            eo = lo.aux[n];
+        else if constexpr (EPI == kLinGated || EPI == kLinAxpy)
+            eo = lo.aux[(size_t)m * lo.ld_aux + n];
+        // a scheduling barrier: the loads above stay here, issued together, rather than sunk to
+        // their uses after the reductions (a round trip each)
+        __builtin_amdgcn_sched_barrier(0);
         if constexpr ((NORM & kNormLn) != 0) {
             // mean, then the centred sum of squares: the two passes of a textbook LayerNorm
             float sum = 0.f;
@@ -627,14 +659,11 @@ __global__ __launch_bounds__(256) void k_linear_f32(const float *x, int ldx, int
         }
         float acc = 0.f;
 #pragma unroll
-        for (int c = 0; c < KC; ++c) acc = __builtin_fmaf(w[c], xv[c], acc); // w is 0 past K
+        for (int c = 0; c < KC; ++c) acc = __builtin_fmaf(w[c], c * 64 + lane < K ? xv[c] : 0.f, acc);
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
         if (lane != 0) continue;
         const float y = acc + b;
-        int seg = 0;
-        if (lo.nseg > 1 && n >= lo.col0[1]) seg = (lo.nseg > 2 && n >= lo.col0[2]) ? 2 : 1;
-        float *o = lo.out[seg] + (size_t)m * lo.ld[seg] + (n - lo.col0[seg]);
         if constexpr (EPI == kLinStore) {
             *o = y;
         } else if constexpr (EPI == kLinGeluErf) {
@@ -645,14 +674,14 @@ __global__ __launch_bounds__(256) void k_linear_f32(const float *x, int ldx, int
         } else if constexpr (EPI == kLinSilu) {
             *o = y / (1.0f + expf(-y));
         } else if constexpr (EPI == kLinSiluAddVec) {
-            const float z = y + lo.aux[n];
+            const float z = y + eo;
             *o = z / (1.0f + expf(-z));
         } else if constexpr (EPI == kLinResidual) {
-            *o = *o + y;
+            *o = er + y;
         } else if constexpr (EPI == kLinGated) {
-            *o = *o + lo.aux[(size_t)m * lo.ld_aux + n] * y;
+            *o = er + eo * y;
         } else { // kLinAxpy
-            *o = lo.aux[(size_t)m * lo.ld_aux + n] + y * lo.alpha;
+            *o = eo + y * lo.alpha;
         }
     }
 }
