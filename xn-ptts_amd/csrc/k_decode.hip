@@ -438,6 +438,12 @@ static bool decode_on_mfma(const PoolView &pv, bool prefix) {
     return pv.cache_dt == DT_BF16 || (pv.cache_dt == DT_I8 && !prefix);
 }
 
+int decode_min_split(const PoolView &pv, bool prefix) {
+    // one wave per (stream, kv head) on MFMA measured slower than two: one kv head of 8 query
+    // heads, caches of 512 rows, 17.0 -> 19.3 us; the int8 window at 2 kv heads 30.0 -> 30.6 us
+    return decode_on_mfma(pv, prefix) ? 2 : 1;
+}
+
 int decode_heads_per_group(const PoolView &pv, bool prefix) {
     // query heads of one kv head share a group's page reads: all of them on MFMA; else four when
     // four divide the group and no stream of the batch keeps a ring prefix (whose second query

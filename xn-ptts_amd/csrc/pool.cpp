@@ -442,8 +442,11 @@ extern "C" xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out)
         return fail(XNP_E_INVALID, "cache dtype %d with activation dtype %d is not supported", d.cache_dtype,
                     d.act_dtype);
     if (d.max_pos <= 0 || !(d.max_period > 0.0f)) return fail(XNP_E_INVALID, "max_pos and max_period must be positive");
-    // default: the fewest waves per (stream, head) whose lanes can index a stream's pages
+    // default: the fewest waves per (stream, head) whose lanes can index a stream's pages (one wave
+    // per group measured fastest where it can: the int8 window 95.3-95.6 -> 91.9-92.2 us, bf16
+    // caches of 256 rows 57 -> 53.6 us; the MFMA decode keeps two, below)
     const int split = d.decode_split ? d.decode_split
+                      : d.max_blocks_per_stream <= kLaneBlocks ? 1
                       : d.max_blocks_per_stream <= kLaneBlocks * 2 ? 2
                       : d.max_blocks_per_stream <= kLaneBlocks * 4 ? 4 : 8;
     if (split != 1 && split != 2 && split != 4 && split != 8)
@@ -1277,6 +1280,8 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
     B.bv.prefix = 0;
     for (int32_t i = 0; i < n; i++) B.bv.prefix |= plans[i].prefix > 0;
     B.bv.split = pool->split;
+    if (!pool->d.decode_split && t == 1)
+        B.bv.split = std::max(B.bv.split, decode_min_split(pool->view(), B.bv.prefix != 0));
     const int gq = t == 1 ? decode_heads_per_group(pool->view(), B.bv.prefix != 0) : 1;
     const int64_t groups = (int64_t)n * t * pool->d.num_heads / gq;
     while (!pool->d.decode_split && B.bv.split < 8 && groups * B.bv.split < 1024)

@@ -124,6 +124,9 @@ hipError_t launch_append(const PoolView &pv, const BatchView &bv, int layer, con
 // prefix in the batch; else 4 when 4 divide the group and no prefix, 2 when 2 do, else 1 (always
 // 1 for int8).
 int decode_heads_per_group(const PoolView &pv, bool prefix);
+// The fewest waves per work group a one-row decode of this pool and batch takes by default: 2 on
+// MFMA (grouped heads), else 1.
+int decode_min_split(const PoolView &pv, bool prefix);
 hipError_t launch_decode(const PoolView &pv, const BatchView &bv, int layer, const void *q,
                          const void *k, const void *v, void *out, float scale, bool fused,
                          hipStream_t stream, const LaunchTiming &timing);
