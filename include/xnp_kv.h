@@ -125,7 +125,7 @@ typedef struct xnp_pool_stats {
     int32_t work_items; /* decode work groups of the open batch: one per (stream, head) */
     int64_t device_bytes;
     int32_t rope_rows;  /* rows of the RoPE tables now (positions 0 .. rope_rows - 1) */
-    int32_t pad;
+    int32_t decode_waves; /* waves per decode work group of the open one-row batch, 0 if none */
 } xnp_pool_stats;
 
 /* ---- pool ------------------------------------------------------------------------------ */

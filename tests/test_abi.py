@@ -206,6 +206,39 @@ def test_decode_runs_one_work_group_per_stream_and_head():
         pool(decode_split=2, max_blocks_per_stream=121)
 
 
+def test_decode_waves_per_group_follow_the_pages_a_wave_indexes():
+    # by default: the fewest waves whose lanes index a stream's pages (one up to 60 pages, two up to
+    # 120, four up to 240, then eight); at least two on the MFMA decode of grouped bf16 heads; and
+    # more for a batch too small to fill the GPU (about 1024 waves); a fixed split stays fixed
+    def waves(streams=160, **kw):
+        args = dict(num_heads=8, num_blocks=streams + 8, max_streams=streams, cache_dtype="bf16", act_dtype="bf16")
+        args.update(kw)
+        p = pool(**args)
+        ids = [p.init_state(16) for _ in range(streams)]
+        p.begin(ids)
+        w = p.stats()["decode_waves"]
+        p.abort()
+        assert p.stats()["decode_waves"] == 0
+        return w
+
+    assert waves(max_blocks_per_stream=60) == 1
+    assert waves(max_blocks_per_stream=61) == 2
+    assert waves(max_blocks_per_stream=121) == 4
+    assert waves(max_blocks_per_stream=241) == 8
+    assert waves(max_blocks_per_stream=8, cache_dtype="i8") == 1
+    # 4 query heads per kv head, 600 streams: 1200 groups of a kv head on MFMA (two waves), or of
+    # four query heads each on the VALU (f32: one wave)
+    assert waves(streams=600, max_blocks_per_stream=8, num_kv_heads=2) == 2
+    assert waves(streams=600, max_blocks_per_stream=8, num_kv_heads=2, cache_dtype="f32", act_dtype="f32") == 1
+    assert waves(streams=160, max_blocks_per_stream=8, num_kv_heads=2) == 4  # 320 groups: grown
+    assert waves(streams=16, max_blocks_per_stream=8) == 8                  # 128 groups: grown to 8
+    assert waves(streams=160, max_blocks_per_stream=8, decode_split=1) == 1
+    p = pool(max_blocks_per_stream=8)
+    p.begin([p.init_state(16)], t=4)  # a prompt step decodes nothing
+    assert p.stats()["decode_waves"] == 0
+    p.abort()
+
+
 # ---- with_seq_budget (transformer.rs:350-392) ------------------------------------------------
 def test_fork_shares_full_pages_and_copies_the_partial_one():
     p = pool()

@@ -576,7 +576,7 @@ extern "C" xnp_status xnp_pool_stats_get(const xnp_pool *pool, xnp_pool_stats *o
     out->work_items = pool->batch.open && pool->batch.t == 1 ? pool->batch.n * pool->d.num_heads : 0;
     out->device_bytes = pool->device_bytes;
     out->rope_rows = pool->rope_rows;
-    out->pad = 0;
+    out->decode_waves = pool->batch.open && pool->batch.t == 1 ? pool->batch.bv.split : 0;
     return XNP_OK;
 }
 
@@ -1198,6 +1198,21 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
     for (int32_t i = 0; i < n; i++) order[i] = i;
     if (t == 1)
         std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) { return plans[a].span > plans[b].span; });
+    // waves per decode work group, unless the caller fixed them: the pool's default (the fewest
+    // whose lanes index a stream's pages), at least two on MFMA; and a batch of few groups fills
+    // few CUs, so give each group more waves (a larger split only raises the pages a group can
+    // index) until the batch has about one wave per SIMD
+    B.bv.prefix = 0;
+    for (int32_t i = 0; i < n; i++) B.bv.prefix |= plans[i].prefix > 0;
+    B.bv.split = pool->split;
+    if (!pool->d.decode_split && t == 1)
+        B.bv.split = std::max(B.bv.split, decode_min_split(pool->view(), B.bv.prefix != 0));
+    {
+        const int gq = t == 1 ? decode_heads_per_group(pool->view(), B.bv.prefix != 0) : 1;
+        const int64_t groups = (int64_t)n * t * pool->d.num_heads / gq;
+        while (!pool->d.decode_split && B.bv.split < 8 && groups * B.bv.split < 1024)
+            B.bv.split *= 2;
+    }
     if (pool->host_only) {
         B.open = true;
         return XNP_OK;
@@ -1274,18 +1289,6 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
     B.bv.plans = (const StreamPlan *)(pool->dbatch + o_plans);
     B.bv.recs = pool->dbatch + o_recs;
     B.bv.rec_stride = pool->rec_stride;
-    // unless the caller fixed the split: a batch of few (stream, head) groups fills few CUs, so give
-    // each group more waves (a larger split only raises the pages a group can index) until the batch
-    // has about one wave per SIMD
-    B.bv.prefix = 0;
-    for (int32_t i = 0; i < n; i++) B.bv.prefix |= plans[i].prefix > 0;
-    B.bv.split = pool->split;
-    if (!pool->d.decode_split && t == 1)
-        B.bv.split = std::max(B.bv.split, decode_min_split(pool->view(), B.bv.prefix != 0));
-    const int gq = t == 1 ? decode_heads_per_group(pool->view(), B.bv.prefix != 0) : 1;
-    const int64_t groups = (int64_t)n * t * pool->d.num_heads / gq;
-    while (!pool->d.decode_split && B.bv.split < 8 && groups * B.bv.split < 1024)
-        B.bv.split *= 2;
     B.bv.masks = (const uint32_t *)(pool->dbatch + o_masks);
     B.bv.wrow = -1;
     B.bv.n = n;

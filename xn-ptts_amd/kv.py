@@ -71,7 +71,8 @@ class StreamInfo(_c.Structure):
 
 class PoolStats(_c.Structure):
     _fields_ = [("free_blocks", _i32), ("open_streams", _i32), ("batch_open", _i32),
-                ("work_items", _i32), ("device_bytes", _c.c_int64), ("rope_rows", _i32), ("pad", _i32)]
+                ("work_items", _i32), ("device_bytes", _c.c_int64), ("rope_rows", _i32),
+                ("decode_waves", _i32)]
 
 
 SIGNATURES = {
