@@ -207,8 +207,9 @@ def test_decode_runs_one_work_group_per_stream_and_head():
 
 
 def test_decode_waves_per_group_follow_the_pages_a_wave_indexes():
-    # by default: the fewest waves whose lanes index a stream's pages (one up to 60 pages, two up to
-    # 120, four up to 240, then eight); at least two on the MFMA decode of grouped bf16 heads; and
+    # by default: the fewest waves whose lanes index a stream's pages (two up to 120 pages, four up
+    # to 240, then eight), one while a head's K and V tiles hold at most 128 KB (32 bf16 pages, 60
+    # int8 ones: a wave's lanes index 60); at least two on the MFMA decode of grouped bf16 heads;
     # more for a batch too small to fill the GPU (about 1024 waves); a fixed split stays fixed
     def waves(streams=160, **kw):
         args = dict(num_heads=8, num_blocks=streams + 8, max_streams=streams, cache_dtype="bf16", act_dtype="bf16")
@@ -221,8 +222,12 @@ def test_decode_waves_per_group_follow_the_pages_a_wave_indexes():
         assert p.stats()["decode_waves"] == 0
         return w
 
-    assert waves(max_blocks_per_stream=60) == 1
-    assert waves(max_blocks_per_stream=61) == 2
+    assert waves(max_blocks_per_stream=32) == 1
+    assert waves(max_blocks_per_stream=33) == 2
+    assert waves(max_blocks_per_stream=60, cache_dtype="i8") == 1
+    assert waves(max_blocks_per_stream=61, cache_dtype="i8") == 2
+    assert waves(max_blocks_per_stream=16, cache_dtype="f32", act_dtype="f32") == 1
+    assert waves(max_blocks_per_stream=17, cache_dtype="f32", act_dtype="f32") == 2
     assert waves(max_blocks_per_stream=121) == 4
     assert waves(max_blocks_per_stream=241) == 8
     assert waves(max_blocks_per_stream=8, cache_dtype="i8") == 1

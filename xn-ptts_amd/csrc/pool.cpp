@@ -442,11 +442,15 @@ extern "C" xnp_status xnp_pool_create(const xnp_pool_desc *desc, xnp_pool **out)
         return fail(XNP_E_INVALID, "cache dtype %d with activation dtype %d is not supported", d.cache_dtype,
                     d.act_dtype);
     if (d.max_pos <= 0 || !(d.max_period > 0.0f)) return fail(XNP_E_INVALID, "max_pos and max_period must be positive");
-    // default: the fewest waves per (stream, head) whose lanes can index a stream's pages (one wave
-    // per group measured fastest where it can: the int8 window 95.3-95.6 -> 91.9-92.2 us, bf16
-    // caches of 256 rows 57 -> 53.6 us; the MFMA decode keeps two, below)
+    // default: the fewest waves per (stream, head) whose lanes can index a stream's pages, and one
+    // wave only while a stream's K and V tiles of one head hold at most 128 KB.  Measured against
+    // two waves: the int8 window (528 rows, 66 KB) 95.3-95.6 -> 91.9-92.2 us, bf16 caches of 256
+    // rows (64 KB) 57 -> 53.6 us, of 512 rows (128 KB) equal, of 900 rows (225 KB) 150.4 -> 151.8
+    // us.  The MFMA decode keeps two (batch_begin).
+    const int cache_esz = d.cache_dtype == XNP_F32 ? 4 : d.cache_dtype == XNP_BF16 ? 2 : 1;
+    const int one_wave_pages = std::min(kLaneBlocks, (128 << 10) / (2 * kBlock * d.head_dim * cache_esz));
     const int split = d.decode_split ? d.decode_split
-                      : d.max_blocks_per_stream <= kLaneBlocks ? 1
+                      : d.max_blocks_per_stream <= one_wave_pages ? 1
                       : d.max_blocks_per_stream <= kLaneBlocks * 2 ? 2
                       : d.max_blocks_per_stream <= kLaneBlocks * 4 ? 4 : 8;
     if (split != 1 && split != 2 && split != 4 && split != 8)
