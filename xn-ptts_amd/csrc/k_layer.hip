@@ -58,8 +58,7 @@ __global__ __launch_bounds__(256) void k_layer_norm(const uint16_t *x, int rows,
     // a scheduling barrier: keeps the loads above here, issued together with x's, rather than
     // sunk to their uses after the row's reductions (a second round trip)
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) sum += __shfl_xor(sum, o);
+    sum = wave_sum(sum);
     const float mean = sum / (float)dim;
     float sq = 0.f;
 #pragma unroll
@@ -69,8 +68,7 @@ __global__ __launch_bounds__(256) void k_layer_norm(const uint16_t *x, int rows,
             const float d = v[c][i] - mean;
             sq = __builtin_fmaf(d, d, sq);
         }
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) sq += __shfl_xor(sq, o);
+    sq = wave_sum(sq);
     const float rstd = 1.0f / __builtin_sqrtf(sq / (float)dim + eps);
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
@@ -637,8 +635,7 @@ __global__ __launch_bounds__(256) void k_linear_f32(const float *x, int ldx, int
             float sum = 0.f;
 #pragma unroll
             for (int c = 0; c < KC; ++c) sum += c * 64 + lane < K ? xv[c] : 0.f;
-#pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o);
+            sum = wave_sum(sum);
             const float mean = sum / (float)K;
             float sq = 0.f;
 #pragma unroll
@@ -646,8 +643,7 @@ __global__ __launch_bounds__(256) void k_linear_f32(const float *x, int ldx, int
                 const float d = c * 64 + lane < K ? xv[c] - mean : 0.f;
                 sq = __builtin_fmaf(d, d, sq);
             }
-#pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
+            sq = wave_sum(sq);
             const float rstd = 1.0f / __builtin_sqrtf(sq / (float)K + ln.eps);
 #pragma unroll
             for (int c = 0; c < KC; ++c) {
@@ -660,8 +656,7 @@ __global__ __launch_bounds__(256) void k_linear_f32(const float *x, int ldx, int
         float acc = 0.f;
 #pragma unroll
         for (int c = 0; c < KC; ++c) acc = __builtin_fmaf(w[c], c * 64 + lane < K ? xv[c] : 0.f, acc);
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
+        acc = wave_sum(acc);
         if (lane != 0) continue;
         const float y = acc + b;
         if constexpr (EPI == kLinStore) {

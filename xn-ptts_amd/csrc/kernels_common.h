@@ -61,6 +61,25 @@ __device__ __forceinline__ int quant(float y, float s) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// The sum of x over the wave's 64 lanes, in every lane, without the LDS pipe: two DPP quad
+// permutes (lanes i ^ 1, i ^ 2), the half-row and row mirrors (i <-> 7 - i in each 8, i <-> 15 - i
+// in each 16), then gfx950's row swaps (i <-> i ^ 16, i <-> i ^ 32).  Each step adds a lane whose
+// partial covers a disjoint set of lanes, so every lane ends with the whole sum; the order of the
+// additions differs from an xor butterfly's (ds_bpermute shuffles, about 100 cycles each).
+template <int CTRL> __device__ __forceinline__ float dpp_move(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_sum(float x) {
+    x += dpp_move<0xB1>(x);  // quad_perm [1, 0, 3, 2]
+    x += dpp_move<0x4E>(x);  // quad_perm [2, 3, 0, 1]
+    x += dpp_move<0x141>(x); // row_half_mirror
+    x += dpp_move<0x140>(x); // row_mirror
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
 // 16 bytes with the non-temporal hint.  A decode launch reads each K/V tile once: streamed, the
 // tiles stop displacing what the launch does reuse in L2 and the memory-side cache (records,
 // tables, queries).  Measured on attend_core's page loads: bf16 decode at 1024 streams 192 ->
