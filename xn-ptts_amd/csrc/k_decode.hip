@@ -3,6 +3,8 @@
 // prefill dispatch.
 #include "kernels_common.h"
 
+#include <type_traits>
+
 namespace xnp {
 
 // ---------------------------------------------------------------------------------------------
@@ -227,8 +229,7 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
             }
 #pragma unroll
             for (int e = 0; e < GQ; ++e) {
-#pragma unroll
-                for (int o = 1; o < LPR; o <<= 1) dw[e] += __shfl_xor(dw[e], o);
+                dw[e] = group_sum<LPR>(dw[e]);
                 if constexpr (CDT == DT_I8) dw[e] *= sk;
                 if constexpr (H16) dw[e] *= pre ? ppow[e] : qpow[e];
                 if constexpr (DOT2 || H16) dw[e] *= qmul;
@@ -324,19 +325,25 @@ __device__ __forceinline__ void attend_core(const PoolView &pv, const BatchView 
             for (int i = 0; i < DPL; ++i) acc[e][i] = __builtin_fmaf(-128.f, vbias[e], acc[e][i]);
         }
         // Merge the row groups: lanes c, c + LPR, c + 2 LPR, ... hold the same dims.
+        auto merge = [&](auto O) {
+            constexpr int o = decltype(O)::value;
+            if constexpr (o >= LPR) {
+                const float mo = xor_lane<o>(m[e]), lo = xor_lane<o>(l[e]);
+                const float mn = fmaxf(m[e], mo);
+                const float a = fast_exp2(m[e] - mn), bb = fast_exp2(mo - mn);
+                l[e] = l[e] * a + lo * bb;
 #pragma unroll
-        for (int o = LPR; o < 64; o <<= 1) {
-            const float mo = __shfl_xor(m[e], o), lo = __shfl_xor(l[e], o);
-            const float mn = fmaxf(m[e], mo);
-            const float a = fast_exp2(m[e] - mn), bb = fast_exp2(mo - mn);
-            l[e] = l[e] * a + lo * bb;
-#pragma unroll
-            for (int i = 0; i < DPL; ++i) {
-                const float ao = __shfl_xor(acc[e][i], o);
-                acc[e][i] = acc[e][i] * a + ao * bb;
+                for (int i = 0; i < DPL; ++i) {
+                    const float ao = xor_lane<o>(acc[e][i]);
+                    acc[e][i] = acc[e][i] * a + ao * bb;
+                }
+                m[e] = mn;
             }
-            m[e] = mn;
-        }
+        };
+        merge(std::integral_constant<int, 4>{});
+        merge(std::integral_constant<int, 8>{});
+        merge(std::integral_constant<int, 16>{});
+        merge(std::integral_constant<int, 32>{});
         // the waves' shares of head h + e go through LDS
         if (g == 0) {
 #pragma unroll

@@ -69,6 +69,32 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 template <int CTRL> __device__ __forceinline__ float dpp_move(float x) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
 }
+// The sum of x over each aligned group of N lanes (N = 1, 2, 4, 8 or 16), in every lane of the
+// group: the first N's steps of wave_sum.
+template <int N> __device__ __forceinline__ float group_sum(float x) {
+    static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "groups within a 16-lane row");
+    if constexpr (N >= 2) x += dpp_move<0xB1>(x);
+    if constexpr (N >= 4) x += dpp_move<0x4E>(x);
+    if constexpr (N >= 8) x += dpp_move<0x141>(x);
+    if constexpr (N >= 16) x += dpp_move<0x140>(x);
+    return x;
+}
+// The value x holds in lane (this lane) ^ O: a DPP row rotation for O = 8 (by 8 within a 16-lane
+// row), gfx950's row swaps for 16 and 32 (each returns both halves; this lane takes its partner's),
+// an LDS-pipe shuffle otherwise.
+template <int O> __device__ __forceinline__ float xor_lane(float x) {
+    if constexpr (O == 8) {
+        return dpp_move<0x128>(x); // row_ror:8
+    } else if constexpr (O == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        return __uint_as_float((__lane_id() & 16) ? r[0] : r[1]);
+    } else if constexpr (O == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        return __uint_as_float((__lane_id() & 32) ? r[0] : r[1]);
+    } else {
+        return __shfl_xor(x, O);
+    }
+}
 __device__ __forceinline__ float wave_sum(float x) {
     x += dpp_move<0xB1>(x);  // quad_perm [1, 0, 3, 2]
     x += dpp_move<0x4E>(x);  // quad_perm [2, 3, 0, 1]
