@@ -876,6 +876,26 @@ def test_rows_written_raw_read_back_the_same(cache):
         assert torch.equal(sback, scales)
 
 
+@pytest.mark.parametrize("cache,act,maxlen", [("bf16", "bf16", 500), ("f32", "f32", 250), ("i8", "bf16", 900)])
+def test_one_wave_per_stream_and_head_at_batch_scale(cache, act, maxlen):
+    # Enough streams (160 x 8 heads) that the batch keeps the pool's default of one wave per
+    # (stream, head): caches whose K and V tiles of one head hold at most 128 KB.  Every stream's
+    # output against the oracle, two steps, and the cache rows of a sample bit for bit.
+    S, L = 160, 1
+    rng = np.random.default_rng(20261203)
+    lens = rng.integers(1, maxlen + 1, S)
+    p = Pair(cache=cache, act=act, streams=S, cap=maxlen + 4, seed=41, L=L, page_seed=17)
+    for i, n in enumerate(lens):
+        p.fill(i, int(n))
+    p.pool.begin(p.ids)
+    assert p.pool.stats()["decode_waves"] == 1
+    p.pool.abort()
+    for _ in range(2):
+        assert p.step() <= TOL[cache]
+    for i in range(0, S, 23):
+        p.assert_cache_equal(i)
+
+
 @pytest.mark.parametrize("split", [2, 8])
 def test_many_streams_at_the_config2_length_distribution(split):
     # 256 streams with cache lengths U[1, 1024] on shuffled pages, each head's pages shared out
