@@ -100,8 +100,10 @@ typedef struct xnp_pool_desc {
                              free list seeded with it (shuffled block tables) */
     int32_t device;       /* HIP device ordinal */
     int32_t decode_split; /* waves sharing one (stream, head) in decode: 1, 2, 4 or 8; a stream
-                             holds at most 60 * decode_split pages; 0: the fewest that fit, raised
-                             per batch (up to 8) while the batch has under 1024 waves */
+                             holds at most 60 * decode_split pages; 0: the fewest that fit (one only
+                             while a head's K and V tiles of a stream hold at most 128 KB), at least
+                             two on the MFMA decode of grouped heads, raised per batch (up to 8)
+                             while the batch has under 1024 waves (xnp_pool_stats.decode_waves) */
 } xnp_pool_desc;
 
 typedef struct xnp_stream_info {
