@@ -947,7 +947,7 @@ def nested_configs(args, xnp, torch, runs):
         t0 = time.perf_counter()
         res = runs[name](sub, xnp, torch)
         keep = {k: v for k, v in res.items() if k not in ("n_gpus", "scaling", "vs_baseline", "data")}
-        keep["baseline_config"] = cfg_index
+        keep["configuration"] = cfg_index
         keep["what"] = what
         keep["wall_s"] = round(time.perf_counter() - t0, 1)
         entries[name] = keep
