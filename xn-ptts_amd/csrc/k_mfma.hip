@@ -286,6 +286,322 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
 }
 
 // ---------------------------------------------------------------------------------------------
+// prompt prefill for streams whose keys fit 256 slots (write_slot + t <= 256): the same
+// contractions and tiles as k_prefill_mfma, but every key of the prompt is held in LDS at once, so
+// each thread issues all of its loads (its queries, the prompt's 4 chunks of K and V and their RoPE
+// rows) before it uses any.  The loads are unconditional (addresses clamped to real rows) and issued
+// in the order they are consumed, so the compiler's waits take them one by one as they land
+// (vector-memory loads complete in issue order) instead of draining the queue at every chunk, and a
+// group never waits on a chain of per-chunk round trips.  Then each thread rotates its keys, writes
+// its K and V pieces into LDS and, for the prompt's own rows, into their pages; one barrier; then
+// the chunks' S^T, softmax and O^T on MFMA from LDS alone.
+//
+// K's and V's LDS rows are 128 bytes, their 16-byte units placed at unit ^ pf_swz(key).  Every read
+// instruction of both contractions and the staging writes fall in distinct banks: the reads of K (16
+// keys at one unit: lanes l16 of each group of 16), the transposed reads of V (4 keys at two adjacent
+// units), and the staging writes (8 keys at all 8 units), whether the LDS serves 128 or 256 bytes a
+// clock.  (The padded 144-byte rows of k_prefill_mfma leave the transposed reads 2-way conflicted.)
+//
+// Work groups are numbered so that each XCD takes a contiguous run of (stream, head) groups: the H
+// groups of one stream read the H 128-byte pieces of the same 1 KB input rows through one L2 and
+// at about the same time.
+constexpr int kPfFastKeys = 256; // key slots a group holds: 4 chunks of 64
+
+__device__ __forceinline__ int pf_swz(int r) {
+    return ((r ^ (r >> 3)) & 1) | (r & 2) | (((r ^ (r >> 2)) & 1) << 2);
+}
+
+// PAGES: some keys of the stream come from its pages (keys before the prompt, or every key when the
+// append ran separately), so their loads wait for the page ids; otherwise every key is a prompt row
+// of the inputs and nothing waits before the loads go out.  DEPTH: chunks whose K/V loads go out
+// before the first is used; the others go out as the first ones are consumed.
+template <bool FUSED, bool PAGES, int DEPTH>
+__device__ __forceinline__ void prefill_fast_group(const PoolView &pv, const BatchView &bv, int layer, const void *q,
+                                                   const void *knew, const void *vnew, void *out, float qmul,
+                                                   int b, int h, uint16_t (*ks)[kPfKeys][kHeadDim],
+                                                   uint16_t (*vs)[kPfKeys][kHeadDim], uint4 *rp, int32_t *spages) {
+    constexpr int NC = kPfFastKeys / kPfKeys;
+    static_assert(DEPTH >= 1 && DEPTH <= NC, "chunks in flight");
+    const int t = bv.t;
+    const StreamPlan P = bv.plans[b];
+    const int32_t *tab = pv.tables + (size_t)P.sid * pv.mbps;
+    // the wave index through readfirstlane: the compiler then knows it (and the tiles, masks and
+    // branches derived from it) to be uniform over the wave, and branches on the scalar unit
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4,
+              l16 = lane & 15;
+    const int c0 = PAGES ? P.write_slot : 0; // slot (= position) of prompt row 0
+    const int kend = c0 + t;                 // keys [0, kend): at most kPfFastKeys
+    const int nch = (kend + kPfKeys - 1) / kPfKeys;
+    const int kvh = h / (pv.H / pv.KVH);
+    const size_t page_elems = (size_t)pv.KVH * kBlock * kHeadDim;
+    uint16_t *kpages = (uint16_t *)pv.pages + tile_index(pv, layer, 0, 0, kvh) * (kBlock * kHeadDim);
+    uint16_t *vpages = (uint16_t *)pv.pages + tile_index(pv, layer, 1, 0, kvh) * (kBlock * kHeadDim);
+    // this thread's share of each chunk: 16 bytes (8 dims, unit spart) of key skey
+    const int skey = tid >> 3, spart = tid & 7;
+
+    // Loads, all unconditional (addresses clamped to real rows) and in the order they are used:
+    // the page of each chunk's key (for its page store, or its load), the RoPE rows of the chunks'
+    // keys (parked in LDS below, so that no register holds them through the loop), this wave's
+    // queries and their RoPE rows, then the chunks' K and V.
+    // The RoPE rows of the chunks' keys go straight into this thread's own LDS pieces (no other thread
+    // reads them; lane l of a wave's 1 KB load lands at 16 l), first of all: loads complete in issue
+    // order, so every wait the compiler places for a later load covers them too.
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int slot = min(c * kPfKeys + skey, kend - 1), i = max(slot - c0, 0);
+        dma16(pv.rope16 + (size_t)(P.key_pos + i) * (kHeadDim / 2) + 4 * spart, &rp[c * 64 * kPfWaves + 64 * w]);
+    }
+    // page ids: thread i < 16 holds block i's (the page stores and page loads read them from LDS)
+    const int my_pg = tab[min(tid, (kend - 1) >> 4)];
+    // this wave's query tiles: (w, nq-1-w) for w < nq/2; the middle one alone when nq is odd
+    const int nq = (t + 15) / 16;
+    int tile[2] = {-1, -1};
+    if (w < nq / 2) {
+        tile[0] = w;
+        tile[1] = nq - 1 - w;
+    } else if (w == nq / 2 && (nq & 1)) {
+        tile[0] = w;
+    }
+    // B operands of S^T: query row 16 tile + l16, dims 32 kc + 8 g .. +7, with their (cos, sin) rows
+    uint4 qraw[2][2], qcs[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int qr = min(16 * max(tile[j], 0) + l16, t - 1);
+        const uint16_t *qp = (const uint16_t *)q + (((size_t)b * t + qr) * pv.H + h) * kHeadDim;
+        const uint32_t *cs = pv.rope16 + (size_t)(P.pos + qr) * (kHeadDim / 2);
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) {
+            qraw[j][kc] = *(const uint4 *)(qp + 32 * kc + 8 * g);
+            qcs[j][kc] = *(const uint4 *)(cs + 16 * kc + 4 * g);
+        }
+    }
+    uint4 kr[NC], vr[NC];
+    auto issue = [&](auto C) {
+        constexpr int c = decltype(C)::value;
+        const int slot = min(c * kPfKeys + skey, kend - 1);
+        const bool fresh = FUSED && slot >= c0;
+        const int i = fresh ? slot - c0 : 0;
+        const size_t arow = (((size_t)b * t + i) * pv.KVH + kvh) * kHeadDim + 8 * spart;
+        const uint16_t *ksrc = (const uint16_t *)knew + arow, *vsrc = (const uint16_t *)vnew + arow;
+        if constexpr (PAGES) {
+            const int pgc = spages[slot >> 4];
+            const int page = pgc >= 0 && pgc < pv.NB ? pgc : 0;
+            const size_t poff = (size_t)page * page_elems + (slot & 15) * kHeadDim + 8 * spart;
+            ksrc = fresh ? ksrc : kpages + poff;
+            vsrc = fresh ? vsrc : vpages + poff;
+        }
+        kr[c] = ld_stream(ksrc);
+        vr[c] = ld_stream(vsrc);
+    };
+    if constexpr (PAGES) { // the page loads need the page ids: a round trip before any chunk goes out
+        if (tid < kPfFastKeys / kBlock) spages[tid] = my_pg;
+        __syncthreads();
+    }
+    issue(std::integral_constant<int, 0>{});
+    if constexpr (DEPTH > 1) issue(std::integral_constant<int, 1>{});
+    if constexpr (DEPTH > 2) issue(std::integral_constant<int, 2>{});
+    if constexpr (DEPTH > 3) issue(std::integral_constant<int, 3>{});
+    // nothing below moves above the loads: an LDS store hoisted above them would wait for the loads
+    // its data comes from before they go out
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (!PAGES)
+        if (tid < kPfFastKeys / kBlock) spages[tid] = my_pg;
+
+    // the queries, rotated at their positions and rounded to bf16 as the reference's bf16 q is
+    bf16x8_t qb[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const bool live = tile[j] >= 0 && 16 * tile[j] + l16 < t;
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) {
+            const uint4 r = rotate8(qraw[j][kc], qcs[j][kc]);
+            qb[j][kc] = as_bf16x8(live ? r : make_uint4(0, 0, 0, 0));
+        }
+    }
+
+    float m[2], lsum[2]; // running max (scaled, log2 units) and this lane's share of the sum
+    f32x4_t o[2][4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        m[j] = -1e30f;
+        lsum[j] = 0.f;
+#pragma unroll
+        for (int dg = 0; dg < 4; ++dg) o[j][dg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    // out[row][h][16 dg + 4 g .. +3] = O / l of tile j, the row's sum reduced over its 4 lanes
+    auto store_tile = [&](int j) {
+        float l = lsum[j];
+        l += xor_lane<16>(l);
+        l += xor_lane<32>(l);
+        const int qrow = 16 * tile[j] + l16;
+        if (qrow >= t) return;
+        const float inv = 1.0f / l;
+        uint16_t *orow = (uint16_t *)out + (((size_t)b * t + qrow) * pv.H + h) * kHeadDim;
+#pragma unroll
+        for (int dg = 0; dg < 4; ++dg)
+            *(uint2 *)(orow + 16 * dg + 4 * g) = make_uint2(pack_bf16(o[j][dg][0] * inv, o[j][dg][1] * inv),
+                                                            pack_bf16(o[j][dg][2] * inv, o[j][dg][3] * inv));
+    };
+    // The lane's LDS read offsets within a chunk slot, computed once: the swizzle of a row depends
+    // on its low 4 bits only, so the slot, the 16-key group, the 32-key half and the second
+    // transposed read are constant offsets from these.
+    //   K (A of S^T):  row l16 (+ 16 kg), unit 4 kc + g
+    //   V (A of O^T):  row 4 g + l16 / 4 (+ 32 kp, + 16), unit 2 dg + (l16 % 4) / 2, half l16 % 2
+    constexpr int kRowB = kHeadDim * 2, kSlotB = kPfKeys * kRowB;
+    const char *ksb = (const char *)&ks[0][0][0], *vsb = (const char *)&vs[0][0][0];
+    int kofs[2], vofs[4];
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) kofs[kc] = l16 * kRowB + 16 * ((4 * kc + g) ^ pf_swz(l16));
+    {
+        const int vrow = 4 * g + (l16 >> 2), vf = pf_swz(vrow), vu = (l16 & 3) >> 1;
+#pragma unroll
+        for (int dg = 0; dg < 4; ++dg) vofs[dg] = vrow * kRowB + 16 * ((2 * dg + vu) ^ vf) + 8 * (l16 & 1);
+    }
+    auto step = [&](auto C) {
+        constexpr int c = decltype(C)::value;
+        const int kbase = c * kPfKeys, u = c & 1;
+        // stage chunk c: a prompt key rotated at its position (rotated whatever the key, then chosen:
+        // a use under a branch lets the compiler sink a load behind the others, and its wait would
+        // then drain them all); the piece into LDS slot c & 1, the prompt's rows into their pages
+        // (complete_kv, transformer.rs:84-91; a page id outside the pool writes nothing)
+        {
+            const int slot = kbase + skey, cl = min(slot, kend - 1);
+            const bool fresh = FUSED && cl >= c0;
+            // kr[c] has landed, and with it the RoPE pieces loaded before it; their LDS read stays below
+            asm volatile("" ::"v"(kr[c].x) : "memory");
+            const uint4 rot = rotate8(kr[c], rp[c * 64 * kPfWaves + tid]);
+            const uint4 kk = fresh ? rot : kr[c];
+            const int pu = 8 * (spart ^ pf_swz(skey));
+            *(uint4 *)&ks[u][skey][pu] = kk;
+            *(uint4 *)&vs[u][skey][pu] = vr[c];
+            // chunk c is in slot c & 1; every reader of chunk c - 2 (same slot) is done; the page ids
+            // are in LDS.  An LDS-only barrier: __syncthreads would also wait for earlier chunks' page
+            // stores, which nothing here reads back.
+            lds_barrier();
+            const int pgc = spages[min(slot, kend - 1) >> 4];
+            if (FUSED && fresh && slot < kend && pgc >= 0 && pgc < pv.NB) {
+                const size_t poff = (size_t)pgc * page_elems + (slot & 15) * kHeadDim + 8 * spart;
+                *(uint4 *)(kpages + poff) = kk;
+                *(uint4 *)(vpages + poff) = vr[c];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int r0 = c0 + 16 * tile[j]; // slot of the tile's first row
+            // skip a tile when every key of the chunk comes after all of its rows (and every chunk
+            // past the keys)
+            if (c >= nch || tile[j] < 0 || kbase > r0 + 15) continue;
+            // key kbase + 16 kg + 4 g + r is seen by row r0 + l16 when 16 kg + 4 g + r <= rel + l16: a
+            // group of 16 keys is seen whole (16 kg + 15 <= rel), not at all (16 kg > rel + 15: its
+            // products and exponentials are skipped, P = 0), or in part (masked key by key)
+            const int rel = r0 - kbase;
+            f32x4_t s[4];
+#pragma unroll
+            for (int kg = 0; kg < 4; ++kg) {
+                s[kg] = f32x4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+                if (16 * kg > rel + 15) continue;
+                s[kg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kc = 0; kc < 2; ++kc) {
+                    const bf16x8_t a = as_bf16x8(*(const uint4 *)(ksb + u * kSlotB + kg * 16 * kRowB + kofs[kc]));
+                    s[kg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qb[j][kc], s[kg], 0, 0, 0);
+                }
+                if (16 * kg + 15 > rel) {
+                    const int lim = rel + l16 - 16 * kg - 4 * g; // the lane's keys r <= lim are seen
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (r > lim) s[kg][r] = -INFINITY;
+                }
+            }
+            float mx = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
+#pragma unroll
+            for (int kg = 1; kg < 4; ++kg)
+                mx = fmaxf(mx, fmaxf(fmaxf(s[kg][0], s[kg][1]), fmaxf(s[kg][2], s[kg][3])));
+            mx = fmaxf(mx, xor_lane<16>(mx));
+            mx = fmaxf(mx, xor_lane<32>(mx));
+            // lazy rescaling, as in decode: the row's sum and accumulators move to a new max only
+            // when some row of the wave saw its max grow by more than 8 (log2 units)
+            const float mn = fmaxf(m[j], mx * qmul);
+            if (__any(mn > m[j] + 8.f)) {
+                const float alpha = fast_exp2(m[j] - mn);
+                lsum[j] *= alpha;
+#pragma unroll
+                for (int dg = 0; dg < 4; ++dg)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) o[j][dg][r] *= alpha;
+                m[j] = mn;
+            }
+            const float mref = m[j];
+            float psum = 0.f;
+            uint32_t pk[4][2];
+#pragma unroll
+            for (int kg = 0; kg < 4; ++kg) {
+                pk[kg][0] = pk[kg][1] = 0u;
+                if (16 * kg > rel + 15) continue;
+                float p[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    p[r] = fast_exp2(__builtin_fmaf(s[kg][r], qmul, -mref));
+                    psum += p[r];
+                }
+                pk[kg][0] = pack_bf16(p[0], p[1]);
+                pk[kg][1] = pack_bf16(p[2], p[3]);
+            }
+            lsum[j] += psum;
+#pragma unroll
+            for (int kp = 0; kp < 2; ++kp) {
+                if (32 * kp > rel + 15) continue; // both groups unseen: P is 0
+                // k slots: keys 32 kp + 4 g .. +3 (elements 0-3) and 32 kp + 16 + 4 g .. +3 (4-7)
+                const bf16x8_t pb =
+                    as_bf16x8(make_uint4(pk[2 * kp][0], pk[2 * kp][1], pk[2 * kp + 1][0], pk[2 * kp + 1][1]));
+#pragma unroll
+                for (int dg = 0; dg < 4; ++dg) {
+                    // V^T: lane gets dim 16 dg + l16 of the same eight keys, by two transposed reads
+                    const char *vp = vsb + u * kSlotB + kp * 32 * kRowB + vofs[dg];
+                    const uint2 lo = lds_read_tr16((const uint16_t *)vp);
+                    const uint2 hi = lds_read_tr16((const uint16_t *)(vp + 16 * kRowB));
+                    const bf16x8_t a = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+                    o[j][dg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, o[j][dg], 0, 0, 0);
+                }
+            }
+        }
+        // the registers of chunk c take chunk c + DEPTH: issued after this chunk's products, so that
+        // they are not held through them
+        if constexpr (c + DEPTH < NC) issue(std::integral_constant<int, c + DEPTH>{});
+    };
+    // every chunk is staged, those past the keys too (clamped copies of the last key, never seen):
+    // then no load is still in flight into a register the code after the steps takes over
+    step(std::integral_constant<int, 0>{});
+    step(std::integral_constant<int, 1>{});
+    step(std::integral_constant<int, 2>{});
+    step(std::integral_constant<int, 3>{});
+    static_assert(NC == 4, "the steps above");
+    // the output after every chunk: a store issued between the chunks would make each later wait for
+    // a chunk's loads wait for it too (the wait counts every access issued after the load it needs)
+    if (tile[0] >= 0) store_tile(0);
+    if (tile[1] >= 0) store_tile(1);
+}
+
+#ifndef XNP_PF_DEPTH
+#define XNP_PF_DEPTH 4
+#endif
+
+template <bool FUSED>
+__global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4))) void k_prefill_fast(
+    PoolView pv, BatchView bv, int layer, const void *q, const void *knew, const void *vnew, void *out, float qmul) {
+    __shared__ __attribute__((aligned(16))) uint16_t ks[2][kPfKeys][kHeadDim]; // K of two chunks, [key][unit ^ pf_swz(key)]
+    __shared__ __attribute__((aligned(16))) uint16_t vs[2][kPfKeys][kHeadDim]; // V, likewise
+    __shared__ uint4 rp[kPfFastKeys / kPfKeys * 64 * kPfWaves];                // each thread's keys' RoPE rows
+    __shared__ int32_t spages[kPfFastKeys / kBlock];                            // the page of each block of keys
+    const int tl = xcd_tile(blockIdx.x, bv.n * pv.H);
+    const int h = tl % pv.H, b = tl / pv.H;
+    if (!FUSED || bv.plans[b].write_slot > 0)
+        prefill_fast_group<FUSED, true, XNP_PF_DEPTH>(pv, bv, layer, q, knew, vnew, out, qmul, b, h, ks, vs, rp, spages);
+    else
+        prefill_fast_group<FUSED, false, XNP_PF_DEPTH>(pv, bv, layer, q, knew, vnew, out, qmul, b, h, ks, vs, rp, spages);
+}
+
+// ---------------------------------------------------------------------------------------------
 // Windowed attention of a Mimi chunk on MFMA (bf16 window cache and activations),
 // transformer.rs:764-781: t query rows over a window cache of W rows (slot p mod W holds position
 // p) and the chunk's own rows, each row seeing the W keys up to itself, for chunks of any length.
@@ -990,6 +1306,12 @@ hipError_t launch_prefill_mfma(const PoolView &pv, const BatchView &bv, int laye
     if (window)
         XNP_LAUNCH(k_prefill_window, dim3(bv.n * pv.H), dim3(64 * kWpWaves), stream, tm, pv, bv, layer, q, k, v, out,
                    qmul);
+    else if (bv.kmax <= kPfFastKeys && fused)
+        XNP_LAUNCH(k_prefill_fast<true>, dim3(bv.n * pv.H), dim3(64 * kPfWaves), stream, tm, pv, bv, layer, q, k, v,
+                   out, qmul);
+    else if (bv.kmax <= kPfFastKeys)
+        XNP_LAUNCH(k_prefill_fast<false>, dim3(bv.n * pv.H), dim3(64 * kPfWaves), stream, tm, pv, bv, layer, q, k, v,
+                   out, qmul);
     else
         XNP_LAUNCH(k_prefill_mfma, dim3(bv.n * pv.H), dim3(64 * kPfWaves), stream, tm, pv, bv, layer, q, k, v, out,
                    qmul, fused ? 1 : 0);

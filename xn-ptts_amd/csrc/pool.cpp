@@ -1207,7 +1207,11 @@ extern "C" xnp_status xnp_batch_begin(xnp_pool *pool, const int32_t *ids, int32_
     // few CUs, so give each group more waves (a larger split only raises the pages a group can
     // index) until the batch has about one wave per SIMD
     B.bv.prefix = 0;
-    for (int32_t i = 0; i < n; i++) B.bv.prefix |= plans[i].prefix > 0;
+    B.bv.kmax = 0;
+    for (int32_t i = 0; i < n; i++) {
+        B.bv.prefix |= plans[i].prefix > 0;
+        B.bv.kmax = std::max(B.bv.kmax, plans[i].write_slot + t);
+    }
     B.bv.split = pool->split;
     if (!pool->d.decode_split && t == 1)
         B.bv.split = std::max(B.bv.split, decode_min_split(pool->view(), B.bv.prefix != 0));

@@ -68,6 +68,7 @@ struct BatchView {
     int32_t split;  // waves per (stream, head) work group
     int32_t prefix; // 1 if some stream of the batch is an absolute ring keeping a prefix
     int32_t wrow;   // a window step run row by row: the row this launch attends (-1 otherwise)
+    int32_t kmax;   // a prompt step (t > 1): the most key slots a stream of it attends, write_slot + t
 };
 
 // A table entry to set before the batch's kernels run.
