@@ -1379,6 +1379,30 @@ int orc_batch_commit(orc_stream **streams, int n) {
     return 0;
 }
 
+/* One single-row ring step on each of n streams, OpenMP across streams: evict slot drop[i] after
+ * prefix 0 when drop[i] >= 0, take slot set[i] for the next row, then append row i of k and v to
+ * `layer` (q null) or attend with row i of q as well (orc_attend, out row i), and commit the row.
+ * The per-stream calls of the s2s session loop (s2s.rs:324-333: evict, set_ring_slot, then the
+ * step) composed, for tests that mirror many streams. */
+int orc_batch_ring_step(orc_stream **streams, int n, int layer, const int *drop, const int *set, const float *q,
+                        const float *k, const float *v, float scale, float *out) {
+    if (n <= 0) return 0;
+    int H = streams[0]->H, KVH = streams[0]->KVH, D = streams[0]->D;
+    int bad = 0;
+#pragma omp parallel for schedule(dynamic, 16) reduction(| : bad)
+    for (int i = 0; i < n; i++) {
+        orc_stream *st = streams[i];
+        const float *ki = k + (size_t)i * KVH * D, *vi = v + (size_t)i * KVH * D;
+        if (drop[i] >= 0 && orc_evict(st, 0, &drop[i], 1)) { bad = 1; continue; }
+        if (orc_set_ring_slot(st, set[i])) { bad = 1; continue; }
+        const int rc = q ? orc_attend(st, layer, 1, q + (size_t)i * H * D, ki, vi, scale, out + (size_t)i * H * D, NULL)
+                         : orc_append(st, layer, 1, ki, vi);
+        if (rc) { bad = 1; continue; }
+        bad |= orc_commit(st, 1) != 0;
+    }
+    return bad ? fail("a stream refused the ring step") : 0;
+}
+
 void orc_set_threads(int n) {
 #ifdef _OPENMP
     omp_set_num_threads(n);

@@ -222,6 +222,11 @@ int orc_flow_q8_step(orc_flow_q8 *m, orc_stream *st, const float *latent_in, con
 int orc_batch_attend(orc_stream **streams, int n, int layer, const float *q, const float *k,
                      const float *v, float scale, float *out);
 int orc_batch_commit(orc_stream **streams, int n);
+/* Each stream i: evict slot drop[i] (if >= 0, prefix 0), set_ring_slot(set[i]), then append row i
+ * of k and v to `layer` (q null) or attend with row i of q (out row i), commit 1 (OpenMP over
+ * streams). */
+int orc_batch_ring_step(orc_stream **streams, int n, int layer, const int *drop, const int *set, const float *q,
+                        const float *k, const float *v, float scale, float *out);
 int orc_threads(void);
 void orc_set_threads(int n);
 

@@ -70,6 +70,8 @@ def lib():
             "orc_batch_attend": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int, ctypes.c_int,
                                                 _fp, _fp, _fp, ctypes.c_float, _fp]),
             "orc_batch_commit": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int]),
+            "orc_batch_ring_step": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int, ctypes.c_int,
+                                                   _ip, _ip, _fp, _fp, _fp, ctypes.c_float, _fp]),
             "orc_threads": (ctypes.c_int, []),
             "orc_set_threads": (None, [ctypes.c_int]),
             "orc_flow_lm_size": (ctypes.c_longlong, [ctypes.c_void_p]),
@@ -312,6 +314,27 @@ def batch_commit(streams):
     n = len(streams)
     arr = (ctypes.c_void_p * n)(*[s.h for s in streams])
     _ok(lib().orc_batch_commit(arr, n))
+
+
+def batch_ring_step(streams, layer, drop, slot, k, v, q=None, scale=0.125):
+    """Each stream i: evict slot drop[i] (if >= 0, prefix 0), take slot slot[i], then append row i of
+    k, v to `layer` (q None) or attend with row i of q as well, and commit the row (OpenMP across
+    streams).  Returns the attention outputs [n][H][D] when q is given."""
+    n = len(streams)
+    arr = (ctypes.c_void_p * n)(*[s.h for s in streams])
+    d = np.ascontiguousarray(drop, np.int32)
+    sl = np.ascontiguousarray(slot, np.int32)
+    k, kp = _f32(k)
+    v, vp = _f32(v)
+    out = None
+    if q is not None:
+        q, qp = _f32(q)
+        out = np.zeros_like(q)
+        op = out.ctypes.data_as(_fp)
+    else:
+        qp = op = None
+    _ok(lib().orc_batch_ring_step(arr, n, layer, d.ctypes.data_as(_ip), sl.ctypes.data_as(_ip), qp, kp, vp, scale, op))
+    return out
 
 
 def batch_commit_t(streams, t):

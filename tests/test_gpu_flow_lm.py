@@ -236,6 +236,41 @@ def test_q8_graph_is_recorded_again_when_a_stream_takes_up_a_ring_prefix():
     assert info["ring_shift"] == 12 and info["ring_prefix"] == P  # three evictions of 4 rows
 
 
+def test_q8_graph_is_recorded_again_when_the_rope_tables_grow():
+    # A pool whose RoPE tables start at 16 rows: the prompt and the frames reach positions past 16
+    # and then past 32, and each growth frees the tables a recorded frame's kernels read.  Replayed
+    # frames must still equal eager frames bit for bit: the growth changes the launch key, and the
+    # graph is recorded again against the new tables.
+    cfg = fl.FlowLMConfig(num_layers=2, flow_depth=2, flow_dim=512, dim_feedforward=1024, n_bins=100, precision="q8")
+    blob = fl.random_weights(cfg, 105, std=0.05, unit_norms=False)
+    rng = np.random.default_rng(106)
+    n, P, frames = 3, 6, 40
+    tokens = rng.integers(0, cfg.n_bins + 1, (n, P)).astype(np.int32)
+    s = torch.cuda.Stream()
+    runs = []
+    for _ in range(2):
+        pool = xnp.KvPool(num_layers=2, num_heads=8, num_blocks=24, max_streams=n, max_blocks_per_stream=4,
+                          cache_dtype="bf16", act_dtype="bf16", max_pos=16, page_seed=6)
+        ids = [pool.init_state(64) for _ in range(n)]
+        lm = xnp.FlowLM(pool, cfg, blob, max_rows=n * P)
+        with torch.cuda.stream(s):
+            lm.prompt_text(ids, tokens)
+        lat = torch.zeros((n, cfg.ldim), dtype=torch.float32, device=DEV)
+        eos = torch.zeros(n, dtype=torch.float32, device=DEV)
+        runs.append((pool, ids, lm, lat, eos))
+    noise = torch.zeros((n, cfg.ldim), dtype=torch.float32, device=DEV)
+    rows = []
+    for f in range(frames):
+        with torch.cuda.stream(s):
+            noise.copy_(torch.from_numpy((0.5 * rng.standard_normal((n, cfg.ldim))).astype(np.float32)).to(DEV))
+            for g, (pool, ids, lm, lat, eos) in enumerate(runs):
+                lm.step(ids, None if f == 0 else lat, noise, lat, eos, stream=s.cuda_stream, graph=(g == 1))
+        s.synchronize()
+        assert torch.equal(runs[0][3], runs[1][3]) and torch.equal(runs[0][4], runs[1][4]), f
+        rows.append(runs[1][0].stats()["rope_rows"])
+    assert rows[0] == 16 and rows[-1] >= 64 and len(set(rows)) >= 3  # grown twice while replaying
+
+
 def test_q8_refuses_an_f32_pool_and_odd_widths():
     cfg = fl.FlowLMConfig(num_layers=1, flow_depth=1, flow_dim=512, dim_feedforward=512, n_bins=10, precision="q8")
     blob = fl.random_weights(cfg, 101)

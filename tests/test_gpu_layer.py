@@ -150,10 +150,11 @@ def test_layer_steps_match_the_oracle(cache, KVH, ls, ff):
 def test_the_layer_step_configuration_at_full_size_spot_checked():
     # The layer-step workload at its full size: 2048 streams x 9 Phonon-40m layers (512 wide, 8 heads
     # x 64, FF 2048, int8 per-channel projections), bf16 caches of U[1,1500] rows loaded as KV, one
-    # single-row step through all 9 layers.  Every stream runs; 13 of them, spread over the lengths
-    # (the longest and the shortest included), go through the oracle's layer step on their own rows
-    # (a layer is per row, and per stream for attention), each layer from the GPU's input to it, so
-    # that every layer is held to the 2e-2 bar on its own.
+    # single-row step through all 9 layers.  Every stream runs, and every stream's layer 0 goes
+    # through the oracle's layer step on a one-layer cache of its own; 13 of them, spread over the
+    # lengths (the longest and the shortest included), go through the oracle's layer step on all 9
+    # layers (a layer is per row, and per stream for attention), each layer from the GPU's input to
+    # it, so that every layer is held to the 2e-2 bar on its own.
     S, L, H, D, dm, ff, cap = 2048, 9, 8, 64, 512, 2048, 1504
     rng = np.random.default_rng(20261205)
     W = [make_weights(rng, ff=ff) for _ in range(L)]
@@ -165,16 +166,22 @@ def test_the_layer_step_configuration_at_full_size_spot_checked():
                       cache_dtype="bf16", act_dtype="bf16", max_pos=2048, page_seed=19)
     ids = [pool.init_state(cap) for _ in range(S)]
     sts = {i: oracle.Stream(L, H, D, cap, cache="bf16", act="bf16") for i in sample}
+    every = [oracle.Stream(1, H, D, n + 2, cache="bf16", act="bf16") for n in lens.tolist()]
     g = torch.Generator(device=DEV).manual_seed(20261205)
     for i, n in enumerate(lens.tolist()):
         pool.advance(ids[i], n)
+        every[i].advance(n)
         if i in sts:
             sts[i].advance(n)
         for layer in range(L):
             kv = torch.randn((2, n, H, D), device=DEV, generator=g)
             pool.load_kv(ids[i], layer, kv)
-            if i in sts:
-                sts[i].load_kv(layer, host(kv))
+            if i in sts or layer == 0:
+                kvh = host(kv)
+                if layer == 0:
+                    every[i].load_kv(0, kvh)
+                if i in sts:
+                    sts[i].load_kv(layer, kvh)
         torch.cuda.synchronize()  # the staged rows are freed on the next iteration
     ws = torch.empty(pool.layer_workspace(S, dm, ff), dtype=torch.uint8, device=DEV)
     xg = dev(normal(rng, (S, 1, dm), "bf16"))
@@ -182,12 +189,19 @@ def test_the_layer_step_configuration_at_full_size_spot_checked():
     pool.begin(ids, t=1)
     for layer in range(L):
         torch.cuda.synchronize()
-        xin = host(xg)[sample]
+        xall = host(xg)
+        xin = xall[sample]
         pool.layer_step(layer, W[layer][1], xg, ws)
         want = oracle.layer_step(sub, layer, W[layer][0], xin)
         torch.cuda.synchronize()
-        got = host(xg)[sample]
+        gall = host(xg)
+        got = gall[sample]
         for j, i in enumerate(sample):
             assert rel_err(got[j], want[j]) <= TOL, (layer, i, int(lens[i]))
+        if layer == 0:  # every stream
+            wall = oracle.layer_step(every, 0, W[0][0], xall)
+            per = np.abs(gall - wall).max(axis=-1) / np.maximum(np.abs(wall).max(axis=-1), 1e-30)
+            worst = int(per.max(axis=-1).argmax())
+            assert per.max() <= TOL, (worst, int(lens[worst]), float(per.max()))
     pool.end()
     assert pool.check_tables() == 0

@@ -396,46 +396,62 @@ def test_window_caches_match_mimis_kv_cache(cache, act):
 def test_int8_window_cache_matches_the_ring_it_stands_for():
     # An int8 window has no counterpart in the reference; it is an absolute ring of `context`
     # slots whose every row evicts the oldest, so the oracle's ring driven that way is its bar:
-    # bit-exact codes and scales, outputs within 2e-2.  Single rows, then rows in pairs.
+    # bit-exact codes and scales, outputs within 2e-2.  Two windows of one batch with different
+    # histories (the second joins 17 rows later, so the held rows and the oldest slot differ
+    # within each launch): single rows, rows in pairs, steps of 5 rows and steps of 30 rows (more
+    # than the window holds: the later rows of a step overwrite the earlier ones, in the same
+    # pages, whose scales then requantize).
     L, H, context = 2, 8, 24
     pool = xnp.KvPool(num_layers=L, num_heads=H, num_blocks=16, max_streams=2, max_blocks_per_stream=2,
                       cache_dtype="i8", act_dtype="bf16", max_pos=4096, page_seed=4)
-    wid = pool.init_window(context)
-    st = oracle.Stream(L, H, 64, context, cache="i8", act="bf16")
-    st.start_ring("absolute", prefix=0)
+    wins = [pool.init_window(context) for _ in range(2)]
+    sts = [oracle.Stream(L, H, 64, context, cache="i8", act="bf16") for _ in range(2)]
+    for st in sts:
+        st.start_ring("absolute", prefix=0)
     rng = np.random.default_rng(51)
-    p = 0
-    for t in [1] * 50 + [2] * 12:
-        q, k, v = (bf16_round(rng.standard_normal((L, 1, t, H, 64)).astype(np.float32) * 2) for _ in range(3))
-        pool.begin([wid], t=t)
+    pos = [0, 0]
+
+    def check(j):
+        n = min(pos[j], context)
+        for layer in range(L):
+            for kv in (0, 1):
+                rows = torch.empty((n, H, 64), dtype=torch.int8, device=DEV)
+                nb = (n - 1) // 16 + 1
+                sc = torch.zeros((nb, H), dtype=torch.float32, device=DEV)
+                pool.read_rows(wins[j], layer, kv, 0, rows, sc)
+                torch.cuda.synchronize()
+                _, q8, osc = sts[j].read_rows(layer, kv, 0, n)
+                assert np.array_equal(rows.cpu().numpy(), q8), (j, pos[j], layer, kv)
+                assert np.array_equal(sc.cpu().numpy().view(np.uint32), osc.view(np.uint32)), (j, pos[j], layer, kv)
+
+    steps = [((0,), 1)] * 17 + [((0, 1), 1)] * 40 + [((0, 1), 2)] * 12 + [((0, 1), 5)] * 6 + [((0, 1), 30)] * 3 \
+        + [((1,), 5)] + [((0, 1), 1)] * 5
+    for which, t in steps:
+        q, k, v = (bf16_round(rng.standard_normal((L, len(which), t, H, 64)).astype(np.float32) * 2) for _ in range(3))
+        pool.begin([wins[j] for j in which], t=t)
         got = []
         for layer in range(L):
-            out = torch.empty((1, t, H, 64), dtype=torch.bfloat16, device=DEV)
+            out = torch.empty((len(which), t, H, 64), dtype=torch.bfloat16, device=DEV)
             pool.attend(layer, dev(q[layer], "bf16"), dev(k[layer], "bf16"), dev(v[layer], "bf16"), out, 0.125)
             torch.cuda.synchronize()
             got.append(host(out))
         pool.end()
-        for i in range(t):  # the oracle's ring, one row at a time over every layer
-            if st.ring_info()["filled"] == context:
-                st.evict(0, [p % context])
-            st.set_ring_slot(p % context)
-            for layer in range(L):
-                want, _ = st.attend(layer, q[layer][0, i:i + 1], k[layer][0, i:i + 1], v[layer][0, i:i + 1])
-                assert rel_err(got[layer][0, i:i + 1], want) <= TOL["i8"], (p, layer)
-            st.commit(1)
-            p += 1
-        if p % 7 == 0 or t == 2:
-            n = min(p, context)
-            for layer in range(L):
-                for kv in (0, 1):
-                    rows = torch.empty((n, H, 64), dtype=torch.int8, device=DEV)
-                    nb = (n - 1) // 16 + 1
-                    sc = torch.zeros((nb, H), dtype=torch.float32, device=DEV)
-                    pool.read_rows(wid, layer, kv, 0, rows, sc)
-                    torch.cuda.synchronize()
-                    _, q8, osc = st.read_rows(layer, kv, 0, n)
-                    assert np.array_equal(rows.cpu().numpy(), q8), (p, layer, kv)
-                    assert np.array_equal(sc.cpu().numpy().view(np.uint32), osc.view(np.uint32)), (p, layer, kv)
+        for b, j in enumerate(which):
+            st = sts[j]
+            for i in range(t):  # the oracle's ring, one row at a time over every layer
+                if st.ring_info()["filled"] == context:
+                    st.evict(0, [pos[j] % context])
+                st.set_ring_slot(pos[j] % context)
+                for layer in range(L):
+                    want, _ = st.attend(layer, q[layer][b, i:i + 1], k[layer][b, i:i + 1], v[layer][b, i:i + 1])
+                    assert rel_err(got[layer][b, i:i + 1], want) <= TOL["i8"], (j, pos[j], layer)
+                st.commit(1)
+                pos[j] += 1
+            if pos[j] % 7 == 0 or t > 1:
+                check(j)
+    assert pos == [17 + 40 + 24 + 30 + 90 + 5, 40 + 24 + 30 + 90 + 5 + 5]
+    for j in range(2):
+        check(j)
 
 
 @pytest.mark.parametrize("cache,act,kvh", [("bf16", "bf16", 8), ("bf16", "bf16", 2), ("f32", "f32", 8)])
@@ -456,29 +472,33 @@ def test_a_long_mimi_chunk_matches_the_kv_cache(cache, act, kvh):
     orcs = [oracle.Window(L, H, 64, context, rows_max=300, act=act) for _ in range(2)]
     rng = np.random.default_rng(53 + kvh)
 
-    def step(t):
-        pool.begin(ids, t=t)
+    def step(t, which=(0, 1)):
+        n = len(which)
+        pool.begin([ids[j] for j in which], t=t)
         for layer in range(L):
-            q = rng.standard_normal((2, t, H, 64)).astype(np.float32)
-            k = rng.standard_normal((2, t, kvh, 64)).astype(np.float32)
-            v = rng.standard_normal((2, t, kvh, 64)).astype(np.float32)
+            q = rng.standard_normal((n, t, H, 64)).astype(np.float32)
+            k = rng.standard_normal((n, t, kvh, 64)).astype(np.float32)
+            v = rng.standard_normal((n, t, kvh, 64)).astype(np.float32)
             if act == "bf16":
                 q, k, v = bf16_round(q), bf16_round(k), bf16_round(v)
-            out = torch.empty((2, t, H, 64), dtype=TORCH_DT[act], device=DEV)
+            out = torch.empty((n, t, H, 64), dtype=TORCH_DT[act], device=DEV)
             pool.attend(layer, dev(q, act), dev(k, act), dev(v, act), out, 0.125)
             torch.cuda.synchronize()
             got = host(out)
-            for j in range(2):
-                want, _ = orcs[j].attend(layer, q[j], np.repeat(k[j], G, axis=1), np.repeat(v[j], G, axis=1))
-                assert rel_err(got[j], want) <= TOL[cache], (t, layer, j)
+            for b, j in enumerate(which):
+                want, _ = orcs[j].attend(layer, q[b], np.repeat(k[b], G, axis=1), np.repeat(v[b], G, axis=1))
+                assert rel_err(got[b], want) <= TOL[cache], (t, layer, j)
         pool.end()
-        for o in orcs:
-            o.commit(t)
+        for j in which:
+            orcs[j].commit(t)
 
+    # window 0 takes a 37-row chunk of its own first: every later launch holds two windows with
+    # different held rows and different oldest slots
+    step(37, which=(0,))
     for t in [300] + [1] * 40 + [2] * 10 + [100]:
         step(t)
     for j in range(2):
-        assert orcs[j].offset == 460 and pool.current_end(ids[j]) == context
+        assert orcs[j].offset == 460 + (37 if j == 0 else 0) and pool.current_end(ids[j]) == context
         win = orcs[j]
         for layer in range(L):
             for kv in (0, 1):
@@ -760,9 +780,11 @@ def test_the_int8_window_configuration_at_full_size_spot_checked():
     # pages with a scale per (page, head), window 512 on 528-slot absolute rings, write heads
     # U[0,4096), histories of U[64,2048] rows as the workload draws them (the long ones wrap their
     # ring four times, each page's scale only growing once the ring has wrapped), each row through
-    # the batched append with one slide per step, then two attend steps.  10 streams spread over the
-    # lengths (the longest and the shortest included) are mirrored on the oracle: outputs within
-    # 2e-2, then every live cache row, code and scale bit-exact.
+    # the batched append with one slide per step, then two attend steps.  Layer 0 of every stream is
+    # mirrored on a one-layer oracle ring of its own (outputs of both attend steps within 2e-2, then
+    # every live code and scale of one stream in 64 bit-exact); 10 streams spread over the lengths
+    # (the longest and the shortest included) are mirrored on all 9 layers: outputs within 2e-2,
+    # then every live cache row, code and scale bit-exact.
     S, L, H, SPAN, WIN = 1024, 9, 8, 528, 512
     rng = np.random.default_rng(20261204)
     heads = rng.integers(0, 4096, S)
@@ -779,6 +801,18 @@ def test_the_int8_window_configuration_at_full_size_spot_checked():
     for i in sample:
         orc[i].start_ring("absolute", prefix=0)
     in_view = {i: 0 for i in sample}
+    every = [oracle.Stream(1, H, 64, SPAN, cache="i8", act="bf16") for _ in range(S)]
+    for st in every:
+        st.start_ring("absolute", prefix=0)
+    every_view = np.zeros(S, np.int64)
+
+    def every_step(act, k, v, q=None):  # slide, then append (or attend) row j on layer 0 of stream act[j]
+        pos = heads[act] + written[act]
+        drop = np.where(every_view[act] == WIN, (pos - WIN) % SPAN, -1)
+        out = oracle.batch_ring_step([every[i] for i in act], 0, drop, pos % SPAN, k, v, q=q)
+        every_view[act] = np.minimum(every_view[act] + 1, WIN)
+        return out
+
     written = np.zeros(S, np.int64)
     g = torch.Generator(device=DEV).manual_seed(20261204)
 
@@ -803,6 +837,7 @@ def test_the_int8_window_configuration_at_full_size_spot_checked():
         for layer in range(L):
             pool.append(layer, kv[2 * layer][:len(act)], kv[2 * layer + 1][:len(act)])
         pool.end()
+        every_step(act, kvh[0][:len(act)], kvh[1][:len(act)])
         for i in sample:
             if start[i] <= s:
                 slide(i)
@@ -813,6 +848,7 @@ def test_the_int8_window_configuration_at_full_size_spot_checked():
                 in_view[i] += 1
         written[act] += 1
     torch.cuda.synchronize()
+    everyone = np.arange(S)
     for _ in range(2):
         pool.slide_batch(ids, 0, SPAN, WIN, 1, heads + written)
         for i in sample:
@@ -823,6 +859,11 @@ def test_the_int8_window_configuration_at_full_size_spot_checked():
             out = torch.empty((S, H, 64), dtype=torch.bfloat16, device=DEV)
             pool.attend(layer, q, k, v, out, 0.125)
             torch.cuda.synchronize()
+            if layer == 0:  # every stream
+                want = every_step(everyone, host(k), host(v), q=host(q))
+                per = np.abs(host(out) - want).max(axis=-1) / np.maximum(np.abs(want).max(axis=-1), 1e-30)
+                worst = int(per.max(axis=-1).argmax())
+                assert per.max() <= 2e-2, (worst, int(lens[worst]), float(per.max()))
             got, qh, kh, vh = host(out[sample]), host(q[sample]), host(k[sample]), host(v[sample])
             for j, i in enumerate(sample):
                 want, _ = orc[i].attend(layer, qh[j:j + 1], kh[j:j + 1], vh[j:j + 1])
@@ -848,6 +889,22 @@ def test_the_int8_window_configuration_at_full_size_spot_checked():
                     _, q8, osc = orc[i].read_rows(layer, kvi, 16 * pg, 16)
                     assert np.array_equal(rows.cpu().numpy()[live], q8[live]), (i, pg, layer, kvi)
                     assert np.array_equal(sc.cpu().numpy().view(np.uint32), osc.view(np.uint32)), (i, pg, layer, kvi)
+    # layer 0 of one stream in 64 (besides the sample), every live slot's code and every live
+    # page's scale against its one-layer oracle ring
+    for i in range(0, S, 64):
+        valid = every[i].ring_info()["valid"]
+        for pg in range(mbps):  # only the pages the ring has written exist
+            live = valid[16 * pg:16 * pg + 16]
+            if not live.any():
+                continue
+            for kvi in (0, 1):
+                rows = torch.empty((16, H, 64), dtype=torch.int8, device=DEV)
+                sc = torch.zeros((1, H), dtype=torch.float32, device=DEV)
+                pool.read_rows(ids[i], 0, kvi, 16 * pg, rows, sc)
+                torch.cuda.synchronize()
+                _, q8, osc = every[i].read_rows(0, kvi, 16 * pg, 16)
+                assert np.array_equal(rows.cpu().numpy()[live], q8[live]), (i, pg, kvi)
+                assert np.array_equal(sc.cpu().numpy().view(np.uint32), osc.view(np.uint32)), (i, pg, kvi)
     assert pool.check_tables() == 0
 
 
@@ -923,9 +980,10 @@ def test_many_streams_at_the_config2_length_distribution(split):
 def test_the_decode_configuration_at_full_size_spot_checked():
     # The batched decode workload at its full size: 1024 streams x 9 layers x 8 heads x 64, bf16
     # pages of 16 on shuffled block tables, cache lengths U[1, 1024], the library's own split.
-    # Every stream runs; 18 of them, spread over the longest-first order (the longest and the
-    # shortest included), are checked against the oracle over two steps: outputs within 2e-2,
-    # then every cache row bit-exact.
+    # Every stream runs, and every stream's layer 0 is held to a one-layer oracle of its own over
+    # both steps (outputs within 2e-2); 18 of them, spread over the longest-first order (the
+    # longest and the shortest included), are checked on all 9 layers: outputs within 2e-2, then
+    # every cache row bit-exact.
     S, L, H, cap = 1024, 9, 8, 1040
     rng = np.random.default_rng(20261203)
     lens = rng.integers(1, 1025, S)
@@ -936,6 +994,7 @@ def test_the_decode_configuration_at_full_size_spot_checked():
                       cache_dtype="bf16", act_dtype="bf16", max_pos=8192, page_seed=13)
     ids = [pool.init_state(cap) for _ in range(S)]
     orc = {i: oracle.Stream(L, H, 64, cap, cache="bf16", act="bf16") for i in sample}
+    every = [oracle.Stream(1, H, 64, n + 4, cache="bf16", act="bf16") for n in lens.tolist()]
     g = torch.Generator(device=DEV).manual_seed(20261203)
 
     def randn(*shape):
@@ -944,13 +1003,18 @@ def test_the_decode_configuration_at_full_size_spot_checked():
     for i, n in enumerate(lens.tolist()):
         # each stream's history through the voice load (f32 rows rounded to bf16 on the device)
         pool.advance(ids[i], n)
+        every[i].advance(n)
         if i in orc:
             orc[i].advance(n)
         for layer in range(L):
             kv = torch.randn((2, n, H, 64), device=DEV, generator=g)
             pool.load_kv(ids[i], layer, kv)
-            if i in orc:
-                orc[i].load_kv(layer, host(kv))
+            if i in orc or layer == 0:
+                kvh = host(kv)
+                if layer == 0:
+                    every[i].load_kv(0, kvh)
+                if i in orc:
+                    orc[i].load_kv(layer, kvh)
         torch.cuda.synchronize()  # the staged rows are freed on the next iteration
     for _ in range(2):
         pool.begin(ids)
@@ -959,11 +1023,18 @@ def test_the_decode_configuration_at_full_size_spot_checked():
             out = torch.empty((S, H, 64), dtype=torch.bfloat16, device=DEV)
             pool.attend(layer, q, k, v, out, 0.125)
             torch.cuda.synchronize()
+            if layer == 0:  # every stream
+                want = oracle.batch_attend(every, 0, host(q), host(k), host(v))
+                got_all = host(out)
+                per = np.abs(got_all - want).max(axis=-1) / np.maximum(np.abs(want).max(axis=-1), 1e-30)
+                worst = int(per.max(axis=-1).argmax())
+                assert per.max() <= 2e-2, (worst, int(lens[worst]), float(per.max()))
             got, qh, kh, vh = host(out[sample]), host(q[sample]), host(k[sample]), host(v[sample])
             for j, i in enumerate(sample):
                 want, _ = orc[i].attend(layer, qh[j:j + 1], kh[j:j + 1], vh[j:j + 1])
                 assert rel_err(got[j:j + 1], want) <= 2e-2, (layer, i, int(lens[i]))
         pool.end()
+        oracle.batch_commit(every)
         for i in sample:
             orc[i].commit(1)
     shim = types.SimpleNamespace(pool=pool, ids=ids, orc=orc, L=L, H=H, KVH=H, cache="bf16")

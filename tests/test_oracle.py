@@ -315,6 +315,46 @@ def test_absolute_ring_equals_shifting_ring():
     assert st["shift"].current_end == st["absolute"].current_end
 
 
+def test_the_batched_ring_step_is_its_per_stream_calls():
+    # orc_batch_ring_step composes evict, set_ring_slot, append or attend, and commit: the same
+    # outputs and cache bytes as those calls made stream by stream (int8 absolute rings on a
+    # 20-slot window of 24 slots, heads at different offsets, 70 steps, the last 5 attending).
+    rng = np.random.default_rng(31)
+    S, H, D, span, win = 5, 2, 64, 24, 20
+    heads = rng.integers(0, 100, S)
+    one = [oracle.Stream(1, H, D, span, cache="i8", act="bf16") for _ in range(S)]
+    bat = [oracle.Stream(1, H, D, span, cache="i8", act="bf16") for _ in range(S)]
+    for st in one + bat:
+        st.start_ring("absolute", prefix=0)
+    in_view = np.zeros(S, np.int64)
+    for step in range(70):
+        pos = heads + step
+        drop = np.where(in_view == win, (pos - win) % span, -1)
+        k, v, q = (bf16_round(rng.standard_normal((S, H, D))) for _ in range(3))
+        attend = step >= 65
+        want = []
+        for i, st in enumerate(one):
+            if drop[i] >= 0:
+                st.evict(0, [int(drop[i])])
+            st.set_ring_slot(int(pos[i] % span))
+            if attend:
+                want.append(st.attend(0, q[i:i + 1], k[i:i + 1], v[i:i + 1])[0][0])
+            else:
+                st.append(0, k[i:i + 1], v[i:i + 1])
+            st.commit(1)
+        got = oracle.batch_ring_step(bat, 0, drop, pos % span, k, v, q=q if attend else None)
+        if attend:
+            assert np.array_equal(got, np.stack(want))
+        in_view = np.minimum(in_view + 1, win)
+    for a, b in zip(one, bat):
+        assert a.ring_info()["write"] == b.ring_info()["write"]
+        assert np.array_equal(a.ring_info()["valid"], b.ring_info()["valid"])
+        for kv in (0, 1):
+            va, qa, sa = a.read_rows(0, kv, 0, span)
+            vb, qb, sb = b.read_rows(0, kv, 0, span)
+            assert np.array_equal(qa, qb) and np.array_equal(sa.view(np.uint32), sb.view(np.uint32))
+
+
 def test_misuse_of_a_ring_is_refused():
     st = oracle.Stream(1, 4, 64, 8)
     st.attend(0, rows(4, 0.0), rows(4, 0.1), rows(4, 0.2))

@@ -105,3 +105,38 @@ def test_a_step_too_large_for_the_static_scratch_is_refused_and_changes_nothing(
     torch.cuda.synchronize()
     assert torch.equal(x.view(torch.int16), before.view(torch.int16))
     assert all(pool.info(i)["current_end"] == 0 for i in ids)
+
+
+def test_a_call_on_another_stream_is_refused_while_the_last_one_may_still_run():
+    # One array per device: pool b's call on HIP stream B, made while pool a's call on stream A is
+    # still queued behind a sleep, is refused (XNP_E_STATE) and runs nothing; once A's work is done,
+    # B takes the array over, and its step equals the workspace step of a third, identical pool.
+    rng = np.random.default_rng(20261209)
+    W = [weights(rng) for _ in range(L)]
+    S, cap = 8, 64
+    a, b, c = make_pool(S, cap), make_pool(S, cap), make_pool(S, cap)
+    ia, ib, ic = ([p.init_state(cap) for _ in range(S)] for p in (a, b, c))
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    xa = dev(normal(rng, (S, 1, DM), "bf16"))
+    x0 = normal(rng, (S, 1, DM), "bf16")
+    xb, xc = dev(x0), dev(x0)
+    torch.cuda.synchronize()
+    a.begin(ia, t=1, stream=sa.cuda_stream)
+    with torch.cuda.stream(sa):
+        torch.cuda._sleep(50_000_000)  # a bounded spin that keeps stream A busy for a while
+    a.layer_step_static(0, W[0], xa)  # queued behind the spin
+    b.begin(ib, t=1, stream=sb.cuda_stream)
+    with pytest.raises(xnp.XnpError) as e:
+        b.layer_step_static(0, W[0], xb)
+    assert e.value.name == "XNP_E_STATE" and "another HIP stream" in e.value.message
+    torch.cuda.synchronize()
+    assert torch.equal(xb.view(torch.int16), dev(x0).view(torch.int16))  # nothing ran on B
+    b.layer_step_static(0, W[0], xb)  # A's work is done: B takes the array over
+    a.end()
+    b.end()
+    ws = torch.empty(c.layer_workspace(S, DM, FF), dtype=torch.uint8, device=DEV)
+    c.begin(ic, t=1)
+    c.layer_step(0, W[0], xc, ws)
+    c.end()
+    torch.cuda.synchronize()
+    assert torch.equal(xb.view(torch.int16), xc.view(torch.int16))

@@ -190,10 +190,16 @@ struct xnp_pool {
         return p;
     }
 
+    // Holders of page p; 0 for no page (-1) or an id outside the pool (only xnp_debug_set_block,
+    // on a host-only pool, can plant one): no path indexes the page counts with such an id.
+    int32_t refs(int32_t p) const { return p >= 0 && p < d.num_blocks ? refcnt[p] : 0; }
+
     void drop_page(int32_t sid, int32_t blk) {
         int32_t p = streams[sid].blocks[blk];
         if (p < 0) return;
-        if (--refcnt[p] == 0) free_pages.push_back(p);
+        // an id outside the pool (only xnp_debug_set_block can plant one) is cleared without
+        // touching the page counts
+        if (p < d.num_blocks && --refcnt[p] == 0) free_pages.push_back(p);
         streams[sid].blocks[blk] = -1;
         patches.push_back({sid, blk, -1, 0});
     }
@@ -323,11 +329,19 @@ struct xnp_pool {
                 rope_host.resize(old);
                 return st;
             }
-            HIP_TRY(hipFree(rope), "freeing the old rope table");
-            if (rope16) HIP_TRY(hipFree(rope16), "freeing the old bf16 rope table");
+            // the pool takes the new tables whole before the old ones go: a failed free below then
+            // leaves a consistent pool (the new tables in use) and reports the failure
+            float2 *old_rope = rope;
+            uint32_t *old_rope16 = rope16;
             device_bytes += (int64_t)((rope_host.size() - old) * (sizeof(float2) + (rope16 ? sizeof(uint32_t) : 0)));
             rope = nr;
             rope16 = n16;
+            rope_rows = (int32_t)rows;
+            const hipError_t e1 = hipFree(old_rope);
+            const hipError_t e2 = old_rope16 ? hipFree(old_rope16) : hipSuccess;
+            if (e1 != hipSuccess) return hip_fail(e1, "freeing the old rope table");
+            if (e2 != hipSuccess) return hip_fail(e2, "freeing the old bf16 rope table");
+            return XNP_OK;
         }
         rope_rows = (int32_t)rows;
         return XNP_OK;
@@ -338,14 +352,14 @@ struct xnp_pool {
         Stream &s = streams[sid];
         int need = 0;
         for (int32_t p : s.blocks)
-            if (p >= 0 && refcnt[p] > 1) need++;
+            if (refs(p) > 1) need++;
         if (need > (int)free_pages.size())
             return fail(XNP_E_OUT_OF_BLOCKS, "out of blocks: %d needed to unshare, %d free", need,
                         (int)free_pages.size());
         std::vector<std::pair<int32_t, int32_t>> copies;
         for (size_t b = 0; b < s.blocks.size(); b++) {
             int32_t p = s.blocks[b];
-            if (p < 0 || refcnt[p] <= 1) continue;
+            if (refs(p) <= 1) continue;
             refcnt[p]--;
             int32_t q = take_page(sid, (int32_t)b);
             copies.push_back({p, q});
@@ -724,7 +738,7 @@ extern "C" xnp_status xnp_stream_fork(xnp_pool *pool, int32_t src, int32_t capac
     for (int32_t b = 0; b < full; b++) {
         int32_t p = s->blocks[b];
         t.blocks[b] = p;
-        pool->refcnt[p]++;
+        if (pool->refs(p) > 0) pool->refcnt[p]++;
         pool->patches.push_back({dst, b, p, 0});
     }
     if (tail) {
@@ -756,7 +770,7 @@ extern "C" xnp_status xnp_stream_info_get(const xnp_pool *pool, int32_t id, xnp_
     for (int32_t p : s->blocks)
         if (p >= 0) {
             blocks++;
-            shared += pool->refcnt[p] > 1;
+            shared += pool->refs(p) > 1;
         }
     out->in_view = in_view;
     out->blocks = blocks;
@@ -821,12 +835,12 @@ static xnp_status own_pages(xnp_pool *pool, int32_t id, int32_t slot0, int32_t n
     Stream &s = pool->streams[id];
     const int32_t b0 = slot0 / kBlock, b1 = (slot0 + n - 1) / kBlock + 1;
     int need = 0;
-    for (int32_t b = b0; b < b1; b++) need += pool->refcnt[s.blocks[b]] > 1;
+    for (int32_t b = b0; b < b1; b++) need += pool->refs(s.blocks[b]) > 1;
     if (need > (int)pool->free_pages.size())
         return fail(XNP_E_OUT_OF_BLOCKS, "out of blocks: %d needed to copy shared pages", need);
     for (int32_t b = b0; b < b1; b++) {
         int32_t p = s.blocks[b];
-        if (pool->refcnt[p] <= 1) continue;
+        if (pool->refs(p) <= 1) continue;
         pool->refcnt[p]--;
         int32_t q = pool->take_page(id, b);
         HIP_TRY(launch_copy_page(pool->view(), p, q, hs), "page copy");
@@ -1636,5 +1650,20 @@ extern "C" xnp_status xnp_layer_step_static(xnp_pool *pool, int32_t layer, const
             return fail(XNP_E_INVALID, "the step of %lld rows needs %llu bytes of scratch; the static scratch holds %llu",
                         (long long)rows, (unsigned long long)need, (unsigned long long)kStaticScratchBytes);
     }
-    return layer_step_impl(pool, layer, w, x, scr, kStaticScratchBytes, hip_stream);
+    // one user of the device's array at a time: a call on another stream than the last one waits for
+    // nothing and is refused while that call's work may still be running
+    hipStream_t hs = (hipStream_t)hip_stream;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    HIP_TRY(hipStreamIsCapturing(hs, &cap), "hipStreamIsCapturing");
+    const bool capturing = cap != hipStreamCaptureStatusNone;
+    switch (static_scratch_claim(pool->d.device, hs, capturing)) {
+    case ScratchClaim::kOk: break;
+    case ScratchClaim::kBusy:
+        return fail(XNP_E_STATE, "the static scratch of device %d is in use by a call on another HIP stream that has not "
+                                 "finished; synchronize with it or call on the same stream", pool->d.device);
+    default: return fail(XNP_E_STATE, "the static scratch of device %d cannot be claimed", pool->d.device);
+    }
+    if (xnp_status st = layer_step_impl(pool, layer, w, x, scr, kStaticScratchBytes, hip_stream)) return st;
+    HIP_TRY(static_scratch_release(pool->d.device, hs, capturing), "recording the static scratch's last use");
+    return XNP_OK;
 }

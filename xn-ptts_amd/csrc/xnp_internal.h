@@ -92,6 +92,13 @@ struct LaunchTiming {
 constexpr uint64_t kStaticScratchBytes = XNP_STATIC_SCRATCH_BYTES;
 hipError_t static_scratch_init(int device);
 void *static_scratch(int device);
+// Calls on one device's array from different streams must not overlap.  claim: kOk when the last
+// call was on `stream`, or its work (on another stream) has finished, or the call is being captured
+// (a graph's order is its own); kBusy while another stream's call may still be using the array.
+// release: after the call's launches, record its completion on `stream` (nothing when capturing).
+enum class ScratchClaim { kOk, kBusy, kError };
+ScratchClaim static_scratch_claim(int device, hipStream_t stream, bool capturing);
+hipError_t static_scratch_release(int device, hipStream_t stream, bool capturing);
 
 // What the open batch's kernel launches are chosen by beyond its size and the caller's buffers: the
 // decode template (a ring prefix in the batch), the waves per work group, and the RoPE tables the
