@@ -39,3 +39,29 @@ def rel_err(got, want) -> float:
     num = np.abs(got - want).max(axis=-1)
     den = np.maximum(np.abs(want).max(axis=-1), 1e-30)
     return float((num / den).max())
+
+
+def rope_f64(x, pos, theta=10000.0):
+    """x [n][H][64] rotated at positions pos [n] in f64, pairs (2i, 2i + 1) by pos / theta^(i / 32)
+    (rope.rs:44-58, 74-95, with exact angles)."""
+    x = np.asarray(x, np.float64)
+    inv = theta ** (-np.arange(32, dtype=np.float64) / 32.0)
+    ang = np.asarray(pos, np.float64)[:, None] * inv[None, :]
+    c, s_ = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    x0, x1 = x[..., 0::2], x[..., 1::2]
+    out = np.empty_like(x)
+    out[..., 0::2] = x0 * c - x1 * s_
+    out[..., 1::2] = x0 * s_ + x1 * c
+    return out
+
+
+def exact_attend(q, keys, vals, scale=0.125):
+    """One query row [H][64] over the rows of a sequence (keys and values [n][H][64], before RoPE,
+    at positions 0 .. n - 1; the query at n - 1), in f64: the mathematics every mode approximates."""
+    n = keys.shape[0]
+    qr = rope_f64(q[None], [n - 1])[0]
+    kr = rope_f64(keys, np.arange(n))
+    sc = np.einsum("hd,nhd->hn", qr, kr) * scale
+    w = np.exp(sc - sc.max(axis=1, keepdims=True))
+    w /= w.sum(axis=1, keepdims=True)
+    return np.einsum("hn,nhd->hd", w, np.asarray(vals, np.float64))

@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from conftest import oracle
-from helpers import bf16_round, lcg, normal, rel_err
+from helpers import bf16_round, exact_attend, lcg, normal, rel_err
 
 THETA = 10000.0
 
@@ -353,6 +353,35 @@ def test_the_batched_ring_step_is_its_per_stream_calls():
             va, qa, sa = a.read_rows(0, kv, 0, span)
             vb, qb, sb = b.read_rows(0, kv, 0, span)
             assert np.array_equal(qa, qb) and np.array_equal(sa.view(np.uint32), sb.view(np.uint32))
+
+
+def test_a_shifting_ring_in_f32_is_the_exact_sequence_without_the_evicted_rows():
+    # The invariant of transformer.rs:1359-1395, against exact arithmetic: an f32 shifting ring run
+    # by the s2s policy (a 7-row prefix, a context of 24 slots, the oldest 8 evicted when full) gives
+    # at every frame the f64 attention of the query over the kept rows at their compacted positions
+    # (exact_attend, RoPE in f64 from the inputs), to f32 rounding; 100 frames.
+    rng = np.random.default_rng(41)
+    H, D, pre, context, drop = 4, 64, 7, 24, 8
+    st = oracle.Stream(1, H, D, pre + context)
+    keys, vals = rng.standard_normal((pre, H, D)).astype(np.float32), rng.standard_normal((pre, H, D)).astype(np.float32)
+    st.append(0, keys, vals)
+    st.commit(pre)
+    st.start_ring("shift", prefix=pre)
+    in_view, worst = 0, 0.0
+    for step in range(100):
+        if in_view == context:
+            oldest = step - in_view
+            st.evict(pre, [pre + (oldest + j) % context for j in range(drop)])
+            keys, vals = np.concatenate([keys[:pre], keys[pre + drop:]]), np.concatenate([vals[:pre], vals[pre + drop:]])
+            in_view -= drop
+        st.set_ring_slot(pre + step % context)
+        q, k, v = (rng.standard_normal((1, H, D)).astype(np.float32) for _ in range(3))
+        out, _ = st.attend(0, q, k, v)
+        st.commit(1)
+        in_view += 1
+        keys, vals = np.concatenate([keys, k]), np.concatenate([vals, v])
+        worst = max(worst, rel_err(out, exact_attend(q[0], keys, vals)[None]))
+    assert worst <= 2e-5, worst
 
 
 def test_misuse_of_a_ring_is_refused():
