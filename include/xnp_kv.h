@@ -321,18 +321,20 @@ xnp_status xnp_layer_norm(const void *x, int32_t rows, int32_t dim, const float 
 typedef enum xnp_epilogue {
     XNP_EPI_STORE = 0, XNP_EPI_GELU_ERF = 1, XNP_EPI_GELU_TANH = 2, XNP_EPI_RESIDUAL = 3,
     /* the flow net's (xnp_flow_linear_q8 only) */
-    XNP_EPI_SILU = 4, XNP_EPI_SILU_ADD = 5, XNP_EPI_GATED = 6, XNP_EPI_AXPY_F32 = 7, XNP_EPI_STORE_F32 = 8
+    XNP_EPI_SILU = 4, XNP_EPI_SILU_ADD = 5, XNP_EPI_GATED = 6, XNP_EPI_AXPY_F32 = 7, XNP_EPI_STORE_F32 = 8,
+    XNP_EPI_ADD_F32 = 9
 } xnp_epilogue;
 xnp_status xnp_linear_q8(const void *x, int32_t rows, int32_t k, const int8_t *w, const float *s,
                          int32_t n, int32_t epilogue, void *y, const float *ls, void *hip_stream);
 /* The flow net's pieces (SimpleMLPAdaLN, mlp.rs:4-11,113-163), as the q8 flow LM runs them:
  * y = bf16(s[j] * sum_k x[m][k] w[j][k] (+ bias[j])) for x [rows][k] bf16 (x_f32: f32, rounded to
- * bf16 as it is read; XNP_EPI_STORE only), w [n][k] int8, any n, k a multiple of 16, then
- * XNP_EPI_STORE y; _GELU_* gelu(y); _RESIDUAL y += y; _SILU silu(y); _SILU_ADD silu(bf16(y +
+ * bf16 as it is read; XNP_EPI_STORE and _ADD_F32 only), w [n][k] int8, any n, k a multiple of 16,
+ * then XNP_EPI_STORE y; _GELU_* gelu(y); _RESIDUAL y += y; _SILU silu(y); _SILU_ADD silu(bf16(y +
  * aux[j])) (aux f32 [n], the time embedding); _GATED y[m][j] = bf16(y[m][j] + bf16(aux[m][j] *
  * y)) (aux bf16, the AdaLN gate); _AXPY_F32 y[m][j] = bf16(bf16(aux[m][j]) + bf16(y * alpha)) (aux
- * and y f32: the solver step); _STORE_F32 y (f32).  Every result rounded to bf16 once; y rows of
- * stride ldy, aux rows of stride ld_aux. */
+ * and y f32: the solver step); _STORE_F32 y (f32); _ADD_F32 y[m][j] = bf16(bf16(aux[m][j]) + y)
+ * (aux f32, ld_aux 0 for one row for every m: the flow LM's conditions, flow_lm.rs:304-307).  Every
+ * result rounded to bf16 once; y rows of stride ldy, aux rows of stride ld_aux. */
 xnp_status xnp_flow_linear_q8(const void *x, int32_t x_f32, int32_t rows, int32_t k, const int8_t *w,
                               const float *s, const float *bias, int32_t n, int32_t epilogue, void *y,
                               int32_t ldy, const void *aux, int32_t ld_aux, float alpha, void *hip_stream);
@@ -350,9 +352,11 @@ xnp_status xnp_quantize_rows(const float *w, int32_t rows, int32_t cols, int8_t 
 /* FlowLM's text prompt and frame steps (TTSModel::prompt_text and generate_step_parts,
  * tts_model.rs:297-378) on f32 kernels, for batches of an f32 pool's streams: the LUT gather,
  * input_linear, the transformer (norms, linears, GELU, residuals around the pool's attention),
- * out_norm, the EOS head and the flow net's LSD decode (SimpleMLPAdaLN, mlp.rs:159-238).  Config
- * subset: no z_proj, no attn_dim override, no grouped heads, no layer scale, no conditions or
- * sinks. */
+ * out_norm, z_proj, the EOS head and the flow net (SimpleMLPAdaLN, mlp.rs:159-238).  FlowLMConfig
+ * (flow_lm.rs:114-146) whole: z_dim, attn_dim, num_kv_heads, the flow types and time norms, and the
+ * conditions broadcast-added to the step input (flow_lm.rs:304-307).  (FlowLM's transformer has no
+ * layer scale: flow_lm.rs:239-249 loads it with None; xnp_layer_step takes one for other callers.)
+ * Text sinks (tts_model.rs:299-301) stay with the caller: the sink row is one more prompt row. */
 typedef enum xnp_time_norm { XNP_TIME_RMS = 0, XNP_TIME_RMS_VAR = 1 } xnp_time_norm; /* mlp.rs:17-28 */
 /* FlowType (flow_lm.rs:372-381): the LSD solver over lsd_steps, or one flow-net call without time
  * conditions (Drifting: the latent is its output; Pointwise: noise plus it). */
@@ -373,15 +377,18 @@ typedef struct xnp_flow_lm_desc {
     int32_t z_dim;                              /* 0: no z_proj; else its width (flow_lm.rs:239-240) */
     int32_t flow_type;                          /* xnp_flow_type */
     int32_t precision;                          /* xnp_flow_precision */
+    int32_t num_kv_heads;                       /* 0: num_heads; else grouped-query kv heads (flow_lm.rs:143-145, 253) */
+    int32_t attn_dim;                           /* 0: d_model; else the attention's query and output width,
+                                                   num_heads x the pool's head_dim (flow_lm.rs:139-141, 252) */
 } xnp_flow_lm_desc;
 
 typedef struct xnp_flow_lm xnp_flow_lm;
 
 /* Floats of the weight blob: every tensor f32, row-major [out][in] for linears, in this order (zd:
- * z_dim when set, else d) --
+ * z_dim when set, else d; a: attn_dim when set, else d; kv: a / num_heads x num_kv_heads) --
  * conditioner.embed [n_bins+1][d]; input_linear [d][ldim]; bos_emb [ldim];
- * per layer: norm1 w, b [d]; in_proj [3d][d]; out_proj [d][d]; norm2 w, b [d]; linear1 [ff][d];
- *   linear2 [d][ff];
+ * per layer: norm1 w, b [d]; in_proj [a + 2 kv][d] (q rows, then k, then v); out_proj [d][a];
+ *   norm2 w, b [d]; linear1 [ff][d]; linear2 [d][ff];
  * out_norm w, b [d]; z_proj [z][d] when z_dim; out_eos w [1][zd], b [1];
  * per time embedder (2, XNP_FLOW_LSD only): freqs [128]; mlp.0 w [F][256], b [F]; mlp.2 w [F][F],
  *   b [F]; alpha [F];
@@ -402,22 +409,31 @@ xnp_status xnp_flow_lm_destroy(xnp_flow_lm *lm);
  * transformer, committed.  Token ids past the table are refused (conditioners.rs:248-256). */
 xnp_status xnp_flow_lm_prompt_text(xnp_flow_lm *lm, const int32_t *ids, int32_t n,
                                    const int32_t *tokens, int32_t t, void *hip_stream);
-/* One frame for streams ids[0..n): latent_in [n][ldim] (NULL: bos_emb for every row), noise
- * [n][ldim] (the solver's start; zeros at temperature 0), latent_out [n][ldim], eos_logit [n], all
- * f32 device memory.  The streams advance by one position. */
+/* The model's summed conditions (FlowLM::condition_providers, flow_lm.rs:218-222, the sum of
+ * conditioners.rs:57-63): cond [dim] host f32, dim == d_model, or NULL for none.  Broadcast-added to
+ * every frame's input_linear output (flow_lm.rs:304-307) whose step passes no conditions of its own.
+ * Copied to the device before the call returns; a recorded frame graph is recorded again. */
+xnp_status xnp_flow_lm_set_condition(xnp_flow_lm *lm, const float *cond, int32_t dim);
+/* One frame for streams ids[0..n): latent_in [n][ldim] (NULL: bos_emb for every row), conditions
+ * [n][d_model] (each stream's FlowLMState::conditions, flow_lm.rs:200, 304-307, as the s2s session
+ * sets per frame, s2s.rs:334; NULL: the model's condition when set, else none), noise [n][ldim] (the
+ * solver's start; zeros at temperature 0), latent_out [n][ldim], eos_logit [n], all f32 device
+ * memory.  The condition row is added to input_linear's output (f32: y + c; q8: bf16(bf16(c) + y)).
+ * The streams advance by one position. */
 xnp_status xnp_flow_lm_step(xnp_flow_lm *lm, const int32_t *ids, int32_t n, const float *latent_in,
-                            const float *noise, float *latent_out, float *eos_logit, void *hip_stream);
+                            const float *conditions, const float *noise, float *latent_out, float *eos_logit,
+                            void *hip_stream);
 /* xnp_flow_lm_step with the frame's launches recorded once in a hipGraph and replayed, as
  * StepGraph records one step and replays it per frame (step_graph.rs:111-122, 234-267).  The plan
  * (positions, pages) is uploaded eagerly each call and read by the recorded kernels from the pool's
  * device buffers, as DeviceStep keeps the position on the device (transformer.rs:111-140).  A new
  * recording is made when n, a buffer or the stream changes, or when the batch's plan picks other
  * kernels than the recorded ones (a stream of the batch took up a ring prefix, another split, a
- * regrown RoPE table); hip_stream must not be the null stream.  Results are those of
- * xnp_flow_lm_step. */
+ * regrown RoPE table, another condition source); hip_stream must not be the null stream.  Results
+ * are those of xnp_flow_lm_step. */
 xnp_status xnp_flow_lm_step_graph(xnp_flow_lm *lm, const int32_t *ids, int32_t n, const float *latent_in,
-                                  const float *noise, float *latent_out, float *eos_logit,
-                                  void *hip_stream);
+                                  const float *conditions, const float *noise, float *latent_out,
+                                  float *eos_logit, void *hip_stream);
 
 /* ---- budgets (plan.rs:25, 43-54) --------------------------------------------------------- */
 int32_t xnp_frame_budget(int32_t num_tokens, double frame_rate);

@@ -887,17 +887,23 @@ typedef struct {
     size_t fin_aw, fin_ab, fin_w, fin_b;
     size_t total;
     int zd; /* the width out_eos and cond_embed read: z_dim, else d_model */
+    int ad; /* the attention's query and output width: attn_dim, else d_model */
+    int kd; /* its key and value width: ad / num_heads x num_kv_heads (transformer.rs:162) */
 } flow_layout;
 
 static int flow_layout_of(const orc_flow_lm_desc *d, flow_layout *L) {
+    const int ad = d->attn_dim ? d->attn_dim : d->d_model, kvh = d->num_kv_heads ? d->num_kv_heads : d->num_heads;
     if (d->num_layers <= 0 || d->num_layers > ORC_MAXL || d->flow_depth < 0 || d->flow_depth > ORC_MAXL ||
-        d->d_model <= 0 || d->num_heads <= 0 || d->d_model % d->num_heads || d->ldim <= 0 || d->flow_dim <= 0 ||
-        d->ff <= 0 || d->n_bins <= 0 || d->z_dim < 0 || d->flow_type < 0 || d->flow_type > 2 ||
+        d->d_model <= 0 || d->num_heads <= 0 || d->ldim <= 0 || d->flow_dim <= 0 || d->ff <= 0 ||
+        d->n_bins <= 0 || d->z_dim < 0 || d->attn_dim < 0 || d->num_kv_heads < 0 || ad % d->num_heads ||
+        kvh > d->num_heads || d->num_heads % kvh || d->flow_type < 0 || d->flow_type > 2 ||
         (d->flow_type == 0 && d->lsd_steps <= 0) || d->precision < 0 || d->precision > 1)
         return fail("bad flow LM shape");
     const size_t dm = d->d_model, F = d->flow_dim, ld = d->ldim, ff = d->ff, fq = ORC_FREQ_DIM;
     const size_t zd = d->z_dim ? (size_t)d->z_dim : dm;
     L->zd = (int)zd;
+    L->ad = ad;
+    L->kd = ad / d->num_heads * kvh;
     size_t o = 0;
 #define TAKE(field, n) (L->field = o, o += (size_t)(n))
     TAKE(embed, (d->n_bins + 1) * dm);
@@ -905,7 +911,7 @@ static int flow_layout_of(const orc_flow_lm_desc *d, flow_layout *L) {
     TAKE(bos, ld);
     for (int l = 0; l < d->num_layers; l++) {
         TAKE(ln1_w[l], dm); TAKE(ln1_b[l], dm);
-        TAKE(wqkv[l], 3 * dm * dm); TAKE(wout[l], dm * dm);
+        TAKE(wqkv[l], ((size_t)L->ad + 2 * (size_t)L->kd) * dm); TAKE(wout[l], dm * (size_t)L->ad);
         TAKE(ln2_w[l], dm); TAKE(ln2_b[l], dm);
         TAKE(w1[l], ff * dm); TAKE(w2[l], dm * ff);
     }
@@ -1052,23 +1058,23 @@ int orc_flow_net(const orc_flow_lm_desc *d, const float *blob, const float *c, c
 /* The transformer over t rows of one stream (transformer.rs:591-634, f32 weights), x [t][d]. */
 static int flow_transformer(const orc_flow_lm_desc *d, const float *blob, const flow_layout *L, orc_stream *st,
                             int t, float *x) {
-    const int dm = d->d_model, ff = d->ff, H = d->num_heads, D = dm / H;
-    float *h = malloc(sizeof(float) * (size_t)t * dm), *qkv = malloc(sizeof(float) * (size_t)t * 3 * dm);
-    float *q = malloc(sizeof(float) * (size_t)t * dm), *k = malloc(sizeof(float) * (size_t)t * dm);
-    float *v = malloc(sizeof(float) * (size_t)t * dm), *att = malloc(sizeof(float) * (size_t)t * dm);
+    const int dm = d->d_model, ff = d->ff, H = d->num_heads, ad = L->ad, kd = L->kd, D = ad / H, nq = ad + 2 * kd;
+    float *h = malloc(sizeof(float) * (size_t)t * dm), *qkv = malloc(sizeof(float) * (size_t)t * nq);
+    float *q = malloc(sizeof(float) * (size_t)t * ad), *k = malloc(sizeof(float) * (size_t)t * kd);
+    float *v = malloc(sizeof(float) * (size_t)t * kd), *att = malloc(sizeof(float) * (size_t)t * ad);
     float *f = malloc(sizeof(float) * (size_t)t * ff);
     int rc = 0;
     for (int l = 0; l < d->num_layers && rc == 0; l++) {
         orc_layer_norm(x, t, dm, blob + L->ln1_w[l], blob + L->ln1_b[l], 1e-5f, ORC_F32, h);
-        orc_linear_f32(h, t, dm, blob + L->wqkv[l], NULL, 3 * dm, qkv);
-        for (int i = 0; i < t; i++) {
-            memcpy(q + (size_t)i * dm, qkv + (size_t)i * 3 * dm, sizeof(float) * dm);
-            memcpy(k + (size_t)i * dm, qkv + (size_t)i * 3 * dm + dm, sizeof(float) * dm);
-            memcpy(v + (size_t)i * dm, qkv + (size_t)i * 3 * dm + 2 * dm, sizeof(float) * dm);
+        orc_linear_f32(h, t, dm, blob + L->wqkv[l], NULL, nq, qkv);
+        for (int i = 0; i < t; i++) { /* q, then k, then v (transformer.rs:195-211) */
+            memcpy(q + (size_t)i * ad, qkv + (size_t)i * nq, sizeof(float) * ad);
+            memcpy(k + (size_t)i * kd, qkv + (size_t)i * nq + ad, sizeof(float) * kd);
+            memcpy(v + (size_t)i * kd, qkv + (size_t)i * nq + ad + kd, sizeof(float) * kd);
         }
         rc = orc_attend(st, l, t, q, k, v, 1.0f / sqrtf((float)D), att, NULL);
         if (rc) break;
-        orc_linear_f32(att, t, dm, blob + L->wout[l], NULL, dm, h);
+        orc_linear_f32(att, t, ad, blob + L->wout[l], NULL, dm, h);
         for (size_t i = 0; i < (size_t)t * dm; i++) x[i] += h[i];
         orc_layer_norm(x, t, dm, blob + L->ln2_w[l], blob + L->ln2_b[l], 1e-5f, ORC_F32, h);
         orc_linear_f32(h, t, dm, blob + L->w1[l], NULL, ff, f);
@@ -1096,7 +1102,7 @@ int orc_flow_lm_prompt_text(const orc_flow_lm_desc *d, const float *blob, orc_st
 }
 
 int orc_flow_lm_step(const orc_flow_lm_desc *d, const float *blob, orc_stream *st, const float *latent_in,
-                     const float *noise, float *latent_out, float *eos_logit) {
+                     const float *cond, const float *noise, float *latent_out, float *eos_logit) {
     flow_layout L;
     if (flow_layout_of(d, &L)) return -1;
     if (d->precision != 0) return fail("a q8 flow LM steps through orc_flow_q8_step");
@@ -1106,6 +1112,8 @@ int orc_flow_lm_step(const orc_flow_lm_desc *d, const float *blob, orc_stream *s
     float *z = malloc(sizeof(float) * L.zd);
     /* input_linear of the previous latent, or of bos_emb on the first step (flow_lm.rs:314-324) */
     orc_linear_f32(latent_in ? latent_in : blob + L.bos, 1, ld, blob + L.in_lin, NULL, dm, x);
+    if (cond) /* the conditions, broadcast-added to the step input (flow_lm.rs:304-307) */
+        for (int j = 0; j < dm; j++) x[j] = x[j] + cond[j];
     int rc = flow_transformer(d, blob, &L, st, 1, x);
     if (rc == 0) {
         ln_mod(x, dm, blob + L.on_w, blob + L.on_b, 1e-5f, NULL, NULL, t_out); /* out_norm (flow_lm.rs:315) */
@@ -1155,6 +1163,7 @@ void orc_flow_linear_q8(const float *x, int rows, int k, const int8_t *q, const 
             case 7:
                 *o = orc_bf16_round(orc_bf16_round(aux[(size_t)m * ld_aux + j]) + orc_bf16_round(y * alpha));
                 break;
+            case 9: *o = orc_bf16_round(orc_bf16_round(aux[(size_t)m * ld_aux + j]) + y); break;
             default: *o = y;
             }
         }
@@ -1239,8 +1248,8 @@ orc_flow_q8 *orc_flow_q8_prepare(const orc_flow_lm_desc *d, const float *blob) {
     const int dm = d->d_model, F = d->flow_dim, ld = d->ldim, ff = d->ff, zd = L.zd;
     qlin_make(&m->in_lin, blob + L.in_lin, dm, ld);
     for (int l = 0; l < d->num_layers; l++) {
-        qlin_make(&m->wqkv[l], blob + L.wqkv[l], 3 * dm, dm);
-        qlin_make(&m->wout[l], blob + L.wout[l], dm, dm);
+        qlin_make(&m->wqkv[l], blob + L.wqkv[l], L.ad + 2 * L.kd, dm);
+        qlin_make(&m->wout[l], blob + L.wout[l], dm, L.ad);
         qlin_make(&m->w1[l], blob + L.w1[l], ff, dm);
         qlin_make(&m->w2[l], blob + L.w2[l], dm, ff);
         orc_layer_weights *w = &m->lw[l];
@@ -1296,7 +1305,7 @@ void orc_flow_q8_free(orc_flow_q8 *m) {
 }
 
 static int q8_transformer(orc_flow_q8 *m, orc_stream *st, int t, float *x) {
-    const float scale = 1.0f / sqrtf((float)(m->d.d_model / m->d.num_heads));
+    const float scale = 1.0f / sqrtf((float)(m->L.ad / m->d.num_heads));
     for (int l = 0; l < m->d.num_layers; l++)
         if (layer_step_one(st, t, l, &m->lw[l], scale, x)) return -1;
     return orc_commit(st, t);
@@ -1317,7 +1326,7 @@ int orc_flow_q8_prompt_text(orc_flow_q8 *m, orc_stream *st, const int *ids, int 
     return rc;
 }
 
-int orc_flow_q8_step(orc_flow_q8 *m, orc_stream *st, const float *latent_in, const float *noise,
+int orc_flow_q8_step(orc_flow_q8 *m, orc_stream *st, const float *latent_in, const float *cond, const float *noise,
                      float *latent_out, float *eos_logit) {
     const orc_flow_lm_desc *d = &m->d;
     const flow_layout *L = &m->L;
@@ -1327,6 +1336,8 @@ int orc_flow_q8_step(orc_flow_q8 *m, orc_stream *st, const float *latent_in, con
     float *ya = malloc(sizeof(float) * F), *xf = malloc(sizeof(float) * F), *ada = malloc(sizeof(float) * 3 * F);
     float *h = malloc(sizeof(float) * F), *h2 = malloc(sizeof(float) * F), *cur = malloc(sizeof(float) * ld);
     q8lin(latent_in ? latent_in : blob + L->bos, 1, &m->in_lin, NULL, x); /* input_linear (flow_lm.rs:314-324) */
+    if (cond) /* the conditions, a bf16 tensor add (flow_lm.rs:304-307) */
+        for (int j = 0; j < dm; j++) x[j] = orc_bf16_round(x[j] + orc_bf16_round(cond[j]));
     int rc = q8_transformer(m, st, 1, x);
     if (rc == 0) {
         orc_layer_norm_mod(x, 1, dm, blob + L->on_w, blob + L->on_b, 1e-5f, NULL, NULL, 0, t_out); /* out_norm */

@@ -152,7 +152,7 @@ int orc_layer_step(orc_stream **streams, int n, int t, int layer, const orc_laye
 /* --- the flow LM around the transformer (flow_lm.rs, mlp.rs, conditioners.rs), f32 ------------ */
 #define ORC_FREQ_DIM 256 /* the time embedders' frequency embedding (mlp.rs:186-193) */
 typedef struct orc_flow_lm_desc {
-    int d_model, num_heads, num_layers, ff;  /* the transformer (no GQA, no layer scale) */
+    int d_model, num_heads, num_layers, ff;  /* the transformer (no layer scale: flow_lm.rs:239-249) */
     int ldim, n_bins, flow_dim, flow_depth;  /* latent width, LUT rows - 1, flow net width, res blocks */
     int lsd_steps;                           /* LSD solver steps (lsd_decode_steps) */
     int gelu;                                /* 0 erf, 1 tanh */
@@ -160,12 +160,14 @@ typedef struct orc_flow_lm_desc {
     int z_dim;                               /* 0: no z_proj; else its width (flow_lm.rs:135, 239-240) */
     int flow_type;                           /* 0 Lsd, 1 Drifting, 2 Pointwise (flow_lm.rs:372-381) */
     int precision;                           /* 0 f32; 1 q8: int8 weights, bf16 activations */
+    int num_kv_heads;                        /* 0: num_heads; else grouped-query kv heads (flow_lm.rs:143-145) */
+    int attn_dim;                            /* 0: d_model; else the attention width (flow_lm.rs:139-141) */
 } orc_flow_lm_desc;
 /* Floats of the weight blob: every tensor f32, row-major [out][in], in this order (zd = z_dim when
- * set, else d) --
+ * set, else d; a = attn_dim when set, else d; kv = a / num_heads x num_kv_heads) --
  * conditioner.embed [n_bins+1][d]; input_linear [d][ldim]; bos_emb [ldim];
- * per layer: norm1 w, b [d]; in_proj [3d][d]; out_proj [d][d]; norm2 w, b [d]; linear1 [ff][d];
- *   linear2 [d][ff];
+ * per layer: norm1 w, b [d]; in_proj [a + 2 kv][d]; out_proj [d][a]; norm2 w, b [d];
+ *   linear1 [ff][d]; linear2 [d][ff];
  * out_norm w, b [d]; z_proj [z][d] when z_dim; out_eos w [1][zd], b [1];
  * per time embedder (2, Lsd only): freqs [128]; mlp.0 w [F][256], b [F]; mlp.2 w [F][F], b [F];
  *   alpha [F];
@@ -187,12 +189,13 @@ int orc_flow_net(const orc_flow_lm_desc *d, const float *blob, const float *c, c
  * (f32 stream), committed.  No text sink. */
 int orc_flow_lm_prompt_text(const orc_flow_lm_desc *d, const float *blob, orc_stream *st,
                             const int *ids, int n);
-/* One frame (generate_step_parts, tts_model.rs:365-378): input_linear of latent_in (NULL: bos_emb),
- * the transformer (committed), out_norm, z_proj, the EOS logit (out_eos) and the flow head on noise
- * [ldim] conditioned on the output (sample_from_noise, flow_lm.rs:363-384): latent_out [ldim],
- * eos_logit [1].  f32 desc only. */
-int orc_flow_lm_step(const orc_flow_lm_desc *d, const float *blob, orc_stream *st,
-                     const float *latent_in, const float *noise, float *latent_out, float *eos_logit);
+/* One frame (generate_step_parts, tts_model.rs:365-378): input_linear of latent_in (NULL: bos_emb)
+ * plus cond [d_model] when not NULL (the conditions, flow_lm.rs:304-307), the transformer
+ * (committed), out_norm, z_proj, the EOS logit (out_eos) and the flow head on noise [ldim]
+ * conditioned on the output (sample_from_noise, flow_lm.rs:363-384): latent_out [ldim], eos_logit
+ * [1].  f32 desc only.  A stream of a grouped-head desc holds num_kv_heads heads of a / num_heads. */
+int orc_flow_lm_step(const orc_flow_lm_desc *d, const float *blob, orc_stream *st, const float *latent_in,
+                     const float *cond, const float *noise, float *latent_out, float *eos_logit);
 
 /* The q8 precision (desc->precision 1), the batched frame's definition: every linear's weight rows
  * quantized as orc_quantize_rows does (biases, norms and the LUT stay f32, the LUT rows and bos
@@ -203,8 +206,9 @@ int orc_flow_lm_step(const orc_flow_lm_desc *d, const float *blob, orc_stream *s
  * transformer is orc_layer_step's.  Streams are bf16 caches with bf16 activations. */
 /* Its pieces.  The q8 linear: y = bf16(s[j] * sum_k bf16(x[m][k]) q[j][k] (+ b[j])), then epi 0:
  * store; 4: silu; 5: silu(bf16(y + aux[j])); 6: out = bf16(out + bf16(aux[m][j] * y)) (the AdaLN
- * gate); 7: out = bf16(bf16(aux[m][j]) + bf16(y * alpha)) (the solver step); 8: store.  Every
- * result is rounded to bf16 once.  out [rows][ldo], aux rows of stride ld_aux. */
+ * gate); 7: out = bf16(bf16(aux[m][j]) + bf16(y * alpha)) (the solver step); 8: store; 9: out =
+ * bf16(bf16(aux[m][j]) + y) (a condition added to the step input).  Every result is rounded to
+ * bf16 once.  out [rows][ldo], aux rows of stride ld_aux (0: one row for every row). */
 void orc_flow_linear_q8(const float *x, int rows, int k, const int8_t *q, const float *s, const float *b, int n,
                         int epi, float *out, int ldo, const float *aux, int ld_aux, float alpha);
 /* LayerNorm of rows (affine w, b or NULL) rounded to bf16, then when shift is given the AdaLN
@@ -215,7 +219,7 @@ typedef struct orc_flow_q8 orc_flow_q8;
 orc_flow_q8 *orc_flow_q8_prepare(const orc_flow_lm_desc *d, const float *blob);
 void orc_flow_q8_free(orc_flow_q8 *m);
 int orc_flow_q8_prompt_text(orc_flow_q8 *m, orc_stream *st, const int *ids, int n);
-int orc_flow_q8_step(orc_flow_q8 *m, orc_stream *st, const float *latent_in, const float *noise,
+int orc_flow_q8_step(orc_flow_q8 *m, orc_stream *st, const float *latent_in, const float *cond, const float *noise,
                      float *latent_out, float *eos_logit);
 
 /* Many streams, one layer: the CPU baseline's batched step (OpenMP over streams). */

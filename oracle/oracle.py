@@ -79,7 +79,7 @@ def lib():
             "orc_flow_time_embedding": (ctypes.c_int, [ctypes.c_void_p, _fp, ctypes.c_float, ctypes.c_float, _fp]),
             "orc_flow_net": (ctypes.c_int, [ctypes.c_void_p, _fp, _fp, _fp, _fp, _fp]),
             "orc_flow_lm_prompt_text": (ctypes.c_int, [ctypes.c_void_p, _fp, ctypes.c_void_p, _ip, ctypes.c_int]),
-            "orc_flow_lm_step": (ctypes.c_int, [ctypes.c_void_p, _fp, ctypes.c_void_p, _fp, _fp, _fp, _fp]),
+            "orc_flow_lm_step": (ctypes.c_int, [ctypes.c_void_p, _fp, ctypes.c_void_p, _fp, _fp, _fp, _fp, _fp]),
             "orc_flow_linear_q8": (None, [_fp, ctypes.c_int, ctypes.c_int, _i8p, _fp, _fp, ctypes.c_int, ctypes.c_int,
                                           _fp, ctypes.c_int, _fp, ctypes.c_int, ctypes.c_float]),
             "orc_layer_norm_mod": (None, [_fp, ctypes.c_int, ctypes.c_int, _fp, _fp, ctypes.c_float, _fp, _fp,
@@ -87,7 +87,7 @@ def lib():
             "orc_flow_q8_prepare": (ctypes.c_void_p, [ctypes.c_void_p, _fp]),
             "orc_flow_q8_free": (None, [ctypes.c_void_p]),
             "orc_flow_q8_prompt_text": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, _ip, ctypes.c_int]),
-            "orc_flow_q8_step": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, _fp, _fp, _fp, _fp]),
+            "orc_flow_q8_step": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, _fp, _fp, _fp, _fp, _fp]),
             "orc_layer_norm": (None, [_fp, ctypes.c_int, ctypes.c_int, _fp, _fp, ctypes.c_float, ctypes.c_int, _fp]),
             "orc_quantize_rows": (None, [_fp, ctypes.c_int, ctypes.c_int, _i8p, _fp]),
             "orc_linear_q8": (None, [_fp, ctypes.c_int, ctypes.c_int, _i8p, _fp, ctypes.c_int, ctypes.c_int, _fp]),
@@ -429,7 +429,7 @@ def layer_step(streams, layer, weights: LayerWeights, x, scale=0.125):
     return x
 
 
-FLOW_EPILOGUES = {"store": 0, "silu": 4, "silu_add": 5, "gated": 6, "axpy_f32": 7, "store_f32": 8}
+FLOW_EPILOGUES = {"store": 0, "silu": 4, "silu_add": 5, "gated": 6, "axpy_f32": 7, "store_f32": 8, "add_f32": 9}
 
 
 def flow_linear_q8(x, q, s, epilogue="store", bias=None, aux=None, out=None, alpha=1.0):
@@ -467,7 +467,7 @@ def layer_norm_mod(x, w=None, b=None, shift=None, scale=None, eps=1e-6):
 class _FlowDescC(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in ("d_model", "num_heads", "num_layers", "ff", "ldim", "n_bins",
                                             "flow_dim", "flow_depth", "lsd_steps", "gelu", "time_norm", "z_dim",
-                                            "flow_type", "precision")]
+                                            "flow_type", "precision", "num_kv_heads", "attn_dim")]
 
 
 FLOW_TYPES = {"lsd": 0, "drifting": 1, "pointwise": 2}
@@ -484,7 +484,8 @@ class FlowLM:
         self.d = _FlowDescC(cfg.d_model, cfg.num_heads, cfg.num_layers, cfg.dim_feedforward, cfg.ldim, cfg.n_bins,
                             cfg.flow_dim, cfg.flow_depth, cfg.lsd_decode_steps, 0 if cfg.gelu == "erf" else 1,
                             0 if cfg.time_rms_norm == "rms" else 1, getattr(cfg, "z_dim", 0),
-                            FLOW_TYPES[getattr(cfg, "flow_type", "lsd")], PRECISIONS[getattr(cfg, "precision", "f32")])
+                            FLOW_TYPES[getattr(cfg, "flow_type", "lsd")], PRECISIONS[getattr(cfg, "precision", "f32")],
+                            getattr(cfg, "num_kv_heads", 0), getattr(cfg, "attn_dim", 0))
         self.blob = np.ascontiguousarray(blob, np.float32)
         n = lib().orc_flow_lm_size(self._dp())
         if n != self.blob.size:
@@ -507,8 +508,9 @@ class FlowLM:
     def stream(self, capacity):
         c = self.cfg
         dt = "bf16" if self.q8 else "f32"
-        return Stream(c.num_layers, c.num_heads, c.d_model // c.num_heads, capacity, cache=dt, act=dt,
-                      max_period=c.max_period)
+        a = getattr(c, "attn_dim", 0) or c.d_model
+        return Stream(c.num_layers, c.num_heads, a // c.num_heads, capacity, cache=dt, act=dt,
+                      kv_heads=getattr(c, "num_kv_heads", 0) or None, max_period=c.max_period)
 
     def time_embedding(self, s, t):
         out = np.zeros(self.cfg.flow_dim, np.float32)
@@ -530,16 +532,19 @@ class FlowLM:
         else:
             _ok(lib().orc_flow_lm_prompt_text(self._dp(), self._bp, st.h, ids.ctypes.data_as(_ip), ids.size))
 
-    def step(self, st, latent_in, noise):
-        """One frame: (latent [ldim], eos logit)."""
+    def step(self, st, latent_in, noise, cond=None):
+        """One frame: (latent [ldim], eos logit); cond [d_model]: the conditions added to the step
+        input (flow_lm.rs:304-307), or None."""
         lat = None if latent_in is None else np.ascontiguousarray(latent_in, np.float32)
         latp = lat.ctypes.data_as(_fp) if lat is not None else None
+        c = None if cond is None else np.ascontiguousarray(cond, np.float32)
+        cp = c.ctypes.data_as(_fp) if c is not None else None
         nz, nzp = _f32(noise)
         out = np.zeros(self.cfg.ldim, np.float32)
         eos = np.zeros(1, np.float32)
         if self.q8:
-            _ok(lib().orc_flow_q8_step(self._q, st.h, latp, nzp, out.ctypes.data_as(_fp), eos.ctypes.data_as(_fp)))
+            _ok(lib().orc_flow_q8_step(self._q, st.h, latp, cp, nzp, out.ctypes.data_as(_fp), eos.ctypes.data_as(_fp)))
         else:
-            _ok(lib().orc_flow_lm_step(self._dp(), self._bp, st.h, latp, nzp, out.ctypes.data_as(_fp),
+            _ok(lib().orc_flow_lm_step(self._dp(), self._bp, st.h, latp, cp, nzp, out.ctypes.data_as(_fp),
                                        eos.ctypes.data_as(_fp)))
         return out, float(eos[0])

@@ -16,24 +16,29 @@ import pytest
 import torch
 
 from conftest import oracle, xnp
-from helpers import rel_err
+from helpers import bf16_round, rel_err
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 fl = xnp.flow_lm
 
 
-def run_pair(cfg, blob, tokens, frames, noise, cap):
+def run_pair(cfg, blob, tokens, frames, noise, cap, cond=None, model_cond=None):
+    """cond [frames][n][d_model]: each stream's conditions per frame; model_cond [d_model]: the
+    model's (used when cond is None)."""
     n = tokens.shape[0]
-    H, D = cfg.num_heads, cfg.d_model // cfg.num_heads
+    H = cfg.num_heads
     mbps = (cap + 15) // 16
     q8 = cfg.precision == "q8"
     dt = "bf16" if q8 else "f32"
     tol = 4e-2 if q8 else 1e-5
-    pool = xnp.KvPool(num_layers=cfg.num_layers, num_heads=H, num_blocks=n * mbps + 8, max_streams=n,
-                      max_blocks_per_stream=mbps, cache_dtype=dt, act_dtype=dt, max_pos=cap + 16, page_seed=3)
+    pool = xnp.KvPool(num_layers=cfg.num_layers, num_heads=H, num_kv_heads=cfg.num_kv_heads or H,
+                      num_blocks=n * mbps + 8, max_streams=n, max_blocks_per_stream=mbps, cache_dtype=dt, act_dtype=dt,
+                      max_pos=cap + 16, page_seed=3)
     ids = [pool.init_state(cap) for _ in range(n)]
     lm = xnp.FlowLM(pool, cfg, blob, max_rows=n * tokens.shape[1])
+    if model_cond is not None:
+        lm.set_condition(model_cond)
     orc = oracle.FlowLM(cfg, blob)
     sts = [orc.stream(cap) for _ in range(n)]
     lm.prompt_text(ids, tokens)
@@ -45,12 +50,14 @@ def run_pair(cfg, blob, tokens, frames, noise, cap):
     nz = torch.from_numpy(noise).to(DEV)
     want_lat = [None] * n
     worst = 0.0
+    cdev = None if cond is None else torch.from_numpy(np.ascontiguousarray(cond, np.float32)).to(DEV)
     for f in range(frames):
-        lm.step(ids, lat_in, nz[f], out, eos)
+        lm.step(ids, lat_in, nz[f], out, eos, conditions=None if cdev is None else cdev[f])
         torch.cuda.synchronize()
         got_lat, got_eos = out.cpu().numpy(), eos.cpu().numpy()
         for i in range(n):
-            wl, we = orc.step(sts[i], want_lat[i], noise[f, i])
+            c = cond[f, i] if cond is not None else model_cond
+            wl, we = orc.step(sts[i], want_lat[i], noise[f, i], cond=c)
             want_lat[i] = wl
             e = max(rel_err(got_lat[i], wl), abs(got_eos[i] - we) / max(1.0, abs(we)))
             worst = max(worst, e)
@@ -151,6 +158,71 @@ def test_flow_lm_variants_match_the_oracle(flow_type, z_dim):
     _, _, sts, worst = run_pair(cfg, blob, tokens, 5, noise, 32)
     assert sts[0].current_end == 10
     print(f"{flow_type} z_dim {z_dim}: worst relative error {worst:.2e}")
+
+
+@pytest.mark.parametrize("precision", ["f32", "q8"])
+@pytest.mark.parametrize("heads,kv_heads,attn_dim,cond", [(8, 2, 0, "stream"), (4, 1, 256, "model"),
+                                                          (4, 2, 256, "stream")])
+def test_grouped_heads_attn_dim_and_conditions_match_the_oracle(precision, heads, kv_heads, attn_dim, cond):
+    # FlowLMConfig's num_kv_heads (flow_lm.rs:143-145, 253: the pool stores kv_heads heads), attn_dim
+    # (flow_lm.rs:139-141, 252: in_proj [a + 2 kv][d], out_proj [d][a], 64-wide heads) and the
+    # conditions broadcast-added to the step input (flow_lm.rs:304-307): each stream's own row per
+    # frame (FlowLMState::conditions, as s2s.rs:334 sets it), or the model's summed conditions
+    # (condition_providers, flow_lm.rs:218-222).  Three streams, a 6-token prompt, 8 frames.
+    cfg = fl.FlowLMConfig(num_layers=2, flow_depth=2, flow_dim=512, dim_feedforward=1024, n_bins=100, d_model=512,
+                          num_heads=heads, num_kv_heads=kv_heads, attn_dim=attn_dim, lsd_decode_steps=2,
+                          precision=precision)
+    blob = fl.random_weights(cfg, 107, std=0.05, unit_norms=False)
+    rng = np.random.default_rng(108)
+    tokens = rng.integers(0, cfg.n_bins + 1, (3, 6)).astype(np.int32)
+    noise = (0.5 * rng.standard_normal((8, 3, cfg.ldim))).astype(np.float32)
+    c = (0.5 * rng.standard_normal((8, 3, cfg.d_model))).astype(np.float32)
+    if precision == "q8":
+        c = bf16_round(c)
+    kw = dict(cond=c) if cond == "stream" else dict(model_cond=c[0, 0])
+    pool, ids, sts, worst = run_pair(cfg, blob, tokens, 8, noise, 32, **kw)
+    assert sts[0].current_end == 14 and pool.current_end(ids[0]) == 14
+    print(f"{precision} {heads} heads over {kv_heads}, attn_dim {attn_dim or 512}, {cond} conditions: "
+          f"worst relative error {worst:.2e}")
+
+
+def test_q8_graph_is_recorded_again_when_the_condition_source_changes():
+    # Frames replayed from a graph equal eager frames bit for bit while the conditions come from the
+    # step's own rows, then from the model's, then from nowhere: each change of source records again.
+    cfg = fl.FlowLMConfig(num_layers=2, flow_depth=2, flow_dim=512, dim_feedforward=1024, n_bins=100,
+                          num_heads=8, num_kv_heads=2, precision="q8")
+    blob = fl.random_weights(cfg, 109, std=0.05, unit_norms=False)
+    rng = np.random.default_rng(110)
+    n, P = 3, 4
+    tokens = rng.integers(0, cfg.n_bins + 1, (n, P)).astype(np.int32)
+    s = torch.cuda.Stream()
+    runs = []
+    for _ in range(2):
+        pool = xnp.KvPool(num_layers=2, num_heads=8, num_kv_heads=2, num_blocks=24, max_streams=n,
+                          max_blocks_per_stream=4, cache_dtype="bf16", act_dtype="bf16", max_pos=128, page_seed=6)
+        ids = [pool.init_state(64) for _ in range(n)]
+        lm = xnp.FlowLM(pool, cfg, blob, max_rows=n * P)
+        with torch.cuda.stream(s):
+            lm.prompt_text(ids, tokens)
+        lat = torch.zeros((n, cfg.ldim), dtype=torch.float32, device=DEV)
+        eos = torch.zeros(n, dtype=torch.float32, device=DEV)
+        runs.append((pool, ids, lm, lat, eos))
+    noise = torch.zeros((n, cfg.ldim), dtype=torch.float32, device=DEV)
+    cond = torch.zeros((n, cfg.d_model), dtype=torch.float32, device=DEV)
+    model = bf16_round(0.5 * rng.standard_normal(cfg.d_model).astype(np.float32))
+    for f in range(18):
+        with torch.cuda.stream(s):
+            noise.copy_(torch.from_numpy((0.5 * rng.standard_normal((n, cfg.ldim))).astype(np.float32)).to(DEV))
+            cond.copy_(torch.from_numpy(bf16_round(0.5 * rng.standard_normal((n, cfg.d_model)))).to(DEV))
+            for g, (pool, ids, lm, lat, eos) in enumerate(runs):
+                if f == 6:
+                    lm.set_condition(model)
+                if f == 12:
+                    lm.set_condition(None)
+                lm.step(ids, None if f == 0 else lat, noise, lat, eos, stream=s.cuda_stream, graph=(g == 1),
+                        conditions=cond if f < 6 else None)
+        s.synchronize()
+        assert torch.equal(runs[0][3], runs[1][3]) and torch.equal(runs[0][4], runs[1][4]), f
 
 
 @pytest.mark.parametrize("flow_type,z_dim,steps", [("lsd", 0, 1), ("lsd", 64, 2), ("drifting", 0, 1),

@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from conftest import oracle, xnp
-from helpers import bf16_round
+from helpers import bf16_round, rel_err
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -103,9 +103,27 @@ def test_flow_linear_q8_reads_f32_rows_rounded():
                        bias=torch.from_numpy(b).to(DEV))
     torch.cuda.synchronize()
     _close(y.float().cpu().numpy(), want, "f32 x")
-    with pytest.raises(xnp.XnpError, match="store epilogue"):
+    with pytest.raises(xnp.XnpError, match="store or add epilogue"):
         xnp.flow_linear_q8(torch.from_numpy(x).to(DEV), torch.from_numpy(q).to(DEV), torch.from_numpy(s).to(DEV), y,
                            "silu")
+
+
+@pytest.mark.parametrize("rows_of_cond", [True, False])
+def test_the_condition_add_on_f32_rows_matches_the_oracle(rows_of_cond):
+    # input_linear plus the conditions (flow_lm.rs:304-307): y[m][j] = bf16(bf16(c[m][j]) + bf16(y)),
+    # with a condition row per row, or one row for every row (ld_aux 0: the model's summed conditions)
+    rng = np.random.default_rng(91 + rows_of_cond)
+    x = rng.standard_normal((70, 32)).astype(np.float32)
+    q, s = oracle.quantize_rows((0.05 * rng.standard_normal((512, 32))).astype(np.float32))
+    c = (0.5 * rng.standard_normal((70, 512) if rows_of_cond else 512)).astype(np.float32)
+    want = oracle.flow_linear_q8(x, q, s, "add_f32", aux=c)
+    y = torch.zeros((70, 512), dtype=torch.bfloat16, device=DEV)
+    xnp.flow_linear_q8(torch.from_numpy(x).to(DEV), torch.from_numpy(q).to(DEV), torch.from_numpy(s).to(DEV), y,
+                       "add_f32", aux=torch.from_numpy(c).to(DEV))
+    torch.cuda.synchronize()
+    _close(y.float().cpu().numpy(), want, "add_f32")
+    plain = oracle.flow_linear_q8(x, q, s, "store")
+    assert rel_err(want, plain) > 0.1  # the condition is there
 
 
 @pytest.mark.parametrize("affine,mod", [(True, True), (False, True), (True, False)])

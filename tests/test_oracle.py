@@ -765,10 +765,13 @@ def test_flow_net_matches_torch():
     assert rel_err(m.flow_net(c, temb, x0), want.numpy()) < 1e-5
 
 
-def _torch_flow_lm(cfg, W, ids, frames, noise):
-    """prompt_text then `frames` generate steps (flow_lm.rs:296-432, tts_model.rs:297-378) in torch f64."""
+def _torch_flow_lm(cfg, W, ids, frames, noise, cond=None):
+    """prompt_text then `frames` generate steps (flow_lm.rs:296-432, tts_model.rs:297-378) in torch f64;
+    cond [frames][d_model]: the conditions added to each step's input (flow_lm.rs:304-307)."""
     H, dm = cfg.num_heads, cfg.d_model
-    D = dm // H
+    ad = cfg.attn_dim or dm  # StreamingMultiheadAttention::load (transformer.rs:155-166)
+    KVH = cfg.num_kv_heads or H
+    D, kd = ad // H, ad // H * KVH
     hist = [{} for _ in range(cfg.num_layers)]
 
     def rope(a, p):
@@ -784,7 +787,9 @@ def _torch_flow_lm(cfg, W, ids, frames, noise):
             p = f"layers.{l}."
             h = torch.nn.functional.layer_norm(x, (dm,), _t(W[p + "norm1.w"]), _t(W[p + "norm1.b"]), eps=1e-5)
             qkv = h @ _t(W[p + "in_proj"]).T
-            q, k, v = (qkv[:, i * dm:(i + 1) * dm].reshape(T, H, D) for i in range(3))
+            q = qkv[:, :ad].reshape(T, H, D)  # then each kv head serves H / KVH query heads (:199-211)
+            k = qkv[:, ad:ad + kd].reshape(T, KVH, D).repeat_interleave(H // KVH, dim=1)
+            v = qkv[:, ad + kd:].reshape(T, KVH, D).repeat_interleave(H // KVH, dim=1)
             q = torch.stack([rope(q[i], pos + i) for i in range(T)])
             k = torch.stack([rope(k[i], pos + i) for i in range(T)])
             hs = hist[l]
@@ -794,7 +799,7 @@ def _torch_flow_lm(cfg, W, ids, frames, noise):
             att = torch.einsum("thd,nhd->thn", q, hs["k"]) / math.sqrt(D)
             causal = torch.arange(n)[None, :] <= (n - T + torch.arange(T))[:, None]
             att = att.masked_fill(~causal[:, None, :], float("-inf")).softmax(-1)
-            x = x + torch.einsum("thn,nhd->thd", att, hs["v"]).reshape(T, dm) @ _t(W[p + "out_proj"]).T
+            x = x + torch.einsum("thn,nhd->thd", att, hs["v"]).reshape(T, ad) @ _t(W[p + "out_proj"]).T
             h = torch.nn.functional.layer_norm(x, (dm,), _t(W[p + "norm2.w"]), _t(W[p + "norm2.b"]), eps=1e-5)
             f = torch.nn.functional.gelu(h @ _t(W[p + "linear1"]).T)
             x = x + f @ _t(W[p + "linear2"]).T
@@ -808,7 +813,10 @@ def _torch_flow_lm(cfg, W, ids, frames, noise):
     if lsd:
         temb = (_torch_time_embed(W, 0, 0.0, cfg.time_rms_norm) + _torch_time_embed(W, 1, 1.0, cfg.time_rms_norm)) / 2
     for f in range(frames):
-        x = transformer((_t(W["input_linear"]) @ latent)[None, :], pos)[0]
+        inp = _t(W["input_linear"]) @ latent
+        if cond is not None:
+            inp = inp + _t(cond[f])
+        x = transformer(inp[None, :], pos)[0]
         pos += 1
         t_out = torch.nn.functional.layer_norm(x, (dm,), _t(W["out_norm.w"]), _t(W["out_norm.b"]), eps=1e-5)
         if cfg.z_dim:  # z_proj, bias-free (flow_lm.rs:320-323)
@@ -821,22 +829,29 @@ def _torch_flow_lm(cfg, W, ids, frames, noise):
     return outs
 
 
-@pytest.mark.parametrize("flow_type,z_dim", [("lsd", 0), ("lsd", 48), ("drifting", 0), ("pointwise", 32)])
-def test_flow_lm_prompt_and_frames_match_torch(flow_type, z_dim):
-    # a 5-token prompt, then 4 frames (from bos_emb, then each frame's latent), noise N(0, 0.5)
-    cfg = _small_flow_cfg(flow_type=flow_type, z_dim=z_dim)
+@pytest.mark.parametrize("flow_type,z_dim,extra", [
+    ("lsd", 0, {}), ("lsd", 48, {}), ("drifting", 0, {}), ("pointwise", 32, {}),
+    ("lsd", 0, dict(num_kv_heads=2, cond=True)),                    # grouped heads, conditions
+    ("pointwise", 32, dict(num_heads=4, attn_dim=256, num_kv_heads=1, cond=True))])  # attn_dim < d_model
+def test_flow_lm_prompt_and_frames_match_torch(flow_type, z_dim, extra):
+    # a 5-token prompt, then 4 frames (from bos_emb, then each frame's latent), noise N(0, 0.5);
+    # with conditions, a different condition row N(0, 0.5) added to each frame's input
+    extra = dict(extra)
+    with_cond = extra.pop("cond", False)
+    cfg = _small_flow_cfg(flow_type=flow_type, z_dim=z_dim, **extra)
     blob = flow_lm.random_weights(cfg, 83, std=0.05, unit_norms=False)
     W = flow_lm.split(cfg, blob)
     m = oracle.FlowLM(cfg, blob)
     rng = np.random.default_rng(84)
     ids = rng.integers(0, cfg.n_bins + 1, 5)
     noise = (0.5 * rng.standard_normal((4, cfg.ldim))).astype(np.float32)
-    want = _torch_flow_lm(cfg, W, ids, 4, noise)
+    cond = (0.5 * rng.standard_normal((4, cfg.d_model))).astype(np.float32) if with_cond else None
+    want = _torch_flow_lm(cfg, W, ids, 4, noise, cond)
     st = m.stream(32)
     m.prompt_text(st, ids)
     lat = None
     for f in range(4):
-        lat, eos = m.step(st, lat, noise[f])
+        lat, eos = m.step(st, lat, noise[f], cond=None if cond is None else cond[f])
         wl, we = want[f]
         assert rel_err(lat, wl) < 2e-5, f
         assert abs(eos - we) <= 2e-5 * max(1.0, abs(we)), f
@@ -855,12 +870,17 @@ def _q8_exact(cfg, blob):
     return blob
 
 
-@pytest.mark.parametrize("flow_type,z_dim", [("lsd", 0), ("pointwise", 64)])
-def test_q8_flow_lm_is_the_f32_one_within_bf16_rounding(flow_type, z_dim):
+@pytest.mark.parametrize("flow_type,z_dim,extra", [("lsd", 0, {}), ("pointwise", 64, {}),
+                                                   ("lsd", 0, dict(num_heads=4, attn_dim=256, num_kv_heads=2, cond=True))])
+def test_q8_flow_lm_is_the_f32_one_within_bf16_rounding(flow_type, z_dim, extra):
     # The q8 precision on weights its quantization reproduces exactly, against the f32 path (pinned
-    # against torch above): only the bf16 rounding of every activation separates them.
+    # against torch above): only the bf16 rounding of every activation separates them.  With grouped
+    # heads, an attention narrower than d_model and a condition row added to every frame's input.
+    extra = dict(extra)
+    with_cond = extra.pop("cond", False)
     kw = dict(d_model=512, num_heads=8, num_layers=2, dim_feedforward=1024, flow_dim=512, flow_depth=2, n_bins=50,
               flow_type=flow_type, z_dim=z_dim)
+    kw.update(extra)
     c32 = flow_lm.FlowLMConfig(**kw)
     cq8 = flow_lm.FlowLMConfig(**kw, precision="q8")
     blob = _q8_exact(c32, flow_lm.random_weights(c32, 85, std=0.05, unit_norms=False))
@@ -874,8 +894,9 @@ def test_q8_flow_lm_is_the_f32_one_within_bf16_rounding(flow_type, z_dim):
     worst = 0.0
     for f in range(8):
         noise = (0.5 * rng.standard_normal(c32.ldim)).astype(np.float32)
-        want, we = f32.step(s32, lat, noise)
-        got, ge = q8.step(sq8, lat, noise)  # both from the f32 path's latent: no drift between them
+        cond = bf16_round(0.5 * rng.standard_normal(c32.d_model)) if with_cond else None
+        want, we = f32.step(s32, lat, noise, cond=cond)
+        got, ge = q8.step(sq8, lat, noise, cond=cond)  # both from the f32 path's latent: no drift between them
         err = rel_err(got, want)
         worst = max(worst, err)
         assert err < 4e-2, (f, err)

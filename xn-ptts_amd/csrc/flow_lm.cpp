@@ -31,24 +31,31 @@ struct Layout {
     size_t fin_aw, fin_ab, fin_w, fin_b;
     size_t total;
     int zd; // the width out_eos and cond_embed read: z_dim, else d_model
+    int ad; // the attention's query and output width: attn_dim, else d_model
+    int kd; // its key and value width: ad / num_heads x num_kv_heads
 };
 
 bool layout_of(const xnp_flow_lm_desc &d, Layout &L) {
+    const int ad = d.attn_dim ? d.attn_dim : d.d_model, kvh = d.num_kv_heads ? d.num_kv_heads : d.num_heads;
     if (d.num_layers <= 0 || d.num_layers > kMaxLayers || d.flow_depth < 0 || d.flow_depth > kMaxLayers ||
-        d.d_model <= 0 || d.num_heads <= 0 || d.d_model % d.num_heads || d.ldim <= 0 || d.flow_dim <= 0 ||
-        d.ff <= 0 || d.n_bins <= 0 || d.z_dim < 0 || d.flow_type < XNP_FLOW_LSD || d.flow_type > XNP_FLOW_POINTWISE ||
+        d.d_model <= 0 || d.num_heads <= 0 || d.ldim <= 0 || d.flow_dim <= 0 || d.ff <= 0 || d.n_bins <= 0 ||
+        d.z_dim < 0 || d.attn_dim < 0 || d.num_kv_heads < 0 || ad % d.num_heads || kvh > d.num_heads ||
+        d.num_heads % kvh || d.flow_type < XNP_FLOW_LSD || d.flow_type > XNP_FLOW_POINTWISE ||
         (d.flow_type == XNP_FLOW_LSD && d.lsd_steps <= 0) || (d.precision != XNP_FLOW_F32 && d.precision != XNP_FLOW_Q8))
         return false;
     const size_t dm = d.d_model, F = d.flow_dim, ld = d.ldim, ff = d.ff, fq = kFreqDim;
     const size_t zd = d.z_dim ? (size_t)d.z_dim : dm;
     L.zd = (int)zd;
+    L.ad = ad;
+    L.kd = ad / d.num_heads * kvh; // StreamingMultiheadAttention::load's kv_dim (transformer.rs:162)
+    const size_t qkv = (size_t)L.ad + 2 * (size_t)L.kd;
     size_t o = 0;
     auto take = [&](size_t &field, size_t n) { field = o, o += n; };
     take(L.embed, ((size_t)d.n_bins + 1) * dm);
     take(L.in_lin, dm * ld);
     take(L.bos, ld);
     for (int l = 0; l < d.num_layers; l++) {
-        take(L.ln1_w[l], dm), take(L.ln1_b[l], dm), take(L.wqkv[l], 3 * dm * dm), take(L.wout[l], dm * dm);
+        take(L.ln1_w[l], dm), take(L.ln1_b[l], dm), take(L.wqkv[l], qkv * dm), take(L.wout[l], dm * L.ad);
         take(L.ln2_w[l], dm), take(L.ln2_b[l], dm), take(L.w1[l], ff * dm), take(L.w2[l], dm * ff);
     }
     take(L.on_w, dm), take(L.on_b, dm), take(L.z_proj, d.z_dim ? zd * dm : 0);
@@ -131,7 +138,7 @@ struct Q8Lin {
 struct FlowGraph {
     hipGraphExec_t exec = nullptr;
     int32_t n = 0;
-    const float *latent_in = nullptr, *noise = nullptr;
+    const float *latent_in = nullptr, *noise = nullptr, *cond = nullptr;
     float *latent_out = nullptr, *eos = nullptr;
     hipStream_t stream = nullptr;
     BatchLaunchKey key; // the batch's kernel choice when recorded
@@ -165,6 +172,8 @@ struct xnp_flow_lm {
     uint16_t *bh = nullptr, *bh2 = nullptr;
     int32_t *dids = nullptr;
     int32_t *hids = nullptr; // pinned staging of token ids
+    float *cond_vec = nullptr; // [d_model]: the model's summed conditions (condition_providers)
+    bool has_cond = false;     // cond_vec is set
     std::vector<void *> allocs;
     const float *W(size_t off) const { return w + off; }
 };
@@ -201,11 +210,12 @@ extern "C" xnp_status xnp_flow_lm_create(xnp_pool *pool, const xnp_flow_lm_desc 
         return pool_fail(XNP_E_INVALID, "the f32 flow LM runs on an f32 pool (f32 cache and activations)");
     if (q8 && (pd.cache_dtype != XNP_BF16 || pd.act_dtype != XNP_BF16))
         return pool_fail(XNP_E_INVALID, "the q8 flow LM runs on a bf16 pool (bf16 cache and activations)");
-    if (pd.num_layers != d.num_layers || pd.num_heads != d.num_heads || pd.num_kv_heads != d.num_heads ||
-        pd.head_dim * d.num_heads != d.d_model)
-        return pool_fail(XNP_E_INVALID, "the pool's layers and heads do not match the flow LM's");
+    if (pd.num_layers != d.num_layers || pd.num_heads != d.num_heads ||
+        pd.num_kv_heads != (d.num_kv_heads ? d.num_kv_heads : d.num_heads) || pd.head_dim * d.num_heads != L.ad)
+        return pool_fail(XNP_E_INVALID, "the pool's layers and heads do not match the flow LM's (%d x %d heads of %d "
+                                        "for an attention %d wide)", pd.num_layers, pd.num_heads, pd.head_dim, L.ad);
     if (d.max_rows <= 0) return pool_fail(XNP_E_INVALID, "max_rows %d", d.max_rows);
-    if (d.d_model > 2048 || d.flow_dim > 2048 || d.ff > 2048 || d.ldim > 2048 || L.zd > 2048)
+    if (d.d_model > 2048 || d.flow_dim > 2048 || d.ff > 2048 || d.ldim > 2048 || L.zd > 2048 || L.ad > 2048)
         return pool_fail(XNP_E_INVALID, "widths above 2048 are not supported");
     if (q8 && (d.d_model % 512 || d.flow_dim % 512 || d.ff % 64 || d.ldim % 16 || L.zd % 16))
         return pool_fail(XNP_E_INVALID, "the q8 flow LM takes d_model and flow_dim multiples of 512, ff of 64, "
@@ -237,7 +247,7 @@ extern "C" xnp_status xnp_flow_lm_create(xnp_pool *pool, const xnp_flow_lm_desc 
     struct {
         float **p;
         size_t n;
-    } common[] = {{&lm->w, L.total}, {&lm->temb, (size_t)(steps ? steps : 1) * F}, {&lm->adab, na}};
+    } common[] = {{&lm->w, L.total}, {&lm->temb, (size_t)(steps ? steps : 1) * F}, {&lm->adab, na}, {&lm->cond_vec, dm}};
     for (auto &b : common)
         if ((e = dalloc((void **)b.p, sizeof(float) * b.n)) != hipSuccess) return fail_hip(e, "flow LM buffers");
     if ((e = dalloc((void **)&lm->dids, sizeof(int32_t) * M)) != hipSuccess) return fail_hip(e, "flow LM ids");
@@ -273,7 +283,7 @@ extern "C" xnp_status xnp_flow_lm_create(xnp_pool *pool, const xnp_flow_lm_desc 
         struct {
             float **p;
             size_t n;
-        } bufs[] = {{&lm->x, M * dm}, {&lm->q, M * dm}, {&lm->k, M * dm}, {&lm->v, M * dm}, {&lm->att, M * dm},
+        } bufs[] = {{&lm->x, M * dm}, {&lm->q, M * L.ad}, {&lm->k, M * L.kd}, {&lm->v, M * L.kd}, {&lm->att, M * L.ad},
                     {&lm->f, M * (size_t)d.ff}, {&lm->ya, M * F}, {&lm->ada, M * na}, {&lm->xf, M * F},
                     {&lm->h2, M * F}, {&lm->z, M * zd}, {&lm->adaw, na * F}};
         for (auto &bf : bufs)
@@ -300,8 +310,8 @@ extern "C" xnp_status xnp_flow_lm_create(xnp_pool *pool, const xnp_flow_lm_desc 
     const size_t ff = d.ff;
     if ((e = upload_q8(weights + L.in_lin, dm, ld, lm->in_lin)) != hipSuccess) return fail_hip(e, "q8 weights");
     for (int l = 0; l < d.num_layers; l++) {
-        if ((e = upload_q8(weights + L.wqkv[l], 3 * dm, dm, lm->wqkv[l])) != hipSuccess ||
-            (e = upload_q8(weights + L.wout[l], dm, dm, lm->wout[l])) != hipSuccess ||
+        if ((e = upload_q8(weights + L.wqkv[l], (size_t)L.ad + 2 * (size_t)L.kd, dm, lm->wqkv[l])) != hipSuccess ||
+            (e = upload_q8(weights + L.wout[l], dm, L.ad, lm->wout[l])) != hipSuccess ||
             (e = upload_q8(weights + L.w1[l], ff, dm, lm->w1[l])) != hipSuccess ||
             (e = upload_q8(weights + L.w2[l], dm, ff, lm->w2[l])) != hipSuccess)
             return fail_hip(e, "q8 weights");
@@ -371,21 +381,22 @@ static xnp_status fl_transformer(xnp_flow_lm *lm, int M, void *hip_stream) {
     const xnp_flow_lm_desc &d = lm->d;
     const Layout &L = lm->L;
     hipStream_t hs = (hipStream_t)hip_stream;
-    const int dm = d.d_model, ff = d.ff;
-    const float scale = 1.0f / std::sqrt((float)(dm / d.num_heads));
+    const int dm = d.d_model, ff = d.ff, ad = L.ad, kd = L.kd;
+    const float scale = 1.0f / std::sqrt((float)(ad / d.num_heads)); // 1 / sqrt(head_dim) (transformer.rs:215)
     for (int l = 0; l < d.num_layers; l++) {
         LinNorm n1; // norm1, applied as in_proj reads x
         n1.w = lm->W(L.ln1_w[l]), n1.b = lm->W(L.ln1_b[l]), n1.eps = 1e-5f;
-        LinOut qkv;
+        LinOut qkv; // q [M][ad], then k and v [M][kd] (transformer.rs:195-211)
         qkv.nseg = 3;
-        qkv.out[0] = lm->q, qkv.ld[0] = dm, qkv.col0[0] = 0;
-        qkv.out[1] = lm->k, qkv.ld[1] = dm, qkv.col0[1] = dm;
-        qkv.out[2] = lm->v, qkv.ld[2] = dm, qkv.col0[2] = 2 * dm;
-        FL_TRY(launch_linear_f32(lm->x, dm, M, dm, lm->W(L.wqkv[l]), nullptr, 3 * dm, kLinStore, qkv, hs, &n1), "in_proj");
+        qkv.out[0] = lm->q, qkv.ld[0] = ad, qkv.col0[0] = 0;
+        qkv.out[1] = lm->k, qkv.ld[1] = kd, qkv.col0[1] = ad;
+        qkv.out[2] = lm->v, qkv.ld[2] = kd, qkv.col0[2] = ad + kd;
+        FL_TRY(launch_linear_f32(lm->x, dm, M, dm, lm->W(L.wqkv[l]), nullptr, ad + 2 * kd, kLinStore, qkv, hs, &n1),
+               "in_proj");
         if (xnp_status st = xnp_attend(lm->pool, l, lm->q, lm->k, lm->v, lm->att, scale, hip_stream)) return st;
         LinOut res;
         res.out[0] = lm->x, res.ld[0] = dm;
-        FL_TRY(launch_linear_f32(lm->att, dm, M, dm, lm->W(L.wout[l]), nullptr, dm, kLinResidual, res, hs), "out_proj");
+        FL_TRY(launch_linear_f32(lm->att, ad, M, ad, lm->W(L.wout[l]), nullptr, dm, kLinResidual, res, hs), "out_proj");
         LinNorm n2; // norm2, applied as linear1 reads x
         n2.w = lm->W(L.ln2_w[l]), n2.b = lm->W(L.ln2_b[l]), n2.eps = 1e-5f;
         LinOut hid;
@@ -438,23 +449,28 @@ extern "C" xnp_status xnp_flow_lm_prompt_text(xnp_flow_lm *lm, const int32_t *id
     return xnp_batch_end(lm->pool);
 }
 
-static xnp_status fl_frame_q8(xnp_flow_lm *lm, int M, const float *latent_in, const float *noise, float *latent_out,
-                              float *eos_logit, void *hip_stream);
+static xnp_status fl_frame_q8(xnp_flow_lm *lm, int M, const float *latent_in, const float *cond, const float *noise,
+                              float *latent_out, float *eos_logit, void *hip_stream);
 
 // The frame's device work after the step's plan is uploaded: input_linear, the transformer, the
 // heads and the flow net, all launches on hip_stream (what a graph of the frame records).
-static xnp_status fl_frame_launches(xnp_flow_lm *lm, int M, const float *latent_in, const float *noise,
-                                    float *latent_out, float *eos_logit, void *hip_stream) {
-    if (lm->d.precision == XNP_FLOW_Q8) return fl_frame_q8(lm, M, latent_in, noise, latent_out, eos_logit, hip_stream);
+// cond: each row's condition (stride d_model), else the model's (one row for all), else none.
+static xnp_status fl_frame_launches(xnp_flow_lm *lm, int M, const float *latent_in, const float *cond,
+                                    const float *noise, float *latent_out, float *eos_logit, void *hip_stream) {
+    if (lm->d.precision == XNP_FLOW_Q8)
+        return fl_frame_q8(lm, M, latent_in, cond, noise, latent_out, eos_logit, hip_stream);
     const xnp_flow_lm_desc &d = lm->d;
     const Layout &L = lm->L;
     hipStream_t hs = (hipStream_t)hip_stream;
     const int dm = d.d_model, F = d.flow_dim, ld = d.ldim;
-    // input_linear of the previous latents, or of bos_emb for every row (flow_lm.rs:314-324, 423-427)
+    // input_linear of the previous latents, or of bos_emb for every row (flow_lm.rs:314-324, 423-427),
+    // plus the condition row (flow_lm.rs:304-307): y + c, as out = aux + 1 * y
     LinOut xo;
     xo.out[0] = lm->x, xo.ld[0] = dm;
+    const float *c_rows = cond ? cond : lm->has_cond ? lm->cond_vec : nullptr;
+    if (c_rows) xo.aux = c_rows, xo.ld_aux = cond ? dm : 0, xo.alpha = 1.0f;
     FL_TRY(launch_linear_f32(latent_in ? latent_in : lm->W(L.bos), latent_in ? ld : 0, M, ld, lm->W(L.in_lin), nullptr,
-                             dm, kLinStore, xo, hs),
+                             dm, c_rows ? kLinAxpy : kLinStore, xo, hs),
            "input_linear");
     if (xnp_status st = fl_transformer(lm, M, hip_stream)) return st;
     // out_norm (flow_lm.rs:315), applied as its readers load x: z_proj (flow_lm.rs:320-323) when the
@@ -521,8 +537,8 @@ static xnp_status fl_frame_launches(xnp_flow_lm *lm, int M, const float *latent_
 
 // The q8 frame: the same steps on bf16 rows, the linears on the MFMA GEMM with their epilogues,
 // the transformer as xnp_layer_step, the LayerNorms (and modulations) as kernels of their own.
-static xnp_status fl_frame_q8(xnp_flow_lm *lm, int M, const float *latent_in, const float *noise, float *latent_out,
-                              float *eos_logit, void *hip_stream) {
+static xnp_status fl_frame_q8(xnp_flow_lm *lm, int M, const float *latent_in, const float *cond, const float *noise,
+                              float *latent_out, float *eos_logit, void *hip_stream) {
     const xnp_flow_lm_desc &d = lm->d;
     const Layout &L = lm->L;
     hipStream_t hs = (hipStream_t)hip_stream;
@@ -539,9 +555,11 @@ static xnp_status fl_frame_q8(xnp_flow_lm *lm, int M, const float *latent_in, co
     do {                                                                                           \
         if (xnp_status st_ = (call)) return st_;                                                   \
     } while (0)
-    // input_linear of the previous latents, or of bos_emb for every row (flow_lm.rs:314-324, 423-427)
-    FL_Q(gemm(latent_in ? latent_in : lm->bos_rows, true, ld, lm->in_lin, nullptr, dm, kStore, lm->bx, dm, nullptr, 0,
-              1.f, "input_linear"));
+    // input_linear of the previous latents, or of bos_emb for every row (flow_lm.rs:314-324, 423-427),
+    // plus the condition row (flow_lm.rs:304-307) as a bf16 tensor add: bf16(bf16(c) + y)
+    const float *c_rows = cond ? cond : lm->has_cond ? lm->cond_vec : nullptr;
+    FL_Q(gemm(latent_in ? latent_in : lm->bos_rows, true, ld, lm->in_lin, nullptr, dm, c_rows ? kAddF32 : kStore, lm->bx,
+              dm, c_rows, cond ? dm : 0, 1.f, "input_linear"));
     FL_Q(fl_transformer_q8(lm, hip_stream));
     FL_TRY(launch_layer_norm(lm->bx, M, dm, lm->W(L.on_w), lm->W(L.on_b), 1e-5f, lm->btout, hs), "out_norm");
     const uint16_t *c = lm->btout;
@@ -589,13 +607,27 @@ static xnp_status fl_step_check(xnp_flow_lm *lm, const int32_t *ids, int32_t n, 
     return XNP_OK;
 }
 
+extern "C" xnp_status xnp_flow_lm_set_condition(xnp_flow_lm *lm, const float *cond, int32_t dim) {
+    if (!lm) return pool_fail(XNP_E_INVALID, "null argument");
+    if (!cond) {
+        lm->has_cond = false;
+        return XNP_OK;
+    }
+    if (dim != lm->d.d_model) return pool_fail(XNP_E_INVALID, "a condition of %d values for d_model %d", dim, lm->d.d_model);
+    FL_TRY(hipSetDevice(pool_desc(lm->pool)->device), "hipSetDevice");
+    FL_TRY(hipMemcpy(lm->cond_vec, cond, sizeof(float) * dim, hipMemcpyHostToDevice), "condition upload");
+    lm->has_cond = true;
+    return XNP_OK;
+}
+
 extern "C" xnp_status xnp_flow_lm_step(xnp_flow_lm *lm, const int32_t *ids, int32_t n, const float *latent_in,
-                                       const float *noise, float *latent_out, float *eos_logit, void *hip_stream) {
+                                       const float *conditions, const float *noise, float *latent_out, float *eos_logit,
+                                       void *hip_stream) {
     if (xnp_status st = fl_step_check(lm, ids, n, noise, latent_out, eos_logit)) return st;
     if (n == 0) return XNP_OK;
     FL_TRY(hipSetDevice(pool_desc(lm->pool)->device), "hipSetDevice");
     if (xnp_status st = xnp_batch_begin(lm->pool, ids, n, 1, hip_stream)) return st;
-    if (xnp_status st = fl_frame_launches(lm, n, latent_in, noise, latent_out, eos_logit, hip_stream)) {
+    if (xnp_status st = fl_frame_launches(lm, n, latent_in, conditions, noise, latent_out, eos_logit, hip_stream)) {
         (void)xnp_batch_abort(lm->pool);
         return st;
     }
@@ -603,8 +635,8 @@ extern "C" xnp_status xnp_flow_lm_step(xnp_flow_lm *lm, const int32_t *ids, int3
 }
 
 extern "C" xnp_status xnp_flow_lm_step_graph(xnp_flow_lm *lm, const int32_t *ids, int32_t n, const float *latent_in,
-                                             const float *noise, float *latent_out, float *eos_logit,
-                                             void *hip_stream) {
+                                             const float *conditions, const float *noise, float *latent_out,
+                                             float *eos_logit, void *hip_stream) {
     if (xnp_status st = fl_step_check(lm, ids, n, noise, latent_out, eos_logit)) return st;
     if (n == 0) return XNP_OK;
     if (!hip_stream) return pool_fail(XNP_E_INVALID, "a graph is recorded on a stream of the caller's, not the null stream");
@@ -617,8 +649,10 @@ extern "C" xnp_status xnp_flow_lm_step_graph(xnp_flow_lm *lm, const int32_t *ids
     // the recorded kernels were chosen by the batch that recorded them: a ring prefix taken up since
     // (s2s.rs:174) changes the decode's template, and the plan sets the waves per group
     const BatchLaunchKey key = batch_launch_key(lm->pool);
+    // the condition source is part of the recording: a step's own rows, the model's, or none
+    const float *cond_src = conditions ? conditions : lm->has_cond ? lm->cond_vec : nullptr;
     const bool same = G.exec && G.n == n && G.latent_in == latent_in && G.noise == noise && G.latent_out == latent_out &&
-                      G.eos == eos_logit && G.stream == hs && G.key == key;
+                      G.eos == eos_logit && G.stream == hs && G.key == key && G.cond == cond_src;
     if (!same) {
         if (G.exec) (void)hipGraphExecDestroy(G.exec);
         G = FlowGraph();
@@ -628,7 +662,7 @@ extern "C" xnp_status xnp_flow_lm_step_graph(xnp_flow_lm *lm, const int32_t *ids
             (void)xnp_batch_abort(lm->pool);
             return pool_fail(XNP_E_HIP, "graph capture: %s", hipGetErrorString(e));
         }
-        xnp_status st = fl_frame_launches(lm, n, latent_in, noise, latent_out, eos_logit, hip_stream);
+        xnp_status st = fl_frame_launches(lm, n, latent_in, conditions, noise, latent_out, eos_logit, hip_stream);
         e = hipStreamEndCapture(hs, &graph);
         if (st == XNP_OK && e == hipSuccess) e = hipGraphInstantiate(&G.exec, graph, nullptr, nullptr, 0);
         if (graph) (void)hipGraphDestroy(graph);
@@ -638,6 +672,7 @@ extern "C" xnp_status xnp_flow_lm_step_graph(xnp_flow_lm *lm, const int32_t *ids
             return st != XNP_OK ? st : pool_fail(XNP_E_HIP, "graph capture: %s", hipGetErrorString(e));
         }
         G.n = n, G.latent_in = latent_in, G.noise = noise, G.latent_out = latent_out, G.eos = eos_logit, G.stream = hs;
+        G.cond = cond_src;
         G.key = key;
     }
     hipError_t e = hipGraphLaunch(G.exec, hs);

@@ -272,7 +272,7 @@ __global__ __launch_bounds__(256 * KS) void k_gemm_q8(const uint16_t *A, int M, 
                     xo[e] = *(const uint4 *)((const uint16_t *)go.out[0] + (size_t)mm * go.ld[0] + nn);
                 if constexpr (EPI == kGated)
                     gt[e] = *(const uint4 *)((const uint16_t *)go.aux + (size_t)mm * go.ld_aux + nn);
-                if constexpr (EPI == kAxpyF32) {
+                if constexpr (EPI == kAxpyF32 || EPI == kAddF32) {
                     ax[e][0] = *(const float4 *)((const float *)go.aux + (size_t)mm * go.ld_aux + nn);
                     ax[e][1] = *(const float4 *)((const float *)go.aux + (size_t)mm * go.ld_aux + nn + 4);
                 }
@@ -421,6 +421,14 @@ __global__ __launch_bounds__(256 * KS) void k_gemm_q8(const uint16_t *A, int M, 
                 float *o = (float *)go.out[0] + (size_t)m * go.ld[0] + ne;
                 *(float4 *)o = make_float4(r8[0], r8[1], r8[2], r8[3]);
                 *(float4 *)(o + 4) = make_float4(r8[4], r8[5], r8[6], r8[7]);
+            } else if constexpr (EPI == kAddF32) {
+                const float cu[8] = {ax[e][0].x, ax[e][0].y, ax[e][0].z, ax[e][0].w,
+                                     ax[e][1].x, ax[e][1].y, ax[e][1].z, ax[e][1].w};
+                float r8[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) r8[i] = bf16_value(bf16_bits(cu[i])) + y[i];
+                *(uint4 *)((uint16_t *)go.out[0] + (size_t)m * go.ld[0] + ne) =
+                    make_uint4(pack_bf16(r8[0], r8[1]), pack_bf16(r8[2], r8[3]), pack_bf16(r8[4], r8[5]), pack_bf16(r8[6], r8[7]));
             } else {
                 float r8[8];
                 const uint32_t *xw = (const uint32_t *)&xo[e], *gw = (const uint32_t *)&gt[e];
@@ -498,6 +506,9 @@ __global__ __launch_bounds__(256 * KS) void k_gemm_q8(const uint16_t *A, int M, 
                     const float cur = bf16_value(bf16_bits(((const float *)go.aux)[(size_t)m * go.ld_aux + n]));
                     ((float *)go.out[0])[(size_t)m * go.ld[0] + n] =
                         bf16_value(bf16_bits(cur + bf16_value(bf16_bits(y * go.alpha))));
+                } else if constexpr (EPI == kAddF32) {
+                    const float c = bf16_value(bf16_bits(((const float *)go.aux)[(size_t)m * go.ld_aux + n]));
+                    ((uint16_t *)go.out[0])[(size_t)m * go.ld[0] + n] = (uint16_t)bf16_bits(c + y);
                 } else { // kStoreF32
                     ((float *)go.out[0])[(size_t)m * go.ld[0] + n] = y;
                 }
@@ -512,7 +523,7 @@ static bool gemm_staged(int N, int epi, const GemmOut &go) {
     const int nout = epi == kStore ? go.nseg : 1;
     for (int j = 0; j < nout; ++j)
         if (!go.out[j] || go.ld[j] % 8 || (uintptr_t)go.out[j] % 16 || (epi == kStore && go.col0[j] % 8)) return false;
-    if ((epi == kGated || epi == kAxpyF32) && (go.ld_aux % 8 || (uintptr_t)go.aux % 16)) return false;
+    if ((epi == kGated || epi == kAxpyF32 || epi == kAddF32) && (go.ld_aux % 8 || (uintptr_t)go.aux % 16)) return false;
     if (epi == kSiluAddVec && (uintptr_t)go.aux % 16) return false;
     if (epi == kResidual && go.ls && (uintptr_t)go.ls % 16) return false;
     return true;
@@ -525,8 +536,11 @@ static hipError_t gemm_q8_stg(const void *A, int M, int K, const int8_t *W, cons
     const uint16_t *a = (const uint16_t *)A;
 #define XNP_GEMM(E) hipLaunchKernelGGL((k_gemm_q8<E, false, MI, KS, STG, NKC>), grid, block, 0, stream, a, M, K, W, s, N, go)
     if (go.a_f32) {
-        if (epi != kStore || NKC != 0) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((k_gemm_q8<kStore, true, MI, KS, STG, 0>), grid, block, 0, stream, a, M, K, W, s, N, go);
+        if ((epi != kStore && epi != kAddF32) || NKC != 0) return hipErrorInvalidValue;
+        if (epi == kStore)
+            hipLaunchKernelGGL((k_gemm_q8<kStore, true, MI, KS, STG, 0>), grid, block, 0, stream, a, M, K, W, s, N, go);
+        else
+            hipLaunchKernelGGL((k_gemm_q8<kAddF32, true, MI, KS, STG, 0>), grid, block, 0, stream, a, M, K, W, s, N, go);
         return hipGetLastError();
     }
     switch (epi) {
@@ -539,6 +553,7 @@ static hipError_t gemm_q8_stg(const void *A, int M, int K, const int8_t *W, cons
     case kGated: XNP_GEMM(kGated); break;
     case kAxpyF32: XNP_GEMM(kAxpyF32); break;
     case kStoreF32: XNP_GEMM(kStoreF32); break;
+    case kAddF32: XNP_GEMM(kAddF32); break;
     default: return hipErrorInvalidValue;
     }
 #undef XNP_GEMM

@@ -1522,12 +1522,16 @@ extern "C" xnp_status xnp_flow_linear_q8(const void *x, int32_t x_f32, int32_t r
                                          void *hip_stream) {
     if (rows < 0 || k <= 0 || n <= 0 || k % 16 || ldy < n)
         return fail(XNP_E_INVALID, "a q8 linear of %d x %d by %d into rows of %d: k a multiple of 16", rows, k, n, ldy);
-    if (epilogue < XNP_EPI_STORE || epilogue > XNP_EPI_STORE_F32) return fail(XNP_E_INVALID, "epilogue %d", epilogue);
-    if (x_f32 && epilogue != XNP_EPI_STORE) return fail(XNP_E_INVALID, "an f32 x takes the store epilogue");
-    const bool needs_aux = epilogue == XNP_EPI_SILU_ADD || epilogue == XNP_EPI_GATED || epilogue == XNP_EPI_AXPY_F32;
+    if (epilogue < XNP_EPI_STORE || epilogue > XNP_EPI_ADD_F32) return fail(XNP_E_INVALID, "epilogue %d", epilogue);
+    if (x_f32 && epilogue != XNP_EPI_STORE && epilogue != XNP_EPI_ADD_F32)
+        return fail(XNP_E_INVALID, "an f32 x takes the store or add epilogue");
+    const bool needs_aux = epilogue == XNP_EPI_SILU_ADD || epilogue == XNP_EPI_GATED || epilogue == XNP_EPI_AXPY_F32 ||
+                           epilogue == XNP_EPI_ADD_F32;
     if (rows > 0 && (!x || !w || !s || !y || (needs_aux && !aux))) return fail(XNP_E_INVALID, "null argument");
     if ((epilogue == XNP_EPI_GATED || epilogue == XNP_EPI_AXPY_F32) && ld_aux < n)
         return fail(XNP_E_INVALID, "aux rows of %d for %d columns", ld_aux, n);
+    if (epilogue == XNP_EPI_ADD_F32 && ld_aux != 0 && ld_aux < n)
+        return fail(XNP_E_INVALID, "aux rows of %d for %d columns (0: one row for every row)", ld_aux, n);
     GemmOut go;
     go.out[0] = y, go.ld[0] = ldy, go.bias = bias, go.aux = aux, go.ld_aux = ld_aux, go.alpha = alpha;
     go.a_f32 = x_f32 != 0;

@@ -160,10 +160,11 @@ hipError_t launch_copy_page(const PoolView &pv, int src_page, int dst_page, hipS
 //   kStore out = y; kGelu* out = bf16(gelu(y)); kResidual out = bf16(out + y (* ls[n], rounded));
 //   kSilu out = bf16(silu(y)); kSiluAddVec z = bf16(y + aux[n]) (f32), out = bf16(silu(z));
 //   kGated out = bf16(out + bf16(aux[m][n] * y)) (aux bf16, the AdaLN gate); kAxpyF32 out (f32) =
-//   bf16(bf16(aux[m][n]) + bf16(y * alpha)) (aux f32); kStoreF32 out (f32) = y.
+//   bf16(bf16(aux[m][n]) + bf16(y * alpha)) (aux f32); kStoreF32 out (f32) = y; kAddF32 out (bf16) =
+//   bf16(bf16(aux[m][n]) + y) (aux f32, ld_aux 0 for one row: a condition broadcast-added).
 enum : int32_t {
     kStore = 0, kGeluErf = 1, kGeluTanh = 2, kResidual = 3, kSilu = 4, kSiluAddVec = 5, kGated = 6, kAxpyF32 = 7,
-    kStoreF32 = 8
+    kStoreF32 = 8, kAddF32 = 9
 };
 
 // Where a q8 projection writes.  kStore: columns [col0[j], col0[j+1]) go to out[j] (row stride
@@ -179,7 +180,7 @@ struct GemmOut {
     const void *aux = nullptr;   // the epilogue's operand (see above)
     int32_t ld_aux = 0;
     float alpha = 1.f;
-    bool a_f32 = false;          // A holds f32, rounded to bf16 as it is staged (kStore only)
+    bool a_f32 = false;          // A holds f32, rounded to bf16 as it is staged (kStore and kAddF32 only)
 };
 
 hipError_t launch_layer_norm(const void *x, int rows, int dim, const float *w, const float *b, float eps, void *out,

@@ -26,8 +26,9 @@ PRECISIONS = {"f32": 0, "q8": 1}
 
 @dataclass
 class FlowLMConfig:
-    """FlowLMConfig (flow_lm.rs:114-146) restricted to what this build runs: no attn_dim override,
-    no grouped heads, no layer scale, no conditions or sinks.  z_dim 0: no z_proj."""
+    """FlowLMConfig (flow_lm.rs:114-146).  z_dim 0: no z_proj; attn_dim 0: d_model; num_kv_heads 0:
+    num_heads.  (FlowLM's transformer has no layer scale, flow_lm.rs:239-249; conditions are given at
+    run time, FlowLM.set_condition and the conditions of FlowLM.step.)"""
     d_model: int = 512
     num_heads: int = 8
     num_layers: int = 6
@@ -43,16 +44,20 @@ class FlowLMConfig:
     z_dim: int = 0
     flow_type: str = "lsd"
     precision: str = "f32"
+    attn_dim: int = 0
+    num_kv_heads: int = 0
 
 
 def layout(cfg: FlowLMConfig):
     """The weight blob's tensors in order: (name, shape).  Every tensor is f32, row-major
     [out][in] for linears."""
     d, F, ld, ff = cfg.d_model, cfg.flow_dim, cfg.ldim, cfg.dim_feedforward
+    a = cfg.attn_dim or d  # StreamingMultiheadAttention::load (transformer.rs:155-166)
+    kv = a // cfg.num_heads * (cfg.num_kv_heads or cfg.num_heads)
     out = [("conditioner.embed", (cfg.n_bins + 1, d)), ("input_linear", (d, ld)), ("bos_emb", (ld,))]
     for i in range(cfg.num_layers):
         p = f"layers.{i}."
-        out += [(p + "norm1.w", (d,)), (p + "norm1.b", (d,)), (p + "in_proj", (3 * d, d)), (p + "out_proj", (d, d)),
+        out += [(p + "norm1.w", (d,)), (p + "norm1.b", (d,)), (p + "in_proj", (a + 2 * kv, d)), (p + "out_proj", (d, a)),
                 (p + "norm2.w", (d,)), (p + "norm2.b", (d,)), (p + "linear1", (ff, d)), (p + "linear2", (d, ff))]
     zd = cfg.z_dim or d
     out += [("out_norm.w", (d,)), ("out_norm.b", (d,))]
@@ -114,7 +119,7 @@ def random_weights(cfg: FlowLMConfig, seed: int, std: float = 0.02, unit_norms: 
 class FlowLMDesc(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in (
         "d_model", "num_heads", "num_layers", "ff", "ldim", "n_bins", "flow_dim", "flow_depth", "lsd_steps",
-        "gelu", "time_norm", "max_rows", "z_dim", "flow_type", "precision")]
+        "gelu", "time_norm", "max_rows", "z_dim", "flow_type", "precision", "num_kv_heads", "attn_dim")]
 
 
 def desc_of(cfg: FlowLMConfig, max_rows: int = 1) -> FlowLMDesc:
@@ -123,7 +128,7 @@ def desc_of(cfg: FlowLMConfig, max_rows: int = 1) -> FlowLMDesc:
                       flow_depth=cfg.flow_depth, lsd_steps=cfg.lsd_decode_steps,
                       gelu=0 if cfg.gelu == "erf" else 1, time_norm=0 if cfg.time_rms_norm == "rms" else 1,
                       max_rows=max_rows, z_dim=cfg.z_dim, flow_type=FLOW_TYPES[cfg.flow_type],
-                      precision=PRECISIONS[cfg.precision])
+                      precision=PRECISIONS[cfg.precision], num_kv_heads=cfg.num_kv_heads, attn_dim=cfg.attn_dim)
 
 
 class FlowLM:
@@ -160,11 +165,21 @@ class FlowLM:
         _check(self._lib.xnp_flow_lm_prompt_text(self._h, arr, len(ids), tokens.ctypes.data, tokens.shape[1],
                                                  _stream(stream)))
 
-    def step(self, ids, latent_in, noise, latent_out, eos_out, stream=None, graph: bool = False):
+    def set_condition(self, cond):
+        """The model's summed conditions (condition_providers, flow_lm.rs:218-222): cond [d_model]
+        host values, or None for none."""
+        if cond is None:
+            _check(self._lib.xnp_flow_lm_set_condition(self._h, None, 0))
+            return
+        c = np.ascontiguousarray(cond, np.float32)
+        _check(self._lib.xnp_flow_lm_set_condition(self._h, c.ctypes.data, c.size))
+
+    def step(self, ids, latent_in, noise, latent_out, eos_out, stream=None, graph: bool = False, conditions=None):
         """One frame for each stream: latent_in [n][ldim] (None: bos_emb), noise [n][ldim],
-        latent_out [n][ldim], eos_out [n] -- f32 device tensors.  graph: replay a recording of the
-        frame's launches (xnp_flow_lm_step_graph; needs a non-null stream)."""
+        latent_out [n][ldim], eos_out [n], conditions [n][d_model] (each stream's
+        FlowLMState::conditions; None: the model's, if set) -- f32 device tensors.  graph: replay a
+        recording of the frame's launches (xnp_flow_lm_step_graph; needs a non-null stream)."""
         arr = (ctypes.c_int32 * len(ids))(*ids)
         fn = self._lib.xnp_flow_lm_step_graph if graph else self._lib.xnp_flow_lm_step
-        _check(fn(self._h, arr, len(ids), _ptr(latent_in), _ptr(noise), _ptr(latent_out), _ptr(eos_out),
-                  _stream(stream)))
+        _check(fn(self._h, arr, len(ids), _ptr(latent_in), _ptr(conditions), _ptr(noise), _ptr(latent_out),
+                  _ptr(eos_out), _stream(stream)))

@@ -118,8 +118,9 @@ SIGNATURES = {
     "xnp_flow_lm_create": (_i32, [_p, _p, _p, _c.c_int64, _c.POINTER(_p)]),
     "xnp_flow_lm_destroy": (_i32, [_p]),
     "xnp_flow_lm_prompt_text": (_i32, [_p, _i32p, _i32, _p, _i32, _p]),
-    "xnp_flow_lm_step": (_i32, [_p, _i32p, _i32, _p, _p, _p, _p, _p]),
-    "xnp_flow_lm_step_graph": (_i32, [_p, _i32p, _i32, _p, _p, _p, _p, _p]),
+    "xnp_flow_lm_set_condition": (_i32, [_p, _p, _i32]),
+    "xnp_flow_lm_step": (_i32, [_p, _i32p, _i32, _p, _p, _p, _p, _p, _p]),
+    "xnp_flow_lm_step_graph": (_i32, [_p, _i32p, _i32, _p, _p, _p, _p, _p, _p]),
     "xnp_frame_budget": (_i32, [_i32, _c.c_double]),
     "xnp_seq_budget": (_i32, [_i32, _i32]),
     "xnp_last_error": (_c.c_char_p, []),
@@ -436,7 +437,7 @@ class KvPool:
 # ---- the rest of the layer (transformer.rs:591-634) ---------------------------------------------
 GELU = {"erf": 0, "tanh": 1}
 EPILOGUES = {"store": 0, "gelu_erf": 1, "gelu_tanh": 2, "residual": 3, "silu": 4, "silu_add": 5, "gated": 6,
-             "axpy_f32": 7, "store_f32": 8}
+             "axpy_f32": 7, "store_f32": 8, "add_f32": 9}
 
 
 class LayerWeights:
@@ -476,7 +477,7 @@ def linear_q8(x, w, s, y, epilogue: str = "store", ls=None, stream=None):
 
 
 def flow_linear_q8(x, w, s, y, epilogue: str = "store", bias=None, aux=None, alpha: float = 1.0, stream=None):
-    """xnp_flow_linear_q8: x [rows][k] bf16 or f32 (f32: rounded as read, store only), w [n][k] int8,
+    """xnp_flow_linear_q8: x [rows][k] bf16 or f32 (f32: rounded as read; store or add_f32), w [n][k] int8,
     s [n], y [rows][>= n] (bf16, or f32 for axpy_f32 / store_f32); aux per the epilogue."""
     k = x.shape[-1]
     rows = x.numel() // k
