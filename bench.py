@@ -394,8 +394,10 @@ def run_prefill(args, xnp, torch):
     roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic_of("prefill", {"streams": S, "prompt": T, "layers": L}, hbm),
-            "kernel": "k_prefill_mfma (fused append + RoPE + causal attention on v_mfma_f32_16x16x32_bf16), "
-                      "one launch per layer",
+            "kernel": ("k_prefill_fast (fused append + RoPE + causal attention on v_mfma_f32_16x16x32_bf16, every "
+                       "key of a prompt held in LDS), one launch per layer" if T <= 256 else
+                       "k_prefill_mfma (fused append + RoPE + causal attention on v_mfma_f32_16x16x32_bf16, keys "
+                       "streamed through LDS), one launch per layer"),
             "avg_kernel_us": round(avg_ms * 1000.0, 2), "bytes_per_launch": hbm,
             "mfma": {"achieved": round(tflops, 2), "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4), "flops_per_launch": flops}}
@@ -757,7 +759,8 @@ def run_frame(args, xnp, torch):
                           f"from one hipGraph after its plan upload",
               "streams": S, "layers": L, "d_model": DM, "ff": FF, "flow": "512 x 6"}
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic_of("frame", {"streams": S, "layers": L, "max_len": args.step_max_len}, float(np.mean(bts))),
             "kernel": "k_decode<bf16> (fused append + RoPE + decode) of layer 0, timed in eager frames",
             "avg_kernel_us": round(avg_ms * 1000.0, 2), "bytes_per_launch": int(np.mean(bts)),
             "decode_share_of_frame": round(L * avg_ms / ms, 3)}
