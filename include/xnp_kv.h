@@ -303,8 +303,12 @@ xnp_status xnp_layer_step(xnp_pool *pool, int32_t layer, const xnp_layer_weights
  * forbid hipMalloc.  The scratch is a fixed array of XNP_STATIC_SCRATCH_BYTES inside the library,
  * one per device, held until the process ends; a step needing more (xnp_layer_workspace) is refused
  * with XNP_E_INVALID.  The call allocates nothing, host or device.  Every call on one device shares
- * that device's array: calls that overlap on one GPU (two pools, two host threads, two streams)
- * race, so the caller orders them.  Nothing in the array needs to start at zero (every byte a step
+ * that device's array, so calls must not overlap: a call is refused with XNP_E_STATE, running
+ * nothing, while another call is issuing its launches (another host thread, any pool or stream) or
+ * while the last call's work on another HIP stream may still be running (it waits for nothing).
+ * Calls ordered on one stream from one thread, or synchronized between, always proceed; a call being
+ * captured into a hipGraph is not checked against others, and the caller orders the graph's launches
+ * with the other users of the array.  Nothing in the array needs to start at zero (every byte a step
  * reads it wrote first in the same call), so the previous call's contents do not matter. */
 #define XNP_STATIC_SCRATCH_BYTES (24u << 20) /* the 2048-row step of a 512-wide, FF 2048 layer takes 18 MiB */
 xnp_status xnp_layer_step_static(xnp_pool *pool, int32_t layer, const xnp_layer_weights *w, void *x,

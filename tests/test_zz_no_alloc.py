@@ -107,6 +107,38 @@ def test_a_step_too_large_for_the_static_scratch_is_refused_and_changes_nothing(
     assert all(pool.info(i)["current_end"] == 0 for i in ids)
 
 
+def test_a_call_that_fails_inside_the_step_lets_go_of_the_static_scratch():
+    # A call holds the device's array from its claim to its release, so that no other call (another
+    # host thread's, on any stream) interleaves launches with it.  A call that fails after its claim
+    # (no batch open; a layer out of range) releases it too: the next call takes it and its step
+    # equals the workspace step of an identical pool.
+    rng = np.random.default_rng(20261210)
+    W = [weights(rng) for _ in range(L)]
+    S, cap = 8, 64
+    a, c = make_pool(S, cap), make_pool(S, cap)
+    ia, ic = ([p.init_state(cap) for _ in range(S)] for p in (a, c))
+    x0 = normal(rng, (S, 1, DM), "bf16")
+    xa, xc = dev(x0), dev(x0)
+    torch.cuda.synchronize()
+    a.begin(ia, t=1)
+    a.abort()
+    with pytest.raises(xnp.XnpError) as e:
+        a.layer_step_static(0, W[0], xa)  # no batch is open
+    assert e.value.name == "XNP_E_STATE" and "no batch" in e.value.message
+    a.begin(ia, t=1)
+    with pytest.raises(xnp.XnpError) as e:
+        a.layer_step_static(L, W[0], xa)  # no such layer
+    assert e.value.name == "XNP_E_INVALID" and "layer" in e.value.message
+    a.layer_step_static(0, W[0], xa)
+    a.end()
+    ws = torch.empty(c.layer_workspace(S, DM, FF), dtype=torch.uint8, device=DEV)
+    c.begin(ic, t=1)
+    c.layer_step(0, W[0], xc, ws)
+    c.end()
+    torch.cuda.synchronize()
+    assert torch.equal(xa.view(torch.int16), xc.view(torch.int16))
+
+
 def test_a_call_on_another_stream_is_refused_while_the_last_one_may_still_run():
     # One array per device: pool b's call on HIP stream B, made while pool a's call on stream A is
     # still queued behind a sleep, is refused (XNP_E_STATE) and runs nothing; once A's work is done,

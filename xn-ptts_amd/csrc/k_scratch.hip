@@ -17,10 +17,13 @@ static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
 constexpr int kScratchDevices = 64;
 static void *g_scratch_addr[kScratchDevices];
 // The stream of the last call on each device's array and an event recorded behind that call's
-// launches: a call on another stream while that work runs would share the array with it.
+// launches: a call on another stream while that work runs would share the array with it.  g_held:
+// a call is between its claim and its release (its launches are being issued), so any other call,
+// on any stream, would interleave its launches with them.
 static hipStream_t g_owner_stream[kScratchDevices];
 static hipEvent_t g_owner_done[kScratchDevices];
 static bool g_owner_used[kScratchDevices];
+static bool g_held[kScratchDevices];
 static std::mutex g_scratch_mu;
 
 hipError_t static_scratch_init(int device) {
@@ -47,15 +50,20 @@ ScratchClaim static_scratch_claim(int device, hipStream_t stream, bool capturing
     if (device < 0 || device >= kScratchDevices) return ScratchClaim::kError;
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (!g_scratch_addr[device]) return ScratchClaim::kError;
-    if (capturing || !g_owner_used[device] || g_owner_stream[device] == stream) return ScratchClaim::kOk;
-    const hipError_t e = hipEventQuery(g_owner_done[device]);
-    if (e == hipSuccess) return ScratchClaim::kOk;
-    return e == hipErrorNotReady ? ScratchClaim::kBusy : ScratchClaim::kError;
+    if (g_held[device]) return ScratchClaim::kBusy;
+    if (!capturing && g_owner_used[device] && g_owner_stream[device] != stream) {
+        const hipError_t e = hipEventQuery(g_owner_done[device]);
+        if (e == hipErrorNotReady) return ScratchClaim::kBusy;
+        if (e != hipSuccess) return ScratchClaim::kError;
+    }
+    g_held[device] = true;
+    return ScratchClaim::kOk;
 }
 
 hipError_t static_scratch_release(int device, hipStream_t stream, bool capturing) {
     if (device < 0 || device >= kScratchDevices) return hipErrorInvalidDevice;
     std::lock_guard<std::mutex> lock(g_scratch_mu);
+    g_held[device] = false;
     if (capturing) return hipSuccess; // a captured call's order is the graph's
     const hipError_t e = hipEventRecord(g_owner_done[device], stream);
     if (e != hipSuccess) return e;

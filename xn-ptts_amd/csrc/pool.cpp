@@ -1654,8 +1654,9 @@ extern "C" xnp_status xnp_layer_step_static(xnp_pool *pool, int32_t layer, const
             return fail(XNP_E_INVALID, "the step of %lld rows needs %llu bytes of scratch; the static scratch holds %llu",
                         (long long)rows, (unsigned long long)need, (unsigned long long)kStaticScratchBytes);
     }
-    // one user of the device's array at a time: a call on another stream than the last one waits for
-    // nothing and is refused while that call's work may still be running
+    // one user of the device's array at a time: a call is refused while another call is issuing its
+    // launches, or while the last call's work on another stream may still be running (it waits for
+    // nothing)
     hipStream_t hs = (hipStream_t)hip_stream;
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     HIP_TRY(hipStreamIsCapturing(hs, &cap), "hipStreamIsCapturing");
@@ -1663,11 +1664,14 @@ extern "C" xnp_status xnp_layer_step_static(xnp_pool *pool, int32_t layer, const
     switch (static_scratch_claim(pool->d.device, hs, capturing)) {
     case ScratchClaim::kOk: break;
     case ScratchClaim::kBusy:
-        return fail(XNP_E_STATE, "the static scratch of device %d is in use by a call on another HIP stream that has not "
-                                 "finished; synchronize with it or call on the same stream", pool->d.device);
+        return fail(XNP_E_STATE, "the static scratch of device %d is in use by another call (one still issuing its "
+                                 "launches, or one on another HIP stream that has not finished); synchronize with it "
+                                 "or order the calls on one stream from one thread", pool->d.device);
     default: return fail(XNP_E_STATE, "the static scratch of device %d cannot be claimed", pool->d.device);
     }
-    if (xnp_status st = layer_step_impl(pool, layer, w, x, scr, kStaticScratchBytes, hip_stream)) return st;
-    HIP_TRY(static_scratch_release(pool->d.device, hs, capturing), "recording the static scratch's last use");
+    const xnp_status st = layer_step_impl(pool, layer, w, x, scr, kStaticScratchBytes, hip_stream);
+    const hipError_t rel = static_scratch_release(pool->d.device, hs, capturing); // on every path
+    if (st) return st;
+    HIP_TRY(rel, "recording the static scratch's last use");
     return XNP_OK;
 }

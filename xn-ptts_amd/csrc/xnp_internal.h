@@ -92,10 +92,13 @@ struct LaunchTiming {
 constexpr uint64_t kStaticScratchBytes = XNP_STATIC_SCRATCH_BYTES;
 hipError_t static_scratch_init(int device);
 void *static_scratch(int device);
-// Calls on one device's array from different streams must not overlap.  claim: kOk when the last
-// call was on `stream`, or its work (on another stream) has finished, or the call is being captured
-// (a graph's order is its own); kBusy while another stream's call may still be using the array.
-// release: after the call's launches, record its completion on `stream` (nothing when capturing).
+// Calls on one device's array must not overlap.  claim: kBusy while another call holds the array
+// (between its claim and its release: its launches are being issued, from any host thread) or
+// while a call on another stream may still be running on the device; otherwise the array is held
+// and kOk (the last call on `stream` itself is ordered before this one by the stream; a call being
+// captured runs only when its graph is launched, in the graph's order).  release: after the call's
+// launches, on every path once claimed, let go of the array and record its completion on `stream`
+// (nothing recorded when capturing).
 enum class ScratchClaim { kOk, kBusy, kError };
 ScratchClaim static_scratch_claim(int device, hipStream_t stream, bool capturing);
 hipError_t static_scratch_release(int device, hipStream_t stream, bool capturing);
