@@ -283,15 +283,17 @@ def test_grouped_heads_on_rings(cache, act, mode):
         p.assert_cache_equal(i)
 
 
+@pytest.mark.parametrize("cache", ["bf16", "i8"])
 @pytest.mark.parametrize("h", [8, 16])
-def test_grouped_heads_on_prefix_rings_take_the_mfma_decode(h):
+def test_grouped_heads_on_prefix_rings_take_the_mfma_decode(cache, h):
     # 8 and 16 query heads over one kv head (the MFMA decode of a whole kv head) on absolute rings
     # with voice prefixes of 0, 5 and 20 rows (20: the prefix ends inside the second page), so that
     # the batch keeps a second query position: keys before a stream's prefix are scored against its
     # query at pos_pre (transformer.rs:879-929 restated as the absolute ring), the others at pos.
+    # int8 pages score both positions in f16, each query with its own power of two and sum.
     # Frames slide over a context of 40 slots with the oldest evicted, 60 steps, every output held to
-    # the oracle and every cache row bit-exact.
-    p = Pair(cache="bf16", act="bf16", H=h, KVH=1, streams=3, cap=96, seed=70 + h)
+    # the oracle and every cache row (int8: codes and scales) bit-exact.
+    p = Pair(cache=cache, act="bf16", H=h, KVH=1, streams=3, cap=96, seed=70 + h)
     prefixes, context = [0, 5, 20], 40
     for i, pre in enumerate(prefixes):
         p.fill(i, pre)
@@ -309,7 +311,7 @@ def test_grouped_heads_on_prefix_rings_take_the_mfma_decode(h):
         worst = max(worst, p.step())
     for i in range(3):
         p.assert_cache_equal(i)
-    assert worst <= TOL["bf16"]
+    assert worst <= TOL[cache]
 
 
 def test_empty_batch_is_a_no_op():
@@ -625,7 +627,8 @@ def test_int8_pools_take_queries_beyond_the_f16_range(kvh, qscale):
     # int8 pages with bf16 activations take the query as f16, scaled by a power of two that fits
     # it: queries of N(0, 1) x 2^17 (components past f16's 65504) and x 2^-20 (below its normal
     # range) on the VALU decode (8 kv heads) and the MFMA one (2 kv heads, 4 query heads each),
-    # after a 9-row prompt through the prompt-row kernel: outputs to the oracle, caches bit-exact
+    # after a 9-row prompt through the MFMA prefill (f16 scores, each query row's own power of two):
+    # outputs to the oracle, caches bit-exact
     p = Pair(cache="i8", act="bf16", H=8, KVH=kvh, streams=3, cap=96, seed=50)
     for i, n in enumerate([0, 20, 47]):
         p.fill(i, n)
@@ -1103,14 +1106,16 @@ def test_prefill_of_a_grouped_head_prompt_at_config3_shape_sample():
 
 def test_the_prefill_configuration_at_full_size_spot_checked():
     # The prefill workload at its full size: 64 streams x 256-position prompts x 9 layers, bf16,
-    # shuffled pages; every stream runs, 8 of them go through the oracle: outputs within 2e-2, then
-    # every cache row the prompt wrote bit-exact.
+    # shuffled pages; every stream runs, 8 of them go through the oracle on every layer, and every
+    # stream's layer 0 goes through a one-layer oracle stream of its own: outputs within 2e-2, then
+    # every cache row the prompt wrote bit-exact (all layers of the sample, layer 0 of every stream).
     S, L, H, T = 64, 9, 8, 256
     pool = xnp.KvPool(num_layers=L, num_heads=H, num_blocks=S * 17 + 8, max_streams=S, max_blocks_per_stream=17,
                       cache_dtype="bf16", act_dtype="bf16", max_pos=1024, page_seed=21)
     ids = [pool.init_state(272) for _ in range(S)]
     sample = list(range(0, S, 9))
     orc = {i: oracle.Stream(L, H, 64, 272, cache="bf16", act="bf16") for i in sample}
+    every = {i: oracle.Stream(1, H, 64, 272, cache="bf16", act="bf16") for i in range(S)}
     g = torch.Generator(device=DEV).manual_seed(20261206)
     pool.begin(ids, t=T)
     for layer in range(L):
@@ -1118,16 +1123,26 @@ def test_the_prefill_configuration_at_full_size_spot_checked():
         out = torch.empty((S, T, H, 64), dtype=torch.bfloat16, device=DEV)
         pool.attend(layer, q, k, v, out, 0.125)
         torch.cuda.synchronize()
-        got, qh, kh, vh = host(out[sample]), host(q[sample]), host(k[sample]), host(v[sample])
-        for j, i in enumerate(sample):
-            want, _ = orc[i].attend(layer, qh[j], kh[j], vh[j])
-            assert rel_err(got[j], want) <= 2e-2, (layer, i)
+        rows = range(S) if layer == 0 else sample
+        got, qh, kh, vh = host(out), host(q), host(k), host(v)
+        for i in rows:
+            if i in orc:
+                want, _ = orc[i].attend(layer, qh[i], kh[i], vh[i])
+                assert rel_err(got[i], want) <= 2e-2, (layer, i)
+            if layer == 0:
+                want, _ = every[i].attend(0, qh[i], kh[i], vh[i])
+                assert rel_err(got[i], want) <= 2e-2, (layer, i, "every")
     pool.end()
     for i in sample:
         orc[i].commit(T)
+    for i in range(S):
+        every[i].commit(T)
     shim = types.SimpleNamespace(pool=pool, ids=ids, orc=orc, L=L, H=H, KVH=H, cache="bf16")
     for i in sample:
         Pair.assert_cache_equal(shim, i)
+    shim0 = types.SimpleNamespace(pool=pool, ids=ids, orc=every, L=1, H=H, KVH=H, cache="bf16")
+    for i in range(S):
+        Pair.assert_cache_equal(shim0, i)
 
 
 def test_prompts_on_reopened_streams_use_live_pages():
@@ -1157,10 +1172,12 @@ def test_prefill_after_a_separate_append(cache, act):
     p.step()
 
 
-def test_long_prompts_take_several_rounds():
+@pytest.mark.parametrize("cache", ["bf16", "i8"])
+def test_long_prompts_take_several_rounds(cache):
     # 300- and 530-row prompts: more than one round of 256 query rows per work group, on top of
-    # prior rows that end mid-page; grouped heads
-    p = Pair(cache="bf16", act="bf16", H=8, KVH=2, streams=2, cap=640, seed=25, L=1, page_seed=10)
+    # prior rows that end mid-page; grouped heads.  int8 pages: the MFMA prefill after the append,
+    # scores in f16 against the codes, each page's scales applied per 16-key group
+    p = Pair(cache=cache, act="bf16", H=8, KVH=2, streams=2, cap=640, seed=25, L=1, page_seed=10)
     p.fill(1, 21)
     assert p.prefill(300, which=[0]) <= 2e-2
     assert p.prefill(530, which=[1]) <= 2e-2
@@ -1189,8 +1206,8 @@ def test_streams_at_the_longest_a_pool_takes(cache, act, kvh):
 @pytest.mark.parametrize("cache,act", [("bf16", "bf16"), ("i8", "bf16"), ("f32", "f32")])
 def test_a_prompt_that_fills_the_longest_stream(cache, act):
     # 7580 rows (ending mid-page), then a 100-row prompt ending on the last slot of page 480: the
-    # prompt reads every page id of the stream (the MFMA prefill keeps them in LDS; int8 and f32
-    # take the row-by-row prompt kernel after the append)
+    # prompt reads every page id of the stream (the MFMA prefill keeps them in LDS; int8 runs it
+    # after the append, f32 takes the row-by-row prompt kernel after the append)
     cap = 480 * 16
     p = Pair(cache=cache, act=act, streams=1, cap=cap, seed=32, L=1, page_seed=13)
     p.fill(0, cap - 100)

@@ -432,17 +432,16 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(Lane
                                         out, qmul, 0); // prompts never run on a ring
 }
 
-// bf16 pools with 2 to 16 query heads per kv head decode a whole kv head per work group on MFMA
-// (k_decode_gqa), a ring prefix (a second query position) included
-// The MFMA decode (k_decode_gqa): 2 to 16 query heads per kv head, bf16 pages, or int8 pages with
-// no ring prefix in the batch (its f16 scores take one query position).  One head per kv head
-// stays on the VALU: on MFMA each lane would carry four scores of which one is live, and the
-// int8 window measured 108.6 us there against 99.5 us (at 4 and 8 heads per kv head: 34 and 23.7
-// us against 70 and 68).
+// The MFMA decode (k_decode_gqa): bf16 activations over bf16 or int8 pages with 2 to 16 query heads
+// per kv head decode a whole kv head per work group, a ring prefix (a second query position)
+// included.  One head per kv head stays on the VALU: on MFMA each lane would carry four scores of
+// which one is live, and the int8 window measured 108.6 us there against 99.5 us (at 4 and 8 heads
+// per kv head: 34 and 23.7 us against 70 and 68).
 static bool decode_on_mfma(const PoolView &pv, bool prefix) {
+    (void)prefix;
     const int G = pv.H / pv.KVH;
     if (pv.act_dt != DT_BF16 || G < 2 || G > 16) return false;
-    return pv.cache_dt == DT_BF16 || (pv.cache_dt == DT_I8 && !prefix);
+    return pv.cache_dt == DT_BF16 || pv.cache_dt == DT_I8;
 }
 
 int decode_min_split(const PoolView &pv, bool prefix) {
@@ -557,7 +556,7 @@ hipError_t launch_prefill(const PoolView &pv, const BatchView &bv, int layer, co
     case DT_F32 * 2 + DT_F32: return prefill_rows_impl<DT_F32, false>(pv, bv, layer, q, out, scale, stream, tm);
     case DT_BF16 * 2 + DT_BF16:
         return launch_prefill_mfma(pv, bv, layer, q, k, v, out, scale, fused, false, stream, tm);
-    case DT_I8 * 2 + DT_BF16: return prefill_rows_impl<DT_I8, true>(pv, bv, layer, q, out, scale, stream, tm);
+    case DT_I8 * 2 + DT_BF16: return launch_prefill_mfma_i8(pv, bv, layer, q, out, scale, stream, tm);
     case DT_I8 * 2 + DT_F32: return prefill_rows_impl<DT_I8, false>(pv, bv, layer, q, out, scale, stream, tm);
     default: return hipErrorInvalidValue;
     }

@@ -44,6 +44,46 @@ __device__ __forceinline__ uint4 rotate8(const uint4 &x, const uint4 &cs) {
     return make_uint4(o4[0], o4[1], o4[2], o4[3]);
 }
 
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+// Scores against int8 pages on MFMA take the rotated bf16 queries as f16.  Each query column (query
+// l16 of a tile: 8 dims in each of its 4 lanes g, at 32 kc + 8 g) is scaled by the power of two 2^-x
+// that fits it into f16 (f16_fit_exponent: exact for every bf16 value the column holds), and summed
+// over its 64 dims: a code c enters the product as the f16 value 1152 + c (c ^ 0x80 under the f16
+// exponent of 1024), so the score is 2^x s_k (sum - 1152 qsum).
+__device__ __forceinline__ void queries_f16(const bf16x8_t (&qq)[2], f16x8_t (&qh)[2], float &qsum, float &qpow) {
+    float xv[16];
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+        uint4 u;
+        __builtin_memcpy(&u, &qq[kc], 16);
+        const uint32_t *w4 = (const uint32_t *)&u;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            xv[8 * kc + 2 * i] = bf16_value(w4[i] & 0xffffu);
+            xv[8 * kc + 2 * i + 1] = bf16_value(w4[i] >> 16);
+        }
+    }
+    const int xq = f16_fit_exponent<16, 16, 2>(xv); // the column's 4 lanes: g = lane / 16
+    qpow = pow2i(xq);
+    qsum = 0.f;
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+        uint32_t h4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float x0 = xv[8 * kc + 2 * i] * pow2i(-xq), x1 = xv[8 * kc + 2 * i + 1] * pow2i(-xq);
+            h4[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x0, x1));
+            qsum += x0;
+            qsum += x1;
+        }
+        qh[kc] = __builtin_bit_cast(f16x8_t, make_uint4(h4[0], h4[1], h4[2], h4[3]));
+    }
+    qsum += __shfl_xor(qsum, 16);
+    qsum += __shfl_xor(qsum, 32);
+}
+
 constexpr int kPfKeys = 64;      // keys per chunk (four pages)
 constexpr int kPfLd = 72;        // LDS row length in bf16: 64 + 8 of padding, rows 16-byte aligned
 constexpr int kPfWaves = 8;      // waves per work group
@@ -52,12 +92,16 @@ constexpr int kPfMaxPages = 512; // page ids a work group keeps in LDS
 static_assert(kPfMaxPages >= kLaneBlocks * 8, "every page of a stream fits (a pool refuses more than 60 x 8)");
 static_assert(64 * kPfWaves == kPfKeys * 8, "one thread stages 16 bytes of one key per chunk");
 
+template <int CDT>
 __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4))) void k_prefill_mfma(
     PoolView pv, BatchView bv, int layer, const void *q, const void *knew, const void *vnew, void *out, float qmul,
     int fused) {
+    static_assert(CDT == DT_BF16 || CDT == DT_I8, "bf16 or int8 pages");
+    constexpr bool I8 = CDT == DT_I8;
     __shared__ __attribute__((aligned(16))) uint16_t ks[2 * kPfKeys][kPfLd]; // K of two chunks, [key][dim]
     __shared__ __attribute__((aligned(16))) uint16_t vs[2 * kPfKeys][kPfLd]; // V of two chunks, [key][dim]
     __shared__ int32_t spages[kPfMaxPages];
+    __shared__ float ssc[2][kPfKeys / kBlock][2]; // int8: each chunk's pages' K and V scales
     const int t = bv.t;
     // plan b is the batch's row b (its out_row): the inputs' and the output's rows are b's, so their
     // addresses do not wait for the plan
@@ -70,6 +114,8 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
     const size_t page_elems = (size_t)pv.KVH * kBlock * kHeadDim;
     uint16_t *kpages = (uint16_t *)pv.pages + tile_index(pv, layer, 0, 0, kvh) * (kBlock * kHeadDim);
     uint16_t *vpages = (uint16_t *)pv.pages + tile_index(pv, layer, 1, 0, kvh) * (kBlock * kHeadDim);
+    const int8_t *kpages8 = (const int8_t *)pv.pages + tile_index(pv, layer, 0, 0, kvh) * (kBlock * kHeadDim);
+    const int8_t *vpages8 = (const int8_t *)pv.pages + tile_index(pv, layer, 1, 0, kvh) * (kBlock * kHeadDim);
     // the stream's page ids for every key any round sees, at most one per thread: loaded here and
     // put into LDS only once the first round's queries and first chunk are on their way, so that
     // those loads go out together instead of each waiting for the one before
@@ -97,18 +143,45 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
         // Loads run one chunk ahead: chunk c's registers are consumed (rotated, stored to LDS
         // buffer c & 1) at step c, which then issues chunk c + 1's loads into them.
         struct Stage {
-            uint4 k, v, rope; // the key's K and V pieces, 4 (cos, sin) pairs as packed bf16
+            uint4 k, v, rope; // the key's K and V pieces (int8: 8 codes each in x, y), 4 (cos, sin) pairs as packed bf16
             int info;         // bit 0: a prompt key, bit 1: write it to its page
+            float sk, sv;     // int8, the first thread of each page's keys: the page's scales
         };
         // LDS: the page ids are in LDS (all but the first round's first chunk, which reads the
         // table itself); a compile-time choice, so that no pointer is selected between the two
         auto issue = [&](int c, Stage &st, auto LDS) {
             const int slot = c * kPfKeys + skey;
             const bool in = c < nch && slot < kend;
-            const bool fresh = fused && slot >= c0; // a prompt key: from the inputs, rotated here
+            const bool fresh = !I8 && fused && slot >= c0; // a prompt key: from the inputs, rotated here
             const int i = fresh ? min(slot - c0, t - 1) : 0;
             const size_t arow = (((size_t)b * t + i) * pv.KVH + kvh) * kHeadDim + 8 * spart;
             st.k = st.v = make_uint4(0, 0, 0, 0);
+            st.sk = st.sv = 0.f;
+            if constexpr (I8) {
+                // int8 pages (the prompt's rows appended before): 8 codes of K and of V; the first
+                // thread of each page's keys also takes its scales (0 for a page outside the pool,
+                // as the bf16 path's zero rows: score 0, no value)
+                if (in) {
+                    const int blk = min(slot >> 4, kPfMaxPages - 1);
+                    int page;
+                    if constexpr (decltype(LDS)::value)
+                        page = spages[blk];
+                    else
+                        page = tab[blk];
+                    if (page >= 0 && page < pv.NB) {
+                        const size_t poff = (size_t)page * page_elems + (slot & 15) * kHeadDim + 8 * spart;
+                        const uint2 kk = *(const uint2 *)(kpages8 + poff), vv = *(const uint2 *)(vpages8 + poff);
+                        st.k = make_uint4(kk.x, kk.y, 0, 0);
+                        st.v = make_uint4(vv.x, vv.y, 0, 0);
+                        if ((skey & 15) == 0 && spart == 0) {
+                            st.sk = pv.scales[tile_index(pv, layer, 0, page, kvh)];
+                            st.sv = pv.scales[tile_index(pv, layer, 1, page, kvh)];
+                        }
+                    }
+                }
+                st.info = 0;
+                return;
+            }
             if (in && fresh) {
                 st.k = ld_stream((const uint16_t *)knew + arow);
                 st.v = ld_stream((const uint16_t *)vnew + arow);
@@ -134,6 +207,8 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
         // first chunk's go out before any is used (rows past the prompt read row t - 1 and are
         // zeroed after).
         bf16x8_t qb[2][2];
+        f16x8_t qh[2][2];                // int8: the queries as f16, scaled by 2^-x per column
+        float qsum[2] = {0.f, 0.f}, qpow[2] = {1.f, 1.f}; // int8: their sums, 2^x
         float m[2], lsum[2]; // running max (scaled, log2 units) and this lane's share of the sum
         f32x4_t o[2][4];
         Stage st;
@@ -167,12 +242,32 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
                     const uint4 r = rotate8(qraw[j][kc], qcs[j][kc]);
                     qb[j][kc] = as_bf16x8(live ? r : make_uint4(0, 0, 0, 0));
                 }
+                if constexpr (I8) queries_f16(qb[j], qh[j], qsum[j], qpow[j]);
             }
         }
         __syncthreads(); // spages written
 
         auto step = [&](int c, Stage &st) {
             const int buf = c & 1, kbase = c * kPfKeys, lb = buf * kPfKeys;
+            if constexpr (I8) {
+                // K codes as f16 1152 + c (one byte permute each: c ^ 0x80 under the f16 exponent of
+                // 1024), V codes as bf16 (exact); the pages' scales beside them
+                uint32_t hk[4], bv2[4];
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const uint32_t kx = (i ? st.k.y : st.k.x) ^ 0x80808080u, vx = i ? st.v.y : st.v.x;
+                    hk[2 * i] = __builtin_amdgcn_perm(0x64646464u, kx, 0x04010400u);
+                    hk[2 * i + 1] = __builtin_amdgcn_perm(0x64646464u, kx, 0x04030402u);
+                    bv2[2 * i] = pack_bf16((float)(int8_t)(vx & 0xffu), (float)(int8_t)((vx >> 8) & 0xffu));
+                    bv2[2 * i + 1] = pack_bf16((float)(int8_t)((vx >> 16) & 0xffu), (float)(int8_t)(vx >> 24));
+                }
+                *(uint4 *)&ks[lb + skey][8 * spart] = make_uint4(hk[0], hk[1], hk[2], hk[3]);
+                *(uint4 *)&vs[lb + skey][8 * spart] = make_uint4(bv2[0], bv2[1], bv2[2], bv2[3]);
+                if ((skey & 15) == 0 && spart == 0) {
+                    ssc[buf][skey >> 4][0] = st.sk;
+                    ssc[buf][skey >> 4][1] = st.sv;
+                }
+            } else {
             // rotate a prompt key at its position; store this thread's piece of the chunk
             {
                 const uint4 kk = st.info & 1 ? rotate8(st.k, st.rope) : st.k;
@@ -188,6 +283,7 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
                 *(uint4 *)&ks[lb + skey][8 * spart] = kk;
                 *(uint4 *)&vs[lb + skey][8 * spart] = st.v;
             }
+            }
             issue(c + 1, st, std::true_type{});
             __syncthreads(); // chunk c is in LDS; every reader of chunk c - 2 (same buffer) is done
 #pragma unroll
@@ -201,8 +297,17 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
                     s[kg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int kc = 0; kc < 2; ++kc) {
-                        const bf16x8_t a = as_bf16x8(*(const uint4 *)&ks[lb + 16 * kg + l16][32 * kc + 8 * g]);
-                        s[kg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qb[j][kc], s[kg], 0, 0, 0);
+                        const uint4 a = *(const uint4 *)&ks[lb + 16 * kg + l16][32 * kc + 8 * g];
+                        if constexpr (I8)
+                            s[kg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), qh[j][kc],
+                                                                          s[kg], 0, 0, 0);
+                        else
+                            s[kg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), qb[j][kc], s[kg], 0, 0, 0);
+                    }
+                    if constexpr (I8) { // the 16 keys of group kg are one page: its K scale, the bias out
+                        const float f = ssc[buf][kg][0] * qpow[j];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) s[kg][r] = __builtin_fmaf(-1152.f, qsum[j], s[kg][r]) * f;
                     }
                 }
                 // lane: query slot r0 + l16 against key slots kbase + 16 kg + 4 g + r
@@ -243,6 +348,11 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
                     for (int r = 0; r < 4; ++r) {
                         p[r] = fast_exp2(__builtin_fmaf(s[kg][r], qmul, -mref));
                         psum += p[r];
+                    }
+                    if constexpr (I8) { // P^T carries p sv (the page's V scale), so O needs none
+                        const float sv = ssc[buf][kg][1];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) p[r] *= sv;
                     }
                     pk[kg][0] = pack_bf16(p[0], p[1]);
                     pk[kg][1] = pack_bf16(p[2], p[3]);
@@ -952,21 +1062,19 @@ __global__ __launch_bounds__(64 * kWpWaves) __attribute__((amdgpu_waves_per_eu(2
 // against the queries rotated at pos_pre (attend_core's second query position), a second S^T of
 // the same K operand on the pages that hold prefix rows, taken row by row in the same lanes.
 //
-// CDT = DT_I8 (int8 pages with f32 scales per (page, kv head), no prefix; the fused append is
-// attend_core's, re-reading the write page's scales after it): the VALU decode's arithmetic moved
-// onto the MFMA.  A code byte c goes
+// CDT = DT_I8 (int8 pages with f32 scales per (page, kv head); the fused append is attend_core's,
+// re-reading the write page's scales after it): the VALU decode's arithmetic moved onto the MFMA.
+// With PREFIX, the queries at pos_pre get an f16 copy, power of two and sum of their own.  A code
+// byte c goes
 // to f16 as 1024 + (c + 128) = 1152 + c by one byte permute (c ^ 0x80 under the f16 exponent of
 // 1024), the rotated bf16 queries convert to f16 exactly, so v_mfma_f32_16x16x32_f16 sums
 // q (1152 + c) and the score is sk (that sum - 1152 sum(q)).  V codes widen to bf16 exactly
 // (|c| <= 127) and P^T carries p sv rounded to bf16, so O needs no bias; the softmax sum keeps p.
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-
 template <int SPLIT, bool PREFIX, int CDT>
 __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4))) void k_decode_gqa(
     PoolView pv, BatchView bv, int layer, const void *q, const void *knew, const void *vnew, void *out, float qmul,
     int fused) {
-    static_assert(CDT == DT_BF16 || (CDT == DT_I8 && !PREFIX), "bf16 pages, or int8 pages without a prefix");
+    static_assert(CDT == DT_BF16 || CDT == DT_I8, "bf16 or int8 pages");
     constexpr bool I8 = CDT == DT_I8;
     constexpr int NL = I8 ? 1 : 2; // 1 KB loads per K or V tile of a page
     constexpr int DEPTH = 2;       // pages in flight ahead of the one being reduced
@@ -1068,39 +1176,13 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
             if constexpr (PREFIX) qpre[kc] = as_bf16x8(live ? rotate8(qraw[kc], pcs[kc]) : make_uint4(0, 0, 0, 0));
         }
     }
-    // int8: the same queries as f16, scaled by a power of two that fits the column into f16
-    // (f16_fit_exponent: exact), and their sum over the 64 dims of the lane's column
-    f16x8_t qh[2];
-    float qsum = 0.f, qpow = 1.f;
+    // int8: the same queries as f16 (PREFIX: those at pos_pre too, with a power of two and a sum
+    // of their own)
+    f16x8_t qh[2], qhp[2];
+    float qsum = 0.f, qpow = 1.f, qsump = 0.f, qpowp = 1.f;
     if constexpr (I8) {
-        float xv[16];
-#pragma unroll
-        for (int kc = 0; kc < 2; ++kc) {
-            uint4 u;
-            __builtin_memcpy(&u, &qb[kc], 16);
-            const uint32_t *w4 = (const uint32_t *)&u;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                xv[8 * kc + 2 * i] = bf16_value(w4[i] & 0xffffu);
-                xv[8 * kc + 2 * i + 1] = bf16_value(w4[i] >> 16);
-            }
-        }
-        const int xq = f16_fit_exponent<16, 16, 2>(xv); // the column's 4 lanes: g = lane / 16
-        qpow = pow2i(xq);
-#pragma unroll
-        for (int kc = 0; kc < 2; ++kc) {
-            uint32_t h4[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float x0 = xv[8 * kc + 2 * i] * pow2i(-xq), x1 = xv[8 * kc + 2 * i + 1] * pow2i(-xq);
-                h4[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x0, x1));
-                qsum += x0;
-                qsum += x1;
-            }
-            qh[kc] = __builtin_bit_cast(f16x8_t, make_uint4(h4[0], h4[1], h4[2], h4[3]));
-        }
-        qsum += __shfl_xor(qsum, 16);
-        qsum += __shfl_xor(qsum, 32);
+        queries_f16(qb, qh, qsum, qpow);
+        if constexpr (PREFIX) queries_f16(qpre, qhp, qsump, qpowp);
     }
 
     float m = -1e30f, lsum = 0.f; // running max (scaled, log2 units) and this lane's share of the sum
@@ -1114,6 +1196,7 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
         // K through the wave's LDS tile into A layout (key l16, dims 32 kc + 8 g); a wave's LDS
         // accesses complete in order, so no barrier
         bf16x8_t ka[2];
+        f16x8_t kh[2];
         if constexpr (I8) {
             const uint32_t *u = (const uint32_t *)&kr[0];
             uint32_t hv[8];
@@ -1126,9 +1209,10 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
             *(uint4 *)&kt[w][lane >> 2][16 * (lane & 3)] = make_uint4(hv[0], hv[1], hv[2], hv[3]);
             *(uint4 *)&kt[w][lane >> 2][16 * (lane & 3) + 8] = make_uint4(hv[4], hv[5], hv[6], hv[7]);
 #pragma unroll
-            for (int kc = 0; kc < 2; ++kc)
-                s = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    __builtin_bit_cast(f16x8_t, *(const uint4 *)&kt[w][l16][32 * kc + 8 * g]), qh[kc], s, 0, 0, 0);
+            for (int kc = 0; kc < 2; ++kc) {
+                kh[kc] = __builtin_bit_cast(f16x8_t, *(const uint4 *)&kt[w][l16][32 * kc + 8 * g]);
+                s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[kc], qh[kc], s, 0, 0, 0);
+            }
             const float sk = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(my_sk), j));
 #pragma unroll
             for (int r = 0; r < 4; ++r) s[r] = __builtin_fmaf(-1152.f, qsum, s[r]) * sk * qpow;
@@ -1146,8 +1230,16 @@ __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(4)))
             const int base = (w + j * SPLIT) * kBlock;
             if (base < R.prefix) {
                 f32x4_t sp = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                if constexpr (I8) {
 #pragma unroll
-                for (int kc = 0; kc < 2; ++kc) sp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[kc], qpre[kc], sp, 0, 0, 0);
+                    for (int kc = 0; kc < 2; ++kc) sp = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[kc], qhp[kc], sp, 0, 0, 0);
+                    const float sk = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(my_sk), j));
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) sp[r] = __builtin_fmaf(-1152.f, qsump, sp[r]) * sk * qpowp;
+                } else {
+#pragma unroll
+                    for (int kc = 0; kc < 2; ++kc) sp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[kc], qpre[kc], sp, 0, 0, 0);
+                }
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     if (base + 4 * g + r < R.prefix) s[r] = sp[r];
@@ -1276,7 +1368,6 @@ hipError_t launch_decode_gqa(const PoolView &pv, const BatchView &bv, int layer,
     const dim3 grid(bv.n * pv.KVH);
     const int f = fused ? 1 : 0;
     if (pv.act_dt != DT_BF16 || (pv.cache_dt != DT_BF16 && pv.cache_dt != DT_I8)) return hipErrorInvalidValue;
-    if (pv.cache_dt == DT_I8 && bv.prefix) return hipErrorInvalidValue; // int8 pages: no prefix
 #define XNP_GQA(S, PFX, C) XNP_LAUNCH((k_decode_gqa<S, PFX, C>), grid, dim3(64 * S), stream, tm, pv, bv, layer, q, k, v, out, qmul, f)
 #define XNP_GQA_SPLIT(PFX, C)                                                                                       \
     switch (bv.split) {                                                                                            \
@@ -1286,7 +1377,9 @@ hipError_t launch_decode_gqa(const PoolView &pv, const BatchView &bv, int layer,
     case 8: XNP_GQA(8, PFX, C); break;                                                                             \
     default: return hipErrorInvalidValue;                                                                          \
     }
-    if (pv.cache_dt == DT_I8) {
+    if (pv.cache_dt == DT_I8 && bv.prefix) {
+        XNP_GQA_SPLIT(true, DT_I8);
+    } else if (pv.cache_dt == DT_I8) {
         XNP_GQA_SPLIT(false, DT_I8);
     } else if (bv.prefix) {
         XNP_GQA_SPLIT(true, DT_BF16);
@@ -1313,8 +1406,19 @@ hipError_t launch_prefill_mfma(const PoolView &pv, const BatchView &bv, int laye
         XNP_LAUNCH(k_prefill_fast<false>, dim3(bv.n * pv.H), dim3(64 * kPfWaves), stream, tm, pv, bv, layer, q, k, v,
                    out, qmul);
     else
-        XNP_LAUNCH(k_prefill_mfma, dim3(bv.n * pv.H), dim3(64 * kPfWaves), stream, tm, pv, bv, layer, q, k, v, out,
-                   qmul, fused ? 1 : 0);
+        XNP_LAUNCH(k_prefill_mfma<DT_BF16>, dim3(bv.n * pv.H), dim3(64 * kPfWaves), stream, tm, pv, bv, layer, q, k, v,
+                   out, qmul, fused ? 1 : 0);
+    return hipGetLastError();
+}
+
+// Prompt rows over int8 pages (bf16 activations), after k_append has written them: k_prefill_mfma
+// reading every key from the pages, scores in f16 against the codes, values in bf16.
+hipError_t launch_prefill_mfma_i8(const PoolView &pv, const BatchView &bv, int layer, const void *q, void *out,
+                                  float scale, hipStream_t stream, const LaunchTiming &tm) {
+    if (pv.cache_dt != DT_I8 || pv.act_dt != DT_BF16) return hipErrorInvalidValue;
+    const float qmul = scale * 1.4426950408889634f;
+    XNP_LAUNCH(k_prefill_mfma<DT_I8>, dim3(bv.n * pv.H), dim3(64 * kPfWaves), stream, tm, pv, bv, layer, q, nullptr,
+               nullptr, out, qmul, 0);
     return hipGetLastError();
 }
 

@@ -358,5 +358,8 @@ hipError_t launch_decode_gqa(const PoolView &pv, const BatchView &bv, int layer,
 hipError_t launch_prefill_mfma(const PoolView &pv, const BatchView &bv, int layer, const void *q, const void *k,
                                const void *v, void *out, float scale, bool fused, bool window, hipStream_t stream,
                                const LaunchTiming &tm);
+// prompt rows over int8 pages (bf16 activations) on MFMA, after the append wrote them
+hipError_t launch_prefill_mfma_i8(const PoolView &pv, const BatchView &bv, int layer, const void *q, void *out,
+                                  float scale, hipStream_t stream, const LaunchTiming &tm);
 
 } // namespace xnp
