@@ -111,15 +111,17 @@ def traffic_of(workload, match, bytes_per_launch):
     runs (profiles/traffic.json: each counter scaled by what it reads for a 1 GiB copy): the counter
     bytes per algorithmic byte of the profiled run, times this run's algorithmic bytes per launch.
     The ratio belongs to the kernel at that workload, so it carries over to any --steps / --warmup;
-    None when the workload (streams, layers, lengths, ...) is not the profiled one."""
+    None when the workload (streams, layers, lengths, ...) matches no profiled setting."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        entry = json.load(f).get(workload)
-    if not entry or entry.get("workload") != match:
-        return None
-    return int(round(entry["traffic_per_algorithmic_byte"] * bytes_per_launch))
+        table = json.load(f)
+    # one entry per profiled setting: "decode", "decode:kv_heads=1", ...
+    for key, entry in table.items():
+        if (key == workload or key.startswith(workload + ":")) and entry.get("workload") == match:
+            return int(round(entry["traffic_per_algorithmic_byte"] * bytes_per_launch))
+    return None
 
 
 def decode_bytes(lens, elem=2, kvh=H):
