@@ -35,6 +35,10 @@
   holding U[64, 2048] rows written so far; per step every stream evicts its oldest row once the
   window is full, appends one and attends over min(n+1, 512) rows.  Value: frames/s.
 
+--workload vendor_gemm: not this library -- the vendor library's bf16 GEMMs (hipBLASLt through torch)
+  at the layer step's four projection shapes and torch's LayerNorm, replayed from a graph, for
+  comparison with the q8 projections.  Value: us per layer for the four GEMMs.
+
 CPU baseline: the oracle (the C restatement, OpenMP over streams) on a bounded sample of the same
 workload, timed on this host's cores.
 """
@@ -801,6 +805,61 @@ def cpu_flowlm(cfg, blob, tokens, seconds, threads):
                       f"{el:.1f} s on {threads} thread{'s' if threads > 1 else ''}"}
 
 
+def run_vendor_gemm(args, xnp, torch):
+    """The vendor library's bf16 GEMMs (torch.nn.functional.linear: hipBLASLt) and LayerNorm at the
+    layer step's shapes, for comparison with the q8 projections: bf16 weights (no widening), no
+    epilogue.  Each op is replayed from a torch graph of 20 calls, so the host's launch rate is out
+    of the time."""
+    dev = torch.device("cuda:0")
+    M = args.step_streams
+    shapes = {"in_proj": (3 * H * D, DM), "out_proj": (DM, H * D), "linear1": (FF, DM), "linear2": (DM, FF)}
+    gen = torch.Generator(device=dev).manual_seed(SEED + 12)
+    stream = torch.cuda.Stream()
+    per, flops = {}, {}
+
+    def time_op(fn, reps=20):
+        with torch.cuda.stream(stream):
+            for _ in range(3):
+                fn()
+        stream.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for _ in range(reps):
+                fn()
+        for _ in range(args.warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1000.0 / (args.steps * reps)
+
+    for name, (N, K) in shapes.items():
+        x = torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16)
+        w = torch.randn((N, K), generator=gen, device=dev).to(torch.bfloat16)
+        y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        per[name] = round(time_op(lambda: torch.matmul(x, w.t(), out=y)), 2)
+        flops[name] = 2.0 * M * N * K
+    x = torch.randn((M, DM), generator=gen, device=dev).to(torch.bfloat16)
+    ln = torch.nn.LayerNorm(DM, device=dev, dtype=torch.bfloat16)
+    with torch.no_grad():
+        ln_us = round(time_op(lambda: ln(x)), 2)
+    total = sum(per.values())
+    config = {"workload": f"the vendor library at the layer step's shapes: {M} rows, bf16 x[M, K] W[N, K]^T for "
+                          f"in_proj, out_proj, linear1, linear2 (d_model {DM}, FF {FF}); LayerNorm of {M} x {DM}",
+              "rows": M, "d_model": DM, "ff": FF}
+    roof = {"bound": "mfma", "achieved": round(sum(flops.values()) / (total * 1e-6) / 1e12, 1),
+            "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(sum(flops.values()) / (total * 1e-6) / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+            "kernel": "torch.matmul (hipBLASLt) bf16, one call per projection; torch LayerNorm",
+            "per_projection_us": per, "layer_norm_us": ln_us}
+    return line("us per layer for the four projections' bf16 GEMMs in the vendor library (comparison only)",
+                total, "us", args, total / 1000.0, "bf16", config, roof, None, higher=False)
+
+
 def run_flowlm(args, xnp, torch):
     dev = torch.device("cuda:0")
     fl = xnp.flow_lm
@@ -880,7 +939,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=["decode", "prefill", "window", "step", "flowlm", "frame"], default="decode")
+    ap.add_argument("--workload", choices=["decode", "prefill", "window", "step", "flowlm", "frame", "vendor_gemm"],
+                    default="decode")
     ap.add_argument("--step-streams", type=int, default=2048)
     ap.add_argument("--step-max-len", type=int, default=1500)
     ap.add_argument("--streams", type=int, default=1024)
@@ -921,7 +981,7 @@ def main():
     xnp = _load("xn_ptts_amd", os.path.join(ROOT, "xn-ptts_amd"))
     xnp.load_library()
     runs = {"decode": run_decode, "prefill": run_prefill, "window": run_window, "step": run_step,
-            "flowlm": run_flowlm, "frame": run_frame}
+            "flowlm": run_flowlm, "frame": run_frame, "vendor_gemm": run_vendor_gemm}
     out = runs[args.workload](args, xnp, torch)
     if args.workload == "decode" and not args.headline_only and headline_args(args):
         out["configs"] = nested_configs(args, xnp, torch, runs)
