@@ -205,3 +205,58 @@ def test_the_layer_step_configuration_at_full_size_spot_checked():
             assert per.max() <= TOL, (worst, int(lens[worst]), float(per.max()))
     pool.end()
     assert pool.check_tables() == 0
+
+
+@pytest.mark.parametrize("ls", [False, True])
+def test_the_layer_step_equals_its_pieces_bit_for_bit(ls):
+    # xnp_layer_step against the same layer composed of the public pieces on a second, identical
+    # pool: layer_norm, linear_q8 (store, residual, gelu) and attend.  The step is those launches in
+    # that order on its own workspace, so every bit must agree: the residual stream and the cache
+    # rows compared as integers.  Row counts that no 16-row band divides (37 single rows, a 7-row
+    # prompt on 5 streams), 300 rows, with and without layer scales.
+    rng = np.random.default_rng(71 + ls)
+    L, H, KVH, D, dm, ff = 1, 8, 8, 64, 512, 2048
+    qd, kd = H * D, KVH * D
+    orc, lw = make_weights(rng, H=H, KVH=KVH, ff=ff, ls=ls)
+    dw = {k: dev(getattr(orc, k), torch.int8 if getattr(orc, k).dtype == np.int8 else torch.float32)
+          for k in ("wqkv", "sqkv", "wout", "sout", "w1", "s1", "w2", "s2", "ln1_w", "ln1_b", "ln2_w", "ln2_b")}
+    dw["ls1"] = dev(orc.ls1, torch.float32) if ls else None
+    dw["ls2"] = dev(orc.ls2, torch.float32) if ls else None
+    S, cap = 300, 48
+    pools = [xnp.KvPool(num_layers=L, num_heads=H, num_kv_heads=KVH, num_blocks=S * (cap // 16) + 8, max_streams=S,
+                        max_blocks_per_stream=cap // 16, cache_dtype="bf16", act_dtype="bf16", max_pos=256,
+                        page_seed=13) for _ in range(2)]
+    ids = [[p.init_state(cap) for _ in range(S)] for p in pools]
+    ws = torch.empty(pools[0].layer_workspace(S * 7, dm, ff), dtype=torch.uint8, device=DEV)
+    for which, t in ((list(range(37)), 1), (list(range(5)), 7), (list(range(S)), 1)):
+        n, M = len(which), len(which) * t
+        x0 = normal(rng, (n, t, dm), "bf16")
+        xa, xb = dev(x0), dev(x0)
+        pools[0].begin([ids[0][i] for i in which], t=t)
+        pools[0].layer_step(0, lw, xa, ws)
+        pools[0].end()
+        pools[1].begin([ids[1][i] for i in which], t=t)
+        h = torch.empty((M, dm), dtype=torch.bfloat16, device=DEV)
+        qkv = torch.empty((M, qd + 2 * kd), dtype=torch.bfloat16, device=DEV)
+        att = torch.empty((M, qd), dtype=torch.bfloat16, device=DEV)
+        f = torch.empty((M, ff), dtype=torch.bfloat16, device=DEV)
+        xv = xb.view(M, dm)
+        xnp.layer_norm(xv, dw["ln1_w"], dw["ln1_b"], h)
+        xnp.linear_q8(h, dw["wqkv"], dw["sqkv"], qkv, "store")
+        q, k, v = (qkv[:, a:b].contiguous() for a, b in ((0, qd), (qd, qd + kd), (qd + kd, qd + 2 * kd)))
+        pools[1].attend(0, q, k, v, att, 1.0 / np.sqrt(D))
+        xnp.linear_q8(att, dw["wout"], dw["sout"], xv, "residual", ls=dw["ls1"])
+        xnp.layer_norm(xv, dw["ln2_w"], dw["ln2_b"], h)
+        xnp.linear_q8(h, dw["w1"], dw["s1"], f, "gelu_erf")
+        xnp.linear_q8(f, dw["w2"], dw["s2"], xv, "residual", ls=dw["ls2"])
+        pools[1].end()
+        torch.cuda.synchronize()
+        assert torch.equal(xa.view(torch.int16), xb.view(torch.int16)), (n, t)
+    for i in (0, 4, 36, 299):
+        n = pools[0].info(ids[0][i])["current_end"]
+        for kv in (0, 1):
+            got = [torch.empty((n, KVH, D), dtype=torch.bfloat16, device=DEV) for _ in range(2)]
+            for p, sid, r in zip(pools, (ids[0][i], ids[1][i]), got):
+                p.read_rows(sid, 0, kv, 0, r)
+            torch.cuda.synchronize()
+            assert torch.equal(got[0].view(torch.int16), got[1].view(torch.int16)), (i, kv)

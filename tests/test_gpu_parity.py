@@ -989,7 +989,7 @@ def test_one_wave_per_stream_and_head_at_batch_scale(cache, act, maxlen):
 
 
 @pytest.mark.parametrize("split", [2, 8])
-def test_many_streams_at_the_config2_length_distribution(split):
+def test_256_streams_with_lengths_uniform_up_to_1024(split):
     # 256 streams with cache lengths U[1, 1024] on shuffled pages, each head's pages shared out
     # over `split` waves that merge in LDS.  Every stream is checked against the oracle.
     S, L = 256, 1
@@ -1096,9 +1096,11 @@ def test_prefill_matches_the_oracle(cache, act):
         p.assert_cache_equal(i)
 
 
-def test_prefill_of_a_grouped_head_prompt_at_config3_shape_sample():
-    # 8 streams x 256-position prompts (the prefill configuration's shape, fewer streams)
-    p = Pair(cache="bf16", act="bf16", streams=8, cap=272, seed=22, L=1, page_seed=6)
+@pytest.mark.parametrize("cache", ["bf16", "i8"])
+def test_prefill_of_256_position_grouped_head_prompts_on_8_streams(cache):
+    # 8 streams x 256-position prompts (the 64-stream prefill workload's shape, fewer streams); int8
+    # pages take the append, then the MFMA prefill reading every key back from the pages
+    p = Pair(cache=cache, act="bf16", streams=8, cap=272, seed=22, L=1, page_seed=6)
     assert p.prefill(256) <= 2e-2
     for i in range(0, 8, 3):
         p.assert_cache_equal(i)
