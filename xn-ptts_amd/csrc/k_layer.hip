@@ -99,7 +99,7 @@ __global__ __launch_bounds__(256) void k_layer_norm(const uint16_t *x, int rows,
             }
             o4[i] = pack_bf16(y[0], y[1]);
         }
-        *(uint4 *)(out + (size_t)row * dim + e0) = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+        st_stream(out + (size_t)row * dim + e0, make_uint4(o4[0], o4[1], o4[2], o4[3]));
     }
 }
 
@@ -406,7 +406,7 @@ __global__ __launch_bounds__(256 * KS) void k_gemm_q8(const uint16_t *A, int M, 
             if constexpr (EPI == kStore) {
                 int seg = 0;
                 if (go.nseg > 1 && ne >= go.col0[1]) seg = (go.nseg > 2 && ne >= go.col0[2]) ? 2 : 1;
-                *(uint4 *)((uint16_t *)go.out[seg] + (size_t)m * go.ld[seg] + (ne - go.col0[seg])) = yv;
+                st_stream((uint16_t *)go.out[seg] + (size_t)m * go.ld[seg] + (ne - go.col0[seg]), yv);
             } else if constexpr (EPI == kStoreF32) {
                 float *o = (float *)go.out[0] + (size_t)m * go.ld[0] + ne;
                 *(float4 *)o = make_float4(y[0], y[1], y[2], y[3]);
@@ -427,8 +427,8 @@ __global__ __launch_bounds__(256 * KS) void k_gemm_q8(const uint16_t *A, int M, 
                 float r8[8];
 #pragma unroll
                 for (int i = 0; i < 8; ++i) r8[i] = bf16_value(bf16_bits(cu[i])) + y[i];
-                *(uint4 *)((uint16_t *)go.out[0] + (size_t)m * go.ld[0] + ne) =
-                    make_uint4(pack_bf16(r8[0], r8[1]), pack_bf16(r8[2], r8[3]), pack_bf16(r8[4], r8[5]), pack_bf16(r8[6], r8[7]));
+                st_stream((uint16_t *)go.out[0] + (size_t)m * go.ld[0] + ne,
+                          make_uint4(pack_bf16(r8[0], r8[1]), pack_bf16(r8[2], r8[3]), pack_bf16(r8[4], r8[5]), pack_bf16(r8[6], r8[7])));
             } else {
                 float r8[8];
                 const uint32_t *xw = (const uint32_t *)&xo[e], *gw = (const uint32_t *)&gt[e];
@@ -455,8 +455,8 @@ __global__ __launch_bounds__(256 * KS) void k_gemm_q8(const uint16_t *A, int M, 
                                 bf16_value(bf16_bits(gate * yi));
                     }
                 }
-                *(uint4 *)((uint16_t *)go.out[0] + (size_t)m * go.ld[0] + ne) =
-                    make_uint4(pack_bf16(r8[0], r8[1]), pack_bf16(r8[2], r8[3]), pack_bf16(r8[4], r8[5]), pack_bf16(r8[6], r8[7]));
+                st_stream((uint16_t *)go.out[0] + (size_t)m * go.ld[0] + ne,
+                          make_uint4(pack_bf16(r8[0], r8[1]), pack_bf16(r8[2], r8[3]), pack_bf16(r8[4], r8[5]), pack_bf16(r8[6], r8[7])));
             }
         }
         return;

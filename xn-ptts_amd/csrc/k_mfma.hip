@@ -276,8 +276,8 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
                     const int page = spages[min(slot >> 4, kPfMaxPages - 1)];
                     if (page >= 0 && page < pv.NB) {
                         const size_t poff = (size_t)page * page_elems + (slot & 15) * kHeadDim + 8 * spart;
-                        *(uint4 *)(kpages + poff) = kk;
-                        *(uint4 *)(vpages + poff) = st.v;
+                        st_stream(kpages + poff, kk);
+                        st_stream(vpages + poff, st.v);
                     }
                 }
                 *(uint4 *)&ks[lb + skey][8 * spart] = kk;
@@ -389,8 +389,8 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
             uint16_t *orow = (uint16_t *)out + (((size_t)b * t + qrow) * pv.H + h) * kHeadDim;
 #pragma unroll
             for (int dg = 0; dg < 4; ++dg)
-                *(uint2 *)(orow + 16 * dg + 4 * g) = make_uint2(pack_bf16(o[j][dg][0] * inv, o[j][dg][1] * inv),
-                                                                pack_bf16(o[j][dg][2] * inv, o[j][dg][3] * inv));
+                st_stream(orow + 16 * dg + 4 * g, make_uint2(pack_bf16(o[j][dg][0] * inv, o[j][dg][1] * inv),
+                                                             pack_bf16(o[j][dg][2] * inv, o[j][dg][3] * inv)));
         }
     }
 }
@@ -549,8 +549,8 @@ __device__ __forceinline__ void prefill_fast_group(const PoolView &pv, const Bat
         uint16_t *orow = (uint16_t *)out + (((size_t)b * t + qrow) * pv.H + h) * kHeadDim;
 #pragma unroll
         for (int dg = 0; dg < 4; ++dg)
-            *(uint2 *)(orow + 16 * dg + 4 * g) = make_uint2(pack_bf16(o[j][dg][0] * inv, o[j][dg][1] * inv),
-                                                            pack_bf16(o[j][dg][2] * inv, o[j][dg][3] * inv));
+            st_stream(orow + 16 * dg + 4 * g, make_uint2(pack_bf16(o[j][dg][0] * inv, o[j][dg][1] * inv),
+                                                         pack_bf16(o[j][dg][2] * inv, o[j][dg][3] * inv)));
     };
     // The lane's LDS read offsets within a chunk slot, computed once: the swizzle of a row depends
     // on its low 4 bits only, so the slot, the 16-key group, the 32-key half and the second
@@ -591,8 +591,8 @@ __device__ __forceinline__ void prefill_fast_group(const PoolView &pv, const Bat
             const int pgc = spages[min(slot, kend - 1) >> 4];
             if (FUSED && fresh && slot < kend && pgc >= 0 && pgc < pv.NB) {
                 const size_t poff = (size_t)pgc * page_elems + (slot & 15) * kHeadDim + 8 * spart;
-                *(uint4 *)(kpages + poff) = kk;
-                *(uint4 *)(vpages + poff) = vr[c];
+                st_stream(kpages + poff, kk);
+                st_stream(vpages + poff, vr[c]);
             }
         }
 #pragma unroll
@@ -1036,8 +1036,8 @@ __global__ __launch_bounds__(64 * kWpWaves) __attribute__((amdgpu_waves_per_eu(2
             const int row = 8 * k + (lane >> 3), unit = lane & 7, p = row >> 5;
             const int qrow = 16 * tq0 + 32 * (p == 0 ? w : kWpRound / 32 - 1 - w) + (row & 31);
             if (act[p] && qrow < t)
-                *(uint4 *)((uint16_t *)out + (((size_t)P.out_row * t + qrow) * pv.H + h) * kHeadDim + 8 * unit) =
-                    *(const uint4 *)(stage + row * kHeadDim + 8 * (unit ^ (row & 7)));
+                st_stream((uint16_t *)out + (((size_t)P.out_row * t + qrow) * pv.H + h) * kHeadDim + 8 * unit,
+                          *(const uint4 *)(stage + row * kHeadDim + 8 * (unit ^ (row & 7))));
         }
     }
 }

@@ -117,6 +117,22 @@ __device__ __forceinline__ uint4 ld_stream(const void *p) {
     return make_uint4(a.x, a.y, a.z, a.w);
 }
 
+// Stores with the non-temporal hint, for 8- or 16-byte pieces of rows that nothing in the launch
+// reads back: they go out to memory as they are written, while the launch still computes, instead
+// of staying dirty in L2 until the launch's end writes L2 back.  Measured: the prefill's page and
+// output stores at 64 streams x 256 positions 28.9 -> 27.8 us per launch; the projections' and
+// LayerNorm's outputs in the 2048-stream layer step 5.20 -> 5.14 ms per step.  The decode's own
+// stores (2 bytes a lane for its output, 4 for the append) stay plain: hinted, they cost 1.5 us of
+// 171 at 1024 streams and 1.3 of 28.6 at one kv head.
+__device__ __forceinline__ void st_stream(void *p, const uint4 &v) {
+    typedef unsigned u32x4_nt __attribute__((ext_vector_type(4)));
+    __builtin_nontemporal_store(u32x4_nt{v.x, v.y, v.z, v.w}, (u32x4_nt *)p);
+}
+__device__ __forceinline__ void st_stream(void *p, const uint2 &v) {
+    typedef unsigned u32x2_nt __attribute__((ext_vector_type(2)));
+    __builtin_nontemporal_store(u32x2_nt{v.x, v.y}, (u32x2_nt *)p);
+}
+
 template <int CDT> constexpr int esize() { return CDT == DT_F32 ? 4 : CDT == DT_BF16 ? 2 : 1; }
 
 // Element offset of row 0 of tile (layer, kv, page, head).
