@@ -377,21 +377,30 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
         for (int c = 0; c < nch; ++c) step(c, st);
         __syncthreads(); // the next round's staging overwrites both buffers
 
-        // out[row][h][16 dg + 4 g .. +3] = O / l, the row's sum reduced over its 4 lanes
+        // out[row][h][..] = O / l, the row's sum reduced over its 4 lanes.  The lane holds dims
+        // 16 dg + 4 g .. +3 of row l16; through rows 16 w .. 16 w + 15 of ks (free after the barrier
+        // above), each store instruction writes 8 whole 128-byte rows, so the non-temporal stores go
+        // out as full lines.
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
+            if (tile[j] < 0) continue;
             float l = lsum[j];
             l += __shfl_xor(l, 16);
             l += __shfl_xor(l, 32);
-            const int qrow = 16 * tile[j] + l16;
-            if (tile[j] < 0 || qrow >= t) continue;
             const float inv = 1.0f / l;
-            uint16_t *orow = (uint16_t *)out + (((size_t)b * t + qrow) * pv.H + h) * kHeadDim;
+            uint16_t(*st)[kPfLd] = &ks[16 * w];
 #pragma unroll
             for (int dg = 0; dg < 4; ++dg)
-                st_stream(orow + 16 * dg + 4 * g, make_uint2(pack_bf16(o[j][dg][0] * inv, o[j][dg][1] * inv),
-                                                             pack_bf16(o[j][dg][2] * inv, o[j][dg][3] * inv)));
+                *(uint2 *)&st[l16][16 * dg + 4 * g] = make_uint2(pack_bf16(o[j][dg][0] * inv, o[j][dg][1] * inv),
+                                                                 pack_bf16(o[j][dg][2] * inv, o[j][dg][3] * inv));
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int r = (lane >> 3) + 8 * i, unit = lane & 7, qrow = 16 * tile[j] + r;
+                const uint4 v = *(const uint4 *)&st[r][8 * unit];
+                if (qrow < t) st_stream((uint16_t *)out + (((size_t)b * t + qrow) * pv.H + h) * kHeadDim + 8 * unit, v);
+            }
         }
+        if (!last) __syncthreads(); // the next round's staging overwrites ks
     }
 }
 
@@ -538,19 +547,28 @@ __device__ __forceinline__ void prefill_fast_group(const PoolView &pv, const Bat
 #pragma unroll
         for (int dg = 0; dg < 4; ++dg) o[j][dg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
-    // out[row][h][16 dg + 4 g .. +3] = O / l of tile j, the row's sum reduced over its 4 lanes
+    // out[row][h][..] = O / l of tile j, the row's sum reduced over its 4 lanes.  The lane holds dims
+    // 16 dg + 4 g .. +3 of row l16; through this wave's 2 KB of LDS (chunk slot 0, which no wave reads
+    // after the last chunk's barrier), each store instruction writes 8 whole 128-byte rows, so the
+    // non-temporal stores go out as full lines (8-byte pieces went out as partial ones: 1.3x the
+    // written bytes).  Unit u of row r sits at unit u ^ (r & 7).
     auto store_tile = [&](int j) {
         float l = lsum[j];
         l += xor_lane<16>(l);
         l += xor_lane<32>(l);
-        const int qrow = 16 * tile[j] + l16;
-        if (qrow >= t) return;
         const float inv = 1.0f / l;
-        uint16_t *orow = (uint16_t *)out + (((size_t)b * t + qrow) * pv.H + h) * kHeadDim;
+        uint16_t *st = (w < 4 ? &ks[0][0][0] : &vs[0][0][0]) + (w & 3) * 16 * kHeadDim;
 #pragma unroll
         for (int dg = 0; dg < 4; ++dg)
-            st_stream(orow + 16 * dg + 4 * g, make_uint2(pack_bf16(o[j][dg][0] * inv, o[j][dg][1] * inv),
-                                                         pack_bf16(o[j][dg][2] * inv, o[j][dg][3] * inv)));
+            *(uint2 *)(st + l16 * kHeadDim + 8 * ((2 * dg + (g >> 1)) ^ (l16 & 7)) + 4 * (g & 1)) =
+                make_uint2(pack_bf16(o[j][dg][0] * inv, o[j][dg][1] * inv),
+                           pack_bf16(o[j][dg][2] * inv, o[j][dg][3] * inv));
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int r = (lane >> 3) + 8 * i, unit = lane & 7, qrow = 16 * tile[j] + r;
+            const uint4 v = *(const uint4 *)(st + r * kHeadDim + 8 * (unit ^ (r & 7)));
+            if (qrow < t) st_stream((uint16_t *)out + (((size_t)b * t + qrow) * pv.H + h) * kHeadDim + 8 * unit, v);
+        }
     };
     // The lane's LDS read offsets within a chunk slot, computed once: the swizzle of a row depends
     // on its low 4 bits only, so the slot, the 16-key group, the 32-key half and the second

@@ -117,13 +117,16 @@ __device__ __forceinline__ uint4 ld_stream(const void *p) {
     return make_uint4(a.x, a.y, a.z, a.w);
 }
 
-// Stores with the non-temporal hint, for 8- or 16-byte pieces of rows that nothing in the launch
-// reads back: they go out to memory as they are written, while the launch still computes, instead
-// of staying dirty in L2 until the launch's end writes L2 back.  Measured: the prefill's page and
-// output stores at 64 streams x 256 positions 28.9 -> 27.8 us per launch; the projections' and
-// LayerNorm's outputs in the 2048-stream layer step 5.20 -> 5.14 ms per step.  The decode's own
-// stores (2 bytes a lane for its output, 4 for the append) stay plain: hinted, they cost 1.5 us of
-// 171 at 1024 streams and 1.3 of 28.6 at one kv head.
+// Stores with the non-temporal hint, for rows that nothing in the launch reads back: they go out to
+// memory as they are written, while the launch still computes, instead of staying dirty in L2 until
+// the launch's end writes L2 back.  Each store instruction should cover whole 128-byte lines (8
+// lanes x 16 bytes per row): hinted 8-byte pieces go out as partial lines (the prefill's output
+// written that way read 1.3x its bytes in WRITE_SIZE).  Measured: the prefill's page and output
+// stores at 64 streams x 256 positions 29.4 -> 26.5-26.9 us per launch (32 x 512 on k_prefill_mfma
+// 50.8 -> 42.4-43.3 us with whole-line output stores); the projections' and LayerNorm's outputs in
+// the 2048-stream layer step 5.23 -> 5.16 ms per step.  The decode's own stores (2 bytes a lane for
+// its output, 4 for the append) stay plain: hinted, they cost 1.5 us of 171 at 1024 streams and
+// 1.3 of 28.6 at one kv head.
 __device__ __forceinline__ void st_stream(void *p, const uint4 &v) {
     typedef unsigned u32x4_nt __attribute__((ext_vector_type(4)));
     __builtin_nontemporal_store(u32x4_nt{v.x, v.y, v.z, v.w}, (u32x4_nt *)p);
