@@ -35,6 +35,11 @@
   holding U[64, 2048] rows written so far; per step every stream evicts its oldest row once the
   window is full, appends one and attends over min(n+1, 512) rows.  Value: frames/s.
 
+--workload mimi: Mimi's windowed attention (2 layers x 8 heads x 64, context 250, bf16): 256 streams,
+  each step a 250-row chunk (a 10 s voice clip at 25 Hz) into a window that already holds 249 rows.
+  Value: positions/s over the whole step (the windowed attention and the window append).  Roofline:
+  the windowed attention launch (q, out, the chunk's k and v, the held rows it sees) against 8 TB/s.
+
 --workload vendor_gemm: not this library -- the vendor library's bf16 GEMMs (hipBLASLt through torch)
   at the layer step's four projection shapes and torch's LayerNorm, replayed from a graph, for
   comparison with the q8 projections.  Value: us per layer for the four GEMMs.
@@ -408,6 +413,102 @@ def run_prefill(args, xnp, torch):
             "mfma": {"achieved": round(tflops, 2), "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4), "flops_per_launch": flops}}
     return line("prompt prefill positions/sec (64 streams x 256); MFMA TFLOP/s % peak", S * T / (ms / 1000.0),
+                "positions/s", args, ms, "bf16", config, roof, cpu, pct=pct)
+
+
+# ---- Mimi's windowed attention (a voice clip through Mimi's transformer) -------------------------------
+# Mimi's transformer (the reference's fixture config: d_model 512, 8 heads, 2 layers, context 250):
+# each step pushes a chunk of rows through a window of `context` positions per stream
+# (transformer.rs:257-318,764-781).
+MIMI_LAYERS, MIMI_CONTEXT = 2, 250
+
+
+def mimi_held(context=MIMI_CONTEXT):
+    """Held rows of a full window that the queries of the next chunk see: row i of the chunk sees the
+    context - 1 - i before the chunk, so row 0 sees context - 1 of them."""
+    return context - 1
+
+
+def mimi_bytes(S, T, held, kvh=H):
+    """One k_prefill_window launch: q and the output (H heads), the chunk's k and v (kvh heads) and the
+    held rows any query sees (K and V, kvh heads), each read or written once, all bf16."""
+    return S * (2 * T * H * D * 2 + 2 * T * kvh * D * 2 + 2 * held * kvh * D * 2)
+
+
+def cpu_mimi(T, seconds, sample=2):
+    oracle = _load("oracle", os.path.join(ROOT, "oracle", "oracle.py"))
+    rng = np.random.default_rng(SEED + 700)
+    wins = [oracle.Window(MIMI_LAYERS, H, D, MIMI_CONTEXT, rows_max=T, act="bf16") for _ in range(sample)]
+
+    def chunk(w):
+        for layer in range(MIMI_LAYERS):
+            q, k, v = (bf16_np(rng.standard_normal((T, H, D))) for _ in range(3))
+            w.attend(layer, q, k, v)
+        w.commit(T)
+
+    for w in wins:  # a full window first, as on the GPU
+        chunk(w)
+    done, t0 = 0, time.perf_counter()
+    while True:
+        for w in wins:
+            chunk(w)
+            done += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {"value": round(done * T / el, 1), "unit": "positions/s", "cores": 1, "kind": "port",
+            "sample": f"{done} chunks of {T} rows x {MIMI_LAYERS} layers on {sample} full {MIMI_CONTEXT}-position "
+                      f"windows, one thread (the oracle's window is not threaded), {el:.1f} s"}
+
+
+def run_mimi(args, xnp, torch):
+    dev = torch.device("cuda:0")
+    S, T, L, C = args.mimi_streams, args.mimi_chunk, MIMI_LAYERS, MIMI_CONTEXT
+    mbps = (C + 15) // 16
+    chunks = args.warmup + args.steps + 2
+    pool = xnp.KvPool(num_layers=L, num_heads=H, num_blocks=S * mbps + 16, max_streams=S, max_blocks_per_stream=mbps,
+                      cache_dtype="bf16", act_dtype="bf16", max_pos=T * chunks + 16, page_seed=SEED + 7)
+    ids = [pool.init_window(C) for _ in range(S)]
+    gen = torch.Generator(device=dev).manual_seed(SEED + 8)
+    q = [torch.randn((S, T, H, D), generator=gen, device=dev).to(torch.bfloat16) for _ in range(L)]
+    k = [torch.randn((S, T, H, D), generator=gen, device=dev).to(torch.bfloat16) for _ in range(L)]
+    v = [torch.randn((S, T, H, D), generator=gen, device=dev).to(torch.bfloat16) for _ in range(L)]
+    out = [torch.empty((S, T, H, D), dtype=torch.bfloat16, device=dev) for _ in range(L)]
+
+    def step(events):
+        pool.begin(ids, t=T)
+        for layer in range(L):
+            if events is not None and events[layer] is not None:
+                pool.time_next(*events[layer])
+            pool.attend(layer, q[layer], k[layer], v[layer], out[layer], 0.125)
+        pool.end()
+
+    step(None)  # the first chunk fills every window: the timed chunks see full windows
+    torch.cuda.synchronize()
+    # each layer's window append runs between the layers' attention launches, so a span would hold it:
+    # one launch per timed step records both events around its own kernel
+    ms, kern, pct = timed_steps(step, args.steps, args.warmup, L, span=False)
+    avg_ms = float(kern.mean())
+    held = mimi_held(C)
+    hbm = mimi_bytes(S, T, held)
+    gbs = hbm / (avg_ms * 1e-3) / 1e9
+    # every query row sees `context` keys (its own and the context - 1 before it) once the window is full
+    flops = 4.0 * D * T * min(C, held + T) * H * S
+    tflops = flops / (avg_ms * 1e-3) / 1e12
+    cpu = None if args.no_cpu else cpu_mimi(T, args.cpu_seconds)
+    config = {"workload": f"Mimi windowed attention: {S} streams, chunks of {T} rows into full {C}-position windows, "
+                          f"{L} layers x {H} heads x {D}, bf16, RoPE theta 10000",
+              "streams": S, "chunk": T, "context": C, "layers": L}
+    roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic_of("mimi", {"streams": S, "chunk": T}, hbm),
+            "kernel": "k_prefill_window (RoPE + windowed attention on v_mfma_f32_32x32x16_bf16, the held rows from "
+                      "the pages and the chunk's own from k and v), one launch per layer; the step's k_window_append "
+                      "(the rows that stay into their slots) is in the step time, not here",
+            "avg_kernel_us": round(avg_ms * 1000.0, 2), "bytes_per_launch": hbm,
+            "mfma": {"achieved": round(tflops, 2), "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4), "flops_per_launch": flops}}
+    return line(f"Mimi windowed attention positions/sec ({S} streams x {T}-row chunks, context {C})", S * T / (ms / 1000.0),
                 "positions/s", args, ms, "bf16", config, roof, cpu, pct=pct)
 
 
@@ -939,7 +1040,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=["decode", "prefill", "window", "step", "flowlm", "frame", "vendor_gemm"],
+    ap.add_argument("--workload", choices=["decode", "prefill", "window", "step", "flowlm", "frame", "mimi",
+                                           "vendor_gemm"],
                     default="decode")
     ap.add_argument("--step-streams", type=int, default=2048)
     ap.add_argument("--step-max-len", type=int, default=1500)
@@ -953,6 +1055,8 @@ def main():
                     help="decode: kv heads stored (grouped query heads; 0: one per query head)")
     ap.add_argument("--prefill-streams", type=int, default=64)
     ap.add_argument("--prompt", type=int, default=256)
+    ap.add_argument("--mimi-streams", type=int, default=256)
+    ap.add_argument("--mimi-chunk", type=int, default=250)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--headline-only", action="store_true",
@@ -981,7 +1085,7 @@ def main():
     xnp = _load("xn_ptts_amd", os.path.join(ROOT, "xn-ptts_amd"))
     xnp.load_library()
     runs = {"decode": run_decode, "prefill": run_prefill, "window": run_window, "step": run_step,
-            "flowlm": run_flowlm, "frame": run_frame, "vendor_gemm": run_vendor_gemm}
+            "flowlm": run_flowlm, "frame": run_frame, "mimi": run_mimi, "vendor_gemm": run_vendor_gemm}
     out = runs[args.workload](args, xnp, torch)
     if args.workload == "decode" and not args.headline_only and headline_args(args):
         out["configs"] = nested_configs(args, xnp, torch, runs)

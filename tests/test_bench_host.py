@@ -41,6 +41,24 @@ def test_window_bytes_count_rows_scales_and_page_ids():
     assert b.window_bytes([16]) == 16384 + 128 + 2048 + 2048 + 1024 + 8
 
 
+def test_mimi_bytes_count_the_chunk_and_the_held_rows_it_sees():
+    b = _bench()
+    # a full window of context 250 holds 249 rows between chunks; row 0 of the next chunk sees all
+    assert b.mimi_held(250) == 249 and b.mimi_held(6) == 5
+    # one stream, a 250-row chunk: q and out (2 x 250 x 8 x 64 x 2 = 512000), the chunk's k and v
+    # (512000), K and V of the 249 held rows (2 x 249 x 8 x 64 x 2 = 509952)
+    assert b.mimi_bytes(1, 250, 249) == 512000 + 512000 + 509952
+    assert b.mimi_bytes(3, 250, 249) == 3 * b.mimi_bytes(1, 250, 249)
+    # two kv heads under 8 query heads: q and out per query head, the rest per kv head
+    assert b.mimi_bytes(1, 4, 5, kvh=2) == 2 * 4 * 8 * 64 * 2 + 2 * 4 * 2 * 64 * 2 + 2 * 5 * 2 * 64 * 2
+
+
+def test_mimi_cpu_baseline_runs_chunks_of_the_oracle_window():
+    b = _bench()
+    cpu = b.cpu_mimi(16, 0.01, sample=1)
+    assert cpu["unit"] == "positions/s" and cpu["value"] > 0 and cpu["kind"] == "port"
+
+
 def test_traffic_comes_from_the_profiled_workload_only():
     b = _bench()
     with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
