@@ -97,50 +97,81 @@ hipError_t launch_append(const PoolView &pv, const BatchView &bv, int layer, con
 // A window step's rows into the window after its attention (Mimi's chunk, bf16 and f32 pools):
 // slot s takes the step's last row i with (p + i) % window == s; a row that a later row of the
 // step overwrites is never written.  One work group per (stream, page of the window), one wave per
-// kv head for the page's 16 slots: each lane (keys in lanes 0-31, values in 32-63, one pair of dims
-// each, as append_row_wave) first loads its pair of every slot's row and its RoPE pair, all 16
-// unconditionally (a slot the step leaves alone loads row 0, never stored), then rotates the keys
-// and stores the rows.  One round trip per wave: a loop of append_row_wave calls waited out one per
-// slot (its stores may alias the next slot's loads), 96 us per layer at 256 streams x 250 rows.
+// kv head for the page's 16 slots.
+//   bf16: lane l takes 16-byte unit l % 8 of the K and V rows of slots l / 8 and l / 8 + 8, and
+//         each slot's row comes from the lane's own arithmetic: four 16-byte loads and the RoPE
+//         pieces of its two keys, all issued unconditionally (a slot the step leaves alone loads
+//         row 0, never stored), then rotate8 on the keys (the packed bf16 table the prefill
+//         kernels rotate with: the same products and roundings as append_row_wave) and four
+//         16-byte stores.
+//   f32:  each lane one pair of dims (keys in lanes 0-31, values in 32-63, as append_row_wave),
+//         every slot's loads first, then the rotations and stores.
+// A loop of append_row_wave calls took 96 us per layer at 256 streams x 250 rows (each slot's loads
+// waited for the previous slot's stores), and one slot per step of a scalar loop 68 us (two
+// integer divisions per slot on the scalar unit).
 
 template <int CDT, bool ABF>
 __global__ __launch_bounds__(1024) void k_window_append(PoolView pv, BatchView bv, int layer, const void *k,
                                                         const void *v) {
-    static_assert(CDT == DT_F32 || CDT == DT_BF16, "bf16 and f32 windows; int8 ones append row by row");
+    static_assert((CDT == DT_BF16 && ABF) || (CDT == DT_F32 && !ABF), "bf16 and f32 windows; int8 ones append row by row");
     const int b = blockIdx.x / pv.mbps, blk = blockIdx.x % pv.mbps;
     const StreamPlan P = bv.plans[b];
-    const int W = P.window, t = bv.t, j = threadIdx.x >> 6, lane = threadIdx.x & 63, kv = lane >> 5, pr = lane & 31;
+    const int W = P.window, t = bv.t, j = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (W <= 0 || kBlock * blk >= W) return;
     const int page = pv.tables[(size_t)P.sid * pv.mbps + blk];
     if (page < 0 || page >= pv.NB) return; // begin took this page; never index the pool without one
-    constexpr int AE = ABF ? 2 : 4;
-    const char *src = (const char *)(kv ? v : k);
-    int row[kBlock];
-    float2 x[kBlock], cs[kBlock];
+    const int rb = ((kBlock * blk - P.pos) % W + W) % W; // the first row of the step in the page's slot 0
+    // the last row of the step in slot kBlock * blk + n, or -1
+    auto last_row = [&](int n) {
+        const int s = kBlock * blk + n, r = (rb + n) % W;
+        return s < W && r < t ? (t <= W ? r : r + W * ((t - 1 - r) / W)) : -1;
+    };
+    if constexpr (CDT == DT_BF16) {
+        const int unit = lane & 7;
+        int row[2];
+        uint4 kx[2], vx[2], cs[2];
 #pragma unroll
-    for (int n = 0; n < kBlock; ++n) {
-        const int s = kBlock * blk + n;
-        const int r = ((s - P.pos) % W + W) % W; // the first row of the step in slot s
-        row[n] = s < W && r < t ? r + W * ((t - 1 - r) / W) : -1; // the last, or none
-        const int i = max(row[n], 0);
-        x[n] = load_pair<ABF>(src + (((size_t)P.out_row * t + i) * pv.KVH + j) * kHeadDim * AE, pr);
-        cs[n] = pv.rope[(size_t)(P.key_pos + i) * (pv.D / 2) + pr];
-    }
-    const size_t tile = tile_index(pv, layer, kv, page, j);
-#pragma unroll
-    for (int n = 0; n < kBlock; ++n) {
-        if (row[n] < 0) continue;
-        float2 y = x[n];
-        if (kv == 0) { // the key rotated at its position (rope.rs:74-95), as append_row_wave rotates it
-            const float a = y.x * cs[n].x, bb = y.y * cs[n].y, e = y.x * cs[n].y, f = y.y * cs[n].x;
-            y.x = round_act<ABF>(a - bb);
-            y.y = round_act<ABF>(e + f);
+        for (int hf = 0; hf < 2; ++hf) {
+            row[hf] = last_row((lane >> 3) + 8 * hf);
+            const int i = max(row[hf], 0);
+            const size_t arow = (((size_t)P.out_row * t + i) * pv.KVH + j) * kHeadDim + 8 * unit;
+            kx[hf] = *(const uint4 *)((const uint16_t *)k + arow);
+            vx[hf] = *(const uint4 *)((const uint16_t *)v + arow);
+            cs[hf] = *(const uint4 *)(pv.rope16 + (size_t)(P.key_pos + i) * (kHeadDim / 2) + 4 * unit);
         }
-        const size_t o = tile * (kBlock * kHeadDim / 2) + n * (kHeadDim / 2) + pr;
-        if constexpr (CDT == DT_F32)
-            ((float2 *)pv.pages)[o] = y;
-        else
-            ((uint32_t *)pv.pages)[o] = bf16_bits(y.x) | (bf16_bits(y.y) << 16);
+        uint16_t *kt = (uint16_t *)pv.pages + tile_index(pv, layer, 0, page, j) * (kBlock * kHeadDim);
+        uint16_t *vt = (uint16_t *)pv.pages + tile_index(pv, layer, 1, page, j) * (kBlock * kHeadDim);
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            if (row[hf] < 0) continue;
+            const int o = ((lane >> 3) + 8 * hf) * kHeadDim + 8 * unit;
+            *(uint4 *)(kt + o) = rotate8(kx[hf], cs[hf]);
+            *(uint4 *)(vt + o) = vx[hf];
+        }
+    } else {
+        const int kv = lane >> 5, pr = lane & 31;
+        const char *src = (const char *)(kv ? v : k);
+        int row[kBlock];
+        float2 x[kBlock], cs[kBlock];
+#pragma unroll
+        for (int n = 0; n < kBlock; ++n) {
+            row[n] = last_row(n);
+            const int i = max(row[n], 0);
+            x[n] = load_pair<false>(src + (((size_t)P.out_row * t + i) * pv.KVH + j) * kHeadDim * 4, pr);
+            cs[n] = pv.rope[(size_t)(P.key_pos + i) * (pv.D / 2) + pr];
+        }
+        const size_t tile = tile_index(pv, layer, kv, page, j);
+#pragma unroll
+        for (int n = 0; n < kBlock; ++n) {
+            if (row[n] < 0) continue;
+            float2 y = x[n];
+            if (kv == 0) { // the key rotated at its position (rope.rs:74-95), as append_row_wave rotates it
+                const float a = y.x * cs[n].x, bb = y.y * cs[n].y, e = y.x * cs[n].y, f = y.y * cs[n].x;
+                y.x = a - bb;
+                y.y = e + f;
+            }
+            ((float2 *)pv.pages)[tile * (kBlock * kHeadDim / 2) + n * (kHeadDim / 2) + pr] = y;
+        }
     }
 }
 

@@ -136,6 +136,20 @@ __device__ __forceinline__ void st_stream(void *p, const uint2 &v) {
     __builtin_nontemporal_store(u32x2_nt{v.x, v.y}, (u32x2_nt *)p);
 }
 
+// Rotate 8 bf16 values (4 pairs) with 4 packed bf16 (cos, sin) pairs, rounded to bf16 (rope.rs:74-95).
+__device__ __forceinline__ uint4 rotate8(const uint4 &x, const uint4 &cs) {
+    const uint32_t *u = (const uint32_t *)&x, *r = (const uint32_t *)&cs;
+    uint32_t o4[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float x0 = bf16_value(u[e] & 0xffffu), x1 = bf16_value(u[e] >> 16);
+        const float c = bf16_value(r[e] & 0xffffu), s = bf16_value(r[e] >> 16);
+        const float a = x0 * c, bb = x1 * s, ee = x0 * s, f = x1 * c;
+        o4[e] = pack_bf16(a - bb, ee + f);
+    }
+    return make_uint4(o4[0], o4[1], o4[2], o4[3]);
+}
+
 template <int CDT> constexpr int esize() { return CDT == DT_F32 ? 4 : CDT == DT_BF16 ? 2 : 1; }
 
 // Element offset of row 0 of tile (layer, kv, page, head).
