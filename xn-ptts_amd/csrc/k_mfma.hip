@@ -539,9 +539,7 @@ __device__ __forceinline__ void prefill_fast_group(const PoolView &pv, const Bat
     // non-temporal stores go out as full lines (8-byte pieces went out as partial ones: 1.3x the
     // written bytes).  Unit u of row r sits at unit u ^ (r & 7).
     auto store_tile = [&](int j) {
-        float l = lsum[j];
-        l += xor_lane<16>(l);
-        l += xor_lane<32>(l);
+        const float l = swap_sum<32>(swap_sum<16>(lsum[j]));
         const float inv = 1.0f / l;
         uint16_t *st = (w < 4 ? &ks[0][0][0] : &vs[0][0][0]) + (w & 3) * 16 * kHeadDim;
 #pragma unroll
@@ -627,12 +625,11 @@ __device__ __forceinline__ void prefill_fast_group(const PoolView &pv, const Bat
                         if (r > lim) s[kg][r] = -INFINITY;
                 }
             }
-            float mx = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
+            // the row's max: a chain of pairs (v_max3), then over the row's 4 lanes by row swaps
+            float mx = fmaxf(s[0][0], s[0][1]);
 #pragma unroll
-            for (int kg = 1; kg < 4; ++kg)
-                mx = fmaxf(mx, fmaxf(fmaxf(s[kg][0], s[kg][1]), fmaxf(s[kg][2], s[kg][3])));
-            mx = fmaxf(mx, xor_lane<16>(mx));
-            mx = fmaxf(mx, xor_lane<32>(mx));
+            for (int e = 2; e < 16; e += 2) mx = fmaxf(fmaxf(mx, s[e >> 2][e & 3]), s[e >> 2][(e & 3) + 1]);
+            mx = swap_max<32>(swap_max<16>(mx));
             // lazy rescaling, as in decode: the row's sum and accumulators move to a new max only
             // when some row of the wave saw its max grow by more than 8 (log2 units)
             const float mn = fmaxf(m[j], mx * qmul);

@@ -95,6 +95,20 @@ template <int O> __device__ __forceinline__ float xor_lane(float x) {
         return __shfl_xor(x, O);
     }
 }
+// The max (sum) of x over lanes l and l ^ O, O = 16 or 32, in both: gfx950's row swaps return the
+// partner's value beside the lane's own, so the two results combine without a lane-index select.
+template <int O> __device__ __forceinline__ float swap_max(float x) {
+    static_assert(O == 16 || O == 32, "row swaps");
+    const auto r = O == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false)
+                           : __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+template <int O> __device__ __forceinline__ float swap_sum(float x) {
+    static_assert(O == 16 || O == 32, "row swaps");
+    const auto r = O == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false)
+                           : __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 __device__ __forceinline__ float wave_sum(float x) {
     x += dpp_move<0xB1>(x);  // quad_perm [1, 0, 3, 2]
     x += dpp_move<0x4E>(x);  // quad_perm [2, 3, 0, 1]
