@@ -305,12 +305,11 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
                         for (int r = 0; r < 4; ++r)
                             if (kbase + 16 * kg + 4 * g + r > qs) s[kg][r] = -INFINITY;
                 }
-                float mx = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
+                // the row's max: a chain of pairs (v_max3), then over the row's 4 lanes by row swaps
+                float mx = fmaxf(s[0][0], s[0][1]);
 #pragma unroll
-                for (int kg = 1; kg < 4; ++kg)
-                    mx = fmaxf(mx, fmaxf(fmaxf(s[kg][0], s[kg][1]), fmaxf(s[kg][2], s[kg][3])));
-                mx = fmaxf(mx, __shfl_xor(mx, 16));
-                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                for (int e = 2; e < 16; e += 2) mx = fmaxf(fmaxf(mx, s[e >> 2][e & 3]), s[e >> 2][(e & 3) + 1]);
+                mx = swap_max<32>(swap_max<16>(mx));
                 // lazy rescaling, as in decode: the row's sum and accumulators move to a new max only
                 // when some row of the wave saw its max grow by more than 8 (log2 units); until then
                 // exponents are taken against the older max and stay below 2^8
@@ -370,9 +369,7 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             if (tile[j] < 0) continue;
-            float l = lsum[j];
-            l += __shfl_xor(l, 16);
-            l += __shfl_xor(l, 32);
+            const float l = swap_sum<32>(swap_sum<16>(lsum[j]));
             const float inv = 1.0f / l;
             uint16_t(*st)[kPfLd] = &ks[16 * w];
 #pragma unroll

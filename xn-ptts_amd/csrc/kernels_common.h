@@ -109,6 +109,15 @@ template <int O> __device__ __forceinline__ float swap_sum(float x) {
                            : __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
+// The max of x over each 32-lane half of the wave, in every lane of the half: DPP steps within each
+// 16-lane row (quad permutes, the half-row and row mirrors), then the row swap with lane l ^ 16.
+__device__ __forceinline__ float half_max(float x) {
+    x = fmaxf(x, dpp_move<0xB1>(x));  // quad_perm [1, 0, 3, 2]
+    x = fmaxf(x, dpp_move<0x4E>(x));  // quad_perm [2, 3, 0, 1]
+    x = fmaxf(x, dpp_move<0x141>(x)); // row_half_mirror
+    x = fmaxf(x, dpp_move<0x140>(x)); // row_mirror
+    return swap_max<16>(x);
+}
 __device__ __forceinline__ float wave_sum(float x) {
     x += dpp_move<0xB1>(x);  // quad_perm [1, 0, 3, 2]
     x += dpp_move<0x4E>(x);  // quad_perm [2, 3, 0, 1]
@@ -210,9 +219,7 @@ __device__ void append_row_wave(const PoolView &pv, int layer, int page, int row
     } else {
         // int8: per-(page, head) scale amax / 127.  A page holding another live row keeps its
         // scale unless this row needs a larger one; then its other rows are requantized.
-        float amax = fmaxf(fabsf(x.x), fabsf(x.y));
-#pragma unroll
-        for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+        const float amax = half_max(fmaxf(fabsf(x.x), fabsf(x.y))); // over this row's 32 lanes
         const float s_row = amax / 127.0f;
         float *sp = pv.scales + tile;
         const float s_old = *sp;
