@@ -714,24 +714,27 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
 // transformer.rs:764-781: t query rows over a window cache of W rows (slot p mod W holds position
 // p) and the chunk's own rows, each row seeing the W keys up to itself, for chunks of any length.
 //
-// One work group of 4 waves per (stream, head), two work groups per CU.  Keys are indexed
+// One work group of 8 waves per (stream, head), two work groups per CU.  Keys are indexed
 // virtually: the window's held rows first (j < ncache, oldest first, at slot (wbase + j) mod W),
 // then the chunk's rows (j = ncache + i: input row i, rotated at its position and rounded to bf16).
 // Query row i has virtual index ncache + i and sees key j when ncache + i - W < j <= ncache + i.
 // The chunk's rows reach the window by their own append (k_window_append); this kernel only reads.
 //
 // Query rows are taken in rounds of 256: 8 pairs of 16-row tiles, pair i rows 32 i .. 32 i + 31 of
-// the round, wave w owning pairs w and 7 - w.  A round's keys (from the window of its first row to
+// the round, wave w owning pair w.  A round's keys (from the window of its first row to
 // its last row) stream through a ring of 3 LDS slots in chunks of 64 (K and V as
 // [key][unit ^ swz(key)], K's rope pieces beside them), loaded straight into LDS
 // (global_load_lds_dwordx4) 2 chunks ahead of the one attended, so that no register holds them.
 // At each chunk a lane waits for its own loads of it, rotates the chunk's own keys among them in
 // place, and one barrier hands the chunk to every wave.
 //
-// The two tiles of a pair are the 32 columns of v_mfma_f32_32x32x16_bf16, and each K and V piece a
-// wave reads from LDS serves both of its pairs: 64 queries.  At two waves per SIMD a wave holds
-// 256 registers: its pairs' queries and accumulators.  Both contractions are computed transposed
-// so that P never leaves registers:
+// The two tiles of a pair are the 32 columns of v_mfma_f32_32x32x16_bf16.  A wave holds one pair's
+// queries and accumulators in 128 registers, so four waves share a SIMD (the chunk and block loops
+// stay rolled: unrolled, the compiler hoists operand reads across them and spills; a few setup values
+// still spill once per group).  With two pairs a wave (4 waves a group, 253 registers, two waves a
+// SIMD) each K and V piece served 64 queries, but the waves waited 44 % of their cycles and the
+// launch took 6 % longer.  Both contractions are computed transposed so that P never leaves
+// registers:
 //   S^T = K Q^T      A = 32 keys of K from LDS (lane: key lane % 32, dims 16 kk + 8 (lane / 32)),
 //                    B = the pair's rotated queries (lane: query column lane % 32, same dims);
 //                    lane l holds column l % 32 against keys 8 (r / 4) + 4 (l / 32) + r % 4;
@@ -745,13 +748,14 @@ typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
 
 constexpr int kWpChunk = 64;  // keys of a chunk
 constexpr int kWpSlots = 3;   // chunk slots of the LDS ring: 2 chunks load while one is attended
-constexpr int kWpWaves = 4;   // waves per work group
-constexpr int kWpPairs = 2;   // tile pairs per wave
-constexpr int kWpRound = 256; // query rows per round: 4 waves x 2 pairs x 32 rows
-// A chunk is 24 direct loads of 1 KB (8 keys each), 6 a wave: 2 each of K, V and K's rope pieces.
+constexpr int kWpWaves = 8;   // waves per work group
+constexpr int kWpPairs = 1;   // tile pairs per wave
+constexpr int kWpRound = 256; // query rows per round: 8 waves x 1 pair x 32 rows
+// A chunk is 24 direct loads of 1 KB (8 keys each), 3 a wave: one each of K, V and K's rope pieces.
 constexpr int kWpLoadsC = kWpChunk / 8 / kWpWaves; // loads of K (of V, of rope pieces) per wave per chunk
+constexpr int kWpKeysW = kWpChunk / kWpWaves;      // keys of a chunk each wave loads
 static_assert(kWpRound == kWpWaves * kWpPairs * 32, "a round is the waves' pairs");
-static_assert(kWpLoadsC == 2 && kWpSlots == 3, "the waits below count 6 loads a chunk, 2 chunks ahead");
+static_assert(kWpLoadsC == 1 && kWpSlots == 3, "the waits below count 3 loads a chunk, 2 chunks ahead");
 
 // K's and V's LDS rows are 128 bytes, their 16-byte units placed at unit ^ swz(key): for 16 keys in
 // a row (the reads of K's pieces) and for keys 4a .. 4a + 3 with two adjacent units each (the
@@ -772,18 +776,18 @@ __device__ __forceinline__ float pair_sum(float x) {
 }
 
 // Vector-memory loads of a wave complete in the order issued (one counter, vmcnt), so a wave waits
-// for chunk c by letting only the `ahead` chunks it issued after it (6 loads each) stay in flight.
+// for chunk c by letting only the `ahead` chunks it issued after it (3 loads each) stay in flight.
 // The loads land in LDS, which the compiler does not track: this wait is the only one they get.
 __device__ __forceinline__ void wait_chunks(int ahead) {
     if (ahead <= 0)
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     else if (ahead == 1)
-        asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
     else
-        asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
 }
 
-__global__ __launch_bounds__(64 * kWpWaves) __attribute__((amdgpu_waves_per_eu(2))) void k_prefill_window(
+__global__ __launch_bounds__(64 * kWpWaves) __attribute__((amdgpu_waves_per_eu(4))) void k_prefill_window(
     PoolView pv, BatchView bv, int layer, const void *q, const void *knew, const void *vnew, void *out, float qmul) {
     __shared__ __attribute__((aligned(16))) uint16_t ks[kWpSlots][kWpChunk][kHeadDim]; // K, [key][unit ^ swz]
     __shared__ __attribute__((aligned(16))) uint16_t vs[kWpSlots][kWpChunk][kHeadDim]; // V, [key][unit ^ swz]
@@ -811,7 +815,7 @@ __global__ __launch_bounds__(64 * kWpWaves) __attribute__((amdgpu_waves_per_eu(2
         const int ln = lane_here(lane);
 #pragma unroll
         for (int i = 0; i < kWpLoadsC; ++i) {
-            const int row = 16 * w + 8 * i, key = row + (ln >> 3), j = min(j0 + key, khi - 1);
+            const int row = kWpKeysW * w + 8 * i, key = row + (ln >> 3), j = min(j0 + key, khi - 1);
             const int unit = (ln & 7) ^ swz(key);
             const uint16_t *ksrc, *vsrc;
             if (j >= nfrom) {
@@ -838,7 +842,7 @@ __global__ __launch_bounds__(64 * kWpWaves) __attribute__((amdgpu_waves_per_eu(2
         const int ln = lane_here(lane);
 #pragma unroll
         for (int i = 0; i < kWpLoadsC; ++i) {
-            const int key = 16 * w + 8 * i + (ln >> 3), j = j0 + key;
+            const int key = kWpKeysW * w + 8 * i + (ln >> 3), j = j0 + key;
             if (j >= khi || j < nfrom) continue;
             uint4 *kp = (uint4 *)&ks[slot][key][8 * (ln & 7)]; // this lane's own pieces
             *kp = rotate8(*kp, rs[slot][w][i][ln]);
@@ -904,7 +908,10 @@ __global__ __launch_bounds__(64 * kWpWaves) __attribute__((amdgpu_waves_per_eu(2
                 if (c < nch) issue(klo + kWpChunk * c, khi, c);
         }
         // the last key any query of the wave sees (pair 1 holds the later rows)
-        const int wq_max = act[1] ? vq_max[1] : act[0] ? vq_max[0] : -1;
+        int wq_max = -1;
+#pragma unroll
+        for (int p = 0; p < kWpPairs; ++p)
+            if (act[p]) wq_max = max(wq_max, vq_max[p]);
 
         float m[kWpPairs], lsum[kWpPairs]; // running max (scaled, log2 units), this lane's share of the sum
         f32x16_t o[kWpPairs][2];           // O^T: dims 32 hh + 8 (r / 4) + 4 hi + r % 4, column col
@@ -919,8 +926,8 @@ __global__ __launch_bounds__(64 * kWpWaves) __attribute__((amdgpu_waves_per_eu(2
         }
 
         for (int cb = 0; cb < nch; cb += kWpSlots) {
-#pragma unroll
-            for (int u = 0; u < kWpSlots; ++u) { // slot and ring indices stay constants
+#pragma unroll 1
+            for (int u = 0; u < kWpSlots; ++u) { // rolled: see above
                 const int c = cb + u;
                 if (c >= nch) break;
                 const int j0 = klo + kWpChunk * c;
@@ -931,6 +938,7 @@ __global__ __launch_bounds__(64 * kWpWaves) __attribute__((amdgpu_waves_per_eu(2
                 lds_barrier(); // chunk c is in LDS; every wave is done with chunk c - 1's slot
                 if (c > 0 && c + kWpSlots - 1 < nch)
                     issue(j0 + kWpChunk * (kWpSlots - 1), khi, (u + kWpSlots - 1) % kWpSlots);
+#pragma unroll 1
                 for (int kb = 0; kb < kWpChunk; kb += 32) {
                     const int jb = j0 + kb; // the block's first key
                     if (jb > wq_max) break; // after every query of the wave
@@ -1012,10 +1020,14 @@ __global__ __launch_bounds__(64 * kWpWaves) __attribute__((amdgpu_waves_per_eu(2
             }
         }
         // The output leaves as whole 128-byte rows: once every wave is done attending, each wave
-        // writes its pairs' O / l (l: the column's sum over its lane pair), rounded to bf16, into 8 KB
-        // of the ring of its own, as [row 32 p + col][unit ^ (row & 7)], and stores 8 rows at a time.
+        // writes its pair's O / l (l: the column's sum over its lane pair), rounded to bf16, into 4 KB
+        // of the K and V rings of its own, as [row 32 p + col][unit ^ (row & 7)], and stores 8 rows at a
+        // time.
         lds_barrier();
-        uint16_t *stage = w < kWpSlots ? &ks[w][0][0] : &vs[w - kWpSlots][0][0];
+        constexpr int kStageRows = 32 * kWpPairs, kRingRows = kWpSlots * kWpChunk;
+        static_assert(kWpWaves * kStageRows <= 2 * kRingRows, "the waves' output tiles fit the K and V rings");
+        uint16_t *stage = kStageRows * w < kRingRows ? &ks[0][0][0] + kStageRows * w * kHeadDim
+                                                     : &vs[0][0][0] + (kStageRows * w - kRingRows) * kHeadDim;
 #pragma unroll
         for (int p = 0; p < kWpPairs; ++p) {
             const float inv = 1.0f / pair_sum(lsum[p]); // not stored for a pair past the round
