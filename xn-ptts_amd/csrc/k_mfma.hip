@@ -865,6 +865,11 @@ __global__ __launch_bounds__(64 * kWpWaves) __attribute__((amdgpu_waves_per_eu(4
         // done.  The round's first chunk goes out ahead of the queries when it reads no page (keys of
         // the step itself), the rest of the ring once the queries are in.
         if (tq0 > 0) __syncthreads();
+        if (tq0 == 0) {
+            // the stream's page ids, read once: the pages of cached keys and of the rows written
+            // (first of all, so that no register holds their addresses through the loads below)
+            for (int i = tid; i < min(pv.mbps, kPfMaxPages); i += 64 * kWpWaves) spages[i] = tab[i];
+        }
         const bool early = klo >= nfrom;
         if (early) issue(klo, khi, 0);
         {
@@ -887,10 +892,6 @@ __global__ __launch_bounds__(64 * kWpWaves) __attribute__((amdgpu_waves_per_eu(4
                     qraw[p][kk] = *(const uint4 *)(qp + 16 * kk + 8 * hi);
                     qcs[p][kk] = *(const uint4 *)(cs + 8 * kk + 4 * hi);
                 }
-            }
-            if (tq0 == 0) {
-                // the stream's page ids, read once: the pages of cached keys and of the rows written
-                for (int i = tid; i < min(pv.mbps, kPfMaxPages); i += 64 * kWpWaves) spages[i] = tab[i];
             }
 #pragma unroll
             for (int p = 0; p < kWpPairs; ++p)
