@@ -306,14 +306,14 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
                             if (kbase + 16 * kg + 4 * g + r > qs) s[kg][r] = -INFINITY;
                 }
                 // the row's max: a chain of pairs (v_max3), then over the row's 4 lanes by row swaps
-                float mx = fmaxf(s[0][0], s[0][1]);
+                float mx = fmax_fin(s[0][0], s[0][1]);
 #pragma unroll
                 for (int e = 2; e < 16; e += 2) mx = fmaxf(fmaxf(mx, s[e >> 2][e & 3]), s[e >> 2][(e & 3) + 1]);
                 mx = swap_max<32>(swap_max<16>(mx));
                 // lazy rescaling, as in decode: the row's sum and accumulators move to a new max only
                 // when some row of the wave saw its max grow by more than 8 (log2 units); until then
                 // exponents are taken against the older max and stay below 2^8
-                const float mn = fmaxf(m[j], mx * qmul);
+                const float mn = fmax_fin(m[j], mx * qmul);
                 if (__any(mn > m[j] + 8.f)) {
                     const float alpha = fast_exp2(m[j] - mn);
                     lsum[j] *= alpha;
@@ -623,13 +623,13 @@ __device__ __forceinline__ void prefill_fast_group(const PoolView &pv, const Bat
                 }
             }
             // the row's max: a chain of pairs (v_max3), then over the row's 4 lanes by row swaps
-            float mx = fmaxf(s[0][0], s[0][1]);
+            float mx = fmax_fin(s[0][0], s[0][1]);
 #pragma unroll
             for (int e = 2; e < 16; e += 2) mx = fmaxf(fmaxf(mx, s[e >> 2][e & 3]), s[e >> 2][(e & 3) + 1]);
             mx = swap_max<32>(swap_max<16>(mx));
             // lazy rescaling, as in decode: the row's sum and accumulators move to a new max only
             // when some row of the wave saw its max grow by more than 8 (log2 units)
-            const float mn = fmaxf(m[j], mx * qmul);
+            const float mn = fmax_fin(m[j], mx * qmul);
             if (__any(mn > m[j] + 8.f)) {
                 const float alpha = fast_exp2(m[j] - mn);
                 lsum[j] *= alpha;
@@ -766,10 +766,7 @@ __device__ __forceinline__ int swz(int key) {
 }
 
 // the pair of a lane's value: lanes l and l ^ 32 exchange (both halves of the result hold both)
-__device__ __forceinline__ float pair_max(float x) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
+__device__ __forceinline__ float pair_max(float x) { return swap_max<32>(x); }
 __device__ __forceinline__ float pair_sum(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
@@ -971,14 +968,14 @@ __global__ __launch_bounds__(64 * kWpWaves) __attribute__((amdgpu_waves_per_eu(4
                                 if (kr > lim || kr <= lim - W) s[r] = -INFINITY;
                             }
                         }
-                        float mx = s[0];
+                        float mx = fmax_fin(s[0], s[1]);
 #pragma unroll
-                        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+                        for (int r = 2; r < 16; ++r) mx = fmaxf(mx, s[r]);
                         mx = pair_max(mx);
                         // lazy rescaling, as in decode: the column's sum and accumulators move to a new
                         // max only when some column of the pair saw its max grow by more than 8 (log2
                         // units); until then exponents are taken against the older max
-                        const float mn = fmaxf(m[p], mx * qmul);
+                        const float mn = fmax_fin(m[p], mx * qmul);
                         if (__any(mn > m[p] + 8.f)) {
                             const float alpha = fast_exp2(m[p] - mn);
                             lsum[p] *= alpha;

@@ -95,13 +95,19 @@ template <int O> __device__ __forceinline__ float xor_lane(float x) {
         return __shfl_xor(x, O);
     }
 }
+// max(a, b) for finite or -inf values: the median of a, b and the largest finite float, one
+// v_med3_f32.  fmaxf quiets each operand the compiler cannot prove quiet first (the results of
+// lane swaps, selects, loads), one more instruction each.  Callers pass scores (finite, or -inf
+// where masked), running maxima and |x| of finite rows.
+__device__ __forceinline__ float fmax_fin(float a, float b) { return __builtin_amdgcn_fmed3f(a, b, 3.40282347e38f); }
+
 // The max (sum) of x over lanes l and l ^ O, O = 16 or 32, in both: gfx950's row swaps return the
 // partner's value beside the lane's own, so the two results combine without a lane-index select.
 template <int O> __device__ __forceinline__ float swap_max(float x) {
     static_assert(O == 16 || O == 32, "row swaps");
     const auto r = O == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false)
                            : __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    return fmax_fin(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 template <int O> __device__ __forceinline__ float swap_sum(float x) {
     static_assert(O == 16 || O == 32, "row swaps");
@@ -112,10 +118,10 @@ template <int O> __device__ __forceinline__ float swap_sum(float x) {
 // The max of x over each 32-lane half of the wave, in every lane of the half: DPP steps within each
 // 16-lane row (quad permutes, the half-row and row mirrors), then the row swap with lane l ^ 16.
 __device__ __forceinline__ float half_max(float x) {
-    x = fmaxf(x, dpp_move<0xB1>(x));  // quad_perm [1, 0, 3, 2]
-    x = fmaxf(x, dpp_move<0x4E>(x));  // quad_perm [2, 3, 0, 1]
-    x = fmaxf(x, dpp_move<0x141>(x)); // row_half_mirror
-    x = fmaxf(x, dpp_move<0x140>(x)); // row_mirror
+    x = fmax_fin(x, dpp_move<0xB1>(x));  // quad_perm [1, 0, 3, 2]
+    x = fmax_fin(x, dpp_move<0x4E>(x));  // quad_perm [2, 3, 0, 1]
+    x = fmax_fin(x, dpp_move<0x141>(x)); // row_half_mirror
+    x = fmax_fin(x, dpp_move<0x140>(x)); // row_mirror
     return swap_max<16>(x);
 }
 __device__ __forceinline__ float wave_sum(float x) {
@@ -159,7 +165,12 @@ __device__ __forceinline__ void st_stream(void *p, const uint2 &v) {
     __builtin_nontemporal_store(u32x2_nt{v.x, v.y}, (u32x2_nt *)p);
 }
 
-// Rotate 8 bf16 values (4 pairs) with 4 packed bf16 (cos, sin) pairs, rounded to bf16 (rope.rs:74-95).
+// Rotate 8 bf16 values (4 pairs) with 4 packed bf16 (cos, sin) pairs, rounded to bf16 (rope.rs:74-95):
+// x0 c - x1 s and x0 s + x1 c, each product rounded to f32, then the sum, then bf16.  A product of
+// two bf16 values has at most 16 significant bits, so it is exact in f32 (outside the subnormal
+// range, below 2^-126), and an fma taking one product unrounded gives the same two roundings with
+// one instruction fewer per output.  (v_dot2_f32_bf16 does not: its sums differ by an f32 ulp now
+// and then, either way, and a zero sum comes out +0 where the separate products give -0.)
 __device__ __forceinline__ uint4 rotate8(const uint4 &x, const uint4 &cs) {
     const uint32_t *u = (const uint32_t *)&x, *r = (const uint32_t *)&cs;
     uint32_t o4[4];
@@ -167,8 +178,7 @@ __device__ __forceinline__ uint4 rotate8(const uint4 &x, const uint4 &cs) {
     for (int e = 0; e < 4; ++e) {
         const float x0 = bf16_value(u[e] & 0xffffu), x1 = bf16_value(u[e] >> 16);
         const float c = bf16_value(r[e] & 0xffffu), s = bf16_value(r[e] >> 16);
-        const float a = x0 * c, bb = x1 * s, ee = x0 * s, f = x1 * c;
-        o4[e] = pack_bf16(a - bb, ee + f);
+        o4[e] = pack_bf16(__builtin_fmaf(x0, c, -(x1 * s)), __builtin_fmaf(x0, s, x1 * c));
     }
     return make_uint4(o4[0], o4[1], o4[2], o4[3]);
 }
