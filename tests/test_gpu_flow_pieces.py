@@ -83,12 +83,38 @@ def test_flow_linear_q8_long_k_within_the_summation_bound(rows, k, n, epilogue):
     xnp.flow_linear_q8(_bf(x), torch.from_numpy(q).to(DEV), torch.from_numpy(s).to(DEV), y, epilogue,
                        bias=torch.from_numpy(b).to(DEV))
     torch.cuda.synchronize()
-    got = y.float().cpu().numpy()
+    _close_within_sum(y.float().cpu().numpy(), want, x, q, s, epilogue)
+
+
+def _close_within_sum(got, want, x, q, s, what):
+    # one bf16 step, plus the recursive-summation bound of both f32 sums, 2 K 2^-24 s sum|x q|
+    k = x.shape[-1]
     bound = 2.0 * k * 2.0 ** -24 * (np.abs(x) @ np.abs(q.astype(np.float32)).T) * s[None, :]
     want64 = np.abs(want.astype(np.float64))
     spacing = np.exp2(np.floor(np.log2(np.maximum(want64, 1e-30))) - 7)
-    assert (np.abs(got.astype(np.float64) - want) <= spacing + bound).all(), epilogue
-    assert (got != want).mean() <= 0.01, (epilogue, float((got != want).mean()))
+    assert (np.abs(got.astype(np.float64) - want) <= spacing + bound).all(), what
+    assert (got != want).mean() <= 0.01, (what, float((got != want).mean()))
+
+
+# 128 x 64 tiles (wide projections that still make 512 work groups with them, such as the stacked
+# adaLN projection at 2048 rows): 257 column tiles by 2 row tiles, the last of one row or of 72; N
+# 8 columns past a multiple of 64 with K of exactly 8 chunks (the staged epilogue, rounds unrolled),
+# or 4 past with K of 8.25 chunks (the per-element epilogue, the looped rounds' past-K masks).  Over
+# 2-3M outputs some lie near zero, where the order of the f32 sum moves them by more than one bf16
+# step; so the bar is the long-K one (a dropped or doubled chunk fails it almost everywhere).
+@pytest.mark.parametrize("rows,k,n", [(129, 512, 16392), (200, 528, 16388)])
+@pytest.mark.parametrize("epilogue", ["store", "store_f32"])
+def test_flow_linear_q8_on_128_row_tiles_matches_the_oracle(rows, k, n, epilogue):
+    rng = np.random.default_rng(rows + k + n)
+    x = bf16_round(rng.standard_normal((rows, k)).astype(np.float32))
+    q, s = oracle.quantize_rows((0.05 * rng.standard_normal((n, k))).astype(np.float32))
+    b = (0.1 * rng.standard_normal(n)).astype(np.float32)
+    want = oracle.flow_linear_q8(x, q, s, epilogue, bias=b)
+    y = torch.zeros((rows, n), dtype=torch.float32 if epilogue == "store_f32" else torch.bfloat16, device=DEV)
+    xnp.flow_linear_q8(_bf(x), torch.from_numpy(q).to(DEV), torch.from_numpy(s).to(DEV), y, epilogue,
+                       bias=torch.from_numpy(b).to(DEV))
+    torch.cuda.synchronize()
+    _close_within_sum(y.float().cpu().numpy(), want, x, q, s, epilogue)
 
 
 def test_flow_linear_q8_reads_f32_rows_rounded():

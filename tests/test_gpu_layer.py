@@ -42,6 +42,18 @@ def test_layer_norm_matches_the_oracle(rows, dim):
 @pytest.mark.parametrize("rows,k,n", [(1, 512, 64), (37, 512, 1536), (200, 512, 2048), (300, 1024, 512), (70, 2048, 512)])
 @pytest.mark.parametrize("epi", ["store", "gelu_erf", "gelu_tanh", "residual"])
 def test_linear_q8_matches_the_oracle(rows, k, n, epi):
+    check_linear_q8(rows, k, n, epi)
+
+
+@pytest.mark.parametrize("epi", ["store", "gelu_erf", "residual"])
+def test_linear_q8_on_128_row_tiles_matches_the_oracle(epi):
+    # Wide projections whose 128 x 64 tiles still make 512 work groups take 128-row tiles (linear1
+    # at 2048 rows): here 257 column tiles by 2 row tiles, the last of one row.  Ragged N and K on
+    # those tiles are in test_gpu_flow_pieces.py.
+    check_linear_q8(129, 512, 16448, epi)
+
+
+def check_linear_q8(rows, k, n, epi):
     rng = np.random.default_rng(rows * 7 + n)
     x = normal(rng, (rows, k), "bf16")
     q, s = xnp.quantize_rows(rng.standard_normal((n, k)).astype(np.float32) * 0.02)

@@ -154,7 +154,9 @@ constexpr int kGmLd = 72; // LDS row length in bf16
 constexpr int kGmPD = 3;  // K chunks of loads in flight
 
 // MI: 16-row MFMA tiles per wave in M, so tiles of 32 MI rows.  MI = 1 doubles the work groups of a
-// narrow projection (N = 512 at 2048 rows gives 256 groups of 64 rows: one wave per SIMD).
+// narrow projection (N = 512 at 2048 rows gives 256 groups of 64 rows: one wave per SIMD).  MI = 4
+// (128 x 64 tiles, each wave 64 x 32) for wide ones that still give two groups per CU: a wave's
+// MFMAs per LDS byte read, and per staged byte, rise by a third.
 //
 // KS: groups of KS x 256 threads.  Half h (256 threads, the tile's 4 waves) takes K chunks h, h + KS,
 // .. into its own LDS buffers; at the end half 1 hands its sums to half 0 through LDS, which adds
@@ -183,16 +185,20 @@ __global__ __launch_bounds__(256 * KS) void k_gemm_q8(const uint16_t *A, int M, 
     const int w = tid >> 6, lane = tid & 63, g = lane >> 4, l16 = lane & 15;
     const int wm = w & 1, wn = w >> 1;
 
-    // staging: A rows a_r (and a_r + 32 when MI = 2), 8 values at k 8 a_k; W row w_r, 16 int8 at
-    // k 16 w_k.
+    // staging: A rows a_r + 32 i, i < MI (the tile's 32 MI rows), 8 values at k 8 a_k; W row w_r, 16
+    // int8 at k 16 w_k.
     // kGmPD chunks of loads are in flight: set c % kGmPD holds chunk c from its load until it is
     // written to LDS.  The words stay as loaded until then -- zeroing past K, rounding f32 A rows
     // and widening W happen at the LDS store, since any use at the load would make the wave wait
     // for it there.
+    constexpr int NA = MI; // A rows a thread stages
     const int a_r = tid >> 3, a_k = tid & 7, w_r = tid >> 2, w_k = tid & 3;
-    const int ar0 = min(m0 + a_r, M - 1), ar1 = min(m0 + a_r + 32 * (MI - 1), M - 1), wr = min(n0 + w_r, N - 1);
+    int ar[NA];
+#pragma unroll
+    for (int i = 0; i < NA; ++i) ar[i] = min(m0 + a_r + 32 * i, M - 1);
+    const int wr = min(n0 + w_r, N - 1);
     constexpr int AW = AF32 ? 2 : 1; // uint4 per 8 A values
-    uint4 ra0[kGmPD][AW], ra1[kGmPD][AW], rw[kGmPD];
+    uint4 ra[NA][kGmPD][AW], rw[kGmPD];
     // NKC > 0: K is a whole number of chunks, so nothing reaches past it and the clamps and masks
     // below drop out (they were 14-18 of a round's 47-51 VALU instructions)
     constexpr bool kWhole = NKC > 0;
@@ -201,17 +207,15 @@ __global__ __launch_bounds__(256 * KS) void k_gemm_q8(const uint16_t *A, int M, 
         // the store
         const int k0 = kc * kGmK;
         const int ka = kWhole || k0 + 8 * a_k < K ? k0 + 8 * a_k : 0, kw = kWhole || k0 + 16 * w_k < K ? k0 + 16 * w_k : 0;
-        if constexpr (AF32) {
-            const float *af = (const float *)A;
-            ra0[set][0] = *(const uint4 *)(af + (size_t)ar0 * K + ka);
-            ra0[set][AW - 1] = *(const uint4 *)(af + (size_t)ar0 * K + ka + 4);
-            if constexpr (MI == 2) {
-                ra1[set][0] = *(const uint4 *)(af + (size_t)ar1 * K + ka);
-                ra1[set][AW - 1] = *(const uint4 *)(af + (size_t)ar1 * K + ka + 4);
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
+            if constexpr (AF32) {
+                const float *af = (const float *)A;
+                ra[i][set][0] = *(const uint4 *)(af + (size_t)ar[i] * K + ka);
+                ra[i][set][AW - 1] = *(const uint4 *)(af + (size_t)ar[i] * K + ka + 4);
+            } else {
+                ra[i][set][0] = *(const uint4 *)(A + (size_t)ar[i] * K + ka);
             }
-        } else {
-            ra0[set][0] = *(const uint4 *)(A + (size_t)ar0 * K + ka);
-            if constexpr (MI == 2) ra1[set][0] = *(const uint4 *)(A + (size_t)ar1 * K + ka);
         }
         rw[set] = *(const uint4 *)(W + (size_t)wr * K + kw);
     };
@@ -230,20 +234,21 @@ __global__ __launch_bounds__(256 * KS) void k_gemm_q8(const uint16_t *A, int M, 
         return pack_bf16((float)(int8_t)((u >> sh) & 0xffu), (float)(int8_t)((u >> (sh + 8)) & 0xffu));
     };
     auto store = [&](int buf, int set, int kc) {
-        uint4 a0 = bf16_row(ra0[set]), a1 = a0, wq = rw[set];
-        if constexpr (MI == 2) a1 = bf16_row(ra1[set]);
+        uint4 av[NA], wq = rw[set];
+#pragma unroll
+        for (int i = 0; i < NA; ++i) av[i] = bf16_row(ra[i][set]);
         // words past K zeroed with masks rather than under a branch: a branch here splits the
         // loop, and past the join the compiler no longer knows which loads are still in flight
         // (it then waits for all of them before the next load)
         if constexpr (!kWhole) {
             const int k0 = kc * kGmK;
             const uint32_t ma = k0 + 8 * a_k < K ? ~0u : 0u, mw = k0 + 16 * w_k < K ? ~0u : 0u;
-            a0 = masked(a0, ma);
-            a1 = masked(a1, ma);
+#pragma unroll
+            for (int i = 0; i < NA; ++i) av[i] = masked(av[i], ma);
             wq = masked(wq, mw);
         }
-        *(uint4 *)&As[h][buf][a_r][8 * a_k] = a0;
-        if constexpr (MI == 2) *(uint4 *)&As[h][buf][a_r + 32][8 * a_k] = a1;
+#pragma unroll
+        for (int i = 0; i < NA; ++i) *(uint4 *)&As[h][buf][a_r + 32 * i][8 * a_k] = av[i];
         *(uint4 *)&Ws[h][buf][w_r][16 * w_k] = make_uint4(widen2(wq.x, 0), widen2(wq.x, 16), widen2(wq.y, 0), widen2(wq.y, 16));
         *(uint4 *)&Ws[h][buf][w_r][16 * w_k + 8] =
             make_uint4(widen2(wq.z, 0), widen2(wq.z, 16), widen2(wq.w, 0), widen2(wq.w, 16));
@@ -575,12 +580,15 @@ hipError_t launch_gemm_q8(const void *A, int M, int K, const int8_t *W, const fl
                           const GemmOut &go, hipStream_t stream) {
     if (M <= 0) return hipSuccess;
     if (N <= 0 || K <= 0 || K % 16) return hipErrorInvalidValue;
-    // 32-row tiles when 64-row ones would leave the chip's 1024 SIMDs under two waves each
-    const int64_t groups64 = (int64_t)((N + kGmT - 1) / kGmT) * ((M + kGmT - 1) / kGmT);
+    // 32-row tiles when 64-row ones would leave the chip's 1024 SIMDs under two waves each; 128-row
+    // tiles when those still give 512 groups (two per CU)
+    const int64_t ntn = (N + kGmT - 1) / kGmT;
+    const int64_t groups64 = ntn * ((M + kGmT - 1) / kGmT), groups128 = ntn * ((M + 127) / 128);
     const bool mi1 = groups64 < 512;
     // two halves per group on alternate K chunks when K is long (32 chunks and more)
     if (K >= 32 * kGmK)
         return mi1 ? gemm_q8_mi<1, 2>(A, M, K, W, s, N, epi, go, stream) : gemm_q8_mi<2, 2>(A, M, K, W, s, N, epi, go, stream);
+    if (groups128 >= 512 && !go.a_f32) return gemm_q8_mi<4, 1>(A, M, K, W, s, N, epi, go, stream);
     return mi1 ? gemm_q8_mi<1, 1>(A, M, K, W, s, N, epi, go, stream) : gemm_q8_mi<2, 1>(A, M, K, W, s, N, epi, go, stream);
 }
 
