@@ -803,6 +803,13 @@ __global__ __launch_bounds__(64 * kWpWaves) __attribute__((amdgpu_waves_per_eu(4
     uint16_t *kpages = (uint16_t *)pv.pages + tile_index(pv, layer, 0, 0, kvh) * (kBlock * kHeadDim);
     uint16_t *vpages = (uint16_t *)pv.pages + tile_index(pv, layer, 1, 0, kvh) * (kBlock * kHeadDim);
 
+    // the K and V rings' LDS addresses, taken once (see lds_addr)
+    const uint32_t ks_at = lds_addr(&ks[0][0][0]), vs_at = lds_addr(&vs[0][0][0]);
+    // the stream's page ids, read once: the pages of cached keys and of the rows written (before the
+    // rounds, so that no register holds their addresses through them; the first round's barrier
+    // precedes every read of them)
+    for (int i = tid; i < min(pv.mbps, kPfMaxPages); i += 64 * kWpWaves) spages[i] = tab[i];
+
     // A chunk's keys j0 + key go straight into LDS slot `slot` by 1 KB loads: lane l of load i of
     // wave w takes key 16 w + 8 i + l / 8 and holds its unit (l % 8) ^ swz(key), and the rope piece
     // of a step's own key to its own place (every load is issued, so that each chunk is 6 loads of
@@ -827,8 +834,9 @@ __global__ __launch_bounds__(64 * kWpWaves) __attribute__((amdgpu_waves_per_eu(4
                 ksrc = kpages + poff;
                 vsrc = vpages + poff;
             }
-            dma16(ksrc, &ks[slot][row][0]);
-            dma16(vsrc, &vs[slot][row][0]);
+            const uint32_t kv_off = (uint32_t)((slot * kWpChunk + row) * kHeadDim) * 2;
+            dma16_at(ksrc, ks_at + kv_off);
+            dma16_at(vsrc, vs_at + kv_off);
             const int r = max(j - ncache, 0);
             dma16(pv.rope16 + (size_t)(P.key_pos + r) * (kHeadDim / 2) + 4 * unit, &rs[slot][w][i][0]);
         }
@@ -862,11 +870,6 @@ __global__ __launch_bounds__(64 * kWpWaves) __attribute__((amdgpu_waves_per_eu(4
         // done.  The round's first chunk goes out ahead of the queries when it reads no page (keys of
         // the step itself), the rest of the ring once the queries are in.
         if (tq0 > 0) __syncthreads();
-        if (tq0 == 0) {
-            // the stream's page ids, read once: the pages of cached keys and of the rows written
-            // (first of all, so that no register holds their addresses through the loads below)
-            for (int i = tid; i < min(pv.mbps, kPfMaxPages); i += 64 * kWpWaves) spages[i] = tab[i];
-        }
         const bool early = klo >= nfrom;
         if (early) issue(klo, khi, 0);
         {

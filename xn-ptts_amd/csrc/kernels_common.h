@@ -298,10 +298,18 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // the chunks issued ahead; the caller's own `s_waitcnt vmcnt(n)` is the wait these loads get.  Every
 // wait the compiler places for its own loads stays correct, as vector-memory accesses complete in
 // the order issued (they can only wait longer).
-__device__ __forceinline__ void dma16(const void *src, void *lds) {
-    const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)lds);
+// The LDS byte address of a pointer into a __shared__ array.  The cast of a generic pointer carries
+// a null check that needs the pointer's high half (the LDS aperture), a register pair kept live
+// from the prologue; taken once of an array's first element, it folds to the array's address, and
+// dma16_at then takes uniform offsets from it.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;
+}
+__device__ __forceinline__ void dma16_at(const void *src, uint32_t lds) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(lds);
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base) : "memory", "m0");
 }
+__device__ __forceinline__ void dma16(const void *src, void *lds) { dma16_at(src, lds_addr(lds)); }
 
 template <int CDT> struct Lanes {
     static constexpr int DPL = 16 / esize<CDT>();
