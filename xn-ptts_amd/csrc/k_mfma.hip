@@ -102,12 +102,14 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
     uint16_t *vpages = (uint16_t *)pv.pages + tile_index(pv, layer, 1, 0, kvh) * (kBlock * kHeadDim);
     const int8_t *kpages8 = (const int8_t *)pv.pages + tile_index(pv, layer, 0, 0, kvh) * (kBlock * kHeadDim);
     const int8_t *vpages8 = (const int8_t *)pv.pages + tile_index(pv, layer, 1, 0, kvh) * (kBlock * kHeadDim);
-    // the stream's page ids for every key any round sees, at most one per thread: loaded here and
-    // put into LDS only once the first round's queries and first chunk are on their way, so that
-    // those loads go out together instead of each waiting for the one before
+    // the stream's page ids for every key any round sees, at most one per thread, loaded straight
+    // into LDS (lane l of wave w: id 64 w + l): no register holds them, and nothing waits for them
+    // before the first round's queries and first chunk go out.  Loads complete in the order
+    // issued, so the waits for those (every wave's query loads come after these) cover them, and
+    // the first round's barrier follows those waits; no earlier read of spages exists.
     const int npg = min((c0 + t + kBlock - 1) / kBlock, kPfMaxPages);
     static_assert(kPfMaxPages <= 64 * kPfWaves, "one page id per thread");
-    const int my_pg = tab[min(tid, npg - 1)];
+    if (64 * w < npg) dma4_at(tab + min(tid, npg - 1), lds_addr(&spages[0]) + 256 * w);
     // this thread's share of a chunk: 16 bytes (8 dims) of one key's K and V
     const int skey = tid >> 3, spart = tid & 7;
 
@@ -215,7 +217,6 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
                 issue(0, st, std::true_type{});
             else
                 issue(0, st, std::false_type{});
-            if (tq0 == 0 && tid < npg) spages[tid] = my_pg;
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 m[j] = -1e30f;
@@ -376,9 +377,12 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(4
             for (int dg = 0; dg < 4; ++dg)
                 *(uint2 *)&st[l16][16 * dg + 4 * g] = make_uint2(pack_bf16(o[j][dg][0] * inv, o[j][dg][1] * inv),
                                                                  pack_bf16(o[j][dg][2] * inv, o[j][dg][3] * inv));
+            // the lane index recomputed here (lane_here): hoisted out of the rounds, the output's
+            // address pieces were held across them and spilled
+            const int ln = lane_here(lane);
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                const int r = (lane >> 3) + 8 * i, unit = lane & 7, qrow = 16 * tile[j] + r;
+                const int r = (ln >> 3) + 8 * i, unit = ln & 7, qrow = 16 * tile[j] + r;
                 const uint4 v = *(const uint4 *)&st[r][8 * unit];
                 if (qrow < t) st_stream((uint16_t *)out + (((size_t)b * t + qrow) * pv.H + h) * kHeadDim + 8 * unit, v);
             }
