@@ -1098,7 +1098,8 @@ NESTED = [("flowlm", 1, "single-stream flow LM, Phonon-31m shape, f32 (batch 1)"
           ("prefill", 3, "prompt prefill, 64 streams x 256 positions"),
           ("window", 4, "int8 KV sliding window (512), 1024 streams"),
           ("step", 5, "full per-frame layer step, 2048 streams"),
-          ("frame", 5, "the batched q8 flow-LM frame around configuration 5's layers (flow net and heads included)")]
+          ("frame", 5, "the batched q8 flow-LM frame around configuration 5's layers (flow net and heads included)"),
+          ("mimi", None, "Mimi's windowed attention (no configuration of its own): 256 streams x 250-row chunks, context 250")]
 
 
 def headline_args(args):

@@ -76,7 +76,8 @@ def test_only_the_default_headline_carries_the_nested_configurations():
     assert b.headline_args(argparse.Namespace(**base))
     for key, value in (("streams", 512), ("max_len", 2048), ("split", 2), ("kv_heads", 1)):
         assert not b.headline_args(argparse.Namespace(**dict(base, **{key: value})))
-    assert sorted({cfg for _, cfg, _ in b.NESTED}) == [1, 3, 4, 5]
+    assert sorted({cfg for _, cfg, _ in b.NESTED if cfg is not None}) == [1, 3, 4, 5]
+    assert {name for name, _, _ in b.NESTED} == {"flowlm", "prefill", "window", "step", "frame", "mimi"}
 
 
 def test_more_than_one_gpu_is_refused_with_a_message():
