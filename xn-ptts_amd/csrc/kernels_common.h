@@ -97,8 +97,8 @@ template <int O> __device__ __forceinline__ float xor_lane(float x) {
 }
 // max(a, b) for finite or -inf values: the median of a, b and the largest finite float, one
 // v_med3_f32.  fmaxf quiets each operand the compiler cannot prove quiet first (the results of
-// lane swaps, selects, loads), one more instruction each.  Callers pass scores (finite, or -inf
-// where masked), running maxima and |x| of finite rows.
+// lane swaps, selects, loads), one more instruction each.  Callers pass attention scores (finite,
+// or -inf where masked) and their running maxima.
 __device__ __forceinline__ float fmax_fin(float a, float b) { return __builtin_amdgcn_fmed3f(a, b, 3.40282347e38f); }
 
 // The max (sum) of x over lanes l and l ^ O, O = 16 or 32, in both: gfx950's row swaps return the
@@ -117,12 +117,15 @@ template <int O> __device__ __forceinline__ float swap_sum(float x) {
 }
 // The max of x over each 32-lane half of the wave, in every lane of the half: DPP steps within each
 // 16-lane row (quad permutes, the half-row and row mirrors), then the row swap with lane l ^ 16.
+// IEEE maxima throughout (fmaxf, not fmax_fin): it takes the int8 rows' amax, whose scale and codes
+// stay the oracle's for any input, infinities included.
 __device__ __forceinline__ float half_max(float x) {
-    x = fmax_fin(x, dpp_move<0xB1>(x));  // quad_perm [1, 0, 3, 2]
-    x = fmax_fin(x, dpp_move<0x4E>(x));  // quad_perm [2, 3, 0, 1]
-    x = fmax_fin(x, dpp_move<0x141>(x)); // row_half_mirror
-    x = fmax_fin(x, dpp_move<0x140>(x)); // row_mirror
-    return swap_max<16>(x);
+    x = fmaxf(x, dpp_move<0xB1>(x));  // quad_perm [1, 0, 3, 2]
+    x = fmaxf(x, dpp_move<0x4E>(x));  // quad_perm [2, 3, 0, 1]
+    x = fmaxf(x, dpp_move<0x141>(x)); // row_half_mirror
+    x = fmaxf(x, dpp_move<0x140>(x)); // row_mirror
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float wave_sum(float x) {
     x += dpp_move<0xB1>(x);  // quad_perm [1, 0, 3, 2]
