@@ -135,8 +135,8 @@ __global__ __launch_bounds__(1024) void k_window_append(PoolView pv, BatchView b
             row[hf] = last_row((lane >> 3) + 8 * hf);
             const int i = max(row[hf], 0);
             const size_t arow = (((size_t)P.out_row * t + i) * pv.KVH + j) * kHeadDim + 8 * unit;
-            kx[hf] = *(const uint4 *)((const uint16_t *)k + arow);
-            vx[hf] = *(const uint4 *)((const uint16_t *)v + arow);
+            kx[hf] = ld_stream((const uint16_t *)k + arow); // read once: streamed past the caches
+            vx[hf] = ld_stream((const uint16_t *)v + arow);
             cs[hf] = *(const uint4 *)(pv.rope16 + (size_t)(P.key_pos + i) * (kHeadDim / 2) + 4 * unit);
         }
         uint16_t *kt = (uint16_t *)pv.pages + tile_index(pv, layer, 0, page, j) * (kBlock * kHeadDim);
