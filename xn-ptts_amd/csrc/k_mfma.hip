@@ -839,8 +839,13 @@ __global__ __launch_bounds__(64 * kWpWaves) __attribute__((amdgpu_waves_per_eu(4
                 vsrc = vpages + poff;
             }
             const uint32_t kv_off = (uint32_t)((slot * kWpChunk + row) * kHeadDim) * 2;
-            dma16_at(ksrc, ks_at + kv_off);
-            dma16_at(vsrc, vs_at + kv_off);
+            if (j0 + row >= nfrom) { // every key of this load is a row of the step: read once, streamed
+                dma16_at_nt(ksrc, ks_at + kv_off);
+                dma16_at_nt(vsrc, vs_at + kv_off);
+            } else {
+                dma16_at(ksrc, ks_at + kv_off);
+                dma16_at(vsrc, vs_at + kv_off);
+            }
             const int r = max(j - ncache, 0);
             dma16(pv.rope16 + (size_t)(P.key_pos + r) * (kHeadDim / 2) + 4 * unit, &rs[slot][w][i][0]);
         }

@@ -313,6 +313,11 @@ __device__ __forceinline__ void dma16_at(const void *src, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base) : "memory", "m0");
 }
 __device__ __forceinline__ void dma16(const void *src, void *lds) { dma16_at(src, lds_addr(lds)); }
+// dma16_at with the non-temporal hint, for data read once (a step's own rows)
+__device__ __forceinline__ void dma16_at_nt(const void *src, uint32_t lds) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(lds);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(base) : "memory", "m0");
+}
 // The same with 4 bytes a lane: lane l's word at src goes to lds + 4 l (global_load_lds_dword).
 __device__ __forceinline__ void dma4_at(const void *src, uint32_t lds) {
     const uint32_t base = __builtin_amdgcn_readfirstlane(lds);
