@@ -142,7 +142,8 @@ __device__ __forceinline__ float wave_sum(float x) {
 // tiles stop displacing what the launch does reuse in L2 and the memory-side cache (records,
 // tables, queries).  Measured on attend_core's page loads: bf16 decode at 1024 streams 192 ->
 // 171 us, int8 window 104.4 -> 95.0 us; on the prefill's key/value staging 32.8 -> 32.2 us.  Only
-// where one load instruction covers whole 128-byte lines (attend_core: 1 KB contiguous per wave).
+// where one load instruction covers whole 128-byte lines (attend_core: 1 KB contiguous per wave):
+// the prefill's query loads, two instructions of 64 bytes a row, took the launch 25.4 -> 30.1 us.
 __device__ __forceinline__ uint4 ld_stream(const void *p) {
     typedef unsigned u32x4_nt __attribute__((ext_vector_type(4)));
     const u32x4_nt a = __builtin_nontemporal_load((const u32x4_nt *)p);
