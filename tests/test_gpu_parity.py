@@ -395,6 +395,39 @@ def test_window_caches_match_mimis_kv_cache(cache, act):
         assert pool.current_end(wids[i]) == contexts[i]  # rows held: the window, full
 
 
+def test_int8_rows_holding_infinities_quantize_as_the_oracle():
+    # An int8 page's scale is its rows' amax / 127, taken with IEEE maxima: a row holding an
+    # infinity gives the page an infinite scale, its infinite elements code -127 (rint(inf / inf) is
+    # NaN, clamped) and every other code of the page 0, the oracle's arithmetic step for step.
+    # Planted through the multi-row append (prompt rows) and the fused single-row append of a
+    # decode step; the outputs are NaN by then and not compared, the cache bytes are, bit for bit.
+    p = Pair(cache="i8", act="bf16", streams=2, cap=64, seed=61, L=1)
+    p.fill(0, 20)
+    p.fill(1, 7)
+    n = 5
+    p.pool.begin([p.ids[0]], t=n)
+    k, v = p.x(n, p.KVH, 64), p.x(n, p.KVH, 64)
+    k[2, 3, 10] = np.inf
+    v[4, 5, 0] = -np.inf
+    p.pool.append(0, dev(k, "bf16"), dev(v, "bf16"))
+    p.orc[0].append(0, k, v)
+    p.pool.end()
+    p.orc[0].commit(n)
+    p.pool.begin(p.ids)
+    q, k, v = p.x(2, p.H, 64), p.x(2, p.KVH, 64), p.x(2, p.KVH, 64)
+    k[1, 0, 7] = -np.inf
+    v[1, 2, 63] = np.inf
+    out = torch.empty((2, p.H, 64), dtype=torch.bfloat16, device=DEV)
+    p.pool.attend(0, dev(q, "bf16"), dev(k, "bf16"), dev(v, "bf16"), out, 0.125)
+    torch.cuda.synchronize()
+    for j in range(2):
+        p.orc[j].attend(0, q[j:j + 1], k[j:j + 1], v[j:j + 1])
+    p.pool.end()
+    for j in range(2):
+        p.orc[j].commit(1)
+        p.assert_cache_equal(j)
+
+
 def test_int8_window_cache_matches_the_ring_it_stands_for():
     # An int8 window has no counterpart in the reference; it is an absolute ring of `context`
     # slots whose every row evicts the oldest, so the oracle's ring driven that way is its bar:
