@@ -5,6 +5,7 @@ oracle's bit for bit; attention outputs are within 1e-5 relative (f32) or 2e-2 r
 int8 KV) of the oracle's f32 outputs, where relative error is max|got - want| / max|want| over
 each (row, head) vector.
 """
+import os
 import types
 
 import numpy as np
@@ -544,6 +545,56 @@ def test_a_long_mimi_chunk_matches_the_kv_cache(cache, act, kvh):
                 want = win.rows(layer, kv)[:, ::G]
                 for i, p in enumerate(range(win.offset - win.len, win.offset)):
                     assert np.array_equal(g[p % context].view(np.uint32), want[i].view(np.uint32)), (j, layer, kv, p)
+
+
+def test_the_mimi_configuration_at_full_size_spot_checked():
+    # The bench's Mimi workload at its size: 256 windows of context 250, 2 layers x 8 heads x 64,
+    # bf16; a first 250-row chunk into empty windows, then a second over the 249 held rows (the
+    # shape the bench times).  Every window's layer 0 is held to the oracle's KvCache (a one-layer
+    # window per stream, run on the host's threads); both layers of a sample of windows, and the
+    # sample's held rows bit for bit at the end.
+    from concurrent.futures import ThreadPoolExecutor
+    S, L, H, context, T = 256, 2, 8, 250, 250
+    pool = xnp.KvPool(num_layers=L, num_heads=H, num_blocks=S * 16 + 8, max_streams=S, max_blocks_per_stream=16,
+                      cache_dtype="bf16", act_dtype="bf16", max_pos=1024, page_seed=18)
+    ids = [pool.init_window(context) for _ in range(S)]
+    sample = [0, 1, 130, 255]
+    full = {i: oracle.Window(L, H, 64, context, rows_max=T, act="bf16") for i in sample}
+    every = [oracle.Window(1, H, 64, context, rows_max=T, act="bf16") for _ in range(S)]
+    rng = np.random.default_rng(71)
+    with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as ex:
+        for chunk in range(2):
+            pool.begin(ids, t=T)
+            for layer in range(L):
+                q, k, v = (bf16_round(rng.standard_normal((S, T, H, 64)).astype(np.float32)) for _ in range(3))
+                out = torch.empty((S, T, H, 64), dtype=torch.bfloat16, device=DEV)
+                pool.attend(layer, dev(q, "bf16"), dev(k, "bf16"), dev(v, "bf16"), out, 0.125)
+                torch.cuda.synchronize()
+                got = host(out)
+                if layer == 0:
+                    wants = list(ex.map(lambda j: every[j].attend(0, q[j], k[j], v[j])[0], range(S)))
+                    worst = max(rel_err(got[j], wants[j]) for j in range(S))
+                    assert worst <= TOL["bf16"], (chunk, worst)
+                for i in sample:
+                    want, _ = full[i].attend(layer, q[i], k[i], v[i])
+                    assert rel_err(got[i], want) <= TOL["bf16"], (chunk, layer, i)
+            pool.end()
+            for w in every:
+                w.commit(T)
+            for i in sample:
+                full[i].commit(T)
+    for i in sample:
+        win = full[i]
+        assert pool.current_end(ids[i]) == context
+        for layer in range(L):
+            for kv in (0, 1):
+                rows = torch.empty((context, H, 64), dtype=torch.bfloat16, device=DEV)
+                pool.read_rows(ids[i], layer, kv, 0, rows)
+                torch.cuda.synchronize()
+                g = rows.float().cpu().numpy()
+                want = win.rows(layer, kv)
+                for r, pos in enumerate(range(win.offset - win.len, win.offset)):
+                    assert np.array_equal(g[pos % context].view(np.uint32), want[r].view(np.uint32)), (i, layer, kv, pos)
 
 
 def test_window_misuse_is_refused():
